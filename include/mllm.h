@@ -1,0 +1,186 @@
+/*
+ * mllm.h -- C ABI of libmllm, the MI355X (gfx950) fused Q4 decode step.
+ *
+ * This is the drop-in boundary for microllm-lab's decode hot path.  Two levels:
+ *
+ *  1. Operator level: the kernels the reference exports from engine/kernels.rs
+ *     (compiled to kernels.wasm and plugged into PetitGPT.gemv by
+ *     engine/worker.js:20-31).  Same argument order and meaning; pointers are
+ *     DEVICE pointers (the reference's are wasm linear-memory offsets); every
+ *     call returns a status code instead of nothing.
+ *
+ *  2. Engine level: the PetitGPT model API of engine/infer.js:289-647
+ *     (constructor, forwardPrompt, forwardDecode, resetCache, cacheLen, gemv)
+ *     plus the GPU engine's multi-token pass (engine/webgpu.js:1120-1138 with
+ *     logitsEach) and its chained decode (CHAIN_TOK, engine/webgpu-metal.js:22,
+ *     609-610).  Host buffers in, host buffers out; weights, KV cache and
+ *     scratch stay resident in HBM.
+ *
+ * Conventions:
+ *   - Return value 0 (MLLM_OK) on success, otherwise an MLLM_ERR_* code; the
+ *     message is available from mllm_last_error() (thread-local).
+ *   - `stream` is a hipStream_t passed as void*; NULL means the default stream.
+ *     Operator calls are asynchronous on that stream.
+ *   - Engine calls are synchronous and not thread-safe per model (the
+ *     reference serialises calls per engine the same way, app.js:58-63).
+ *   - Arrays of group-32 Q4 weights use the PGW1 layout: packed [m][n/2] bytes
+ *     (element 2k in the low nibble of byte k, 2k+1 in the high nibble) and
+ *     scales [m][n/32] f32; w = (nibble - 8) * scale.
+ */
+#ifndef MLLM_H
+#define MLLM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLLM_OK 0
+#define MLLM_ERR_INVALID 1     /* bad argument or shape */
+#define MLLM_ERR_HIP 2         /* HIP runtime error */
+#define MLLM_ERR_OOM 3         /* device allocation failed */
+#define MLLM_ERR_UNSUPPORTED 4 /* shape/format this build does not handle */
+#define MLLM_ERR_DEVICE 5      /* a kernel reported an error (e.g. barrier time-out) */
+
+/* Thread-local message for the last non-zero return (never NULL). */
+const char *mllm_last_error(void);
+
+/* kernels.rs:133-136 kernel_version() -> 1.  This library reports 1 as well:
+ * the operator semantics below are the reference's version-1 semantics. */
+int mllm_kernel_version(void);
+
+/* ========================================================================
+ * Operator level (device pointers)
+ * ====================================================================== */
+
+/* kernels.rs:13-39 gemv_f32(m, n, w, x, y): y[m] = W[m][n] . x[n] */
+int mllm_gemv_f32(int m, int n, const float *w, const float *x, float *y, void *stream);
+
+/* kernels.rs:41-57 gemv_q8(m, n, q, scale, x, y): per-row Q8,
+ * y[i] = scale[i] * sum_k q[i][k] * x[k]   (weights.js:96-104 layout) */
+int mllm_gemv_q8(int m, int n, const int8_t *q, const float *scale, const float *x, float *y, void *stream);
+
+/* kernels.rs:59-97 gemv_q4(m, n, packed, scale, group, x, y) and
+ * infer.js:88-116 gemvQ4: y[i] = sum_g scale[i][g] * sum_k (nib - 8) * x[g*32+k].
+ * group must be 32; n % 32 == 0. */
+int mllm_gemv_q4(int m, int n, const uint8_t *packed, const float *scale, int group, const float *x, float *y,
+                 void *stream);
+
+/* No reference counterpart (BASELINE config 2 asks for it; the reference's Q8
+ * is per-row only): Q8 group-32, q [m][n] i8 + scale [m][n/32] f32. */
+int mllm_gemv_q8_g32(int m, int n, const int8_t *q, const float *scale, const float *x, float *y, void *stream);
+
+/* infer.js:118-132 gemmGeneric for a Q4 matrix: y[t][m] = W . x[t][n] for
+ * t tokens, each row bit-identical to mllm_gemv_q4 on that token. */
+int mllm_gemm_q4(int t, int m, int n, const uint8_t *packed, const float *scale, int group, const float *x, float *y,
+                 void *stream);
+
+/* No reference counterpart: one launch over `count` Q4 GEMVs of the same
+ * shape (a layer stack), arrays of device pointers in device memory. */
+int mllm_gemv_q4_batched(int count, int m, int n, const uint8_t *const *packed, const float *const *scale,
+                         const float *const *x, float *const *y, void *stream);
+
+/* kernels.rs:99-120 rms_norm(n, x, w, out, tokens) with eps as a parameter
+ * (the reference hard-codes 1e-6: infer.js:8, kernels.rs:106). */
+int mllm_rms_norm(int n, const float *x, const float *w, float *out, int tokens, float eps, void *stream);
+
+/* kernels.rs:122-131 silu_mul(n, a, b): a[i] = silu(a[i]) * b[i] */
+int mllm_silu_mul(int n, float *a, const float *b, void *stream);
+
+/* weights.js:106-123 dequantizeToF32 (q4 branch): out[m][n], bit-exact. */
+int mllm_dequant_q4(int m, int n, const uint8_t *packed, const float *scale, int group, float *out, void *stream);
+
+/* ========================================================================
+ * Engine level (infer.js PetitGPT)
+ * ====================================================================== */
+
+/* Model configuration: the PGW1 header fields (weights.js:17-29) plus the
+ * two numeric choices the header does not carry. */
+typedef struct mllm_config {
+  int32_t arch; /* 0 = llama, 1 = gpt2 (weights.js:15-16) */
+  int32_t vocab_size, n_layers, d_model, n_heads, n_kv_heads, d_ff, max_seq_len;
+  double rope_theta, rope_pct;
+  float norm_eps;  /* RMSNorm eps; the reference uses 1e-6 (infer.js:8) */
+  int32_t kv_fp16; /* 0: f32 KV cache as the reference; 1: fp16 KV cache */
+} mllm_config;
+
+/* Storage codes: the PGW1 dtype codes (weights.js:3) plus 5 = Q8 group-32. */
+#define MLLM_F32 0
+#define MLLM_F16 1
+#define MLLM_BF16 2
+#define MLLM_Q8 3
+#define MLLM_Q4 4
+#define MLLM_Q8G32 5
+
+/* One entry of the PGW1 JSON tensor table (convert_hf_to_pgw.py:44-69);
+ * offsets are relative to the payload start. */
+typedef struct mllm_tensor {
+  const char *name;
+  int32_t storage;
+  int32_t rows, cols, group; /* 1-D tensors: rows = 1 */
+  uint64_t offset, nbytes, scale_offset, scale_nbytes;
+} mllm_tensor;
+
+typedef struct mllm_model mllm_model;
+
+/* new PetitGPT(bundle) (infer.js:290-311) + the device upload of
+ * GpuPetitGPT.init (webgpu.js:892-1106): copies the payload to HBM once and
+ * allocates the KV cache and scratch.  payload is host memory.  Tensor names
+ * follow the converters (lm_head, blocks.{i}.attn.qkv, ...).  Q4 matrices only
+ * (plus f32 norms/biases/positions). */
+int mllm_model_create(const mllm_config *cfg, const void *payload, uint64_t payload_nbytes,
+                      const mllm_tensor *tensors, int n_tensors, mllm_model **out);
+/* GpuPetitGPT.destroy (webgpu.js:1284-1297); NULL is accepted. */
+int mllm_model_destroy(mllm_model *model);
+
+/* infer.js:348-358 resetCache; cacheLen getter/setter. */
+int mllm_reset_cache(mllm_model *model);
+int mllm_cache_len(const mllm_model *model);
+int mllm_set_cache_len(mllm_model *model, int len);
+
+/* infer.js:553-577 forwardPrompt(ids): positions 0..n-1, cacheLen = n.
+ * logits (host, vocab floats) receives the last row; argmax (nullable) its
+ * first-maximum index (infer.js:240-250). */
+int mllm_forward_prompt(mllm_model *model, const int32_t *ids, int n, float *logits, int32_t *argmax);
+
+/* infer.js:579-601 forwardDecode(id): one token at position cacheLen,
+ * cacheLen += 1.  logits and argmax are nullable. */
+int mllm_forward_decode(mllm_model *model, int32_t id, float *logits, int32_t *argmax);
+
+/* The multi-token pass of webgpu.js:557-686 (logitsEach): ids[0..n) at
+ * positions cacheLen..cacheLen+n-1 with a causal mask, one argmax per row
+ * (argmax[n]); logits [n][vocab] optional.  Every row is bit-identical to the
+ * forward_decode call that would have computed it.  Leaves cacheLen += n; the
+ * caller rolls it back with mllm_set_cache_len after acceptance
+ * (webgpu.js:1254,1263).  n <= mllm_max_pass_tokens(). */
+int mllm_forward_verify(mllm_model *model, const int32_t *ids, int n, int32_t *argmax, float *logits);
+int mllm_max_pass_tokens(const mllm_model *model);
+
+/* Chained greedy decode on the device (CHAIN_TOK, webgpu-metal.js:609-610;
+ * webgpu.js:1202-1226): starting from token `first` at position cacheLen,
+ * run up to n_steps decode steps where each step's argmax feeds the next
+ * step, without host round trips.  Stops after a step that emits eos_id
+ * (eos_id < 0: never).  out_ids receives the emitted ids, *n_out their count;
+ * cacheLen advances by *n_out.  For gpt2 the argmax applies argmaxGpt2's
+ * 3-gram block and 1.15 penalty (infer.js:252-287) over hist[0..n_hist)
+ * followed by the ids emitted here. */
+int mllm_decode_chain(mllm_model *model, int32_t first, int n_steps, int32_t eos_id, const int32_t *hist, int n_hist,
+                      int32_t *out_ids, int *n_out);
+
+/* model.gemv(name, x, y) (infer.js:338-346): host x [cols] -> host y [rows]. */
+int mllm_model_gemv(mllm_model *model, const char *name, const float *x, float *y);
+
+/* Execution mode of the decode step: 0 = one persistent kernel per pass
+ * (grid barriers between phases), 1 = one kernel per phase replayed from a
+ * HIP graph.  Default: 0. */
+int mllm_set_exec_mode(mllm_model *model, int mode);
+
+/* Bytes of device memory the model holds (GpuPetitGPT.bytesAllocated). */
+uint64_t mllm_model_device_bytes(const mllm_model *model);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,201 @@
+// mllm_device.h -- device building blocks shared by the operator kernels and
+// the decode engine (gfx950, wave64, 256-thread workgroups).
+//
+// GEMV scheme for group-32 Q4 at batch 1 (no MFMA):
+//   * A row-major [m][n/2] nibble matrix is one contiguous byte stream, and the
+//     16-byte "chunk" c (= 32 weights = one quant group) has its scale at
+//     scale[c].  Consecutive threads take consecutive chunks, so every 128-bit
+//     load of a wavefront covers 1 KiB of contiguous HBM.
+//   * The activation vector x is staged once per workgroup in LDS as
+//     [group][36] floats (32 used, 4 of skew so neighbouring lanes' 128-bit LDS
+//     reads land in different banks), with the per-group sum xsum[g].
+//   * In registers a chunk is unpacked as two masked dwords per 8 weights
+//     (v_cvt_f32_ubyte0..3 on (d & 0x0f0f0f0f) and ((d >> 4) & 0x0f0f0f0f));
+//     the "-8" is applied once per group as  sum(q*x) - 8*sum(x), then * scale.
+//   * Per-chunk partials go to LDS and each row is summed over its groups in
+//     ascending order by one thread: a fixed order, so a row's result does not
+//     depend on how many tokens share the pass (the verify pass relies on it).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mllm {
+
+constexpr int WG = 256;          // threads per workgroup
+constexpr int XS = 36;           // LDS floats per staged 32-float group
+constexpr int CPT = 4;           // chunks per thread per sub-tile
+constexpr int SUB_CH = WG * CPT; // chunks per sub-tile
+
+struct Q4Mat {
+  const uint4 *q;  // packed nibbles, as 16-byte chunks
+  const float *s;  // one scale per chunk
+  int rows, cols;  // cols % 32 == 0
+};
+
+// AND through inline asm: the mask stays opaque to the known-bits combiner,
+// so (float)((v >> 8k) & 0xff) below selects v_cvt_f32_ubyte{k} on the masked
+// dword instead of a v_bfe_u32 per weight.
+__device__ __forceinline__ uint32_t and_opaque(uint32_t v, uint32_t mask) {
+  uint32_t r;
+  asm("v_and_b32 %0, %1, %2" : "=v"(r) : "s"(mask), "v"(v));
+  return r;
+}
+
+__device__ __forceinline__ float ubyte(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xFFu); }
+
+// One 16-byte chunk (32 weights of one group) against 32 staged floats:
+// returns sum_k q_k * x_k with q_k the raw nibble (0..15).  Even elements are
+// the low nibbles; odd elements are taken in place (16 * q) and rescaled by
+// 1/16 (exact) at the end: 2 ANDs + 8 conversions + 8 FMAs per 8 weights.
+__device__ __forceinline__ float q4_chunk_dot(const uint4 w, const float *__restrict__ xg) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t lo = and_opaque(dw[j], 0x0F0F0F0Fu);
+    const uint32_t hi = and_opaque(dw[j], 0xF0F0F0F0u);
+    const float4 xa = *reinterpret_cast<const float4 *>(xg + 8 * j);
+    const float4 xb = *reinterpret_cast<const float4 *>(xg + 8 * j + 4);
+    a0 = __builtin_fmaf(ubyte(lo, 0), xa.x, a0);
+    a1 = __builtin_fmaf(ubyte(hi, 0), xa.y, a1);
+    a2 = __builtin_fmaf(ubyte(lo, 1), xa.z, a2);
+    a3 = __builtin_fmaf(ubyte(hi, 1), xa.w, a3);
+    a0 = __builtin_fmaf(ubyte(lo, 2), xb.x, a0);
+    a1 = __builtin_fmaf(ubyte(hi, 2), xb.y, a1);
+    a2 = __builtin_fmaf(ubyte(lo, 3), xb.z, a2);
+    a3 = __builtin_fmaf(ubyte(hi, 3), xb.w, a3);
+  }
+  return (a0 + a2) + (a1 + a3) * 0.0625f;
+}
+
+// 16 signed 8-bit weights against 16 floats: sum((u - 128) * x) with
+// u = q ^ 0x80 converted by v_cvt_f32_ubyte; the -128 is folded by the caller.
+__device__ __forceinline__ float q8_chunk_dot(const uint4 w, const float *__restrict__ xg) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  const uint32_t dw[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u, w.w ^ 0x80808080u};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float4 xa = *reinterpret_cast<const float4 *>(xg + 4 * j);
+    a0 = __builtin_fmaf(ubyte(dw[j], 0), xa.x, a0);
+    a1 = __builtin_fmaf(ubyte(dw[j], 1), xa.y, a1);
+    a2 = __builtin_fmaf(ubyte(dw[j], 2), xa.z, a2);
+    a3 = __builtin_fmaf(ubyte(dw[j], 3), xa.w, a3);
+  }
+  return (a0 + a1) + (a2 + a3);
+}
+
+// Deterministic block-wide sum for 256 threads; red needs 4 floats of LDS.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  const float r = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ float block_max(float v, float *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return r;
+}
+
+// (value, index) "better" relation of infer.js argmax: larger value, then
+// lower index (the first maximum).
+__device__ __forceinline__ bool amax_better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ void wave_argmax(float &v, int &i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(i, o, 64);
+    if (amax_better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+// Per-group sums of the staged activations: xsum[t*ng+g] = sum_k xs[(t*ng+g)*XS+k]
+// in ascending k.  Call after xs is complete (a barrier follows inside).
+__device__ __forceinline__ void stage_group_sums(const float *xs, float *xsum, int m, int ng) {
+  for (int i = threadIdx.x; i < m * ng; i += WG) {
+    const float *p = xs + i * XS;
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) s += p[k];
+    xsum[i] = s;
+  }
+  __syncthreads();
+}
+
+// Plain staging of m vectors x[t*ldx + i] (i < n) into the skewed layout.
+__device__ __forceinline__ void stage_plain(const float *__restrict__ x, int ldx, int m, int n, float *xs,
+                                            float *xsum) {
+  const int ng = n >> 5;
+  for (int t = 0; t < m; ++t)
+    for (int i = threadIdx.x; i < n; i += WG) xs[(t * ng + (i >> 5)) * XS + (i & 31)] = x[(size_t)t * ldx + i];
+  __syncthreads();
+  stage_group_sums(xs, xsum, m, ng);
+}
+
+// Q4 GEMV over rows [row0, row0 + nrows) of W for m staged vectors:
+// out[t*ostride + r] = sum_g sc * (sum_k q*x - 8*xsum).  part needs m*SUB_CH floats.
+// gfirst = threadIdx.x % ng and gstep = WG % ng are precomputed by the caller.
+__device__ __forceinline__ void gemv_q4_rows(const Q4Mat &W, int row0, int nrows, int m, const float *xs,
+                                             const float *xsum, int ng, int gfirst, int gstep, float *part,
+                                             float *out, int ostride) {
+  const int tid = threadIdx.x;
+  const int rows_per_sub = SUB_CH / ng > 0 ? SUB_CH / ng : 1;
+  for (int rs = 0; rs < nrows; rs += rows_per_sub) {
+    const int nr = min(rows_per_sub, nrows - rs);
+    const int nch = nr * ng;
+    const size_t cbase = (size_t)(row0 + rs) * ng;
+    uint4 w[CPT];
+    float s[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int c = tid + j * WG;
+      if (c < nch) {
+        w[j] = W.q[cbase + c];
+        s[j] = W.s[cbase + c];
+      }
+    }
+    int g = gfirst;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int c = tid + j * WG;
+      if (c < nch) {
+        for (int t = 0; t < m; ++t) {
+          const float d = q4_chunk_dot(w[j], xs + (t * ng + g) * XS);
+          part[t * nch + c] = (d - 8.f * xsum[t * ng + g]) * s[j];
+        }
+      }
+      g += gstep;
+      if (g >= ng) g -= ng;
+    }
+    __syncthreads();
+    for (int i = tid; i < nr * m; i += WG) {
+      const int t = i / nr, r = i - t * nr;
+      const float *p = part + t * nch + r * ng;
+      float acc = 0.f;
+      for (int k = 0; k < ng; ++k) acc += p[k];
+      out[t * ostride + rs + r] = acc;
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace mllm

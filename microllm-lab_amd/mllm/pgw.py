@@ -1,0 +1,312 @@
+"""PGW1 weight container: reader, writer, quantisers and synthetic models.
+
+Format (reader: engine/weights.js:5-39; writer: tools/convert_hf_to_pgw.py:125-144
+and tools/convert_gpt2_to_pgw.py:166-184):
+
+  bytes 0..3    "PGW1"
+  byte  4       dtype code (weights.js:3): 0 f32, 1 f16, 2 bf16, 3 q8, 4 q4
+  byte  5       arch: 0 llama, 1 gpt2
+  u32 @ 8..36   vocab, nLayers, dModel, nHeads, nKvHeads, dFf, maxSeqLen, qGroup
+  u32 @ 40/44/48 tableOff (=256), tableLen, payloadOff (16-aligned)
+  f64 @ 56/64   ropeTheta, ropePct
+  JSON table    [{name, shape, kind, storage, group, scaleOffset, scaleNbytes, offset, nbytes}]
+  payload       per q4 tensor: f32 scales [rows][cols/32] then packed nibbles [rows][cols/2]
+
+The tensor order and JSON key order follow the converters so a file written here
+is laid out the way the reference writes one.
+"""
+from __future__ import annotations
+
+import json
+import struct
+from dataclasses import dataclass, field
+from io import BytesIO
+from typing import Dict, List, Optional
+
+import numpy as np
+
+GROUP = 32
+DTYPE_CODE = {0: "f32", 1: "f16", 2: "bf16", 3: "q8", 4: "q4"}
+STORAGE_CODE = {"f32": 0, "f16": 1, "bf16": 2, "q8": 3, "q4": 4, "q8g32": 5}
+
+
+# --------------------------------------------------------------------------
+# quantisers
+# --------------------------------------------------------------------------
+def quant_q4(mat: np.ndarray, group: int = GROUP):
+    """Vectorised restatement of convert_hf_to_pgw.py:18-34.
+
+    Per group of 32: amax = max|x|; sc = amax/8 in f64 (1.0 if amax == 0),
+    stored as f32; q = clip(rint(x / f32(sc)) + 8, 0, 15) computed in float32
+    (NumPy divides a float32 array by a Python float in float32); the even
+    element goes to the low nibble.
+    """
+    mat = np.ascontiguousarray(mat, dtype=np.float32)
+    rows, cols = mat.shape
+    if cols % group:
+        raise ValueError(f"cols {cols} not divisible by group {group}")
+    ng = cols // group
+    ch = mat.reshape(rows, ng, group)
+    amax = np.abs(ch).max(axis=-1)
+    sc = np.where(amax > 0, amax.astype(np.float64) / 8.0, 1.0).astype(np.float32)
+    q = np.clip(np.rint(ch / sc[..., None]) + np.float32(8.0), 0, 15).astype(np.uint8)
+    packed = (q[..., 0::2] | (q[..., 1::2] << 4)).reshape(rows, cols // 2)
+    return np.ascontiguousarray(packed), np.ascontiguousarray(sc)
+
+
+def _quant_q8_spans(ch: np.ndarray):
+    amax = np.abs(ch).max(axis=-1)
+    sc = np.where(amax > 0, amax.astype(np.float64) / 127.0, 1.0).astype(np.float32)
+    q = np.clip(np.rint(ch / sc[..., None]), -127, 127).astype(np.int8)
+    return q, sc
+
+
+def quant_q8g32(mat: np.ndarray):
+    """Build-defined Q8 group-32 (the reference has no such format): i8 [m][n] + f32 [m][n/32]."""
+    mat = np.ascontiguousarray(mat, dtype=np.float32)
+    rows, cols = mat.shape
+    q, sc = _quant_q8_spans(mat.reshape(rows, cols // 32, 32))
+    return np.ascontiguousarray(q.reshape(rows, cols)), np.ascontiguousarray(sc)
+
+
+def quant_q8row(mat: np.ndarray):
+    """Per-row Q8 in the reference's storage layout (weights.js:96-104): i8 [m][n] + f32 [m]."""
+    mat = np.ascontiguousarray(mat, dtype=np.float32)
+    q, sc = _quant_q8_spans(mat)
+    return np.ascontiguousarray(q), np.ascontiguousarray(sc)
+
+
+def dequant_q4(packed: np.ndarray, scales: np.ndarray, group: int = GROUP) -> np.ndarray:
+    """weights.js:106-123 (vectorised)."""
+    rows = packed.shape[0]
+    cols = packed.shape[1] * 2
+    lo = (packed & 15).astype(np.int32) - 8
+    hi = (packed >> 4).astype(np.int32) - 8
+    q = np.empty((rows, cols), np.float64)
+    q[:, 0::2] = lo
+    q[:, 1::2] = hi
+    sc = np.repeat(scales.astype(np.float64), group, axis=1)
+    return (q * sc).astype(np.float32)
+
+
+# --------------------------------------------------------------------------
+# container
+# --------------------------------------------------------------------------
+@dataclass
+class Config:
+    arch: str = "llama"
+    vocab_size: int = 49152
+    n_layers: int = 30
+    d_model: int = 576
+    n_heads: int = 9
+    n_kv_heads: int = 3
+    d_ff: int = 1536
+    max_seq_len: int = 2048
+    q_group: int = GROUP
+    rope_theta: float = 100000.0
+    rope_pct: float = 1.0
+
+    @property
+    def head_dim(self) -> int:
+        return self.d_model // self.n_heads
+
+
+@dataclass
+class Bundle:
+    """What parsePgw returns (weights.js:39): kind, cfg, tensors, buffer, payloadOff."""
+
+    kind: str
+    cfg: Config
+    tensors: Dict[str, dict]
+    buffer: bytes
+    payload_off: int
+    order: List[str] = field(default_factory=list)
+
+    @property
+    def payload(self) -> memoryview:
+        return memoryview(self.buffer)[self.payload_off:]
+
+    def array(self, name: str) -> np.ndarray:
+        """Typed view of a tensor's data (weights.js:42-62)."""
+        t = self.tensors[name]
+        st = t["storage"]
+        dt = {"f32": np.float32, "f16": np.uint16, "bf16": np.uint16, "q8": np.int8, "q8g32": np.int8,
+              "q4": np.uint8}[st]
+        a = np.frombuffer(self.buffer, dtype=dt, count=t["nbytes"] // np.dtype(dt).itemsize,
+                          offset=self.payload_off + t["offset"])
+        shape = t["shape"]
+        if st == "q4":
+            return a.reshape(shape[0], shape[1] // 2)
+        return a.reshape(shape)
+
+    def scales(self, name: str) -> np.ndarray:
+        """weights.js:64-67"""
+        t = self.tensors[name]
+        a = np.frombuffer(self.buffer, dtype=np.float32, count=t["scaleNbytes"] // 4,
+                          offset=self.payload_off + t["scaleOffset"])
+        rows = t["shape"][0]
+        return a.reshape(rows, -1)
+
+
+def parse_pgw(buf: bytes) -> Bundle:
+    """Restatement of weights.js:5-39."""
+    buf = bytes(buf)
+    if buf[0:4] != b"PGW1":
+        raise ValueError(f"bad magic {buf[0:4]!r}")
+    kind = DTYPE_CODE.get(buf[4], "f32")
+    arch = "gpt2" if buf[5] == 1 else "llama"
+    vocab, nl, d, nh, nkv, dff, ms, qg = struct.unpack_from("<8I", buf, 8)
+    table_off, table_len, payload_off = struct.unpack_from("<III", buf, 40)
+    theta = struct.unpack_from("<d", buf, 56)[0] or 10000.0
+    pct = struct.unpack_from("<d", buf, 64)[0] or 1.0
+    cfg = Config(arch, vocab, nl, d, nh, nkv, dff, ms, qg or 32, theta, pct)
+    table = json.loads(buf[table_off:table_off + table_len].decode("utf-8"))
+    tensors = {e["name"]: e for e in table}
+    if cfg.arch == "gpt2" and "blocks.0.ln1" not in tensors and "blocks.0.norm1" in tensors:
+        cfg.arch = "llama"
+    return Bundle(kind, cfg, tensors, buf, payload_off, [e["name"] for e in table])
+
+
+class PgwWriter:
+    """Accumulates tensors in the converters' blob order (convert_hf_to_pgw.py:37-72)."""
+
+    def __init__(self):
+        self.blobs = BytesIO()
+        self.entries: List[dict] = []
+
+    def add_q4(self, name: str, arr: np.ndarray):
+        packed, scales = quant_q4(arr)
+        self.add_q4_packed(name, packed, scales, arr.shape)
+
+    def add_q4_packed(self, name, packed, scales, shape):
+        scale_off = self.blobs.tell()
+        self.blobs.write(np.ascontiguousarray(scales, np.float32).tobytes())
+        data_off = self.blobs.tell()
+        self.blobs.write(np.ascontiguousarray(packed, np.uint8).tobytes())
+        self.entries.append({
+            "name": name,
+            "shape": [int(shape[0]), int(shape[1])],
+            "kind": "q4",
+            "storage": "q4",
+            "group": GROUP,
+            "scaleOffset": scale_off,
+            "scaleNbytes": int(scales.size * 4),
+            "offset": data_off,
+            "nbytes": int(packed.size),
+        })
+
+    def add_f32(self, name: str, arr: np.ndarray):
+        data = np.ascontiguousarray(arr, dtype=np.float32)
+        off = self.blobs.tell()
+        self.blobs.write(data.tobytes())
+        self.entries.append({
+            "name": name,
+            "shape": list(data.shape),
+            "kind": "q4",
+            "storage": "f32",
+            "offset": off,
+            "nbytes": int(data.nbytes),
+        })
+
+    def finish(self, cfg: Config, header_group: Optional[int] = None) -> bytes:
+        payload = self.blobs.getvalue()
+        table = json.dumps(self.entries, separators=(",", ":")).encode("utf-8")
+        table_off = 256
+        pad = (16 - ((table_off + len(table)) % 16)) % 16
+        payload_off = table_off + len(table) + pad
+        header = bytearray(256)
+        header[0:4] = b"PGW1"
+        header[4] = 4
+        header[5] = 1 if cfg.arch == "gpt2" else 0
+        qg = GROUP if header_group is None else header_group
+        struct.pack_into("<8I", header, 8, cfg.vocab_size, cfg.n_layers, cfg.d_model, cfg.n_heads,
+                         cfg.n_kv_heads, cfg.d_ff, cfg.max_seq_len, qg)
+        struct.pack_into("<III", header, 40, table_off, len(table), payload_off)
+        struct.pack_into("<d", header, 56, cfg.rope_theta)
+        struct.pack_into("<d", header, 64, cfg.rope_pct)
+        return bytes(header) + table + b"\x00" * pad + payload
+
+
+# --------------------------------------------------------------------------
+# synthetic models (no checkpoints exist offline)
+# --------------------------------------------------------------------------
+CONFIGS = {
+    # SmolLM2-135M shape (models/smollm2-135m-instruct/card.json)
+    "smollm2-135m": Config("llama", 49152, 30, 576, 9, 3, 1536, 2048, 32, 100000.0, 1.0),
+    # SmolLM2-360M shape (models/smollm2-360m-instruct/card.json)
+    "smollm2-360m": Config("llama", 49152, 32, 960, 15, 5, 2560, 2048, 32, 100000.0, 1.0),
+    # GPT-2 124M shape (models/gpt2/card.json)
+    "gpt2-124m": Config("gpt2", 50257, 12, 768, 12, 12, 3072, 1024, 32, 10000.0, 1.0),
+}
+
+
+def _normal(rng: np.random.Generator, shape, std: float = 0.02) -> np.ndarray:
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+
+def make_llama(cfg: Config, seed: int = 0, std: float = 0.02, norm_gain: float = 1.0) -> bytes:
+    """Llama-style PGW1 in convert_hf_to_pgw.py:104-122 order; weights N(0, std),
+    quantised by quant_q4; norm gains constant."""
+    rng = np.random.default_rng(seed)
+    hd = cfg.d_model // cfg.n_heads
+    kv = cfg.n_kv_heads * hd
+    w = PgwWriter()
+    w.add_q4("lm_head", _normal(rng, (cfg.vocab_size, cfg.d_model), std))
+    ones = np.full(cfg.d_model, norm_gain, np.float32)
+    for i in range(cfg.n_layers):
+        w.add_f32(f"blocks.{i}.norm1", ones)
+        w.add_q4(f"blocks.{i}.attn.qkv", _normal(rng, (cfg.d_model + 2 * kv, cfg.d_model), std))
+        w.add_q4(f"blocks.{i}.attn.proj", _normal(rng, (cfg.d_model, cfg.d_model), std))
+        w.add_f32(f"blocks.{i}.norm2", ones)
+        w.add_q4(f"blocks.{i}.mlp.w1", _normal(rng, (cfg.d_ff, cfg.d_model), std))
+        w.add_q4(f"blocks.{i}.mlp.w3", _normal(rng, (cfg.d_ff, cfg.d_model), std))
+        w.add_q4(f"blocks.{i}.mlp.w2", _normal(rng, (cfg.d_model, cfg.d_ff), std))
+    w.add_f32("norm_f", ones)
+    return w.finish(cfg)
+
+
+def make_gpt2(cfg: Config, seed: int = 0, std: float = 0.02, scale_factors: Optional[np.ndarray] = None,
+              bias_std: float = 0.0) -> bytes:
+    """GPT-2 PGW1 in convert_gpt2_to_pgw.py:135-164 order; header qGroup = 1 as the
+    converter writes it (convert_gpt2_to_pgw.py:175).  LN gamma 1, beta 0,
+    biases N(0, bias_std) (0 by default), scale_factors 1 unless given."""
+    rng = np.random.default_rng(seed)
+    d, ff = cfg.d_model, cfg.d_ff
+    w = PgwWriter()
+    sf = np.ones(d, np.float32) if scale_factors is None else np.asarray(scale_factors, np.float32)
+    w.add_f32("scale_factors", sf)
+    w.add_q4("lm_head", _normal(rng, (cfg.vocab_size, d), std))
+    w.add_f32("wpe", _normal(rng, (cfg.max_seq_len, d), std))
+    w.add_f32("ln_f", np.concatenate([np.ones(d, np.float32) / sf, np.zeros(d, np.float32) / sf]))
+    ln = np.concatenate([np.ones(d, np.float32), np.zeros(d, np.float32)])
+
+    def bias(n):
+        return _normal(rng, (n,), bias_std) if bias_std > 0 else np.zeros(n, np.float32)
+
+    for i in range(cfg.n_layers):
+        w.add_f32(f"blocks.{i}.ln1", ln)
+        w.add_q4(f"blocks.{i}.attn.qkv", _normal(rng, (3 * d, d), std))
+        w.add_f32(f"blocks.{i}.attn.qkv_bias", bias(3 * d))
+        w.add_q4(f"blocks.{i}.attn.proj", _normal(rng, (d, d), std))
+        w.add_f32(f"blocks.{i}.attn.proj_bias", bias(d))
+        w.add_f32(f"blocks.{i}.ln2", ln)
+        w.add_q4(f"blocks.{i}.mlp.fc", _normal(rng, (ff, d), std))
+        w.add_f32(f"blocks.{i}.mlp.fc_bias", bias(ff))
+        w.add_q4(f"blocks.{i}.mlp.proj", _normal(rng, (d, ff), std))
+        w.add_f32(f"blocks.{i}.mlp.proj_bias", bias(d))
+    return w.finish(cfg, header_group=1)
+
+
+def make_model(cfg: Config, seed: int = 0, **kw) -> bytes:
+    return make_gpt2(cfg, seed, **kw) if cfg.arch == "gpt2" else make_llama(cfg, seed, **kw)
+
+
+def small_config(arch: str = "llama", **over) -> Config:
+    """Tiny shapes for CPU-oracle parity tests."""
+    if arch == "gpt2":
+        c = Config("gpt2", 512, 2, 128, 2, 2, 512, 64, 32, 10000.0, 1.0)
+    else:
+        c = Config("llama", 512, 2, 128, 2, 1, 256, 64, 32, 10000.0, 1.0)
+    for k, v in over.items():
+        setattr(c, k, v)
+    return c

@@ -1,0 +1,119 @@
+"""Oracle pinning: quantiser and dequantiser (CPU).
+
+quant_q4 is pinned against golden vectors written by the reference's own
+quant_q4 (tools/convert_hf_to_pgw.py:18-34) via tests/golden/make_quant_q4_vectors.py;
+the dequantiser is pinned by the error bound and exact requantisation, which a
+swapped nibble order or a wrong offset would break.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from mllm import pgw
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_q4_vectors.npz")
+
+
+def golden_cases():
+    z = np.load(GOLDEN)
+    names = sorted({k.split("__")[0] for k in z.files})
+    return [(n, z[n + "__x"], z[n + "__packed"], z[n + "__scales"]) for n in names]
+
+
+@pytest.mark.parametrize("case", golden_cases(), ids=lambda c: c[0])
+def test_quant_q4_matches_reference_golden(oracle_lib, case):
+    name, x, packed, scales = case
+    p, s = oracle_lib.quant_q4(x)
+    assert np.array_equal(p, packed), name
+    assert np.array_equal(s.view(np.uint32), scales.view(np.uint32)), name
+    p2, s2 = pgw.quant_q4(x)  # the vectorised writer used for synthetic models
+    assert np.array_equal(p2, packed), name
+    assert np.array_equal(s2.view(np.uint32), scales.view(np.uint32)), name
+
+
+def test_near_tie_case_discriminates_division_precision():
+    """The golden near-tie row is one where a float64 division would pick a
+    different nibble than the reference's float32 division."""
+    z = np.load(GOLDEN)
+    x, packed, sc = z["near_ties__x"], z["near_ties__packed"], z["near_ties__scales"]
+    q = np.empty(x.shape, np.uint8)
+    q[:, 0::2] = packed & 15
+    q[:, 1::2] = packed >> 4
+    q64 = np.clip(np.rint(x.astype(np.float64) / np.repeat(sc.astype(np.float64), 32, axis=1)) + 8, 0, 15)
+    assert (q64.astype(np.uint8) != q).any()
+
+
+def test_quant_q4_special_cases(oracle_lib):
+    x = np.zeros((1, 32), np.float32)
+    p, s = oracle_lib.quant_q4(x)
+    assert s[0, 0] == 1.0 and (p == 0x88).all()  # amax 0 -> sc 1, every q = 8
+    x[0, 0], x[0, 1] = 3.0, -3.0
+    p, s = oracle_lib.quant_q4(x)
+    assert s[0, 0] == np.float32(3.0 / 8)
+    assert p[0, 0] & 15 == 15  # +amax -> 16 clipped to 15
+    assert p[0, 0] >> 4 == 0  # -amax -> 0
+    # ties to even: amax 8 -> sc 1; 0.5 -> 0 (+8 = 8), 1.5 -> 2 (10), -0.5 -> -0 (8), 2.5 -> 2 (10)
+    x = np.zeros((1, 32), np.float32)
+    x[0, :5] = [8.0, 0.5, 1.5, -0.5, 2.5]
+    p, _ = oracle_lib.quant_q4(x)
+    q = [p[0, 0] & 15, p[0, 0] >> 4, p[0, 1] & 15, p[0, 1] >> 4, p[0, 2] & 15]
+    assert q == [15, 8, 10, 8, 10]
+
+
+def test_quant_q4_brute_force_small(oracle_lib, rng):
+    """Every element's nibble is the nearest representable level (brute force over 0..15)."""
+    x = (rng.standard_normal((8, 64)) * 0.05).astype(np.float32)
+    p, s = oracle_lib.quant_q4(x)
+    deq = oracle_lib.dequant_q4(p, s)
+    for r in range(8):
+        for c in range(64):
+            sc = s[r, c // 32]
+            levels = (np.arange(16) - 8) * np.float64(sc)
+            err = np.abs(levels - x[r, c])
+            best = err.min()
+            assert abs(deq[r, c] - x[r, c]) <= best + 1e-12 + sc * 1e-6
+
+
+def test_dequant_error_bound_and_requant(oracle_lib, rng):
+    x = (rng.standard_normal((16, 96)) * 0.02).astype(np.float32)
+    p, s = oracle_lib.quant_q4(x)
+    d = oracle_lib.dequant_q4(p, s)
+    bound = np.repeat(s, 32, axis=1) * 0.5000001
+    inside = x < np.repeat(s * 7.5, 32, axis=1)  # above 7.5*sc the +8 level clips to +7
+    assert (np.abs(d - x)[inside] <= bound[inside]).all()
+    # the dequantised matrix requantises to the same nibbles where its amax is unchanged
+    p2, s2 = oracle_lib.quant_q4(d)
+    same = np.repeat(s2 == s, 16, axis=1)
+    assert np.array_equal(p2[same], p[same])
+    # vectorised dequant agrees bit for bit
+    assert np.array_equal(pgw.dequant_q4(p, s).view(np.uint32), d.view(np.uint32))
+
+
+def test_dequant_exhaustive_bytes(oracle_lib):
+    """All 256 byte values x scale edge cases: element 2k = low nibble, 2k+1 = high."""
+    packed = np.tile(np.arange(256, dtype=np.uint8), (4, 1))[:, :256].reshape(4, 256)
+    scales = np.array([[1.0] * 16, [0.0] * 16, [1.4e-45] * 16, [3.0e38] * 16], np.float32)
+    d = oracle_lib.dequant_q4(packed, scales)
+    for r in range(4):
+        for b in (0, 1, 0x0F, 0xF0, 0x87, 0x78, 0xFF):
+            lo = (b & 15) - 8
+            hi = (b >> 4) - 8
+            assert d[r, 2 * b] == np.float32(np.float64(lo) * np.float64(scales[r, 0]))
+            assert d[r, 2 * b + 1] == np.float32(np.float64(hi) * np.float64(scales[r, 0]))
+
+
+def test_quant_q8_rules(oracle_lib, rng):
+    """Build-defined Q8 (no reference quantiser; parity unpinned): stated rule only."""
+    x = (rng.standard_normal((4, 64)) * 0.02).astype(np.float32)
+    q, s = oracle_lib.quant_q8g32(x)
+    assert q.dtype == np.int8 and np.abs(q).max() <= 127
+    d = oracle_lib.dequant_q8g32(q, s)
+    assert (np.abs(d - x) <= np.repeat(s, 32, axis=1) * 0.5000001).all()
+    q2, s2 = pgw.quant_q8g32(x)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+    qr, sr = oracle_lib.quant_q8row(x)
+    qr2, sr2 = pgw.quant_q8row(x)
+    assert np.array_equal(qr, qr2) and np.array_equal(sr, sr2)
+    dr = oracle_lib.dequant_q8row(qr, sr)
+    assert (np.abs(dr - x) <= sr[:, None] * 0.5000001).all()
