@@ -1,0 +1,375 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X fused Q4 decode step.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Headline (value): decode tok/s of the 135M Q4 model at batch 1 -- BASELINE
+config 1: SmolLM2-135M shape, weights N(0, 0.02) from seed 0 quantised by the
+converter's quant_q4, a 32-token prompt uniform over the vocab (seed 1),
+greedy decode.  A step is one decode token; K chained steps are timed after
+the prompt has been prefilled, with the weights and KV cache resident in HBM.
+
+One JSON line on stdout carries, besides the driver's fields:
+  roofline      the dominant decode-phase kernel: algorithmic bytes per launch
+                / its mean duration, HIP events on the model's stream
+  cpu_baseline  the oracle (C restatement of engine/infer.js, fp64 accumulate,
+                1 thread) on a bounded sample of the same decode
+  gemv_sweep    config 2: Q4 / Q8 group-32 GEMV GB/s on the 360M shapes
+                (warm = MALL-resident, cold = rotating >= 1 GiB of copies,
+                stacked = 32 matrices per launch)
+  configs       config 3 (prompt-lookup speculation, k = 4 / 8), config 4
+                (GPT-2 124M), config 5 (362M, fp16 KV, 1536-token prefill)
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "microllm-lab_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+import numpy as np  # noqa: E402
+
+METRIC = "decode tok/s (135M Q4, bs1) + Q4 GEMV GB/s as % of 8 TB/s HBM peak"
+HBM_PEAK_GBS = 8000.0
+PHASES = ("QKV", "ATTN", "O", "UP", "DOWN", "LM", "ARGMAX")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- bytes
+def q4_bytes(rows, cols):
+    return rows * cols // 2 + rows * (cols // 32) * 4
+
+
+def phase_bytes(cfg, seq, kv_bytes=4):
+    """Algorithmic bytes per launch of each phase at one decode token with `seq`
+    positions in the cache: weights + activations read and written."""
+    D, FF, V = cfg.d_model, cfg.d_ff, cfg.vocab_size
+    hd = D // cfg.n_heads
+    kvd = cfg.n_kv_heads * hd
+    qkv_rows = D + 2 * kvd
+    return {
+        "QKV": q4_bytes(qkv_rows, D) + 4 * D * 2 + 4 * qkv_rows,
+        "ATTN": 2 * cfg.n_kv_heads * seq * hd * kv_bytes + 4 * D + 4 * (D + cfg.n_heads * 2),
+        "O": q4_bytes(D, D) + 4 * D + 4 * D * 2,
+        "UP": (1 if cfg.arch == "gpt2" else 2) * q4_bytes(FF, D) + 4 * D * 2 + 4 * FF,
+        "DOWN": q4_bytes(D, FF) + 4 * FF + 4 * D * 2,
+        "LM": q4_bytes(V, D) + 4 * D * 2 + 4 * V,
+        "ARGMAX": 0,
+    }
+
+
+def token_bytes(cfg, seq, kv_bytes=4):
+    """BASELINE.md's per-token algorithmic bytes: Q4 weights + norms + KV read."""
+    D, FF = cfg.d_model, cfg.d_ff
+    hd = D // cfg.n_heads
+    kvd = cfg.n_kv_heads * hd
+    mats = q4_bytes(D + 2 * kvd, D) + q4_bytes(D, D) + (1 if cfg.arch == "gpt2" else 2) * q4_bytes(FF, D) + q4_bytes(D, FF)
+    weights = cfg.n_layers * mats + q4_bytes(cfg.vocab_size, D)
+    norms = (2 * cfg.n_layers + 1) * D * 4
+    kv = 2 * cfg.n_kv_heads * hd * kv_bytes * cfg.n_layers * seq
+    return weights + norms + kv
+
+
+# ---------------------------------------------------------------- decode
+def bench_decode(mllm, pgw, torch, args):
+    cfg = pgw.CONFIGS["smollm2-135m"]
+    t = time.time()
+    bundle = pgw.parse_pgw(pgw.make_llama(cfg, seed=0))
+    log(f"[bench] 135M model generated in {time.time() - t:.1f}s")
+    prompt = [int(v) for v in np.random.default_rng(1).integers(0, cfg.vocab_size, 32)]
+    g = mllm.PetitGPT(bundle, exec_mode=args.exec_mode)
+    # warmup: W chained steps after a prefill
+    g.resetCache()
+    g.forwardPrompt(prompt)
+    if args.warmup > 0:
+        g.decodeChain(g.last_argmax, args.warmup)
+    # timed region: K chained decode steps after an (untimed) prefill
+    g.resetCache()
+    g.forwardPrompt(prompt)
+    first = g.last_argmax
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ids = g.decodeChain(first, args.steps)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    gpu_ms, n = g.last_timing()
+    assert n == args.steps == len(ids)
+    wall = t1 - t0
+    # per-phase kernel times (events around each launch, same stream)
+    g.resetCache()
+    g.forwardPrompt(prompt)
+    prof = g.profile_decode(first, 32)
+    seq_mean = len(prompt) + 16
+    pb = phase_bytes(cfg, seq_mean)
+    per_token_us = {ph: prof[ph] * (cfg.n_layers if ph in ("QKV", "ATTN", "O", "UP", "DOWN") else 1) for ph in PHASES}
+    dom = max(per_token_us, key=per_token_us.get)
+    achieved = pb[dom] / (prof[dom] * 1e-6) / 1e9
+    g.destroy()
+    mean_seq = len(prompt) + (args.steps + 1) / 2
+    step_bytes = token_bytes(cfg, mean_seq)
+    return {
+        "value": args.steps / wall,
+        "ms_per_step": wall / args.steps * 1e3,
+        "kernel_ms_per_step": gpu_ms / args.steps,
+        "first_ids": ids[:8],
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"k_phase<{dom}> (decode phase {dom}, 135M, seq ~{seq_mean})",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 5),
+            "traffic": None,
+            "bytes_per_launch": pb[dom],
+            "us_per_launch": round(prof[dom], 3),
+        },
+        "phase_us": {k: round(v, 3) for k, v in prof.items()},
+        "decode_step_gbs": round(step_bytes / (wall / args.steps) / 1e9, 2),
+        "decode_step_bytes": step_bytes,
+    }
+
+
+def bench_cpu(pgw, oracle, budget_s):
+    """The oracle (infer.js arithmetic in C, one thread) on the same model:
+    prefill 32 tokens untimed, then time greedy decode steps for ~budget_s."""
+    cfg = pgw.CONFIGS["smollm2-135m"]
+    bundle = pgw.parse_pgw(pgw.make_llama(cfg, seed=0))
+    prompt = [int(v) for v in np.random.default_rng(1).integers(0, cfg.vocab_size, 32)]
+    m = oracle.OracleModel(bundle)
+    lg = m.forward_prompt(prompt)
+    tok = oracle.argmax(lg)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        tok = oracle.argmax(m.forward_decode(tok))
+        n += 1
+        if time.perf_counter() - t0 > budget_s or n >= 256:
+            break
+    dt = time.perf_counter() - t0
+    m.close()
+    return {
+        "value": round(n / dt, 3),
+        "unit": "tok/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"135M Q4 greedy decode, {n} steps after a 32-token prompt, oracle/mllm_oracle.c "
+                  f"(engine/infer.js fp64 arithmetic), 1 thread, host nproc={os.cpu_count()}",
+    }
+
+
+# ---------------------------------------------------------------- GEMV sweep
+def bench_gemv(torch, abi, pgw):
+    shapes = [(960, 960), (320, 960), (2560, 960), (960, 2560), (49152, 960)]
+    stream = torch.cuda.current_stream()
+    sp = C.c_void_p(stream.cuda_stream)
+    rng = np.random.default_rng(2)
+    out = []
+    for fmt in ("q4", "q8g32"):
+        for (m, n) in shapes:
+            wbytes = m * n // 2 if fmt == "q4" else m * n
+            sbytes = m * (n // 32) * 4
+            algo = wbytes + sbytes + 4 * n + 4 * m
+            copies = max(4, math.ceil((1 << 30) / (wbytes + sbytes)))
+            W = torch.randint(0, 256, (copies, wbytes), dtype=torch.uint8, device="cuda")
+            S = torch.empty((copies, sbytes // 4), dtype=torch.float32, device="cuda").uniform_(1e-3, 1e-2)
+            x = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).cuda()
+            y = torch.empty(m, dtype=torch.float32, device="cuda")
+
+            def launch(i):
+                if fmt == "q4":
+                    rc = abi.lib().mllm_gemv_q4(m, n, W[i].data_ptr(), S[i].data_ptr(), 32, x.data_ptr(),
+                                                y.data_ptr(), sp)
+                else:
+                    rc = abi.lib().mllm_gemv_q8_g32(m, n, W[i].data_ptr(), S[i].data_ptr(), x.data_ptr(),
+                                                    y.data_ptr(), sp)
+                abi.check("gemv", rc)
+
+            res = {"fmt": fmt, "shape": [m, n], "bytes": algo}
+            for mode in ("warm", "cold"):
+                reps = 200 if mode == "warm" else max(200, copies)  # cold: every copy once, >= 1 GiB
+                for i in range(10):
+                    launch(0 if mode == "warm" else i % copies)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for i in range(reps):
+                    launch(0 if mode == "warm" else i % copies)
+                e1.record(stream)
+                e1.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / reps
+                res[f"{mode}_us"] = round(us, 3)
+                res[f"{mode}_gbs"] = round(algo / us / 1e3, 1)
+            if fmt == "q4":
+                # layer-stacked: 32 distinct matrices per launch
+                cnt = 32
+                groups = max(1, copies // cnt)
+                tabs = []
+                for gi in range(min(groups, 64)):
+                    idx = [(gi * cnt + j) % copies for j in range(cnt)]
+                    tp = torch.tensor([W[i].data_ptr() for i in idx], dtype=torch.int64, device="cuda")
+                    ts = torch.tensor([S[i].data_ptr() for i in idx], dtype=torch.int64, device="cuda")
+                    tx = torch.tensor([x.data_ptr()] * cnt, dtype=torch.int64, device="cuda")
+                    ys = torch.empty((cnt, m), dtype=torch.float32, device="cuda")
+                    ty = torch.tensor([ys[j].data_ptr() for j in range(cnt)], dtype=torch.int64, device="cuda")
+                    tabs.append((tp, ts, tx, ty, ys))
+                reps = 100
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                for i in range(3):
+                    tp, ts, tx, ty, _ = tabs[i % len(tabs)]
+                    abi.check("batched", abi.lib().mllm_gemv_q4_batched(cnt, m, n, tp.data_ptr(), ts.data_ptr(),
+                                                                        tx.data_ptr(), ty.data_ptr(), sp))
+                e0.record(stream)
+                for i in range(reps):
+                    tp, ts, tx, ty, _ = tabs[i % len(tabs)]
+                    abi.check("batched", abi.lib().mllm_gemv_q4_batched(cnt, m, n, tp.data_ptr(), ts.data_ptr(),
+                                                                        tx.data_ptr(), ty.data_ptr(), sp))
+                e1.record(stream)
+                e1.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / reps
+                res["stacked32_us"] = round(us, 3)
+                res["stacked32_gbs"] = round(cnt * algo / us / 1e3, 1)
+                del tabs
+            res["cold_frac_hbm"] = round(res["cold_gbs"] / HBM_PEAK_GBS, 4)
+            out.append(res)
+            del W, S
+            torch.cuda.empty_cache()
+            log(f"[bench] gemv {fmt} {m}x{n}: {res}")
+    return out
+
+
+# ---------------------------------------------------------------- configs 3-5
+def spans_prompt(rng, vocab, length, copy_frac=0.4):
+    out = []
+    while len(out) < length:
+        n = int(rng.integers(8, 33))
+        if out and rng.random() < copy_frac and len(out) > n:
+            s = int(rng.integers(0, len(out) - n))
+            out += out[s:s + n]
+        else:
+            out += [int(v) for v in rng.integers(0, vocab, n)]
+    return out[:length]
+
+
+def bench_configs(mllm, pgw, args):
+    res = {}
+    # config 3: prompt-lookup speculation on the 135M shape
+    cfg = pgw.CONFIGS["smollm2-135m"]
+    g = mllm.PetitGPT(pgw.parse_pgw(pgw.make_llama(cfg, seed=0)), exec_mode=args.exec_mode)
+    prompt = spans_prompt(np.random.default_rng(3), cfg.vocab_size, 512)
+    base = g.generate(prompt, maxNewTokens=256, mode="chain")
+    base = g.generate(prompt, maxNewTokens=256, mode="chain")
+    spec3 = {"prompt": 512, "new": 256, "chain_tok_s": round(255 / ((base["totalMs"] - base["ttftMs"]) / 1e3), 1)}
+    for k in (4, 8):
+        r = g.generate(prompt, maxNewTokens=256, mode="spec", specK=k)
+        r = g.generate(prompt, maxNewTokens=256, mode="spec", specK=k)
+        spec3[f"k{k}"] = {
+            "tok_s": round(255 / ((r["totalMs"] - r["ttftMs"]) / 1e3), 1),
+            "specHits": r["specHits"],
+            "specTries": r["specTries"],
+            "same_as_greedy": r["generatedIds"] == base["generatedIds"],
+        }
+    g.destroy()
+    res["spec_135m"] = spec3
+    # config 4: GPT-2 124M, 16-token prompt, 256 tokens with argmaxGpt2
+    cfg = pgw.CONFIGS["gpt2-124m"]
+    g = mllm.PetitGPT(pgw.parse_pgw(pgw.make_gpt2(cfg, seed=0)), exec_mode=args.exec_mode)
+    prompt = [int(v) for v in np.random.default_rng(4).integers(0, cfg.vocab_size, 16)]
+    r = g.generate(prompt, maxNewTokens=256, mode="chain")
+    r = g.generate(prompt, maxNewTokens=256, mode="chain")
+    res["gpt2_124m"] = {"decode_tok_s": round(255 / ((r["totalMs"] - r["ttftMs"]) / 1e3), 1),
+                        "ttft_ms": round(r["ttftMs"], 2), "distinct_ids": len(set(r["generatedIds"]))}
+    g.destroy()
+    # config 5: 362M, fp16 KV, 1536-token prefill then 512 decode steps to 2048
+    cfg = pgw.CONFIGS["smollm2-360m"]
+    g = mllm.PetitGPT(pgw.parse_pgw(pgw.make_llama(cfg, seed=0)), kv_fp16=True, exec_mode=args.exec_mode)
+    prompt = [int(v) for v in np.random.default_rng(5).integers(0, cfg.vocab_size, 1536)]
+    t0 = time.perf_counter()
+    g.forwardPrompt(prompt)
+    ttft = time.perf_counter() - t0
+    first = g.last_argmax
+    t0 = time.perf_counter()
+    ids = g.decodeChain(first, 511)
+    dt = time.perf_counter() - t0
+    mean_seq = 1536 + 256
+    res["smollm2_360m_fp16kv"] = {"prefill_ms": round(ttft * 1e3, 1), "decode_tok_s": round(len(ids) / dt, 1),
+                                  "decode_step_gbs": round(token_bytes(cfg, mean_seq, 2) / (dt / len(ids)) / 1e9, 1)}
+    g.destroy()
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=127, help="decode steps timed (tokens 2..K+1)")
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--exec-mode", type=int, default=1, help="1 graph (default), 2 direct launches, 0 persistent")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-configs", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the decode step is batch-1 and single-device, see DESIGN.md for how it would shard", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.steps + args.warmup + 40 > 2048:
+        print("--steps/--warmup out of range for a 2048 context", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import mllm
+    from mllm import abi, pgw
+
+    abi.lib()
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dec = bench_decode(mllm, pgw, torch, args)
+    log(f"[bench] decode {dec['value']:.1f} tok/s, phases {dec['phase_us']}")
+    line = {
+        "metric": METRIC,
+        "value": round(dec["value"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4 weights, f32 arithmetic",
+        "data": "synthetic: N(0,0.02) weights (seed 0) quantised by quant_q4; 32 prompt ids uniform (seed 1)",
+        "config": {"workload": "smollm2-135m-q4 greedy decode, 32-token prompt, batch 1 (BASELINE config 1)",
+                   "exec_mode": args.exec_mode, "kv_cache": "f32"},
+        "roofline": dec["roofline"],
+        "kernel_ms_per_step": round(dec["kernel_ms_per_step"], 4),
+        "phase_us": dec["phase_us"],
+        "decode_step_gbs": dec["decode_step_gbs"],
+        "decode_step_bytes": dec["decode_step_bytes"],
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = bench_cpu(pgw, __import__("oracle"), args.cpu_seconds)
+        line["speedup_vs_cpu"] = round(line["value"] / line["cpu_baseline"]["value"], 1)
+    if not args.no_sweep:
+        sweep = bench_gemv(torch, abi, pgw)
+        line["gemv_sweep"] = sweep
+        best = max(r["cold_gbs"] for r in sweep if r["fmt"] == "q4")
+        line["gemv_q4_best_cold_frac_hbm"] = round(best / HBM_PEAK_GBS, 4)
+    if not args.no_configs:
+        line["configs"] = bench_configs(mllm, pgw, args)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

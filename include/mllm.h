@@ -64,7 +64,7 @@ int mllm_gemv_q8(int m, int n, const int8_t *q, const float *scale, const float 
 
 /* kernels.rs:59-97 gemv_q4(m, n, packed, scale, group, x, y) and
  * infer.js:88-116 gemvQ4: y[i] = sum_g scale[i][g] * sum_k (nib - 8) * x[g*32+k].
- * group must be 32; n % 32 == 0. */
+ * group must be 32; n % 32 == 0; packed and x 16-byte aligned. */
 int mllm_gemv_q4(int m, int n, const uint8_t *packed, const float *scale, int group, const float *x, float *y,
                  void *stream);
 
@@ -78,7 +78,8 @@ int mllm_gemm_q4(int t, int m, int n, const uint8_t *packed, const float *scale,
                  void *stream);
 
 /* No reference counterpart: one launch over `count` Q4 GEMVs of the same
- * shape (a layer stack), arrays of device pointers in device memory. */
+ * shape (a layer stack), arrays of device pointers in device memory (every
+ * packed and x pointer 16-byte aligned). */
 int mllm_gemv_q4_batched(int count, int m, int n, const uint8_t *const *packed, const float *const *scale,
                          const float *const *x, float *const *y, void *stream);
 
@@ -172,10 +173,26 @@ int mllm_decode_chain(mllm_model *model, int32_t first, int n_steps, int32_t eos
 /* model.gemv(name, x, y) (infer.js:338-346): host x [cols] -> host y [rows]. */
 int mllm_model_gemv(mllm_model *model, const char *name, const float *x, float *y);
 
-/* Execution mode of the decode step: 0 = one persistent kernel per pass
- * (grid barriers between phases), 1 = one kernel per phase replayed from a
- * HIP graph.  Default: 0. */
+/* Execution mode of the decode step: 1 (default) = one kernel per phase, a
+ * chained decode step replayed from a HIP graph; 2 = the same kernels
+ * launched directly (for profilers); 0 = one persistent cooperative kernel per
+ * launch with grid barriers between phases; 3 = one persistent cooperative
+ * kernel per launch whose work items wait only for the items they read
+ * (per-item completion flags).  Results are bit-identical across modes. */
 int mllm_set_exec_mode(mllm_model *model, int mode);
+
+/* GpuPetitGPT.lastTiming {n, gpuMs} (webgpu.js:1143-1160): the time between
+ * HIP events recorded on the model's stream immediately before and after the
+ * kernels of the last forward / chain call, and the tokens it produced. */
+int mllm_last_timing(const mllm_model *model, float *gpu_ms, int *n_tokens);
+
+/* Per-phase timing of the decode step, the per-kernel counterpart of
+ * lastTiming (webgpu.js:1143-1160): runs n_steps chained steps from token
+ * `first` at position cacheLen, launching each phase kernel directly with HIP
+ * events recorded on the model's stream around it, and writes the mean
+ * microseconds per launch of the phases QKV, ATTN, O, UP, DOWN, LM, ARGMAX to
+ * phase_us[0..7).  cacheLen advances by n_steps. */
+int mllm_profile_decode(mllm_model *model, int32_t first, int n_steps, float *phase_us);
 
 /* Bytes of device memory the model holds (GpuPetitGPT.bytesAllocated). */
 uint64_t mllm_model_device_bytes(const mllm_model *model);

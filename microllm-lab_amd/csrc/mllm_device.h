@@ -141,60 +141,118 @@ __device__ __forceinline__ void stage_group_sums(const float *xs, float *xsum, i
   __syncthreads();
 }
 
+// Copy m rows x[t*ldx + i] (i < n, n % 32 == 0, 16-byte aligned rows) into
+// the skewed layout.  Loads go out in batches of 4 float4 per thread before
+// any LDS store, so a batch costs one memory latency, not one per element.
+__device__ __forceinline__ void stage_rows(const float *__restrict__ x, int ldx, int m, int n, float *xs) {
+  const int nq = n >> 2, total = m * nq, ng = n >> 5;
+  for (int base = 0; base < total; base += 4 * WG) {
+    float4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int f = base + threadIdx.x + k * WG;
+      if (f < total) {
+        const int t = f / nq, q = f - t * nq;
+        v[k] = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + 4 * q);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int f = base + threadIdx.x + k * WG;
+      if (f < total) {
+        const int t = f / nq, i = 4 * (f - t * nq);
+        *reinterpret_cast<float4 *>(xs + (t * ng + (i >> 5)) * XS + (i & 31)) = v[k];
+      }
+    }
+  }
+}
+
 // Plain staging of m vectors x[t*ldx + i] (i < n) into the skewed layout.
 __device__ __forceinline__ void stage_plain(const float *__restrict__ x, int ldx, int m, int n, float *xs,
                                             float *xsum) {
-  const int ng = n >> 5;
-  for (int t = 0; t < m; ++t)
-    for (int i = threadIdx.x; i < n; i += WG) xs[(t * ng + (i >> 5)) * XS + (i & 31)] = x[(size_t)t * ldx + i];
+  stage_rows(x, ldx, m, n, xs);
   __syncthreads();
-  stage_group_sums(xs, xsum, m, ng);
+  stage_group_sums(xs, xsum, m, n >> 5);
 }
 
-// Q4 GEMV over rows [row0, row0 + nrows) of W for m staged vectors:
-// out[t*ostride + r] = sum_g sc * (sum_k q*x - 8*xsum).  part needs m*SUB_CH floats.
-// gfirst = threadIdx.x % ng and gstep = WG % ng are precomputed by the caller.
+// Sum of a row's n group partials in a fixed order: eight interleaved
+// accumulators (k mod 8) so the LDS reads overlap, then a fixed tree.
+__device__ __forceinline__ float row_sum(const float *p, int n) {
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int k = 0;
+  for (; k + 8 <= n; k += 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j] += p[k + j];
+  }
+  for (int j = 0; k < n; ++k, ++j) a[j] += p[k];
+  return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+}
+
+// ---------------------------------------------------------------- tiles
+// A tile is up to two contiguous row ranges [r0a, r0a+na) and [r0b, r0b+nb)
+// of one matrix (two ranges let a QKV tile hold both RoPE partners d and
+// d+32 of a head).  Its chunks are loaded into registers first (tile_load),
+// so the loads are in flight while the activations are staged, then
+// consumed by tile_compute.  C = chunks per thread.
+template <int C>
+struct TileRegs {
+  uint4 w[C];
+  float s[C];
+};
+
+template <int C>
+__device__ __forceinline__ void tile_load(const Q4Mat &W, int r0a, int na, int r0b, int ng, int nch,
+                                          TileRegs<C> &R) {
+  const int split = na * ng;
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const int c = threadIdx.x + j * WG;
+    if (c < nch) {
+      const size_t gc = c < split ? (size_t)r0a * ng + c : (size_t)r0b * ng + (c - split);
+      R.w[j] = W.q[gc];
+      R.s[j] = W.s[gc];
+    }
+  }
+}
+
+// out[t*ostride + r] for tile row r in [0, nrows): rows of range a first.
+// part needs m*nch floats of LDS.  gfirst = threadIdx.x % ng, gstep = WG % ng.
+template <int C>
+__device__ __forceinline__ void tile_compute(const TileRegs<C> &R, int nrows, int ng, int nch, int m,
+                                             const float *xs, const float *xsum, int gfirst, int gstep,
+                                             float *part, float *out, int ostride) {
+  int g = gfirst;
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const int c = threadIdx.x + j * WG;
+    if (c < nch) {
+      for (int t = 0; t < m; ++t) {
+        const float d = q4_chunk_dot(R.w[j], xs + (t * ng + g) * XS);
+        part[t * nch + c] = (d - 8.f * xsum[t * ng + g]) * R.s[j];
+      }
+    }
+    g += gstep;
+    if (g >= ng) g -= ng;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nrows * m; i += WG) {
+    const int t = i / nrows, r = i - t * nrows;
+    out[t * ostride + r] = row_sum(part + t * nch + r * ng, ng);
+  }
+  __syncthreads();
+}
+
+// Q4 GEMV over rows [row0, row0 + nrows) of W for m staged vectors, in
+// sub-tiles of at most SUB_CH chunks: out[t*ostride + r].
 __device__ __forceinline__ void gemv_q4_rows(const Q4Mat &W, int row0, int nrows, int m, const float *xs,
                                              const float *xsum, int ng, int gfirst, int gstep, float *part,
                                              float *out, int ostride) {
-  const int tid = threadIdx.x;
   const int rows_per_sub = SUB_CH / ng > 0 ? SUB_CH / ng : 1;
   for (int rs = 0; rs < nrows; rs += rows_per_sub) {
     const int nr = min(rows_per_sub, nrows - rs);
-    const int nch = nr * ng;
-    const size_t cbase = (size_t)(row0 + rs) * ng;
-    uint4 w[CPT];
-    float s[CPT];
-#pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      const int c = tid + j * WG;
-      if (c < nch) {
-        w[j] = W.q[cbase + c];
-        s[j] = W.s[cbase + c];
-      }
-    }
-    int g = gfirst;
-#pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      const int c = tid + j * WG;
-      if (c < nch) {
-        for (int t = 0; t < m; ++t) {
-          const float d = q4_chunk_dot(w[j], xs + (t * ng + g) * XS);
-          part[t * nch + c] = (d - 8.f * xsum[t * ng + g]) * s[j];
-        }
-      }
-      g += gstep;
-      if (g >= ng) g -= ng;
-    }
-    __syncthreads();
-    for (int i = tid; i < nr * m; i += WG) {
-      const int t = i / nr, r = i - t * nr;
-      const float *p = part + t * nch + r * ng;
-      float acc = 0.f;
-      for (int k = 0; k < ng; ++k) acc += p[k];
-      out[t * ostride + rs + r] = acc;
-    }
-    __syncthreads();
+    TileRegs<CPT> R;
+    tile_load<CPT>(W, row0 + rs, nr, 0, ng, nr * ng, R);
+    tile_compute<CPT>(R, nr, ng, nr * ng, m, xs, xsum, gfirst, gstep, part, out + rs, ostride);
   }
 }
 

@@ -4,7 +4,7 @@
 // One decode step = L x [QKV, ATTN, O, UP, DOWN] + LM + ARGMAX phases
 // (engine/infer.js:579-601; the reference GPU runs the same graph as 244
 // dispatches, engine/webgpu-metal.js:1242-1322):
-//   QKV   (one workgroup per 64-row head tile of blocks.i.attn.qkv)
+//   QKV   16-row tiles of blocks.i.attn.qkv holding RoPE partner rows d, d+32
 //         prologue: embed (layer 0) or load x; RMSNorm/LayerNorm in LDS
 //         epilogue: bias (gpt2), RoPE (llama), q -> scratch, k/v -> KV cache
 //   ATTN  (one workgroup per (token, 256-position split, head))
@@ -13,15 +13,18 @@
 //   UP    prologue: norm2; gate and up rows of the same index -> silu(g)*u
 //         (gpt2: fc + bias -> GELU-tanh)
 //   DOWN  epilogue x += W_2.h (+ bias)
-//   LM    prologue: final norm; logits + per-tile argmax (gpt2 chain: 3-gram
+//   LM    prologue: final norm; grid-stride row tiles with the next tile's
+//         weights in flight; logits + per-tile argmax (gpt2 chain: 3-gram
 //         block and repetition penalty of infer.js:252-287)
 //   ARGMAX one workgroup: first maximum over tiles; chained decode feeds it
 //         back as the next input token (CHAIN_TOK, webgpu-metal.js:609-610).
+// Every GEMV phase issues its weight loads before it stages the activations,
+// so the two memory latencies overlap.
 //
-// Execution: mode 0 runs every phase of a pass (or of n chained steps) in one
-// persistent cooperative kernel with a grid barrier between phases; mode 1
-// launches one kernel per phase and replays a captured HIP graph per chained
-// step.  Both modes run the same per-item device code.
+// Execution: mode 1 (default) replays a HIP graph of one kernel per phase;
+// mode 2 launches the same kernels directly; mode 0 runs all phases in one
+// persistent cooperative kernel with a grid barrier between phases.  All
+// modes run the same per-item device code.
 //
 // Every per-token computation (norm, GEMV row, attention split, combine,
 // argmax) runs the same instruction sequence whatever the number of tokens in
@@ -46,6 +49,9 @@ constexpr int HD = 64;    // head dimension of every supported config
 constexpr int ACH = 256;  // positions per attention split (one per thread)
 constexpr int MAXT = 16;  // tokens per pass (upper bound; LDS sets the real one)
 constexpr int APS = 68;   // floats per attention partial: m, l, pad, pad, acc[64]
+constexpr int TC = 2;     // tile capacity of the decode phases: TC * WG chunks
+constexpr int TILE_TARGET = 320;  // chunks per GEMV tile (~0.15 us of VALU on one CU)
+constexpr int QSPLIT = 4;         // QKV tiles per head
 constexpr unsigned kSpinLimit = 1u << 22;
 
 enum Phase { PH_QKV = 0, PH_ATTN, PH_O, PH_UP, PH_DOWN, PH_LM, PH_ARGMAX, PH_COUNT };
@@ -65,13 +71,15 @@ struct PassState {
   int eos;       // chain stop id (-1: none)
   int done;      // chain reached eos
   int n_hist;    // tokens in hist[] (gpt2 argmax history / chain output)
-  int err;       // barrier time-out
+  int err;       // barrier / flag-wait time-out
+  int bad_tok;   // ARGMAX found no finite maximum (chain fed token 0 instead)
+  int epoch;     // mode 3: epoch of the launch's first step
   int tok[MAXT];
   int res[MAXT];  // argmax per lm row
 };
 
 struct DecParams {
-  int arch, L, D, NH, NKV, FF, V, max_seq, rd, kv_fp16, nsplit_max;
+  int arch, L, D, NH, NKV, FF, V, max_seq, kv_fp16, nsplit_max;
   float eps, attn_scale;
   const LayerW *layers;
   Q4Mat lm;
@@ -82,12 +90,16 @@ struct DecParams {
   float *attp;  // [MAXT][NH][nsplit_max][APS]
   float *ff;    // [MAXT][FF]
   float *logits;  // [MAXT][V]
-  float *amv;     // [MAXT][lm_items]
+  float *amv;     // [MAXT][lm_tiles]
   int *ami;
-  int lm_items, lm_rpt, o_rpt, up_rpt, dn_rpt;
+  int o_rpt, up_rpt, dn_rpt, lm_rpt, lm_tiles, lm_grid;
   PassState *st;
   int *hist;      // [max_seq + 1]
   unsigned *bar;  // grid barrier: count, generation
+  // mode 3 item flags: per layer [qkv | attn | o | up | down], then lm[grid], argmax
+  int *flags;
+  int fl_stride, fl_qkv, fl_attn, fl_o, fl_up, fl_down, fl_lm, fl_argmax;
+  int n_o, n_up, n_down;
 };
 
 // ---------------------------------------------------------------- helpers
@@ -97,105 +109,236 @@ __device__ __forceinline__ size_t kv_index(const DecParams &P, int li, int which
   return ((((size_t)li * 2 + which) * P.NKV + h) * P.max_seq + pos) * HD;
 }
 
+// Norm gains (and LayerNorm betas) of this thread's elements i = tid + k*WG,
+// loaded into registers up front (d_model <= 1024).
+struct Gains {
+  float g[4], b[4];
+};
+
+__device__ __forceinline__ Gains load_gains(const DecParams &P, const float *w) {
+  Gains G;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int i = threadIdx.x + k * WG;
+    if (i < P.D) {
+      G.g[k] = w[i];
+      G.b[k] = P.arch == 1 ? w[P.D + i] : 0.f;
+    }
+  }
+  return G;
+}
+
 // Normalise m staged raw vectors in place (skewed layout): RMSNorm
 // (infer.js:134-143) or LayerNorm (infer.js:147-164, eps 1e-5).
-__device__ void norm_staged(const DecParams &P, float *xs, int m, const float *w, float *red) {
+__device__ void norm_staged(const DecParams &P, float *xs, int m, const Gains &G, float *red) {
   const int D = P.D, ng = D >> 5;
   for (int t = 0; t < m; ++t) {
     float *xt = xs + t * ng * XS;
     if (P.arch == 1) {
       float s = 0.f;
-      for (int i = threadIdx.x; i < D; i += WG) s += xt[skew(i)];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + k * WG;
+        if (i < D) s += xt[skew(i)];
+      }
       const float mean = block_sum(s, red) / (float)D;
       float v = 0.f;
-      for (int i = threadIdx.x; i < D; i += WG) {
-        const float d = xt[skew(i)] - mean;
-        v = __builtin_fmaf(d, d, v);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + k * WG;
+        if (i < D) {
+          const float d = xt[skew(i)] - mean;
+          v = __builtin_fmaf(d, d, v);
+        }
       }
       const float inv = 1.0f / sqrtf(block_sum(v, red) / (float)D + 1e-5f);
-      for (int i = threadIdx.x; i < D; i += WG) {
-        const int k = skew(i);
-        xt[k] = __builtin_fmaf((xt[k] - mean) * inv, w[i], w[D + i]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + k * WG;
+        if (i < D) {
+          const int j = skew(i);
+          xt[j] = __builtin_fmaf((xt[j] - mean) * inv, G.g[k], G.b[k]);
+        }
       }
     } else {
       float s = 0.f;
-      for (int i = threadIdx.x; i < D; i += WG) s = __builtin_fmaf(xt[skew(i)], xt[skew(i)], s);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + k * WG;
+        if (i < D) s = __builtin_fmaf(xt[skew(i)], xt[skew(i)], s);
+      }
       const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + P.eps);
-      for (int i = threadIdx.x; i < D; i += WG) {
-        const int k = skew(i);
-        xt[k] = xt[k] * inv * w[i];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + k * WG;
+        if (i < D) {
+          const int j = skew(i);
+          xt[j] = xt[j] * inv * G.g[k];
+        }
       }
     }
   }
   __syncthreads();
 }
 
-// LDS carve-up shared by the GEMV phases.
+// Stage the residual stream rows [t0, t0+m) of P.x, normalise them with
+// the prefetched gains, and form the group sums.
+__device__ __forceinline__ void stage_normed(const DecParams &P, int t0, int m, const Gains &G, float *xs,
+                                             float *xsum, float *red) {
+  const int D = P.D, ng = D >> 5;
+  stage_rows(P.x + (size_t)t0 * D, D, m, D, xs);
+  __syncthreads();
+  norm_staged(P, xs, m, G, red);
+  stage_group_sums(xs, xsum, m, ng);
+}
+
+// LDS carve-up shared by the GEMV phases (floats):
+// red[16] | xs[m][ng][XS] | xsum[m][ng] | part[m][TC*WG] | out[...]
 struct Lds {
-  float *xs, *xsum, *part, *out, *red;
+  float *red, *xs, *xsum, *part, *out;
 };
 
-__device__ __forceinline__ Lds carve(float *smem, int m, int ng, int out_floats) {
+__device__ __forceinline__ Lds carve(float *smem, int m, int ng) {
   Lds s;
-  s.red = smem;  // 16 floats
+  s.red = smem;
   s.xs = smem + 16;
   s.xsum = s.xs + m * ng * XS;
   s.part = s.xsum + m * ng;
-  s.out = s.part + m * SUB_CH;
-  (void)out_floats;
+  s.out = s.part + m * TC * WG;
   return s;
 }
 
-// ---------------------------------------------------------------- phases
-__device__ void phase_qkv(const DecParams &P, int li, int item, float *smem) {
-  const PassState &S = *P.st;
-  const int m = S.ntok, D = P.D, ng = D >> 5;
-  Lds s = carve(smem, m, ng, m * HD);
-  const LayerW &Lw = P.layers[li];
-  // stage the residual stream (layer 0: embed it, infer.js:360-420)
-  for (int t = 0; t < m; ++t) {
-    float *xt = s.xs + t * ng * XS;
-    if (li == 0) {
-      const int tok = S.tok[t];
-      const uint8_t *row = reinterpret_cast<const uint8_t *>(P.lm.q) + (size_t)tok * (D >> 1);
-      const float *sc = P.lm.s + (size_t)tok * ng;
-      const int pos = min(S.pos0 + t, P.max_seq - 1);
-      for (int i = threadIdx.x; i < D; i += WG) {
-        const int b = row[i >> 1];
-        float v = (float)(((i & 1) ? (b >> 4) : (b & 15)) - 8) * sc[i >> 5];
-        if (P.arch == 1) {
-          if (P.sf) v = v / P.sf[i];
-          v = v + P.wpe[(size_t)pos * D + i];
-        }
-        xt[skew(i)] = v;
-        if (item == 0) P.x[(size_t)t * D + i] = v;
+// ---------------------------------------------------------------- dataflow
+// Mode 3 orders work items with per-item completion flags instead of kernel
+// boundaries or grid barriers.  An item's flag holds the epoch (step number)
+// it last completed; a consumer waits until every producer flag it depends on
+// (up to three contiguous ranges) has reached the current epoch.  Wave 0
+// polls with agent-scope loads and takes an acquire fence; the producer
+// publishes with an agent-scope release store after a workgroup barrier.
+// Waits are bounded: on time-out st->err is set and every later wait of the
+// launch returns at once, so the grid always drains.
+struct Dep {
+  const int *f[3];
+  int n[3];
+  int ep;
+};
+
+__device__ __forceinline__ void dep_wait(const DecParams &P, const Dep &d) {
+  if (d.n[0] + d.n[1] + d.n[2] == 0) return;
+  if (threadIdx.x < 64) {
+    unsigned spins = 0;
+    for (;;) {
+      bool ok = true;
+#pragma unroll
+      for (int r = 0; r < 3; ++r)
+        for (int k = threadIdx.x; k < d.n[r]; k += 64)
+          ok &= __hip_atomic_load(d.f[r] + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= d.ep;
+      if (__all(ok)) break;
+      if (++spins > kSpinLimit || __hip_atomic_load(&P.st->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+        if (threadIdx.x == 0) __hip_atomic_store(&P.st->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
       }
-    } else {
-      for (int i = threadIdx.x; i < D; i += WG) xt[skew(i)] = P.x[(size_t)t * D + i];
+      __builtin_amdgcn_s_sleep(1);
     }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
-  norm_staged(P, s.xs, m, Lw.n1, s.red);
-  stage_group_sums(s.xs, s.xsum, m, ng);
-  gemv_q4_rows(Lw.qkv, item * HD, HD, m, s.xs, s.xsum, ng, threadIdx.x % ng, WG % ng, s.part, s.out, HD);
-  // epilogue
-  const bool is_q = item < P.NH, is_k = !is_q && item < P.NH + P.NKV;
-  const int kvh = is_q ? 0 : (is_k ? item - P.NH : item - P.NH - P.NKV);
-  const int half = P.rd >> 1;
-  for (int e = threadIdx.x; e < m * HD; e += WG) {
-    const int t = e / HD, d = e - t * HD;
-    float v = s.out[e];
+}
+
+__device__ __forceinline__ void dep_signal(int *flag, int ep) {
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(flag, ep, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------- phases
+__device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, int item, const Dep &dep,
+                          float *smem) {
+  const int D = P.D, ng = D >> 5;
+  const int head = item / QSPLIT, quarter = item - head * QSPLIT;
+  const int ra = head * HD + quarter * 8, rb = ra + 32;  // RoPE partners d and d + 32
+  const int nch = 16 * ng;
+  TileRegs<TC> R;
+  tile_load<TC>(Lw.qkv, ra, 8, rb, ng, nch, R);
+  const Gains G = load_gains(P, Lw.n1);
+  dep_wait(P, dep);
+  Lds s = carve(smem, m, ng);
+  const PassState &S = *P.st;
+  const int pos0 = S.pos0;
+  // this thread's epilogue element (m * 16 <= WG): its RoPE table entries or
+  // bias, fetched before the staging so the epilogue does not wait for them
+  const bool is_q = head < P.NH, is_k = !is_q && head < P.NH + P.NKV;
+  const int e_own = threadIdx.x, t_own = e_own >> 4, r_own = e_own & 15;
+  const int d_own = quarter * 8 + (r_own & 7) + (r_own >> 3) * 32;
+  float c_own = 0.f, s_own = 0.f, b_own = 0.f;
+  if (e_own < m * 16) {
     if (P.arch == 1) {
-      v = v + Lw.qkv_b[item * HD + d];
-    } else if (!(!is_q && !is_k) && d < P.rd) {
-      const int pos = S.pos0 + t;
-      const float mate = d < half ? -s.out[t * HD + d + half] : s.out[t * HD + d - half];
-      v = __builtin_fmaf(v, P.rope_cos[(size_t)pos * P.rd + d], mate * P.rope_sin[(size_t)pos * P.rd + d]);
+      b_own = Lw.qkv_b[head * HD + d_own];
+    } else if (is_q || is_k) {
+      const size_t ri = (size_t)(pos0 + t_own) * HD + d_own;
+      c_own = P.rope_cos[ri];
+      s_own = P.rope_sin[ri];
+    }
+  }
+  if (li == 0) {
+    // embed (infer.js:360-420): dequantised tied lm_head row; gpt2 divides by
+    // scale_factors and adds the learned position.  Item 0 writes the residual.
+    for (int t = 0; t < m; ++t) {
+      float *xt = s.xs + t * ng * XS;
+      const int tok = min(max(S.tok[t], 0), P.V - 1);  // host and ARGMAX keep it in range
+      const uint8_t *row = reinterpret_cast<const uint8_t *>(P.lm.q) + (size_t)tok * (D >> 1);
+      const float *sc = P.lm.s + (size_t)tok * ng;
+      const int pos = min(pos0 + t, P.max_seq - 1);
+      int bv[4];
+      float sv[4], sfv[4], pv4[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {  // D <= 1024: at most 4 elements per thread, loads first
+        const int i = threadIdx.x + k * WG;
+        if (i < D) {
+          bv[k] = row[i >> 1];
+          sv[k] = sc[i >> 5];
+          if (P.arch == 1) {
+            sfv[k] = P.sf ? P.sf[i] : 1.f;
+            pv4[k] = P.wpe[(size_t)pos * D + i];
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + k * WG;
+        if (i < D) {
+          float v = (float)(((i & 1) ? (bv[k] >> 4) : (bv[k] & 15)) - 8) * sv[k];
+          if (P.arch == 1) {
+            if (P.sf) v = v / sfv[k];
+            v = v + pv4[k];
+          }
+          xt[skew(i)] = v;
+          if (item == 0) P.x[(size_t)t * D + i] = v;
+        }
+      }
+    }
+    __syncthreads();
+    norm_staged(P, s.xs, m, G, s.red);
+    stage_group_sums(s.xs, s.xsum, m, ng);
+  } else {
+    stage_normed(P, 0, m, G, s.xs, s.xsum, s.red);
+  }
+  tile_compute<TC>(R, 16, ng, nch, m, s.xs, s.xsum, threadIdx.x % ng, WG % ng, s.part, s.out, 16);
+  // epilogue: tile row r < 8 is head dim d = quarter*8 + r, r >= 8 is d + 32
+  const int kvh = is_q ? 0 : (is_k ? head - P.NH : head - P.NH - P.NKV);
+  if (e_own < m * 16) {
+    const int e = e_own, t = t_own, r = r_own, d = d_own;
+    float v = s.out[e];
+    const int pos = pos0 + t;
+    if (P.arch == 1) {
+      v = v + b_own;
+    } else if (is_q || is_k) {
+      const float mate = r < 8 ? -s.out[e + 8] : s.out[e - 8];
+      v = __builtin_fmaf(v, c_own, mate * s_own);
     }
     if (is_q) {
-      P.q[(size_t)t * P.NH * HD + item * HD + d] = v;
+      P.q[(size_t)t * P.NH * HD + head * HD + d] = v;
     } else {
-      const size_t k = kv_index(P, li, is_k ? 0 : 1, kvh, S.pos0 + t) + d;
+      const size_t k = kv_index(P, li, is_k ? 0 : 1, kvh, pos) + d;
       if (P.kv_fp16)
         reinterpret_cast<__half *>(P.kv)[k] = __float2half_rn(v);
       else
@@ -204,144 +347,198 @@ __device__ void phase_qkv(const DecParams &P, int li, int item, float *smem) {
   }
 }
 
-__device__ void phase_attn(const DecParams &P, int li, int item, float *smem) {
-  const PassState &S = *P.st;
+// One (token, split, head) item.  After pos arrives, every load of the item
+// (q, the K rows, the V rows) is issued at once: thread i owns key i of the
+// split; thread (kg, d4) owns V[kg + 16j][4*d4 .. 4*d4+3] for j < 16.
+__device__ void phase_attn(const DecParams &P, int m, int li, int item, const Dep &dep, float *smem) {
+  dep_wait(P, dep);
   const int per_tok = P.NH * P.nsplit_max;
   const int t = item / per_tok;
   const int rem = item - t * per_tok;
   const int sp = rem / P.NH, h = rem - sp * P.NH;
-  if (t >= S.ntok) return;
-  const int pos = S.pos0 + t;
+  if (t >= m) return;
+  const int pos = P.st->pos0 + t;
   const int s0 = sp * ACH;
   if (s0 > pos) return;
   const int cnt = min(ACH, pos + 1 - s0);
   const int kvh = h / (P.NH / P.NKV);
-  float *qs = smem;       // 64
-  float *es = qs + HD;    // 256
-  float *pv = es + ACH;   // 4 x 64
-  float *red = pv + 4 * HD;
-  if (threadIdx.x < HD) qs[threadIdx.x] = P.q[(size_t)t * P.NH * HD + h * HD + threadIdx.x];
-  __syncthreads();
+  float *qs = smem;        // 64
+  float *es = qs + HD;     // 256
+  float *pv = es + ACH;    // 16 x 64
+  float *red = pv + 16 * HD;
   const size_t kbase = kv_index(P, li, 0, kvh, s0), vbase = kv_index(P, li, 1, kvh, s0);
-  float score = -INFINITY;
   const int i = threadIdx.x;
-  if (i < cnt) {
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    if (P.kv_fp16) {
-      const uint4 *kr = reinterpret_cast<const uint4 *>(reinterpret_cast<const __half *>(P.kv) + kbase + (size_t)i * HD);
+  const int d4 = threadIdx.x & 15, kg = threadIdx.x >> 4;
+  float4 kr[HD / 4];
+  float4 vr[16];
+  if (threadIdx.x < HD) qs[threadIdx.x] = P.q[(size_t)t * P.NH * HD + h * HD + threadIdx.x];
+  if (P.kv_fp16) {
+    const __half *kvh16 = reinterpret_cast<const __half *>(P.kv);
+    if (i < cnt) {
+      const uint4 *row = reinterpret_cast<const uint4 *>(kvh16 + kbase + (size_t)i * HD);
 #pragma unroll
       for (int j = 0; j < HD / 8; ++j) {
-        const uint4 u = kr[j];
+        const uint4 u = row[j];
         const __half2 *hp = reinterpret_cast<const __half2 *>(&u);
         const float2 f0 = __half22float2(hp[0]), f1 = __half22float2(hp[1]);
         const float2 f2 = __half22float2(hp[2]), f3 = __half22float2(hp[3]);
-        a0 = __builtin_fmaf(qs[8 * j + 0], f0.x, a0);
-        a1 = __builtin_fmaf(qs[8 * j + 1], f0.y, a1);
-        a2 = __builtin_fmaf(qs[8 * j + 2], f1.x, a2);
-        a3 = __builtin_fmaf(qs[8 * j + 3], f1.y, a3);
-        a0 = __builtin_fmaf(qs[8 * j + 4], f2.x, a0);
-        a1 = __builtin_fmaf(qs[8 * j + 5], f2.y, a1);
-        a2 = __builtin_fmaf(qs[8 * j + 6], f3.x, a2);
-        a3 = __builtin_fmaf(qs[8 * j + 7], f3.y, a3);
+        kr[2 * j] = make_float4(f0.x, f0.y, f1.x, f1.y);
+        kr[2 * j + 1] = make_float4(f2.x, f2.y, f3.x, f3.y);
       }
-    } else {
-      const float4 *kr = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(P.kv) + kbase + (size_t)i * HD);
+    }
 #pragma unroll
-      for (int j = 0; j < HD / 4; ++j) {
-        const float4 k4 = kr[j];
-        a0 = __builtin_fmaf(qs[4 * j + 0], k4.x, a0);
-        a1 = __builtin_fmaf(qs[4 * j + 1], k4.y, a1);
-        a2 = __builtin_fmaf(qs[4 * j + 2], k4.z, a2);
-        a3 = __builtin_fmaf(qs[4 * j + 3], k4.w, a3);
+    for (int j = 0; j < 16; ++j) {
+      const int k = kg + 16 * j;
+      if (k < cnt) {
+        const uint2 u = *reinterpret_cast<const uint2 *>(kvh16 + vbase + (size_t)k * HD + 4 * d4);
+        const __half2 *hp = reinterpret_cast<const __half2 *>(&u);
+        const float2 f0 = __half22float2(hp[0]), f1 = __half22float2(hp[1]);
+        vr[j] = make_float4(f0.x, f0.y, f1.x, f1.y);
       }
+    }
+  } else {
+    const float *kv32 = reinterpret_cast<const float *>(P.kv);
+    if (i < cnt) {
+      const float4 *row = reinterpret_cast<const float4 *>(kv32 + kbase + (size_t)i * HD);
+#pragma unroll
+      for (int j = 0; j < HD / 4; ++j) kr[j] = row[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int k = kg + 16 * j;
+      if (k < cnt) vr[j] = *reinterpret_cast<const float4 *>(kv32 + vbase + (size_t)k * HD + 4 * d4);
+    }
+  }
+  __syncthreads();
+  float score = -INFINITY;
+  if (i < cnt) {
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int j = 0; j < HD / 4; ++j) {
+      a0 = __builtin_fmaf(qs[4 * j + 0], kr[j].x, a0);
+      a1 = __builtin_fmaf(qs[4 * j + 1], kr[j].y, a1);
+      a2 = __builtin_fmaf(qs[4 * j + 2], kr[j].z, a2);
+      a3 = __builtin_fmaf(qs[4 * j + 3], kr[j].w, a3);
     }
     score = ((a0 + a1) + (a2 + a3)) * P.attn_scale;
   }
   const float mx = block_max(score, red);
-  const float e = i < cnt ? expf(score - mx) : 0.f;
-  es[i] = e;
-  const float l = block_sum(e, red);  // contains the barrier that publishes es[]
-  const int d = threadIdx.x & (HD - 1), g4 = threadIdx.x >> 6;
-  float acc = 0.f;
-  if (P.kv_fp16) {
-    const __half *vr = reinterpret_cast<const __half *>(P.kv) + vbase + d;
-    for (int k = g4; k < cnt; k += 4) acc = __builtin_fmaf(es[k], __half2float(vr[(size_t)k * HD]), acc);
-  } else {
-    const float *vr = reinterpret_cast<const float *>(P.kv) + vbase + d;
-    for (int k = g4; k < cnt; k += 4) acc = __builtin_fmaf(es[k], vr[(size_t)k * HD], acc);
+  es[i] = i < cnt ? expf(score - mx) : 0.f;
+  const float l = block_sum(es[i], red);  // contains the barrier that publishes es[]
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int k = kg + 16 * j;
+    if (k < cnt) {
+      const float e = es[k];
+      acc.x = __builtin_fmaf(e, vr[j].x, acc.x);
+      acc.y = __builtin_fmaf(e, vr[j].y, acc.y);
+      acc.z = __builtin_fmaf(e, vr[j].z, acc.z);
+      acc.w = __builtin_fmaf(e, vr[j].w, acc.w);
+    }
   }
-  pv[g4 * HD + d] = acc;
+  *reinterpret_cast<float4 *>(pv + kg * HD + 4 * d4) = acc;
   __syncthreads();
   float *dst = P.attp + ((size_t)(t * P.NH + h) * P.nsplit_max + sp) * APS;
-  if (threadIdx.x < HD) dst[4 + threadIdx.x] = (pv[threadIdx.x] + pv[HD + threadIdx.x]) +
-                                               (pv[2 * HD + threadIdx.x] + pv[3 * HD + threadIdx.x]);
+  if (threadIdx.x < HD) {
+    float a = 0.f;
+    for (int g = 0; g < 16; ++g) a += pv[g * HD + threadIdx.x];
+    dst[4 + threadIdx.x] = a;
+  }
   if (threadIdx.x == 0) {
     dst[0] = mx;
     dst[1] = l;
   }
 }
 
-__device__ void phase_o(const DecParams &P, int li, int item, float *smem) {
-  const PassState &S = *P.st;
-  const int m = S.ntok, D = P.D, ng = D >> 5;
+__device__ void phase_o(const DecParams &P, const LayerW &Lw, int m, int item, const Dep &dep, float *smem) {
+  const int D = P.D, ng = D >> 5;
   const int row0 = item * P.o_rpt;
   const int nr = min(P.o_rpt, D - row0);
-  Lds s = carve(smem, m, ng, m * P.o_rpt);
-  // combine the attention splits (flash-decoding merge, splits in order)
+  TileRegs<TC> R;
+  tile_load<TC>(Lw.proj, row0, nr, 0, ng, nr * ng, R);
+  dep_wait(P, dep);
+  const int pos0 = P.st->pos0;
+  // the residual this thread will update, fetched with the weights
+  const int e0 = threadIdx.x;
+  const bool own = e0 < m * nr;
+  const int et = own ? e0 / nr : 0, er = own ? e0 - et * nr : 0;
+  const float xres = own ? P.x[(size_t)et * D + row0 + er] : 0.f;
+  const float bres = own && P.arch == 1 ? Lw.proj_b[row0 + er] : 0.f;
+  Lds s = carve(smem, m, ng);
+  // combine the attention splits (flash-decoding merge, splits in order);
+  // split 0's values for this thread's (up to 4) elements are loaded first
   for (int t = 0; t < m; ++t) {
-    const int ns = (S.pos0 + t) / ACH + 1;
-    for (int e = threadIdx.x; e < D; e += WG) {
-      const int h = e >> 6, d = e & 63;
-      const float *p = P.attp + (size_t)(t * P.NH + h) * P.nsplit_max * APS;
-      float M = p[0];
-      for (int k = 1; k < ns; ++k) M = fmaxf(M, p[k * APS]);
-      float l = 0.f, a = 0.f;
-      for (int k = 0; k < ns; ++k) {
-        const float w = expf(p[k * APS] - M);
-        l = __builtin_fmaf(p[k * APS + 1], w, l);
-        a = __builtin_fmaf(p[k * APS + 4 + d], w, a);
+    const int ns = (pos0 + t) / ACH + 1;
+    float m0[4], l0[4], a0[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {  // D <= 1024
+      const int e = threadIdx.x + k * WG;
+      if (e < D) {
+        const float *p = P.attp + (size_t)(t * P.NH + (e >> 6)) * P.nsplit_max * APS;
+        m0[k] = p[0];
+        l0[k] = p[1];
+        a0[k] = p[4 + (e & 63)];
       }
-      s.xs[t * ng * XS + skew(e)] = a / l;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int e = threadIdx.x + k * WG;
+      if (e < D) {
+        const int h = e >> 6, d = e & 63;
+        const float *p = P.attp + (size_t)(t * P.NH + h) * P.nsplit_max * APS;
+        float M = m0[k];
+        for (int j = 1; j < ns; ++j) M = fmaxf(M, p[j * APS]);
+        const float w0 = expf(m0[k] - M);
+        float l = __builtin_fmaf(l0[k], w0, 0.f), a = __builtin_fmaf(a0[k], w0, 0.f);
+        for (int j = 1; j < ns; ++j) {
+          const float w = expf(p[j * APS] - M);
+          l = __builtin_fmaf(p[j * APS + 1], w, l);
+          a = __builtin_fmaf(p[j * APS + 4 + d], w, a);
+        }
+        s.xs[t * ng * XS + skew(e)] = a / l;
+      }
     }
   }
   __syncthreads();
   stage_group_sums(s.xs, s.xsum, m, ng);
-  const LayerW &Lw = P.layers[li];
-  gemv_q4_rows(Lw.proj, row0, nr, m, s.xs, s.xsum, ng, threadIdx.x % ng, WG % ng, s.part, s.out, P.o_rpt);
+  tile_compute<TC>(R, nr, ng, nr * ng, m, s.xs, s.xsum, threadIdx.x % ng, WG % ng, s.part, s.out, P.o_rpt);
   for (int e = threadIdx.x; e < m * nr; e += WG) {
     const int t = e / nr, r = e - t * nr;
     float y = s.out[t * P.o_rpt + r];
-    if (P.arch == 1) y = y + Lw.proj_b[row0 + r];
-    float &x = P.x[(size_t)t * D + row0 + r];
-    x = x + y;
+    if (P.arch == 1) y = y + (e == e0 ? bres : Lw.proj_b[row0 + r]);
+    const float x = e == e0 ? xres : P.x[(size_t)t * D + row0 + r];
+    P.x[(size_t)t * D + row0 + r] = x + y;
   }
 }
 
-__device__ void phase_up(const DecParams &P, int li, int item, float *smem) {
-  const PassState &S = *P.st;
-  const int m = S.ntok, D = P.D, ng = D >> 5;
+__device__ void phase_up(const DecParams &P, const LayerW &Lw, int m, int item, const Dep &dep, float *smem) {
+  const int D = P.D, ng = D >> 5;
   const int row0 = item * P.up_rpt;
   const int nr = min(P.up_rpt, P.FF - row0);
-  Lds s = carve(smem, m, ng, 2 * m * P.up_rpt);
-  const LayerW &Lw = P.layers[li];
-  for (int t = 0; t < m; ++t)
-    for (int i = threadIdx.x; i < D; i += WG) s.xs[t * ng * XS + skew(i)] = P.x[(size_t)t * D + i];
-  __syncthreads();
-  norm_staged(P, s.xs, m, Lw.n2, s.red);
-  stage_group_sums(s.xs, s.xsum, m, ng);
+  const bool gpt2 = P.arch == 1;
+  TileRegs<TC> Rg, Ru;
+  tile_load<TC>(Lw.w1, row0, nr, 0, ng, nr * ng, Rg);
+  if (!gpt2) tile_load<TC>(Lw.w3, row0, nr, 0, ng, nr * ng, Ru);
+  const Gains G = load_gains(P, Lw.n2);
+  const bool own = (int)threadIdx.x < m * nr;
+  const float fcb = gpt2 && own ? Lw.fc_b[row0 + threadIdx.x % nr] : 0.f;
+  dep_wait(P, dep);
+  Lds s = carve(smem, m, ng);
+  stage_normed(P, 0, m, G, s.xs, s.xsum, s.red);
   const int gf = threadIdx.x % ng, gs = WG % ng;
   float *og = s.out, *ou = s.out + m * P.up_rpt;
-  gemv_q4_rows(Lw.w1, row0, nr, m, s.xs, s.xsum, ng, gf, gs, s.part, og, P.up_rpt);
-  if (P.arch == 1) {
+  tile_compute<TC>(Rg, nr, ng, nr * ng, m, s.xs, s.xsum, gf, gs, s.part, og, P.up_rpt);
+  if (gpt2) {
     for (int e = threadIdx.x; e < m * nr; e += WG) {
       const int t = e / nr, r = e - t * nr;
-      const float v = og[t * P.up_rpt + r] + Lw.fc_b[row0 + r];
+      const float v = og[t * P.up_rpt + r] + (e == (int)threadIdx.x ? fcb : Lw.fc_b[row0 + r]);
       P.ff[(size_t)t * P.FF + row0 + r] =
           0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
     }
     return;
   }
-  gemv_q4_rows(Lw.w3, row0, nr, m, s.xs, s.xsum, ng, gf, gs, s.part, ou, P.up_rpt);
+  tile_compute<TC>(Ru, nr, ng, nr * ng, m, s.xs, s.xsum, gf, gs, s.part, ou, P.up_rpt);
   for (int e = threadIdx.x; e < m * nr; e += WG) {
     const int t = e / nr, r = e - t * nr;
     const float g = og[t * P.up_rpt + r];
@@ -349,21 +546,27 @@ __device__ void phase_up(const DecParams &P, int li, int item, float *smem) {
   }
 }
 
-__device__ void phase_down(const DecParams &P, int li, int item, float *smem) {
-  const PassState &S = *P.st;
-  const int m = S.ntok, D = P.D, ngf = P.FF >> 5;
+__device__ void phase_down(const DecParams &P, const LayerW &Lw, int m, int item, const Dep &dep, float *smem) {
+  const int D = P.D, ngf = P.FF >> 5;
   const int row0 = item * P.dn_rpt;
   const int nr = min(P.dn_rpt, D - row0);
-  Lds s = carve(smem, m, ngf, m * P.dn_rpt);
-  const LayerW &Lw = P.layers[li];
+  TileRegs<TC> R;
+  tile_load<TC>(Lw.w2, row0, nr, 0, ngf, nr * ngf, R);
+  dep_wait(P, dep);
+  const int e0 = threadIdx.x;
+  const bool own = e0 < m * nr;
+  const int et = own ? e0 / nr : 0, er = own ? e0 - et * nr : 0;
+  const float xres = own ? P.x[(size_t)et * D + row0 + er] : 0.f;
+  const float bres = own && P.arch == 1 ? Lw.mproj_b[row0 + er] : 0.f;
+  Lds s = carve(smem, m, ngf);
   stage_plain(P.ff, P.FF, m, P.FF, s.xs, s.xsum);
-  gemv_q4_rows(Lw.w2, row0, nr, m, s.xs, s.xsum, ngf, threadIdx.x % ngf, WG % ngf, s.part, s.out, P.dn_rpt);
+  tile_compute<TC>(R, nr, ngf, nr * ngf, m, s.xs, s.xsum, threadIdx.x % ngf, WG % ngf, s.part, s.out, P.dn_rpt);
   for (int e = threadIdx.x; e < m * nr; e += WG) {
     const int t = e / nr, r = e - t * nr;
     float y = s.out[t * P.dn_rpt + r];
-    if (P.arch == 1) y = y + Lw.mproj_b[row0 + r];
-    float &x = P.x[(size_t)t * D + row0 + r];
-    x = x + y;
+    if (P.arch == 1) y = y + (e == e0 ? bres : Lw.mproj_b[row0 + r]);
+    const float x = e == e0 ? xres : P.x[(size_t)t * D + row0 + r];
+    P.x[(size_t)t * D + row0 + r] = x + y;
   }
 }
 
@@ -378,17 +581,25 @@ __device__ __forceinline__ float gpt2_adjust(float v, int i, const int *ban, int
   return v;
 }
 
-__device__ void phase_lm(const DecParams &P, int item, float *smem) {
+// lm_head over row tiles wg, wg + nwg, ...; the next tile's weights are
+// loaded while the current one is computed.
+__device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, const Dep &dep, float *smem) {
   const PassState &S = *P.st;
-  if (S.lm_rows == 0) return;
-  const int m_all = S.ntok;
-  const int tb = S.lm_rows == 1 ? m_all - 1 : 0;
+  const int lm_rows = S.lm_rows;
+  if (lm_rows == 0 || wg >= P.lm_tiles) return;
+  const int tb = lm_rows == 1 ? m_all - 1 : 0;
   const int m = m_all - tb;
-  const int D = P.D, ng = D >> 5;
-  const int row0 = item * P.lm_rpt;
-  const int nr = min(P.lm_rpt, P.V - row0);
-  Lds s = carve(smem, m, ng, m * P.lm_rpt);
-  int *lists = reinterpret_cast<int *>(s.out + m * P.lm_rpt);  // [0]: nban, [1]: nrec, [2..34): rec, then ban
+  const int D = P.D, ng = D >> 5, rpt = P.lm_rpt;
+  TileRegs<TC> R[2];
+  int tile = wg;
+  {
+    const int r0 = tile * rpt, nr = min(rpt, P.V - r0);
+    tile_load<TC>(P.lm, r0, nr, 0, ng, nr * ng, R[0]);
+  }
+  const Gains G = load_gains(P, P.norm_f);
+  dep_wait(P, dep);
+  Lds s = carve(smem, m, ng);
+  int *lists = reinterpret_cast<int *>(s.out + m * rpt);  // [0]: nban, [1]: nrec, [2..34): rec, then ban
   const bool penal = P.arch == 1 && S.chain;
   if (penal && threadIdx.x == 0) {
     // infer.js:252-287 over hist[0..n): banned = tokens that would repeat the
@@ -404,39 +615,46 @@ __device__ void phase_lm(const DecParams &P, int item, float *smem) {
     lists[0] = nban;
     lists[1] = nrec;
   }
-  for (int t = 0; t < m; ++t)
-    for (int i = threadIdx.x; i < D; i += WG) s.xs[t * ng * XS + skew(i)] = P.x[(size_t)(tb + t) * D + i];
-  __syncthreads();
-  norm_staged(P, s.xs, m, P.norm_f, s.red);
-  stage_group_sums(s.xs, s.xsum, m, ng);
-  gemv_q4_rows(P.lm, row0, nr, m, s.xs, s.xsum, ng, threadIdx.x % ng, WG % ng, s.part, s.out, P.lm_rpt);
-  for (int e = threadIdx.x; e < m * nr; e += WG) {
-    const int t = e / nr, r = e - t * nr;
-    P.logits[(size_t)(tb + t) * P.V + row0 + r] = s.out[t * P.lm_rpt + r];
-  }
-  if (threadIdx.x < 64) {
-    const int nban = penal ? lists[0] : 0, nrec = penal ? lists[1] : 0;
-    for (int t = 0; t < m; ++t) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int r = threadIdx.x; r < nr; r += 64) {
-        float v = s.out[t * P.lm_rpt + r];
-        if (penal) v = gpt2_adjust(v, row0 + r, lists + 34, nban, lists + 2, nrec);
-        if (amax_better(v, row0 + r, bv, bi)) {
-          bv = v;
-          bi = row0 + r;
+  stage_normed(P, tb, m, G, s.xs, s.xsum, s.red);
+  const int gf = threadIdx.x % ng, gs = WG % ng;
+  const int nban = penal ? lists[0] : 0, nrec = penal ? lists[1] : 0;
+  for (int k = 0; tile < P.lm_tiles; ++k, tile += nwg) {
+    const int r0 = tile * rpt, nr = min(rpt, P.V - r0);
+    const int next = tile + nwg;
+    if (next < P.lm_tiles) {
+      const int n0 = next * rpt, nn = min(rpt, P.V - n0);
+      tile_load<TC>(P.lm, n0, nn, 0, ng, nn * ng, R[(k + 1) & 1]);
+    }
+    tile_compute<TC>(R[k & 1], nr, ng, nr * ng, m, s.xs, s.xsum, gf, gs, s.part, s.out, rpt);
+    for (int e = threadIdx.x; e < m * nr; e += WG) {
+      const int t = e / nr, r = e - t * nr;
+      P.logits[(size_t)(tb + t) * P.V + r0 + r] = s.out[t * rpt + r];
+    }
+    if (threadIdx.x < 64) {
+      for (int t = 0; t < m; ++t) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int r = threadIdx.x; r < nr; r += 64) {
+          float v = s.out[t * rpt + r];
+          if (penal) v = gpt2_adjust(v, r0 + r, lists + 34, nban, lists + 2, nrec);
+          if (amax_better(v, r0 + r, bv, bi)) {
+            bv = v;
+            bi = r0 + r;
+          }
+        }
+        wave_argmax(bv, bi);
+        if (threadIdx.x == 0) {
+          P.amv[(size_t)(tb + t) * P.lm_tiles + tile] = bv;
+          P.ami[(size_t)(tb + t) * P.lm_tiles + tile] = bi;
         }
       }
-      wave_argmax(bv, bi);
-      if (threadIdx.x == 0) {
-        P.amv[(size_t)(tb + t) * P.lm_items + item] = bv;
-        P.ami[(size_t)(tb + t) * P.lm_items + item] = bi;
-      }
     }
+    __syncthreads();
   }
 }
 
-__device__ void phase_argmax(const DecParams &P, float *smem) {
+__device__ void phase_argmax(const DecParams &P, const Dep &dep, float *smem) {
+  dep_wait(P, dep);
   PassState &S = *P.st;
   if (S.lm_rows == 0) return;
   const int tb = S.lm_rows == 1 ? S.ntok - 1 : 0;
@@ -445,12 +663,24 @@ __device__ void phase_argmax(const DecParams &P, float *smem) {
   for (int t = tb; t < S.ntok; ++t) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int k = threadIdx.x; k < P.lm_items; k += WG) {
-      const float v = P.amv[(size_t)t * P.lm_items + k];
-      const int i = P.ami[(size_t)t * P.lm_items + k];
-      if (amax_better(v, i, bv, bi)) {
-        bv = v;
-        bi = i;
+    for (int base = 0; base < P.lm_tiles; base += 16 * WG) {
+      float vv[16];
+      int iv[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {  // all loads of the batch before any compare
+        const int k = base + threadIdx.x + j * WG;
+        if (k < P.lm_tiles) {
+          vv[j] = P.amv[(size_t)t * P.lm_tiles + k];
+          iv[j] = P.ami[(size_t)t * P.lm_tiles + k];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int k = base + threadIdx.x + j * WG;
+        if (k < P.lm_tiles && amax_better(vv[j], iv[j], bv, bi)) {
+          bv = vv[j];
+          bi = iv[j];
+        }
       }
     }
     wave_argmax(bv, bi);
@@ -473,7 +703,11 @@ __device__ void phase_argmax(const DecParams &P, float *smem) {
     __syncthreads();
   }
   if (threadIdx.x == 0 && S.chain) {
-    const int tok = S.res[S.ntok - 1];
+    int tok = S.res[S.ntok - 1];
+    if (tok < 0 || tok >= P.V) {  // no finite maximum (non-finite logits)
+      S.bad_tok = 1;
+      tok = 0;
+    }
     P.hist[S.n_hist] = tok;
     S.n_hist = S.n_hist + 1;
     S.tok[0] = tok;
@@ -482,38 +716,49 @@ __device__ void phase_argmax(const DecParams &P, float *smem) {
   }
 }
 
-__device__ __forceinline__ int phase_items(const DecParams &P, int ph, int m) {
+__host__ __device__ __forceinline__ int phase_items(const DecParams &P, int ph, int m) {
   switch (ph) {
-  case PH_QKV: return P.NH + 2 * P.NKV;
+  case PH_QKV: return (P.NH + 2 * P.NKV) * QSPLIT;
   case PH_ATTN: return m * P.NH * P.nsplit_max;
   case PH_O: return (P.D + P.o_rpt - 1) / P.o_rpt;
   case PH_UP: return (P.FF + P.up_rpt - 1) / P.up_rpt;
   case PH_DOWN: return (P.D + P.dn_rpt - 1) / P.dn_rpt;
-  case PH_LM: return P.lm_items;
+  case PH_LM: return P.lm_grid;
   default: return 1;
   }
 }
 
-__device__ __forceinline__ void run_item(const DecParams &P, int ph, int li, int item, float *smem) {
+__device__ __forceinline__ void run_item(const DecParams &P, const LayerW &Lw, int ph, int m, int li, int item,
+                                         int nitems, const Dep &dep, float *smem) {
   switch (ph) {
-  case PH_QKV: phase_qkv(P, li, item, smem); break;
-  case PH_ATTN: phase_attn(P, li, item, smem); break;
-  case PH_O: phase_o(P, li, item, smem); break;
-  case PH_UP: phase_up(P, li, item, smem); break;
-  case PH_DOWN: phase_down(P, li, item, smem); break;
-  case PH_LM: phase_lm(P, item, smem); break;
-  default: phase_argmax(P, smem); break;
+  case PH_QKV: phase_qkv(P, Lw, m, li, item, dep, smem); break;
+  case PH_ATTN: phase_attn(P, m, li, item, dep, smem); break;
+  case PH_O: phase_o(P, Lw, m, item, dep, smem); break;
+  case PH_UP: phase_up(P, Lw, m, item, dep, smem); break;
+  case PH_DOWN: phase_down(P, Lw, m, item, dep, smem); break;
+  case PH_LM: phase_lm(P, m, item, nitems, dep, smem); break;
+  default: phase_argmax(P, dep, smem); break;
   }
   __syncthreads();
 }
 
 // ---------------------------------------------------------------- kernels
-// Mode 1: one kernel per phase (grid = items of that phase).
-__global__ __launch_bounds__(WG) void k_phase(DecParams P, int ph, int li) {
+// Modes 1 and 2: one kernel per phase (grid = items of that phase).
+// The layer's weight pointers come in as a kernel argument, so the first
+// weight loads do not wait for a table lookup.  One symbol per phase so
+// profilers report the phases apart.
+template <int PH>
+__global__ __launch_bounds__(WG) void k_phase(DecParams P, LayerW Lw, int li, int m) {
   extern __shared__ float4 smem4[];
   if (P.st->done) return;
-  run_item(P, ph, li, blockIdx.x, reinterpret_cast<float *>(smem4));
+  const Dep none{};
+  run_item(P, Lw, PH, m, li, blockIdx.x, gridDim.x, none, reinterpret_cast<float *>(smem4));
 }
+
+using PhaseKernel = void (*)(DecParams, LayerW, int, int);
+static const PhaseKernel kPhaseKernels[PH_COUNT] = {k_phase<PH_QKV>, k_phase<PH_ATTN>, k_phase<PH_O>,
+                                                    k_phase<PH_UP>,  k_phase<PH_DOWN>, k_phase<PH_LM>,
+                                                    k_phase<PH_ARGMAX>};
 
 // Grid barrier for the persistent kernel: arrival counter + generation word
 // at agent scope; the last arriver resets the counter and bumps the
@@ -554,18 +799,107 @@ __global__ __launch_bounds__(WG) void k_persistent(DecParams P, int steps) {
     if (__hip_atomic_load(&P.st->done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
     const int m = P.st->ntok;
     for (int li = 0; li < P.L; ++li) {
+      const LayerW Lw = P.layers[li];
+      const Dep none{};
       for (int ph = PH_QKV; ph <= PH_DOWN; ++ph) {
         const int n = phase_items(P, ph, m);
-        for (int it = blockIdx.x; it < n; it += nb) run_item(P, ph, li, it, smem);
+        for (int it = blockIdx.x; it < n; it += nb) run_item(P, Lw, ph, m, li, it, n, none, smem);
         grid_barrier(P, nb, gen);
       }
     }
     if (P.st->lm_rows) {
-      for (int it = blockIdx.x; it < P.lm_items; it += nb) run_item(P, PH_LM, 0, it, smem);
+      const LayerW none{};
+      const Dep nodep{};
+      run_item(P, none, PH_LM, m, 0, blockIdx.x, nb, nodep, smem);
       grid_barrier(P, nb, gen);
-      if (blockIdx.x == 0) run_item(P, PH_ARGMAX, 0, 0, smem);
+      if (blockIdx.x == 0) run_item(P, none, PH_ARGMAX, m, 0, 0, 1, nodep, smem);
       grid_barrier(P, nb, gen);
     }
+  }
+}
+
+// Mode 3: every item of `steps` passes in one cooperative launch, ordered by
+// per-item flags.  Item dependencies (producer ranges):
+//   QKV(l)   <- DOWN(l-1), all items       (layer 0: previous step's ARGMAX)
+//   ATTN(l)  <- QKV(l) tiles of the query head, its K head and its V head
+//   O(l)     <- ATTN(l), all items of the pass
+//   UP(l)    <- O(l);  DOWN(l) <- UP(l);  LM <- DOWN(L-1);  ARGMAX <- LM
+// Each workgroup also waits for the previous step's ARGMAX before starting a
+// step, so a chain that hit eos is seen by every workgroup at the same step.
+__global__ __launch_bounds__(WG) void k_dataflow(DecParams P, int steps) {
+  extern __shared__ float4 smem4[];
+  float *smem = reinterpret_cast<float *>(smem4);
+  const int nb = gridDim.x, wg = blockIdx.x;
+  const int base = __hip_atomic_load(&P.st->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int *const argmax_flag = P.flags + P.fl_argmax;
+  for (int step = 0; step < steps; ++step) {
+    const int ep = base + step;
+    if (step > 0) {
+      const Dep d{{argmax_flag, nullptr, nullptr}, {1, 0, 0}, ep - 1};
+      dep_wait(P, d);
+      if (__hip_atomic_load(&P.st->done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+    }
+    const int m = P.st->ntok;
+    const int n_attn = m * P.NH * P.nsplit_max;
+    for (int li = 0; li < P.L; ++li) {
+      const LayerW Lw = P.layers[li];
+      int *const fl = P.flags + (size_t)li * P.fl_stride;
+      const int *const prev_down = li > 0 ? fl - P.fl_stride + P.fl_down : nullptr;
+      for (int ph = PH_QKV; ph <= PH_DOWN; ++ph) {
+        const int n = phase_items(P, ph, m);
+        for (int it = wg; it < n; it += nb) {
+          Dep d{{nullptr, nullptr, nullptr}, {0, 0, 0}, ep};
+          int *mine = nullptr;
+          switch (ph) {
+          case PH_QKV:
+            if (li > 0) {
+              d.f[0] = prev_down;
+              d.n[0] = P.n_down;
+            }
+            mine = fl + P.fl_qkv + it;
+            break;
+          case PH_ATTN: {
+            const int h = (it % (P.NH * P.nsplit_max)) % P.NH;
+            const int kvh = h / (P.NH / P.NKV);
+            d.f[0] = fl + P.fl_qkv + h * QSPLIT;
+            d.f[1] = fl + P.fl_qkv + (P.NH + kvh) * QSPLIT;
+            d.f[2] = fl + P.fl_qkv + (P.NH + P.NKV + kvh) * QSPLIT;
+            d.n[0] = d.n[1] = d.n[2] = QSPLIT;
+            mine = fl + P.fl_attn + it;
+            break;
+          }
+          case PH_O:
+            d.f[0] = fl + P.fl_attn;
+            d.n[0] = n_attn;
+            mine = fl + P.fl_o + it;
+            break;
+          case PH_UP:
+            d.f[0] = fl + P.fl_o;
+            d.n[0] = P.n_o;
+            mine = fl + P.fl_up + it;
+            break;
+          default:
+            d.f[0] = fl + P.fl_up;
+            d.n[0] = P.n_up;
+            mine = fl + P.fl_down + it;
+            break;
+          }
+          run_item(P, Lw, ph, m, li, it, n, d, smem);
+          dep_signal(mine, ep);
+        }
+      }
+    }
+    if (P.st->lm_rows) {
+      const LayerW none{};
+      const Dep dl{{P.flags + (size_t)(P.L - 1) * P.fl_stride + P.fl_down, nullptr, nullptr}, {P.n_down, 0, 0}, ep};
+      run_item(P, none, PH_LM, m, 0, wg, nb, dl, smem);
+      dep_signal(P.flags + P.fl_lm + wg, ep);
+      if (wg == 0) {
+        const Dep da{{P.flags + P.fl_lm, nullptr, nullptr}, {nb, 0, 0}, ep};
+        run_item(P, none, PH_ARGMAX, m, 0, 0, 1, da, smem);
+      }
+    }
+    if (wg == 0) dep_signal(argmax_flag, ep);
   }
 }
 
@@ -599,12 +933,18 @@ struct mllm_model {
   float *d_gemv_x = nullptr, *d_gemv_y = nullptr;
   DecParams P{};
   int cache_len = 0;
-  int exec_mode = 0;
+  int exec_mode = 1;
   int max_pass = 1;
   size_t lds_max = 0;
   int persist_grid = 0;
+  int flow_grid = 0;
+  int epoch = 0;  // mode 3: last epoch used
   uint64_t device_bytes = 0;
   hipGraphExec_t chain_graph = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;  // around the kernels of the last call
+  std::vector<hipEvent_t> prof_ev;          // mllm_profile_decode
+  float last_ms = 0.f;
+  int last_tokens = 0;
   std::vector<void *> allocs;
 };
 
@@ -617,19 +957,22 @@ int dev_alloc(mllm_model *M, void **p, size_t bytes) {
   return 0;
 }
 
-size_t lds_for(const mllm_config &c, int m) {
-  // Largest LDS carve over the phases for m tokens (floats).
-  const int ngd = c.d_model / 32, ngf = c.d_ff / 32;
-  const size_t base = 16;
-  auto gemv = [&](int ng, int outf) { return base + (size_t)m * ng * XS + (size_t)m * ng + (size_t)m * SUB_CH + outf; };
-  const int rpt_d = SUB_CH / ngd, rpt_f = SUB_CH / ngf;
+// Tile rows per item: about TILE_TARGET chunks, at most TC * WG.
+int tile_rows(int ng, int per_row_mats = 1) { return std::max(1, TILE_TARGET / (ng * per_row_mats)); }
+
+// Dynamic LDS (bytes) of a pass of m tokens: the largest phase carve.
+size_t lds_for(const DecParams &P, int m) {
+  const int ngd = P.D / 32, ngf = P.FF / 32;
+  auto gemv = [&](int ng, size_t outf) {
+    return 16 + (size_t)m * ng * XS + (size_t)m * ng + (size_t)m * TC * WG + outf;
+  };
   size_t f = 0;
-  f = std::max(f, gemv(ngd, m * HD));                    // qkv
-  f = std::max(f, gemv(ngd, m * rpt_d));                 // o
-  f = std::max(f, gemv(ngd, 2 * m * rpt_d));             // up
-  f = std::max(f, gemv(ngf, m * rpt_f));                 // down
-  f = std::max(f, gemv(ngd, m * rpt_d + 34 + c.max_seq_len));  // lm + argmax lists
-  f = std::max(f, (size_t)(HD + ACH + 4 * HD + 16));      // attn
+  f = std::max(f, gemv(ngd, (size_t)m * 16));                                     // qkv
+  f = std::max(f, gemv(ngd, (size_t)m * P.o_rpt));                                // o
+  f = std::max(f, gemv(ngd, (size_t)2 * m * P.up_rpt));                           // up
+  f = std::max(f, gemv(ngf, (size_t)m * P.dn_rpt));                               // down
+  f = std::max(f, gemv(ngd, (size_t)m * P.lm_rpt + 34 + (size_t)P.max_seq));     // lm + argmax lists
+  f = std::max(f, (size_t)(HD + ACH + 16 * HD + 16));                             // attn
   return f * sizeof(float);
 }
 
@@ -671,20 +1014,47 @@ int upload_state(mllm_model *M) {
 }
 
 int launch_phase(mllm_model *M, int ph, int li, int m) {
-  const DecParams &P = M->P;
-  int n = 1;
-  switch (ph) {
-  case PH_QKV: n = P.NH + 2 * P.NKV; break;
-  case PH_ATTN: n = m * P.NH * P.nsplit_max; break;
-  case PH_O: n = (P.D + P.o_rpt - 1) / P.o_rpt; break;
-  case PH_UP: n = (P.FF + P.up_rpt - 1) / P.up_rpt; break;
-  case PH_DOWN: n = (P.D + P.dn_rpt - 1) / P.dn_rpt; break;
-  case PH_LM: n = P.lm_items; break;
-  default: n = 1;
-  }
-  hipLaunchKernelGGL(k_phase, dim3(n), dim3(WG), M->lds_max, M->stream, M->P, ph, li);
+  const int n = phase_items(M->P, ph, m);
+  const LayerW Lw = ph <= PH_DOWN ? M->layers[li] : LayerW{};
+  hipLaunchKernelGGL(kPhaseKernels[ph], dim3(n), dim3(WG), lds_for(M->P, m), M->stream, M->P, Lw, li, m);
   MLLM_HIP(hipGetLastError());
   return 0;
+}
+
+// The chained decode step as an explicit graph: one kernel node per phase in
+// a linear chain (built with node APIs rather than stream capture).
+int build_chain_graph(mllm_model *M) {
+  hipGraph_t g;
+  MLLM_HIP(hipGraphCreate(&g, 0));
+  hipGraphNode_t prev = nullptr;
+  const size_t lds = lds_for(M->P, 1);
+  int m = 1;
+  auto add = [&](int ph, int li) -> int {
+    LayerW Lw = ph <= PH_DOWN ? M->layers[li] : LayerW{};
+    void *args[] = {&M->P, &Lw, &li, &m};
+    hipKernelNodeParams kp;
+    memset(&kp, 0, sizeof kp);
+    kp.func = reinterpret_cast<void *>(kPhaseKernels[ph]);
+    kp.gridDim = dim3(phase_items(M->P, ph, 1));
+    kp.blockDim = dim3(WG);
+    kp.sharedMemBytes = (unsigned)lds;
+    kp.kernelParams = args;
+    hipGraphNode_t node;
+    MLLM_HIP(hipGraphAddKernelNode(&node, g, prev ? &prev : nullptr, prev ? 1 : 0, &kp));
+    prev = node;
+    return 0;
+  };
+  int rc = 0;
+  for (int li = 0; li < M->cfg.n_layers && !rc; ++li)
+    for (int ph = PH_QKV; ph <= PH_DOWN && !rc; ++ph) rc = add(ph, li);
+  if (!rc) rc = add(PH_LM, 0);
+  if (!rc) rc = add(PH_ARGMAX, 0);
+  if (!rc) {
+    hipError_t e = hipGraphInstantiate(&M->chain_graph, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) rc = hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
+  }
+  (void)hipGraphDestroy(g);
+  return rc;
 }
 
 int enqueue_pass_phases(mllm_model *M, int m, bool lm) {
@@ -698,21 +1068,32 @@ int enqueue_pass_phases(mllm_model *M, int m, bool lm) {
   return 0;
 }
 
-int launch_persistent(mllm_model *M, int steps) {
+int launch_dataflow(mllm_model *M, int steps, int m) {
+  M->h_st->epoch = M->epoch + 1;
+  if (int rc = upload_state(M)) return rc;
+  void *args[] = {&M->P, &steps};
+  MLLM_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(k_dataflow), dim3(M->flow_grid), dim3(WG), args,
+                                      lds_for(M->P, m), M->stream));
+  M->epoch += steps;
+  return 0;
+}
+
+int launch_persistent(mllm_model *M, int steps, int m) {
   void *args[] = {&M->P, &steps};
   MLLM_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(k_persistent), dim3(M->persist_grid), dim3(WG),
-                                      args, M->lds_max, M->stream));
+                                      args, lds_for(M->P, m), M->stream));
   return 0;
 }
 
 int check_device_err(mllm_model *M) {
-  int err = 0;
-  MLLM_HIP(hipMemcpy(&err, &M->d_st->err, sizeof(int), hipMemcpyDeviceToHost));
-  if (err) {
-    int zero = 0;
-    MLLM_HIP(hipMemcpy(&M->d_st->err, &zero, sizeof(int), hipMemcpyHostToDevice));
+  int err[2] = {0, 0};
+  MLLM_HIP(hipMemcpy(err, &M->d_st->err, sizeof(err), hipMemcpyDeviceToHost));
+  if (err[0] || err[1]) {
+    int zero[2] = {0, 0};
+    MLLM_HIP(hipMemcpy(&M->d_st->err, zero, sizeof(zero), hipMemcpyHostToDevice));
     MLLM_HIP(hipMemset(M->d_bar, 0, 2 * sizeof(unsigned)));
-    return set_error(MLLM_ERR_DEVICE, "decode kernel grid barrier timed out");
+    return set_error(MLLM_ERR_DEVICE, err[0] ? "decode kernel grid barrier timed out"
+                                             : "chained decode produced no finite maximum logit");
   }
   return 0;
 }
@@ -727,12 +1108,18 @@ int run_pass(mllm_model *M, const int32_t *ids, int m, int pos0, int lm_rows) {
   s.eos = -1;
   for (int i = 0; i < m; ++i) s.tok[i] = ids[i];
   if (int rc = upload_state(M)) return rc;
-  if (M->exec_mode == 0) {
-    if (int rc = launch_persistent(M, 1)) return rc;
+  MLLM_HIP(hipEventRecord(M->ev0, M->stream));
+  if (M->exec_mode == 3) {
+    if (int rc = launch_dataflow(M, 1, m)) return rc;
+  } else if (M->exec_mode == 0) {
+    if (int rc = launch_persistent(M, 1, m)) return rc;
   } else {
     if (int rc = enqueue_pass_phases(M, m, lm_rows != 0)) return rc;
   }
+  MLLM_HIP(hipEventRecord(M->ev1, M->stream));
   MLLM_HIP(hipStreamSynchronize(M->stream));
+  MLLM_HIP(hipEventElapsedTime(&M->last_ms, M->ev0, M->ev1));
+  M->last_tokens = m;
   return check_device_err(M);
 }
 
@@ -779,6 +1166,9 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   if (c.d_model % 32 || c.d_ff % 32 || c.d_model > 4096 || c.d_ff > 16384)
     return set_error(MLLM_ERR_UNSUPPORTED, "d_model %d / d_ff %d unsupported", c.d_model, c.d_ff);
   if (c.arch == 1 && c.n_kv_heads != c.n_heads) return set_error(MLLM_ERR_INVALID, "gpt2 needs n_kv_heads == n_heads");
+  if (c.d_model > 1024) return set_error(MLLM_ERR_UNSUPPORTED, "d_model %d unsupported (<= 1024)", c.d_model);
+  if (c.arch == 0 && (int)floor(HD * c.rope_pct) != HD)
+    return set_error(MLLM_ERR_UNSUPPORTED, "partial rotary (ropePct %g) unsupported", c.rope_pct);
 
   mllm_model *M = new mllm_model();
   M->cfg = c;
@@ -792,6 +1182,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   M->num_cus = prop.multiProcessorCount;
   if (hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking) != hipSuccess)
     return fail(set_error(MLLM_ERR_HIP, "stream create"));
+  if (hipEventCreate(&M->ev0) != hipSuccess || hipEventCreate(&M->ev1) != hipSuccess)
+    return fail(set_error(MLLM_ERR_HIP, "event create"));
 
   // weights: the payload as-is (16-byte aligned tensors, PGW1 layout)
   M->payload_bytes = payload_nbytes;
@@ -860,7 +1252,6 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   if (c.arch == 0) {
     int rd = 0;
     std::vector<float> cs = build_rope_table(c, HD, false, &rd), sn = build_rope_table(c, HD, true, &rd);
-    P.rd = rd;
     if (int rc = dev_alloc(M, (void **)&M->d_rope_cos, cs.size() * 4)) return fail(rc);
     if (int rc = dev_alloc(M, (void **)&M->d_rope_sin, sn.size() * 4)) return fail(rc);
     if (hipMemcpy(M->d_rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
@@ -876,18 +1267,23 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
 
   // tiles
   const int ngd = D / 32, ngf = FF / 32;
-  P.o_rpt = std::max(1, SUB_CH / ngd);
-  P.up_rpt = std::max(1, SUB_CH / ngd);
-  P.dn_rpt = std::max(1, SUB_CH / ngf);
-  P.lm_rpt = std::max(1, SUB_CH / ngd);
-  P.lm_items = (V + P.lm_rpt - 1) / P.lm_rpt;
+  P.o_rpt = tile_rows(ngd);
+  P.up_rpt = tile_rows(ngd, c.arch == 1 ? 1 : 2);
+  P.dn_rpt = tile_rows(ngf);
+  P.lm_rpt = tile_rows(ngd);
+  P.lm_tiles = (V + P.lm_rpt - 1) / P.lm_rpt;
+  P.lm_grid = P.lm_tiles;  // one tile per workgroup: every tile's loads in flight at once
+  // every GEMV tile must fit the TC * WG chunk registers of a workgroup
+  const int cap = TC * WG;
+  if (16 * ngd > cap || P.o_rpt * ngd > cap || P.up_rpt * ngd > cap || P.dn_rpt * ngf > cap || P.lm_rpt * ngd > cap)
+    return fail(set_error(MLLM_ERR_UNSUPPORTED, "tile exceeds %d chunks (d_model %d, d_ff %d)", cap, D, FF));
 
   // pass size bound by LDS (160 KiB on gfx950)
   const size_t lds_cap = (size_t)prop.sharedMemPerBlock > 0 ? (size_t)prop.sharedMemPerBlock : 65536;
   int mp = 1;
-  while (mp < MAXT && lds_for(c, mp + 1) <= lds_cap) ++mp;
+  while (mp < MAXT && lds_for(P, mp + 1) <= lds_cap) ++mp;
   M->max_pass = mp;
-  M->lds_max = lds_for(c, mp);
+  M->lds_max = lds_for(P, mp);
   if (M->lds_max > lds_cap) return fail(set_error(MLLM_ERR_UNSUPPORTED, "model needs more LDS than the device has"));
 
   // activations, KV cache, scratch
@@ -898,8 +1294,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   if (!rc) rc = dev_alloc(M, (void **)&M->d_attp, sizeof(float) * MAXT * NH * P.nsplit_max * APS);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_ff, sizeof(float) * MAXT * FF);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_logits, sizeof(float) * MAXT * (size_t)V);
-  if (!rc) rc = dev_alloc(M, (void **)&M->d_amv, sizeof(float) * MAXT * P.lm_items);
-  if (!rc) rc = dev_alloc(M, (void **)&M->d_ami, sizeof(int) * MAXT * P.lm_items);
+  if (!rc) rc = dev_alloc(M, (void **)&M->d_amv, sizeof(float) * MAXT * P.lm_tiles);
+  if (!rc) rc = dev_alloc(M, (void **)&M->d_ami, sizeof(int) * MAXT * P.lm_tiles);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_hist, sizeof(int) * (c.max_seq_len + 1));
   if (!rc) rc = dev_alloc(M, (void **)&M->d_st, sizeof(PassState));
   if (!rc) rc = dev_alloc(M, (void **)&M->d_bar, 64);
@@ -924,11 +1320,12 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   P.bar = M->d_bar;
 
   if (M->lds_max > 64 * 1024) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(k_persistent), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)M->lds_max) != hipSuccess ||
-        hipFuncSetAttribute(reinterpret_cast<const void *>(k_phase), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)M->lds_max) != hipSuccess)
-      return fail(set_error(MLLM_ERR_HIP, "LDS attribute"));
+    bool ok = hipFuncSetAttribute(reinterpret_cast<const void *>(k_persistent),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)M->lds_max) == hipSuccess;
+    for (int ph = 0; ph < PH_COUNT; ++ph)
+      ok = ok && hipFuncSetAttribute(reinterpret_cast<const void *>(kPhaseKernels[ph]),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)M->lds_max) == hipSuccess;
+    if (!ok) return fail(set_error(MLLM_ERR_HIP, "LDS attribute"));
   }
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(k_persistent), WG,
@@ -936,6 +1333,36 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       per_cu < 1)
     per_cu = 1;
   M->persist_grid = M->num_cus * std::min(per_cu, 1);
+  {
+    bool ok = true;
+    if (M->lds_max > 64 * 1024)
+      ok = hipFuncSetAttribute(reinterpret_cast<const void *>(k_dataflow), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)M->lds_max) == hipSuccess;
+    int fcu = 0;
+    if (!ok || hipOccupancyMaxActiveBlocksPerMultiprocessor(&fcu, reinterpret_cast<const void *>(k_dataflow), WG,
+                                                             M->lds_max) != hipSuccess || fcu < 1)
+      fcu = 1;
+    M->flow_grid = M->num_cus * std::min(fcu, 2);
+  }
+  // mode 3 flags: per layer [qkv | attn | o | up | down], then lm[grid], argmax
+  {
+    DecParams &Q = M->P;
+    const int n_qkv = (Q.NH + 2 * Q.NKV) * QSPLIT;
+    Q.n_o = (Q.D + Q.o_rpt - 1) / Q.o_rpt;
+    Q.n_up = (Q.FF + Q.up_rpt - 1) / Q.up_rpt;
+    Q.n_down = (Q.D + Q.dn_rpt - 1) / Q.dn_rpt;
+    Q.fl_qkv = 0;
+    Q.fl_attn = n_qkv;
+    Q.fl_o = Q.fl_attn + MAXT * Q.NH * Q.nsplit_max;
+    Q.fl_up = Q.fl_o + Q.n_o;
+    Q.fl_down = Q.fl_up + Q.n_up;
+    Q.fl_stride = Q.fl_down + Q.n_down;
+    Q.fl_lm = Q.L * Q.fl_stride;
+    Q.fl_argmax = Q.fl_lm + M->flow_grid;
+    const size_t nflags = (size_t)Q.fl_argmax + 1;
+    if (int rc = dev_alloc(M, (void **)&Q.flags, nflags * sizeof(int))) return fail(rc);
+    if (hipMemset(Q.flags, 0, nflags * sizeof(int)) != hipSuccess) return fail(set_error(MLLM_ERR_HIP, "memset"));
+  }
   *out = M;
   clear_error();
   return 0;
@@ -947,6 +1374,9 @@ extern "C" int mllm_model_destroy(mllm_model *M) {
   if (M->chain_graph) hipGraphExecDestroy(M->chain_graph);
   for (void *p : M->allocs) hipFree(p);
   if (M->h_st) hipHostFree(M->h_st);
+  for (hipEvent_t e : M->prof_ev) (void)hipEventDestroy(e);
+  if (M->ev0) hipEventDestroy(M->ev0);
+  if (M->ev1) hipEventDestroy(M->ev1);
   if (M->stream) hipStreamDestroy(M->stream);
   delete M;
   return 0;
@@ -971,7 +1401,7 @@ extern "C" int mllm_max_pass_tokens(const mllm_model *M) { return M ? M->max_pas
 
 extern "C" int mllm_set_exec_mode(mllm_model *M, int mode) {
   MLLM_CHECK(M, "null model");
-  MLLM_CHECK(mode == 0 || mode == 1, "exec mode %d", mode);
+  MLLM_CHECK(mode >= 0 && mode <= 3, "exec mode %d", mode);
   M->exec_mode = mode;
   return 0;
 }
@@ -1039,29 +1469,90 @@ extern "C" int mllm_decode_chain(mllm_model *M, int32_t first, int n_steps, int3
   s.n_hist = n_hist;
   s.tok[0] = first;
   if (int rc = upload_state(M)) return rc;
-  if (M->exec_mode == 0) {
-    if (int rc = launch_persistent(M, n_steps)) return rc;
+  MLLM_HIP(hipEventRecord(M->ev0, M->stream));
+  if (M->exec_mode == 3) {
+    if (int rc = launch_dataflow(M, n_steps, 1)) return rc;
+  } else if (M->exec_mode == 0) {
+    if (int rc = launch_persistent(M, n_steps, 1)) return rc;
+  } else if (M->exec_mode == 2) {
+    for (int i = 0; i < n_steps; ++i)
+      if (int rc = enqueue_pass_phases(M, 1, true)) return rc;
   } else {
-    if (!M->chain_graph) {
-      hipGraph_t g;
-      MLLM_HIP(hipStreamBeginCapture(M->stream, hipStreamCaptureModeThreadLocal));
-      int rc = enqueue_pass_phases(M, 1, true);
-      hipError_t e = hipStreamEndCapture(M->stream, &g);
-      if (rc) return rc;
-      MLLM_HIP(e);
-      e = hipGraphInstantiate(&M->chain_graph, g, nullptr, nullptr, 0);
-      hipGraphDestroy(g);
-      MLLM_HIP(e);
-    }
+    if (!M->chain_graph)
+      if (int rc = build_chain_graph(M)) return rc;
     for (int i = 0; i < n_steps; ++i) MLLM_HIP(hipGraphLaunch(M->chain_graph, M->stream));
   }
+  MLLM_HIP(hipEventRecord(M->ev1, M->stream));
   MLLM_HIP(hipStreamSynchronize(M->stream));
+  MLLM_HIP(hipEventElapsedTime(&M->last_ms, M->ev0, M->ev1));
   if (int rc = check_device_err(M)) return rc;
   MLLM_HIP(hipMemcpy(&s, M->d_st, sizeof(PassState), hipMemcpyDeviceToHost));
   const int emitted = s.n_hist - n_hist;
   MLLM_HIP(hipMemcpy(out_ids, M->d_hist + n_hist, sizeof(int32_t) * emitted, hipMemcpyDeviceToHost));
   *n_out = emitted;
+  M->last_tokens = emitted;
   M->cache_len += emitted;
+  return 0;
+}
+
+extern "C" int mllm_profile_decode(mllm_model *M, int32_t first, int n_steps, float *phase_us) {
+  MLLM_CHECK(M && phase_us, "null argument");
+  MLLM_CHECK(n_steps > 0, "n_steps %d", n_steps);
+  MLLM_CHECK(M->cache_len + n_steps <= M->cfg.max_seq_len, "profile run exceeds the context");
+  if (int rc = check_ids(M, &first, 1)) return rc;
+  const int L = M->cfg.n_layers;
+  const int per_step = L * 5 + 2;
+  if ((int)M->prof_ev.size() < 2 * per_step) {
+    for (hipEvent_t e : M->prof_ev) (void)hipEventDestroy(e);
+    M->prof_ev.assign(2 * per_step, nullptr);
+    for (auto &e : M->prof_ev) MLLM_HIP(hipEventCreate(&e));
+  }
+  PassState &s = *M->h_st;
+  memset(&s, 0, sizeof s);
+  s.pos0 = M->cache_len;
+  s.ntok = 1;
+  s.lm_rows = 1;
+  s.chain = 1;
+  s.eos = -1;
+  s.tok[0] = first;
+  if (int rc = upload_state(M)) return rc;
+  double sum[PH_COUNT] = {0};
+  int cnt[PH_COUNT] = {0};
+  for (int step = 0; step < n_steps; ++step) {
+    int k = 0;
+    std::vector<int> phs;
+    for (int li = 0; li < L; ++li)
+      for (int ph = PH_QKV; ph <= PH_DOWN; ++ph, ++k) {
+        MLLM_HIP(hipEventRecord(M->prof_ev[2 * k], M->stream));
+        if (int rc = launch_phase(M, ph, li, 1)) return rc;
+        MLLM_HIP(hipEventRecord(M->prof_ev[2 * k + 1], M->stream));
+        phs.push_back(ph);
+      }
+    for (int ph = PH_LM; ph <= PH_ARGMAX; ++ph, ++k) {
+      MLLM_HIP(hipEventRecord(M->prof_ev[2 * k], M->stream));
+      if (int rc = launch_phase(M, ph, 0, 1)) return rc;
+      MLLM_HIP(hipEventRecord(M->prof_ev[2 * k + 1], M->stream));
+      phs.push_back(ph);
+    }
+    MLLM_HIP(hipStreamSynchronize(M->stream));
+    for (int j = 0; j < k; ++j) {
+      float ms = 0;
+      MLLM_HIP(hipEventElapsedTime(&ms, M->prof_ev[2 * j], M->prof_ev[2 * j + 1]));
+      sum[phs[j]] += ms;
+      cnt[phs[j]] += 1;
+    }
+  }
+  if (int rc = check_device_err(M)) return rc;
+  MLLM_HIP(hipMemcpy(&s, M->d_st, sizeof(PassState), hipMemcpyDeviceToHost));
+  M->cache_len += n_steps;
+  for (int ph = 0; ph < PH_COUNT; ++ph) phase_us[ph] = cnt[ph] ? (float)(sum[ph] / cnt[ph] * 1000.0) : 0.f;
+  return 0;
+}
+
+extern "C" int mllm_last_timing(const mllm_model *M, float *gpu_ms, int *n_tokens) {
+  MLLM_CHECK(M, "null model");
+  if (gpu_ms) *gpu_ms = M->last_ms;
+  if (n_tokens) *n_tokens = M->last_tokens;
   return 0;
 }
 

@@ -94,7 +94,7 @@ __global__ __launch_bounds__(WG) void k_gemv_q8(const uint4 *__restrict__ q, con
   float *xs = smem;
   float *xsum16 = xs + ng * XS;
   float *part = xsum16 + nc;
-  for (int i = threadIdx.x; i < cols; i += WG) xs[(i >> 5) * XS + (i & 31)] = x[i];
+  stage_rows(x, cols, 1, cols, xs);
   __syncthreads();
   for (int c = threadIdx.x; c < nc; c += WG) {
     const float *p = xs + (c >> 1) * XS + (c & 1) * 16;
@@ -253,7 +253,7 @@ extern "C" int mllm_gemv_q4(int m, int n, const uint8_t *packed, const float *sc
                             float *y, void *stream) {
   if (int rc = check_q4_shape(m, n, group)) return rc;
   MLLM_CHECK(packed && scale && x && y, "null pointer");
-  MLLM_CHECK(((uintptr_t)packed & 15) == 0, "packed must be 16-byte aligned");
+  MLLM_CHECK((((uintptr_t)packed | (uintptr_t)x) & 15) == 0, "packed and x must be 16-byte aligned");
   return q4_gemm(1, m, n, packed, scale, x, y, as_stream(stream));
 }
 
@@ -262,7 +262,7 @@ extern "C" int mllm_gemm_q4(int t, int m, int n, const uint8_t *packed, const fl
   if (int rc = check_q4_shape(m, n, group)) return rc;
   MLLM_CHECK(t > 0, "t=%d", t);
   MLLM_CHECK(packed && scale && x && y, "null pointer");
-  MLLM_CHECK(((uintptr_t)packed & 15) == 0, "packed must be 16-byte aligned");
+  MLLM_CHECK((((uintptr_t)packed | (uintptr_t)x) & 15) == 0, "packed and x must be 16-byte aligned");
   return q4_gemm(t, m, n, packed, scale, x, y, as_stream(stream));
 }
 
@@ -290,7 +290,7 @@ static int q8_common(int m, int n, const int8_t *q, const float *scale, const fl
   MLLM_CHECK(m > 0 && n > 0 && n % 32 == 0, "invalid shape m=%d n=%d (n %% 32 == 0 required)", m, n);
   if (n > kMaxCols) return set_error(MLLM_ERR_UNSUPPORTED, "n=%d exceeds %d", n, kMaxCols);
   MLLM_CHECK(q && scale && x && y, "null pointer");
-  MLLM_CHECK(((uintptr_t)q & 15) == 0, "q must be 16-byte aligned");
+  MLLM_CHECK((((uintptr_t)q | (uintptr_t)x) & 15) == 0, "q and x must be 16-byte aligned");
   const int nc = n / 16, ng = n / 32;
   const int rpt = SUB_CH / nc > 0 ? SUB_CH / nc : 1;
   const int ntiles = (m + rpt - 1) / rpt;

@@ -1,0 +1,58 @@
+/**
+ * Drive HipPetitGPT on a .pgw file (the flow of engine/worker.js:34-181:
+ * load -> new engine -> generate with streaming onToken).
+ *   node run_generate.mjs <model.pgw> <spec.json>   -> prints one JSON line
+ * spec: { prompt: [...], maxNewTokens, eosId, mode, specK, kvFp16, execMode,
+ *         decodeLogits: [ids...] }  (decodeLogits: teacher-forced tokens whose
+ *         logits are returned for comparison)
+ */
+import fs from "fs";
+import { parsePgw } from "./weights.mjs";
+import { HipPetitGPT } from "./engine.mjs";
+
+async function main() {
+  const [, , pgwPath, specPath] = process.argv;
+  const spec = JSON.parse(fs.readFileSync(specPath, "utf8"));
+  const bundle = parsePgw(fs.readFileSync(pgwPath));
+  const model = new HipPetitGPT(bundle, { kvFp16: !!spec.kvFp16, execMode: spec.execMode });
+  const streamed = [];
+  const res = await model.generate(spec.prompt, {
+    maxNewTokens: spec.maxNewTokens,
+    eosId: spec.eosId !== undefined ? spec.eosId : -1,
+    mode: spec.mode || "greedy",
+    specK: spec.specK || 4,
+    onToken: async (t) => {
+      streamed.push(t);
+    },
+  });
+  const rows = [];
+  if (spec.decodeLogits) {
+    model.resetCache();
+    rows.push(Array.from(model.forwardPrompt(spec.prompt)));
+    for (const t of spec.decodeLogits) rows.push(Array.from(model.forwardDecode(t)));
+  }
+  const out = {
+    generatedIds: res.generatedIds,
+    streamed,
+    stopReason: res.stopReason,
+    specHits: res.specHits,
+    specTries: res.specTries,
+    mode: res.mode,
+    bytesAllocated: model.bytesAllocated,
+    rows,
+  };
+  model.destroy();
+  let destroyedError = null;
+  try {
+    model.forwardDecode(1);
+  } catch (e) {
+    destroyedError = String(e.message);
+  }
+  out.destroyedError = destroyedError;
+  console.log(JSON.stringify(out));
+}
+
+main().catch((e) => {
+  console.error(e && e.stack ? e.stack : String(e));
+  process.exit(1);
+});

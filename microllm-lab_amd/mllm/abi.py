@@ -43,6 +43,8 @@ SIGNATURES = {
     "mllm_model_gemv": ([P, C.c_char_p, P, P], I),
     "mllm_set_exec_mode": ([P, I], I),
     "mllm_model_device_bytes": ([P], C.c_uint64),
+    "mllm_last_timing": ([P, P, P], I),
+    "mllm_profile_decode": ([P, C.c_int32, I, P], I),
 }
 
 
@@ -72,6 +74,13 @@ def lib() -> C.CDLL:
     """Load libmllm.so (raises if it was not built)."""
     global _lib
     if _lib is None:
+        try:
+            # torch ships its own HIP runtime under the same soname; loading it
+            # first makes libmllm bind to that one, so the process holds a
+            # single runtime and torch tensors and libmllm share the device.
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"libmllm.so not built at {LIB_PATH}; run __graft_entry__.build()")
         L = C.CDLL(LIB_PATH)

@@ -62,7 +62,7 @@ def argmax_gpt2(logits: np.ndarray, history: List[int], no_repeat_ngram: int = 3
 class PetitGPT:
     """infer.js PetitGPT on the MI355X decode step."""
 
-    def __init__(self, bundle: Bundle, norm_eps: float = 1e-6, kv_fp16: bool = False, exec_mode: int = 0):
+    def __init__(self, bundle: Bundle, norm_eps: float = 1e-6, kv_fp16: bool = False, exec_mode: int = 1):
         self.bundle = bundle
         self.cfg = bundle.cfg
         self.kind = bundle.kind
@@ -106,6 +106,21 @@ class PetitGPT:
     def set_exec_mode(self, mode: int):
         abi.call("mllm_set_exec_mode", self._h, int(mode))
         self.exec_mode = int(mode)
+
+    def last_timing(self):
+        """(gpu_ms, tokens) of the last call, from HIP events on the model stream."""
+        ms = C.c_float(0)
+        n = C.c_int(0)
+        abi.call("mllm_last_timing", self._h, C.byref(ms), C.byref(n))
+        return float(ms.value), int(n.value)
+
+    PHASES = ("QKV", "ATTN", "O", "UP", "DOWN", "LM", "ARGMAX")
+
+    def profile_decode(self, first: int, n_steps: int) -> dict:
+        """Mean microseconds per launch of each decode phase (events on the model stream)."""
+        out = (C.c_float * 7)()
+        abi.call("mllm_profile_decode", self._h, int(first), int(n_steps), out)
+        return {name: float(out[i]) for i, name in enumerate(self.PHASES)}
 
     @property
     def bytesAllocated(self) -> int:

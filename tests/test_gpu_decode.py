@@ -1,0 +1,195 @@
+"""GPU parity of the engine-level C ABI (PetitGPT API) against the oracle.
+
+Bars: logits within max-abs 1e-2 of the fp64-accumulating
+oracle, written here as LOGIT_TOL; greedy argmax identical wherever the oracle's
+top-2 margin exceeds 1e-2; the verify pass, both execution modes and chained
+decode bit-identical to single-token decode of the same engine.
+"""
+import numpy as np
+import pytest
+
+import mllm
+from mllm import pgw
+
+gpu = pytest.mark.gpu
+LOGIT_TOL = 1e-2
+MARGIN = 1e-2
+
+
+def margin(logits):
+    top2 = np.partition(logits, -2)[-2:]
+    return float(top2[1] - top2[0])
+
+
+def teacher_forced(gpu_model, ref, prompt, steps, rng):
+    """Feed the same token sequence to both; compare every step's logits."""
+    lg = gpu_model.forwardPrompt(prompt).copy()
+    lr = ref.forward_prompt(prompt)
+    worst = float(np.abs(lg - lr).max())
+    agree = [int(np.argmax(lg)) == int(np.argmax(lr)) or margin(lr) <= MARGIN]
+    tok = int(np.argmax(lr))
+    for _ in range(steps):
+        lg = gpu_model.forwardDecode(tok).copy()
+        lr = ref.forward_decode(tok)
+        worst = max(worst, float(np.abs(lg - lr).max()))
+        agree.append(int(np.argmax(lg)) == int(np.argmax(lr)) or margin(lr) <= MARGIN)
+        tok = int(rng.integers(0, gpu_model.cfg.vocab_size)) if rng is not None else int(np.argmax(lr))
+    return worst, all(agree)
+
+
+def build(arch="llama", seed=1, **over):
+    cfg = pgw.small_config(arch, **over)
+    return pgw.parse_pgw(pgw.make_model(cfg, seed=seed))
+
+
+@gpu
+@pytest.mark.parametrize("arch", ["llama", "gpt2"])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+def test_small_teacher_forced_vs_oracle(oracle_lib, arch, mode):
+    bundle = build(arch, seed=3)
+    print(f"decode small {arch} mode={mode}", flush=True)
+    g = mllm.PetitGPT(bundle, exec_mode=mode)
+    ref = oracle_lib.OracleModel(bundle)
+    rng = np.random.default_rng(4)
+    prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 9)]
+    worst, agree = teacher_forced(g, ref, prompt, 12, rng)
+    g.destroy()
+    assert worst < LOGIT_TOL and agree, worst
+
+
+@gpu
+def test_exec_modes_bit_identical():
+    bundle = build("llama", seed=5)
+    outs = []
+    for mode in (0, 1, 2, 3):
+        g = mllm.PetitGPT(bundle, exec_mode=mode)
+        rows = [g.forwardPrompt([1, 2, 3, 4, 5]).copy()]
+        for t in (6, 7, 8):
+            rows.append(g.forwardDecode(t).copy())
+        outs.append(np.stack(rows))
+        g.destroy()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
+    assert np.array_equal(outs[0].view(np.uint32), outs[3].view(np.uint32))
+
+
+@gpu
+@pytest.mark.parametrize("n", [2, 5, 9])
+def test_verify_rows_bit_identical_to_decode(n):
+    bundle = build("llama", seed=6)
+    g = mllm.PetitGPT(bundle)
+    prompt = [3, 1, 4, 1, 5, 9, 2, 6]
+    extra = [5, 3, 5, 8, 9, 7, 9, 3, 2][:n]
+    g.forwardPrompt(prompt)
+    am, lg = g.forwardVerify(extra, want_logits=True)
+    assert g.cacheLen == len(prompt) + n
+    g.forwardPrompt(prompt)
+    for i, t in enumerate(extra):
+        row = g.forwardDecode(t).copy()
+        assert np.array_equal(row.view(np.uint32), lg[i].view(np.uint32)), i
+        assert am[i] == g.last_argmax
+    g.destroy()
+
+
+@gpu
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+def test_chain_equals_host_greedy(mode):
+    bundle = build("llama", seed=7)
+    g = mllm.PetitGPT(bundle, exec_mode=mode)
+    prompt = [10, 20, 30, 40]
+    greedy = g.generate(prompt, maxNewTokens=20, mode="greedy")["generatedIds"]
+    chain = g.generate(prompt, maxNewTokens=20, mode="chain", chainChunk=7)["generatedIds"]
+    g.destroy()
+    assert chain == greedy
+
+
+@gpu
+@pytest.mark.parametrize("mode", [1, 3])
+def test_chain_stops_at_eos(mode):
+    bundle = build("llama", seed=7)
+    g = mllm.PetitGPT(bundle, exec_mode=mode)
+    prompt = [10, 20, 30, 40]
+    greedy = g.generate(prompt, maxNewTokens=12, mode="greedy")["generatedIds"]
+    eos = greedy[5]
+    first = greedy.index(eos)
+    r = g.generate(prompt, maxNewTokens=12, eosId=eos, mode="chain")
+    g.destroy()
+    assert r["generatedIds"] == greedy[:first + 1] and r["stopReason"] == "eos"
+
+
+@gpu
+@pytest.mark.parametrize("mode", [1, 3])
+def test_gpt2_chain_penalty_equals_host_argmax_gpt2(mode):
+    """Device argmaxGpt2 (3-gram block + 1.15 penalty) == host rule on host logits."""
+    bundle = build("gpt2", seed=8)
+    g = mllm.PetitGPT(bundle, exec_mode=mode)
+    prompt = [1, 2, 3, 4, 5]
+    greedy = g.generate(prompt, maxNewTokens=24, mode="greedy")["generatedIds"]
+    chain = g.generate(prompt, maxNewTokens=24, mode="chain", chainChunk=5)["generatedIds"]
+    g.destroy()
+    assert chain == greedy
+    assert len(set(greedy)) > 3  # the penalty keeps it from echoing one token
+
+
+@gpu
+@pytest.mark.parametrize("mode", [1, 3])
+def test_long_context_splits_vs_oracle(oracle_lib, mode):
+    """Context beyond one 256-position attention split (several splits merged)."""
+    bundle = build("llama", seed=9, max_seq_len=1024)
+    g = mllm.PetitGPT(bundle, exec_mode=mode)
+    ref = oracle_lib.OracleModel(bundle)
+    rng = np.random.default_rng(2)
+    prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 600)]
+    worst, agree = teacher_forced(g, ref, prompt, 4, rng)
+    g.destroy()
+    assert worst < LOGIT_TOL and agree, worst
+
+
+@gpu
+def test_fp16_kv_within_tolerance(oracle_lib):
+    bundle = build("llama", seed=10, max_seq_len=512)
+    g = mllm.PetitGPT(bundle, kv_fp16=True)
+    ref = oracle_lib.OracleModel(bundle)
+    rng = np.random.default_rng(3)
+    prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 300)]
+    worst, agree = teacher_forced(g, ref, prompt, 6, rng)
+    g.destroy()
+    assert worst < LOGIT_TOL and agree, worst
+
+
+@gpu
+def test_model_gemv_plug_point(oracle_lib):
+    bundle = build("llama", seed=12)
+    g = mllm.PetitGPT(bundle)
+    ref = oracle_lib.OracleModel(bundle)
+    x = np.random.default_rng(0).standard_normal(bundle.cfg.d_model).astype(np.float32)
+    for name in ("blocks.0.attn.qkv", "blocks.1.mlp.w1", "lm_head"):
+        assert np.abs(g.gemv(name, x) - ref.gemv(name, x)).max() < 1e-4
+    g.destroy()
+
+
+@gpu
+def test_smollm2_135m_prefill_decode_vs_oracle(oracle_lib):
+    """Config 1 shape at full size: 32-token prompt then 4 greedy steps."""
+    cfg = pgw.CONFIGS["smollm2-135m"]
+    bundle = pgw.parse_pgw(pgw.make_llama(cfg, seed=0))
+    g = mllm.PetitGPT(bundle)
+    ref = oracle_lib.OracleModel(bundle)
+    rng = np.random.default_rng(1)
+    prompt = [int(v) for v in rng.integers(0, cfg.vocab_size, 32)]
+    worst, agree = teacher_forced(g, ref, prompt, 4, None)
+    g.destroy()
+    assert worst < LOGIT_TOL and agree, worst
+
+
+@gpu
+def test_gpt2_124m_prefill_decode_vs_oracle(oracle_lib):
+    cfg = pgw.CONFIGS["gpt2-124m"]
+    bundle = pgw.parse_pgw(pgw.make_gpt2(cfg, seed=0))
+    g = mllm.PetitGPT(bundle)
+    ref = oracle_lib.OracleModel(bundle)
+    rng = np.random.default_rng(4)
+    prompt = [int(v) for v in rng.integers(0, cfg.vocab_size, 16)]
+    worst, agree = teacher_forced(g, ref, prompt, 3, None)
+    g.destroy()
+    assert worst < LOGIT_TOL and agree, worst

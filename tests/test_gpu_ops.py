@@ -1,0 +1,171 @@
+"""GPU parity of the operator-level C ABI against the oracle.
+
+Bars: dequant bit-exact; GEMV rows within a float32 accumulation bound of the
+fp64 oracle (|err| <= 2e-6 * sum|w||x| + 1e-7, written per row); the t-token
+GEMM and the batched GEMV bit-identical to the single GEMV.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from mllm import abi, pgw
+
+torch = pytest.importorskip("torch")
+gpu = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def ptr(t):
+    return C.c_void_p(t.data_ptr())
+
+
+def row_bound(W, x):
+    return 2e-6 * (np.abs(W.astype(np.float64)) @ np.abs(x.astype(np.float64))) + 1e-7
+
+
+SHAPES = [(7, 32), (33, 64), (576, 576), (960, 576), (3072, 576), (576, 1536), (960, 960), (320, 960),
+          (2560, 960), (960, 2560), (2304, 768), (768, 3072), (49152, 960), (50257, 768)]
+
+
+@gpu
+@pytest.mark.parametrize("m,n", SHAPES)
+def test_gemv_q4_vs_oracle(oracle_lib, m, n):
+    rng = np.random.default_rng(m * 7 + n)
+    w = (rng.standard_normal((m, n)) * 0.02).astype(np.float32)
+    packed, sc = pgw.quant_q4(w)
+    x = rng.standard_normal(n).astype(np.float32)
+    dp, ds, dx = dev(packed), dev(sc), dev(x)
+    dy = torch.empty(m, dtype=torch.float32, device="cuda")
+    print(f"gemv_q4 m={m} n={n}", flush=True)
+    abi.call("mllm_gemv_q4", m, n, ptr(dp), ptr(ds), 32, ptr(dx), ptr(dy), None)
+    y = host(dy)
+    ref = oracle_lib.gemv_q4(packed, sc, x, mode="js")
+    W = oracle_lib.dequant_q4(packed, sc)
+    assert (np.abs(y - ref) <= row_bound(W, x)).all()
+
+
+@gpu
+def test_gemm_q4_rows_bit_identical_to_gemv():
+    rng = np.random.default_rng(5)
+    m, n, t = 1000, 960, 9
+    packed, sc = pgw.quant_q4((rng.standard_normal((m, n)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((t, n)).astype(np.float32)
+    dp, ds, dx = dev(packed), dev(sc), dev(x)
+    dy = torch.empty((t, m), dtype=torch.float32, device="cuda")
+    abi.call("mllm_gemm_q4", t, m, n, ptr(dp), ptr(ds), 32, ptr(dx), ptr(dy), None)
+    y = host(dy)
+    for i in range(t):
+        d1 = torch.empty(m, dtype=torch.float32, device="cuda")
+        abi.call("mllm_gemv_q4", m, n, ptr(dp), ptr(ds), 32, ptr(dx[i]), ptr(d1), None)
+        assert np.array_equal(host(d1).view(np.uint32), y[i].view(np.uint32))
+
+
+@gpu
+def test_gemv_q4_batched_matches_single():
+    rng = np.random.default_rng(6)
+    count, m, n = 5, 320, 960
+    mats = [pgw.quant_q4((rng.standard_normal((m, n)) * 0.02).astype(np.float32)) for _ in range(count)]
+    xs = [dev(rng.standard_normal(n).astype(np.float32)) for _ in range(count)]
+    dps = [dev(p) for p, _ in mats]
+    dss = [dev(s) for _, s in mats]
+    ys = [torch.empty(m, dtype=torch.float32, device="cuda") for _ in range(count)]
+    table = lambda ts: dev(np.array([t.data_ptr() for t in ts], np.uint64))  # noqa: E731
+    tp, ts_, tx, ty = table(dps), table(dss), table(xs), table(ys)
+    abi.call("mllm_gemv_q4_batched", count, m, n, ptr(tp), ptr(ts_), ptr(tx), ptr(ty), None)
+    torch.cuda.synchronize()
+    for i in range(count):
+        d1 = torch.empty(m, dtype=torch.float32, device="cuda")
+        abi.call("mllm_gemv_q4", m, n, ptr(dps[i]), ptr(dss[i]), 32, ptr(xs[i]), ptr(d1), None)
+        assert np.array_equal(host(d1), host(ys[i]))
+
+
+@gpu
+@pytest.mark.parametrize("m,n", [(96, 64), (960, 960), (2560, 960), (49152, 960)])
+def test_gemv_q8_row_and_g32_vs_oracle(oracle_lib, m, n):
+    rng = np.random.default_rng(m + n)
+    w = (rng.standard_normal((m, n)) * 0.02).astype(np.float32)
+    x = rng.standard_normal(n).astype(np.float32)
+    dx = dev(x)
+    q, s = pgw.quant_q8row(w)
+    dq, ds = dev(q), dev(s)  # keep the device buffers alive until the kernel has run
+    dy = torch.empty(m, dtype=torch.float32, device="cuda")
+    abi.call("mllm_gemv_q8", m, n, ptr(dq), ptr(ds), ptr(dx), ptr(dy), None)
+    ref = oracle_lib.gemv_q8(q, s, x)
+    W = oracle_lib.dequant_q8row(q, s)
+    assert (np.abs(host(dy) - ref) <= row_bound(W, x)).all()
+    qg, sg = pgw.quant_q8g32(w)
+    dqg, dsg = dev(qg), dev(sg)
+    abi.call("mllm_gemv_q8_g32", m, n, ptr(dqg), ptr(dsg), ptr(dx), ptr(dy), None)
+    refg = oracle_lib.gemv_q8g32(qg, sg, x)
+    Wg = oracle_lib.dequant_q8g32(qg, sg)
+    assert (np.abs(host(dy) - refg) <= row_bound(Wg, x)).all()
+
+
+@gpu
+@pytest.mark.parametrize("m,n", [(5, 7), (64, 576), (300, 1000)])
+def test_gemv_f32_vs_oracle(oracle_lib, m, n):
+    rng = np.random.default_rng(n)
+    w = rng.standard_normal((m, n)).astype(np.float32)
+    x = rng.standard_normal(n).astype(np.float32)
+    dy = torch.empty(m, dtype=torch.float32, device="cuda")
+    dw, dx = dev(w), dev(x)
+    abi.call("mllm_gemv_f32", m, n, ptr(dw), ptr(dx), ptr(dy), None)
+    assert (np.abs(host(dy) - oracle_lib.gemv_f32(w, x)) <= row_bound(w, x)).all()
+
+
+@gpu
+def test_rms_norm_and_silu_mul_vs_oracle(oracle_lib):
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((3, 576)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 576).astype(np.float32)
+    out = torch.empty((3, 576), dtype=torch.float32, device="cuda")
+    dx, dw = dev(x), dev(w)
+    abi.call("mllm_rms_norm", 576, ptr(dx), ptr(dw), ptr(out), 3, C.c_float(1e-6), None)
+    assert np.allclose(host(out), oracle_lib.rms_norm(x, w, 1e-6, "js"), rtol=2e-6, atol=2e-6)
+    a = (rng.standard_normal(1536) * 3).astype(np.float32)
+    b = rng.standard_normal(1536).astype(np.float32)
+    da, db = dev(a), dev(b)
+    abi.call("mllm_silu_mul", 1536, ptr(da), ptr(db), None)
+    assert np.allclose(host(da), oracle_lib.silu_mul(a, b, "js"), rtol=4e-6, atol=1e-7)
+
+
+@gpu
+def test_dequant_q4_bit_exact(oracle_lib):
+    rng = np.random.default_rng(9)
+    m, n = 70, 576
+    packed = rng.integers(0, 256, (m, n // 2), dtype=np.uint8)
+    sc = (rng.standard_normal((m, n // 32)) * 0.01).astype(np.float32)
+    sc[0, :] = [0.0, 1.4e-45, 3e38, -1.0] * 4 + [1e-38, 7.0]
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    dp, ds = dev(packed), dev(sc)
+    abi.call("mllm_dequant_q4", m, n, ptr(dp), ptr(ds), 32, ptr(out), None)
+    assert np.array_equal(host(out).view(np.uint32), oracle_lib.dequant_q4(packed, sc).view(np.uint32))
+
+
+@gpu
+def test_gemv_q4_linearity_full_lm_head():
+    """Size-independent property at the 360M lm_head shape: W(a+b) = Wa + Wb
+    within float32 rounding."""
+    rng = np.random.default_rng(10)
+    m, n = 49152, 960
+    packed, sc = pgw.quant_q4((rng.standard_normal((m, n)) * 0.02).astype(np.float32))
+    dp, ds = dev(packed), dev(sc)
+    a = rng.standard_normal(n).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    outs = []
+    for v in (a, b, (a + b).astype(np.float32)):
+        dy = torch.empty(m, dtype=torch.float32, device="cuda")
+        dv = dev(v)
+        abi.call("mllm_gemv_q4", m, n, ptr(dp), ptr(ds), 32, ptr(dv), ptr(dy), None)
+        torch.cuda.synchronize()
+        outs.append(host(dy))
+    assert np.abs(outs[2] - (outs[0] + outs[1])).max() < 1e-4

@@ -1,0 +1,68 @@
+"""The Node.js host side (microllm-lab_amd/js): the PGW reader and the sampling
+/ draft helpers on the CPU, and the HipPetitGPT engine through the N-API addon
+on the GPU, each compared with the Python mirror of the same API."""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+import mllm
+from mllm import pgw
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+JS = os.path.join(ROOT, "microllm-lab_amd", "js")
+NODE = shutil.which("node")
+pytestmark = pytest.mark.skipif(NODE is None, reason="node not installed")
+
+
+def run_node(script, *args, timeout=300):
+    r = subprocess.run([NODE, os.path.join(JS, script), *args], capture_output=True, text=True, timeout=timeout)
+    assert r.returncode == 0, r.stderr
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def test_js_parse_pgw_and_sampling(tmp_path, oracle_lib):
+    cfg = pgw.small_config("gpt2")
+    buf = pgw.make_gpt2(cfg, seed=2)
+    (tmp_path / "m.pgw").write_bytes(buf)
+    rng = np.random.default_rng(0)
+    drafts = [{"seq": [int(v) for v in rng.integers(0, 4, int(rng.integers(0, 24)))], "k": int(rng.integers(1, 9)),
+               "n": 3} for _ in range(30)]
+    argm = [[float(v) for v in rng.standard_normal(9).astype(np.float32)] for _ in range(5)] + [[0.5, 0.5, 0.1]]
+    gp = [{"logits": [float(v) for v in rng.standard_normal(10).astype(np.float32)],
+           "hist": [int(v) for v in rng.integers(0, 10, int(rng.integers(0, 30)))]} for _ in range(30)]
+    (tmp_path / "cases.json").write_text(json.dumps({"drafts": drafts, "argmax": argm, "gpt2": gp}))
+    out = run_node("selftest.mjs", str(tmp_path / "m.pgw"), str(tmp_path / "cases.json"))
+    b = pgw.parse_pgw(buf)
+    assert out["kind"] == "q4" and out["cfg"]["arch"] == "gpt2" and out["payloadOff"] == b.payload_off
+    assert out["cfg"]["qGroup"] == 1 and out["cfg"]["nLayers"] == cfg.n_layers
+    assert [t["name"] for t in out["table"]] == b.order
+    for t in out["table"]:
+        e = b.tensors[t["name"]]
+        assert t["offset"] == e["offset"] and t["nbytes"] == e["nbytes"]
+    assert out["drafts"] == [oracle_lib.lookup_draft(d["seq"], d["k"], d["n"]) for d in drafts]
+    assert out["argmax"] == [oracle_lib.argmax(np.array(a, np.float32)) for a in argm]
+    assert out["argmaxGpt2"] == [oracle_lib.argmax_gpt2(np.array(c["logits"], np.float32), c["hist"]) for c in gp]
+    assert "bad magic" in out["badMagic"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("arch,mode", [("llama", "greedy"), ("llama", "chain"), ("llama", "spec"), ("gpt2", "chain")])
+def test_js_engine_matches_python_engine(tmp_path, arch, mode):
+    bundle_bytes = pgw.make_model(pgw.small_config(arch), seed=5)
+    (tmp_path / "m.pgw").write_bytes(bundle_bytes)
+    prompt = [3, 9, 27, 81, 3, 9, 27, 81, 3, 9]
+    spec = {"prompt": prompt, "maxNewTokens": 16, "mode": mode, "specK": 4, "decodeLogits": [5, 6]}
+    (tmp_path / "spec.json").write_text(json.dumps(spec))
+    out = run_node("run_generate.mjs", str(tmp_path / "m.pgw"), str(tmp_path / "spec.json"))
+    g = mllm.PetitGPT(pgw.parse_pgw(bundle_bytes))
+    want = g.generate(prompt, maxNewTokens=16, mode="greedy")
+    rows = [g.forwardPrompt(prompt).copy()] + [g.forwardDecode(t).copy() for t in (5, 6)]
+    g.destroy()
+    assert out["generatedIds"] == want["generatedIds"]
+    assert out["streamed"] == out["generatedIds"]
+    assert np.array_equal(np.array(out["rows"], np.float32), np.stack(rows))
+    assert "destroyed" in out["destroyedError"]
