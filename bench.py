@@ -80,6 +80,30 @@ def token_bytes(cfg, seq, kv_bytes=4):
     return weights + norms + kv
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes recorded in profiles/decode_traffic.json (scaled by the same counters
+    read on a plain copy of known size), or None when no record matches."""
+    path = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return None if rec is None else rec.get("hbm_bytes_per_launch")
+
+
+def copy_calibration(torch):
+    """A plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE."""
+    n = 256 << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5}), flush=True)
+
+
 # ---------------------------------------------------------------- decode
 def bench_decode(mllm, pgw, torch, args):
     cfg = pgw.CONFIGS["smollm2-135m"]
@@ -114,6 +138,16 @@ def bench_decode(mllm, pgw, torch, args):
     per_token_us = {ph: prof[ph] * (cfg.n_layers if ph in ("QKV", "ATTN", "O", "UP", "DOWN") else 1) for ph in PHASES}
     dom = max(per_token_us, key=per_token_us.get)
     achieved = pb[dom] / (prof[dom] * 1e-6) / 1e9
+    # host loop: forwardDecode per token with the logits copied back (PCIe-inclusive; not `value`)
+    g.resetCache()
+    g.forwardPrompt(prompt)
+    nxt = g.last_argmax
+    n_host = 32
+    t0 = time.perf_counter()
+    for _ in range(n_host):
+        g.forwardDecode(nxt)
+        nxt = g.last_argmax
+    host_tok_s = n_host / (time.perf_counter() - t0)
     g.destroy()
     mean_seq = len(prompt) + (args.steps + 1) / 2
     step_bytes = token_bytes(cfg, mean_seq)
@@ -129,13 +163,14 @@ def bench_decode(mllm, pgw, torch, args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 5),
-            "traffic": None,
+            "traffic": measured_traffic(f"k_phase<{dom}>"),
             "bytes_per_launch": pb[dom],
             "us_per_launch": round(prof[dom], 3),
         },
         "phase_us": {k: round(v, 3) for k, v in prof.items()},
         "decode_step_gbs": round(step_bytes / (wall / args.steps) / 1e9, 2),
         "decode_step_bytes": step_bytes,
+        "host_loop_tok_s": round(host_tok_s, 1),
     }
 
 
@@ -316,6 +351,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 256 MiB device copy (counter calibration for the traffic figure)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -335,6 +372,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        copy_calibration(torch)
+        return
     dec = bench_decode(mllm, pgw, torch, args)
     log(f"[bench] decode {dec['value']:.1f} tok/s, phases {dec['phase_us']}")
     line = {
@@ -348,15 +388,16 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4 weights, f32 arithmetic",
+        "dtype": "f32",
         "data": "synthetic: N(0,0.02) weights (seed 0) quantised by quant_q4; 32 prompt ids uniform (seed 1)",
         "config": {"workload": "smollm2-135m-q4 greedy decode, 32-token prompt, batch 1 (BASELINE config 1)",
-                   "exec_mode": args.exec_mode, "kv_cache": "f32"},
+                   "weights": "q4 group-32 (PGW1)", "exec_mode": args.exec_mode, "kv_cache": "f32"},
         "roofline": dec["roofline"],
         "kernel_ms_per_step": round(dec["kernel_ms_per_step"], 4),
         "phase_us": dec["phase_us"],
         "decode_step_gbs": dec["decode_step_gbs"],
         "decode_step_bytes": dec["decode_step_bytes"],
+        "host_loop_tok_s": dec["host_loop_tok_s"],
     }
     if not args.no_cpu:
         line["cpu_baseline"] = bench_cpu(pgw, __import__("oracle"), args.cpu_seconds)

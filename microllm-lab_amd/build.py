@@ -7,10 +7,17 @@ hipcc cross-compiles for gfx950 without a GPU.  All HIP code is built with
 packed-FP32 instructions disabled (-Xclang -target-feature -Xclang
 -packed-fp32-ops) and without FMA contraction (the kernels spell their FMAs
 out), so results do not depend on the compiler's contraction choices.
+
+Every kernel's register and scratch usage is recorded from the compiler's
+resource-usage remarks into _build/resource_usage.json, and the build fails
+if any kernel uses scratch memory: a register array that the compiler moved
+to scratch turns each access into a memory round trip (and adds HBM traffic).
 """
 from __future__ import annotations
 
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -36,6 +43,9 @@ HIP_FLAGS = [
 ]
 
 
+RESOURCE_JSON = os.path.join(BUILD, "resource_usage.json")
+
+
 def _run(cmd):
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     # hipcc's host pass does not know the packed-fp32 feature; drop that line
@@ -45,17 +55,42 @@ def _run(cmd):
     return lines
 
 
+def _resource_usage(lines):
+    """{kernel: {field: value}} from -Rpass-analysis=kernel-resource-usage remarks."""
+    out, cur = {}, None
+    for ln in lines:
+        m = re.search(r"remark: Function Name: (\S+)", ln)
+        if m:
+            cur = out.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"remark:\s+([A-Za-z ]+?)(?: \[[^\]]*\])?: (\d+) \[-Rpass", ln)
+        if m and cur is not None:
+            cur[m.group(1).strip()] = int(m.group(2))
+    return out
+
+
 def build_lib(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     objs = []
 
     def compile_one(src):
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-        _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
-        return obj
+        lines = _run([HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", os.path.join(CSRC, src),
+                      "-o", obj])
+        return obj, _resource_usage(lines)
 
     with ThreadPoolExecutor(max_workers=len(HIP_SOURCES)) as ex:
-        objs = list(ex.map(compile_one, HIP_SOURCES))
+        results = list(ex.map(compile_one, HIP_SOURCES))
+    objs = [o for o, _ in results]
+    usage = {}
+    for _, u in results:
+        usage.update(u)
+    with open(RESOURCE_JSON, "w") as f:
+        json.dump(usage, f, indent=1, sort_keys=True)
+    spilled = {k: v for k, v in usage.items() if v.get("ScratchSize", 0) > 0}
+    if spilled:
+        raise RuntimeError("kernels use scratch memory: " + ", ".join(f"{k} ({v['ScratchSize']} B/lane)"
+                                                                      for k, v in sorted(spilled.items())))
     tmp = LIB + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, LIB)

@@ -147,10 +147,13 @@ __device__ __forceinline__ void stage_group_sums(const float *xs, float *xsum, i
 __device__ __forceinline__ void stage_rows(const float *__restrict__ x, int ldx, int m, int n, float *xs) {
   const int nq = n >> 2, total = m * nq, ng = n >> 5;
   for (int base = 0; base < total; base += 4 * WG) {
+    // Every element of v is written on every path: a partially written
+    // register array is kept in scratch memory by the compiler.
     float4 v[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int f = base + threadIdx.x + k * WG;
+      v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (f < total) {
         const int t = f / nq, q = f - t * nq;
         v[k] = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + 4 * q);
@@ -221,18 +224,28 @@ template <int C>
 __device__ __forceinline__ void tile_compute(const TileRegs<C> &R, int nrows, int ng, int nch, int m,
                                              const float *xs, const float *xsum, int gfirst, int gstep,
                                              float *part, float *out, int ostride) {
-  int g = gfirst;
+  // Group index of each register chunk, computed once; the token loop is the
+  // outer one so every R.w[j] / R.s[j] access has a constant index and the
+  // tile stays in VGPRs (a runtime index would move it to scratch memory).
+  int gj[C];
+  {
+    int g = gfirst;
 #pragma unroll
-  for (int j = 0; j < C; ++j) {
-    const int c = threadIdx.x + j * WG;
-    if (c < nch) {
-      for (int t = 0; t < m; ++t) {
-        const float d = q4_chunk_dot(R.w[j], xs + (t * ng + g) * XS);
-        part[t * nch + c] = (d - 8.f * xsum[t * ng + g]) * R.s[j];
+    for (int j = 0; j < C; ++j) {
+      gj[j] = g;
+      g += gstep;
+      if (g >= ng) g -= ng;
+    }
+  }
+  for (int t = 0; t < m; ++t) {
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const int c = threadIdx.x + j * WG;
+      if (c < nch) {
+        const float d = q4_chunk_dot(R.w[j], xs + (t * ng + gj[j]) * XS);
+        part[t * nch + c] = (d - 8.f * xsum[t * ng + gj[j]]) * R.s[j];
       }
     }
-    g += gstep;
-    if (g >= ng) g -= ng;
   }
   __syncthreads();
   for (int i = threadIdx.x; i < nrows * m; i += WG) {

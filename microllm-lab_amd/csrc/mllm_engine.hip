@@ -50,7 +50,13 @@ constexpr int ACH = 256;  // positions per attention split (one per thread)
 constexpr int MAXT = 16;  // tokens per pass (upper bound; LDS sets the real one)
 constexpr int APS = 68;   // floats per attention partial: m, l, pad, pad, acc[64]
 constexpr int TC = 2;     // tile capacity of the decode phases: TC * WG chunks
-constexpr int TILE_TARGET = 320;  // chunks per GEMV tile (~0.15 us of VALU on one CU)
+#ifndef MLLM_TILE_TARGET
+#define MLLM_TILE_TARGET 320
+#endif
+#ifndef MLLM_LM_TILES_PER_WG
+#define MLLM_LM_TILES_PER_WG 1
+#endif
+constexpr int TILE_TARGET = MLLM_TILE_TARGET;  // chunks per GEMV tile (~0.15 us of VALU on one CU)
 constexpr int QSPLIT = 4;         // QKV tiles per head
 constexpr unsigned kSpinLimit = 1u << 22;
 
@@ -581,8 +587,50 @@ __device__ __forceinline__ float gpt2_adjust(float v, int i, const int *ban, int
   return v;
 }
 
+// One lm_head tile whose weights are in R: logits rows [r0, r0+nr) of the m
+// tokens from tb, then the tile's first maximum per token (gpt2 chain: with
+// the argmaxGpt2 adjustments).
+__device__ __forceinline__ void lm_tile(const DecParams &P, const TileRegs<TC> &R, int tile, int tb, int m,
+                                        const Lds &s, bool penal, const int *lists, int nban, int nrec) {
+  const int ng = P.D >> 5, rpt = P.lm_rpt;
+  const int r0 = tile * rpt, nr = min(rpt, P.V - r0);
+  tile_compute<TC>(R, nr, ng, nr * ng, m, s.xs, s.xsum, threadIdx.x % ng, WG % ng, s.part, s.out, rpt);
+  for (int e = threadIdx.x; e < m * nr; e += WG) {
+    const int t = e / nr, r = e - t * nr;
+    P.logits[(size_t)(tb + t) * P.V + r0 + r] = s.out[t * rpt + r];
+  }
+  if (threadIdx.x < 64) {
+    for (int t = 0; t < m; ++t) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int r = threadIdx.x; r < nr; r += 64) {
+        float v = s.out[t * rpt + r];
+        if (penal) v = gpt2_adjust(v, r0 + r, lists + 34, nban, lists + 2, nrec);
+        if (amax_better(v, r0 + r, bv, bi)) {
+          bv = v;
+          bi = r0 + r;
+        }
+      }
+      wave_argmax(bv, bi);
+      if (threadIdx.x == 0) {
+        P.amv[(size_t)(tb + t) * P.lm_tiles + tile] = bv;
+        P.ami[(size_t)(tb + t) * P.lm_tiles + tile] = bi;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ void lm_load(const DecParams &P, int tile, TileRegs<TC> &R) {
+  if (tile < P.lm_tiles) {
+    const int ng = P.D >> 5, r0 = tile * P.lm_rpt, nr = min(P.lm_rpt, P.V - r0);
+    tile_load<TC>(P.lm, r0, nr, 0, ng, nr * ng, R);
+  }
+}
+
 // lm_head over row tiles wg, wg + nwg, ...; the next tile's weights are
-// loaded while the current one is computed.
+// loaded while the current one is computed (two register sets used in
+// turn, each with constant indices so both stay in VGPRs).
 __device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, const Dep &dep, float *smem) {
   const PassState &S = *P.st;
   const int lm_rows = S.lm_rows;
@@ -590,12 +638,9 @@ __device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, const D
   const int tb = lm_rows == 1 ? m_all - 1 : 0;
   const int m = m_all - tb;
   const int D = P.D, ng = D >> 5, rpt = P.lm_rpt;
-  TileRegs<TC> R[2];
+  TileRegs<TC> Ra, Rb;
   int tile = wg;
-  {
-    const int r0 = tile * rpt, nr = min(rpt, P.V - r0);
-    tile_load<TC>(P.lm, r0, nr, 0, ng, nr * ng, R[0]);
-  }
+  lm_load(P, tile, Ra);
   const Gains G = load_gains(P, P.norm_f);
   dep_wait(P, dep);
   Lds s = carve(smem, m, ng);
@@ -616,40 +661,15 @@ __device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, const D
     lists[1] = nrec;
   }
   stage_normed(P, tb, m, G, s.xs, s.xsum, s.red);
-  const int gf = threadIdx.x % ng, gs = WG % ng;
   const int nban = penal ? lists[0] : 0, nrec = penal ? lists[1] : 0;
-  for (int k = 0; tile < P.lm_tiles; ++k, tile += nwg) {
-    const int r0 = tile * rpt, nr = min(rpt, P.V - r0);
-    const int next = tile + nwg;
-    if (next < P.lm_tiles) {
-      const int n0 = next * rpt, nn = min(rpt, P.V - n0);
-      tile_load<TC>(P.lm, n0, nn, 0, ng, nn * ng, R[(k + 1) & 1]);
-    }
-    tile_compute<TC>(R[k & 1], nr, ng, nr * ng, m, s.xs, s.xsum, gf, gs, s.part, s.out, rpt);
-    for (int e = threadIdx.x; e < m * nr; e += WG) {
-      const int t = e / nr, r = e - t * nr;
-      P.logits[(size_t)(tb + t) * P.V + r0 + r] = s.out[t * rpt + r];
-    }
-    if (threadIdx.x < 64) {
-      for (int t = 0; t < m; ++t) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int r = threadIdx.x; r < nr; r += 64) {
-          float v = s.out[t * rpt + r];
-          if (penal) v = gpt2_adjust(v, r0 + r, lists + 34, nban, lists + 2, nrec);
-          if (amax_better(v, r0 + r, bv, bi)) {
-            bv = v;
-            bi = r0 + r;
-          }
-        }
-        wave_argmax(bv, bi);
-        if (threadIdx.x == 0) {
-          P.amv[(size_t)(tb + t) * P.lm_tiles + tile] = bv;
-          P.ami[(size_t)(tb + t) * P.lm_tiles + tile] = bi;
-        }
-      }
-    }
-    __syncthreads();
+  while (tile < P.lm_tiles) {
+    lm_load(P, tile + nwg, Rb);
+    lm_tile(P, Ra, tile, tb, m, s, penal, lists, nban, nrec);
+    tile += nwg;
+    if (tile >= P.lm_tiles) break;
+    lm_load(P, tile + nwg, Ra);
+    lm_tile(P, Rb, tile, tb, m, s, penal, lists, nban, nrec);
+    tile += nwg;
   }
 }
 
@@ -1272,7 +1292,10 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   P.dn_rpt = tile_rows(ngf);
   P.lm_rpt = tile_rows(ngd);
   P.lm_tiles = (V + P.lm_rpt - 1) / P.lm_rpt;
-  P.lm_grid = P.lm_tiles;  // one tile per workgroup: every tile's loads in flight at once
+  // MLLM_LM_TILES_PER_WG = 1: one tile per workgroup, every tile's loads in
+  // flight at once; larger values trade workgroups for the register double
+  // buffer of phase_lm.
+  P.lm_grid = (P.lm_tiles + MLLM_LM_TILES_PER_WG - 1) / MLLM_LM_TILES_PER_WG;
   // every GEMV tile must fit the TC * WG chunk registers of a workgroup
   const int cap = TC * WG;
   if (16 * ngd > cap || P.o_rpt * ngd > cap || P.up_rpt * ngd > cap || P.dn_rpt * ngf > cap || P.lm_rpt * ngd > cap)

@@ -27,9 +27,16 @@ function now() {
 }
 
 export class HipPetitGPT {
-  constructor(bundle, opts) {
+  /**
+   * bundle: a parsePgw() result, or a CPU PetitGPT (its .bundle is used), so
+   * the GpuPetitGPT construction of webgpu.js:867 (new X(cpu, info); await
+   * x.init()) works unchanged.  The payload is copied to the device here; the
+   * class keeps no reference to the host buffer afterwards.
+   */
+  constructor(source, opts) {
     const o = opts || {};
-    this.bundle = bundle;
+    const bundle = source && source.bundle && source.bundle.cfg ? source.bundle : source;
+    if (!bundle || !bundle.cfg) throw new Error("HipPetitGPT needs a parsePgw() bundle or a PetitGPT");
     this.cfg = bundle.cfg;
     this.kind = bundle.kind;
     this.isGpt2 = bundle.cfg.arch === "gpt2";
@@ -59,6 +66,11 @@ export class HipPetitGPT {
     this.mode = `hip-${bundle.kind}`;
     this.lastArgmax = 0;
     this.lastTiming = null;
+  }
+
+  /** GpuPetitGPT.init() counterpart: the device copy is made by the constructor. */
+  async init() {
+    return this;
   }
 
   get cacheLen() {

@@ -10,7 +10,9 @@ import ctypes as C
 import os
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG_DIR, "libmllm.so")
+# MLLM_LIBRARY may name another build of the same library (e.g. one compiled
+# with different tuning constants); it must export the same symbols.
+LIB_PATH = os.environ.get("MLLM_LIBRARY") or os.path.join(PKG_DIR, "libmllm.so")
 
 MLLM_OK = 0
 ERR_NAMES = {1: "INVALID", 2: "HIP", 3: "OOM", 4: "UNSUPPORTED", 5: "DEVICE"}

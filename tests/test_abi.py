@@ -1,6 +1,7 @@
 """CPU checks of the C-ABI library: it loads, exports every entry point that
 include/mllm.h declares, and rejects bad arguments before touching the GPU."""
 import ctypes as C
+import json
 import os
 import re
 
@@ -47,3 +48,16 @@ def test_null_pointer_errors():
     assert abi.lib().mllm_model_create(None, None, 0, None, 0, None) == 1
     assert abi.lib().mllm_model_destroy(None) == 0
     assert abi.lib().mllm_cache_len(None) == -1
+
+
+def test_no_kernel_uses_scratch_memory():
+    """The build records each kernel's resources (compiler remarks); a kernel
+    whose register arrays went to scratch memory pays a memory round trip per
+    access and extra HBM traffic."""
+    path = os.path.join(ROOT, "microllm-lab_amd", "_build", "resource_usage.json")
+    if not os.path.exists(path):
+        pytest.skip("library not built in this tree")
+    with open(path) as f:
+        usage = json.load(f)
+    assert usage, "no kernels recorded"
+    assert {k: v["ScratchSize"] for k, v in usage.items() if v.get("ScratchSize", 0)} == {}
