@@ -38,7 +38,7 @@ import numpy as np  # noqa: E402
 
 METRIC = "decode tok/s (135M Q4, bs1) + Q4 GEMV GB/s as % of 8 TB/s HBM peak"
 HBM_PEAK_GBS = 8000.0
-PHASES = ("QKV", "ATTN", "O", "UP", "DOWN", "LM", "ARGMAX")
+LAYER_PHASES = ("QKV", "ATTN", "MLP")
 
 
 def log(*a):
@@ -51,19 +51,21 @@ def q4_bytes(rows, cols):
 
 
 def phase_bytes(cfg, seq, kv_bytes=4):
-    """Algorithmic bytes per launch of each phase at one decode token with `seq`
-    positions in the cache: weights + activations read and written."""
+    """Algorithmic bytes per launch of each decode phase at one token with `seq`
+    positions in the cache: the weights it reads once plus one read of its input
+    vector and one write of its output (the split-K partials the engine passes
+    between phases are implementation traffic and are not counted)."""
     D, FF, V = cfg.d_model, cfg.d_ff, cfg.vocab_size
     hd = D // cfg.n_heads
     kvd = cfg.n_kv_heads * hd
     qkv_rows = D + 2 * kvd
+    mlp_in = 1 if cfg.arch == "gpt2" else 2
     return {
         "QKV": q4_bytes(qkv_rows, D) + 4 * D * 2 + 4 * qkv_rows,
-        "ATTN": 2 * cfg.n_kv_heads * seq * hd * kv_bytes + 4 * D + 4 * (D + cfg.n_heads * 2),
-        "O": q4_bytes(D, D) + 4 * D + 4 * D * 2,
-        "UP": (1 if cfg.arch == "gpt2" else 2) * q4_bytes(FF, D) + 4 * D * 2 + 4 * FF,
-        "DOWN": q4_bytes(D, FF) + 4 * FF + 4 * D * 2,
-        "LM": q4_bytes(V, D) + 4 * D * 2 + 4 * V,
+        "ATTN": 2 * cfg.n_kv_heads * seq * hd * kv_bytes + 4 * D + q4_bytes(D, D) + 4 * D,
+        "MLP": mlp_in * q4_bytes(FF, D) + q4_bytes(D, FF) + 4 * D * 2 + 4 * D,
+        "FINAL": 4 * D * 3,
+        "LM": q4_bytes(V, D) + 4 * D + 4 * V,
         "ARGMAX": 0,
     }
 
@@ -135,7 +137,7 @@ def bench_decode(mllm, pgw, torch, args):
     prof = g.profile_decode(first, 32)
     seq_mean = len(prompt) + 16
     pb = phase_bytes(cfg, seq_mean)
-    per_token_us = {ph: prof[ph] * (cfg.n_layers if ph in ("QKV", "ATTN", "O", "UP", "DOWN") else 1) for ph in PHASES}
+    per_token_us = {ph: us * (cfg.n_layers if ph in LAYER_PHASES else 1) for ph, us in prof.items()}
     dom = max(per_token_us, key=per_token_us.get)
     achieved = pb[dom] / (prof[dom] * 1e-6) / 1e9
     # host loop: forwardDecode per token with the logits copied back (PCIe-inclusive; not `value`)

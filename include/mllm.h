@@ -176,9 +176,8 @@ int mllm_model_gemv(mllm_model *model, const char *name, const float *x, float *
 /* Execution mode of the decode step: 1 (default) = one kernel per phase, a
  * chained decode step replayed from a HIP graph; 2 = the same kernels
  * launched directly (for profilers); 0 = one persistent cooperative kernel per
- * launch with grid barriers between phases; 3 = one persistent cooperative
- * kernel per launch whose work items wait only for the items they read
- * (per-item completion flags).  Results are bit-identical across modes. */
+ * launch with grid barriers between phases.  Results are bit-identical
+ * across modes. */
 int mllm_set_exec_mode(mllm_model *model, int mode);
 
 /* GpuPetitGPT.lastTiming {n, gpuMs} (webgpu.js:1143-1160): the time between
@@ -188,11 +187,15 @@ int mllm_last_timing(const mllm_model *model, float *gpu_ms, int *n_tokens);
 
 /* Per-phase timing of the decode step, the per-kernel counterpart of
  * lastTiming (webgpu.js:1143-1160): runs n_steps chained steps from token
- * `first` at position cacheLen, launching each phase kernel directly with HIP
- * events recorded on the model's stream around it, and writes the mean
- * microseconds per launch of the phases QKV, ATTN, O, UP, DOWN, LM, ARGMAX to
- * phase_us[0..7).  cacheLen advances by n_steps. */
+ * `first` at position cacheLen, launching each phase kernel directly on the
+ * model's stream with HIP events that stamp the kernel's own begin and end
+ * (hipExtLaunchKernel), and writes the mean microseconds per launch of each
+ * phase to phase_us[0..MLLM_PHASES): QKV, ATTN, MLP, FINAL, LM, ARGMAX (names
+ * from mllm_phase_name).  cacheLen advances by n_steps. */
+#define MLLM_PHASES 6
 int mllm_profile_decode(mllm_model *model, int32_t first, int n_steps, float *phase_us);
+/* Name of decode phase `phase` (0 <= phase < MLLM_PHASES), else NULL. */
+const char *mllm_phase_name(int phase);
 
 /* Bytes of device memory the model holds (GpuPetitGPT.bytesAllocated). */
 uint64_t mllm_model_device_bytes(const mllm_model *model);

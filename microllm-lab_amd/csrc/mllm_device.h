@@ -85,10 +85,62 @@ __device__ __forceinline__ float q8_chunk_dot(const uint4 w, const float *__rest
   return (a0 + a1) + (a2 + a3);
 }
 
+// Cross-lane moves through DPP (a VALU operand modifier) instead of
+// ds_bpermute, which goes through the LDS crossbar and costs an LDS round
+// trip per step.  Control codes (GFX9 DPP16): quad_perm(1,0,3,2) = 0xB1,
+// quad_perm(2,3,0,1) = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140.
+// Callers run them with all 64 lanes active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+
+// The partner of lane ^ 1 (quad_perm), e.g. the two groups of a row pair.
+__device__ __forceinline__ float lane_xor1(float v) { return dpp_f<0xB1>(v); }
+
+// Sum over each 16-lane row, left in every lane of the row: pairs (xor 1),
+// quads (xor 2), half rows (mirror within 8), rows (mirror within 16).
+// Every lane of a row ends with the same bits (each step adds the same two
+// values).
+__device__ __forceinline__ float row16_sum(float v) {
+  v = v + dpp_f<0xB1>(v);
+  v = v + dpp_f<0x4E>(v);
+  v = v + dpp_f<0x141>(v);
+  v = v + dpp_f<0x140>(v);
+  return v;
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return v;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Wave-wide sum / max, uniform in the wave: rows reduced with DPP, then the
+// four row results read as scalars and combined as (r0 + r1) + (r2 + r3).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
 // Deterministic block-wide sum for 256 threads; red needs 4 floats of LDS.
 __device__ __forceinline__ float block_sum(float v, float *red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v = wave_sum(v);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wv] = v;
@@ -99,8 +151,7 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 }
 
 __device__ __forceinline__ float block_max(float v, float *red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  v = wave_max(v);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wv] = v;
@@ -116,16 +167,37 @@ __device__ __forceinline__ bool amax_better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
+template <int CTRL>
+__device__ __forceinline__ void amax_step(float &v, int &i) {
+  const float ov = dpp_f<CTRL>(v);
+  const int oi = dpp_i<CTRL>(i);
+  if (amax_better(ov, oi, v, i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+// Wave-wide first maximum (value, index), uniform in the wave.  The relation
+// is a total order on (value, index) pairs, so the result does not depend on
+// the combining order.
 __device__ __forceinline__ void wave_argmax(float &v, int &i) {
+  amax_step<0xB1>(v, i);
+  amax_step<0x4E>(v, i);
+  amax_step<0x141>(v, i);
+  amax_step<0x140>(v, i);
+  float bv = readlane_f(v, 0);
+  int bi = __builtin_amdgcn_readlane(i, 0);
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(v, o, 64);
-    const int oi = __shfl_xor(i, o, 64);
-    if (amax_better(ov, oi, v, i)) {
-      v = ov;
-      i = oi;
+  for (int r = 16; r < 64; r += 16) {
+    const float rv = readlane_f(v, r);
+    const int ri = __builtin_amdgcn_readlane(i, r);
+    if (amax_better(rv, ri, bv, bi)) {
+      bv = rv;
+      bi = ri;
     }
   }
+  v = bv;
+  i = bi;
 }
 
 // Per-group sums of the staged activations: xsum[t*ng+g] = sum_k xs[(t*ng+g)*XS+k]

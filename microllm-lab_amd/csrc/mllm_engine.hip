@@ -1,35 +1,44 @@
 // mllm_engine.hip -- the fused single-token Q4 decode step on MI355X and the
 // engine-level C ABI (PetitGPT API of engine/infer.js:289-647).
 //
-// One decode step = L x [QKV, ATTN, O, UP, DOWN] + LM + ARGMAX phases
-// (engine/infer.js:579-601; the reference GPU runs the same graph as 244
+// One decode step = L x [QKV, ATTN, MLP] + FINAL + LM + ARGMAX kernels
+// (the graph of engine/infer.js:579-601; the reference GPU runs it as 244
 // dispatches, engine/webgpu-metal.js:1242-1322):
-//   QKV   16-row tiles of blocks.i.attn.qkv holding RoPE partner rows d, d+32
-//         prologue: embed (layer 0) or load x; RMSNorm/LayerNorm in LDS
-//         epilogue: bias (gpt2), RoPE (llama), q -> scratch, k/v -> KV cache
-//   ATTN  (one workgroup per (token, 256-position split, head))
-//         scores, split-local softmax statistics and P.V -> partials (m, l, acc)
-//   O     prologue: combine the splits -> attention output; epilogue x += W_o.att
-//   UP    prologue: norm2; gate and up rows of the same index -> silu(g)*u
-//         (gpt2: fc + bias -> GELU-tanh)
-//   DOWN  epilogue x += W_2.h (+ bias)
-//   LM    prologue: final norm; grid-stride row tiles with the next tile's
-//         weights in flight; logits + per-tile argmax (gpt2 chain: 3-gram
-//         block and repetition penalty of infer.js:252-287)
+//   QKV    16-row tiles of blocks.i.attn.qkv holding RoPE partner rows d, d+32
+//          prologue: embed (layer 0) or x = xb + sum of the previous layer's
+//          down-projection partials; RMSNorm/LayerNorm in LDS
+//          epilogue: bias (gpt2), RoPE (llama), q -> scratch, k/v -> KV cache
+//   ATTN   one workgroup per (token, 256-position split, head): scores,
+//          split-local softmax statistics and P.V.  The last split of a
+//          (token, head) to finish (the only one below 256 positions) merges
+//          the splits and multiplies the head's attention output by its
+//          64-column slice of attn.proj: a per-head partial of W_o . att.
+//   MLP    one workgroup per 64 hidden units: x = xa + sum of the per-head
+//          partials (+ proj bias), norm2, gate and up rows of its units ->
+//          silu(g)*u (gpt2: fc + bias -> GELU-tanh), then those units'
+//          64-column slice of the down projection: a per-chunk partial of
+//          W_2 . h
+//   FINAL  per token: x = xb + the down partials (+ bias), final norm
+//   LM     grid-stride row tiles of the tied lm_head with the next tile's
+//          weights in flight; logits + per-tile argmax (gpt2 chain: 3-gram
+//          block and repetition penalty of infer.js:252-287)
 //   ARGMAX one workgroup: first maximum over tiles; chained decode feeds it
-//         back as the next input token (CHAIN_TOK, webgpu-metal.js:609-610).
-// Every GEMV phase issues its weight loads before it stages the activations,
-// so the two memory latencies overlap.
+//          back as the next input token (CHAIN_TOK, webgpu-metal.js:609-610).
+// The split-K partials are summed by their consumer in a fixed order, so
+// every result is deterministic.  Every GEMV issues its weight loads before
+// it stages its activations, so the two memory latencies overlap.
 //
 // Execution: mode 1 (default) replays a HIP graph of one kernel per phase;
-// mode 2 launches the same kernels directly; mode 0 runs all phases in one
-// persistent cooperative kernel with a grid barrier between phases.  All
-// modes run the same per-item device code.
+// mode 2 launches the same kernels directly.  Both run the same kernels.  (A
+// persistent kernel with grid barriers between phases measured slower than
+// graph replay here: one barrier over 256 workgroups cost ~17 us against
+// ~1.6 us per graph node.)
 //
-// Every per-token computation (norm, GEMV row, attention split, combine,
-// argmax) runs the same instruction sequence whatever the number of tokens in
-// the pass, so a row of the multi-token verify pass is bit-identical to the
-// single-token decode of that position.
+// Every per-token computation (norm, GEMV row, attention split, merge, the
+// partial sums, argmax) runs the same instruction sequence whatever the
+// number of tokens in the pass, so a row of the multi-token verify pass is
+// bit-identical to the single-token decode of that position.
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -45,27 +54,28 @@
 
 namespace mllm {
 
-constexpr int HD = 64;    // head dimension of every supported config
-constexpr int ACH = 256;  // positions per attention split (one per thread)
-constexpr int MAXT = 16;  // tokens per pass (upper bound; LDS sets the real one)
-constexpr int APS = 68;   // floats per attention partial: m, l, pad, pad, acc[64]
-constexpr int TC = 2;     // tile capacity of the decode phases: TC * WG chunks
-#ifndef MLLM_TILE_TARGET
-#define MLLM_TILE_TARGET 320
-#endif
 #ifndef MLLM_LM_TILES_PER_WG
 #define MLLM_LM_TILES_PER_WG 1
 #endif
-constexpr int TILE_TARGET = MLLM_TILE_TARGET;  // chunks per GEMV tile (~0.15 us of VALU on one CU)
-constexpr int QSPLIT = 4;         // QKV tiles per head
-constexpr unsigned kSpinLimit = 1u << 22;
 
-enum Phase { PH_QKV = 0, PH_ATTN, PH_O, PH_UP, PH_DOWN, PH_LM, PH_ARGMAX, PH_COUNT };
+constexpr int HD = 64;     // head dimension of every supported config
+constexpr int ACH = 256;   // positions per attention split (one per thread)
+constexpr int MAXT = 16;   // tokens per pass (upper bound; LDS sets the real one)
+constexpr int APS = 68;    // floats per attention partial: m, l, pad, pad, acc[64]
+constexpr int TC = 2;      // chunk registers per thread of a QKV / LM tile (TC * WG chunks)
+constexpr int TILE_TARGET = 320;  // chunks per LM tile (~0.15 us of VALU on one CU)
+constexpr int QSPLIT = 4;  // QKV tiles per head
+constexpr int UNITS = 64;  // hidden units per MLP item (two 32-column groups of mlp.w2)
+constexpr int SC = 8;      // chunk registers per thread of the MLP tiles and column slices
+constexpr int PB = 8;      // partials per block of the fixed-order partial sums
+
+enum Phase { PH_QKV = 0, PH_ATTN, PH_MLP, PH_FINAL, PH_LM, PH_ARGMAX, PH_COUNT };
 
 struct LayerW {
   Q4Mat qkv, proj, w1, w3, w2;  // gpt2: w1 = mlp.fc, w2 = mlp.proj
   const float *n1, *n2;         // RMS gains; gpt2: LayerNorm gamma || beta
   const float *qkv_b, *proj_b, *fc_b, *mproj_b;
+  const float *prev_mproj_b;    // gpt2: the previous layer's mlp.proj bias
 };
 
 // Device-resident description of the current pass; every phase reads it.
@@ -77,39 +87,41 @@ struct PassState {
   int eos;       // chain stop id (-1: none)
   int done;      // chain reached eos
   int n_hist;    // tokens in hist[] (gpt2 argmax history / chain output)
-  int err;       // barrier / flag-wait time-out
+  int err;       // device-side error flag (reported by the next host check)
   int bad_tok;   // ARGMAX found no finite maximum (chain fed token 0 instead)
-  int epoch;     // mode 3: epoch of the launch's first step
   int tok[MAXT];
   int res[MAXT];  // argmax per lm row
 };
 
 struct DecParams {
-  int arch, L, D, NH, NKV, FF, V, max_seq, kv_fp16, nsplit_max;
+  int arch, L, D, NH, NKV, FF, V, max_seq, kv_fp16, nsplit_max, nchunk;
   float eps, attn_scale;
   const LayerW *layers;
   Q4Mat lm;
   const float *norm_f, *wpe, *sf, *rope_cos, *rope_sin;
-  float *x;     // [MAXT][D] residual stream
-  float *q;     // [MAXT][NH*HD] queries after RoPE
-  void *kv;     // [L][2][NKV][max_seq][HD] (f32 or f16)
-  float *attp;  // [MAXT][NH][nsplit_max][APS]
-  float *ff;    // [MAXT][FF]
+  const float *last_mproj_b;  // gpt2: mlp.proj bias of the last layer
+  float *xa;      // [MAXT][D] residual entering the attention block
+  float *xb;      // [MAXT][D] residual entering the MLP block
+  float *opart;   // [MAXT][NH][D] per-head partials of W_o . att
+  float *dpart;   // [MAXT][nchunk][D] per-chunk partials of W_2 . h
+  float *xn;      // [MAXT][D] final-normed rows for the lm_head
+  float *q;       // [MAXT][NH*HD] queries after RoPE
+  void *kv;       // [L][2][NKV][max_seq][HD] (f32 or f16)
+  float *attp;    // [MAXT][NH][nsplit_max][APS]
+  unsigned *cnt;  // [MAXT][NH] finished splits of the current layer
   float *logits;  // [MAXT][V]
   float *amv;     // [MAXT][lm_tiles]
   int *ami;
-  int o_rpt, up_rpt, dn_rpt, lm_rpt, lm_tiles, lm_grid;
+  int lm_rpt, lm_tiles, lm_grid;
   PassState *st;
   int *hist;      // [max_seq + 1]
-  unsigned *bar;  // grid barrier: count, generation
-  // mode 3 item flags: per layer [qkv | attn | o | up | down], then lm[grid], argmax
-  int *flags;
-  int fl_stride, fl_qkv, fl_attn, fl_o, fl_up, fl_down, fl_lm, fl_argmax;
-  int n_o, n_up, n_down;
 };
 
 // ---------------------------------------------------------------- helpers
 __device__ __forceinline__ int skew(int i) { return (i >> 5) * XS + (i & 31); }
+
+// LDS regions read or written as float4 start on a 16-byte boundary.
+__host__ __device__ __forceinline__ size_t al4(size_t n) { return (n + 3) & ~(size_t)3; }
 
 __device__ __forceinline__ size_t kv_index(const DecParams &P, int li, int which, int h, int pos) {
   return ((((size_t)li * 2 + which) * P.NKV + h) * P.max_seq + pos) * HD;
@@ -126,6 +138,8 @@ __device__ __forceinline__ Gains load_gains(const DecParams &P, const float *w) 
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int i = threadIdx.x + k * WG;
+    G.g[k] = 0.f;
+    G.b[k] = 0.f;
     if (i < P.D) {
       G.g[k] = w[i];
       G.b[k] = P.arch == 1 ? w[P.D + i] : 0.f;
@@ -187,89 +201,205 @@ __device__ void norm_staged(const DecParams &P, float *xs, int m, const Gains &G
   __syncthreads();
 }
 
-// Stage the residual stream rows [t0, t0+m) of P.x, normalise them with
-// the prefetched gains, and form the group sums.
-__device__ __forceinline__ void stage_normed(const DecParams &P, int t0, int m, const Gains &G, float *xs,
-                                             float *xsum, float *red) {
-  const int D = P.D, ng = D >> 5;
-  stage_rows(P.x + (size_t)t0 * D, D, m, D, xs);
-  __syncthreads();
-  norm_staged(P, xs, m, G, red);
-  stage_group_sums(xs, xsum, m, ng);
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
-// LDS carve-up shared by the GEMV phases (floats):
-// red[16] | xs[m][ng][XS] | xsum[m][ng] | part[m][TC*WG] | out[...]
-struct Lds {
-  float *red, *xs, *xsum, *part, *out;
+// Residual rows t = t0 .. t0+m-1:
+//   x[t] = base[t] + (((B_0 + B_1) + ... + B_{nb-1}) + bias)
+// where B_b sums parts[t][p] for p in [b*PB, min(np, (b+1)*PB)) in ascending
+// p (from +0).  The rows go to the skewed LDS layout xs[t - t0] and, when
+// `out` is set, to out[t].  The order of every addition is fixed by np alone.
+// Each thread loads two (block, float4-column) items per round before adding,
+// so a round costs one memory latency.  blk needs nb * D floats of LDS.
+// The first round of token t0 is loaded by resid_prefetch, which a phase
+// calls before it issues its weight loads: loads retire in issue order, so
+// activations issued first can be consumed while the weights still stream.
+struct ResidPre {
+  float4 v[2][PB];
+  float4 xb, bb;
 };
 
-__device__ __forceinline__ Lds carve(float *smem, int m, int ng) {
-  Lds s;
-  s.red = smem;
-  s.xs = smem + 16;
-  s.xsum = s.xs + m * ng * XS;
-  s.part = s.xsum + m * ng;
-  s.out = s.part + m * TC * WG;
-  return s;
-}
-
-// ---------------------------------------------------------------- dataflow
-// Mode 3 orders work items with per-item completion flags instead of kernel
-// boundaries or grid barriers.  An item's flag holds the epoch (step number)
-// it last completed; a consumer waits until every producer flag it depends on
-// (up to three contiguous ranges) has reached the current epoch.  Wave 0
-// polls with agent-scope loads and takes an acquire fence; the producer
-// publishes with an agent-scope release store after a workgroup barrier.
-// Waits are bounded: on time-out st->err is set and every later wait of the
-// launch returns at once, so the grid always drains.
-struct Dep {
-  const int *f[3];
-  int n[3];
-  int ep;
-};
-
-__device__ __forceinline__ void dep_wait(const DecParams &P, const Dep &d) {
-  if (d.n[0] + d.n[1] + d.n[2] == 0) return;
-  if (threadIdx.x < 64) {
-    unsigned spins = 0;
-    for (;;) {
-      bool ok = true;
+__device__ __forceinline__ void resid_load(const float4 *pt, int nq, int np, int nitems, int i0, float4 (&v)[2][PB]) {
+  const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int r = 0; r < 3; ++r)
-        for (int k = threadIdx.x; k < d.n[r]; k += 64)
-          ok &= __hip_atomic_load(d.f[r] + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= d.ep;
-      if (__all(ok)) break;
-      if (++spins > kSpinLimit || __hip_atomic_load(&P.st->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-        if (threadIdx.x == 0) __hip_atomic_store(&P.st->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
+  for (int u = 0; u < 2; ++u) {
+    const int it = i0 + u * WG;
+    const int b = it / nq, c = it - b * nq;
+#pragma unroll
+    for (int k = 0; k < PB; ++k) {
+      const int p = b * PB + k;
+      v[u][k] = zero;
+      if (it < nitems && p < np) v[u][k] = pt[(size_t)p * nq + c];
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+}
+
+__device__ __forceinline__ void resid_add(int nq, int np, int nitems, int i0, const float4 (&v)[2][PB], float *blk) {
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int it = i0 + u * WG;
+    if (it < nitems) {
+      const int b = it / nq;
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int k = 0; k < PB; ++k)
+        if (b * PB + k < np) a = add4(a, v[u][k]);
+      reinterpret_cast<float4 *>(blk)[it] = a;
+    }
+  }
+}
+
+__device__ __forceinline__ void resid_prefetch(const float *base, const float *parts, int np, const float *bias, int t0,
+                                               int D, ResidPre &R) {
+  const int nq = D >> 2, nb = (np + PB - 1) / PB;
+  const int q = threadIdx.x;  // D <= 1024: one float4 column per thread
+  R.xb = make_float4(0.f, 0.f, 0.f, 0.f);
+  R.bb = R.xb;
+  if (q < nq) {
+    R.xb = reinterpret_cast<const float4 *>(base + (size_t)t0 * D)[q];
+    if (bias) R.bb = reinterpret_cast<const float4 *>(bias)[q];
+  }
+  resid_load(reinterpret_cast<const float4 *>(parts + (size_t)t0 * np * D), nq, np, nq * nb, threadIdx.x, R.v);
+}
+
+// Block sums of row t (all rounds but the prefetched one when `first` is
+// set), then the row itself: xs[tt] and out[t].
+__device__ __forceinline__ void resid_row(const float *parts, int np, int t, int tt, int D, float4 xb, float4 bb,
+                                          bool has_bias, bool skip_first, float *xs, float *out, float *blk) {
+  const int nq = D >> 2, ng = D >> 5, nb = (np + PB - 1) / PB, nitems = nq * nb;
+  const float4 *pt = reinterpret_cast<const float4 *>(parts + (size_t)t * np * D);
+  for (int i0 = threadIdx.x + (skip_first ? 2 * WG : 0); i0 < nitems; i0 += 2 * WG) {
+    float4 v[2][PB];
+    resid_load(pt, nq, np, nitems, i0, v);
+    resid_add(nq, np, nitems, i0, v, blk);
+  }
+  __syncthreads();
+  const int q = threadIdx.x;
+  if (q < nq) {
+    const float4 *b4 = reinterpret_cast<const float4 *>(blk);
+    float4 s = b4[q];
+    for (int b = 1; b < nb; ++b) s = add4(s, b4[b * nq + q]);
+    if (has_bias) s = add4(s, bb);
+    const float4 v = add4(xb, s);
+    const int i = 4 * q;
+    *reinterpret_cast<float4 *>(xs + (tt * ng + (i >> 5)) * XS + (i & 31)) = v;
+    if (out) reinterpret_cast<float4 *>(out + (size_t)t * D)[q] = v;
   }
   __syncthreads();
 }
 
-__device__ __forceinline__ void dep_signal(int *flag, int ep) {
+__device__ void stage_residual(const float *base, const float *parts, int np, const float *bias, int t0, int m,
+                               int D, float *xs, float *out, float *blk, const ResidPre &R) {
+  const int nq = D >> 2, nb = (np + PB - 1) / PB;
+  const float4 bb = R.bb;
+  // token t0: its first round is in R
+  resid_add(nq, np, nq * nb, threadIdx.x, R.v, blk);
+  resid_row(parts, np, t0, 0, D, R.xb, bb, bias != nullptr, true, xs, out, blk);
+  for (int tt = 1; tt < m; ++tt) {
+    const int t = t0 + tt;
+    float4 xb = make_float4(0.f, 0.f, 0.f, 0.f);
+    if ((int)threadIdx.x < nq) xb = reinterpret_cast<const float4 *>(base + (size_t)t * D)[threadIdx.x];
+    resid_row(parts, np, t, tt, D, xb, bb, bias != nullptr, false, xs, out, blk);
+  }
+}
+
+// One token's GEMV over a row tile held in registers (chunk c = tid + k*WG
+// of rows ng groups wide, c < nch): out[r] for r < nch / ng, with the
+// arithmetic of tile_compute (bit-identical rows).
+template <int C>
+__device__ __forceinline__ void gemv_tok(const TileRegs<C> &R, int nch, int ng, const float *xs, const float *xsum,
+                                         float *part, float *out) {
+  int g = threadIdx.x % ng;
+  const int gstep = WG % ng;
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    const int c = threadIdx.x + k * WG;
+    if (c < nch) part[c] = (q4_chunk_dot(R.w[k], xs + g * XS) - 8.f * xsum[g]) * R.s[k];
+    g += gstep;
+    if (g >= ng) g -= ng;
+  }
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_store(flag, ep, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  for (int r = threadIdx.x; r < nch / ng; r += WG) out[r] = row_sum(part + r * ng, ng);
+  __syncthreads();
+}
+
+// A two-group column slice of a matrix with ng groups per row: chunk
+// c = 2r + j (r < rows, j < 2) is row r, group g0 + j.
+template <int C>
+__device__ __forceinline__ void slice_load(const Q4Mat &W, int g0, int rows, TileRegs<C> &R) {
+  const int ng = W.cols >> 5;
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    const int c = threadIdx.x + k * WG;
+    if (c < 2 * rows) {
+      const size_t gc = (size_t)(c >> 1) * ng + g0 + (c & 1);
+      R.w[k] = W.q[gc];
+      R.s[k] = W.s[gc];
+    }
+  }
+}
+
+// The slice against two staged groups v (skewed, 2 x XS) with sums vsum[2]:
+// out[r] = part(group g0) + part(group g0 + 1), the row_sum order of two
+// groups.  Neighbouring lanes hold the pair; every lane takes part in the
+// shuffle.
+template <int C>
+__device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const float *v, const float *vsum,
+                                           float *out) {
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    const int c = threadIdx.x + k * WG;
+    const int j = c & 1;
+    float p = 0.f;
+    if (c < 2 * rows) p = (q4_chunk_dot(R.w[k], v + j * XS) - 8.f * vsum[j]) * R.s[k];
+    const float sum = p + lane_xor1(p);
+    if (c < 2 * rows && j == 0) out[c >> 1] = sum;
+  }
 }
 
 // ---------------------------------------------------------------- phases
-__device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, int item, const Dep &dep,
-                          float *smem) {
+__device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, int item, bool done, float *smem) {
   const int D = P.D, ng = D >> 5;
   const int head = item / QSPLIT, quarter = item - head * QSPLIT;
   const int ra = head * HD + quarter * 8, rb = ra + 32;  // RoPE partners d and d + 32
   const int nch = 16 * ng;
+  const PassState &S = *P.st;
+  const int pos0 = S.pos0;
+  // activations first (the embedding row, or the residual and the previous
+  // layer's partials), then the weight tile
+  const bool gpt2 = P.arch == 1;
+  int bv[4] = {0, 0, 0, 0};
+  float sv[4] = {0.f, 0.f, 0.f, 0.f}, sfv[4] = {1.f, 1.f, 1.f, 1.f}, pv4[4] = {0.f, 0.f, 0.f, 0.f};
+  ResidPre RP;
+  if (li == 0) {
+    // embed (infer.js:360-420): dequantised tied lm_head row; gpt2 divides by
+    // scale_factors and adds the learned position.  Loads of token 0 here.
+    const int tok = min(max(S.tok[0], 0), P.V - 1);  // host and ARGMAX keep it in range
+    const uint8_t *row = reinterpret_cast<const uint8_t *>(P.lm.q) + (size_t)tok * (D >> 1);
+    const float *sc = P.lm.s + (size_t)tok * ng;
+    const int pos = min(pos0, P.max_seq - 1);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {  // D <= 1024: at most 4 elements per thread
+      const int i = threadIdx.x + k * WG;
+      if (i < D) {
+        bv[k] = row[i >> 1];
+        sv[k] = sc[i >> 5];
+        if (gpt2) {
+          sfv[k] = P.sf ? P.sf[i] : 1.f;
+          pv4[k] = P.wpe[(size_t)pos * D + i];
+        }
+      }
+    }
+  } else {
+    resid_prefetch(P.xb, P.dpart, P.nchunk, gpt2 ? Lw.prev_mproj_b : nullptr, 0, D, RP);
+  }
   TileRegs<TC> R;
   tile_load<TC>(Lw.qkv, ra, 8, rb, ng, nch, R);
   const Gains G = load_gains(P, Lw.n1);
-  dep_wait(P, dep);
-  Lds s = carve(smem, m, ng);
-  const PassState &S = *P.st;
-  const int pos0 = S.pos0;
+  if (done) return;  // a chained decode that reached eos: loads only, no stores
+  float *red = smem, *xs = red + 16, *xsum = xs + m * ng * XS, *part = xsum + m * ng, *out = part + m * nch;
+  float *blk = smem + al4(16 + (size_t)m * ng * XS + m * ng + m * nch + m * 16);
   // this thread's epilogue element (m * 16 <= WG): its RoPE table entries or
   // bias, fetched before the staging so the epilogue does not wait for them
   const bool is_q = head < P.NH, is_k = !is_q && head < P.NH + P.NKV;
@@ -277,7 +407,7 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
   const int d_own = quarter * 8 + (r_own & 7) + (r_own >> 3) * 32;
   float c_own = 0.f, s_own = 0.f, b_own = 0.f;
   if (e_own < m * 16) {
-    if (P.arch == 1) {
+    if (gpt2) {
       b_own = Lw.qkv_b[head * HD + d_own];
     } else if (is_q || is_k) {
       const size_t ri = (size_t)(pos0 + t_own) * HD + d_own;
@@ -286,25 +416,24 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
     }
   }
   if (li == 0) {
-    // embed (infer.js:360-420): dequantised tied lm_head row; gpt2 divides by
-    // scale_factors and adds the learned position.  Item 0 writes the residual.
+    // item 0 writes xa
     for (int t = 0; t < m; ++t) {
-      float *xt = s.xs + t * ng * XS;
-      const int tok = min(max(S.tok[t], 0), P.V - 1);  // host and ARGMAX keep it in range
-      const uint8_t *row = reinterpret_cast<const uint8_t *>(P.lm.q) + (size_t)tok * (D >> 1);
-      const float *sc = P.lm.s + (size_t)tok * ng;
-      const int pos = min(pos0 + t, P.max_seq - 1);
-      int bv[4];
-      float sv[4], sfv[4], pv4[4];
+      float *xt = xs + t * ng * XS;
+      if (t > 0) {
+        const int tok = min(max(S.tok[t], 0), P.V - 1);
+        const uint8_t *row = reinterpret_cast<const uint8_t *>(P.lm.q) + (size_t)tok * (D >> 1);
+        const float *sc = P.lm.s + (size_t)tok * ng;
+        const int pos = min(pos0 + t, P.max_seq - 1);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {  // D <= 1024: at most 4 elements per thread, loads first
-        const int i = threadIdx.x + k * WG;
-        if (i < D) {
-          bv[k] = row[i >> 1];
-          sv[k] = sc[i >> 5];
-          if (P.arch == 1) {
-            sfv[k] = P.sf ? P.sf[i] : 1.f;
-            pv4[k] = P.wpe[(size_t)pos * D + i];
+        for (int k = 0; k < 4; ++k) {
+          const int i = threadIdx.x + k * WG;
+          if (i < D) {
+            bv[k] = row[i >> 1];
+            sv[k] = sc[i >> 5];
+            if (gpt2) {
+              sfv[k] = P.sf ? P.sf[i] : 1.f;
+              pv4[k] = P.wpe[(size_t)pos * D + i];
+            }
           }
         }
       }
@@ -313,32 +442,33 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
         const int i = threadIdx.x + k * WG;
         if (i < D) {
           float v = (float)(((i & 1) ? (bv[k] >> 4) : (bv[k] & 15)) - 8) * sv[k];
-          if (P.arch == 1) {
+          if (gpt2) {
             if (P.sf) v = v / sfv[k];
             v = v + pv4[k];
           }
           xt[skew(i)] = v;
-          if (item == 0) P.x[(size_t)t * D + i] = v;
+          if (item == 0) P.xa[(size_t)t * D + i] = v;
         }
       }
     }
     __syncthreads();
-    norm_staged(P, s.xs, m, G, s.red);
-    stage_group_sums(s.xs, s.xsum, m, ng);
   } else {
-    stage_normed(P, 0, m, G, s.xs, s.xsum, s.red);
+    stage_residual(P.xb, P.dpart, P.nchunk, gpt2 ? Lw.prev_mproj_b : nullptr, 0, m, D, xs,
+                   item == 0 ? P.xa : nullptr, blk, RP);
   }
-  tile_compute<TC>(R, 16, ng, nch, m, s.xs, s.xsum, threadIdx.x % ng, WG % ng, s.part, s.out, 16);
+  norm_staged(P, xs, m, G, red);
+  stage_group_sums(xs, xsum, m, ng);
+  tile_compute<TC>(R, 16, ng, nch, m, xs, xsum, threadIdx.x % ng, WG % ng, part, out, 16);
   // epilogue: tile row r < 8 is head dim d = quarter*8 + r, r >= 8 is d + 32
   const int kvh = is_q ? 0 : (is_k ? head - P.NH : head - P.NH - P.NKV);
   if (e_own < m * 16) {
     const int e = e_own, t = t_own, r = r_own, d = d_own;
-    float v = s.out[e];
+    float v = out[e];
     const int pos = pos0 + t;
     if (P.arch == 1) {
       v = v + b_own;
     } else if (is_q || is_k) {
-      const float mate = r < 8 ? -s.out[e + 8] : s.out[e - 8];
+      const float mate = r < 8 ? -out[e + 8] : out[e - 8];
       v = __builtin_fmaf(v, c_own, mate * s_own);
     }
     if (is_q) {
@@ -353,25 +483,35 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
   }
 }
 
-// One (token, split, head) item.  After pos arrives, every load of the item
-// (q, the K rows, the V rows) is issued at once: thread i owns key i of the
-// split; thread (kg, d4) owns V[kg + 16j][4*d4 .. 4*d4+3] for j < 16.
-__device__ void phase_attn(const DecParams &P, int m, int li, int item, const Dep &dep, float *smem) {
-  dep_wait(P, dep);
+// One (token, split, head) item.  Every load of the item (q, the K rows, the
+// V rows) is issued at once: thread i owns key i of the split; thread
+// (kg, d4) owns V[kg + 16j][4*d4 .. 4*d4+3] for j < 16.  The last split of
+// (token, head) to finish -- counted in P.cnt; a single split is its own
+// last -- merges the splits (flash-decoding merge in split order) and writes
+// the head's partial of the attention output projection to P.opart.
+__device__ void phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, int item, bool done, float *smem) {
   const int per_tok = P.NH * P.nsplit_max;
   const int t = item / per_tok;
   const int rem = item - t * per_tok;
   const int sp = rem / P.NH, h = rem - sp * P.NH;
-  if (t >= m) return;
+  if (t >= m || done) return;
   const int pos = P.st->pos0 + t;
   const int s0 = sp * ACH;
   if (s0 > pos) return;
+  const int ns = pos / ACH + 1;
+  const bool solo = ns == 1;
+  const int D = P.D;
+  TileRegs<SC> Ro;
   const int cnt = min(ACH, pos + 1 - s0);
   const int kvh = h / (P.NH / P.NKV);
-  float *qs = smem;        // 64
-  float *es = qs + HD;     // 256
-  float *pv = es + ACH;    // 16 x 64
-  float *red = pv + 16 * HD;
+  float *qs = smem;          // 64
+  float *es = qs + HD;       // 256
+  float *pv = es + ACH;      // 16 x 64
+  float *red = pv + 16 * HD; // 16
+  float *own = red + 16;     // 64: this split's P.V
+  float *att = own + HD;     // 2 x XS: merged head output, skewed
+  float *asum = att + 2 * XS;  // 2
+  int *flag = reinterpret_cast<int *>(asum + 2);
   const size_t kbase = kv_index(P, li, 0, kvh, s0), vbase = kv_index(P, li, 1, kvh, s0);
   const int i = threadIdx.x;
   const int d4 = threadIdx.x & 15, kg = threadIdx.x >> 4;
@@ -415,6 +555,7 @@ __device__ void phase_attn(const DecParams &P, int m, int li, int item, const De
       if (k < cnt) vr[j] = *reinterpret_cast<const float4 *>(kv32 + vbase + (size_t)k * HD + 4 * d4);
     }
   }
+  if (solo) slice_load<SC>(Lw.proj, 2 * h, D, Ro);  // W_o columns of this head, behind the K/V loads
   __syncthreads();
   float score = -INFINITY;
   if (i < cnt) {
@@ -445,135 +586,138 @@ __device__ void phase_attn(const DecParams &P, int m, int li, int item, const De
   }
   *reinterpret_cast<float4 *>(pv + kg * HD + 4 * d4) = acc;
   __syncthreads();
-  float *dst = P.attp + ((size_t)(t * P.NH + h) * P.nsplit_max + sp) * APS;
   if (threadIdx.x < HD) {
     float a = 0.f;
     for (int g = 0; g < 16; ++g) a += pv[g * HD + threadIdx.x];
-    dst[4 + threadIdx.x] = a;
+    own[threadIdx.x] = a;
   }
-  if (threadIdx.x == 0) {
-    dst[0] = mx;
-    dst[1] = l;
-  }
-}
-
-__device__ void phase_o(const DecParams &P, const LayerW &Lw, int m, int item, const Dep &dep, float *smem) {
-  const int D = P.D, ng = D >> 5;
-  const int row0 = item * P.o_rpt;
-  const int nr = min(P.o_rpt, D - row0);
-  TileRegs<TC> R;
-  tile_load<TC>(Lw.proj, row0, nr, 0, ng, nr * ng, R);
-  dep_wait(P, dep);
-  const int pos0 = P.st->pos0;
-  // the residual this thread will update, fetched with the weights
-  const int e0 = threadIdx.x;
-  const bool own = e0 < m * nr;
-  const int et = own ? e0 / nr : 0, er = own ? e0 - et * nr : 0;
-  const float xres = own ? P.x[(size_t)et * D + row0 + er] : 0.f;
-  const float bres = own && P.arch == 1 ? Lw.proj_b[row0 + er] : 0.f;
-  Lds s = carve(smem, m, ng);
-  // combine the attention splits (flash-decoding merge, splits in order);
-  // split 0's values for this thread's (up to 4) elements are loaded first
-  for (int t = 0; t < m; ++t) {
-    const int ns = (pos0 + t) / ACH + 1;
-    float m0[4], l0[4], a0[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {  // D <= 1024
-      const int e = threadIdx.x + k * WG;
-      if (e < D) {
-        const float *p = P.attp + (size_t)(t * P.NH + (e >> 6)) * P.nsplit_max * APS;
-        m0[k] = p[0];
-        l0[k] = p[1];
-        a0[k] = p[4 + (e & 63)];
-      }
+  const float *parts = P.attp + (size_t)(t * P.NH + h) * P.nsplit_max * APS;
+  if (!solo) {
+    // publish this split, then count it; the last one merges
+    float *dst = P.attp + ((size_t)(t * P.NH + h) * P.nsplit_max + sp) * APS;
+    __syncthreads();
+    if (threadIdx.x < HD) dst[4 + threadIdx.x] = own[threadIdx.x];
+    if (threadIdx.x == 0) {
+      dst[0] = mx;
+      dst[1] = l;
     }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int e = threadIdx.x + k * WG;
-      if (e < D) {
-        const int h = e >> 6, d = e & 63;
-        const float *p = P.attp + (size_t)(t * P.NH + h) * P.nsplit_max * APS;
-        float M = m0[k];
-        for (int j = 1; j < ns; ++j) M = fmaxf(M, p[j * APS]);
-        const float w0 = expf(m0[k] - M);
-        float l = __builtin_fmaf(l0[k], w0, 0.f), a = __builtin_fmaf(a0[k], w0, 0.f);
-        for (int j = 1; j < ns; ++j) {
-          const float w = expf(p[j * APS] - M);
-          l = __builtin_fmaf(p[j * APS + 1], w, l);
-          a = __builtin_fmaf(p[j * APS + 4 + d], w, a);
-        }
-        s.xs[t * ng * XS + skew(e)] = a / l;
-      }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned *c = P.cnt + t * P.NH + h;
+      const unsigned done = atomicAdd(c, 1u);
+      flag[0] = done == (unsigned)(ns - 1);
+      if (flag[0]) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    __syncthreads();
+    if (!flag[0]) return;
+    __threadfence();
+    slice_load<SC>(Lw.proj, 2 * h, D, Ro);
   }
   __syncthreads();
-  stage_group_sums(s.xs, s.xsum, m, ng);
-  tile_compute<TC>(R, nr, ng, nr * ng, m, s.xs, s.xsum, threadIdx.x % ng, WG % ng, s.part, s.out, P.o_rpt);
-  for (int e = threadIdx.x; e < m * nr; e += WG) {
-    const int t = e / nr, r = e - t * nr;
-    float y = s.out[t * P.o_rpt + r];
-    if (P.arch == 1) y = y + (e == e0 ? bres : Lw.proj_b[row0 + r]);
-    const float x = e == e0 ? xres : P.x[(size_t)t * D + row0 + r];
-    P.x[(size_t)t * D + row0 + r] = x + y;
-  }
-}
-
-__device__ void phase_up(const DecParams &P, const LayerW &Lw, int m, int item, const Dep &dep, float *smem) {
-  const int D = P.D, ng = D >> 5;
-  const int row0 = item * P.up_rpt;
-  const int nr = min(P.up_rpt, P.FF - row0);
-  const bool gpt2 = P.arch == 1;
-  TileRegs<TC> Rg, Ru;
-  tile_load<TC>(Lw.w1, row0, nr, 0, ng, nr * ng, Rg);
-  if (!gpt2) tile_load<TC>(Lw.w3, row0, nr, 0, ng, nr * ng, Ru);
-  const Gains G = load_gains(P, Lw.n2);
-  const bool own = (int)threadIdx.x < m * nr;
-  const float fcb = gpt2 && own ? Lw.fc_b[row0 + threadIdx.x % nr] : 0.f;
-  dep_wait(P, dep);
-  Lds s = carve(smem, m, ng);
-  stage_normed(P, 0, m, G, s.xs, s.xsum, s.red);
-  const int gf = threadIdx.x % ng, gs = WG % ng;
-  float *og = s.out, *ou = s.out + m * P.up_rpt;
-  tile_compute<TC>(Rg, nr, ng, nr * ng, m, s.xs, s.xsum, gf, gs, s.part, og, P.up_rpt);
-  if (gpt2) {
-    for (int e = threadIdx.x; e < m * nr; e += WG) {
-      const int t = e / nr, r = e - t * nr;
-      const float v = og[t * P.up_rpt + r] + (e == (int)threadIdx.x ? fcb : Lw.fc_b[row0 + r]);
-      P.ff[(size_t)t * P.FF + row0 + r] =
-          0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+  if (threadIdx.x < HD) {
+    const int d = threadIdx.x;
+    float v;
+    if (solo) {
+      v = own[d] / l;  // the merge below with one split: weight expf(0) = 1
+    } else {
+      float M = sp == 0 ? mx : parts[0];
+      for (int j = 1; j < ns; ++j) M = fmaxf(M, j == sp ? mx : parts[j * APS]);
+      const float m0 = sp == 0 ? mx : parts[0], l0 = sp == 0 ? l : parts[1], a0 = sp == 0 ? own[d] : parts[4 + d];
+      const float w0 = expf(m0 - M);
+      float ls = __builtin_fmaf(l0, w0, 0.f), as = __builtin_fmaf(a0, w0, 0.f);
+      for (int j = 1; j < ns; ++j) {
+        const float mj = j == sp ? mx : parts[j * APS];
+        const float lj = j == sp ? l : parts[j * APS + 1];
+        const float aj = j == sp ? own[d] : parts[j * APS + 4 + d];
+        const float w = expf(mj - M);
+        ls = __builtin_fmaf(lj, w, ls);
+        as = __builtin_fmaf(aj, w, as);
+      }
+      v = as / ls;
     }
-    return;
+    att[skew(d)] = v;
   }
-  tile_compute<TC>(Ru, nr, ng, nr * ng, m, s.xs, s.xsum, gf, gs, s.part, ou, P.up_rpt);
-  for (int e = threadIdx.x; e < m * nr; e += WG) {
-    const int t = e / nr, r = e - t * nr;
-    const float g = og[t * P.up_rpt + r];
-    P.ff[(size_t)t * P.FF + row0 + r] = (g / (1.0f + expf(-g))) * ou[t * P.up_rpt + r];
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) s += att[threadIdx.x * XS + k];
+    asum[threadIdx.x] = s;
   }
+  __syncthreads();
+  slice_gemv<SC>(Ro, D, att, asum, P.opart + (size_t)(t * P.NH + h) * D);
 }
 
-__device__ void phase_down(const DecParams &P, const LayerW &Lw, int m, int item, const Dep &dep, float *smem) {
-  const int D = P.D, ngf = P.FF >> 5;
-  const int row0 = item * P.dn_rpt;
-  const int nr = min(P.dn_rpt, D - row0);
-  TileRegs<TC> R;
-  tile_load<TC>(Lw.w2, row0, nr, 0, ngf, nr * ngf, R);
-  dep_wait(P, dep);
-  const int e0 = threadIdx.x;
-  const bool own = e0 < m * nr;
-  const int et = own ? e0 / nr : 0, er = own ? e0 - et * nr : 0;
-  const float xres = own ? P.x[(size_t)et * D + row0 + er] : 0.f;
-  const float bres = own && P.arch == 1 ? Lw.mproj_b[row0 + er] : 0.f;
-  Lds s = carve(smem, m, ngf);
-  stage_plain(P.ff, P.FF, m, P.FF, s.xs, s.xsum);
-  tile_compute<TC>(R, nr, ngf, nr * ngf, m, s.xs, s.xsum, threadIdx.x % ngf, WG % ngf, s.part, s.out, P.dn_rpt);
-  for (int e = threadIdx.x; e < m * nr; e += WG) {
-    const int t = e / nr, r = e - t * nr;
-    float y = s.out[t * P.dn_rpt + r];
-    if (P.arch == 1) y = y + (e == e0 ? bres : Lw.mproj_b[row0 + r]);
-    const float x = e == e0 ? xres : P.x[(size_t)t * D + row0 + r];
-    P.x[(size_t)t * D + row0 + r] = x + y;
+// Hidden units [item*UNITS, (item+1)*UNITS): gate/up (or fc) rows, the
+// activation, then the units' two-group slice of the down projection.
+__device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item, bool done, float *smem) {
+  const int D = P.D, ng = D >> 5;
+  const bool gpt2 = P.arch == 1;
+  const int r0 = item * UNITS;
+  const int nch = UNITS * ng;
+  ResidPre RP;
+  resid_prefetch(P.xa, P.opart, P.NH, gpt2 ? Lw.proj_b : nullptr, 0, D, RP);
+  TileRegs<SC> Rg, Ru, Rd;
+  tile_load<SC>(Lw.w1, r0, UNITS, 0, ng, nch, Rg);
+  if (!gpt2) tile_load<SC>(Lw.w3, r0, UNITS, 0, ng, nch, Ru);
+  const Gains G = load_gains(P, Lw.n2);
+  if (done) return;
+  const bool own = (int)threadIdx.x < m * UNITS;
+  const float fcb = gpt2 && own ? Lw.fc_b[r0 + (threadIdx.x & (UNITS - 1))] : 0.f;
+  float *red = smem, *xs = red + 16, *xsum = xs + m * ng * XS, *part = xsum + m * ng, *go = part + nch;
+  float *uo = go + m * UNITS;
+  float *hs = smem + al4(16 + (size_t)m * ng * XS + m * ng + nch + 2 * m * UNITS);
+  float *hsum = hs + m * 2 * XS, *blk = hsum + al4(2 * m);
+  stage_residual(P.xa, P.opart, P.NH, gpt2 ? Lw.proj_b : nullptr, 0, m, D, xs, item == 0 ? P.xb : nullptr, blk, RP);
+  slice_load<SC>(Lw.w2, 2 * item, D, Rd);
+  norm_staged(P, xs, m, G, red);
+  stage_group_sums(xs, xsum, m, ng);
+  for (int t = 0; t < m; ++t) {
+    gemv_tok<SC>(Rg, nch, ng, xs + t * ng * XS, xsum + t * ng, part, go + t * UNITS);
+    if (!gpt2) gemv_tok<SC>(Ru, nch, ng, xs + t * ng * XS, xsum + t * ng, part, uo + t * UNITS);
   }
+  for (int e = threadIdx.x; e < m * UNITS; e += WG) {
+    const int t = e / UNITS, r = e - t * UNITS;
+    const float g = go[e];
+    float h;
+    if (gpt2) {
+      const float v = g + (e == (int)threadIdx.x ? fcb : Lw.fc_b[r0 + r]);
+      h = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+    } else {
+      h = (g / (1.0f + expf(-g))) * uo[e];
+    }
+    hs[t * 2 * XS + skew(r)] = h;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < 2 * m) {
+    const float *p = hs + threadIdx.x * XS;
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) s += p[k];
+    hsum[threadIdx.x] = s;
+  }
+  __syncthreads();
+  for (int t = 0; t < m; ++t)
+    slice_gemv<SC>(Rd, D, hs + t * 2 * XS, hsum + 2 * t, P.dpart + ((size_t)t * P.nchunk + item) * D);
+}
+
+// Item t: the residual after the last layer, final norm -> xn[t] (only the
+// rows the lm_head reads).
+__device__ void phase_final(const DecParams &P, int m, int item, bool done, float *smem) {
+  const PassState &S = *P.st;
+  if (S.lm_rows == 0 || done) return;
+  const int tb = S.lm_rows == 1 ? m - 1 : 0;
+  const int t = item;
+  if (t < tb || t >= m) return;
+  const int D = P.D, ng = D >> 5;
+  ResidPre RP;
+  resid_prefetch(P.xb, P.dpart, P.nchunk, P.arch == 1 ? P.last_mproj_b : nullptr, t, D, RP);
+  const Gains G = load_gains(P, P.norm_f);
+  float *red = smem, *xs = red + 16, *blk = xs + ng * XS;
+  stage_residual(P.xb, P.dpart, P.nchunk, P.arch == 1 ? P.last_mproj_b : nullptr, t, 1, D, xs, nullptr, blk, RP);
+  norm_staged(P, xs, 1, G, red);
+  for (int i = threadIdx.x; i < D; i += WG) P.xn[(size_t)t * D + i] = xs[skew(i)];
 }
 
 // argmaxGpt2 (infer.js:252-287) adjustment of one logit given the banned and
@@ -587,11 +731,16 @@ __device__ __forceinline__ float gpt2_adjust(float v, int i, const int *ban, int
   return v;
 }
 
+struct LmLds {
+  float *xs, *xsum, *part, *out;
+  int *lists;
+};
+
 // One lm_head tile whose weights are in R: logits rows [r0, r0+nr) of the m
 // tokens from tb, then the tile's first maximum per token (gpt2 chain: with
 // the argmaxGpt2 adjustments).
 __device__ __forceinline__ void lm_tile(const DecParams &P, const TileRegs<TC> &R, int tile, int tb, int m,
-                                        const Lds &s, bool penal, const int *lists, int nban, int nrec) {
+                                        const LmLds &s, bool penal, int nban, int nrec) {
   const int ng = P.D >> 5, rpt = P.lm_rpt;
   const int r0 = tile * rpt, nr = min(rpt, P.V - r0);
   tile_compute<TC>(R, nr, ng, nr * ng, m, s.xs, s.xsum, threadIdx.x % ng, WG % ng, s.part, s.out, rpt);
@@ -605,7 +754,7 @@ __device__ __forceinline__ void lm_tile(const DecParams &P, const TileRegs<TC> &
       int bi = 0x7fffffff;
       for (int r = threadIdx.x; r < nr; r += 64) {
         float v = s.out[t * rpt + r];
-        if (penal) v = gpt2_adjust(v, r0 + r, lists + 34, nban, lists + 2, nrec);
+        if (penal) v = gpt2_adjust(v, r0 + r, s.lists + 34, nban, s.lists + 2, nrec);
         if (amax_better(v, r0 + r, bv, bi)) {
           bv = v;
           bi = r0 + r;
@@ -631,52 +780,56 @@ __device__ __forceinline__ void lm_load(const DecParams &P, int tile, TileRegs<T
 // lm_head over row tiles wg, wg + nwg, ...; the next tile's weights are
 // loaded while the current one is computed (two register sets used in
 // turn, each with constant indices so both stay in VGPRs).
-__device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, const Dep &dep, float *smem) {
+__device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, bool done, float *smem) {
+  if (wg >= P.lm_tiles) return;
+  TileRegs<TC> Ra, Rb;
+  int tile = wg;
+  lm_load(P, tile, Ra);  // independent of the pass state: in flight before it arrives
   const PassState &S = *P.st;
   const int lm_rows = S.lm_rows;
-  if (lm_rows == 0 || wg >= P.lm_tiles) return;
+  if (lm_rows == 0 || done) return;
   const int tb = lm_rows == 1 ? m_all - 1 : 0;
   const int m = m_all - tb;
   const int D = P.D, ng = D >> 5, rpt = P.lm_rpt;
-  TileRegs<TC> Ra, Rb;
-  int tile = wg;
-  lm_load(P, tile, Ra);
-  const Gains G = load_gains(P, P.norm_f);
-  dep_wait(P, dep);
-  Lds s = carve(smem, m, ng);
-  int *lists = reinterpret_cast<int *>(s.out + m * rpt);  // [0]: nban, [1]: nrec, [2..34): rec, then ban
+  LmLds s;
+  s.xs = smem;
+  s.xsum = s.xs + m * ng * XS;
+  s.part = s.xsum + m * ng;
+  s.out = s.part + m * TC * WG;
+  s.lists = reinterpret_cast<int *>(s.out + m * rpt);  // [0]: nban, [1]: nrec, [2..34): rec, then ban
   const bool penal = P.arch == 1 && S.chain;
   if (penal && threadIdx.x == 0) {
     // infer.js:252-287 over hist[0..n): banned = tokens that would repeat the
     // last 3-gram, recent = the last 32 tokens.
     const int n = S.n_hist;
     int nrec = 0, nban = 0;
-    for (int h = max(0, n - 32); h < n; ++h) lists[2 + nrec++] = P.hist[h];
+    for (int h = max(0, n - 32); h < n; ++h) s.lists[2 + nrec++] = P.hist[h];
     if (n >= 2) {
       const int t1 = P.hist[n - 2], t2 = P.hist[n - 1];
       for (int h = 0; h < n - 2; ++h)
-        if (P.hist[h] == t1 && P.hist[h + 1] == t2) lists[34 + nban++] = P.hist[h + 2];
+        if (P.hist[h] == t1 && P.hist[h + 1] == t2) s.lists[34 + nban++] = P.hist[h + 2];
     }
-    lists[0] = nban;
-    lists[1] = nrec;
+    s.lists[0] = nban;
+    s.lists[1] = nrec;
   }
-  stage_normed(P, tb, m, G, s.xs, s.xsum, s.red);
-  const int nban = penal ? lists[0] : 0, nrec = penal ? lists[1] : 0;
+  stage_rows(P.xn + (size_t)tb * D, D, m, D, s.xs);
+  __syncthreads();
+  stage_group_sums(s.xs, s.xsum, m, ng);
+  const int nban = penal ? s.lists[0] : 0, nrec = penal ? s.lists[1] : 0;
   while (tile < P.lm_tiles) {
     lm_load(P, tile + nwg, Rb);
-    lm_tile(P, Ra, tile, tb, m, s, penal, lists, nban, nrec);
+    lm_tile(P, Ra, tile, tb, m, s, penal, nban, nrec);
     tile += nwg;
     if (tile >= P.lm_tiles) break;
     lm_load(P, tile + nwg, Ra);
-    lm_tile(P, Rb, tile, tb, m, s, penal, lists, nban, nrec);
+    lm_tile(P, Rb, tile, tb, m, s, penal, nban, nrec);
     tile += nwg;
   }
 }
 
-__device__ void phase_argmax(const DecParams &P, const Dep &dep, float *smem) {
-  dep_wait(P, dep);
+__device__ void phase_argmax(const DecParams &P, bool done, float *smem) {
   PassState &S = *P.st;
-  if (S.lm_rows == 0) return;
+  if (S.lm_rows == 0 || done) return;
   const int tb = S.lm_rows == 1 ? S.ntok - 1 : 0;
   float *rv = smem;
   int *ri = reinterpret_cast<int *>(smem + 4);
@@ -689,6 +842,8 @@ __device__ void phase_argmax(const DecParams &P, const Dep &dep, float *smem) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {  // all loads of the batch before any compare
         const int k = base + threadIdx.x + j * WG;
+        vv[j] = -INFINITY;
+        iv[j] = 0x7fffffff;
         if (k < P.lm_tiles) {
           vv[j] = P.amv[(size_t)t * P.lm_tiles + k];
           iv[j] = P.ami[(size_t)t * P.lm_tiles + k];
@@ -740,26 +895,26 @@ __host__ __device__ __forceinline__ int phase_items(const DecParams &P, int ph, 
   switch (ph) {
   case PH_QKV: return (P.NH + 2 * P.NKV) * QSPLIT;
   case PH_ATTN: return m * P.NH * P.nsplit_max;
-  case PH_O: return (P.D + P.o_rpt - 1) / P.o_rpt;
-  case PH_UP: return (P.FF + P.up_rpt - 1) / P.up_rpt;
-  case PH_DOWN: return (P.D + P.dn_rpt - 1) / P.dn_rpt;
+  case PH_MLP: return P.nchunk;
+  case PH_FINAL: return m;
   case PH_LM: return P.lm_grid;
   default: return 1;
   }
 }
 
+// done: the chained decode already emitted eos.  Each phase still issues
+// its first loads (they do not depend on the pass state, whose load then
+// overlaps them) but stores nothing.
 __device__ __forceinline__ void run_item(const DecParams &P, const LayerW &Lw, int ph, int m, int li, int item,
-                                         int nitems, const Dep &dep, float *smem) {
+                                         int nitems, bool done, float *smem) {
   switch (ph) {
-  case PH_QKV: phase_qkv(P, Lw, m, li, item, dep, smem); break;
-  case PH_ATTN: phase_attn(P, m, li, item, dep, smem); break;
-  case PH_O: phase_o(P, Lw, m, item, dep, smem); break;
-  case PH_UP: phase_up(P, Lw, m, item, dep, smem); break;
-  case PH_DOWN: phase_down(P, Lw, m, item, dep, smem); break;
-  case PH_LM: phase_lm(P, m, item, nitems, dep, smem); break;
-  default: phase_argmax(P, dep, smem); break;
+  case PH_QKV: phase_qkv(P, Lw, m, li, item, done, smem); break;
+  case PH_ATTN: phase_attn(P, Lw, m, li, item, done, smem); break;
+  case PH_MLP: phase_mlp(P, Lw, m, item, done, smem); break;
+  case PH_FINAL: phase_final(P, m, item, done, smem); break;
+  case PH_LM: phase_lm(P, m, item, nitems, done, smem); break;
+  default: phase_argmax(P, done, smem); break;
   }
-  __syncthreads();
 }
 
 // ---------------------------------------------------------------- kernels
@@ -770,158 +925,14 @@ __device__ __forceinline__ void run_item(const DecParams &P, const LayerW &Lw, i
 template <int PH>
 __global__ __launch_bounds__(WG) void k_phase(DecParams P, LayerW Lw, int li, int m) {
   extern __shared__ float4 smem4[];
-  if (P.st->done) return;
-  const Dep none{};
-  run_item(P, Lw, PH, m, li, blockIdx.x, gridDim.x, none, reinterpret_cast<float *>(smem4));
+  const bool done = P.st->done != 0;
+  run_item(P, Lw, PH, m, li, blockIdx.x, gridDim.x, done, reinterpret_cast<float *>(smem4));
 }
 
 using PhaseKernel = void (*)(DecParams, LayerW, int, int);
-static const PhaseKernel kPhaseKernels[PH_COUNT] = {k_phase<PH_QKV>, k_phase<PH_ATTN>, k_phase<PH_O>,
-                                                    k_phase<PH_UP>,  k_phase<PH_DOWN>, k_phase<PH_LM>,
-                                                    k_phase<PH_ARGMAX>};
-
-// Grid barrier for the persistent kernel: arrival counter + generation word
-// at agent scope; the last arriver resets the counter and bumps the
-// generation.  The spin is bounded: on time-out it records st->err and every
-// later barrier of the launch returns at once, so the grid always drains.
-__device__ __forceinline__ void grid_barrier(const DecParams &P, unsigned nblocks, unsigned &gen) {
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    if (__hip_atomic_load(&P.st->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
-      const unsigned old = __hip_atomic_fetch_add(&P.bar[0], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      if (old == nblocks - 1) {
-        __hip_atomic_store(&P.bar[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&P.bar[1], gen + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-      } else {
-        unsigned spins = 0;
-        while (__hip_atomic_load(&P.bar[1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == gen) {
-          if (++spins > kSpinLimit) {
-            __hip_atomic_store(&P.st->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-          }
-          __builtin_amdgcn_s_sleep(1);
-        }
-      }
-    }
-    gen += 1;
-    __atomic_thread_fence(__ATOMIC_ACQUIRE);
-  }
-  __syncthreads();
-}
-
-// Mode 0: every phase of `steps` passes in one cooperative launch.
-__global__ __launch_bounds__(WG) void k_persistent(DecParams P, int steps) {
-  extern __shared__ float4 smem4[];
-  float *smem = reinterpret_cast<float *>(smem4);
-  const unsigned nb = gridDim.x;
-  unsigned gen = __hip_atomic_load(&P.bar[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (int step = 0; step < steps; ++step) {
-    if (__hip_atomic_load(&P.st->done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
-    const int m = P.st->ntok;
-    for (int li = 0; li < P.L; ++li) {
-      const LayerW Lw = P.layers[li];
-      const Dep none{};
-      for (int ph = PH_QKV; ph <= PH_DOWN; ++ph) {
-        const int n = phase_items(P, ph, m);
-        for (int it = blockIdx.x; it < n; it += nb) run_item(P, Lw, ph, m, li, it, n, none, smem);
-        grid_barrier(P, nb, gen);
-      }
-    }
-    if (P.st->lm_rows) {
-      const LayerW none{};
-      const Dep nodep{};
-      run_item(P, none, PH_LM, m, 0, blockIdx.x, nb, nodep, smem);
-      grid_barrier(P, nb, gen);
-      if (blockIdx.x == 0) run_item(P, none, PH_ARGMAX, m, 0, 0, 1, nodep, smem);
-      grid_barrier(P, nb, gen);
-    }
-  }
-}
-
-// Mode 3: every item of `steps` passes in one cooperative launch, ordered by
-// per-item flags.  Item dependencies (producer ranges):
-//   QKV(l)   <- DOWN(l-1), all items       (layer 0: previous step's ARGMAX)
-//   ATTN(l)  <- QKV(l) tiles of the query head, its K head and its V head
-//   O(l)     <- ATTN(l), all items of the pass
-//   UP(l)    <- O(l);  DOWN(l) <- UP(l);  LM <- DOWN(L-1);  ARGMAX <- LM
-// Each workgroup also waits for the previous step's ARGMAX before starting a
-// step, so a chain that hit eos is seen by every workgroup at the same step.
-__global__ __launch_bounds__(WG) void k_dataflow(DecParams P, int steps) {
-  extern __shared__ float4 smem4[];
-  float *smem = reinterpret_cast<float *>(smem4);
-  const int nb = gridDim.x, wg = blockIdx.x;
-  const int base = __hip_atomic_load(&P.st->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  int *const argmax_flag = P.flags + P.fl_argmax;
-  for (int step = 0; step < steps; ++step) {
-    const int ep = base + step;
-    if (step > 0) {
-      const Dep d{{argmax_flag, nullptr, nullptr}, {1, 0, 0}, ep - 1};
-      dep_wait(P, d);
-      if (__hip_atomic_load(&P.st->done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
-    }
-    const int m = P.st->ntok;
-    const int n_attn = m * P.NH * P.nsplit_max;
-    for (int li = 0; li < P.L; ++li) {
-      const LayerW Lw = P.layers[li];
-      int *const fl = P.flags + (size_t)li * P.fl_stride;
-      const int *const prev_down = li > 0 ? fl - P.fl_stride + P.fl_down : nullptr;
-      for (int ph = PH_QKV; ph <= PH_DOWN; ++ph) {
-        const int n = phase_items(P, ph, m);
-        for (int it = wg; it < n; it += nb) {
-          Dep d{{nullptr, nullptr, nullptr}, {0, 0, 0}, ep};
-          int *mine = nullptr;
-          switch (ph) {
-          case PH_QKV:
-            if (li > 0) {
-              d.f[0] = prev_down;
-              d.n[0] = P.n_down;
-            }
-            mine = fl + P.fl_qkv + it;
-            break;
-          case PH_ATTN: {
-            const int h = (it % (P.NH * P.nsplit_max)) % P.NH;
-            const int kvh = h / (P.NH / P.NKV);
-            d.f[0] = fl + P.fl_qkv + h * QSPLIT;
-            d.f[1] = fl + P.fl_qkv + (P.NH + kvh) * QSPLIT;
-            d.f[2] = fl + P.fl_qkv + (P.NH + P.NKV + kvh) * QSPLIT;
-            d.n[0] = d.n[1] = d.n[2] = QSPLIT;
-            mine = fl + P.fl_attn + it;
-            break;
-          }
-          case PH_O:
-            d.f[0] = fl + P.fl_attn;
-            d.n[0] = n_attn;
-            mine = fl + P.fl_o + it;
-            break;
-          case PH_UP:
-            d.f[0] = fl + P.fl_o;
-            d.n[0] = P.n_o;
-            mine = fl + P.fl_up + it;
-            break;
-          default:
-            d.f[0] = fl + P.fl_up;
-            d.n[0] = P.n_up;
-            mine = fl + P.fl_down + it;
-            break;
-          }
-          run_item(P, Lw, ph, m, li, it, n, d, smem);
-          dep_signal(mine, ep);
-        }
-      }
-    }
-    if (P.st->lm_rows) {
-      const LayerW none{};
-      const Dep dl{{P.flags + (size_t)(P.L - 1) * P.fl_stride + P.fl_down, nullptr, nullptr}, {P.n_down, 0, 0}, ep};
-      run_item(P, none, PH_LM, m, 0, wg, nb, dl, smem);
-      dep_signal(P.flags + P.fl_lm + wg, ep);
-      if (wg == 0) {
-        const Dep da{{P.flags + P.fl_lm, nullptr, nullptr}, {nb, 0, 0}, ep};
-        run_item(P, none, PH_ARGMAX, m, 0, 0, 1, da, smem);
-      }
-    }
-    if (wg == 0) dep_signal(argmax_flag, ep);
-  }
-}
+static const PhaseKernel kPhaseKernels[PH_COUNT] = {k_phase<PH_QKV>,   k_phase<PH_ATTN>, k_phase<PH_MLP>,
+                                                    k_phase<PH_FINAL>, k_phase<PH_LM>,   k_phase<PH_ARGMAX>};
+static const char *const kPhaseNames[PH_COUNT] = {"QKV", "ATTN", "MLP", "FINAL", "LM", "ARGMAX"};
 
 }  // namespace mllm
 
@@ -944,11 +955,9 @@ struct mllm_model {
   };
   std::vector<Named> tensors;
   float *d_rope_cos = nullptr, *d_rope_sin = nullptr;
-  float *d_x = nullptr, *d_q = nullptr, *d_attp = nullptr, *d_ff = nullptr, *d_logits = nullptr, *d_amv = nullptr;
-  int *d_ami = nullptr, *d_hist = nullptr;
-  void *d_kv = nullptr;
+  float *d_logits = nullptr;
+  int *d_hist = nullptr;
   PassState *d_st = nullptr;
-  unsigned *d_bar = nullptr;
   PassState *h_st = nullptr;  // pinned
   float *d_gemv_x = nullptr, *d_gemv_y = nullptr;
   DecParams P{};
@@ -956,9 +965,6 @@ struct mllm_model {
   int exec_mode = 1;
   int max_pass = 1;
   size_t lds_max = 0;
-  int persist_grid = 0;
-  int flow_grid = 0;
-  int epoch = 0;  // mode 3: last epoch used
   uint64_t device_bytes = 0;
   hipGraphExec_t chain_graph = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;  // around the kernels of the last call
@@ -977,22 +983,29 @@ int dev_alloc(mllm_model *M, void **p, size_t bytes) {
   return 0;
 }
 
-// Tile rows per item: about TILE_TARGET chunks, at most TC * WG.
-int tile_rows(int ng, int per_row_mats = 1) { return std::max(1, TILE_TARGET / (ng * per_row_mats)); }
+// LM tile rows: about TILE_TARGET chunks, at most TC * WG.
+int lm_tile_rows(int ng) { return std::max(1, std::min(TILE_TARGET, TC * WG) / ng); }
 
-// Dynamic LDS (bytes) of a pass of m tokens: the largest phase carve.
+// Dynamic LDS floats of each phase for a pass of m tokens (the carve-ups in
+// the phase functions).
+size_t lds_floats(const DecParams &P, int ph, int m) {
+  const size_t ngd = P.D / 32, D = P.D;
+  const size_t blk_o = (size_t)((P.NH + PB - 1) / PB) * D, blk_d = (size_t)((P.nchunk + PB - 1) / PB) * D;
+  switch (ph) {
+  case PH_QKV: return al4(16 + m * ngd * XS + m * ngd + m * 16 * ngd + m * 16) + blk_d;
+  case PH_ATTN: return HD + ACH + 16 * HD + 16 + HD + 2 * XS + 2 + 4;
+  case PH_MLP:
+    return al4(16 + m * ngd * XS + m * ngd + UNITS * ngd + 2 * (size_t)m * UNITS) + (size_t)m * 2 * XS + al4(2 * m) +
+           blk_o;
+  case PH_FINAL: return 16 + ngd * XS + blk_d;
+  case PH_LM: return m * ngd * XS + m * ngd + (size_t)m * TC * WG + (size_t)m * P.lm_rpt + 34 + P.max_seq;
+  default: return 16;
+  }
+}
+
 size_t lds_for(const DecParams &P, int m) {
-  const int ngd = P.D / 32, ngf = P.FF / 32;
-  auto gemv = [&](int ng, size_t outf) {
-    return 16 + (size_t)m * ng * XS + (size_t)m * ng + (size_t)m * TC * WG + outf;
-  };
   size_t f = 0;
-  f = std::max(f, gemv(ngd, (size_t)m * 16));                                     // qkv
-  f = std::max(f, gemv(ngd, (size_t)m * P.o_rpt));                                // o
-  f = std::max(f, gemv(ngd, (size_t)2 * m * P.up_rpt));                           // up
-  f = std::max(f, gemv(ngf, (size_t)m * P.dn_rpt));                               // down
-  f = std::max(f, gemv(ngd, (size_t)m * P.lm_rpt + 34 + (size_t)P.max_seq));     // lm + argmax lists
-  f = std::max(f, (size_t)(HD + ACH + 16 * HD + 16));                             // attn
+  for (int ph = 0; ph < PH_COUNT; ++ph) f = std::max(f, lds_floats(P, ph, m));
   return f * sizeof(float);
 }
 
@@ -1016,7 +1029,10 @@ int get_q4(mllm_model *M, const std::string &n, int rows, int cols, Q4Mat *out) 
   return 0;
 }
 
-int get_f32(mllm_model *M, const std::string &n, size_t count, const float **out, bool required = true) {
+// f32 tensor of at least `count` elements; `vec4` tensors are read as float4
+// and must be 16-byte aligned.
+int get_f32(mllm_model *M, const std::string &n, size_t count, const float **out, bool required = true,
+            bool vec4 = false) {
   const auto *t = find(M, n);
   if (!t) {
     *out = nullptr;
@@ -1024,6 +1040,8 @@ int get_f32(mllm_model *M, const std::string &n, size_t count, const float **out
   }
   if (t->storage != MLLM_F32 || (size_t)t->rows * t->cols < count)
     return set_error(MLLM_ERR_INVALID, "tensor %s must be f32 with >= %zu elements", n.c_str(), count);
+  if (vec4 && ((uintptr_t)t->data & 15) != 0)
+    return set_error(MLLM_ERR_INVALID, "tensor %s is not 16-byte aligned", n.c_str());
   *out = reinterpret_cast<const float *>(t->data);
   return 0;
 }
@@ -1033,12 +1051,32 @@ int upload_state(mllm_model *M) {
   return 0;
 }
 
-int launch_phase(mllm_model *M, int ph, int li, int m) {
+// With events e0/e1 the launch goes through hipExtLaunchKernel, which stamps
+// the kernel's own begin and end (the same interval a kernel trace reports).
+int launch_phase(mllm_model *M, int ph, int li, int m, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr) {
   const int n = phase_items(M->P, ph, m);
-  const LayerW Lw = ph <= PH_DOWN ? M->layers[li] : LayerW{};
+  LayerW Lw = ph <= PH_MLP ? M->layers[li] : LayerW{};
+  if (e0 && e1) {
+    DecParams P = M->P;
+    int li_ = li, m_ = m;
+    void *args[] = {&P, &Lw, &li_, &m_};
+    MLLM_HIP(hipExtLaunchKernel(reinterpret_cast<const void *>(kPhaseKernels[ph]), dim3(n), dim3(WG), args,
+                                lds_for(M->P, m), M->stream, e0, e1, 0));
+    return 0;
+  }
   hipLaunchKernelGGL(kPhaseKernels[ph], dim3(n), dim3(WG), lds_for(M->P, m), M->stream, M->P, Lw, li, m);
   MLLM_HIP(hipGetLastError());
   return 0;
+}
+
+// The phases of one pass in order: (phase, layer) pairs.
+std::vector<std::pair<int, int>> pass_phases(const mllm_model *M, bool lm) {
+  std::vector<std::pair<int, int>> v;
+  for (int li = 0; li < M->cfg.n_layers; ++li)
+    for (int ph = PH_QKV; ph <= PH_MLP; ++ph) v.emplace_back(ph, li);
+  if (lm)
+    for (int ph = PH_FINAL; ph <= PH_ARGMAX; ++ph) v.emplace_back(ph, 0);
+  return v;
 }
 
 // The chained decode step as an explicit graph: one kernel node per phase in
@@ -1049,8 +1087,10 @@ int build_chain_graph(mllm_model *M) {
   hipGraphNode_t prev = nullptr;
   const size_t lds = lds_for(M->P, 1);
   int m = 1;
-  auto add = [&](int ph, int li) -> int {
-    LayerW Lw = ph <= PH_DOWN ? M->layers[li] : LayerW{};
+  int rc = 0;
+  for (const auto &pl : pass_phases(M, true)) {
+    int ph = pl.first, li = pl.second;
+    LayerW Lw = ph <= PH_MLP ? M->layers[li] : LayerW{};
     void *args[] = {&M->P, &Lw, &li, &m};
     hipKernelNodeParams kp;
     memset(&kp, 0, sizeof kp);
@@ -1060,15 +1100,13 @@ int build_chain_graph(mllm_model *M) {
     kp.sharedMemBytes = (unsigned)lds;
     kp.kernelParams = args;
     hipGraphNode_t node;
-    MLLM_HIP(hipGraphAddKernelNode(&node, g, prev ? &prev : nullptr, prev ? 1 : 0, &kp));
+    hipError_t e = hipGraphAddKernelNode(&node, g, prev ? &prev : nullptr, prev ? 1 : 0, &kp);
+    if (e != hipSuccess) {
+      rc = hip_fail(e, "hipGraphAddKernelNode", __FILE__, __LINE__);
+      break;
+    }
     prev = node;
-    return 0;
-  };
-  int rc = 0;
-  for (int li = 0; li < M->cfg.n_layers && !rc; ++li)
-    for (int ph = PH_QKV; ph <= PH_DOWN && !rc; ++ph) rc = add(ph, li);
-  if (!rc) rc = add(PH_LM, 0);
-  if (!rc) rc = add(PH_ARGMAX, 0);
+  }
   if (!rc) {
     hipError_t e = hipGraphInstantiate(&M->chain_graph, g, nullptr, nullptr, 0);
     if (e != hipSuccess) rc = hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
@@ -1078,30 +1116,8 @@ int build_chain_graph(mllm_model *M) {
 }
 
 int enqueue_pass_phases(mllm_model *M, int m, bool lm) {
-  for (int li = 0; li < M->cfg.n_layers; ++li)
-    for (int ph = PH_QKV; ph <= PH_DOWN; ++ph)
-      if (int rc = launch_phase(M, ph, li, m)) return rc;
-  if (lm) {
-    if (int rc = launch_phase(M, PH_LM, 0, m)) return rc;
-    if (int rc = launch_phase(M, PH_ARGMAX, 0, m)) return rc;
-  }
-  return 0;
-}
-
-int launch_dataflow(mllm_model *M, int steps, int m) {
-  M->h_st->epoch = M->epoch + 1;
-  if (int rc = upload_state(M)) return rc;
-  void *args[] = {&M->P, &steps};
-  MLLM_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(k_dataflow), dim3(M->flow_grid), dim3(WG), args,
-                                      lds_for(M->P, m), M->stream));
-  M->epoch += steps;
-  return 0;
-}
-
-int launch_persistent(mllm_model *M, int steps, int m) {
-  void *args[] = {&M->P, &steps};
-  MLLM_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(k_persistent), dim3(M->persist_grid), dim3(WG),
-                                      args, lds_for(M->P, m), M->stream));
+  for (const auto &pl : pass_phases(M, lm))
+    if (int rc = launch_phase(M, pl.first, pl.second, m)) return rc;
   return 0;
 }
 
@@ -1111,8 +1127,7 @@ int check_device_err(mllm_model *M) {
   if (err[0] || err[1]) {
     int zero[2] = {0, 0};
     MLLM_HIP(hipMemcpy(&M->d_st->err, zero, sizeof(zero), hipMemcpyHostToDevice));
-    MLLM_HIP(hipMemset(M->d_bar, 0, 2 * sizeof(unsigned)));
-    return set_error(MLLM_ERR_DEVICE, err[0] ? "decode kernel grid barrier timed out"
+    return set_error(MLLM_ERR_DEVICE, err[0] ? "decode kernel reported an error"
                                              : "chained decode produced no finite maximum logit");
   }
   return 0;
@@ -1129,13 +1144,7 @@ int run_pass(mllm_model *M, const int32_t *ids, int m, int pos0, int lm_rows) {
   for (int i = 0; i < m; ++i) s.tok[i] = ids[i];
   if (int rc = upload_state(M)) return rc;
   MLLM_HIP(hipEventRecord(M->ev0, M->stream));
-  if (M->exec_mode == 3) {
-    if (int rc = launch_dataflow(M, 1, m)) return rc;
-  } else if (M->exec_mode == 0) {
-    if (int rc = launch_persistent(M, 1, m)) return rc;
-  } else {
-    if (int rc = enqueue_pass_phases(M, m, lm_rows != 0)) return rc;
-  }
+  if (int rc = enqueue_pass_phases(M, m, lm_rows != 0)) return rc;
   MLLM_HIP(hipEventRecord(M->ev1, M->stream));
   MLLM_HIP(hipStreamSynchronize(M->stream));
   MLLM_HIP(hipEventElapsedTime(&M->last_ms, M->ev0, M->ev1));
@@ -1183,10 +1192,11 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   MLLM_CHECK(c.d_model % c.n_heads == 0 && c.n_heads % c.n_kv_heads == 0, "heads do not divide");
   if (c.d_model / c.n_heads != HD)
     return set_error(MLLM_ERR_UNSUPPORTED, "head_dim %d unsupported (64 only)", c.d_model / c.n_heads);
-  if (c.d_model % 32 || c.d_ff % 32 || c.d_model > 4096 || c.d_ff > 16384)
-    return set_error(MLLM_ERR_UNSUPPORTED, "d_model %d / d_ff %d unsupported", c.d_model, c.d_ff);
+  if (c.d_model % 32 || c.d_model > 1024)
+    return set_error(MLLM_ERR_UNSUPPORTED, "d_model %d unsupported (a multiple of 32, <= 1024)", c.d_model);
+  if (c.d_ff % UNITS || c.d_ff > 16384)
+    return set_error(MLLM_ERR_UNSUPPORTED, "d_ff %d unsupported (a multiple of %d, <= 16384)", c.d_ff, UNITS);
   if (c.arch == 1 && c.n_kv_heads != c.n_heads) return set_error(MLLM_ERR_INVALID, "gpt2 needs n_kv_heads == n_heads");
-  if (c.d_model > 1024) return set_error(MLLM_ERR_UNSUPPORTED, "d_model %d unsupported (<= 1024)", c.d_model);
   if (c.arch == 0 && (int)floor(HD * c.rope_pct) != HD)
     return set_error(MLLM_ERR_UNSUPPORTED, "partial rotary (ropePct %g) unsupported", c.rope_pct);
 
@@ -1235,9 +1245,10 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       if (!rc) rc = get_f32(M, b + "ln1", 2 * D, &w.n1);
       if (!rc) rc = get_f32(M, b + "ln2", 2 * D, &w.n2);
       if (!rc) rc = get_f32(M, b + "attn.qkv_bias", D + 2 * kvd, &w.qkv_b);
-      if (!rc) rc = get_f32(M, b + "attn.proj_bias", D, &w.proj_b);
+      if (!rc) rc = get_f32(M, b + "attn.proj_bias", D, &w.proj_b, true, true);
       if (!rc) rc = get_f32(M, b + "mlp.fc_bias", FF, &w.fc_b);
-      if (!rc) rc = get_f32(M, b + "mlp.proj_bias", D, &w.mproj_b);
+      if (!rc) rc = get_f32(M, b + "mlp.proj_bias", D, &w.mproj_b, true, true);
+      w.prev_mproj_b = i > 0 ? M->layers[i - 1].mproj_b : nullptr;
     } else {
       if (!rc) rc = get_q4(M, b + "mlp.w1", FF, D, &w.w1);
       if (!rc) rc = get_q4(M, b + "mlp.w3", FF, D, &w.w3);
@@ -1257,6 +1268,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   P.V = V;
   P.max_seq = c.max_seq_len;
   P.kv_fp16 = c.kv_fp16 ? 1 : 0;
+  P.nchunk = FF / UNITS;
   P.eps = c.norm_eps > 0 ? c.norm_eps : 1e-6f;
   P.attn_scale = (float)(1.0 / sqrt((double)HD));
   P.nsplit_max = (c.max_seq_len + ACH - 1) / ACH;
@@ -1266,6 +1278,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
     if (!rc) rc = get_f32(M, "wpe", (size_t)c.max_seq_len * D, &P.wpe);
     if (!rc) rc = get_f32(M, "scale_factors", D, &P.sf, false);
     if (rc) return fail(rc);
+    P.last_mproj_b = M->layers[L - 1].mproj_b;
   } else {
     if (int rc = get_f32(M, "norm_f", D, &P.norm_f)) return fail(rc);
   }
@@ -1285,21 +1298,17 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
     return fail(set_error(MLLM_ERR_HIP, "layer table upload"));
   P.layers = M->d_layers;
 
-  // tiles
-  const int ngd = D / 32, ngf = FF / 32;
-  P.o_rpt = tile_rows(ngd);
-  P.up_rpt = tile_rows(ngd, c.arch == 1 ? 1 : 2);
-  P.dn_rpt = tile_rows(ngf);
-  P.lm_rpt = tile_rows(ngd);
+  // tiles: QKV 16 rows x ng <= TC * WG chunks (d_model <= 1024); the MLP and
+  // the head slices fit SC * WG chunks (UNITS x ng and 2 x d_model)
+  const int ngd = D / 32;
+  P.lm_rpt = lm_tile_rows(ngd);
   P.lm_tiles = (V + P.lm_rpt - 1) / P.lm_rpt;
   // MLLM_LM_TILES_PER_WG = 1: one tile per workgroup, every tile's loads in
   // flight at once; larger values trade workgroups for the register double
   // buffer of phase_lm.
   P.lm_grid = (P.lm_tiles + MLLM_LM_TILES_PER_WG - 1) / MLLM_LM_TILES_PER_WG;
-  // every GEMV tile must fit the TC * WG chunk registers of a workgroup
-  const int cap = TC * WG;
-  if (16 * ngd > cap || P.o_rpt * ngd > cap || P.up_rpt * ngd > cap || P.dn_rpt * ngf > cap || P.lm_rpt * ngd > cap)
-    return fail(set_error(MLLM_ERR_UNSUPPORTED, "tile exceeds %d chunks (d_model %d, d_ff %d)", cap, D, FF));
+  if (16 * ngd > TC * WG || UNITS * ngd > SC * WG || 2 * D > SC * WG)
+    return fail(set_error(MLLM_ERR_UNSUPPORTED, "tiles exceed the chunk registers (d_model %d)", D));
 
   // pass size bound by LDS (160 KiB on gfx950)
   const size_t lds_cap = (size_t)prop.sharedMemPerBlock > 0 ? (size_t)prop.sharedMemPerBlock : 65536;
@@ -1311,80 +1320,39 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
 
   // activations, KV cache, scratch
   const size_t kv_elems = (size_t)L * 2 * NKV * c.max_seq_len * HD;
-  int rc = dev_alloc(M, (void **)&M->d_x, sizeof(float) * MAXT * D);
-  if (!rc) rc = dev_alloc(M, (void **)&M->d_q, sizeof(float) * MAXT * NH * HD);
-  if (!rc) rc = dev_alloc(M, &M->d_kv, kv_elems * (c.kv_fp16 ? 2 : 4));
-  if (!rc) rc = dev_alloc(M, (void **)&M->d_attp, sizeof(float) * MAXT * NH * P.nsplit_max * APS);
-  if (!rc) rc = dev_alloc(M, (void **)&M->d_ff, sizeof(float) * MAXT * FF);
+  int rc = dev_alloc(M, (void **)&P.xa, sizeof(float) * MAXT * D);
+  if (!rc) rc = dev_alloc(M, (void **)&P.xb, sizeof(float) * MAXT * D);
+  if (!rc) rc = dev_alloc(M, (void **)&P.opart, sizeof(float) * MAXT * NH * D);
+  if (!rc) rc = dev_alloc(M, (void **)&P.dpart, sizeof(float) * MAXT * P.nchunk * D);
+  if (!rc) rc = dev_alloc(M, (void **)&P.xn, sizeof(float) * MAXT * D);
+  if (!rc) rc = dev_alloc(M, (void **)&P.q, sizeof(float) * MAXT * NH * HD);
+  if (!rc) rc = dev_alloc(M, &P.kv, kv_elems * (c.kv_fp16 ? 2 : 4));
+  if (!rc) rc = dev_alloc(M, (void **)&P.attp, sizeof(float) * MAXT * NH * P.nsplit_max * APS);
+  if (!rc) rc = dev_alloc(M, (void **)&P.cnt, sizeof(unsigned) * MAXT * NH);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_logits, sizeof(float) * MAXT * (size_t)V);
-  if (!rc) rc = dev_alloc(M, (void **)&M->d_amv, sizeof(float) * MAXT * P.lm_tiles);
-  if (!rc) rc = dev_alloc(M, (void **)&M->d_ami, sizeof(int) * MAXT * P.lm_tiles);
+  if (!rc) rc = dev_alloc(M, (void **)&P.amv, sizeof(float) * MAXT * P.lm_tiles);
+  if (!rc) rc = dev_alloc(M, (void **)&P.ami, sizeof(int) * MAXT * P.lm_tiles);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_hist, sizeof(int) * (c.max_seq_len + 1));
   if (!rc) rc = dev_alloc(M, (void **)&M->d_st, sizeof(PassState));
-  if (!rc) rc = dev_alloc(M, (void **)&M->d_bar, 64);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_gemv_x, sizeof(float) * std::max(FF, D) * 4);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_gemv_y, sizeof(float) * std::max((size_t)V, (size_t)std::max(FF, D + 2 * kvd)));
   if (rc) return fail(rc);
   if (hipHostMalloc((void **)&M->h_st, sizeof(PassState), hipHostMallocDefault) != hipSuccess)
     return fail(set_error(MLLM_ERR_HIP, "pinned state"));
-  if (hipMemset(M->d_bar, 0, 64) != hipSuccess || hipMemset(M->d_st, 0, sizeof(PassState)) != hipSuccess ||
-      hipMemset(M->d_kv, 0, kv_elems * (c.kv_fp16 ? 2 : 4)) != hipSuccess)
+  if (hipMemset(M->d_st, 0, sizeof(PassState)) != hipSuccess ||
+      hipMemset(P.cnt, 0, sizeof(unsigned) * MAXT * NH) != hipSuccess ||
+      hipMemset(P.kv, 0, kv_elems * (c.kv_fp16 ? 2 : 4)) != hipSuccess)
     return fail(set_error(MLLM_ERR_HIP, "memset"));
-  P.x = M->d_x;
-  P.q = M->d_q;
-  P.kv = M->d_kv;
-  P.attp = M->d_attp;
-  P.ff = M->d_ff;
   P.logits = M->d_logits;
-  P.amv = M->d_amv;
-  P.ami = M->d_ami;
   P.hist = M->d_hist;
   P.st = M->d_st;
-  P.bar = M->d_bar;
 
   if (M->lds_max > 64 * 1024) {
-    bool ok = hipFuncSetAttribute(reinterpret_cast<const void *>(k_persistent),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)M->lds_max) == hipSuccess;
+    bool ok = true;
     for (int ph = 0; ph < PH_COUNT; ++ph)
       ok = ok && hipFuncSetAttribute(reinterpret_cast<const void *>(kPhaseKernels[ph]),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)M->lds_max) == hipSuccess;
     if (!ok) return fail(set_error(MLLM_ERR_HIP, "LDS attribute"));
-  }
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(k_persistent), WG,
-                                                   M->lds_max) != hipSuccess ||
-      per_cu < 1)
-    per_cu = 1;
-  M->persist_grid = M->num_cus * std::min(per_cu, 1);
-  {
-    bool ok = true;
-    if (M->lds_max > 64 * 1024)
-      ok = hipFuncSetAttribute(reinterpret_cast<const void *>(k_dataflow), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)M->lds_max) == hipSuccess;
-    int fcu = 0;
-    if (!ok || hipOccupancyMaxActiveBlocksPerMultiprocessor(&fcu, reinterpret_cast<const void *>(k_dataflow), WG,
-                                                             M->lds_max) != hipSuccess || fcu < 1)
-      fcu = 1;
-    M->flow_grid = M->num_cus * std::min(fcu, 2);
-  }
-  // mode 3 flags: per layer [qkv | attn | o | up | down], then lm[grid], argmax
-  {
-    DecParams &Q = M->P;
-    const int n_qkv = (Q.NH + 2 * Q.NKV) * QSPLIT;
-    Q.n_o = (Q.D + Q.o_rpt - 1) / Q.o_rpt;
-    Q.n_up = (Q.FF + Q.up_rpt - 1) / Q.up_rpt;
-    Q.n_down = (Q.D + Q.dn_rpt - 1) / Q.dn_rpt;
-    Q.fl_qkv = 0;
-    Q.fl_attn = n_qkv;
-    Q.fl_o = Q.fl_attn + MAXT * Q.NH * Q.nsplit_max;
-    Q.fl_up = Q.fl_o + Q.n_o;
-    Q.fl_down = Q.fl_up + Q.n_up;
-    Q.fl_stride = Q.fl_down + Q.n_down;
-    Q.fl_lm = Q.L * Q.fl_stride;
-    Q.fl_argmax = Q.fl_lm + M->flow_grid;
-    const size_t nflags = (size_t)Q.fl_argmax + 1;
-    if (int rc = dev_alloc(M, (void **)&Q.flags, nflags * sizeof(int))) return fail(rc);
-    if (hipMemset(Q.flags, 0, nflags * sizeof(int)) != hipSuccess) return fail(set_error(MLLM_ERR_HIP, "memset"));
   }
   *out = M;
   clear_error();
@@ -1424,7 +1392,7 @@ extern "C" int mllm_max_pass_tokens(const mllm_model *M) { return M ? M->max_pas
 
 extern "C" int mllm_set_exec_mode(mllm_model *M, int mode) {
   MLLM_CHECK(M, "null model");
-  MLLM_CHECK(mode >= 0 && mode <= 3, "exec mode %d", mode);
+  MLLM_CHECK(mode == 1 || mode == 2, "exec mode %d (1: graph replay, 2: direct launches)", mode);
   M->exec_mode = mode;
   return 0;
 }
@@ -1493,11 +1461,7 @@ extern "C" int mllm_decode_chain(mllm_model *M, int32_t first, int n_steps, int3
   s.tok[0] = first;
   if (int rc = upload_state(M)) return rc;
   MLLM_HIP(hipEventRecord(M->ev0, M->stream));
-  if (M->exec_mode == 3) {
-    if (int rc = launch_dataflow(M, n_steps, 1)) return rc;
-  } else if (M->exec_mode == 0) {
-    if (int rc = launch_persistent(M, n_steps, 1)) return rc;
-  } else if (M->exec_mode == 2) {
+  if (M->exec_mode == 2) {
     for (int i = 0; i < n_steps; ++i)
       if (int rc = enqueue_pass_phases(M, 1, true)) return rc;
   } else {
@@ -1523,8 +1487,8 @@ extern "C" int mllm_profile_decode(mllm_model *M, int32_t first, int n_steps, fl
   MLLM_CHECK(n_steps > 0, "n_steps %d", n_steps);
   MLLM_CHECK(M->cache_len + n_steps <= M->cfg.max_seq_len, "profile run exceeds the context");
   if (int rc = check_ids(M, &first, 1)) return rc;
-  const int L = M->cfg.n_layers;
-  const int per_step = L * 5 + 2;
+  const auto phases = pass_phases(M, true);
+  const int per_step = (int)phases.size();
   if ((int)M->prof_ev.size() < 2 * per_step) {
     for (hipEvent_t e : M->prof_ev) (void)hipEventDestroy(e);
     M->prof_ev.assign(2 * per_step, nullptr);
@@ -1542,27 +1506,15 @@ extern "C" int mllm_profile_decode(mllm_model *M, int32_t first, int n_steps, fl
   double sum[PH_COUNT] = {0};
   int cnt[PH_COUNT] = {0};
   for (int step = 0; step < n_steps; ++step) {
-    int k = 0;
-    std::vector<int> phs;
-    for (int li = 0; li < L; ++li)
-      for (int ph = PH_QKV; ph <= PH_DOWN; ++ph, ++k) {
-        MLLM_HIP(hipEventRecord(M->prof_ev[2 * k], M->stream));
-        if (int rc = launch_phase(M, ph, li, 1)) return rc;
-        MLLM_HIP(hipEventRecord(M->prof_ev[2 * k + 1], M->stream));
-        phs.push_back(ph);
-      }
-    for (int ph = PH_LM; ph <= PH_ARGMAX; ++ph, ++k) {
-      MLLM_HIP(hipEventRecord(M->prof_ev[2 * k], M->stream));
-      if (int rc = launch_phase(M, ph, 0, 1)) return rc;
-      MLLM_HIP(hipEventRecord(M->prof_ev[2 * k + 1], M->stream));
-      phs.push_back(ph);
-    }
+    for (int k = 0; k < per_step; ++k)
+      if (int rc = launch_phase(M, phases[k].first, phases[k].second, 1, M->prof_ev[2 * k], M->prof_ev[2 * k + 1]))
+        return rc;
     MLLM_HIP(hipStreamSynchronize(M->stream));
-    for (int j = 0; j < k; ++j) {
+    for (int k = 0; k < per_step; ++k) {
       float ms = 0;
-      MLLM_HIP(hipEventElapsedTime(&ms, M->prof_ev[2 * j], M->prof_ev[2 * j + 1]));
-      sum[phs[j]] += ms;
-      cnt[phs[j]] += 1;
+      MLLM_HIP(hipEventElapsedTime(&ms, M->prof_ev[2 * k], M->prof_ev[2 * k + 1]));
+      sum[phases[k].first] += ms;
+      cnt[phases[k].first] += 1;
     }
   }
   if (int rc = check_device_err(M)) return rc;
@@ -1570,6 +1522,10 @@ extern "C" int mllm_profile_decode(mllm_model *M, int32_t first, int n_steps, fl
   M->cache_len += n_steps;
   for (int ph = 0; ph < PH_COUNT; ++ph) phase_us[ph] = cnt[ph] ? (float)(sum[ph] / cnt[ph] * 1000.0) : 0.f;
   return 0;
+}
+
+extern "C" const char *mllm_phase_name(int phase) {
+  return phase >= 0 && phase < PH_COUNT ? kPhaseNames[phase] : nullptr;
 }
 
 extern "C" int mllm_last_timing(const mllm_model *M, float *gpu_ms, int *n_tokens) {

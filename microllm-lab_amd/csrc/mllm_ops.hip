@@ -148,8 +148,7 @@ __global__ __launch_bounds__(WG) void k_gemv_f32(const float *__restrict__ w, co
   } else {
     for (int k = lane; k < cols; k += 64) acc = __builtin_fmaf(wr[k], x[k], acc);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  acc = wave_sum(acc);
   if (lane == 0) y[row] = acc;
 }
 

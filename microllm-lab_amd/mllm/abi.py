@@ -47,6 +47,7 @@ SIGNATURES = {
     "mllm_model_device_bytes": ([P], C.c_uint64),
     "mllm_last_timing": ([P, P, P], I),
     "mllm_profile_decode": ([P, C.c_int32, I, P], I),
+    "mllm_phase_name": ([I], C.c_char_p),
 }
 
 

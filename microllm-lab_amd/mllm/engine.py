@@ -114,13 +114,18 @@ class PetitGPT:
         abi.call("mllm_last_timing", self._h, C.byref(ms), C.byref(n))
         return float(ms.value), int(n.value)
 
-    PHASES = ("QKV", "ATTN", "O", "UP", "DOWN", "LM", "ARGMAX")
+    N_PHASES = 6  # MLLM_PHASES
+
+    @staticmethod
+    def phase_names() -> list:
+        return [abi.lib().mllm_phase_name(i).decode() for i in range(PetitGPT.N_PHASES)]
 
     def profile_decode(self, first: int, n_steps: int) -> dict:
-        """Mean microseconds per launch of each decode phase (events on the model stream)."""
-        out = (C.c_float * 7)()
+        """Mean microseconds per launch of each decode phase: the kernels' own
+        begin/end stamps (hipExtLaunchKernel events on the model stream)."""
+        out = (C.c_float * self.N_PHASES)()
         abi.call("mllm_profile_decode", self._h, int(first), int(n_steps), out)
-        return {name: float(out[i]) for i, name in enumerate(self.PHASES)}
+        return {name: float(out[i]) for i, name in enumerate(self.phase_names())}
 
     @property
     def bytesAllocated(self) -> int:

@@ -44,7 +44,7 @@ def build(arch="llama", seed=1, **over):
 
 @gpu
 @pytest.mark.parametrize("arch", ["llama", "gpt2"])
-@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("mode", [1, 2])
 def test_small_teacher_forced_vs_oracle(oracle_lib, arch, mode):
     bundle = build(arch, seed=3)
     print(f"decode small {arch} mode={mode}", flush=True)
@@ -61,7 +61,7 @@ def test_small_teacher_forced_vs_oracle(oracle_lib, arch, mode):
 def test_exec_modes_bit_identical():
     bundle = build("llama", seed=5)
     outs = []
-    for mode in (0, 1, 2, 3):
+    for mode in (1, 2):
         g = mllm.PetitGPT(bundle, exec_mode=mode)
         rows = [g.forwardPrompt([1, 2, 3, 4, 5]).copy()]
         for t in (6, 7, 8):
@@ -69,8 +69,6 @@ def test_exec_modes_bit_identical():
         outs.append(np.stack(rows))
         g.destroy()
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
-    assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
-    assert np.array_equal(outs[0].view(np.uint32), outs[3].view(np.uint32))
 
 
 @gpu
@@ -92,7 +90,7 @@ def test_verify_rows_bit_identical_to_decode(n):
 
 
 @gpu
-@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("mode", [1, 2])
 def test_chain_equals_host_greedy(mode):
     bundle = build("llama", seed=7)
     g = mllm.PetitGPT(bundle, exec_mode=mode)
@@ -104,7 +102,7 @@ def test_chain_equals_host_greedy(mode):
 
 
 @gpu
-@pytest.mark.parametrize("mode", [1, 3])
+@pytest.mark.parametrize("mode", [1, 2])
 def test_chain_stops_at_eos(mode):
     bundle = build("llama", seed=7)
     g = mllm.PetitGPT(bundle, exec_mode=mode)
@@ -118,7 +116,7 @@ def test_chain_stops_at_eos(mode):
 
 
 @gpu
-@pytest.mark.parametrize("mode", [1, 3])
+@pytest.mark.parametrize("mode", [1, 2])
 def test_gpt2_chain_penalty_equals_host_argmax_gpt2(mode):
     """Device argmaxGpt2 (3-gram block + 1.15 penalty) == host rule on host logits."""
     bundle = build("gpt2", seed=8)
@@ -132,7 +130,7 @@ def test_gpt2_chain_penalty_equals_host_argmax_gpt2(mode):
 
 
 @gpu
-@pytest.mark.parametrize("mode", [1, 3])
+@pytest.mark.parametrize("mode", [1, 2])
 def test_long_context_splits_vs_oracle(oracle_lib, mode):
     """Context beyond one 256-position attention split (several splits merged)."""
     bundle = build("llama", seed=9, max_seq_len=1024)

@@ -33,7 +33,7 @@ def row_bound(W, x):
 
 
 SHAPES = [(7, 32), (33, 64), (576, 576), (960, 576), (3072, 576), (576, 1536), (960, 960), (320, 960),
-          (2560, 960), (960, 2560), (2304, 768), (768, 3072), (49152, 960), (50257, 768)]
+          (2560, 960), (960, 2560), (2304, 768), (768, 3072), (49152, 960), (50257, 768), (64, 8192), (3, 16384)]
 
 
 @gpu
