@@ -138,25 +138,39 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
-// Deterministic block-wide sum for 256 threads; red needs 4 floats of LDS.
+// Pairwise tree over N = 2^k values: (tree(lower half) + tree(upper half)).
+template <int N>
+__device__ __forceinline__ float tree_sum(const float *r) {
+  if constexpr (N == 1) return r[0];
+  else return tree_sum<N / 2>(r) + tree_sum<N / 2>(r + N / 2);
+}
+template <int N>
+__device__ __forceinline__ float tree_max(const float *r) {
+  if constexpr (N == 1) return r[0];
+  else return fmaxf(tree_max<N / 2>(r), tree_max<N / 2>(r + N / 2));
+}
+
+// Deterministic block-wide sum for NT threads; red needs NT / 64 floats of LDS.
+template <int NT = WG>
 __device__ __forceinline__ float block_sum(float v, float *red) {
   v = wave_sum(v);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wv] = v;
   __syncthreads();
-  const float r = (red[0] + red[1]) + (red[2] + red[3]);
+  const float r = tree_sum<NT / 64>(red);
   __syncthreads();
   return r;
 }
 
+template <int NT = WG>
 __device__ __forceinline__ float block_max(float v, float *red) {
   v = wave_max(v);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wv] = v;
   __syncthreads();
-  const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float r = tree_max<NT / 64>(red);
   __syncthreads();
   return r;
 }
@@ -202,8 +216,9 @@ __device__ __forceinline__ void wave_argmax(float &v, int &i) {
 
 // Per-group sums of the staged activations: xsum[t*ng+g] = sum_k xs[(t*ng+g)*XS+k]
 // in ascending k.  Call after xs is complete (a barrier follows inside).
+template <int NT = WG>
 __device__ __forceinline__ void stage_group_sums(const float *xs, float *xsum, int m, int ng) {
-  for (int i = threadIdx.x; i < m * ng; i += WG) {
+  for (int i = threadIdx.x; i < m * ng; i += NT) {
     const float *p = xs + i * XS;
     float s = 0.f;
 #pragma unroll
@@ -216,15 +231,16 @@ __device__ __forceinline__ void stage_group_sums(const float *xs, float *xsum, i
 // Copy m rows x[t*ldx + i] (i < n, n % 32 == 0, 16-byte aligned rows) into
 // the skewed layout.  Loads go out in batches of 4 float4 per thread before
 // any LDS store, so a batch costs one memory latency, not one per element.
+template <int NT = WG>
 __device__ __forceinline__ void stage_rows(const float *__restrict__ x, int ldx, int m, int n, float *xs) {
   const int nq = n >> 2, total = m * nq, ng = n >> 5;
-  for (int base = 0; base < total; base += 4 * WG) {
+  for (int base = 0; base < total; base += 4 * NT) {
     // Every element of v is written on every path: a partially written
     // register array is kept in scratch memory by the compiler.
     float4 v[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int f = base + threadIdx.x + k * WG;
+      const int f = base + threadIdx.x + k * NT;
       v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (f < total) {
         const int t = f / nq, q = f - t * nq;
@@ -233,7 +249,7 @@ __device__ __forceinline__ void stage_rows(const float *__restrict__ x, int ldx,
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int f = base + threadIdx.x + k * WG;
+      const int f = base + threadIdx.x + k * NT;
       if (f < total) {
         const int t = f / nq, i = 4 * (f - t * nq);
         *reinterpret_cast<float4 *>(xs + (t * ng + (i >> 5)) * XS + (i & 31)) = v[k];
@@ -275,13 +291,13 @@ struct TileRegs {
   float s[C];
 };
 
-template <int C>
+template <int C, int NT = WG>
 __device__ __forceinline__ void tile_load(const Q4Mat &W, int r0a, int na, int r0b, int ng, int nch,
                                           TileRegs<C> &R) {
   const int split = na * ng;
 #pragma unroll
   for (int j = 0; j < C; ++j) {
-    const int c = threadIdx.x + j * WG;
+    const int c = threadIdx.x + j * NT;
     if (c < nch) {
       const size_t gc = c < split ? (size_t)r0a * ng + c : (size_t)r0b * ng + (c - split);
       R.w[j] = W.q[gc];
@@ -291,8 +307,8 @@ __device__ __forceinline__ void tile_load(const Q4Mat &W, int r0a, int na, int r
 }
 
 // out[t*ostride + r] for tile row r in [0, nrows): rows of range a first.
-// part needs m*nch floats of LDS.  gfirst = threadIdx.x % ng, gstep = WG % ng.
-template <int C>
+// part needs m*nch floats of LDS.  gfirst = threadIdx.x % ng, gstep = NT % ng.
+template <int C, int NT = WG>
 __device__ __forceinline__ void tile_compute(const TileRegs<C> &R, int nrows, int ng, int nch, int m,
                                              const float *xs, const float *xsum, int gfirst, int gstep,
                                              float *part, float *out, int ostride) {
@@ -312,7 +328,7 @@ __device__ __forceinline__ void tile_compute(const TileRegs<C> &R, int nrows, in
   for (int t = 0; t < m; ++t) {
 #pragma unroll
     for (int j = 0; j < C; ++j) {
-      const int c = threadIdx.x + j * WG;
+      const int c = threadIdx.x + j * NT;
       if (c < nch) {
         const float d = q4_chunk_dot(R.w[j], xs + (t * ng + gj[j]) * XS);
         part[t * nch + c] = (d - 8.f * xsum[t * ng + gj[j]]) * R.s[j];
@@ -320,7 +336,7 @@ __device__ __forceinline__ void tile_compute(const TileRegs<C> &R, int nrows, in
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < nrows * m; i += WG) {
+  for (int i = threadIdx.x; i < nrows * m; i += NT) {
     const int t = i / nrows, r = i - t * nrows;
     out[t * ostride + r] = row_sum(part + t * nch + r * ng, ng);
   }

@@ -62,11 +62,22 @@ constexpr int HD = 64;     // head dimension of every supported config
 constexpr int ACH = 256;   // positions per attention split (one per thread)
 constexpr int MAXT = 16;   // tokens per pass (upper bound; LDS sets the real one)
 constexpr int APS = 68;    // floats per attention partial: m, l, pad, pad, acc[64]
-constexpr int TC = 2;      // chunk registers per thread of a QKV / LM tile (TC * WG chunks)
+constexpr int TC = 2;      // chunk registers per thread of an LM tile (TC * WG chunks)
+// Threads per workgroup of each phase.  The QKV, MLP and FINAL phases are
+// chains of dependent steps (loads, reductions, small GEMVs) inside few
+// workgroups: 1024 threads put four waves on every SIMD of the CU, so each
+// step's latency is shared out instead of serialised in one wave per SIMD.
+constexpr int QT = 1024;   // QKV
+constexpr int AT = WG;     // ATTN: one thread per position of a 256-position split
+constexpr int MT = 1024;   // MLP
+constexpr int FT = 1024;   // FINAL
+constexpr int LT = WG;     // LM, ARGMAX
 constexpr int TILE_TARGET = 320;  // chunks per LM tile (~0.15 us of VALU on one CU)
 constexpr int QSPLIT = 4;  // QKV tiles per head
 constexpr int UNITS = 64;  // hidden units per MLP item (two 32-column groups of mlp.w2)
-constexpr int SC = 8;      // chunk registers per thread of the MLP tiles and column slices
+constexpr int SC = 8;      // chunk registers per thread of an ATTN head slice (SC * AT chunks)
+constexpr int MC = 2;      // chunk registers per thread of the MLP tiles and slices (MC * MT chunks)
+constexpr int QC = 1;      // chunk registers per thread of a QKV tile (QC * QT chunks)
 constexpr int PB = 8;      // partials per block of the fixed-order partial sums
 
 enum Phase { PH_QKV = 0, PH_ATTN, PH_MLP, PH_FINAL, PH_LM, PH_ARGMAX, PH_COUNT };
@@ -127,17 +138,20 @@ __device__ __forceinline__ size_t kv_index(const DecParams &P, int li, int which
   return ((((size_t)li * 2 + which) * P.NKV + h) * P.max_seq + pos) * HD;
 }
 
-// Norm gains (and LayerNorm betas) of this thread's elements i = tid + k*WG,
+// Norm gains (and LayerNorm betas) of this thread's elements i = tid + k*NT,
 // loaded into registers up front (d_model <= 1024).
+template <int NT>
 struct Gains {
-  float g[4], b[4];
+  static constexpr int K = (1024 + NT - 1) / NT;
+  float g[K], b[K];
 };
 
-__device__ __forceinline__ Gains load_gains(const DecParams &P, const float *w) {
-  Gains G;
+template <int NT>
+__device__ __forceinline__ Gains<NT> load_gains(const DecParams &P, const float *w) {
+  Gains<NT> G;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int i = threadIdx.x + k * WG;
+  for (int k = 0; k < Gains<NT>::K; ++k) {
+    const int i = threadIdx.x + k * NT;
     G.g[k] = 0.f;
     G.b[k] = 0.f;
     if (i < P.D) {
@@ -150,31 +164,33 @@ __device__ __forceinline__ Gains load_gains(const DecParams &P, const float *w) 
 
 // Normalise m staged raw vectors in place (skewed layout): RMSNorm
 // (infer.js:134-143) or LayerNorm (infer.js:147-164, eps 1e-5).
-__device__ void norm_staged(const DecParams &P, float *xs, int m, const Gains &G, float *red) {
+template <int NT>
+__device__ void norm_staged(const DecParams &P, float *xs, int m, const Gains<NT> &G, float *red) {
+  constexpr int K = Gains<NT>::K;
   const int D = P.D, ng = D >> 5;
   for (int t = 0; t < m; ++t) {
     float *xt = xs + t * ng * XS;
     if (P.arch == 1) {
       float s = 0.f;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = threadIdx.x + k * WG;
+      for (int k = 0; k < K; ++k) {
+        const int i = threadIdx.x + k * NT;
         if (i < D) s += xt[skew(i)];
       }
-      const float mean = block_sum(s, red) / (float)D;
+      const float mean = block_sum<NT>(s, red) / (float)D;
       float v = 0.f;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = threadIdx.x + k * WG;
+      for (int k = 0; k < K; ++k) {
+        const int i = threadIdx.x + k * NT;
         if (i < D) {
           const float d = xt[skew(i)] - mean;
           v = __builtin_fmaf(d, d, v);
         }
       }
-      const float inv = 1.0f / sqrtf(block_sum(v, red) / (float)D + 1e-5f);
+      const float inv = 1.0f / sqrtf(block_sum<NT>(v, red) / (float)D + 1e-5f);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = threadIdx.x + k * WG;
+      for (int k = 0; k < K; ++k) {
+        const int i = threadIdx.x + k * NT;
         if (i < D) {
           const int j = skew(i);
           xt[j] = __builtin_fmaf((xt[j] - mean) * inv, G.g[k], G.b[k]);
@@ -183,14 +199,14 @@ __device__ void norm_staged(const DecParams &P, float *xs, int m, const Gains &G
     } else {
       float s = 0.f;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = threadIdx.x + k * WG;
+      for (int k = 0; k < K; ++k) {
+        const int i = threadIdx.x + k * NT;
         if (i < D) s = __builtin_fmaf(xt[skew(i)], xt[skew(i)], s);
       }
-      const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)D + P.eps);
+      const float inv = 1.0f / sqrtf(block_sum<NT>(s, red) / (float)D + P.eps);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = threadIdx.x + k * WG;
+      for (int k = 0; k < K; ++k) {
+        const int i = threadIdx.x + k * NT;
         if (i < D) {
           const int j = skew(i);
           xt[j] = xt[j] * inv * G.g[k];
@@ -215,16 +231,20 @@ __device__ __forceinline__ float4 add4(float4 a, float4 b) {
 // The first round of token t0 is loaded by resid_prefetch, which a phase
 // calls before it issues its weight loads: loads retire in issue order, so
 // activations issued first can be consumed while the weights still stream.
+// U items per thread per round: two with 256 threads, one with 1024.
+template <int NT>
 struct ResidPre {
-  float4 v[2][PB];
+  static constexpr int U = NT >= 1024 ? 1 : 2;
+  float4 v[U][PB];
   float4 xb, bb;
 };
 
-__device__ __forceinline__ void resid_load(const float4 *pt, int nq, int np, int nitems, int i0, float4 (&v)[2][PB]) {
+template <int NT, int U>
+__device__ __forceinline__ void resid_load(const float4 *pt, int nq, int np, int nitems, int i0, float4 (&v)[U][PB]) {
   const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int it = i0 + u * WG;
+  for (int u = 0; u < U; ++u) {
+    const int it = i0 + u * NT;
     const int b = it / nq, c = it - b * nq;
 #pragma unroll
     for (int k = 0; k < PB; ++k) {
@@ -235,10 +255,11 @@ __device__ __forceinline__ void resid_load(const float4 *pt, int nq, int np, int
   }
 }
 
-__device__ __forceinline__ void resid_add(int nq, int np, int nitems, int i0, const float4 (&v)[2][PB], float *blk) {
+template <int NT, int U>
+__device__ __forceinline__ void resid_add(int nq, int np, int nitems, int i0, const float4 (&v)[U][PB], float *blk) {
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int it = i0 + u * WG;
+  for (int u = 0; u < U; ++u) {
+    const int it = i0 + u * NT;
     if (it < nitems) {
       const int b = it / nq;
       float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -250,8 +271,9 @@ __device__ __forceinline__ void resid_add(int nq, int np, int nitems, int i0, co
   }
 }
 
+template <int NT>
 __device__ __forceinline__ void resid_prefetch(const float *base, const float *parts, int np, const float *bias, int t0,
-                                               int D, ResidPre &R) {
+                                               int D, ResidPre<NT> &R) {
   const int nq = D >> 2, nb = (np + PB - 1) / PB;
   const int q = threadIdx.x;  // D <= 1024: one float4 column per thread
   R.xb = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -260,19 +282,22 @@ __device__ __forceinline__ void resid_prefetch(const float *base, const float *p
     R.xb = reinterpret_cast<const float4 *>(base + (size_t)t0 * D)[q];
     if (bias) R.bb = reinterpret_cast<const float4 *>(bias)[q];
   }
-  resid_load(reinterpret_cast<const float4 *>(parts + (size_t)t0 * np * D), nq, np, nq * nb, threadIdx.x, R.v);
+  resid_load<NT, ResidPre<NT>::U>(reinterpret_cast<const float4 *>(parts + (size_t)t0 * np * D), nq, np, nq * nb,
+                                  threadIdx.x, R.v);
 }
 
-// Block sums of row t (all rounds but the prefetched one when `first` is
+// Block sums of row t (all rounds but the prefetched one when skip_first is
 // set), then the row itself: xs[tt] and out[t].
+template <int NT>
 __device__ __forceinline__ void resid_row(const float *parts, int np, int t, int tt, int D, float4 xb, float4 bb,
                                           bool has_bias, bool skip_first, float *xs, float *out, float *blk) {
+  constexpr int U = ResidPre<NT>::U;
   const int nq = D >> 2, ng = D >> 5, nb = (np + PB - 1) / PB, nitems = nq * nb;
   const float4 *pt = reinterpret_cast<const float4 *>(parts + (size_t)t * np * D);
-  for (int i0 = threadIdx.x + (skip_first ? 2 * WG : 0); i0 < nitems; i0 += 2 * WG) {
-    float4 v[2][PB];
-    resid_load(pt, nq, np, nitems, i0, v);
-    resid_add(nq, np, nitems, i0, v, blk);
+  for (int i0 = threadIdx.x + (skip_first ? U * NT : 0); i0 < nitems; i0 += U * NT) {
+    float4 v[U][PB];
+    resid_load<NT, U>(pt, nq, np, nitems, i0, v);
+    resid_add<NT, U>(nq, np, nitems, i0, v, blk);
   }
   __syncthreads();
   const int q = threadIdx.x;
@@ -289,49 +314,50 @@ __device__ __forceinline__ void resid_row(const float *parts, int np, int t, int
   __syncthreads();
 }
 
+template <int NT>
 __device__ void stage_residual(const float *base, const float *parts, int np, const float *bias, int t0, int m,
-                               int D, float *xs, float *out, float *blk, const ResidPre &R) {
+                               int D, float *xs, float *out, float *blk, const ResidPre<NT> &R) {
   const int nq = D >> 2, nb = (np + PB - 1) / PB;
   const float4 bb = R.bb;
   // token t0: its first round is in R
-  resid_add(nq, np, nq * nb, threadIdx.x, R.v, blk);
-  resid_row(parts, np, t0, 0, D, R.xb, bb, bias != nullptr, true, xs, out, blk);
+  resid_add<NT, ResidPre<NT>::U>(nq, np, nq * nb, threadIdx.x, R.v, blk);
+  resid_row<NT>(parts, np, t0, 0, D, R.xb, bb, bias != nullptr, true, xs, out, blk);
   for (int tt = 1; tt < m; ++tt) {
     const int t = t0 + tt;
     float4 xb = make_float4(0.f, 0.f, 0.f, 0.f);
     if ((int)threadIdx.x < nq) xb = reinterpret_cast<const float4 *>(base + (size_t)t * D)[threadIdx.x];
-    resid_row(parts, np, t, tt, D, xb, bb, bias != nullptr, false, xs, out, blk);
+    resid_row<NT>(parts, np, t, tt, D, xb, bb, bias != nullptr, false, xs, out, blk);
   }
 }
 
-// One token's GEMV over a row tile held in registers (chunk c = tid + k*WG
+// One token's GEMV over a row tile held in registers (chunk c = tid + k*NT
 // of rows ng groups wide, c < nch): out[r] for r < nch / ng, with the
 // arithmetic of tile_compute (bit-identical rows).
-template <int C>
+template <int C, int NT>
 __device__ __forceinline__ void gemv_tok(const TileRegs<C> &R, int nch, int ng, const float *xs, const float *xsum,
                                          float *part, float *out) {
   int g = threadIdx.x % ng;
-  const int gstep = WG % ng;
+  const int gstep = NT % ng;
 #pragma unroll
   for (int k = 0; k < C; ++k) {
-    const int c = threadIdx.x + k * WG;
+    const int c = threadIdx.x + k * NT;
     if (c < nch) part[c] = (q4_chunk_dot(R.w[k], xs + g * XS) - 8.f * xsum[g]) * R.s[k];
     g += gstep;
     if (g >= ng) g -= ng;
   }
   __syncthreads();
-  for (int r = threadIdx.x; r < nch / ng; r += WG) out[r] = row_sum(part + r * ng, ng);
+  for (int r = threadIdx.x; r < nch / ng; r += NT) out[r] = row_sum(part + r * ng, ng);
   __syncthreads();
 }
 
 // A two-group column slice of a matrix with ng groups per row: chunk
 // c = 2r + j (r < rows, j < 2) is row r, group g0 + j.
-template <int C>
+template <int C, int NT>
 __device__ __forceinline__ void slice_load(const Q4Mat &W, int g0, int rows, TileRegs<C> &R) {
   const int ng = W.cols >> 5;
 #pragma unroll
   for (int k = 0; k < C; ++k) {
-    const int c = threadIdx.x + k * WG;
+    const int c = threadIdx.x + k * NT;
     if (c < 2 * rows) {
       const size_t gc = (size_t)(c >> 1) * ng + g0 + (c & 1);
       R.w[k] = W.q[gc];
@@ -344,12 +370,12 @@ __device__ __forceinline__ void slice_load(const Q4Mat &W, int g0, int rows, Til
 // out[r] = part(group g0) + part(group g0 + 1), the row_sum order of two
 // groups.  Neighbouring lanes hold the pair; every lane takes part in the
 // shuffle.
-template <int C>
+template <int C, int NT>
 __device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const float *v, const float *vsum,
                                            float *out) {
 #pragma unroll
   for (int k = 0; k < C; ++k) {
-    const int c = threadIdx.x + k * WG;
+    const int c = threadIdx.x + k * NT;
     const int j = c & 1;
     float p = 0.f;
     if (c < 2 * rows) p = (q4_chunk_dot(R.w[k], v + j * XS) - 8.f * vsum[j]) * R.s[k];
@@ -369,9 +395,17 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
   // activations first (the embedding row, or the residual and the previous
   // layer's partials), then the weight tile
   const bool gpt2 = P.arch == 1;
-  int bv[4] = {0, 0, 0, 0};
-  float sv[4] = {0.f, 0.f, 0.f, 0.f}, sfv[4] = {1.f, 1.f, 1.f, 1.f}, pv4[4] = {0.f, 0.f, 0.f, 0.f};
-  ResidPre RP;
+  constexpr int K = Gains<QT>::K;  // elements per thread (d_model <= 1024)
+  int bv[K];
+  float sv[K], sfv[K], pv4[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    bv[k] = 0;
+    sv[k] = 0.f;
+    sfv[k] = 1.f;
+    pv4[k] = 0.f;
+  }
+  ResidPre<QT> RP;
   if (li == 0) {
     // embed (infer.js:360-420): dequantised tied lm_head row; gpt2 divides by
     // scale_factors and adds the learned position.  Loads of token 0 here.
@@ -380,8 +414,8 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
     const float *sc = P.lm.s + (size_t)tok * ng;
     const int pos = min(pos0, P.max_seq - 1);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {  // D <= 1024: at most 4 elements per thread
-      const int i = threadIdx.x + k * WG;
+    for (int k = 0; k < K; ++k) {
+      const int i = threadIdx.x + k * QT;
       if (i < D) {
         bv[k] = row[i >> 1];
         sv[k] = sc[i >> 5];
@@ -392,15 +426,15 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
       }
     }
   } else {
-    resid_prefetch(P.xb, P.dpart, P.nchunk, gpt2 ? Lw.prev_mproj_b : nullptr, 0, D, RP);
+    resid_prefetch<QT>(P.xb, P.dpart, P.nchunk, gpt2 ? Lw.prev_mproj_b : nullptr, 0, D, RP);
   }
-  TileRegs<TC> R;
-  tile_load<TC>(Lw.qkv, ra, 8, rb, ng, nch, R);
-  const Gains G = load_gains(P, Lw.n1);
+  TileRegs<QC> R;
+  tile_load<QC, QT>(Lw.qkv, ra, 8, rb, ng, nch, R);
+  const Gains<QT> G = load_gains<QT>(P, Lw.n1);
   if (done) return;  // a chained decode that reached eos: loads only, no stores
   float *red = smem, *xs = red + 16, *xsum = xs + m * ng * XS, *part = xsum + m * ng, *out = part + m * nch;
   float *blk = smem + al4(16 + (size_t)m * ng * XS + m * ng + m * nch + m * 16);
-  // this thread's epilogue element (m * 16 <= WG): its RoPE table entries or
+  // this thread's epilogue element (m * 16 <= QT): its RoPE table entries or
   // bias, fetched before the staging so the epilogue does not wait for them
   const bool is_q = head < P.NH, is_k = !is_q && head < P.NH + P.NKV;
   const int e_own = threadIdx.x, t_own = e_own >> 4, r_own = e_own & 15;
@@ -425,8 +459,8 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
         const float *sc = P.lm.s + (size_t)tok * ng;
         const int pos = min(pos0 + t, P.max_seq - 1);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int i = threadIdx.x + k * WG;
+        for (int k = 0; k < K; ++k) {
+          const int i = threadIdx.x + k * QT;
           if (i < D) {
             bv[k] = row[i >> 1];
             sv[k] = sc[i >> 5];
@@ -438,8 +472,8 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
         }
       }
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = threadIdx.x + k * WG;
+      for (int k = 0; k < K; ++k) {
+        const int i = threadIdx.x + k * QT;
         if (i < D) {
           float v = (float)(((i & 1) ? (bv[k] >> 4) : (bv[k] & 15)) - 8) * sv[k];
           if (gpt2) {
@@ -453,12 +487,12 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
     }
     __syncthreads();
   } else {
-    stage_residual(P.xb, P.dpart, P.nchunk, gpt2 ? Lw.prev_mproj_b : nullptr, 0, m, D, xs,
-                   item == 0 ? P.xa : nullptr, blk, RP);
+    stage_residual<QT>(P.xb, P.dpart, P.nchunk, gpt2 ? Lw.prev_mproj_b : nullptr, 0, m, D, xs,
+                       item == 0 ? P.xa : nullptr, blk, RP);
   }
-  norm_staged(P, xs, m, G, red);
-  stage_group_sums(xs, xsum, m, ng);
-  tile_compute<TC>(R, 16, ng, nch, m, xs, xsum, threadIdx.x % ng, WG % ng, part, out, 16);
+  norm_staged<QT>(P, xs, m, G, red);
+  stage_group_sums<QT>(xs, xsum, m, ng);
+  tile_compute<QC, QT>(R, 16, ng, nch, m, xs, xsum, threadIdx.x % ng, QT % ng, part, out, 16);
   // epilogue: tile row r < 8 is head dim d = quarter*8 + r, r >= 8 is d + 32
   const int kvh = is_q ? 0 : (is_k ? head - P.NH : head - P.NH - P.NKV);
   if (e_own < m * 16) {
@@ -555,7 +589,7 @@ __device__ void phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, 
       if (k < cnt) vr[j] = *reinterpret_cast<const float4 *>(kv32 + vbase + (size_t)k * HD + 4 * d4);
     }
   }
-  if (solo) slice_load<SC>(Lw.proj, 2 * h, D, Ro);  // W_o columns of this head, behind the K/V loads
+  if (solo) slice_load<SC, AT>(Lw.proj, 2 * h, D, Ro);  // W_o columns of this head, behind the K/V loads
   __syncthreads();
   float score = -INFINITY;
   if (i < cnt) {
@@ -612,7 +646,7 @@ __device__ void phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, 
     __syncthreads();
     if (!flag[0]) return;
     __threadfence();
-    slice_load<SC>(Lw.proj, 2 * h, D, Ro);
+    slice_load<SC, AT>(Lw.proj, 2 * h, D, Ro);
   }
   __syncthreads();
   if (threadIdx.x < HD) {
@@ -646,7 +680,7 @@ __device__ void phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, 
     asum[threadIdx.x] = s;
   }
   __syncthreads();
-  slice_gemv<SC>(Ro, D, att, asum, P.opart + (size_t)(t * P.NH + h) * D);
+  slice_gemv<SC, AT>(Ro, D, att, asum, P.opart + (size_t)(t * P.NH + h) * D);
 }
 
 // Hidden units [item*UNITS, (item+1)*UNITS): gate/up (or fc) rows, the
@@ -656,12 +690,12 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item,
   const bool gpt2 = P.arch == 1;
   const int r0 = item * UNITS;
   const int nch = UNITS * ng;
-  ResidPre RP;
-  resid_prefetch(P.xa, P.opart, P.NH, gpt2 ? Lw.proj_b : nullptr, 0, D, RP);
-  TileRegs<SC> Rg, Ru, Rd;
-  tile_load<SC>(Lw.w1, r0, UNITS, 0, ng, nch, Rg);
-  if (!gpt2) tile_load<SC>(Lw.w3, r0, UNITS, 0, ng, nch, Ru);
-  const Gains G = load_gains(P, Lw.n2);
+  ResidPre<MT> RP;
+  resid_prefetch<MT>(P.xa, P.opart, P.NH, gpt2 ? Lw.proj_b : nullptr, 0, D, RP);
+  TileRegs<MC> Rg, Ru, Rd;
+  tile_load<MC, MT>(Lw.w1, r0, UNITS, 0, ng, nch, Rg);
+  if (!gpt2) tile_load<MC, MT>(Lw.w3, r0, UNITS, 0, ng, nch, Ru);
+  const Gains<MT> G = load_gains<MT>(P, Lw.n2);
   if (done) return;
   const bool own = (int)threadIdx.x < m * UNITS;
   const float fcb = gpt2 && own ? Lw.fc_b[r0 + (threadIdx.x & (UNITS - 1))] : 0.f;
@@ -669,15 +703,16 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item,
   float *uo = go + m * UNITS;
   float *hs = smem + al4(16 + (size_t)m * ng * XS + m * ng + nch + 2 * m * UNITS);
   float *hsum = hs + m * 2 * XS, *blk = hsum + al4(2 * m);
-  stage_residual(P.xa, P.opart, P.NH, gpt2 ? Lw.proj_b : nullptr, 0, m, D, xs, item == 0 ? P.xb : nullptr, blk, RP);
-  slice_load<SC>(Lw.w2, 2 * item, D, Rd);
-  norm_staged(P, xs, m, G, red);
-  stage_group_sums(xs, xsum, m, ng);
+  stage_residual<MT>(P.xa, P.opart, P.NH, gpt2 ? Lw.proj_b : nullptr, 0, m, D, xs, item == 0 ? P.xb : nullptr, blk,
+                     RP);
+  slice_load<MC, MT>(Lw.w2, 2 * item, D, Rd);
+  norm_staged<MT>(P, xs, m, G, red);
+  stage_group_sums<MT>(xs, xsum, m, ng);
   for (int t = 0; t < m; ++t) {
-    gemv_tok<SC>(Rg, nch, ng, xs + t * ng * XS, xsum + t * ng, part, go + t * UNITS);
-    if (!gpt2) gemv_tok<SC>(Ru, nch, ng, xs + t * ng * XS, xsum + t * ng, part, uo + t * UNITS);
+    gemv_tok<MC, MT>(Rg, nch, ng, xs + t * ng * XS, xsum + t * ng, part, go + t * UNITS);
+    if (!gpt2) gemv_tok<MC, MT>(Ru, nch, ng, xs + t * ng * XS, xsum + t * ng, part, uo + t * UNITS);
   }
-  for (int e = threadIdx.x; e < m * UNITS; e += WG) {
+  for (int e = threadIdx.x; e < m * UNITS; e += MT) {
     const int t = e / UNITS, r = e - t * UNITS;
     const float g = go[e];
     float h;
@@ -699,7 +734,7 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item,
   }
   __syncthreads();
   for (int t = 0; t < m; ++t)
-    slice_gemv<SC>(Rd, D, hs + t * 2 * XS, hsum + 2 * t, P.dpart + ((size_t)t * P.nchunk + item) * D);
+    slice_gemv<MC, MT>(Rd, D, hs + t * 2 * XS, hsum + 2 * t, P.dpart + ((size_t)t * P.nchunk + item) * D);
 }
 
 // Item t: the residual after the last layer, final norm -> xn[t] (only the
@@ -711,13 +746,13 @@ __device__ void phase_final(const DecParams &P, int m, int item, bool done, floa
   const int t = item;
   if (t < tb || t >= m) return;
   const int D = P.D, ng = D >> 5;
-  ResidPre RP;
-  resid_prefetch(P.xb, P.dpart, P.nchunk, P.arch == 1 ? P.last_mproj_b : nullptr, t, D, RP);
-  const Gains G = load_gains(P, P.norm_f);
+  ResidPre<FT> RP;
+  resid_prefetch<FT>(P.xb, P.dpart, P.nchunk, P.arch == 1 ? P.last_mproj_b : nullptr, t, D, RP);
+  const Gains<FT> G = load_gains<FT>(P, P.norm_f);
   float *red = smem, *xs = red + 16, *blk = xs + ng * XS;
-  stage_residual(P.xb, P.dpart, P.nchunk, P.arch == 1 ? P.last_mproj_b : nullptr, t, 1, D, xs, nullptr, blk, RP);
-  norm_staged(P, xs, 1, G, red);
-  for (int i = threadIdx.x; i < D; i += WG) P.xn[(size_t)t * D + i] = xs[skew(i)];
+  stage_residual<FT>(P.xb, P.dpart, P.nchunk, P.arch == 1 ? P.last_mproj_b : nullptr, t, 1, D, xs, nullptr, blk, RP);
+  norm_staged<FT>(P, xs, 1, G, red);
+  for (int i = threadIdx.x; i < D; i += FT) P.xn[(size_t)t * D + i] = xs[skew(i)];
 }
 
 // argmaxGpt2 (infer.js:252-287) adjustment of one logit given the banned and
@@ -922,8 +957,12 @@ __device__ __forceinline__ void run_item(const DecParams &P, const LayerW &Lw, i
 // The layer's weight pointers come in as a kernel argument, so the first
 // weight loads do not wait for a table lookup.  One symbol per phase so
 // profilers report the phases apart.
+__host__ __device__ constexpr int phase_threads(int ph) {
+  return ph == PH_QKV ? QT : ph == PH_ATTN ? AT : ph == PH_MLP ? MT : ph == PH_FINAL ? FT : LT;
+}
+
 template <int PH>
-__global__ __launch_bounds__(WG) void k_phase(DecParams P, LayerW Lw, int li, int m) {
+__global__ __launch_bounds__(phase_threads(PH)) void k_phase(DecParams P, LayerW Lw, int li, int m) {
   extern __shared__ float4 smem4[];
   const bool done = P.st->done != 0;
   run_item(P, Lw, PH, m, li, blockIdx.x, gridDim.x, done, reinterpret_cast<float *>(smem4));
@@ -1060,11 +1099,12 @@ int launch_phase(mllm_model *M, int ph, int li, int m, hipEvent_t e0 = nullptr, 
     DecParams P = M->P;
     int li_ = li, m_ = m;
     void *args[] = {&P, &Lw, &li_, &m_};
-    MLLM_HIP(hipExtLaunchKernel(reinterpret_cast<const void *>(kPhaseKernels[ph]), dim3(n), dim3(WG), args,
+    MLLM_HIP(hipExtLaunchKernel(reinterpret_cast<const void *>(kPhaseKernels[ph]), dim3(n), dim3(phase_threads(ph)), args,
                                 lds_for(M->P, m), M->stream, e0, e1, 0));
     return 0;
   }
-  hipLaunchKernelGGL(kPhaseKernels[ph], dim3(n), dim3(WG), lds_for(M->P, m), M->stream, M->P, Lw, li, m);
+  hipLaunchKernelGGL(kPhaseKernels[ph], dim3(n), dim3(phase_threads(ph)), lds_for(M->P, m), M->stream, M->P, Lw, li,
+                     m);
   MLLM_HIP(hipGetLastError());
   return 0;
 }
@@ -1096,7 +1136,7 @@ int build_chain_graph(mllm_model *M) {
     memset(&kp, 0, sizeof kp);
     kp.func = reinterpret_cast<void *>(kPhaseKernels[ph]);
     kp.gridDim = dim3(phase_items(M->P, ph, 1));
-    kp.blockDim = dim3(WG);
+    kp.blockDim = dim3(phase_threads(ph));
     kp.sharedMemBytes = (unsigned)lds;
     kp.kernelParams = args;
     hipGraphNode_t node;
@@ -1298,8 +1338,9 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
     return fail(set_error(MLLM_ERR_HIP, "layer table upload"));
   P.layers = M->d_layers;
 
-  // tiles: QKV 16 rows x ng <= TC * WG chunks (d_model <= 1024); the MLP and
-  // the head slices fit SC * WG chunks (UNITS x ng and 2 x d_model)
+  // tiles: QKV 16 rows x ng <= QC * QT chunks (d_model <= 1024); the MLP
+  // tiles and slices fit MC * MT chunks (UNITS x ng and 2 x d_model), an
+  // attention head's W_o slice SC * AT chunks
   const int ngd = D / 32;
   P.lm_rpt = lm_tile_rows(ngd);
   P.lm_tiles = (V + P.lm_rpt - 1) / P.lm_rpt;
@@ -1307,7 +1348,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   // flight at once; larger values trade workgroups for the register double
   // buffer of phase_lm.
   P.lm_grid = (P.lm_tiles + MLLM_LM_TILES_PER_WG - 1) / MLLM_LM_TILES_PER_WG;
-  if (16 * ngd > TC * WG || UNITS * ngd > SC * WG || 2 * D > SC * WG)
+  if (16 * ngd > QC * QT || UNITS * ngd > MC * MT || 2 * D > MC * MT || 2 * D > SC * AT || 16 * ngd > TC * LT)
     return fail(set_error(MLLM_ERR_UNSUPPORTED, "tiles exceed the chunk registers (d_model %d)", D));
 
   // pass size bound by LDS (160 KiB on gfx950)
