@@ -231,30 +231,46 @@ __device__ __forceinline__ void stage_group_sums(const float *xs, float *xsum, i
 // Copy m rows x[t*ldx + i] (i < n, n % 32 == 0, 16-byte aligned rows) into
 // the skewed layout.  Loads go out in batches of 4 float4 per thread before
 // any LDS store, so a batch costs one memory latency, not one per element.
+// stage_rows_load / stage_rows_store split one batch (float4 index base +
+// tid + k*NT) so a caller can issue it ahead of other loads; stage_rows
+// then copies the batches from `from` on.
+// Loads here are branch-free: an out-of-range lane reads a valid element
+// (its index clamped) and the value is ignored where it is used.  A load
+// inside a divergent branch makes the compiler wait for it at the join,
+// which would serialise loads meant to be in flight together.
 template <int NT = WG>
-__device__ __forceinline__ void stage_rows(const float *__restrict__ x, int ldx, int m, int n, float *xs) {
+__device__ __forceinline__ void stage_rows_load(const float *__restrict__ x, int ldx, int m, int n, int base,
+                                                float4 (&v)[4]) {
+  const int nq = n >> 2, total = m * nq;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int f = min(base + (int)threadIdx.x + k * NT, total - 1);
+    const int t = f / nq, q = f - t * nq;
+    v[k] = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + 4 * q);
+  }
+}
+
+template <int NT = WG>
+__device__ __forceinline__ void stage_rows_store(int m, int n, int base, const float4 (&v)[4], float *xs) {
   const int nq = n >> 2, total = m * nq, ng = n >> 5;
-  for (int base = 0; base < total; base += 4 * NT) {
-    // Every element of v is written on every path: a partially written
-    // register array is kept in scratch memory by the compiler.
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int f = base + threadIdx.x + k * NT;
+    if (f < total) {
+      const int t = f / nq, i = 4 * (f - t * nq);
+      *reinterpret_cast<float4 *>(xs + (t * ng + (i >> 5)) * XS + (i & 31)) = v[k];
+    }
+  }
+}
+
+template <int NT = WG>
+__device__ __forceinline__ void stage_rows(const float *__restrict__ x, int ldx, int m, int n, float *xs,
+                                           int from = 0) {
+  const int nq = n >> 2, total = m * nq;
+  for (int base = from; base < total; base += 4 * NT) {
     float4 v[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int f = base + threadIdx.x + k * NT;
-      v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (f < total) {
-        const int t = f / nq, q = f - t * nq;
-        v[k] = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + 4 * q);
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int f = base + threadIdx.x + k * NT;
-      if (f < total) {
-        const int t = f / nq, i = 4 * (f - t * nq);
-        *reinterpret_cast<float4 *>(xs + (t * ng + (i >> 5)) * XS + (i & 31)) = v[k];
-      }
-    }
+    stage_rows_load<NT>(x, ldx, m, n, base, v);
+    stage_rows_store<NT>(m, n, base, v, xs);
   }
 }
 
@@ -291,18 +307,17 @@ struct TileRegs {
   float s[C];
 };
 
+// Branch-free: chunks past nch load the tile's last chunk (ignored later).
 template <int C, int NT = WG>
 __device__ __forceinline__ void tile_load(const Q4Mat &W, int r0a, int na, int r0b, int ng, int nch,
                                           TileRegs<C> &R) {
   const int split = na * ng;
 #pragma unroll
   for (int j = 0; j < C; ++j) {
-    const int c = threadIdx.x + j * NT;
-    if (c < nch) {
-      const size_t gc = c < split ? (size_t)r0a * ng + c : (size_t)r0b * ng + (c - split);
-      R.w[j] = W.q[gc];
-      R.s[j] = W.s[gc];
-    }
+    const int c = min((int)threadIdx.x + j * NT, nch - 1);
+    const size_t gc = c < split ? (size_t)r0a * ng + c : (size_t)r0b * ng + (c - split);
+    R.w[j] = W.q[gc];
+    R.s[j] = W.s[gc];
   }
 }
 

@@ -68,17 +68,18 @@ constexpr int TC = 2;      // chunk registers per thread of an LM tile (TC * WG 
 // workgroups: 1024 threads put four waves on every SIMD of the CU, so each
 // step's latency is shared out instead of serialised in one wave per SIMD.
 constexpr int QT = 1024;   // QKV
-constexpr int AT = WG;     // ATTN: one thread per position of a 256-position split
+constexpr int AT = 1024;   // ATTN: four threads per key of a 256-key split
 constexpr int MT = 1024;   // MLP
 constexpr int FT = 1024;   // FINAL
 constexpr int LT = WG;     // LM, ARGMAX
 constexpr int TILE_TARGET = 320;  // chunks per LM tile (~0.15 us of VALU on one CU)
 constexpr int QSPLIT = 4;  // QKV tiles per head
 constexpr int UNITS = 64;  // hidden units per MLP item (two 32-column groups of mlp.w2)
-constexpr int SC = 8;      // chunk registers per thread of an ATTN head slice (SC * AT chunks)
+constexpr int SC = 2;      // chunk registers per thread of an ATTN head slice (SC * AT chunks)
 constexpr int MC = 2;      // chunk registers per thread of the MLP tiles and slices (MC * MT chunks)
 constexpr int QC = 1;      // chunk registers per thread of a QKV tile (QC * QT chunks)
 constexpr int PB = 8;      // partials per block of the fixed-order partial sums
+constexpr int NBMAX = 8;   // blocks per partial sum (<= PB * NBMAX partials: heads, 64-unit chunks)
 
 enum Phase { PH_QKV = 0, PH_ATTN, PH_MLP, PH_FINAL, PH_LM, PH_ARGMAX, PH_COUNT };
 
@@ -151,70 +152,62 @@ __device__ __forceinline__ Gains<NT> load_gains(const DecParams &P, const float 
   Gains<NT> G;
 #pragma unroll
   for (int k = 0; k < Gains<NT>::K; ++k) {
-    const int i = threadIdx.x + k * NT;
-    G.g[k] = 0.f;
-    G.b[k] = 0.f;
-    if (i < P.D) {
-      G.g[k] = w[i];
-      G.b[k] = P.arch == 1 ? w[P.D + i] : 0.f;
-    }
+    const int i = min((int)threadIdx.x + k * NT, P.D - 1);  // branch-free load; lanes past D unused
+    G.g[k] = w[i];
+    G.b[k] = P.arch == 1 ? w[P.D + i] : 0.f;
   }
   return G;
 }
 
-// Normalise m staged raw vectors in place (skewed layout): RMSNorm
-// (infer.js:134-143) or LayerNorm (infer.js:147-164, eps 1e-5).
+// Block-wide sum of one value per thread (NT threads, <= 16 waves) into
+// every thread: each wave reduces its 64 values with DPP, wave 0 folds the
+// wave results in order (lanes w < NT/64, DPP row sum), and the total goes
+// back through LDS.  red needs 17 floats.
 template <int NT>
-__device__ void norm_staged(const DecParams &P, float *xs, int m, const Gains<NT> &G, float *red) {
-  constexpr int K = Gains<NT>::K;
-  const int D = P.D, ng = D >> 5;
-  for (int t = 0; t < m; ++t) {
-    float *xt = xs + t * ng * XS;
-    if (P.arch == 1) {
-      float s = 0.f;
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const int i = threadIdx.x + k * NT;
-        if (i < D) s += xt[skew(i)];
-      }
-      const float mean = block_sum<NT>(s, red) / (float)D;
-      float v = 0.f;
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const int i = threadIdx.x + k * NT;
-        if (i < D) {
-          const float d = xt[skew(i)] - mean;
-          v = __builtin_fmaf(d, d, v);
-        }
-      }
-      const float inv = 1.0f / sqrtf(block_sum<NT>(v, red) / (float)D + 1e-5f);
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const int i = threadIdx.x + k * NT;
-        if (i < D) {
-          const int j = skew(i);
-          xt[j] = __builtin_fmaf((xt[j] - mean) * inv, G.g[k], G.b[k]);
-        }
-      }
-    } else {
-      float s = 0.f;
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const int i = threadIdx.x + k * NT;
-        if (i < D) s = __builtin_fmaf(xt[skew(i)], xt[skew(i)], s);
-      }
-      const float inv = 1.0f / sqrtf(block_sum<NT>(s, red) / (float)D + P.eps);
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const int i = threadIdx.x + k * NT;
-        if (i < D) {
-          const int j = skew(i);
-          xt[j] = xt[j] * inv * G.g[k];
-        }
-      }
-    }
+__device__ __forceinline__ float block_sum_fast(float v, float *red) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const float r = row16_sum(v);
+  const float w = (readlane_f(r, 0) + readlane_f(r, 16)) + (readlane_f(r, 32) + readlane_f(r, 48));
+  if (lane == 0) red[wv] = w;
+  __syncthreads();
+  if (wv == 0) {
+    const float t = row16_sum(lane < NT / 64 ? red[lane] : 0.f);
+    if (lane == 0) red[16] = t;
   }
   __syncthreads();
+  return red[16];
+}
+
+// Normalise m staged raw vectors in place (skewed layout) and write their
+// group sums xsum[t*ng + g]: RMSNorm (infer.js:134-143) or LayerNorm
+// (infer.js:147-164, eps 1e-5).  Thread i owns element i (d_model <= NT);
+// the group sums come from the normalised values of each 32-lane half-wave
+// (two DPP rows).  1/sqrt is the hardware reciprocal square root.
+template <int NT>
+__device__ void norm_staged(const DecParams &P, float *xs, float *xsum, float *red, int m, const Gains<NT> &G) {
+  static_assert(NT >= 1024, "one element per thread (d_model <= 1024)");
+  const int D = P.D, ng = D >> 5, lane = threadIdx.x & 63, i = threadIdx.x;
+  const float inv_d = 1.0f / (float)D;
+  for (int t = 0; t < m; ++t) {
+    float *xt = xs + t * ng * XS;
+    const float x = i < D ? xt[skew(i)] : 0.f;
+    float y;
+    if (P.arch == 1) {
+      const float mean = block_sum_fast<NT>(x, red) * inv_d;
+      const float d = i < D ? x - mean : 0.f;
+      const float var = block_sum_fast<NT>(d * d, red) * inv_d;
+      y = __builtin_fmaf(d * __builtin_amdgcn_rsqf(var + 1e-5f), G.g[0], G.b[0]);
+    } else {
+      const float ss = block_sum_fast<NT>(x * x, red) * inv_d;
+      y = x * __builtin_amdgcn_rsqf(ss + P.eps) * G.g[0];
+    }
+    if (i >= D) y = 0.f;
+    if (i < D) xt[skew(i)] = y;
+    const float r = row16_sum(y);
+    const float ga = readlane_f(r, 0) + readlane_f(r, 16), gb = readlane_f(r, 32) + readlane_f(r, 48);
+    if ((lane == 0 || lane == 32) && i < D) xsum[t * ng + (i >> 5)] = lane == 0 ? ga : gb;
+    __syncthreads();
+  }
 }
 
 __device__ __forceinline__ float4 add4(float4 a, float4 b) {
@@ -239,9 +232,10 @@ struct ResidPre {
   float4 xb, bb;
 };
 
+// Branch-free loads: an item or partial past the end reads partial 0 of
+// column 0 (valid memory) and resid_add leaves it out.
 template <int NT, int U>
 __device__ __forceinline__ void resid_load(const float4 *pt, int nq, int np, int nitems, int i0, float4 (&v)[U][PB]) {
-  const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int it = i0 + u * NT;
@@ -249,25 +243,30 @@ __device__ __forceinline__ void resid_load(const float4 *pt, int nq, int np, int
 #pragma unroll
     for (int k = 0; k < PB; ++k) {
       const int p = b * PB + k;
-      v[u][k] = zero;
-      if (it < nitems && p < np) v[u][k] = pt[(size_t)p * nq + c];
+      const bool ok = it < nitems && p < np;
+      v[u][k] = pt[ok ? (size_t)p * nq + c : 0];
     }
   }
 }
 
+// The loaded registers are consumed on every lane (only the store is
+// conditional): a load consumed inside a divergent branch leaves the
+// compiler unsure it has completed, and it then waits for every load in
+// flight before the register is reused.
 template <int NT, int U>
 __device__ __forceinline__ void resid_add(int nq, int np, int nitems, int i0, const float4 (&v)[U][PB], float *blk) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int it = i0 + u * NT;
-    if (it < nitems) {
-      const int b = it / nq;
-      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int b = it / nq;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int k = 0; k < PB; ++k)
-        if (b * PB + k < np) a = add4(a, v[u][k]);
-      reinterpret_cast<float4 *>(blk)[it] = a;
+    for (int k = 0; k < PB; ++k) {
+      const float4 w = v[u][k];
+      const bool use = b * PB + k < np;
+      a = add4(a, make_float4(use ? w.x : 0.f, use ? w.y : 0.f, use ? w.z : 0.f, use ? w.w : 0.f));
     }
+    if (it < nitems) reinterpret_cast<float4 *>(blk)[it] = a;
   }
 }
 
@@ -275,13 +274,12 @@ template <int NT>
 __device__ __forceinline__ void resid_prefetch(const float *base, const float *parts, int np, const float *bias, int t0,
                                                int D, ResidPre<NT> &R) {
   const int nq = D >> 2, nb = (np + PB - 1) / PB;
-  const int q = threadIdx.x;  // D <= 1024: one float4 column per thread
-  R.xb = make_float4(0.f, 0.f, 0.f, 0.f);
-  R.bb = R.xb;
-  if (q < nq) {
-    R.xb = reinterpret_cast<const float4 *>(base + (size_t)t0 * D)[q];
-    if (bias) R.bb = reinterpret_cast<const float4 *>(bias)[q];
-  }
+  const int q = min((int)threadIdx.x, nq - 1);  // D <= 1024: one float4 column per thread (branch-free)
+  R.xb = reinterpret_cast<const float4 *>(base + (size_t)t0 * D)[q];
+  // unconditional load (of base itself when there is no bias): a load in a
+  // branch leaves the compiler unsure whether it is pending, and it then
+  // waits for every load in flight at the next reuse of its register
+  R.bb = reinterpret_cast<const float4 *>(bias ? bias : base)[q];
   resid_load<NT, ResidPre<NT>::U>(reinterpret_cast<const float4 *>(parts + (size_t)t0 * np * D), nq, np, nq * nb,
                                   threadIdx.x, R.v);
 }
@@ -300,13 +298,19 @@ __device__ __forceinline__ void resid_row(const float *parts, int np, int t, int
     resid_add<NT, U>(nq, np, nitems, i0, v, blk);
   }
   __syncthreads();
-  const int q = threadIdx.x;
-  if (q < nq) {
-    const float4 *b4 = reinterpret_cast<const float4 *>(blk);
-    float4 s = b4[q];
-    for (int b = 1; b < nb; ++b) s = add4(s, b4[b * nq + q]);
-    if (has_bias) s = add4(s, bb);
-    const float4 v = add4(xb, s);
+  // every lane combines (column clamped), only the stores are conditional:
+  // xb and bb are loads and are consumed outside any branch
+  const int q = min((int)threadIdx.x, nq - 1);
+  const float4 *b4 = reinterpret_cast<const float4 *>(blk);
+  float4 s = b4[q];
+  // fixed trip count: a runtime loop here made the compiler wait for every
+  // load in flight (the weights) before entering it
+#pragma unroll
+  for (int b = 1; b < NBMAX; ++b)
+    if (b < nb) s = add4(s, b4[b * nq + q]);
+  if (has_bias) s = add4(s, bb);
+  const float4 v = add4(xb, s);
+  if ((int)threadIdx.x < nq) {
     const int i = 4 * q;
     *reinterpret_cast<float4 *>(xs + (tt * ng + (i >> 5)) * XS + (i & 31)) = v;
     if (out) reinterpret_cast<float4 *>(out + (size_t)t * D)[q] = v;
@@ -324,8 +328,7 @@ __device__ void stage_residual(const float *base, const float *parts, int np, co
   resid_row<NT>(parts, np, t0, 0, D, R.xb, bb, bias != nullptr, true, xs, out, blk);
   for (int tt = 1; tt < m; ++tt) {
     const int t = t0 + tt;
-    float4 xb = make_float4(0.f, 0.f, 0.f, 0.f);
-    if ((int)threadIdx.x < nq) xb = reinterpret_cast<const float4 *>(base + (size_t)t * D)[threadIdx.x];
+    const float4 xb = reinterpret_cast<const float4 *>(base + (size_t)t * D)[min((int)threadIdx.x, nq - 1)];
     resid_row<NT>(parts, np, t, tt, D, xb, bb, bias != nullptr, false, xs, out, blk);
   }
 }
@@ -357,12 +360,10 @@ __device__ __forceinline__ void slice_load(const Q4Mat &W, int g0, int rows, Til
   const int ng = W.cols >> 5;
 #pragma unroll
   for (int k = 0; k < C; ++k) {
-    const int c = threadIdx.x + k * NT;
-    if (c < 2 * rows) {
-      const size_t gc = (size_t)(c >> 1) * ng + g0 + (c & 1);
-      R.w[k] = W.q[gc];
-      R.s[k] = W.s[gc];
-    }
+    const int c = min((int)threadIdx.x + k * NT, 2 * rows - 1);  // branch-free; extra lanes unused
+    const size_t gc = (size_t)(c >> 1) * ng + g0 + (c & 1);
+    R.w[k] = W.q[gc];
+    R.s[k] = W.s[gc];
   }
 }
 
@@ -415,40 +416,37 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
     const int pos = min(pos0, P.max_seq - 1);
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      const int i = threadIdx.x + k * QT;
-      if (i < D) {
-        bv[k] = row[i >> 1];
-        sv[k] = sc[i >> 5];
-        if (gpt2) {
-          sfv[k] = P.sf ? P.sf[i] : 1.f;
-          pv4[k] = P.wpe[(size_t)pos * D + i];
-        }
+      const int i = min((int)threadIdx.x + k * QT, D - 1);  // branch-free; lanes past D unused
+      bv[k] = row[i >> 1];
+      sv[k] = sc[i >> 5];
+      if (gpt2) {
+        sfv[k] = P.sf ? P.sf[i] : 1.f;
+        pv4[k] = P.wpe[(size_t)pos * D + i];
       }
     }
   } else {
     resid_prefetch<QT>(P.xb, P.dpart, P.nchunk, gpt2 ? Lw.prev_mproj_b : nullptr, 0, D, RP);
   }
+  // loads retire in issue order: everything the prologue reads goes out
+  // before the weight tile, so the prologue never waits for the weights
+  const Gains<QT> G = load_gains<QT>(P, Lw.n1);
   TileRegs<QC> R;
   tile_load<QC, QT>(Lw.qkv, ra, 8, rb, ng, nch, R);
-  const Gains<QT> G = load_gains<QT>(P, Lw.n1);
   if (done) return;  // a chained decode that reached eos: loads only, no stores
-  float *red = smem, *xs = red + 16, *xsum = xs + m * ng * XS, *part = xsum + m * ng, *out = part + m * nch;
-  float *blk = smem + al4(16 + (size_t)m * ng * XS + m * ng + m * nch + m * 16);
+  float *red = smem, *xs = red + 20, *xsum = xs + m * ng * XS, *part = xsum + m * ng, *out = part + m * nch;
+  float *blk = smem + al4(20 + (size_t)m * ng * XS + m * ng + m * nch + m * 16);
   // this thread's epilogue element (m * 16 <= QT): its RoPE table entries or
   // bias, fetched before the staging so the epilogue does not wait for them
   const bool is_q = head < P.NH, is_k = !is_q && head < P.NH + P.NKV;
   const int e_own = threadIdx.x, t_own = e_own >> 4, r_own = e_own & 15;
   const int d_own = quarter * 8 + (r_own & 7) + (r_own >> 3) * 32;
-  float c_own = 0.f, s_own = 0.f, b_own = 0.f;
-  if (e_own < m * 16) {
-    if (gpt2) {
-      b_own = Lw.qkv_b[head * HD + d_own];
-    } else if (is_q || is_k) {
-      const size_t ri = (size_t)(pos0 + t_own) * HD + d_own;
-      c_own = P.rope_cos[ri];
-      s_own = P.rope_sin[ri];
-    }
-  }
+  // unconditional loads (gpt2: the bias twice; llama: the RoPE tables, also
+  // for V rows that do not use them; positions clamped for lanes past m * 16)
+  const size_t ri = (size_t)min(pos0 + t_own, P.max_seq - 1) * HD + d_own;
+  const float *pc = gpt2 ? Lw.qkv_b + head * HD + d_own : P.rope_cos + ri;
+  const float *ps = gpt2 ? pc : P.rope_sin + ri;
+  const float c_own = *pc, s_own = *ps;
+  const float b_own = c_own;
   if (li == 0) {
     // item 0 writes xa
     for (int t = 0; t < m; ++t) {
@@ -460,14 +458,12 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
         const int pos = min(pos0 + t, P.max_seq - 1);
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-          const int i = threadIdx.x + k * QT;
-          if (i < D) {
-            bv[k] = row[i >> 1];
-            sv[k] = sc[i >> 5];
-            if (gpt2) {
-              sfv[k] = P.sf ? P.sf[i] : 1.f;
-              pv4[k] = P.wpe[(size_t)pos * D + i];
-            }
+          const int i = min((int)threadIdx.x + k * QT, D - 1);
+          bv[k] = row[i >> 1];
+          sv[k] = sc[i >> 5];
+          if (gpt2) {
+            sfv[k] = P.sf ? P.sf[i] : 1.f;
+            pv4[k] = P.wpe[(size_t)pos * D + i];
           }
         }
       }
@@ -490,8 +486,7 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
     stage_residual<QT>(P.xb, P.dpart, P.nchunk, gpt2 ? Lw.prev_mproj_b : nullptr, 0, m, D, xs,
                        item == 0 ? P.xa : nullptr, blk, RP);
   }
-  norm_staged<QT>(P, xs, m, G, red);
-  stage_group_sums<QT>(xs, xsum, m, ng);
+  norm_staged<QT>(P, xs, xsum, red, m, G);
   tile_compute<QC, QT>(R, 16, ng, nch, m, xs, xsum, threadIdx.x % ng, QT % ng, part, out, 16);
   // epilogue: tile row r < 8 is head dim d = quarter*8 + r, r >= 8 is d + 32
   const int kvh = is_q ? 0 : (is_k ? head - P.NH : head - P.NH - P.NKV);
@@ -517,12 +512,13 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
   }
 }
 
-// One (token, split, head) item.  Every load of the item (q, the K rows, the
-// V rows) is issued at once: thread i owns key i of the split; thread
-// (kg, d4) owns V[kg + 16j][4*d4 .. 4*d4+3] for j < 16.  The last split of
-// (token, head) to finish -- counted in P.cnt; a single split is its own
-// last -- merges the splits (flash-decoding merge in split order) and writes
-// the head's partial of the attention output projection to P.opart.
+// One (token, split, head) item, 1024 threads.  Every load of the item (q,
+// the K rows, the V rows) is issued at once: the score of key p of the split
+// is formed by the four lanes 4p .. 4p+3 (16 dimensions each, joined with
+// DPP); thread (kg, d4) owns V[kg + 64j][4*d4 .. 4*d4+3] for j < 4.  The last
+// split of (token, head) to finish -- counted in P.cnt; a single split is its
+// own last -- merges the splits (flash-decoding merge in split order) and
+// writes the head's partial of the attention output projection to P.opart.
 __device__ void phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, int item, bool done, float *smem) {
   const int per_tok = P.NH * P.nsplit_max;
   const int t = item / per_tok;
@@ -538,26 +534,30 @@ __device__ void phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, 
   TileRegs<SC> Ro;
   const int cnt = min(ACH, pos + 1 - s0);
   const int kvh = h / (P.NH / P.NKV);
-  float *qs = smem;          // 64
-  float *es = qs + HD;       // 256
-  float *pv = es + ACH;      // 16 x 64
-  float *red = pv + 16 * HD; // 16
-  float *own = red + 16;     // 64: this split's P.V
-  float *att = own + HD;     // 2 x XS: merged head output, skewed
+  float *qs = smem;            // 64
+  float *es = qs + HD;         // 256: exp weights
+  float *sc = es + ACH;        // 256: scores
+  float *pv = sc + ACH;        // 64 x 64
+  float *pv2 = pv + 64 * HD;   // 4 x 64
+  float *red = pv2 + 4 * HD;   // 16
+  float *own = red + 16;       // 64: this split's P.V
+  float *att = own + HD;       // 2 x XS: merged head output, skewed
   float *asum = att + 2 * XS;  // 2
   int *flag = reinterpret_cast<int *>(asum + 2);
   const size_t kbase = kv_index(P, li, 0, kvh, s0), vbase = kv_index(P, li, 1, kvh, s0);
-  const int i = threadIdx.x;
+  const int kp = threadIdx.x >> 2, ku = threadIdx.x & 3;  // key of the split, quarter of its dimensions
   const int d4 = threadIdx.x & 15, kg = threadIdx.x >> 4;
-  float4 kr[HD / 4];
-  float4 vr[16];
+  float4 kr[4];
+  float4 vr[4];
   if (threadIdx.x < HD) qs[threadIdx.x] = P.q[(size_t)t * P.NH * HD + h * HD + threadIdx.x];
+  // K/V loads only for keys below cnt (at short contexts most lanes have
+  // none; duplicated clamped loads measured slower here)
   if (P.kv_fp16) {
     const __half *kvh16 = reinterpret_cast<const __half *>(P.kv);
-    if (i < cnt) {
-      const uint4 *row = reinterpret_cast<const uint4 *>(kvh16 + kbase + (size_t)i * HD);
+    if (kp < cnt) {
+      const uint4 *row = reinterpret_cast<const uint4 *>(kvh16 + kbase + (size_t)kp * HD + 16 * ku);
 #pragma unroll
-      for (int j = 0; j < HD / 8; ++j) {
+      for (int j = 0; j < 2; ++j) {
         const uint4 u = row[j];
         const __half2 *hp = reinterpret_cast<const __half2 *>(&u);
         const float2 f0 = __half22float2(hp[0]), f1 = __half22float2(hp[1]);
@@ -567,8 +567,8 @@ __device__ void phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, 
       }
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int k = kg + 16 * j;
+    for (int j = 0; j < 4; ++j) {
+      const int k = kg + 64 * j;
       if (k < cnt) {
         const uint2 u = *reinterpret_cast<const uint2 *>(kvh16 + vbase + (size_t)k * HD + 4 * d4);
         const __half2 *hp = reinterpret_cast<const __half2 *>(&u);
@@ -578,53 +578,76 @@ __device__ void phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, 
     }
   } else {
     const float *kv32 = reinterpret_cast<const float *>(P.kv);
-    if (i < cnt) {
-      const float4 *row = reinterpret_cast<const float4 *>(kv32 + kbase + (size_t)i * HD);
+    if (kp < cnt) {
+      const float4 *row = reinterpret_cast<const float4 *>(kv32 + kbase + (size_t)kp * HD + 16 * ku);
 #pragma unroll
-      for (int j = 0; j < HD / 4; ++j) kr[j] = row[j];
+      for (int j = 0; j < 4; ++j) kr[j] = row[j];
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int k = kg + 16 * j;
+    for (int j = 0; j < 4; ++j) {
+      const int k = kg + 64 * j;
       if (k < cnt) vr[j] = *reinterpret_cast<const float4 *>(kv32 + vbase + (size_t)k * HD + 4 * d4);
     }
   }
   if (solo) slice_load<SC, AT>(Lw.proj, 2 * h, D, Ro);  // W_o columns of this head, behind the K/V loads
   __syncthreads();
-  float score = -INFINITY;
-  if (i < cnt) {
+  float part = 0.f;
+  if (kp < cnt) {
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    const float *qq = qs + 16 * ku;
 #pragma unroll
-    for (int j = 0; j < HD / 4; ++j) {
-      a0 = __builtin_fmaf(qs[4 * j + 0], kr[j].x, a0);
-      a1 = __builtin_fmaf(qs[4 * j + 1], kr[j].y, a1);
-      a2 = __builtin_fmaf(qs[4 * j + 2], kr[j].z, a2);
-      a3 = __builtin_fmaf(qs[4 * j + 3], kr[j].w, a3);
+    for (int j = 0; j < 4; ++j) {
+      a0 = __builtin_fmaf(qq[4 * j + 0], kr[j].x, a0);
+      a1 = __builtin_fmaf(qq[4 * j + 1], kr[j].y, a1);
+      a2 = __builtin_fmaf(qq[4 * j + 2], kr[j].z, a2);
+      a3 = __builtin_fmaf(qq[4 * j + 3], kr[j].w, a3);
     }
-    score = ((a0 + a1) + (a2 + a3)) * P.attn_scale;
+    part = (a0 + a1) + (a2 + a3);
   }
-  const float mx = block_max(score, red);
-  es[i] = i < cnt ? expf(score - mx) : 0.f;
-  const float l = block_sum(es[i], red);  // contains the barrier that publishes es[]
+  // the four quarters: (q0 + q1) + (q2 + q3) in every lane of the quad
+  part = part + dpp_f<0xB1>(part);
+  part = part + dpp_f<0x4E>(part);
+  const float score = kp < cnt ? part * P.attn_scale : -INFINITY;
+  // softmax statistics, reduced by every wave itself (no cross-wave
+  // exchange): the scores, then the weights, go through LDS once each
+  const int lane = threadIdx.x & 63;
+  if (ku == 0) sc[kp] = score;
+  __syncthreads();
+  float ml = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ml = fmaxf(ml, sc[lane + 64 * j]);  // -inf past cnt
+  const float mx = wave_max(ml);
+  const float e = kp < cnt ? expf(score - mx) : 0.f;
+  if (ku == 0) es[kp] = e;
+  __syncthreads();
+  float ll = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ll += es[lane + 64 * j];
+  const float l = wave_sum(ll);
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int k = kg + 16 * j;
+  for (int j = 0; j < 4; ++j) {
+    const int k = kg + 64 * j;
     if (k < cnt) {
-      const float e = es[k];
-      acc.x = __builtin_fmaf(e, vr[j].x, acc.x);
-      acc.y = __builtin_fmaf(e, vr[j].y, acc.y);
-      acc.z = __builtin_fmaf(e, vr[j].z, acc.z);
-      acc.w = __builtin_fmaf(e, vr[j].w, acc.w);
+      const float ek = es[k];
+      acc.x = __builtin_fmaf(ek, vr[j].x, acc.x);
+      acc.y = __builtin_fmaf(ek, vr[j].y, acc.y);
+      acc.z = __builtin_fmaf(ek, vr[j].z, acc.z);
+      acc.w = __builtin_fmaf(ek, vr[j].w, acc.w);
     }
   }
   *reinterpret_cast<float4 *>(pv + kg * HD + 4 * d4) = acc;
   __syncthreads();
-  if (threadIdx.x < HD) {
+  if (threadIdx.x < 4 * HD) {  // key groups 16q .. 16q+15 of dimension d
+    const int d = threadIdx.x & (HD - 1), q = threadIdx.x >> 6;
     float a = 0.f;
-    for (int g = 0; g < 16; ++g) a += pv[g * HD + threadIdx.x];
-    own[threadIdx.x] = a;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) a += pv[(16 * q + g) * HD + d];
+    pv2[q * HD + d] = a;
   }
+  __syncthreads();
+  if (threadIdx.x < HD) own[threadIdx.x] = (pv2[threadIdx.x] + pv2[HD + threadIdx.x]) +
+                                           (pv2[2 * HD + threadIdx.x] + pv2[3 * HD + threadIdx.x]);
   const float *parts = P.attp + (size_t)(t * P.NH + h) * P.nsplit_max * APS;
   if (!solo) {
     // publish this split, then count it; the last one merges
@@ -639,8 +662,8 @@ __device__ void phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, 
     __syncthreads();
     if (threadIdx.x == 0) {
       unsigned *c = P.cnt + t * P.NH + h;
-      const unsigned done = atomicAdd(c, 1u);
-      flag[0] = done == (unsigned)(ns - 1);
+      const unsigned arrived = atomicAdd(c, 1u);
+      flag[0] = arrived == (unsigned)(ns - 1);
       if (flag[0]) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
@@ -692,22 +715,21 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item,
   const int nch = UNITS * ng;
   ResidPre<MT> RP;
   resid_prefetch<MT>(P.xa, P.opart, P.NH, gpt2 ? Lw.proj_b : nullptr, 0, D, RP);
+  const Gains<MT> G = load_gains<MT>(P, Lw.n2);  // before the weights (loads retire in issue order)
   TileRegs<MC> Rg, Ru, Rd;
   tile_load<MC, MT>(Lw.w1, r0, UNITS, 0, ng, nch, Rg);
   if (!gpt2) tile_load<MC, MT>(Lw.w3, r0, UNITS, 0, ng, nch, Ru);
-  const Gains<MT> G = load_gains<MT>(P, Lw.n2);
   if (done) return;
-  const bool own = (int)threadIdx.x < m * UNITS;
-  const float fcb = gpt2 && own ? Lw.fc_b[r0 + (threadIdx.x & (UNITS - 1))] : 0.f;
-  float *red = smem, *xs = red + 16, *xsum = xs + m * ng * XS, *part = xsum + m * ng, *go = part + nch;
+  // unconditional load (llama reads its norm gains instead and ignores it)
+  const float fcb = (gpt2 ? Lw.fc_b + r0 : Lw.n2)[threadIdx.x & (UNITS - 1)];
+  float *red = smem, *xs = red + 20, *xsum = xs + m * ng * XS, *part = xsum + m * ng, *go = part + nch;
   float *uo = go + m * UNITS;
-  float *hs = smem + al4(16 + (size_t)m * ng * XS + m * ng + nch + 2 * m * UNITS);
+  float *hs = smem + al4(20 + (size_t)m * ng * XS + m * ng + nch + 2 * m * UNITS);
   float *hsum = hs + m * 2 * XS, *blk = hsum + al4(2 * m);
   stage_residual<MT>(P.xa, P.opart, P.NH, gpt2 ? Lw.proj_b : nullptr, 0, m, D, xs, item == 0 ? P.xb : nullptr, blk,
                      RP);
   slice_load<MC, MT>(Lw.w2, 2 * item, D, Rd);
-  norm_staged<MT>(P, xs, m, G, red);
-  stage_group_sums<MT>(xs, xsum, m, ng);
+  norm_staged<MT>(P, xs, xsum, red, m, G);
   for (int t = 0; t < m; ++t) {
     gemv_tok<MC, MT>(Rg, nch, ng, xs + t * ng * XS, xsum + t * ng, part, go + t * UNITS);
     if (!gpt2) gemv_tok<MC, MT>(Ru, nch, ng, xs + t * ng * XS, xsum + t * ng, part, uo + t * UNITS);
@@ -749,9 +771,10 @@ __device__ void phase_final(const DecParams &P, int m, int item, bool done, floa
   ResidPre<FT> RP;
   resid_prefetch<FT>(P.xb, P.dpart, P.nchunk, P.arch == 1 ? P.last_mproj_b : nullptr, t, D, RP);
   const Gains<FT> G = load_gains<FT>(P, P.norm_f);
-  float *red = smem, *xs = red + 16, *blk = xs + ng * XS;
+  // red: 20 floats; xsum: ng <= 32 (unused by the lm_head)
+  float *red = smem, *xsum = smem + 20, *xs = smem + 52, *blk = xs + ng * XS;
   stage_residual<FT>(P.xb, P.dpart, P.nchunk, P.arch == 1 ? P.last_mproj_b : nullptr, t, 1, D, xs, nullptr, blk, RP);
-  norm_staged<FT>(P, xs, 1, G, red);
+  norm_staged<FT>(P, xs, xsum, red, 1, G);
   for (int i = threadIdx.x; i < D; i += FT) P.xn[(size_t)t * D + i] = xs[skew(i)];
 }
 
@@ -817,15 +840,18 @@ __device__ __forceinline__ void lm_load(const DecParams &P, int tile, TileRegs<T
 // turn, each with constant indices so both stay in VGPRs).
 __device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, bool done, float *smem) {
   if (wg >= P.lm_tiles) return;
-  TileRegs<TC> Ra, Rb;
-  int tile = wg;
-  lm_load(P, tile, Ra);  // independent of the pass state: in flight before it arrives
   const PassState &S = *P.st;
   const int lm_rows = S.lm_rows;
   if (lm_rows == 0 || done) return;
   const int tb = lm_rows == 1 ? m_all - 1 : 0;
   const int m = m_all - tb;
   const int D = P.D, ng = D >> 5, rpt = P.lm_rpt;
+  // the normed rows first, then the weights (loads retire in issue order)
+  float4 xv[4];
+  stage_rows_load<LT>(P.xn + (size_t)tb * D, D, m, D, 0, xv);
+  TileRegs<TC> Ra, Rb;
+  int tile = wg;
+  lm_load(P, tile, Ra);
   LmLds s;
   s.xs = smem;
   s.xsum = s.xs + m * ng * XS;
@@ -847,7 +873,8 @@ __device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, bool do
     s.lists[0] = nban;
     s.lists[1] = nrec;
   }
-  stage_rows(P.xn + (size_t)tb * D, D, m, D, s.xs);
+  stage_rows_store<LT>(m, D, 0, xv, s.xs);
+  stage_rows<LT>(P.xn + (size_t)tb * D, D, m, D, s.xs, 4 * LT);
   __syncthreads();
   stage_group_sums(s.xs, s.xsum, m, ng);
   const int nban = penal ? s.lists[0] : 0, nrec = penal ? s.lists[1] : 0;
@@ -961,16 +988,22 @@ __host__ __device__ constexpr int phase_threads(int ph) {
   return ph == PH_QKV ? QT : ph == PH_ATTN ? AT : ph == PH_MLP ? MT : ph == PH_FINAL ? FT : LT;
 }
 
-template <int PH>
+// ONE = 1: the single-token instance (m is the constant 1, so the token
+// loops vanish); the decode step runs it.  ONE = 0 takes m from the argument.
+// Both run the same per-token code.
+template <int PH, int ONE>
 __global__ __launch_bounds__(phase_threads(PH)) void k_phase(DecParams P, LayerW Lw, int li, int m) {
   extern __shared__ float4 smem4[];
   const bool done = P.st->done != 0;
-  run_item(P, Lw, PH, m, li, blockIdx.x, gridDim.x, done, reinterpret_cast<float *>(smem4));
+  run_item(P, Lw, PH, ONE ? 1 : m, li, blockIdx.x, gridDim.x, done, reinterpret_cast<float *>(smem4));
 }
 
 using PhaseKernel = void (*)(DecParams, LayerW, int, int);
-static const PhaseKernel kPhaseKernels[PH_COUNT] = {k_phase<PH_QKV>,   k_phase<PH_ATTN>, k_phase<PH_MLP>,
-                                                    k_phase<PH_FINAL>, k_phase<PH_LM>,   k_phase<PH_ARGMAX>};
+static const PhaseKernel kPhaseKernels[2][PH_COUNT] = {
+    {k_phase<PH_QKV, 0>, k_phase<PH_ATTN, 0>, k_phase<PH_MLP, 0>, k_phase<PH_FINAL, 0>, k_phase<PH_LM, 0>,
+     k_phase<PH_ARGMAX, 0>},
+    {k_phase<PH_QKV, 1>, k_phase<PH_ATTN, 1>, k_phase<PH_MLP, 1>, k_phase<PH_FINAL, 1>, k_phase<PH_LM, 1>,
+     k_phase<PH_ARGMAX, 1>}};
 static const char *const kPhaseNames[PH_COUNT] = {"QKV", "ATTN", "MLP", "FINAL", "LM", "ARGMAX"};
 
 }  // namespace mllm
@@ -1031,12 +1064,12 @@ size_t lds_floats(const DecParams &P, int ph, int m) {
   const size_t ngd = P.D / 32, D = P.D;
   const size_t blk_o = (size_t)((P.NH + PB - 1) / PB) * D, blk_d = (size_t)((P.nchunk + PB - 1) / PB) * D;
   switch (ph) {
-  case PH_QKV: return al4(16 + m * ngd * XS + m * ngd + m * 16 * ngd + m * 16) + blk_d;
-  case PH_ATTN: return HD + ACH + 16 * HD + 16 + HD + 2 * XS + 2 + 4;
+  case PH_QKV: return al4(20 + m * ngd * XS + m * ngd + m * 16 * ngd + m * 16) + blk_d;
+  case PH_ATTN: return HD + 2 * ACH + 64 * HD + 4 * HD + 16 + HD + 2 * XS + 2 + 4;
   case PH_MLP:
-    return al4(16 + m * ngd * XS + m * ngd + UNITS * ngd + 2 * (size_t)m * UNITS) + (size_t)m * 2 * XS + al4(2 * m) +
+    return al4(20 + m * ngd * XS + m * ngd + UNITS * ngd + 2 * (size_t)m * UNITS) + (size_t)m * 2 * XS + al4(2 * m) +
            blk_o;
-  case PH_FINAL: return 16 + ngd * XS + blk_d;
+  case PH_FINAL: return 52 + ngd * XS + blk_d;
   case PH_LM: return m * ngd * XS + m * ngd + (size_t)m * TC * WG + (size_t)m * P.lm_rpt + 34 + P.max_seq;
   default: return 16;
   }
@@ -1099,12 +1132,13 @@ int launch_phase(mllm_model *M, int ph, int li, int m, hipEvent_t e0 = nullptr, 
     DecParams P = M->P;
     int li_ = li, m_ = m;
     void *args[] = {&P, &Lw, &li_, &m_};
-    MLLM_HIP(hipExtLaunchKernel(reinterpret_cast<const void *>(kPhaseKernels[ph]), dim3(n), dim3(phase_threads(ph)), args,
+    MLLM_HIP(hipExtLaunchKernel(reinterpret_cast<const void *>(kPhaseKernels[m == 1][ph]), dim3(n),
+                                dim3(phase_threads(ph)), args,
                                 lds_for(M->P, m), M->stream, e0, e1, 0));
     return 0;
   }
-  hipLaunchKernelGGL(kPhaseKernels[ph], dim3(n), dim3(phase_threads(ph)), lds_for(M->P, m), M->stream, M->P, Lw, li,
-                     m);
+  hipLaunchKernelGGL(kPhaseKernels[m == 1][ph], dim3(n), dim3(phase_threads(ph)), lds_for(M->P, m), M->stream, M->P,
+                     Lw, li, m);
   MLLM_HIP(hipGetLastError());
   return 0;
 }
@@ -1134,7 +1168,7 @@ int build_chain_graph(mllm_model *M) {
     void *args[] = {&M->P, &Lw, &li, &m};
     hipKernelNodeParams kp;
     memset(&kp, 0, sizeof kp);
-    kp.func = reinterpret_cast<void *>(kPhaseKernels[ph]);
+    kp.func = reinterpret_cast<void *>(kPhaseKernels[1][ph]);
     kp.gridDim = dim3(phase_items(M->P, ph, 1));
     kp.blockDim = dim3(phase_threads(ph));
     kp.sharedMemBytes = (unsigned)lds;
@@ -1234,8 +1268,10 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
     return set_error(MLLM_ERR_UNSUPPORTED, "head_dim %d unsupported (64 only)", c.d_model / c.n_heads);
   if (c.d_model % 32 || c.d_model > 1024)
     return set_error(MLLM_ERR_UNSUPPORTED, "d_model %d unsupported (a multiple of 32, <= 1024)", c.d_model);
-  if (c.d_ff % UNITS || c.d_ff > 16384)
-    return set_error(MLLM_ERR_UNSUPPORTED, "d_ff %d unsupported (a multiple of %d, <= 16384)", c.d_ff, UNITS);
+  if (c.d_ff % UNITS || c.d_ff > UNITS * PB * NBMAX)
+    return set_error(MLLM_ERR_UNSUPPORTED, "d_ff %d unsupported (a multiple of %d, <= %d)", c.d_ff, UNITS,
+                     UNITS * PB * NBMAX);
+  if (c.n_heads > PB * NBMAX) return set_error(MLLM_ERR_UNSUPPORTED, "n_heads %d > %d", c.n_heads, PB * NBMAX);
   if (c.arch == 1 && c.n_kv_heads != c.n_heads) return set_error(MLLM_ERR_INVALID, "gpt2 needs n_kv_heads == n_heads");
   if (c.arch == 0 && (int)floor(HD * c.rope_pct) != HD)
     return set_error(MLLM_ERR_UNSUPPORTED, "partial rotary (ropePct %g) unsupported", c.rope_pct);
@@ -1390,9 +1426,10 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
 
   if (M->lds_max > 64 * 1024) {
     bool ok = true;
-    for (int ph = 0; ph < PH_COUNT; ++ph)
-      ok = ok && hipFuncSetAttribute(reinterpret_cast<const void *>(kPhaseKernels[ph]),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)M->lds_max) == hipSuccess;
+    for (int one = 0; one < 2; ++one)
+      for (int ph = 0; ph < PH_COUNT; ++ph)
+        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void *>(kPhaseKernels[one][ph]),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)M->lds_max) == hipSuccess;
     if (!ok) return fail(set_error(MLLM_ERR_HIP, "LDS attribute"));
   }
   *out = M;
