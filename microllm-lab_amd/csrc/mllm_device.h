@@ -69,6 +69,83 @@ __device__ __forceinline__ float q4_chunk_dot(const uint4 w, const float *__rest
   return (a0 + a2) + (a1 + a3) * 0.0625f;
 }
 
+// Two chunks of the same group (e.g. the gate and up rows of one hidden
+// unit) against one read of the 32 staged activations: each result has the
+// arithmetic of q4_chunk_dot.
+__device__ __forceinline__ void q4_chunk_dot2(const uint4 wa, const uint4 wb, const float *__restrict__ xg, float &da,
+                                              float &db) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
+  const uint32_t dwa[4] = {wa.x, wa.y, wa.z, wa.w}, dwb[4] = {wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float4 xa = *reinterpret_cast<const float4 *>(xg + 8 * j);
+    const float4 xb = *reinterpret_cast<const float4 *>(xg + 8 * j + 4);
+    const uint32_t la = and_opaque(dwa[j], 0x0F0F0F0Fu), ha = and_opaque(dwa[j], 0xF0F0F0F0u);
+    const uint32_t lb = and_opaque(dwb[j], 0x0F0F0F0Fu), hb = and_opaque(dwb[j], 0xF0F0F0F0u);
+    a0 = __builtin_fmaf(ubyte(la, 0), xa.x, a0);
+    a1 = __builtin_fmaf(ubyte(ha, 0), xa.y, a1);
+    a2 = __builtin_fmaf(ubyte(la, 1), xa.z, a2);
+    a3 = __builtin_fmaf(ubyte(ha, 1), xa.w, a3);
+    a0 = __builtin_fmaf(ubyte(la, 2), xb.x, a0);
+    a1 = __builtin_fmaf(ubyte(ha, 2), xb.y, a1);
+    a2 = __builtin_fmaf(ubyte(la, 3), xb.z, a2);
+    a3 = __builtin_fmaf(ubyte(ha, 3), xb.w, a3);
+    b0 = __builtin_fmaf(ubyte(lb, 0), xa.x, b0);
+    b1 = __builtin_fmaf(ubyte(hb, 0), xa.y, b1);
+    b2 = __builtin_fmaf(ubyte(lb, 1), xa.z, b2);
+    b3 = __builtin_fmaf(ubyte(hb, 1), xa.w, b3);
+    b0 = __builtin_fmaf(ubyte(lb, 2), xb.x, b0);
+    b1 = __builtin_fmaf(ubyte(hb, 2), xb.y, b1);
+    b2 = __builtin_fmaf(ubyte(lb, 3), xb.z, b2);
+    b3 = __builtin_fmaf(ubyte(hb, 3), xb.w, b3);
+  }
+  da = (a0 + a2) + (a1 + a3) * 0.0625f;
+  db = (b0 + b2) + (b1 + b3) * 0.0625f;
+}
+
+// q4_chunk_dot2 with the group's 32 activations in registers.
+__device__ __forceinline__ void q4_chunk_dot2_reg(const uint4 wa, const uint4 wb, const float (&x)[32], float &da,
+                                                  float &db) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
+  const uint32_t dwa[4] = {wa.x, wa.y, wa.z, wa.w}, dwb[4] = {wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float *xg = x + 8 * j;
+    const uint32_t la = and_opaque(dwa[j], 0x0F0F0F0Fu), ha = and_opaque(dwa[j], 0xF0F0F0F0u);
+    const uint32_t lb = and_opaque(dwb[j], 0x0F0F0F0Fu), hb = and_opaque(dwb[j], 0xF0F0F0F0u);
+    a0 = __builtin_fmaf(ubyte(la, 0), xg[0], a0);
+    a1 = __builtin_fmaf(ubyte(ha, 0), xg[1], a1);
+    a2 = __builtin_fmaf(ubyte(la, 1), xg[2], a2);
+    a3 = __builtin_fmaf(ubyte(ha, 1), xg[3], a3);
+    a0 = __builtin_fmaf(ubyte(la, 2), xg[4], a0);
+    a1 = __builtin_fmaf(ubyte(ha, 2), xg[5], a1);
+    a2 = __builtin_fmaf(ubyte(la, 3), xg[6], a2);
+    a3 = __builtin_fmaf(ubyte(ha, 3), xg[7], a3);
+    b0 = __builtin_fmaf(ubyte(lb, 0), xg[0], b0);
+    b1 = __builtin_fmaf(ubyte(hb, 0), xg[1], b1);
+    b2 = __builtin_fmaf(ubyte(lb, 1), xg[2], b2);
+    b3 = __builtin_fmaf(ubyte(hb, 1), xg[3], b3);
+    b0 = __builtin_fmaf(ubyte(lb, 2), xg[4], b0);
+    b1 = __builtin_fmaf(ubyte(hb, 2), xg[5], b1);
+    b2 = __builtin_fmaf(ubyte(lb, 3), xg[6], b2);
+    b3 = __builtin_fmaf(ubyte(hb, 3), xg[7], b3);
+  }
+  da = (a0 + a2) + (a1 + a3) * 0.0625f;
+  db = (b0 + b2) + (b1 + b3) * 0.0625f;
+}
+
+// The 32 staged activations of one group (skewed layout) into registers.
+__device__ __forceinline__ void load_group(const float *xg, float (&x)[32]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float4 v = *reinterpret_cast<const float4 *>(xg + 4 * j);
+    x[4 * j] = v.x;
+    x[4 * j + 1] = v.y;
+    x[4 * j + 2] = v.z;
+    x[4 * j + 3] = v.w;
+  }
+}
+
 // 16 signed 8-bit weights against 16 floats: sum((u - 128) * x) with
 // u = q ^ 0x80 converted by v_cvt_f32_ubyte; the -128 is folded by the caller.
 __device__ __forceinline__ float q8_chunk_dot(const uint4 w, const float *__restrict__ xg) {
@@ -316,6 +393,22 @@ __device__ __forceinline__ void tile_load(const Q4Mat &W, int r0a, int na, int r
   for (int j = 0; j < C; ++j) {
     const int c = min((int)threadIdx.x + j * NT, nch - 1);
     const size_t gc = c < split ? (size_t)r0a * ng + c : (size_t)r0b * ng + (c - split);
+    R.w[j] = W.q[gc];
+    R.s[j] = W.s[gc];
+  }
+}
+
+// Rows [r0, r0 + nrows) of W, chunk c = tid + j*stride (stride a multiple of
+// ng: all of a thread's chunks are one group, tid % ng).  Threads past the
+// stride and chunks past nrows*ng load the tile's last chunk (unused).
+template <int C>
+__device__ __forceinline__ void tile_load_strided(const Q4Mat &W, int r0, int nrows, int ng, int stride,
+                                                  TileRegs<C> &R) {
+  const int nch = nrows * ng;
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const int c = min(min((int)threadIdx.x, stride - 1) + j * stride, nch - 1);
+    const size_t gc = (size_t)r0 * ng + c;
     R.w[j] = W.q[gc];
     R.s[j] = W.s[gc];
   }

@@ -716,45 +716,59 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item,
   ResidPre<MT> RP;
   resid_prefetch<MT>(P.xa, P.opart, P.NH, gpt2 ? Lw.proj_b : nullptr, 0, D, RP);
   const Gains<MT> G = load_gains<MT>(P, Lw.n2);  // before the weights (loads retire in issue order)
+  // gate/up chunk c = tid + j*S (S = (MT / ng) * ng): every chunk of a thread
+  // is group tid % ng, so its activations are read from LDS once
+  const int S = (MT / ng) * ng;
   TileRegs<MC> Rg, Ru, Rd;
-  tile_load<MC, MT>(Lw.w1, r0, UNITS, 0, ng, nch, Rg);
-  if (!gpt2) tile_load<MC, MT>(Lw.w3, r0, UNITS, 0, ng, nch, Ru);
+  tile_load_strided<MC>(Lw.w1, r0, UNITS, ng, S, Rg);
+  if (!gpt2) tile_load_strided<MC>(Lw.w3, r0, UNITS, ng, S, Ru);
   if (done) return;
   // unconditional load (llama reads its norm gains instead and ignores it)
   const float fcb = (gpt2 ? Lw.fc_b + r0 : Lw.n2)[threadIdx.x & (UNITS - 1)];
-  float *red = smem, *xs = red + 20, *xsum = xs + m * ng * XS, *part = xsum + m * ng, *go = part + nch;
-  float *uo = go + m * UNITS;
-  float *hs = smem + al4(20 + (size_t)m * ng * XS + m * ng + nch + 2 * m * UNITS);
+  float *red = smem, *xs = red + 20, *xsum = xs + m * ng * XS, *part = xsum + m * ng;  // part: gate || up
+  float *hs = smem + al4(20 + (size_t)m * ng * XS + m * ng + 2 * nch);
   float *hsum = hs + m * 2 * XS, *blk = hsum + al4(2 * m);
   stage_residual<MT>(P.xa, P.opart, P.NH, gpt2 ? Lw.proj_b : nullptr, 0, m, D, xs, item == 0 ? P.xb : nullptr, blk,
                      RP);
-  slice_load<MC, MT>(Lw.w2, 2 * item, D, Rd);
   norm_staged<MT>(P, xs, xsum, red, m, G);
+  slice_load<MC, MT>(Lw.w2, 2 * item, D, Rd);  // needed last: behind everything the prologue reads
+  const int g = threadIdx.x % ng;
   for (int t = 0; t < m; ++t) {
-    gemv_tok<MC, MT>(Rg, nch, ng, xs + t * ng * XS, xsum + t * ng, part, go + t * UNITS);
-    if (!gpt2) gemv_tok<MC, MT>(Ru, nch, ng, xs + t * ng * XS, xsum + t * ng, part, uo + t * UNITS);
-  }
-  for (int e = threadIdx.x; e < m * UNITS; e += MT) {
-    const int t = e / UNITS, r = e - t * UNITS;
-    const float g = go[e];
-    float h;
-    if (gpt2) {
-      const float v = g + (e == (int)threadIdx.x ? fcb : Lw.fc_b[r0 + r]);
-      h = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
-    } else {
-      h = (g / (1.0f + expf(-g))) * uo[e];
-    }
-    hs[t * 2 * XS + skew(r)] = h;
-  }
-  __syncthreads();
-  if ((int)threadIdx.x < 2 * m) {
-    const float *p = hs + threadIdx.x * XS;
-    float s = 0.f;
+    // gate and up chunk partials of this token in one pass (the arithmetic
+    // of tile_compute), one barrier, then wave 0 (unit r = lane) forms the
+    // rows, the activation and the two group sums of h
+    float xr[32];
+    load_group(xs + (t * ng + g) * XS, xr);
+    const float xsg = 8.f * xsum[t * ng + g];
 #pragma unroll
-    for (int k = 0; k < 32; ++k) s += p[k];
-    hsum[threadIdx.x] = s;
+    for (int k = 0; k < MC; ++k) {
+      const int c = threadIdx.x + k * S;
+      if ((int)threadIdx.x < S && c < nch) {
+        float dg, du;
+        q4_chunk_dot2_reg(Rg.w[k], gpt2 ? Rg.w[k] : Ru.w[k], xr, dg, du);
+        part[c] = (dg - xsg) * Rg.s[k];
+        if (!gpt2) part[nch + c] = (du - xsg) * Ru.s[k];
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < UNITS) {  // exactly wave 0
+      const int r = threadIdx.x;
+      const float gv = row_sum(part + r * ng, ng);
+      float h;
+      if (gpt2) {
+        const float v = gv + fcb;
+        h = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+      } else {
+        h = (gv / (1.0f + expf(-gv))) * row_sum(part + nch + r * ng, ng);
+      }
+      hs[t * 2 * XS + skew(r)] = h;
+      const float rs = row16_sum(h);
+      const float ga = readlane_f(rs, 0) + readlane_f(rs, 16), gb = readlane_f(rs, 32) + readlane_f(rs, 48);
+      if (r == 0) hsum[2 * t] = ga;
+      if (r == 32) hsum[2 * t + 1] = gb;
+    }
+    __syncthreads();
   }
-  __syncthreads();
   for (int t = 0; t < m; ++t)
     slice_gemv<MC, MT>(Rd, D, hs + t * 2 * XS, hsum + 2 * t, P.dpart + ((size_t)t * P.nchunk + item) * D);
 }
@@ -1067,8 +1081,7 @@ size_t lds_floats(const DecParams &P, int ph, int m) {
   case PH_QKV: return al4(20 + m * ngd * XS + m * ngd + m * 16 * ngd + m * 16) + blk_d;
   case PH_ATTN: return HD + 2 * ACH + 64 * HD + 4 * HD + 16 + HD + 2 * XS + 2 + 4;
   case PH_MLP:
-    return al4(20 + m * ngd * XS + m * ngd + UNITS * ngd + 2 * (size_t)m * UNITS) + (size_t)m * 2 * XS + al4(2 * m) +
-           blk_o;
+    return al4(20 + m * ngd * XS + m * ngd + 2 * UNITS * ngd) + (size_t)m * 2 * XS + al4(2 * m) + blk_o;
   case PH_FINAL: return 52 + ngd * XS + blk_d;
   case PH_LM: return m * ngd * XS + m * ngd + (size_t)m * TC * WG + (size_t)m * P.lm_rpt + 34 + P.max_seq;
   default: return 16;
@@ -1384,7 +1397,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   // flight at once; larger values trade workgroups for the register double
   // buffer of phase_lm.
   P.lm_grid = (P.lm_tiles + MLLM_LM_TILES_PER_WG - 1) / MLLM_LM_TILES_PER_WG;
-  if (16 * ngd > QC * QT || UNITS * ngd > MC * MT || 2 * D > MC * MT || 2 * D > SC * AT || 16 * ngd > TC * LT)
+  if (16 * ngd > QC * QT || UNITS * ngd > MC * ((MT / ngd) * ngd) || 2 * D > MC * MT || 2 * D > SC * AT ||
+      16 * ngd > TC * LT)
     return fail(set_error(MLLM_ERR_UNSUPPORTED, "tiles exceed the chunk registers (d_model %d)", D));
 
   // pass size bound by LDS (160 KiB on gfx950)
