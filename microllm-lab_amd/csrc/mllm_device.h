@@ -27,6 +27,17 @@ constexpr int XS = 36;           // LDS floats per staged 32-float group
 constexpr int CPT = 4;           // chunks per thread per sub-tile
 constexpr int SUB_CH = WG * CPT; // chunks per sub-tile
 
+// The thread index as a value the compiler cannot move.  Inside the
+// persistent decode kernel's loops it would otherwise hoist every
+// thread-dependent address and lane mask of every phase out of the loops and
+// keep them all live at once, past the register budget of a 1024-thread
+// workgroup; recomputing them where they are used costs a few VALU ops.
+__device__ __forceinline__ int tid() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 struct Q4Mat {
   const uint4 *q;  // packed nibbles, as 16-byte chunks
   const float *s;  // one scale per chunk
@@ -53,6 +64,30 @@ __device__ __forceinline__ float q4_chunk_dot(const uint4 w, const float *__rest
   const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
+    const uint32_t lo = and_opaque(dw[j], 0x0F0F0F0Fu);
+    const uint32_t hi = and_opaque(dw[j], 0xF0F0F0F0u);
+    const float4 xa = *reinterpret_cast<const float4 *>(xg + 8 * j);
+    const float4 xb = *reinterpret_cast<const float4 *>(xg + 8 * j + 4);
+    a0 = __builtin_fmaf(ubyte(lo, 0), xa.x, a0);
+    a1 = __builtin_fmaf(ubyte(hi, 0), xa.y, a1);
+    a2 = __builtin_fmaf(ubyte(lo, 1), xa.z, a2);
+    a3 = __builtin_fmaf(ubyte(hi, 1), xa.w, a3);
+    a0 = __builtin_fmaf(ubyte(lo, 2), xb.x, a0);
+    a1 = __builtin_fmaf(ubyte(hi, 2), xb.y, a1);
+    a2 = __builtin_fmaf(ubyte(lo, 3), xb.z, a2);
+    a3 = __builtin_fmaf(ubyte(hi, 3), xb.w, a3);
+  }
+  return (a0 + a2) + (a1 + a3) * 0.0625f;
+}
+
+// q4_chunk_dot with the activations read in two halves, so only 16 of them
+// are live at a time (same operations in the same order: the same bits).
+__device__ __forceinline__ float q4_chunk_dot_lean(const uint4 w, const float *__restrict__ xg) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j == 2) __builtin_amdgcn_sched_barrier(0);
     const uint32_t lo = and_opaque(dw[j], 0x0F0F0F0Fu);
     const uint32_t hi = and_opaque(dw[j], 0xF0F0F0F0u);
     const float4 xa = *reinterpret_cast<const float4 *>(xg + 8 * j);
@@ -162,6 +197,58 @@ __device__ __forceinline__ float q8_chunk_dot(const uint4 w, const float *__rest
   return (a0 + a1) + (a2 + a3);
 }
 
+// ---------------------------------------------------------------- coherent access
+// Values one workgroup hands to another (activations, partial sums, the KV
+// cache, the pass state) are stored and loaded with device-scope (sc1) buffer
+// instructions.  Each XCD of the chip has its own L2; an sc1 store writes
+// through it and an sc1 load does not return a line that another XCD may
+// have changed, so a handoff inside one launch needs no L2 write-back or
+// invalidate (which a release/acquire fence at agent scope would issue).
+// The buffer resource covers [base, base + 2 GiB); base must be uniform in
+// the wave (kernel arguments and values derived from them), the per-lane
+// part goes in the 32-bit byte offset.
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+constexpr int CP_SC1 = 16;  // cache-policy operand: device scope
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const void *base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ float4 coh_ld4(const void *base, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(coh_rsrc(base), (int)off, 0, CP_SC1);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+__device__ __forceinline__ uint4 coh_ld16(const void *base, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(coh_rsrc(base), (int)off, 0, CP_SC1);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 coh_ld8(const void *base, uint32_t off) {
+  const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(coh_rsrc(base), (int)off, 0, CP_SC1);
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ float coh_ldf(const void *base, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(coh_rsrc(base), (int)off, 0, CP_SC1));
+}
+__device__ __forceinline__ int coh_ldi(const void *base, uint32_t off) {
+  return (int)__builtin_amdgcn_raw_buffer_load_b32(coh_rsrc(base), (int)off, 0, CP_SC1);
+}
+__device__ __forceinline__ void coh_st4(void *base, uint32_t off, float4 v) {
+  const u32x4_t u = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+  __builtin_amdgcn_raw_buffer_store_b128(u, coh_rsrc(base), (int)off, 0, CP_SC1);
+}
+__device__ __forceinline__ void coh_stf(void *base, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), coh_rsrc(base), (int)off, 0, CP_SC1);
+}
+__device__ __forceinline__ void coh_sti(void *base, uint32_t off, int v) {
+  __builtin_amdgcn_raw_buffer_store_b32((unsigned)v, coh_rsrc(base), (int)off, 0, CP_SC1);
+}
+__device__ __forceinline__ void coh_sth(void *base, uint32_t off, unsigned short v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, coh_rsrc(base), (int)off, 0, CP_SC1);
+}
+// Wait until this thread's stores (and loads) have completed: a workgroup
+// barrier alone does not wait for them.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0) */ }
+
 // Cross-lane moves through DPP (a VALU operand modifier) instead of
 // ds_bpermute, which goes through the LDS crossbar and costs an LDS round
 // trip per step.  Control codes (GFX9 DPP16): quad_perm(1,0,3,2) = 0xB1,
@@ -231,7 +318,7 @@ __device__ __forceinline__ float tree_max(const float *r) {
 template <int NT = WG>
 __device__ __forceinline__ float block_sum(float v, float *red) {
   v = wave_sum(v);
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = tid() & 63, wv = tid() >> 6;
   __syncthreads();
   if (lane == 0) red[wv] = v;
   __syncthreads();
@@ -243,7 +330,7 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 template <int NT = WG>
 __device__ __forceinline__ float block_max(float v, float *red) {
   v = wave_max(v);
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = tid() & 63, wv = tid() >> 6;
   __syncthreads();
   if (lane == 0) red[wv] = v;
   __syncthreads();
@@ -295,7 +382,7 @@ __device__ __forceinline__ void wave_argmax(float &v, int &i) {
 // in ascending k.  Call after xs is complete (a barrier follows inside).
 template <int NT = WG>
 __device__ __forceinline__ void stage_group_sums(const float *xs, float *xsum, int m, int ng) {
-  for (int i = threadIdx.x; i < m * ng; i += NT) {
+  for (int i = tid(); i < m * ng; i += NT) {
     const float *p = xs + i * XS;
     float s = 0.f;
 #pragma unroll
@@ -321,7 +408,7 @@ __device__ __forceinline__ void stage_rows_load(const float *__restrict__ x, int
   const int nq = n >> 2, total = m * nq;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int f = min(base + (int)threadIdx.x + k * NT, total - 1);
+    const int f = min(base + (int)tid() + k * NT, total - 1);
     const int t = f / nq, q = f - t * nq;
     v[k] = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + 4 * q);
   }
@@ -332,7 +419,7 @@ __device__ __forceinline__ void stage_rows_store(int m, int n, int base, const f
   const int nq = n >> 2, total = m * nq, ng = n >> 5;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int f = base + threadIdx.x + k * NT;
+    const int f = base + tid() + k * NT;
     if (f < total) {
       const int t = f / nq, i = 4 * (f - t * nq);
       *reinterpret_cast<float4 *>(xs + (t * ng + (i >> 5)) * XS + (i & 31)) = v[k];
@@ -391,7 +478,7 @@ __device__ __forceinline__ void tile_load(const Q4Mat &W, int r0a, int na, int r
   const int split = na * ng;
 #pragma unroll
   for (int j = 0; j < C; ++j) {
-    const int c = min((int)threadIdx.x + j * NT, nch - 1);
+    const int c = min((int)tid() + j * NT, nch - 1);
     const size_t gc = c < split ? (size_t)r0a * ng + c : (size_t)r0b * ng + (c - split);
     R.w[j] = W.q[gc];
     R.s[j] = W.s[gc];
@@ -407,7 +494,7 @@ __device__ __forceinline__ void tile_load_strided(const Q4Mat &W, int r0, int nr
   const int nch = nrows * ng;
 #pragma unroll
   for (int j = 0; j < C; ++j) {
-    const int c = min(min((int)threadIdx.x, stride - 1) + j * stride, nch - 1);
+    const int c = min(min((int)tid(), stride - 1) + j * stride, nch - 1);
     const size_t gc = (size_t)r0 * ng + c;
     R.w[j] = W.q[gc];
     R.s[j] = W.s[gc];
@@ -415,7 +502,7 @@ __device__ __forceinline__ void tile_load_strided(const Q4Mat &W, int r0, int nr
 }
 
 // out[t*ostride + r] for tile row r in [0, nrows): rows of range a first.
-// part needs m*nch floats of LDS.  gfirst = threadIdx.x % ng, gstep = NT % ng.
+// part needs m*nch floats of LDS.  gfirst = tid() % ng, gstep = NT % ng.
 template <int C, int NT = WG>
 __device__ __forceinline__ void tile_compute(const TileRegs<C> &R, int nrows, int ng, int nch, int m,
                                              const float *xs, const float *xsum, int gfirst, int gstep,
@@ -436,7 +523,7 @@ __device__ __forceinline__ void tile_compute(const TileRegs<C> &R, int nrows, in
   for (int t = 0; t < m; ++t) {
 #pragma unroll
     for (int j = 0; j < C; ++j) {
-      const int c = threadIdx.x + j * NT;
+      const int c = tid() + j * NT;
       if (c < nch) {
         const float d = q4_chunk_dot(R.w[j], xs + (t * ng + gj[j]) * XS);
         part[t * nch + c] = (d - 8.f * xsum[t * ng + gj[j]]) * R.s[j];
@@ -444,7 +531,7 @@ __device__ __forceinline__ void tile_compute(const TileRegs<C> &R, int nrows, in
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < nrows * m; i += NT) {
+  for (int i = tid(); i < nrows * m; i += NT) {
     const int t = i / nrows, r = i - t * nrows;
     out[t * ostride + r] = row_sum(part + t * nch + r * ng, ng);
   }

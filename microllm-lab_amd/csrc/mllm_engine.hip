@@ -42,6 +42,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <stddef.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -73,11 +74,16 @@ constexpr int MT = 1024;   // MLP
 constexpr int FT = 1024;   // FINAL
 constexpr int LT = WG;     // LM, ARGMAX
 constexpr int TILE_TARGET = 320;  // chunks per LM tile (~0.15 us of VALU on one CU)
-constexpr int QSPLIT = 4;  // QKV tiles per head
+constexpr int NWV = 16;    // waves of a 1024-thread workgroup: token t's serial work runs on wave t % NWV
 constexpr int UNITS = 64;  // hidden units per MLP item (two 32-column groups of mlp.w2)
 constexpr int SC = 2;      // chunk registers per thread of an ATTN head slice (SC * AT chunks)
 constexpr int MC = 2;      // chunk registers per thread of the MLP tiles and slices (MC * MT chunks)
-constexpr int QC = 1;      // chunk registers per thread of a QKV tile (QC * QT chunks)
+constexpr int QC = 2;      // chunk registers per thread of a QKV item: one head, 64 rows (QC * QT chunks)
+// Chunk registers per thread of the fused q/k/v tile of a decode attention
+// item (3 x 64 rows x d_model/32 chunks over 1024 threads): 4 up to d_model
+// 672, 5 up to 832, 6 up to 1024.  The kernels are instantiated for each.
+constexpr int aqc_for(int ng) { return (3 * HD * ng + 1023) / 1024 <= 4 ? 4 : (3 * HD * ng + 1023) / 1024; }
+constexpr int FTC = 4;     // chunk registers per thread of a persistent-kernel lm_head tile (FTC * 1024 chunks)
 constexpr int PB = 8;      // partials per block of the fixed-order partial sums
 constexpr int NBMAX = 8;   // blocks per partial sum (<= PB * NBMAX partials: heads, 64-unit chunks)
 
@@ -117,6 +123,7 @@ struct DecParams {
   float *opart;   // [MAXT][NH][D] per-head partials of W_o . att
   float *dpart;   // [MAXT][nchunk][D] per-chunk partials of W_2 . h
   float *xn;      // [MAXT][D] final-normed rows for the lm_head
+  float *xnsum;   // [MAXT][32] their group sums
   float *q;       // [MAXT][NH*HD] queries after RoPE
   void *kv;       // [L][2][NKV][max_seq][HD] (f32 or f16)
   float *attp;    // [MAXT][NH][nsplit_max][APS]
@@ -129,6 +136,23 @@ struct DecParams {
   int *hist;      // [max_seq + 1]
 };
 
+// What a phase needs to know about the pass besides the parameters.
+struct Step {
+  int pos0;   // position of token 0
+  bool done;  // a chained decode already emitted eos: issue the first loads, store nothing
+};
+
+// The pass state is read and written with coherent access: inside the
+// persistent kernel ARGMAX updates it for workgroups on other XCDs.
+#define ST_OFF(field) ((uint32_t)offsetof(PassState, field))
+__device__ __forceinline__ int st_ld(const DecParams &P, uint32_t off) { return coh_ldi(P.st, off); }
+__device__ __forceinline__ void st_st(const DecParams &P, uint32_t off, int v) { coh_sti(P.st, off, v); }
+
+// No wait: the kernel-per-phase modes order phases by kernel boundaries.
+struct NoWait {
+  __device__ bool operator()() const { return false; }
+};
+
 // ---------------------------------------------------------------- helpers
 __device__ __forceinline__ int skew(int i) { return (i >> 5) * XS + (i & 31); }
 
@@ -139,113 +163,69 @@ __device__ __forceinline__ size_t kv_index(const DecParams &P, int li, int which
   return ((((size_t)li * 2 + which) * P.NKV + h) * P.max_seq + pos) * HD;
 }
 
-// Norm gains (and LayerNorm betas) of this thread's elements i = tid + k*NT,
-// loaded into registers up front (d_model <= 1024).
-template <int NT>
-struct Gains {
-  static constexpr int K = (1024 + NT - 1) / NT;
-  float g[K], b[K];
-};
-
-template <int NT>
-__device__ __forceinline__ Gains<NT> load_gains(const DecParams &P, const float *w) {
-  Gains<NT> G;
-#pragma unroll
-  for (int k = 0; k < Gains<NT>::K; ++k) {
-    const int i = min((int)threadIdx.x + k * NT, P.D - 1);  // branch-free load; lanes past D unused
-    G.g[k] = w[i];
-    G.b[k] = P.arch == 1 ? w[P.D + i] : 0.f;
-  }
-  return G;
-}
-
-// Block-wide sum of one value per thread (NT threads, <= 16 waves) into
-// every thread: each wave reduces its 64 values with DPP, wave 0 folds the
-// wave results in order (lanes w < NT/64, DPP row sum), and the total goes
-// back through LDS.  red needs 17 floats.
-template <int NT>
-__device__ __forceinline__ float block_sum_fast(float v, float *red) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const float r = row16_sum(v);
-  const float w = (readlane_f(r, 0) + readlane_f(r, 16)) + (readlane_f(r, 32) + readlane_f(r, 48));
-  if (lane == 0) red[wv] = w;
-  __syncthreads();
-  if (wv == 0) {
-    const float t = row16_sum(lane < NT / 64 ? red[lane] : 0.f);
-    if (lane == 0) red[16] = t;
-  }
-  __syncthreads();
-  return red[16];
-}
-
-// Normalise m staged raw vectors in place (skewed layout) and write their
-// group sums xsum[t*ng + g]: RMSNorm (infer.js:134-143) or LayerNorm
-// (infer.js:147-164, eps 1e-5).  Thread i owns element i (d_model <= NT);
-// the group sums come from the normalised values of each 32-lane half-wave
-// (two DPP rows).  1/sqrt is the hardware reciprocal square root.
-template <int NT>
-__device__ void norm_staged(const DecParams &P, float *xs, float *xsum, float *red, int m, const Gains<NT> &G) {
-  static_assert(NT >= 1024, "one element per thread (d_model <= 1024)");
-  const int D = P.D, ng = D >> 5, lane = threadIdx.x & 63, i = threadIdx.x;
-  const float inv_d = 1.0f / (float)D;
-  for (int t = 0; t < m; ++t) {
-    float *xt = xs + t * ng * XS;
-    const float x = i < D ? xt[skew(i)] : 0.f;
-    float y;
-    if (P.arch == 1) {
-      const float mean = block_sum_fast<NT>(x, red) * inv_d;
-      const float d = i < D ? x - mean : 0.f;
-      const float var = block_sum_fast<NT>(d * d, red) * inv_d;
-      y = __builtin_fmaf(d * __builtin_amdgcn_rsqf(var + 1e-5f), G.g[0], G.b[0]);
-    } else {
-      const float ss = block_sum_fast<NT>(x * x, red) * inv_d;
-      y = x * __builtin_amdgcn_rsqf(ss + P.eps) * G.g[0];
-    }
-    if (i >= D) y = 0.f;
-    if (i < D) xt[skew(i)] = y;
-    const float r = row16_sum(y);
-    const float ga = readlane_f(r, 0) + readlane_f(r, 16), gb = readlane_f(r, 32) + readlane_f(r, 48);
-    if ((lane == 0 || lane == 32) && i < D) xsum[t * ng + (i >> 5)] = lane == 0 ? ga : gb;
-    __syncthreads();
-  }
-}
+// ---------------------------------------------------------------- residual and norm
+// A phase's serial per-token work (the residual sum, the norm, row sums,
+// the RoPE and activation epilogues) runs on one wave: token t on wave
+// t % NWV.  The other waves wait at the next barrier instead of running the
+// same dependent chain four waves to a SIMD.  Loads and dot products use
+// every wave.  Which wave runs a token does not change its arithmetic, so a
+// row of a multi-token pass is bit-identical to the single-token step.
+__device__ __forceinline__ int wave_id() { return tid() >> 6; }
+__device__ __forceinline__ int lane_id() { return tid() & 63; }
 
 __device__ __forceinline__ float4 add4(float4 a, float4 b) {
   return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
-// Residual rows t = t0 .. t0+m-1:
-//   x[t] = base[t] + (((B_0 + B_1) + ... + B_{nb-1}) + bias)
-// where B_b sums parts[t][p] for p in [b*PB, min(np, (b+1)*PB)) in ascending
-// p (from +0).  The rows go to the skewed LDS layout xs[t - t0] and, when
-// `out` is set, to out[t].  The order of every addition is fixed by np alone.
-// Each thread loads two (block, float4-column) items per round before adding,
-// so a round costs one memory latency.  blk needs nb * D floats of LDS.
-// The first round of token t0 is loaded by resid_prefetch, which a phase
-// calls before it issues its weight loads: loads retire in issue order, so
-// activations issued first can be consumed while the weights still stream.
-// U items per thread per round: two with 256 threads, one with 1024.
-template <int NT>
-struct ResidPre {
-  static constexpr int U = NT >= 1024 ? 1 : 2;
-  float4 v[U][PB];
-  float4 xb, bb;
+// The norm gains (LayerNorm: gamma || beta) and the residual's bias go to
+// LDS, where the norm wave reads them: gl[0, 2D) gains, gl[2D, 3D) bias.
+// Loaded into registers (three per thread, d_model <= 1024) with the item's
+// other early loads, stored once they have arrived.
+struct GainsReg {
+  float g[3];
+};
+__device__ __forceinline__ void gains_load(const DecParams &P, const float *w, const float *bias, GainsReg &G) {
+  const int n = P.arch == 1 ? 2 * P.D : P.D;
+  const int tot = n + (bias ? P.D : 0);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int e = min(tid() + k * 1024, tot - 1);  // branch-free; lanes past tot unused
+    G.g[k] = e < n ? w[e] : bias[e - n];
+  }
+}
+__device__ __forceinline__ void gains_store(const DecParams &P, const float *bias, const GainsReg &G, float *gl) {
+  const int n = P.arch == 1 ? 2 * P.D : P.D;
+  const int tot = n + (bias ? P.D : 0);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int e = tid() + k * 1024;
+    if (e < tot) gl[e < n ? e : 2 * P.D + (e - n)] = G.g[k];
+  }
+}
+
+// The residual of one token:
+//   x = base + (((B_0 + B_1) + ... + B_{nb-1}) + bias)
+// where B_b sums parts[p] for p in [b*PB, min(np, (b+1)*PB)) in ascending p
+// (from +0).  The order of every addition is fixed by np alone.
+// The block sums use every thread of a 1024-thread workgroup: item
+// it = b * nq + c (round it / 1024) forms B_b of float4 column c into blk[it]
+// (LDS).  A round's loads all go out before its first add, so a round costs
+// one memory latency; round 0 can be loaded ahead (resid_blocks_load) so its
+// latency overlaps the weight loads.  Branch-free: an item or partial past
+// the end reads partial 0 of column 0 (valid memory) and is left out.
+struct ResidReg {
+  float4 v[PB];
 };
 
-// Branch-free loads: an item or partial past the end reads partial 0 of
-// column 0 (valid memory) and resid_add leaves it out.
-template <int NT, int U>
-__device__ __forceinline__ void resid_load(const float4 *pt, int nq, int np, int nitems, int i0, float4 (&v)[U][PB]) {
+__device__ __forceinline__ void resid_blocks_load(const float *pt, int nq, int np, int round, ResidReg &R) {
+  const int nitems = nq * ((np + PB - 1) / PB);
+  const int it = tid() + round * 1024;
+  const int b = it / nq, c = it - b * nq;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int it = i0 + u * NT;
-    const int b = it / nq, c = it - b * nq;
-#pragma unroll
-    for (int k = 0; k < PB; ++k) {
-      const int p = b * PB + k;
-      const bool ok = it < nitems && p < np;
-      v[u][k] = pt[ok ? (size_t)p * nq + c : 0];
-    }
+  for (int k = 0; k < PB; ++k) {
+    const int p = b * PB + k;
+    const bool ok = it < nitems && p < np;
+    R.v[k] = coh_ld4(pt, 16u * (ok ? (uint32_t)(p * nq + c) : 0u));
   }
 }
 
@@ -253,104 +233,154 @@ __device__ __forceinline__ void resid_load(const float4 *pt, int nq, int np, int
 // conditional): a load consumed inside a divergent branch leaves the
 // compiler unsure it has completed, and it then waits for every load in
 // flight before the register is reused.
-template <int NT, int U>
-__device__ __forceinline__ void resid_add(int nq, int np, int nitems, int i0, const float4 (&v)[U][PB], float *blk) {
+__device__ __forceinline__ void resid_blocks_add(int nq, int np, int round, const ResidReg &R, float *blk) {
+  const int nitems = nq * ((np + PB - 1) / PB);
+  const int it = tid() + round * 1024;
+  const int b = it / nq;
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int it = i0 + u * NT;
-    const int b = it / nq;
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int k = 0; k < PB; ++k) {
-      const float4 w = v[u][k];
-      const bool use = b * PB + k < np;
-      a = add4(a, make_float4(use ? w.x : 0.f, use ? w.y : 0.f, use ? w.z : 0.f, use ? w.w : 0.f));
-    }
-    if (it < nitems) reinterpret_cast<float4 *>(blk)[it] = a;
+  for (int k = 0; k < PB; ++k) {
+    const float4 w = R.v[k];
+    const bool use = b * PB + k < np;
+    a = add4(a, make_float4(use ? w.x : 0.f, use ? w.y : 0.f, use ? w.z : 0.f, use ? w.w : 0.f));
+  }
+  if (it < nitems) reinterpret_cast<float4 *>(blk)[it] = a;
+}
+
+// Every round of the block sums, round 0 already loaded into R0 (at most
+// two rounds: nq * nb <= 2048).
+__device__ __forceinline__ void resid_blocks_rest(const float *pt, int nq, int np, const ResidReg &R0, float *blk) {
+  resid_blocks_add(nq, np, 0, R0, blk);
+  if (nq * ((np + PB - 1) / PB) > 1024) {
+    ResidReg R1;
+    resid_blocks_load(pt, nq, np, 1, R1);
+    resid_blocks_add(nq, np, 1, R1, blk);
   }
 }
 
-template <int NT>
-__device__ __forceinline__ void resid_prefetch(const float *base, const float *parts, int np, const float *bias, int t0,
-                                               int D, ResidPre<NT> &R) {
-  const int nq = D >> 2, nb = (np + PB - 1) / PB;
-  const int q = min((int)threadIdx.x, nq - 1);  // D <= 1024: one float4 column per thread (branch-free)
-  R.xb = reinterpret_cast<const float4 *>(base + (size_t)t0 * D)[q];
-  // unconditional load (of base itself when there is no bias): a load in a
-  // branch leaves the compiler unsure whether it is pending, and it then
-  // waits for every load in flight at the next reuse of its register
-  R.bb = reinterpret_cast<const float4 *>(bias ? bias : base)[q];
-  resid_load<NT, ResidPre<NT>::U>(reinterpret_cast<const float4 *>(parts + (size_t)t0 * np * D), nq, np, nq * nb,
-                                  threadIdx.x, R.v);
+__device__ __forceinline__ void resid_blocks(const float *pt, int nq, int np, float *blk) {
+  ResidReg R0;
+  resid_blocks_load(pt, nq, np, 0, R0);
+  resid_blocks_rest(pt, nq, np, R0, blk);
 }
 
-// Block sums of row t (all rounds but the prefetched one when skip_first is
-// set), then the row itself: xs[tt] and out[t].
-template <int NT>
-__device__ __forceinline__ void resid_row(const float *parts, int np, int t, int tt, int D, float4 xb, float4 bb,
-                                          bool has_bias, bool skip_first, float *xs, float *out, float *blk) {
-  constexpr int U = ResidPre<NT>::U;
-  const int nq = D >> 2, ng = D >> 5, nb = (np + PB - 1) / PB, nitems = nq * nb;
-  const float4 *pt = reinterpret_cast<const float4 *>(parts + (size_t)t * np * D);
-  for (int i0 = threadIdx.x + (skip_first ? U * NT : 0); i0 < nitems; i0 += U * NT) {
-    float4 v[U][PB];
-    resid_load<NT, U>(pt, nq, np, nitems, i0, v);
-    resid_add<NT, U>(nq, np, nitems, i0, v, blk);
-  }
-  __syncthreads();
-  // every lane combines (column clamped), only the stores are conditional:
-  // xb and bb are loads and are consumed outside any branch
-  const int q = min((int)threadIdx.x, nq - 1);
+// One token's residual and norm, one float4 column q < nq per thread
+// (threads 0 .. nq-1, d_model <= 1024):
+//   x = base + (((B_0 + B_1) + ... + B_{nb-1}) + bias)
+// from the block sums in blk, then RMSNorm (infer.js:134-143,
+// x * (1/sqrt(mean(x^2) + eps)) * w) or LayerNorm (infer.js:147-164,
+// eps 1e-5): each wave sums its columns with DPP, the waves' sums are added
+// in order.  1/sqrt is the hardware reciprocal square root.  The
+// normalised row goes to xs_t (skewed) and the sum of every 32-element
+// group (8 neighbouring lanes x 4) to xsum_t.  The gains (LayerNorm:
+// gamma || beta) and the bias are in gl[0, 2D) and gl[2D, 3D).  Every
+// thread of the workgroup must call it (it holds barriers); red needs
+// 2 x 16 floats.
+struct ColOut {
+  float *x;     // the residual row (coherent store), or null
+  float *y;     // the normalised row (coherent store), or null
+  float *ysum;  // its group sums (coherent store), or null
+};
+
+__device__ __forceinline__ float4 col_finish(const float *blk, int nq, int np, float4 base, const float *gl, int D,
+                                             bool has_bias) {
+  const int q = min(tid(), nq - 1), nb = (np + PB - 1) / PB;  // threads past the row: a valid column, unused
   const float4 *b4 = reinterpret_cast<const float4 *>(blk);
   float4 s = b4[q];
-  // fixed trip count: a runtime loop here made the compiler wait for every
-  // load in flight (the weights) before entering it
-#pragma unroll
-  for (int b = 1; b < NBMAX; ++b)
-    if (b < nb) s = add4(s, b4[b * nq + q]);
-  if (has_bias) s = add4(s, bb);
-  const float4 v = add4(xb, s);
-  if ((int)threadIdx.x < nq) {
-    const int i = 4 * q;
-    *reinterpret_cast<float4 *>(xs + (tt * ng + (i >> 5)) * XS + (i & 31)) = v;
-    if (out) reinterpret_cast<float4 *>(out + (size_t)t * D)[q] = v;
-  }
-  __syncthreads();
+  for (int b = 1; b < nb; ++b) s = add4(s, b4[b * nq + q]);
+  if (has_bias) s = add4(s, reinterpret_cast<const float4 *>(gl + 2 * D)[q]);
+  return add4(base, s);
 }
 
-template <int NT>
-__device__ void stage_residual(const float *base, const float *parts, int np, const float *bias, int t0, int m,
-                               int D, float *xs, float *out, float *blk, const ResidPre<NT> &R) {
-  const int nq = D >> 2, nb = (np + PB - 1) / PB;
-  const float4 bb = R.bb;
-  // token t0: its first round is in R
-  resid_add<NT, ResidPre<NT>::U>(nq, np, nq * nb, threadIdx.x, R.v, blk);
-  resid_row<NT>(parts, np, t0, 0, D, R.xb, bb, bias != nullptr, true, xs, out, blk);
-  for (int tt = 1; tt < m; ++tt) {
-    const int t = t0 + tt;
-    const float4 xb = reinterpret_cast<const float4 *>(base + (size_t)t * D)[min((int)threadIdx.x, nq - 1)];
-    resid_row<NT>(parts, np, t, tt, D, xb, bb, bias != nullptr, false, xs, out, blk);
+// Sum over the first nw waves of one value per thread, into every thread.
+__device__ __forceinline__ float waves_sum(float v, int nw, float *red) {
+  const int wv = wave_id();
+  if (wv < nw) {
+    const float w = wave_sum(v);
+    if (lane_id() == 0) red[wv] = w;
+  }
+  __syncthreads();
+  float t = red[0];
+  for (int k = 1; k < nw; ++k) t += red[k];
+  return t;
+}
+
+__device__ __forceinline__ void col_norm(const DecParams &P, float4 x, const float *gl, float *red, float *xs_t,
+                                         float *xsum_t, const ColOut &o) {
+  const int D = P.D, nq = D >> 2, q = tid(), nw = (nq + 63) >> 6;
+  const bool in = q < nq;
+  if (!in) x = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (o.x && in) coh_st4(o.x, 16u * q, x);
+  const float inv_d = 1.0f / (float)D;
+  const float4 *g4 = reinterpret_cast<const float4 *>(gl);
+  const int qc = min(q, nq - 1);
+  float4 y;
+  if (P.arch == 1) {
+    const float mean = waves_sum((x.x + x.y) + (x.z + x.w), nw, red) * inv_d;
+    const float4 d = in ? make_float4(x.x - mean, x.y - mean, x.z - mean, x.w - mean) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float r =
+        __builtin_amdgcn_rsqf(waves_sum((d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w), nw, red + 16) * inv_d + 1e-5f);
+    const float4 g = g4[qc], b = g4[(D >> 2) + qc];
+    y = make_float4(__builtin_fmaf(d.x * r, g.x, b.x), __builtin_fmaf(d.y * r, g.y, b.y),
+                    __builtin_fmaf(d.z * r, g.z, b.z), __builtin_fmaf(d.w * r, g.w, b.w));
+  } else {
+    const float r = __builtin_amdgcn_rsqf(waves_sum((x.x * x.x + x.y * x.y) + (x.z * x.z + x.w * x.w), nw, red) * inv_d +
+                                          P.eps);
+    const float4 g = g4[qc];
+    y = make_float4(x.x * r * g.x, x.y * r * g.y, x.z * r * g.z, x.w * r * g.w);
+  }
+  if (!in) y = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (wave_id() < nw) {
+    float v = (y.x + y.y) + (y.z + y.w);
+    v = v + dpp_f<0xB1>(v);   // pairs
+    v = v + dpp_f<0x4E>(v);   // quads
+    v = v + dpp_f<0x141>(v);  // 8 lanes (half-row mirror)
+    if (in) {
+      if (xs_t) *reinterpret_cast<float4 *>(xs_t + (q >> 3) * XS + ((4 * q) & 31)) = y;
+      if (o.y) coh_st4(o.y, 16u * q, y);
+      if ((q & 7) == 0) {
+        if (xsum_t) xsum_t[q >> 3] = v;
+        if (o.ysum) coh_stf(o.ysum, 4u * (q >> 3), v);
+      }
+    }
   }
 }
 
-// One token's GEMV over a row tile held in registers (chunk c = tid + k*NT
-// of rows ng groups wide, c < nch): out[r] for r < nch / ng, with the
-// arithmetic of tile_compute (bit-identical rows).
-template <int C, int NT>
-__device__ __forceinline__ void gemv_tok(const TileRegs<C> &R, int nch, int ng, const float *xs, const float *xsum,
-                                         float *part, float *out) {
-  int g = threadIdx.x % ng;
-  const int gstep = NT % ng;
+// The base column of this thread (coherent load, branch-free).
+__device__ __forceinline__ float4 col_base_load(const float *base, int nq) {
+  return coh_ld4(base, 16u * min(tid(), nq - 1));
+}
+
+// Per-chunk partials of a tile in registers for m staged tokens:
+// part[t*nch + c] (the arithmetic of tile_compute); no barrier.
+template <int C>
+__device__ __forceinline__ void tile_partials(const TileRegs<C> &R, int ng, int nch, int m, const float *xs,
+                                              const float *xsum, float *part) {
+  int gj[C];
+  {
+    int g = tid() % ng;
+    const int gstep = 1024 % ng;
 #pragma unroll
-  for (int k = 0; k < C; ++k) {
-    const int c = threadIdx.x + k * NT;
-    if (c < nch) part[c] = (q4_chunk_dot(R.w[k], xs + g * XS) - 8.f * xsum[g]) * R.s[k];
-    g += gstep;
-    if (g >= ng) g -= ng;
+    for (int j = 0; j < C; ++j) {
+      gj[j] = g;
+      g += gstep;
+      if (g >= ng) g -= ng;
+    }
   }
-  __syncthreads();
-  for (int r = threadIdx.x; r < nch / ng; r += NT) out[r] = row_sum(part + r * ng, ng);
-  __syncthreads();
+  for (int t = 0; t < m; ++t) {
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const int c = tid() + j * 1024;
+      if (c < nch) {
+        const float d = q4_chunk_dot_lean(R.w[j], xs + (t * ng + gj[j]) * XS);
+        part[t * nch + c] = (d - 8.f * xsum[t * ng + gj[j]]) * R.s[j];
+      }
+      // one chunk at a time: the activations of several chunks in flight at
+      // once would not fit beside the registers the caller holds (the other
+      // waves of the SIMD hide the LDS latency)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
 }
 
 // A two-group column slice of a matrix with ng groups per row: chunk
@@ -360,7 +390,7 @@ __device__ __forceinline__ void slice_load(const Q4Mat &W, int g0, int rows, Til
   const int ng = W.cols >> 5;
 #pragma unroll
   for (int k = 0; k < C; ++k) {
-    const int c = min((int)threadIdx.x + k * NT, 2 * rows - 1);  // branch-free; extra lanes unused
+    const int c = min((int)tid() + k * NT, 2 * rows - 1);  // branch-free; extra lanes unused
     const size_t gc = (size_t)(c >> 1) * ng + g0 + (c & 1);
     R.w[k] = W.q[gc];
     R.s[k] = W.s[gc];
@@ -369,232 +399,268 @@ __device__ __forceinline__ void slice_load(const Q4Mat &W, int g0, int rows, Til
 
 // The slice against two staged groups v (skewed, 2 x XS) with sums vsum[2]:
 // out[r] = part(group g0) + part(group g0 + 1), the row_sum order of two
-// groups.  Neighbouring lanes hold the pair; every lane takes part in the
-// shuffle.
+// groups (coherent stores).  Neighbouring lanes hold the pair; every lane
+// takes part in the shuffle.
 template <int C, int NT>
 __device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const float *v, const float *vsum,
                                            float *out) {
 #pragma unroll
   for (int k = 0; k < C; ++k) {
-    const int c = threadIdx.x + k * NT;
+    const int c = tid() + k * NT;
     const int j = c & 1;
     float p = 0.f;
     if (c < 2 * rows) p = (q4_chunk_dot(R.w[k], v + j * XS) - 8.f * vsum[j]) * R.s[k];
     const float sum = p + lane_xor1(p);
-    if (c < 2 * rows && j == 0) out[c >> 1] = sum;
+    if (c < 2 * rows && j == 0) coh_stf(out, 4u * (c >> 1), sum);
   }
+}
+
+// Three 64-row ranges r0, r1, r2 of one matrix as one tile (chunk c of row
+// c / ng of the ranges in order).  Branch-free: chunks past the tile load its
+// last chunk (unused).
+template <int C>
+__device__ __forceinline__ void tile_load3(const Q4Mat &W, int r0, int r1, int r2, int ng, TileRegs<C> &R) {
+  const int per = HD * ng, nch = 3 * per;
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const int c = min(tid() + j * 1024, nch - 1);
+    const int k = c / per, cc = c - k * per;
+    // arithmetic, not a select chain (which the compiler turns into a table
+    // in scratch memory)
+    const int rb = r0 + (k >= 1 ? r1 - r0 : 0) + (k >= 2 ? r2 - r1 : 0);
+    const size_t gc = (size_t)rb * ng + cc;
+    R.w[j] = W.q[gc];
+    R.s[j] = W.s[gc];
+  }
+}
+
+// Embedding column q = tid of one token (infer.js:360-420): the
+// dequantised row of the tied lm_head; gpt2 divides it by scale_factors
+// (when present) and adds the learned position.  Branch-free (the column is
+// clamped for threads past the row).
+__device__ __forceinline__ float4 embed_col(const DecParams &P, int tok, int pos) {
+  const int D = P.D, ng = D >> 5, q = min(tid(), (D >> 2) - 1);
+  const bool gpt2 = P.arch == 1;
+  const uint8_t *row = reinterpret_cast<const uint8_t *>(P.lm.q) + (size_t)tok * (D >> 1);
+  const unsigned short b2 = *reinterpret_cast<const unsigned short *>(row + 2 * q);
+  const float s = (P.lm.s + (size_t)tok * ng)[q >> 3];
+  float4 e = make_float4((float)((int)(b2 & 15) - 8) * s, (float)((int)((b2 >> 4) & 15) - 8) * s,
+                         (float)((int)((b2 >> 8) & 15) - 8) * s, (float)((int)(b2 >> 12) - 8) * s);
+  if (gpt2) {
+    if (P.sf) {
+      const float4 f = reinterpret_cast<const float4 *>(P.sf)[q];
+      e = make_float4(e.x / f.x, e.y / f.y, e.z / f.z, e.w / f.w);
+    }
+    e = add4(e, reinterpret_cast<const float4 *>(P.wpe + (size_t)pos * D)[q]);
+  }
+  return e;
 }
 
 // ---------------------------------------------------------------- phases
-__device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, int item, bool done, float *smem) {
-  const int D = P.D, ng = D >> 5;
-  const int head = item / QSPLIT, quarter = item - head * QSPLIT;
-  const int ra = head * HD + quarter * 8, rb = ra + 32;  // RoPE partners d and d + 32
-  const int nch = 16 * ng;
-  const PassState &S = *P.st;
-  const int pos0 = S.pos0;
-  // activations first (the embedding row, or the residual and the previous
-  // layer's partials), then the weight tile
-  const bool gpt2 = P.arch == 1;
-  constexpr int K = Gains<QT>::K;  // elements per thread (d_model <= 1024)
-  int bv[K];
-  float sv[K], sfv[K], pv4[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    bv[k] = 0;
-    sv[k] = 0.f;
-    sfv[k] = 1.f;
-    pv4[k] = 0.f;
-  }
-  ResidPre<QT> RP;
-  if (li == 0) {
-    // embed (infer.js:360-420): dequantised tied lm_head row; gpt2 divides by
-    // scale_factors and adds the learned position.  Loads of token 0 here.
-    const int tok = min(max(S.tok[0], 0), P.V - 1);  // host and ARGMAX keep it in range
-    const uint8_t *row = reinterpret_cast<const uint8_t *>(P.lm.q) + (size_t)tok * (D >> 1);
-    const float *sc = P.lm.s + (size_t)tok * ng;
-    const int pos = min(pos0, P.max_seq - 1);
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int i = min((int)threadIdx.x + k * QT, D - 1);  // branch-free; lanes past D unused
-      bv[k] = row[i >> 1];
-      sv[k] = sc[i >> 5];
-      if (gpt2) {
-        sfv[k] = P.sf ? P.sf[i] : 1.f;
-        pv4[k] = P.wpe[(size_t)pos * D + i];
-      }
-    }
-  } else {
-    resid_prefetch<QT>(P.xb, P.dpart, P.nchunk, gpt2 ? Lw.prev_mproj_b : nullptr, 0, D, RP);
-  }
-  // loads retire in issue order: everything the prologue reads goes out
-  // before the weight tile, so the prologue never waits for the weights
-  const Gains<QT> G = load_gains<QT>(P, Lw.n1);
+// Every phase is written once for both ways of running it.
+//   FLOW = 0 (one kernel per phase): the activations are loaded first, then
+//     the weights; loads retire in issue order, so the prologue never waits
+//     for the weights.
+//   FLOW = 1 (the persistent kernel): the weights are loaded first, then
+//     wait() blocks until the producers of this item's inputs have published
+//     them (it returns true once the chained decode has ended), then the
+//     activations are loaded.
+// The arithmetic is the same in both, so both give the same bits.
+
+// QKV item: one head's 64 rows of attn.qkv (query head, K head or V head),
+// so the RoPE partners d and d + 32 are in the item.
+struct QkvPre {
   TileRegs<QC> R;
-  tile_load<QC, QT>(Lw.qkv, ra, 8, rb, ng, nch, R);
-  if (done) return;  // a chained decode that reached eos: loads only, no stores
-  float *red = smem, *xs = red + 20, *xsum = xs + m * ng * XS, *part = xsum + m * ng, *out = part + m * nch;
-  float *blk = smem + al4(20 + (size_t)m * ng * XS + m * ng + m * nch + m * 16);
-  // this thread's epilogue element (m * 16 <= QT): its RoPE table entries or
-  // bias, fetched before the staging so the epilogue does not wait for them
-  const bool is_q = head < P.NH, is_k = !is_q && head < P.NH + P.NKV;
-  const int e_own = threadIdx.x, t_own = e_own >> 4, r_own = e_own & 15;
-  const int d_own = quarter * 8 + (r_own & 7) + (r_own >> 3) * 32;
-  // unconditional loads (gpt2: the bias twice; llama: the RoPE tables, also
-  // for V rows that do not use them; positions clamped for lanes past m * 16)
-  const size_t ri = (size_t)min(pos0 + t_own, P.max_seq - 1) * HD + d_own;
-  const float *pc = gpt2 ? Lw.qkv_b + head * HD + d_own : P.rope_cos + ri;
-  const float *ps = gpt2 ? pc : P.rope_sin + ri;
-  const float c_own = *pc, s_own = *ps;
-  const float b_own = c_own;
-  if (li == 0) {
-    // item 0 writes xa
-    for (int t = 0; t < m; ++t) {
-      float *xt = xs + t * ng * XS;
-      if (t > 0) {
-        const int tok = min(max(S.tok[t], 0), P.V - 1);
-        const uint8_t *row = reinterpret_cast<const uint8_t *>(P.lm.q) + (size_t)tok * (D >> 1);
-        const float *sc = P.lm.s + (size_t)tok * ng;
-        const int pos = min(pos0 + t, P.max_seq - 1);
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          const int i = min((int)threadIdx.x + k * QT, D - 1);
-          bv[k] = row[i >> 1];
-          sv[k] = sc[i >> 5];
-          if (gpt2) {
-            sfv[k] = P.sf ? P.sf[i] : 1.f;
-            pv4[k] = P.wpe[(size_t)pos * D + i];
-          }
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const int i = threadIdx.x + k * QT;
-        if (i < D) {
-          float v = (float)(((i & 1) ? (bv[k] >> 4) : (bv[k] & 15)) - 8) * sv[k];
-          if (gpt2) {
-            if (P.sf) v = v / sfv[k];
-            v = v + pv4[k];
-          }
-          xt[skew(i)] = v;
-          if (item == 0) P.xa[(size_t)t * D + i] = v;
-        }
-      }
+  float c_own, s_own;  // llama: RoPE cos/sin of (token wave, dim lane); gpt2: bias of row lane
+};
+
+__device__ __forceinline__ void qkv_pre(const DecParams &P, const LayerW &Lw, int head, int pos0, QkvPre &Q) {
+  const int ng = P.D >> 5;
+  tile_load<QC, QT>(Lw.qkv, head * HD, HD, 0, ng, HD * ng, Q.R);
+  const int d = lane_id();
+  const size_t ri = (size_t)min(pos0 + wave_id(), P.max_seq - 1) * HD + d;  // positions clamped past m
+  const float *pc = P.arch == 1 ? Lw.qkv_b + head * HD + d : P.rope_cos + ri;
+  const float *ps = P.arch == 1 ? pc : P.rope_sin + ri;
+  Q.c_own = *pc;
+  Q.s_own = *ps;
+}
+
+template <bool FLOW, class W>
+__device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, int head, const Step &st, float *smem,
+                          W &&wait) {
+  const int D = P.D, ng = D >> 5, nq = D >> 2;
+  const int nch = HD * ng;
+  const int pos0 = st.pos0;
+  const bool gpt2 = P.arch == 1;
+  const int nb = (P.nchunk + PB - 1) / PB;
+  float *gl = smem, *xs = gl + al4(3 * D), *xsum = xs + m * ng * XS, *part = xsum + al4(m * ng);
+  float *blk = part + m * nch;  // 2 x nb * D (alternating tokens), then red
+  const float *rbias = gpt2 && li > 0 ? Lw.prev_mproj_b : nullptr;
+  QkvPre Q;
+  GainsReg GR;
+  if (FLOW) {
+    qkv_pre(P, Lw, head, pos0, Q);
+    gains_load(P, Lw.n1, rbias, GR);
+    gains_store(P, rbias, GR, gl);
+    if (wait()) return;
+  }
+  const int wv = wave_id(), lane = lane_id();
+  float *red = blk + 2 * nb * D;  // 32
+  ResidReg R0;
+  float4 base = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (!FLOW) {
+    // loads retire in issue order: everything the prologue reads goes out
+    // before the weight tile, so the prologue never waits for the weights
+    if (li > 0) {
+      base = col_base_load(P.xb, nq);
+      resid_blocks_load(P.dpart, nq, P.nchunk, 0, R0);
+    }
+    gains_load(P, Lw.n1, rbias, GR);
+    qkv_pre(P, Lw, head, pos0, Q);
+    if (st.done) return;  // a chained decode that reached eos: loads only, no stores
+    if (li > 0) resid_blocks_rest(P.dpart, nq, P.nchunk, R0, blk);
+    gains_store(P, rbias, GR, gl);
+  }
+  // stage every token: x, the norm, xs and xsum
+  for (int t = 0; t < m; ++t) {
+    float *bt = blk + (t & 1) * nb * D;
+    if (li == 0) {
+      const int tok = min(max(st_ld(P, ST_OFF(tok) + 4u * t), 0), P.V - 1);  // host and ARGMAX keep it in range
+      base = embed_col(P, tok, min(pos0 + t, P.max_seq - 1));
+    } else if (FLOW || t > 0) {
+      base = col_base_load(P.xb + (size_t)t * D, nq);
+      resid_blocks(P.dpart + (size_t)t * P.nchunk * D, nq, P.nchunk, bt);
     }
     __syncthreads();
-  } else {
-    stage_residual<QT>(P.xb, P.dpart, P.nchunk, gpt2 ? Lw.prev_mproj_b : nullptr, 0, m, D, xs,
-                       item == 0 ? P.xa : nullptr, blk, RP);
+    const float4 x = li == 0 ? base : col_finish(bt, nq, P.nchunk, base, gl, D, rbias != nullptr);
+    col_norm(P, x, gl, red, xs + t * ng * XS, xsum + t * ng, ColOut{head == 0 ? P.xa + (size_t)t * D : nullptr});
   }
-  norm_staged<QT>(P, xs, xsum, red, m, G);
-  tile_compute<QC, QT>(R, 16, ng, nch, m, xs, xsum, threadIdx.x % ng, QT % ng, part, out, 16);
-  // epilogue: tile row r < 8 is head dim d = quarter*8 + r, r >= 8 is d + 32
-  const int kvh = is_q ? 0 : (is_k ? head - P.NH : head - P.NH - P.NKV);
-  if (e_own < m * 16) {
-    const int e = e_own, t = t_own, r = r_own, d = d_own;
-    float v = out[e];
+  __syncthreads();
+  tile_partials<QC>(Q.R, ng, nch, m, xs, xsum, part);
+  __syncthreads();
+  // epilogue on the token's wave: lane d is head dimension d
+  for (int t = wv; t < m; t += NWV) {
+    const int d = lane;
+    float v = row_sum(part + t * nch + d * ng, ng);
     const int pos = pos0 + t;
-    if (P.arch == 1) {
-      v = v + b_own;
+    const bool is_q = head < P.NH, is_k = !is_q && head < P.NH + P.NKV;
+    if (gpt2) {
+      v = v + Q.c_own;  // the bias
     } else if (is_q || is_k) {
-      const float mate = r < 8 ? -out[e + 8] : out[e - 8];
-      v = __builtin_fmaf(v, c_own, mate * s_own);
+      const float mate = __shfl_xor(v, 32);  // rotate-half partner d +- 32
+      v = __builtin_fmaf(v, Q.c_own, (d < 32 ? -mate : mate) * Q.s_own);
     }
     if (is_q) {
-      P.q[(size_t)t * P.NH * HD + head * HD + d] = v;
+      coh_stf(P.q, 4u * (t * P.NH * HD + head * HD + d), v);
     } else {
+      const int kvh = is_k ? head - P.NH : head - P.NH - P.NKV;
       const size_t k = kv_index(P, li, is_k ? 0 : 1, kvh, pos) + d;
       if (P.kv_fp16)
-        reinterpret_cast<__half *>(P.kv)[k] = __float2half_rn(v);
+        coh_sth(P.kv, 2u * (uint32_t)k, __half_as_ushort(__float2half_rn(v)));
       else
-        reinterpret_cast<float *>(P.kv)[k] = v;
+        coh_stf(P.kv, 4u * (uint32_t)k, v);
     }
   }
 }
 
-// One (token, split, head) item, 1024 threads.  Every load of the item (q,
-// the K rows, the V rows) is issued at once: the score of key p of the split
-// is formed by the four lanes 4p .. 4p+3 (16 dimensions each, joined with
-// DPP); thread (kg, d4) owns V[kg + 64j][4*d4 .. 4*d4+3] for j < 4.  The last
-// split of (token, head) to finish -- counted in P.cnt; a single split is its
-// own last -- merges the splits (flash-decoding merge in split order) and
-// writes the head's partial of the attention output projection to P.opart.
-__device__ void phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, int item, bool done, float *smem) {
-  const int per_tok = P.NH * P.nsplit_max;
-  const int t = item / per_tok;
-  const int rem = item - t * per_tok;
-  const int sp = rem / P.NH, h = rem - sp * P.NH;
-  if (t >= m || done) return;
-  const int pos = P.st->pos0 + t;
-  const int s0 = sp * ACH;
-  if (s0 > pos) return;
-  const int ns = pos / ACH + 1;
-  const bool solo = ns == 1;
-  const int D = P.D;
-  TileRegs<SC> Ro;
-  const int cnt = min(ACH, pos + 1 - s0);
-  const int kvh = h / (P.NH / P.NKV);
-  float *qs = smem;            // 64
-  float *es = qs + HD;         // 256: exp weights
-  float *sc = es + ACH;        // 256: scores
-  float *pv = sc + ACH;        // 64 x 64
-  float *pv2 = pv + 64 * HD;   // 4 x 64
-  float *red = pv2 + 4 * HD;   // 16
-  float *own = red + 16;       // 64: this split's P.V
-  float *att = own + HD;       // 2 x XS: merged head output, skewed
-  float *asum = att + 2 * XS;  // 2
-  int *flag = reinterpret_cast<int *>(asum + 2);
-  const size_t kbase = kv_index(P, li, 0, kvh, s0), vbase = kv_index(P, li, 1, kvh, s0);
-  const int kp = threadIdx.x >> 2, ku = threadIdx.x & 3;  // key of the split, quarter of its dimensions
-  const int d4 = threadIdx.x & 15, kg = threadIdx.x >> 4;
-  float4 kr[4];
-  float4 vr[4];
-  if (threadIdx.x < HD) qs[threadIdx.x] = P.q[(size_t)t * P.NH * HD + h * HD + threadIdx.x];
-  // K/V loads only for keys below cnt (at short contexts most lanes have
-  // none; duplicated clamped loads measured slower here)
-  if (P.kv_fp16) {
-    const __half *kvh16 = reinterpret_cast<const __half *>(P.kv);
-    if (kp < cnt) {
-      const uint4 *row = reinterpret_cast<const uint4 *>(kvh16 + kbase + (size_t)kp * HD + 16 * ku);
+// ---------------------------------------------------------------- attention
+// One (token, split, head) item, 1024 threads.  Every K/V load of the item
+// is issued at once: the score of key p of the split is formed by the four
+// lanes 4p .. 4p+3 (16 dimensions each, joined with DPP); thread (kg, d4)
+// owns V[kg + 64j][4*d4 .. 4*d4+3] for j < 4.  The last split of (token,
+// head) to finish -- counted in P.cnt; a single split is its own last --
+// merges the splits (flash-decoding merge in split order) and writes the
+// head's partial of the attention output projection to P.opart.
+struct AttnLds {
+  float *qs;    // 64: the query
+  float *es;    // 256: exp weights
+  float *sc;    // 256: scores
+  float *pv;    // 64 x 64
+  float *pv2;   // 4 x 64
+  float *own;   // 64: this split's P.V
+  float *att;   // 2 x XS: merged head output, skewed
+  float *asum;  // 2
+  int *flag;
+};
+constexpr int ATT_LDS = HD + 2 * ACH + 64 * HD + 4 * HD + HD + 2 * XS + 2 + 2;  // floats
+
+__device__ __forceinline__ AttnLds attn_lds(float *base) {
+  AttnLds A;
+  A.qs = base;
+  A.es = A.qs + HD;
+  A.sc = A.es + ACH;
+  A.pv = A.sc + ACH;
+  A.pv2 = A.pv + 64 * HD;
+  A.own = A.pv2 + 4 * HD;
+  A.att = A.own + HD;
+  A.asum = A.att + 2 * XS;
+  A.flag = reinterpret_cast<int *>(A.asum + 2);
+  return A;
+}
+
+// K rows of keys kp < nkeys (four lanes per key) and V rows (thread (kg, d4))
+// of the split starting at position s0 (coherent loads).  Keys at and past
+// nkeys are not loaded (at short contexts most lanes have none; duplicated
+// clamped loads measured slower here).
+__device__ __forceinline__ void attn_k_load(const DecParams &P, int li, int kvh, int s0, int nkeys, float4 (&kr)[4]) {
+  const uint32_t kbase = (uint32_t)kv_index(P, li, 0, kvh, s0);
+  const int kp = tid() >> 2, ku = tid() & 3;
+  if (kp < nkeys) {
+    if (P.kv_fp16) {
+      const uint32_t off = 2u * (kbase + kp * HD + 16 * ku);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const uint4 u = row[j];
+        const uint4 u = coh_ld16(P.kv, off + 16u * j);
         const __half2 *hp = reinterpret_cast<const __half2 *>(&u);
         const float2 f0 = __half22float2(hp[0]), f1 = __half22float2(hp[1]);
         const float2 f2 = __half22float2(hp[2]), f3 = __half22float2(hp[3]);
         kr[2 * j] = make_float4(f0.x, f0.y, f1.x, f1.y);
         kr[2 * j + 1] = make_float4(f2.x, f2.y, f3.x, f3.y);
       }
-    }
+    } else {
+      const uint32_t off = 4u * (kbase + kp * HD + 16 * ku);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int k = kg + 64 * j;
-      if (k < cnt) {
-        const uint2 u = *reinterpret_cast<const uint2 *>(kvh16 + vbase + (size_t)k * HD + 4 * d4);
+      for (int j = 0; j < 4; ++j) kr[j] = coh_ld4(P.kv, off + 16u * j);
+    }
+  }
+}
+
+__device__ __forceinline__ void attn_v_load(const DecParams &P, int li, int kvh, int s0, int nkeys, float4 (&vr)[4]) {
+  const uint32_t vbase = (uint32_t)kv_index(P, li, 1, kvh, s0);
+  const int d4 = tid() & 15, kg = tid() >> 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int k = kg + 64 * j;
+    if (k < nkeys) {
+      if (P.kv_fp16) {
+        const uint2 u = coh_ld8(P.kv, 2u * (vbase + k * HD + 4 * d4));
         const __half2 *hp = reinterpret_cast<const __half2 *>(&u);
         const float2 f0 = __half22float2(hp[0]), f1 = __half22float2(hp[1]);
         vr[j] = make_float4(f0.x, f0.y, f1.x, f1.y);
+      } else {
+        vr[j] = coh_ld4(P.kv, 4u * (vbase + k * HD + 4 * d4));
       }
     }
-  } else {
-    const float *kv32 = reinterpret_cast<const float *>(P.kv);
-    if (kp < cnt) {
-      const float4 *row = reinterpret_cast<const float4 *>(kv32 + kbase + (size_t)kp * HD + 16 * ku);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) kr[j] = row[j];
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int k = kg + 64 * j;
-      if (k < cnt) vr[j] = *reinterpret_cast<const float4 *>(kv32 + vbase + (size_t)k * HD + 4 * d4);
-    }
   }
-  if (solo) slice_load<SC, AT>(Lw.proj, 2 * h, D, Ro);  // W_o columns of this head, behind the K/V loads
+}
+
+// Scores, split-local softmax statistics, P.V, the merge and the head's
+// W_o slice, with the query staged in A.qs and the keys in kr/vr.  Ro holds
+// the slice when ro_loaded; the merging split of a multi-split head loads it
+// otherwise.  Returns true in the workgroup that wrote the head's output.
+template <int C>
+__device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, int h, int ns, int cnt,
+                          const float4 (&kr)[4], const float4 (&vr)[4], TileRegs<C> &Ro, bool ro_loaded,
+                          const AttnLds &A) {
+  const int D = P.D;
+  const bool solo = ns == 1;
+  const int kp = tid() >> 2, ku = tid() & 3;
+  const int d4 = tid() & 15, kg = tid() >> 4;
   __syncthreads();
   float part = 0.f;
   if (kp < cnt) {
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    const float *qq = qs + 16 * ku;
+    const float *qq = A.qs + 16 * ku;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       a0 = __builtin_fmaf(qq[4 * j + 0], kr[j].x, a0);
@@ -610,156 +676,360 @@ __device__ void phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, 
   const float score = kp < cnt ? part * P.attn_scale : -INFINITY;
   // softmax statistics, reduced by every wave itself (no cross-wave
   // exchange): the scores, then the weights, go through LDS once each
-  const int lane = threadIdx.x & 63;
-  if (ku == 0) sc[kp] = score;
+  const int lane = tid() & 63;
+  if (ku == 0) A.sc[kp] = score;
   __syncthreads();
   float ml = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) ml = fmaxf(ml, sc[lane + 64 * j]);  // -inf past cnt
+  for (int j = 0; j < 4; ++j) ml = fmaxf(ml, A.sc[lane + 64 * j]);  // -inf past cnt
   const float mx = wave_max(ml);
   const float e = kp < cnt ? expf(score - mx) : 0.f;
-  if (ku == 0) es[kp] = e;
+  if (ku == 0) A.es[kp] = e;
   __syncthreads();
   float ll = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) ll += es[lane + 64 * j];
+  for (int j = 0; j < 4; ++j) ll += A.es[lane + 64 * j];
   const float l = wave_sum(ll);
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int k = kg + 64 * j;
     if (k < cnt) {
-      const float ek = es[k];
+      const float ek = A.es[k];
       acc.x = __builtin_fmaf(ek, vr[j].x, acc.x);
       acc.y = __builtin_fmaf(ek, vr[j].y, acc.y);
       acc.z = __builtin_fmaf(ek, vr[j].z, acc.z);
       acc.w = __builtin_fmaf(ek, vr[j].w, acc.w);
     }
   }
-  *reinterpret_cast<float4 *>(pv + kg * HD + 4 * d4) = acc;
+  *reinterpret_cast<float4 *>(A.pv + kg * HD + 4 * d4) = acc;
   __syncthreads();
-  if (threadIdx.x < 4 * HD) {  // key groups 16q .. 16q+15 of dimension d
-    const int d = threadIdx.x & (HD - 1), q = threadIdx.x >> 6;
+  if (tid() < 4 * HD) {  // key groups 16q .. 16q+15 of dimension d
+    const int d = tid() & (HD - 1), q = tid() >> 6;
     float a = 0.f;
 #pragma unroll
-    for (int g = 0; g < 16; ++g) a += pv[(16 * q + g) * HD + d];
-    pv2[q * HD + d] = a;
+    for (int g = 0; g < 16; ++g) a += A.pv[(16 * q + g) * HD + d];
+    A.pv2[q * HD + d] = a;
   }
   __syncthreads();
-  if (threadIdx.x < HD) own[threadIdx.x] = (pv2[threadIdx.x] + pv2[HD + threadIdx.x]) +
-                                           (pv2[2 * HD + threadIdx.x] + pv2[3 * HD + threadIdx.x]);
+  if (tid() < HD)
+    A.own[tid()] = (A.pv2[tid()] + A.pv2[HD + tid()]) + (A.pv2[2 * HD + tid()] + A.pv2[3 * HD + tid()]);
+  // split partials of (t, h): [nsplit_max][APS] floats (m, l, pad, pad, acc[64])
   const float *parts = P.attp + (size_t)(t * P.NH + h) * P.nsplit_max * APS;
   if (!solo) {
     // publish this split, then count it; the last one merges
     float *dst = P.attp + ((size_t)(t * P.NH + h) * P.nsplit_max + sp) * APS;
     __syncthreads();
-    if (threadIdx.x < HD) dst[4 + threadIdx.x] = own[threadIdx.x];
-    if (threadIdx.x == 0) {
-      dst[0] = mx;
-      dst[1] = l;
+    if (tid() < HD) coh_stf(dst, 4u * (4 + tid()), A.own[tid()]);
+    if (tid() == 0) {
+      coh_stf(dst, 0, mx);
+      coh_stf(dst, 4, l);
     }
-    __threadfence();
+    wait_stores();
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid() == 0) {
       unsigned *c = P.cnt + t * P.NH + h;
       const unsigned arrived = atomicAdd(c, 1u);
-      flag[0] = arrived == (unsigned)(ns - 1);
-      if (flag[0]) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      A.flag[0] = arrived == (unsigned)(ns - 1);
+      if (A.flag[0]) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (!flag[0]) return;
-    __threadfence();
-    slice_load<SC, AT>(Lw.proj, 2 * h, D, Ro);
+    if (!A.flag[0]) return false;
+    if (!ro_loaded) slice_load<C, AT>(Lw.proj, 2 * h, D, Ro);
   }
   __syncthreads();
-  if (threadIdx.x < HD) {
-    const int d = threadIdx.x;
+  if (tid() < HD) {
+    const int d = tid();
     float v;
     if (solo) {
-      v = own[d] / l;  // the merge below with one split: weight expf(0) = 1
+      v = A.own[d] / l;  // the merge below with one split: weight expf(0) = 1
     } else {
-      float M = sp == 0 ? mx : parts[0];
-      for (int j = 1; j < ns; ++j) M = fmaxf(M, j == sp ? mx : parts[j * APS]);
-      const float m0 = sp == 0 ? mx : parts[0], l0 = sp == 0 ? l : parts[1], a0 = sp == 0 ? own[d] : parts[4 + d];
+      float M = sp == 0 ? mx : coh_ldf(parts, 0);
+      for (int j = 1; j < ns; ++j) M = fmaxf(M, j == sp ? mx : coh_ldf(parts, 4u * (j * APS)));
+      const float m0 = sp == 0 ? mx : coh_ldf(parts, 0), l0 = sp == 0 ? l : coh_ldf(parts, 4),
+                  a0 = sp == 0 ? A.own[d] : coh_ldf(parts, 4u * (4 + d));
       const float w0 = expf(m0 - M);
       float ls = __builtin_fmaf(l0, w0, 0.f), as = __builtin_fmaf(a0, w0, 0.f);
       for (int j = 1; j < ns; ++j) {
-        const float mj = j == sp ? mx : parts[j * APS];
-        const float lj = j == sp ? l : parts[j * APS + 1];
-        const float aj = j == sp ? own[d] : parts[j * APS + 4 + d];
+        const float mj = j == sp ? mx : coh_ldf(parts, 4u * (j * APS));
+        const float lj = j == sp ? l : coh_ldf(parts, 4u * (j * APS + 1));
+        const float aj = j == sp ? A.own[d] : coh_ldf(parts, 4u * (j * APS + 4 + d));
         const float w = expf(mj - M);
         ls = __builtin_fmaf(lj, w, ls);
         as = __builtin_fmaf(aj, w, as);
       }
       v = as / ls;
     }
-    att[skew(d)] = v;
+    A.att[skew(d)] = v;
+    // the two group sums of the head output (lanes 0-31, 32-63)
+    const float rs = row16_sum(v);
+    const float ga = readlane_f(rs, 0) + readlane_f(rs, 16), gb = readlane_f(rs, 32) + readlane_f(rs, 48);
+    if (d == 0) A.asum[0] = ga;
+    if (d == 32) A.asum[1] = gb;
   }
   __syncthreads();
-  if (threadIdx.x < 2) {
-    float s = 0.f;
+  slice_gemv<C, AT>(Ro, D, A.att, A.asum, P.opart + (size_t)(t * P.NH + h) * D);
+  return true;
+}
+
+// Multi-token passes: the item reads its query and the K/V rows that the
+// QKV phase stored.
+template <bool FLOW, class W>
+__device__ bool phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, int item, const Step &st,
+                           float *smem, W &&wait) {
+  const int per_tok = P.NH * P.nsplit_max;
+  const int t = item / per_tok;
+  const int rem = item - t * per_tok;
+  const int sp = rem / P.NH, h = rem - sp * P.NH;
+  if (t >= m || st.done) return false;
+  const int pos = st.pos0 + t;
+  const int s0 = sp * ACH;
+  if (s0 > pos) return false;
+  const int ns = pos / ACH + 1;
+  TileRegs<SC> Ro;
+  if (FLOW) {
+    slice_load<SC, AT>(Lw.proj, 2 * h, P.D, Ro);  // W_o columns of this head
+    if (wait()) return false;
+  }
+  const int cnt = min(ACH, pos + 1 - s0);
+  const AttnLds A = attn_lds(smem);
+  float4 kr[4], vr[4];
+  if (tid() < HD) A.qs[tid()] = coh_ldf(P.q, 4u * ((t * P.NH + h) * HD + tid()));
+  attn_k_load(P, li, h / (P.NH / P.NKV), s0, cnt, kr);
+  attn_v_load(P, li, h / (P.NH / P.NKV), s0, cnt, vr);
+  const bool ro = FLOW || ns == 1;
+  if (!FLOW && ns == 1) slice_load<SC, AT>(Lw.proj, 2 * h, P.D, Ro);  // behind the K/V loads
+  return attn_core<SC>(P, Lw, t, sp, h, ns, cnt, kr, vr, Ro, ro, A);
+}
+
+// Weights and other inputs of a fused decode attention item that do not
+// depend on the previous phase: the q/k/v tile, the head's W_o slice, this
+// thread's RoPE entries (gpt2: its row's bias) and the norm gains.
+template <int AQC>
+__device__ __forceinline__ void attn1_pre(const DecParams &P, const LayerW &Lw, int rq, int rk, int rv, int h, int pos,
+                                          int row_own, const float *rbias, TileRegs<AQC> &Wt, TileRegs<SC> &Ro,
+                                          float &c_own, float &s_own, GainsReg &GR) {
+  const int ng = P.D >> 5;
+  tile_load3<AQC>(Lw.qkv, rq, rk, rv, ng, Wt);
+  slice_load<SC, AT>(Lw.proj, 2 * h, P.D, Ro);
+  const size_t ri = (size_t)min(pos, P.max_seq - 1) * HD + lane_id();
+  const float *pc = P.arch == 1 ? Lw.qkv_b + min(row_own, rv + HD - 1) : P.rope_cos + ri;
+  const float *ps = P.arch == 1 ? pc : P.rope_sin + ri;
+  c_own = *pc;
+  s_own = *ps;
+  gains_load(P, Lw.n1, rbias, GR);
+}
+
+// Single-token attention item (split sp, head h) with the QKV projection
+// fused in: the item forms its own query head and its K/V head's rows of
+// attn.qkv from the residual (the K/V rows are formed again by every query
+// head that shares them), then attends over its split.  The split holding
+// the current position takes the new K/V row from LDS, rounded as the cache
+// stores it; the first query head of the group writes it to the cache.
+// Every row has the arithmetic of phase_qkv (same chunk partials, same row
+// order), so the step matches a multi-token pass bit for bit.
+template <bool FLOW, int AQC, class W>
+__device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int item, const Step &st, float *smem,
+                            W &&wait) {
+  const int sp = item / P.NH, h = item - sp * P.NH;
+  if (st.done) return false;
+  const int pos = st.pos0;
+  const int s0 = sp * ACH;
+  if (s0 > pos) return false;
+  const int ns = pos / ACH + 1;
+  const bool last = sp == ns - 1;
+  const int rep = P.NH / P.NKV, kvh = h / rep;
+  const bool writer = last && h % rep == 0;
+  const int D = P.D, ng = D >> 5, nq = D >> 2;
+  const int nch = 3 * HD * ng;
+  const int cnt = min(ACH, pos + 1 - s0);
+  const bool gpt2 = P.arch == 1;
+  const float *rbias = gpt2 && li > 0 ? Lw.prev_mproj_b : nullptr;
+  const int nb = (P.nchunk + PB - 1) / PB;
+  float *gl = smem, *xs = gl + al4(3 * D), *xsum = xs + ng * XS, *part = xsum + al4(ng);
+  float *blk = part + nch, *red = blk + nb * D, *kvn = red + 32;  // kvn: the new K row (64) then V row (64)
+  const AttnLds A = attn_lds(kvn + 2 * HD);
+  const int wv = wave_id(), lane = lane_id();
+  // rows of the fused tile: [q head h | K head kvh | V head kvh], 64 each
+  const int rq = h * HD, rk = (P.NH + kvh) * HD, rv = (P.NH + P.NKV + kvh) * HD;
+  TileRegs<AQC> Wt;
+  TileRegs<SC> Ro;
+  GainsReg GR;
+  float c_own = 0.f, s_own = 0.f;
+  float4 kr[4], vr[4];
+  ResidReg R0;
+  float4 base = make_float4(0.f, 0.f, 0.f, 0.f);
+  // wave w < 3 forms row (w: q, k, v) lane d of the tile: its RoPE entries
+  // at pos (q and k) or its bias (gpt2)
+  const int row_own = rq + min(wv, 2) * (rk - rq) + (wv >= 2 ? rv - rk - (rk - rq) : 0) + lane;
+  // The cached K rows are loaded once the residual's block sums are formed
+  // (their registers are then free), the V rows once the q/k/v tile is
+  // consumed; their latency overlaps the norm, the q/k/v rows and the scores.
+  if (FLOW) {
+    attn1_pre(P, Lw, rq, rk, rv, h, pos, row_own, rbias, Wt, Ro, c_own, s_own, GR);
+    gains_store(P, rbias, GR, gl);
+    if (wait()) return false;
+    if (li > 0) {
+      base = col_base_load(P.xb, nq);
+      resid_blocks(P.dpart, nq, P.nchunk, blk);
+    }
+  } else {
+    // activations first, then the weights (loads retire in issue order)
+    if (li > 0) {
+      base = col_base_load(P.xb, nq);
+      resid_blocks_load(P.dpart, nq, P.nchunk, 0, R0);
+    }
+    attn1_pre(P, Lw, rq, rk, rv, h, pos, row_own, rbias, Wt, Ro, c_own, s_own, GR);
+    if (li > 0) resid_blocks_rest(P.dpart, nq, P.nchunk, R0, blk);
+    gains_store(P, rbias, GR, gl);
+  }
+  // stage boundaries are fixed (sched_barrier) so that the tile, the K rows
+  // and the V rows are not all held at once
+  __builtin_amdgcn_sched_barrier(0);
+  attn_k_load(P, li, kvh, s0, last ? cnt - 1 : cnt, kr);  // cached positions: written by earlier steps
+  __builtin_amdgcn_sched_barrier(0);
+  // the residual (layer 0: the embedding) and the norm
+  if (li == 0) base = embed_col(P, min(max(st_ld(P, ST_OFF(tok)), 0), P.V - 1), min(pos, P.max_seq - 1));
+  __syncthreads();
+  const float4 x = li == 0 ? base : col_finish(blk, nq, P.nchunk, base, gl, D, rbias != nullptr);
+  col_norm(P, x, gl, red, xs, xsum, ColOut{item == 0 ? P.xa : nullptr});
+  __syncthreads();
+  tile_partials<AQC>(Wt, ng, nch, 1, xs, xsum, part);
+  __builtin_amdgcn_sched_barrier(0);
+  attn_v_load(P, li, kvh, s0, last ? cnt - 1 : cnt, vr);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+  // rows: wave 0 the query, wave 1 the key, wave 2 the value (lane d)
+  if (wv < 3) {
+    float v = row_sum(part + (wv * HD + lane) * ng, ng);
+    if (gpt2) {
+      v = v + c_own;  // the bias
+    } else if (wv < 2) {
+      const float mate = __shfl_xor(v, 32);  // rotate-half partner d +- 32
+      v = __builtin_fmaf(v, c_own, (lane < 32 ? -mate : mate) * s_own);
+    }
+    if (wv == 0) {
+      A.qs[lane] = v;
+    } else {
+      const size_t k = kv_index(P, li, wv - 1, kvh, pos) + lane;
+      float r = v;
+      if (P.kv_fp16) {
+        const __half hv = __float2half_rn(v);
+        r = __half2float(hv);
+        if (writer) coh_sth(P.kv, 2u * (uint32_t)k, __half_as_ushort(hv));
+      } else if (writer) {
+        coh_stf(P.kv, 4u * (uint32_t)k, v);
+      }
+      kvn[(wv - 1) * HD + lane] = r;
+    }
+  }
+  __syncthreads();
+  if (last) {
+    // the current position (key cnt - 1 of this split) from LDS
+    const int kp = tid() >> 2, ku = tid() & 3, d4 = tid() & 15, kg = tid() >> 4;
+    if (kp == cnt - 1) {
 #pragma unroll
-    for (int k = 0; k < 32; ++k) s += att[threadIdx.x * XS + k];
-    asum[threadIdx.x] = s;
+      for (int j = 0; j < 4; ++j) kr[j] = reinterpret_cast<const float4 *>(kvn)[4 * ku + j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (kg + 64 * j == cnt - 1) vr[j] = reinterpret_cast<const float4 *>(kvn + HD)[d4];
   }
-  __syncthreads();
-  slice_gemv<SC, AT>(Ro, D, att, asum, P.opart + (size_t)(t * P.NH + h) * D);
+  return attn_core<SC>(P, Lw, 0, sp, h, ns, cnt, kr, vr, Ro, true, A);
 }
 
 // Hidden units [item*UNITS, (item+1)*UNITS): gate/up (or fc) rows, the
 // activation, then the units' two-group slice of the down projection.
-__device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item, bool done, float *smem) {
-  const int D = P.D, ng = D >> 5;
-  const bool gpt2 = P.arch == 1;
-  const int r0 = item * UNITS;
-  const int nch = UNITS * ng;
-  ResidPre<MT> RP;
-  resid_prefetch<MT>(P.xa, P.opart, P.NH, gpt2 ? Lw.proj_b : nullptr, 0, D, RP);
-  const Gains<MT> G = load_gains<MT>(P, Lw.n2);  // before the weights (loads retire in issue order)
+struct MlpPre {
+  TileRegs<MC> Rg, Ru, Rd;
+  float fcb;
+};
+
+__device__ __forceinline__ void mlp_pre_up(const DecParams &P, const LayerW &Lw, int item, MlpPre &M) {
+  const int ng = P.D >> 5, r0 = item * UNITS;
   // gate/up chunk c = tid + j*S (S = (MT / ng) * ng): every chunk of a thread
   // is group tid % ng, so its activations are read from LDS once
   const int S = (MT / ng) * ng;
-  TileRegs<MC> Rg, Ru, Rd;
-  tile_load_strided<MC>(Lw.w1, r0, UNITS, ng, S, Rg);
-  if (!gpt2) tile_load_strided<MC>(Lw.w3, r0, UNITS, ng, S, Ru);
-  if (done) return;
+  tile_load_strided<MC>(Lw.w1, r0, UNITS, ng, S, M.Rg);
+  if (P.arch != 1) tile_load_strided<MC>(Lw.w3, r0, UNITS, ng, S, M.Ru);
   // unconditional load (llama reads its norm gains instead and ignores it)
-  const float fcb = (gpt2 ? Lw.fc_b + r0 : Lw.n2)[threadIdx.x & (UNITS - 1)];
-  float *red = smem, *xs = red + 20, *xsum = xs + m * ng * XS, *part = xsum + m * ng;  // part: gate || up
-  float *hs = smem + al4(20 + (size_t)m * ng * XS + m * ng + 2 * nch);
-  float *hsum = hs + m * 2 * XS, *blk = hsum + al4(2 * m);
-  stage_residual<MT>(P.xa, P.opart, P.NH, gpt2 ? Lw.proj_b : nullptr, 0, m, D, xs, item == 0 ? P.xb : nullptr, blk,
-                     RP);
-  norm_staged<MT>(P, xs, xsum, red, m, G);
-  slice_load<MC, MT>(Lw.w2, 2 * item, D, Rd);  // needed last: behind everything the prologue reads
-  const int g = threadIdx.x % ng;
+  M.fcb = (P.arch == 1 ? Lw.fc_b + r0 : Lw.n2)[lane_id()];
+}
+
+template <bool FLOW, class W>
+__device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item, const Step &st, float *smem,
+                          W &&wait) {
+  const int D = P.D, ng = D >> 5, nq = D >> 2;
+  const bool gpt2 = P.arch == 1;
+  const int nch = UNITS * ng;
+  const int S = (MT / ng) * ng;
+  const int nb = (P.NH + PB - 1) / PB;
+  float *gl = smem, *xs = gl + al4(3 * D), *xsum = xs + m * ng * XS, *part = xsum + al4(m * ng);  // part: 2 x (gate || up)
+  float *hs = part + 4 * nch, *hsum = hs + m * 2 * XS, *blk = hsum + al4(2 * m);  // blk: 2 x nb * D, then red
+  float *red = blk + 2 * nb * D;
+  const float *rbias = gpt2 ? Lw.proj_b : nullptr;
+  MlpPre M;
+  GainsReg GR;
+  if (FLOW) {
+    mlp_pre_up(P, Lw, item, M);
+    slice_load<MC, MT>(Lw.w2, 2 * item, D, M.Rd);
+    gains_load(P, Lw.n2, rbias, GR);
+    gains_store(P, rbias, GR, gl);
+    if (wait()) return;
+  }
+  const int wv = wave_id(), lane = lane_id();
+  float4 base = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (!FLOW) {
+    base = col_base_load(P.xa, nq);
+    ResidReg R0;
+    resid_blocks_load(P.opart, nq, P.NH, 0, R0);
+    gains_load(P, Lw.n2, rbias, GR);
+    mlp_pre_up(P, Lw, item, M);  // before the down slice (loads retire in issue order)
+    if (st.done) return;
+    resid_blocks_rest(P.opart, nq, P.NH, R0, blk);
+    gains_store(P, rbias, GR, gl);
+  }
   for (int t = 0; t < m; ++t) {
-    // gate and up chunk partials of this token in one pass (the arithmetic
-    // of tile_compute), one barrier, then wave 0 (unit r = lane) forms the
-    // rows, the activation and the two group sums of h
+    float *bt = blk + (t & 1) * nb * D;
+    if (FLOW || t > 0) {
+      base = col_base_load(P.xa + (size_t)t * D, nq);
+      resid_blocks(P.opart + (size_t)t * P.NH * D, nq, P.NH, bt);
+    }
+    __syncthreads();
+    col_norm(P, col_finish(bt, nq, P.NH, base, gl, D, gpt2), gl, red, xs + t * ng * XS, xsum + t * ng,
+             ColOut{item == 0 ? P.xb + (size_t)t * D : nullptr});
+  }
+  if (!FLOW) slice_load<MC, MT>(Lw.w2, 2 * item, D, M.Rd);  // needed last: behind everything the prologue reads
+  __syncthreads();
+  const int g = tid() % ng;
+  for (int t = 0; t < m; ++t) {
+    // gate and up chunk partials of token t (the arithmetic of
+    // tile_compute), one barrier, then the token's wave (unit r = lane)
+    // forms the rows, the activation and the two group sums of h
+    float *pt = part + (t & 1) * 2 * nch;
     float xr[32];
     load_group(xs + (t * ng + g) * XS, xr);
     const float xsg = 8.f * xsum[t * ng + g];
 #pragma unroll
     for (int k = 0; k < MC; ++k) {
-      const int c = threadIdx.x + k * S;
-      if ((int)threadIdx.x < S && c < nch) {
+      const int c = tid() + k * S;
+      if ((int)tid() < S && c < nch) {
         float dg, du;
-        q4_chunk_dot2_reg(Rg.w[k], gpt2 ? Rg.w[k] : Ru.w[k], xr, dg, du);
-        part[c] = (dg - xsg) * Rg.s[k];
-        if (!gpt2) part[nch + c] = (du - xsg) * Ru.s[k];
+        q4_chunk_dot2_reg(M.Rg.w[k], gpt2 ? M.Rg.w[k] : M.Ru.w[k], xr, dg, du);
+        pt[c] = (dg - xsg) * M.Rg.s[k];
+        if (!gpt2) pt[nch + c] = (du - xsg) * M.Ru.s[k];
       }
     }
     __syncthreads();
-    if (threadIdx.x < UNITS) {  // exactly wave 0
-      const int r = threadIdx.x;
-      const float gv = row_sum(part + r * ng, ng);
+    if (wv == (t & (NWV - 1))) {
+      const int r = lane;
+      const float gv = row_sum(pt + r * ng, ng);
       float h;
       if (gpt2) {
-        const float v = gv + fcb;
+        const float v = gv + M.fcb;
         h = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
       } else {
-        h = (gv / (1.0f + expf(-gv))) * row_sum(part + nch + r * ng, ng);
+        h = (gv / (1.0f + expf(-gv))) * row_sum(pt + nch + r * ng, ng);
       }
       hs[t * 2 * XS + skew(r)] = h;
       const float rs = row16_sum(h);
@@ -767,29 +1037,41 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item,
       if (r == 0) hsum[2 * t] = ga;
       if (r == 32) hsum[2 * t + 1] = gb;
     }
-    __syncthreads();
   }
+  __syncthreads();
   for (int t = 0; t < m; ++t)
-    slice_gemv<MC, MT>(Rd, D, hs + t * 2 * XS, hsum + 2 * t, P.dpart + ((size_t)t * P.nchunk + item) * D);
+    slice_gemv<MC, MT>(M.Rd, D, hs + t * 2 * XS, hsum + 2 * t, P.dpart + ((size_t)t * P.nchunk + item) * D);
 }
 
-// Item t: the residual after the last layer, final norm -> xn[t] (only the
-// rows the lm_head reads).
-__device__ void phase_final(const DecParams &P, int m, int item, bool done, float *smem) {
-  const PassState &S = *P.st;
-  if (S.lm_rows == 0 || done) return;
-  const int tb = S.lm_rows == 1 ? m - 1 : 0;
+// The last layer's residual and the final norm of token t, on wave 0:
+// xs/xsum (LDS) for the lm_head of the persistent kernel, or xn/xnsum
+// (coherent stores) for the lm_head kernel.  blk needs nb * D floats; the
+// caller has staged the norm_f gains in gl.
+__device__ __forceinline__ void final_row(const DecParams &P, int t, float *blk, const float *gl, float *xs,
+                                          float *xsum, bool to_global) {
+  const int D = P.D, nq = D >> 2;
+  const float4 base = col_base_load(P.xb + (size_t)t * D, nq);
+  resid_blocks(P.dpart + (size_t)t * P.nchunk * D, nq, P.nchunk, blk);
+  __syncthreads();
+  const float4 x = col_finish(blk, nq, P.nchunk, base, gl, D, P.arch == 1);
+  col_norm(P, x, gl, blk + ((P.nchunk + PB - 1) / PB) * D, xs, xsum,
+           ColOut{nullptr, to_global ? P.xn + (size_t)t * D : nullptr, to_global ? P.xnsum + t * 32 : nullptr});
+}
+
+// Kernel-per-phase mode: item t writes xn[t], xnsum[t] (only the rows the
+// lm_head reads).
+__device__ void phase_final(const DecParams &P, int m, int item, const Step &st, float *smem) {
+  const int lm_rows = st_ld(P, ST_OFF(lm_rows));
+  if (lm_rows == 0 || st.done) return;
+  const int tb = lm_rows == 1 ? m - 1 : 0;
   const int t = item;
   if (t < tb || t >= m) return;
-  const int D = P.D, ng = D >> 5;
-  ResidPre<FT> RP;
-  resid_prefetch<FT>(P.xb, P.dpart, P.nchunk, P.arch == 1 ? P.last_mproj_b : nullptr, t, D, RP);
-  const Gains<FT> G = load_gains<FT>(P, P.norm_f);
-  // red: 20 floats; xsum: ng <= 32 (unused by the lm_head)
-  float *red = smem, *xsum = smem + 20, *xs = smem + 52, *blk = xs + ng * XS;
-  stage_residual<FT>(P.xb, P.dpart, P.nchunk, P.arch == 1 ? P.last_mproj_b : nullptr, t, 1, D, xs, nullptr, blk, RP);
-  norm_staged<FT>(P, xs, xsum, red, 1, G);
-  for (int i = threadIdx.x; i < D; i += FT) P.xn[(size_t)t * D + i] = xs[skew(i)];
+  float *gl = smem, *blk = gl + al4(3 * P.D);
+  const float *rbias = P.arch == 1 ? P.last_mproj_b : nullptr;
+  GainsReg GR;
+  gains_load(P, P.norm_f, rbias, GR);
+  gains_store(P, rbias, GR, gl);
+  final_row(P, t, blk, gl, nullptr, nullptr, true);
 }
 
 // argmaxGpt2 (infer.js:252-287) adjustment of one logit given the banned and
@@ -808,23 +1090,32 @@ struct LmLds {
   int *lists;
 };
 
+// Row tiles of the tied lm_head: rpt rows each, ntiles tiles.  The
+// kernel-per-phase mode uses 256-thread tiles of P.lm_rpt rows; the
+// persistent kernel uses 1024-thread tiles.  Every row's arithmetic is the
+// same (tile_compute), and the first maximum does not depend on the tiling.
+struct LmGeom {
+  int rpt, ntiles;
+};
+
 // One lm_head tile whose weights are in R: logits rows [r0, r0+nr) of the m
 // tokens from tb, then the tile's first maximum per token (gpt2 chain: with
 // the argmaxGpt2 adjustments).
-__device__ __forceinline__ void lm_tile(const DecParams &P, const TileRegs<TC> &R, int tile, int tb, int m,
-                                        const LmLds &s, bool penal, int nban, int nrec) {
-  const int ng = P.D >> 5, rpt = P.lm_rpt;
+template <int TCN, int NT>
+__device__ __forceinline__ void lm_tile(const DecParams &P, const LmGeom &L, const TileRegs<TCN> &R, int tile, int tb,
+                                        int m, const LmLds &s, bool penal, int nban, int nrec) {
+  const int ng = P.D >> 5, rpt = L.rpt;
   const int r0 = tile * rpt, nr = min(rpt, P.V - r0);
-  tile_compute<TC>(R, nr, ng, nr * ng, m, s.xs, s.xsum, threadIdx.x % ng, WG % ng, s.part, s.out, rpt);
-  for (int e = threadIdx.x; e < m * nr; e += WG) {
+  tile_compute<TCN, NT>(R, nr, ng, nr * ng, m, s.xs, s.xsum, tid() % ng, NT % ng, s.part, s.out, rpt);
+  for (int e = tid(); e < m * nr; e += NT) {
     const int t = e / nr, r = e - t * nr;
     P.logits[(size_t)(tb + t) * P.V + r0 + r] = s.out[t * rpt + r];
   }
-  if (threadIdx.x < 64) {
+  if (tid() < 64) {
     for (int t = 0; t < m; ++t) {
       float bv = -INFINITY;
       int bi = 0x7fffffff;
-      for (int r = threadIdx.x; r < nr; r += 64) {
+      for (int r = tid(); r < nr; r += 64) {
         float v = s.out[t * rpt + r];
         if (penal) v = gpt2_adjust(v, r0 + r, s.lists + 34, nban, s.lists + 2, nrec);
         if (amax_better(v, r0 + r, bv, bi)) {
@@ -833,102 +1124,132 @@ __device__ __forceinline__ void lm_tile(const DecParams &P, const TileRegs<TC> &
         }
       }
       wave_argmax(bv, bi);
-      if (threadIdx.x == 0) {
-        P.amv[(size_t)(tb + t) * P.lm_tiles + tile] = bv;
-        P.ami[(size_t)(tb + t) * P.lm_tiles + tile] = bi;
+      if (tid() == 0) {
+        coh_stf(P.amv, 4u * ((tb + t) * P.lm_tiles + tile), bv);
+        coh_sti(P.ami, 4u * ((tb + t) * P.lm_tiles + tile), bi);
       }
     }
   }
   __syncthreads();
 }
 
-__device__ __forceinline__ void lm_load(const DecParams &P, int tile, TileRegs<TC> &R) {
-  if (tile < P.lm_tiles) {
-    const int ng = P.D >> 5, r0 = tile * P.lm_rpt, nr = min(P.lm_rpt, P.V - r0);
-    tile_load<TC>(P.lm, r0, nr, 0, ng, nr * ng, R);
+template <int TCN, int NT>
+__device__ __forceinline__ void lm_load(const DecParams &P, const LmGeom &L, int tile, TileRegs<TCN> &R) {
+  if (tile < L.ntiles) {
+    const int ng = P.D >> 5, r0 = tile * L.rpt, nr = min(L.rpt, P.V - r0);
+    tile_load<TCN, NT>(P.lm, r0, nr, 0, ng, nr * ng, R);
   }
 }
 
-// lm_head over row tiles wg, wg + nwg, ...; the next tile's weights are
-// loaded while the current one is computed (two register sets used in
-// turn, each with constant indices so both stay in VGPRs).
-__device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, bool done, float *smem) {
-  if (wg >= P.lm_tiles) return;
-  const PassState &S = *P.st;
-  const int lm_rows = S.lm_rows;
-  if (lm_rows == 0 || done) return;
+// infer.js:252-287 over hist[0..n) (thread 0): banned = tokens that would
+// repeat the last 3-gram, recent = the last 32 tokens.
+__device__ __forceinline__ void gpt2_lists(const DecParams &P, int *lists) {
+  const int n = st_ld(P, ST_OFF(n_hist));
+  int nrec = 0, nban = 0;
+  for (int h = max(0, n - 32); h < n; ++h) lists[2 + nrec++] = coh_ldi(P.hist, 4u * h);
+  if (n >= 2) {
+    const int t1 = coh_ldi(P.hist, 4u * (n - 2)), t2 = coh_ldi(P.hist, 4u * (n - 1));
+    for (int h = 0; h < n - 2; ++h)
+      if (coh_ldi(P.hist, 4u * h) == t1 && coh_ldi(P.hist, 4u * (h + 1)) == t2) lists[34 + nban++] = coh_ldi(P.hist, 4u * (h + 2));
+  }
+  lists[0] = nban;
+  lists[1] = nrec;
+}
+
+// Kernel-per-phase lm_head: row tiles wg, wg + nwg, ...; the normed rows and
+// their group sums come from FINAL (xn, xnsum); the next tile's weights are
+// loaded while the current one is computed (two register sets used in turn,
+// each with constant indices so both stay in VGPRs).
+__device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, const Step &st, float *smem) {
+  const LmGeom L{P.lm_rpt, P.lm_tiles};
+  if (wg >= L.ntiles) return;
+  const int lm_rows = st_ld(P, ST_OFF(lm_rows));
+  if (lm_rows == 0 || st.done) return;
   const int tb = lm_rows == 1 ? m_all - 1 : 0;
   const int m = m_all - tb;
-  const int D = P.D, ng = D >> 5, rpt = P.lm_rpt;
-  // the normed rows first, then the weights (loads retire in issue order)
-  float4 xv[4];
-  stage_rows_load<LT>(P.xn + (size_t)tb * D, D, m, D, 0, xv);
+  const int D = P.D, ng = D >> 5, nq = D >> 2;
   TileRegs<TC> Ra, Rb;
   int tile = wg;
-  lm_load(P, tile, Ra);
+  // the normed rows first, then the weights (loads retire in issue order)
+  float4 xv[4];
+  float sv = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int f = min(tid() + k * LT, m * nq - 1);  // branch-free; extra lanes unused
+    xv[k] = coh_ld4(P.xn + (size_t)tb * D, 16u * f);
+  }
+  {
+    const int f = min(tid(), m * ng - 1);
+    sv = coh_ldf(P.xnsum, 4u * ((tb + f / ng) * 32 + f % ng));
+  }
+  lm_load<TC, LT>(P, L, tile, Ra);
   LmLds s;
   s.xs = smem;
   s.xsum = s.xs + m * ng * XS;
-  s.part = s.xsum + m * ng;
-  s.out = s.part + m * TC * WG;
-  s.lists = reinterpret_cast<int *>(s.out + m * rpt);  // [0]: nban, [1]: nrec, [2..34): rec, then ban
-  const bool penal = P.arch == 1 && S.chain;
-  if (penal && threadIdx.x == 0) {
-    // infer.js:252-287 over hist[0..n): banned = tokens that would repeat the
-    // last 3-gram, recent = the last 32 tokens.
-    const int n = S.n_hist;
-    int nrec = 0, nban = 0;
-    for (int h = max(0, n - 32); h < n; ++h) s.lists[2 + nrec++] = P.hist[h];
-    if (n >= 2) {
-      const int t1 = P.hist[n - 2], t2 = P.hist[n - 1];
-      for (int h = 0; h < n - 2; ++h)
-        if (P.hist[h] == t1 && P.hist[h + 1] == t2) s.lists[34 + nban++] = P.hist[h + 2];
+  s.part = s.xsum + al4(m * ng);
+  s.out = s.part + m * TC * LT;
+  s.lists = reinterpret_cast<int *>(s.out + m * L.rpt);  // [0]: nban, [1]: nrec, [2..34): rec, then ban
+  const bool penal = P.arch == 1 && st_ld(P, ST_OFF(chain)) != 0;
+  if (penal && tid() == 0) gpt2_lists(P, s.lists);
+  for (int base = 0; base < m * nq; base += 4 * LT) {
+    if (base > 0)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int f = min(base + tid() + k * LT, m * nq - 1);
+        xv[k] = coh_ld4(P.xn + (size_t)tb * D, 16u * f);
+      }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int f = base + tid() + k * LT;
+      if (f < m * nq) {
+        const int t = f / nq, i = 4 * (f - t * nq);
+        *reinterpret_cast<float4 *>(s.xs + (t * ng + (i >> 5)) * XS + (i & 31)) = xv[k];
+      }
     }
-    s.lists[0] = nban;
-    s.lists[1] = nrec;
   }
-  stage_rows_store<LT>(m, D, 0, xv, s.xs);
-  stage_rows<LT>(P.xn + (size_t)tb * D, D, m, D, s.xs, 4 * LT);
+  if (tid() < m * ng) s.xsum[tid()] = sv;
+  for (int f = tid() + LT; f < m * ng; f += LT) s.xsum[f] = coh_ldf(P.xnsum, 4u * ((tb + f / ng) * 32 + f % ng));
   __syncthreads();
-  stage_group_sums(s.xs, s.xsum, m, ng);
   const int nban = penal ? s.lists[0] : 0, nrec = penal ? s.lists[1] : 0;
-  while (tile < P.lm_tiles) {
-    lm_load(P, tile + nwg, Rb);
-    lm_tile(P, Ra, tile, tb, m, s, penal, nban, nrec);
+  while (tile < L.ntiles) {
+    lm_load<TC, LT>(P, L, tile + nwg, Rb);
+    lm_tile<TC, LT>(P, L, Ra, tile, tb, m, s, penal, nban, nrec);
     tile += nwg;
-    if (tile >= P.lm_tiles) break;
-    lm_load(P, tile + nwg, Ra);
-    lm_tile(P, Rb, tile, tb, m, s, penal, nban, nrec);
+    if (tile >= L.ntiles) break;
+    lm_load<TC, LT>(P, L, tile + nwg, Ra);
+    lm_tile<TC, LT>(P, L, Rb, tile, tb, m, s, penal, nban, nrec);
     tile += nwg;
   }
 }
 
-__device__ void phase_argmax(const DecParams &P, bool done, float *smem) {
-  PassState &S = *P.st;
-  if (S.lm_rows == 0 || done) return;
-  const int tb = S.lm_rows == 1 ? S.ntok - 1 : 0;
+// First maximum over the tiles' (value, index) pairs of each lm row; the
+// chained decode feeds it back as the next input token.
+template <int NT>
+__device__ void phase_argmax(const DecParams &P, int ntiles, const Step &st, float *smem) {
+  const int lm_rows = st_ld(P, ST_OFF(lm_rows));
+  if (lm_rows == 0 || st.done) return;
+  const int ntok = st_ld(P, ST_OFF(ntok));
+  const int tb = lm_rows == 1 ? ntok - 1 : 0;
+  constexpr int NW = NT / 64;
   float *rv = smem;
-  int *ri = reinterpret_cast<int *>(smem + 4);
-  for (int t = tb; t < S.ntok; ++t) {
+  int *ri = reinterpret_cast<int *>(smem + NW);
+  int last = 0;
+  for (int t = tb; t < ntok; ++t) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int base = 0; base < P.lm_tiles; base += 16 * WG) {
+    for (int base = 0; base < ntiles; base += 16 * NT) {
       float vv[16];
       int iv[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {  // all loads of the batch before any compare
-        const int k = base + threadIdx.x + j * WG;
-        vv[j] = -INFINITY;
-        iv[j] = 0x7fffffff;
-        if (k < P.lm_tiles) {
-          vv[j] = P.amv[(size_t)t * P.lm_tiles + k];
-          iv[j] = P.ami[(size_t)t * P.lm_tiles + k];
-        }
+        const int k = min(base + (int)tid() + j * NT, ntiles - 1);
+        vv[j] = coh_ldf(P.amv, 4u * (t * P.lm_tiles + k));
+        iv[j] = coh_ldi(P.ami, 4u * (t * P.lm_tiles + k));
       }
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int k = base + threadIdx.x + j * WG;
-        if (k < P.lm_tiles && amax_better(vv[j], iv[j], bv, bi)) {
+        const int k = base + tid() + j * NT;
+        if (k < ntiles && amax_better(vv[j], iv[j], bv, bi)) {
           bv = vv[j];
           bi = iv[j];
         }
@@ -936,60 +1257,47 @@ __device__ void phase_argmax(const DecParams &P, bool done, float *smem) {
     }
     wave_argmax(bv, bi);
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) {
-      rv[threadIdx.x >> 6] = bv;
-      ri[threadIdx.x >> 6] = bi;
+    if ((tid() & 63) == 0) {
+      rv[tid() >> 6] = bv;
+      ri[tid() >> 6] = bi;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid() == 0) {
       float v = rv[0];
       int i = ri[0];
-      for (int w = 1; w < 4; ++w)
+      for (int w = 1; w < NW; ++w)
         if (amax_better(rv[w], ri[w], v, i)) {
           v = rv[w];
           i = ri[w];
         }
-      S.res[t] = i;
+      st_st(P, ST_OFF(res) + 4u * t, i);
+      last = i;
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0 && S.chain) {
-    int tok = S.res[S.ntok - 1];
+  if (tid() == 0 && st_ld(P, ST_OFF(chain))) {
+    int tok = last;
     if (tok < 0 || tok >= P.V) {  // no finite maximum (non-finite logits)
-      S.bad_tok = 1;
+      st_st(P, ST_OFF(bad_tok), 1);
       tok = 0;
     }
-    P.hist[S.n_hist] = tok;
-    S.n_hist = S.n_hist + 1;
-    S.tok[0] = tok;
-    S.pos0 = S.pos0 + 1;
-    if (tok == S.eos) S.done = 1;
+    const int n_hist = st_ld(P, ST_OFF(n_hist));
+    coh_sti(P.hist, 4u * n_hist, tok);
+    st_st(P, ST_OFF(n_hist), n_hist + 1);
+    st_st(P, ST_OFF(tok), tok);
+    st_st(P, ST_OFF(pos0), st.pos0 + 1);
+    if (tok == st_ld(P, ST_OFF(eos))) st_st(P, ST_OFF(done), 1);
   }
 }
 
 __host__ __device__ __forceinline__ int phase_items(const DecParams &P, int ph, int m) {
   switch (ph) {
-  case PH_QKV: return (P.NH + 2 * P.NKV) * QSPLIT;
+  case PH_QKV: return P.NH + 2 * P.NKV;
   case PH_ATTN: return m * P.NH * P.nsplit_max;
   case PH_MLP: return P.nchunk;
   case PH_FINAL: return m;
   case PH_LM: return P.lm_grid;
   default: return 1;
-  }
-}
-
-// done: the chained decode already emitted eos.  Each phase still issues
-// its first loads (they do not depend on the pass state, whose load then
-// overlaps them) but stores nothing.
-__device__ __forceinline__ void run_item(const DecParams &P, const LayerW &Lw, int ph, int m, int li, int item,
-                                         int nitems, bool done, float *smem) {
-  switch (ph) {
-  case PH_QKV: phase_qkv(P, Lw, m, li, item, done, smem); break;
-  case PH_ATTN: phase_attn(P, Lw, m, li, item, done, smem); break;
-  case PH_MLP: phase_mlp(P, Lw, m, item, done, smem); break;
-  case PH_FINAL: phase_final(P, m, item, done, smem); break;
-  case PH_LM: phase_lm(P, m, item, nitems, done, smem); break;
-  default: phase_argmax(P, done, smem); break;
   }
 }
 
@@ -1008,17 +1316,241 @@ __host__ __device__ constexpr int phase_threads(int ph) {
 template <int PH, int ONE>
 __global__ __launch_bounds__(phase_threads(PH)) void k_phase(DecParams P, LayerW Lw, int li, int m) {
   extern __shared__ float4 smem4[];
-  const bool done = P.st->done != 0;
-  run_item(P, Lw, PH, ONE ? 1 : m, li, blockIdx.x, gridDim.x, done, reinterpret_cast<float *>(smem4));
+  float *smem = reinterpret_cast<float *>(smem4);
+  const Step st{st_ld(P, ST_OFF(pos0)), st_ld(P, ST_OFF(done)) != 0};
+  const int mm = ONE ? 1 : m;
+  const int item = blockIdx.x;
+  switch (PH) {
+  case PH_QKV: phase_qkv<false>(P, Lw, mm, li, item, st, smem, NoWait{}); break;
+  case PH_ATTN: phase_attn<false>(P, Lw, mm, li, item, st, smem, NoWait{}); break;
+  case PH_MLP: phase_mlp<false>(P, Lw, mm, item, st, smem, NoWait{}); break;
+  case PH_FINAL: phase_final(P, mm, item, st, smem); break;
+  case PH_LM: phase_lm(P, mm, item, gridDim.x, st, smem); break;
+  default: phase_argmax<LT>(P, P.lm_tiles, st, smem); break;
+  }
+}
+
+// The decode step's attention item (QKV fused in), one instance per tile size.
+template <int AQC>
+__global__ __launch_bounds__(AT) void k_attn1(DecParams P, LayerW Lw, int li, int m) {
+  extern __shared__ float4 smem4[];
+  float *smem = reinterpret_cast<float *>(smem4);
+  const Step st{st_ld(P, ST_OFF(pos0)), st_ld(P, ST_OFF(done)) != 0};
+  (void)m;
+  phase_attn1<false, AQC>(P, Lw, li, blockIdx.x, st, smem, NoWait{});
 }
 
 using PhaseKernel = void (*)(DecParams, LayerW, int, int);
+static const PhaseKernel kAttn1Kernels[3] = {k_attn1<4>, k_attn1<5>, k_attn1<6>};
 static const PhaseKernel kPhaseKernels[2][PH_COUNT] = {
     {k_phase<PH_QKV, 0>, k_phase<PH_ATTN, 0>, k_phase<PH_MLP, 0>, k_phase<PH_FINAL, 0>, k_phase<PH_LM, 0>,
      k_phase<PH_ARGMAX, 0>},
     {k_phase<PH_QKV, 1>, k_phase<PH_ATTN, 1>, k_phase<PH_MLP, 1>, k_phase<PH_FINAL, 1>, k_phase<PH_LM, 1>,
      k_phase<PH_ARGMAX, 1>}};
 static const char *const kPhaseNames[PH_COUNT] = {"QKV", "ATTN", "MLP", "FINAL", "LM", "ARGMAX"};
+
+// ---------------------------------------------------------------- persistent kernel
+// Mode 3: the single-token decode of `steps` chained tokens in one
+// cooperative launch of 1024-thread workgroups, one per CU.  Per layer the
+// items are the attention (split, head) items, each with its QKV rows fused
+// in, and the MLP chunks; workgroup w runs items w, w + G, ... of every layer in order, so a
+// workgroup's next weights are loaded as soon as it has finished its previous
+// item, while other workgroups still produce that item's inputs.  After its
+// last layer item every workgroup loads its lm_head tile, waits for the last
+// layer, forms the final norm itself (no separate FINAL step) and computes
+// the tile; the last workgroup to finish its tile takes the argmax.
+//
+// Ordering is by per-item epoch flags instead of kernel boundaries: when an
+// item's outputs are stored (coherent stores, then a wait for their
+// completion) the item's flag is set to the step's epoch; a consumer polls
+// the flags of exactly the items it reads.  Dependencies:
+//   ATTN(l)     <- MLP(l-1), every chunk     (l = 0: the previous step's ARGMAX)
+//   MLP(l)      <- ATTN(l), every head (set by the split that merged the head)
+//   LM          <- MLP(L-1), every chunk;   ARGMAX: the last LM workgroup
+// Every item depends only on items earlier in the order (layer, stage) and
+// every workgroup runs its items in that order, so with all workgroups
+// resident (a cooperative launch) the grid always makes progress.  Flags
+// hold epochs, which grow across launches, so they are never cleared.
+struct FlowGeom {
+  int *flags;             // [L][NH + nm] attention heads and MLP chunks, LM counter, ARGMAX
+  int ep0, steps;         // epoch of the launch's first step; chained steps
+  int na, nm, ni;         // items per layer: attention (split, head) items, MLP chunks; ni = na + nm
+  int lm_rpt, lm_tiles;   // lm_head tiles of the 1024-thread role (one per workgroup w < lm_tiles, then w + G ...)
+};
+
+constexpr int FLT = 1024;               // threads per workgroup of the persistent kernel
+constexpr unsigned kSpinLimit = 1u << 22;  // polls before a wait gives up (seconds)
+
+__device__ __forceinline__ int flag_ld(const int *f) {
+  return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void flag_st(int *f, int v) {
+  __hip_atomic_store(f, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wave 0 polls up to three flag ranges until every flag holds >= e; the
+// other waves wait at the barrier.  The poll is bounded: on time-out, or
+// once another workgroup has failed, st->err is set and the wait returns
+// (the host then reports the error; every later wait of the launch returns
+// at once, so the grid drains).
+__device__ void flow_wait(const DecParams &P, const int *f0, int n0, const int *f1, int n1, const int *f2, int n2,
+                          int e) {
+  if (tid() < 64) {
+    const int lane = tid();
+    unsigned spins = 0;
+    bool failed = __builtin_amdgcn_readfirstlane(st_ld(P, ST_OFF(err))) != 0;
+    while (!failed) {
+      bool ok = true;
+      for (int i = lane; i < n0; i += 64) ok &= flag_ld(f0 + i) >= e;
+      for (int i = lane; i < n1; i += 64) ok &= flag_ld(f1 + i) >= e;
+      for (int i = lane; i < n2; i += 64) ok &= flag_ld(f2 + i) >= e;
+      if (__all(ok)) break;
+      ++spins;
+      if ((spins & 15) == 0) failed = __builtin_amdgcn_readfirstlane(st_ld(P, ST_OFF(err))) != 0;
+      if (spins > kSpinLimit) {
+        if (lane == 0) st_st(P, ST_OFF(err), 1);
+        failed = true;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// The item's outputs are complete (every thread waits for its own stores),
+// then its flag is set.
+__device__ __forceinline__ void flow_publish(int *f, int e) {
+  wait_stores();
+  __syncthreads();
+  if (tid() == 0) flag_st(f, e);
+}
+
+// A workgroup's waits within one step.  The first wait of a step also waits
+// for the previous step's ARGMAX and reads `done` (the chain emitted eos).
+struct FlowCtl {
+  const DecParams &P;
+  const int *am_flag;
+  int e;
+  bool pending;  // the step's ARGMAX wait is still due
+  bool done;
+  __device__ bool wait(const int *f0, int n0, const int *f1 = nullptr, int n1 = 0, const int *f2 = nullptr,
+                       int n2 = 0) {
+    if (pending) {
+      flow_wait(P, am_flag, 1, nullptr, 0, nullptr, 0, e - 1);
+      pending = false;
+      done = st_ld(P, ST_OFF(done)) != 0;
+    }
+    if (done) return true;
+    if (n0 + n1 + n2) flow_wait(P, f0, n0, f1, n1, f2, n2, e);
+    return false;
+  }
+};
+
+// The persistent kernel's lm_head share of one workgroup (tiles wg, wg + G,
+// ...), after the final norm it forms itself.  Returns true when this
+// workgroup computed at least one tile.
+template <class W>
+__device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, const Step &st, float *smem, W &&wait) {
+  if (wg >= L.ntiles) return false;
+  const int D = P.D, ng = D >> 5;
+  TileRegs<FTC> Ra, Rb;
+  int tile = wg;
+  lm_load<FTC, FLT>(P, L, tile, Ra);
+  LmLds s;
+  float *gl = smem;
+  s.xs = gl + al4(3 * D);
+  s.xsum = s.xs + ng * XS;
+  s.part = s.xsum + al4(ng);
+  s.out = s.part + FTC * FLT;
+  s.lists = reinterpret_cast<int *>(s.out + L.rpt);
+  float *blk = reinterpret_cast<float *>(s.lists + 34 + P.max_seq);
+  const float *rbias = P.arch == 1 ? P.last_mproj_b : nullptr;
+  GainsReg GR;
+  gains_load(P, P.norm_f, rbias, GR);
+  gains_store(P, rbias, GR, gl);
+  if (wait()) return false;
+  const bool penal = P.arch == 1 && st_ld(P, ST_OFF(chain)) != 0;
+  if (penal && tid() == 0) gpt2_lists(P, s.lists);
+  final_row(P, 0, blk, gl, s.xs, s.xsum, false);
+  __syncthreads();
+  const int nban = penal ? s.lists[0] : 0, nrec = penal ? s.lists[1] : 0;
+  while (tile < L.ntiles) {
+    lm_load<FTC, FLT>(P, L, tile + nwg, Rb);
+    lm_tile<FTC, FLT>(P, L, Ra, tile, 0, 1, s, penal, nban, nrec);
+    tile += nwg;
+    if (tile >= L.ntiles) break;
+    lm_load<FTC, FLT>(P, L, tile + nwg, Ra);
+    lm_tile<FTC, FLT>(P, L, Rb, tile, 0, 1, s, penal, nban, nrec);
+    tile += nwg;
+  }
+  return true;
+}
+
+template <int AQC>
+__global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
+  extern __shared__ float4 smem4[];
+  float *smem = reinterpret_cast<float *>(smem4);
+  const int w = blockIdx.x, G = gridDim.x;
+  const int stride = P.NH + F.nm;
+  int *const lm_cnt = F.flags + P.L * stride;
+  int *const am_flag = lm_cnt + 1;
+  const int nlm = min(G, F.lm_tiles);  // workgroups with lm_head tiles
+  const LmGeom lg{F.lm_rpt, F.lm_tiles};
+  const int pos_start = st_ld(P, ST_OFF(pos0));
+  int *const red = reinterpret_cast<int *>(smem);
+  for (int step = 0; step < F.steps; ++step) {
+    FlowCtl C{P, am_flag, F.ep0 + step, step > 0, false};
+    const int e = C.e;
+    const Step st{pos_start + step, false};
+    for (int lv = 0; lv < P.L && !C.done; ++lv) {
+      // the layer and item indices are made opaque to the compiler: it would
+      // otherwise hoist per-thread addresses out of the loops and keep them
+      // live past the register budget of a 1024-thread workgroup
+      int li = lv;
+      asm volatile("" : "+s"(li));
+      const LayerW &Lw = P.layers[li];  // fields loaded where they are used (scalar registers are scarce)
+      int *const fl = F.flags + li * stride;
+      for (int jv = w; jv < F.ni && !C.done; jv += G) {
+        int j = jv;
+        asm volatile("" : "+s"(j));
+        if (j < F.na) {
+          const int h = j % P.NH;
+          const int *dep = fl - stride + P.NH;  // MLP chunks of the previous layer
+          const int ndep = li > 0 ? F.nm : 0;
+          const bool merged = phase_attn1<true, AQC>(P, Lw, li, j, st, smem, [&] { return C.wait(dep, ndep); });
+          if (merged && !C.done) flow_publish(fl + h, e);
+        } else {
+          const int it = j - F.na;
+          phase_mlp<true>(P, Lw, 1, it, st, smem, [&] { return C.wait(fl, P.NH); });
+          if (!C.done) flow_publish(fl + P.NH + it, e);
+        }
+      }
+    }
+    if (!C.done && w < nlm) {
+      const int *dep = F.flags + (P.L - 1) * stride + P.NH;
+      const bool did = flow_lm(P, lg, w, G, st, smem, [&] { return C.wait(dep, F.nm); });
+      if (did && !C.done) {
+        // the last lm_head workgroup to finish takes the argmax
+        wait_stores();
+        __syncthreads();
+        if (tid() == 0) {
+          const int arrived = atomicAdd(lm_cnt, 1);
+          red[0] = arrived == nlm - 1;
+          if (red[0]) __hip_atomic_store(lm_cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (red[0]) {
+          __syncthreads();
+          phase_argmax<FLT>(P, F.lm_tiles, st, smem);
+          flow_publish(am_flag, e);
+        }
+      }
+    }
+    if (C.done) break;
+  }
+}
+
+using FlowKernel = void (*)(DecParams, FlowGeom);
+static const FlowKernel kFlowKernels[3] = {k_flow<4>, k_flow<5>, k_flow<6>};
 
 }  // namespace mllm
 
@@ -1053,6 +1585,12 @@ struct mllm_model {
   size_t lds_max = 0;
   uint64_t device_bytes = 0;
   hipGraphExec_t chain_graph = nullptr;
+  // persistent kernel (exec mode 3)
+  FlowGeom flow{};
+  int flow_grid = 0;      // 0: not available on this device
+  size_t flow_lds = 0;
+  int flow_epoch = 0;     // epochs used so far (flags hold epochs, never cleared)
+  int aq_idx = 0;         // instance of the decode attention item / persistent kernel (tile size 4, 5, 6)
   hipEvent_t ev0 = nullptr, ev1 = nullptr;  // around the kernels of the last call
   std::vector<hipEvent_t> prof_ev;          // mllm_profile_decode
   float last_ms = 0.f;
@@ -1076,16 +1614,31 @@ int lm_tile_rows(int ng) { return std::max(1, std::min(TILE_TARGET, TC * WG) / n
 // the phase functions).
 size_t lds_floats(const DecParams &P, int ph, int m) {
   const size_t ngd = P.D / 32, D = P.D;
-  const size_t blk_o = (size_t)((P.NH + PB - 1) / PB) * D, blk_d = (size_t)((P.nchunk + PB - 1) / PB) * D;
+  const size_t nbo = (P.NH + PB - 1) / PB, nbd = (P.nchunk + PB - 1) / PB;
   switch (ph) {
-  case PH_QKV: return al4(20 + m * ngd * XS + m * ngd + m * 16 * ngd + m * 16) + blk_d;
-  case PH_ATTN: return HD + 2 * ACH + 64 * HD + 4 * HD + 16 + HD + 2 * XS + 2 + 4;
+  case PH_QKV: return al4(3 * D) + m * ngd * XS + al4(m * ngd) + (size_t)m * HD * ngd + 2 * nbd * D + 32;
+  case PH_ATTN:
+    if (m == 1) return al4(3 * D) + ngd * XS + al4(ngd) + 3 * HD * ngd + nbd * D + 32 + 2 * HD + ATT_LDS;
+    return ATT_LDS;
   case PH_MLP:
-    return al4(20 + m * ngd * XS + m * ngd + 2 * UNITS * ngd) + (size_t)m * 2 * XS + al4(2 * m) + blk_o;
-  case PH_FINAL: return 52 + ngd * XS + blk_d;
-  case PH_LM: return m * ngd * XS + m * ngd + (size_t)m * TC * WG + (size_t)m * P.lm_rpt + 34 + P.max_seq;
-  default: return 16;
+    return al4(3 * D) + m * ngd * XS + al4(m * ngd) + 4 * UNITS * ngd + (size_t)m * 2 * XS + al4(2 * m) + 2 * nbo * D +
+           32;
+  case PH_FINAL: return al4(3 * D) + nbd * D + 32;
+  case PH_LM: return m * ngd * XS + al4(m * ngd) + (size_t)m * TC * LT + (size_t)m * P.lm_rpt + 34 + P.max_seq;
+  default: return 2 * (LT / 64);
   }
+}
+
+// The persistent kernel: every phase at m = 1, the lm_head and ARGMAX
+// with 1024-thread workgroups.
+size_t flow_lds_bytes(const DecParams &P, const FlowGeom &F) {
+  const size_t ngd = P.D / 32;
+  size_t f = 2 * (FLT / 64);
+  for (int ph = PH_QKV; ph <= PH_FINAL; ++ph) f = std::max(f, lds_floats(P, ph, 1));
+  const size_t nbd = (P.nchunk + PB - 1) / PB;
+  f = std::max(f, al4(3 * (size_t)P.D) + ngd * XS + al4(ngd) + (size_t)FTC * FLT + (size_t)F.lm_rpt + 34 + P.max_seq +
+                      nbd * P.D + 32);
+  return f * sizeof(float);
 }
 
 size_t lds_for(const DecParams &P, int m) {
@@ -1136,6 +1689,13 @@ int upload_state(mllm_model *M) {
   return 0;
 }
 
+// The kernel of phase ph in a pass of m tokens: the decode step (m = 1) runs
+// the attention item with the QKV rows fused in.
+PhaseKernel phase_kernel(const mllm_model *M, int ph, int m) {
+  if (m == 1 && ph == PH_ATTN) return kAttn1Kernels[M->aq_idx];
+  return kPhaseKernels[m == 1][ph];
+}
+
 // With events e0/e1 the launch goes through hipExtLaunchKernel, which stamps
 // the kernel's own begin and end (the same interval a kernel trace reports).
 int launch_phase(mllm_model *M, int ph, int li, int m, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr) {
@@ -1145,22 +1705,36 @@ int launch_phase(mllm_model *M, int ph, int li, int m, hipEvent_t e0 = nullptr, 
     DecParams P = M->P;
     int li_ = li, m_ = m;
     void *args[] = {&P, &Lw, &li_, &m_};
-    MLLM_HIP(hipExtLaunchKernel(reinterpret_cast<const void *>(kPhaseKernels[m == 1][ph]), dim3(n),
+    MLLM_HIP(hipExtLaunchKernel(reinterpret_cast<const void *>(phase_kernel(M, ph, m)), dim3(n),
                                 dim3(phase_threads(ph)), args,
                                 lds_for(M->P, m), M->stream, e0, e1, 0));
     return 0;
   }
-  hipLaunchKernelGGL(kPhaseKernels[m == 1][ph], dim3(n), dim3(phase_threads(ph)), lds_for(M->P, m), M->stream, M->P,
+  hipLaunchKernelGGL(phase_kernel(M, ph, m), dim3(n), dim3(phase_threads(ph)), lds_for(M->P, m), M->stream, M->P,
                      Lw, li, m);
   MLLM_HIP(hipGetLastError());
   return 0;
 }
 
+// One cooperative launch of the persistent kernel: `steps` single-token
+// steps (chained when the pass state says so).
+int launch_flow(mllm_model *M, int steps) {
+  FlowGeom F = M->flow;
+  F.ep0 = M->flow_epoch + 1;
+  F.steps = steps;
+  M->flow_epoch += steps;
+  void *args[] = {&M->P, &F};
+  MLLM_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(kFlowKernels[M->aq_idx]), dim3(M->flow_grid),
+                                      dim3(FLT), args,
+                                      M->flow_lds, M->stream));
+  return 0;
+}
+
 // The phases of one pass in order: (phase, layer) pairs.
-std::vector<std::pair<int, int>> pass_phases(const mllm_model *M, bool lm) {
+std::vector<std::pair<int, int>> pass_phases(const mllm_model *M, bool lm, int m) {
   std::vector<std::pair<int, int>> v;
   for (int li = 0; li < M->cfg.n_layers; ++li)
-    for (int ph = PH_QKV; ph <= PH_MLP; ++ph) v.emplace_back(ph, li);
+    for (int ph = m == 1 ? PH_ATTN : PH_QKV; ph <= PH_MLP; ++ph) v.emplace_back(ph, li);
   if (lm)
     for (int ph = PH_FINAL; ph <= PH_ARGMAX; ++ph) v.emplace_back(ph, 0);
   return v;
@@ -1175,13 +1749,13 @@ int build_chain_graph(mllm_model *M) {
   const size_t lds = lds_for(M->P, 1);
   int m = 1;
   int rc = 0;
-  for (const auto &pl : pass_phases(M, true)) {
+  for (const auto &pl : pass_phases(M, true, 1)) {
     int ph = pl.first, li = pl.second;
     LayerW Lw = ph <= PH_MLP ? M->layers[li] : LayerW{};
     void *args[] = {&M->P, &Lw, &li, &m};
     hipKernelNodeParams kp;
     memset(&kp, 0, sizeof kp);
-    kp.func = reinterpret_cast<void *>(kPhaseKernels[1][ph]);
+    kp.func = reinterpret_cast<void *>(phase_kernel(M, ph, 1));
     kp.gridDim = dim3(phase_items(M->P, ph, 1));
     kp.blockDim = dim3(phase_threads(ph));
     kp.sharedMemBytes = (unsigned)lds;
@@ -1203,7 +1777,7 @@ int build_chain_graph(mllm_model *M) {
 }
 
 int enqueue_pass_phases(mllm_model *M, int m, bool lm) {
-  for (const auto &pl : pass_phases(M, lm))
+  for (const auto &pl : pass_phases(M, lm, m))
     if (int rc = launch_phase(M, pl.first, pl.second, m)) return rc;
   return 0;
 }
@@ -1231,7 +1805,11 @@ int run_pass(mllm_model *M, const int32_t *ids, int m, int pos0, int lm_rows) {
   for (int i = 0; i < m; ++i) s.tok[i] = ids[i];
   if (int rc = upload_state(M)) return rc;
   MLLM_HIP(hipEventRecord(M->ev0, M->stream));
-  if (int rc = enqueue_pass_phases(M, m, lm_rows != 0)) return rc;
+  if (M->exec_mode == 3 && m == 1 && lm_rows == 1) {
+    if (int rc = launch_flow(M, 1)) return rc;
+  } else {
+    if (int rc = enqueue_pass_phases(M, m, lm_rows != 0)) return rc;
+  }
   MLLM_HIP(hipEventRecord(M->ev1, M->stream));
   MLLM_HIP(hipStreamSynchronize(M->stream));
   MLLM_HIP(hipEventElapsedTime(&M->last_ms, M->ev0, M->ev1));
@@ -1277,6 +1855,9 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
                  c.vocab_size > 0 && c.max_seq_len > 0,
              "invalid config");
   MLLM_CHECK(c.d_model % c.n_heads == 0 && c.n_heads % c.n_kv_heads == 0, "heads do not divide");
+  // coherent loads and stores address the KV cache with 32-bit byte offsets
+  MLLM_CHECK((uint64_t)c.n_layers * 2 * c.n_kv_heads * c.max_seq_len * HD * (c.kv_fp16 ? 2 : 4) < (1ull << 31),
+             "KV cache of %d layers x %d positions exceeds 2 GiB", c.n_layers, c.max_seq_len);
   if (c.d_model / c.n_heads != HD)
     return set_error(MLLM_ERR_UNSUPPORTED, "head_dim %d unsupported (64 only)", c.d_model / c.n_heads);
   if (c.d_model % 32 || c.d_model > 1024)
@@ -1397,7 +1978,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   // flight at once; larger values trade workgroups for the register double
   // buffer of phase_lm.
   P.lm_grid = (P.lm_tiles + MLLM_LM_TILES_PER_WG - 1) / MLLM_LM_TILES_PER_WG;
-  if (16 * ngd > QC * QT || UNITS * ngd > MC * ((MT / ngd) * ngd) || 2 * D > MC * MT || 2 * D > SC * AT ||
+  M->aq_idx = aqc_for(ngd) - 4;
+  if (HD * ngd > QC * QT || UNITS * ngd > MC * ((MT / ngd) * ngd) || 2 * D > MC * MT || 2 * D > SC * AT ||
       16 * ngd > TC * LT)
     return fail(set_error(MLLM_ERR_UNSUPPORTED, "tiles exceed the chunk registers (d_model %d)", D));
 
@@ -1416,6 +1998,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   if (!rc) rc = dev_alloc(M, (void **)&P.opart, sizeof(float) * MAXT * NH * D);
   if (!rc) rc = dev_alloc(M, (void **)&P.dpart, sizeof(float) * MAXT * P.nchunk * D);
   if (!rc) rc = dev_alloc(M, (void **)&P.xn, sizeof(float) * MAXT * D);
+  if (!rc) rc = dev_alloc(M, (void **)&P.xnsum, sizeof(float) * MAXT * 32);
   if (!rc) rc = dev_alloc(M, (void **)&P.q, sizeof(float) * MAXT * NH * HD);
   if (!rc) rc = dev_alloc(M, &P.kv, kv_elems * (c.kv_fp16 ? 2 : 4));
   if (!rc) rc = dev_alloc(M, (void **)&P.attp, sizeof(float) * MAXT * NH * P.nsplit_max * APS);
@@ -1438,12 +2021,43 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   P.hist = M->d_hist;
   P.st = M->d_st;
 
+  // persistent kernel: geometry, LDS, one resident workgroup set, flags
+  {
+    FlowGeom &F = M->flow;
+    F.na = phase_items(P, PH_ATTN, 1);
+    F.nm = phase_items(P, PH_MLP, 1);
+    F.ni = F.na + F.nm;
+    F.lm_rpt = std::min(V, std::max(1, (FTC * FLT) / ngd));
+    F.lm_tiles = (V + F.lm_rpt - 1) / F.lm_rpt;
+    M->flow_lds = flow_lds_bytes(P, F);
+    int per_cu = 0;
+    const bool lds_ok = M->flow_lds <= lds_cap &&
+                        (M->flow_lds <= 64 * 1024 ||
+                         hipFuncSetAttribute(reinterpret_cast<const void *>(kFlowKernels[M->aq_idx]),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)M->flow_lds) == hipSuccess);
+    int coop = 0;
+    (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, M->device);
+    if (lds_ok && coop && F.lm_tiles <= P.lm_tiles &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(kFlowKernels[M->aq_idx]), FLT,
+                                                     M->flow_lds) == hipSuccess &&
+        per_cu > 0) {
+      const int G = per_cu * M->num_cus;
+      const size_t nflags = (size_t)L * (NH + F.nm) + 2 + G;
+      if (int rc = dev_alloc(M, (void **)&F.flags, sizeof(int) * nflags)) return fail(rc);
+      if (hipMemset(F.flags, 0, sizeof(int) * nflags) != hipSuccess) return fail(set_error(MLLM_ERR_HIP, "memset"));
+      M->flow_grid = G;
+    }
+    (void)hipGetLastError();
+  }
   if (M->lds_max > 64 * 1024) {
     bool ok = true;
     for (int one = 0; one < 2; ++one)
       for (int ph = 0; ph < PH_COUNT; ++ph)
         ok = ok && hipFuncSetAttribute(reinterpret_cast<const void *>(kPhaseKernels[one][ph]),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)M->lds_max) == hipSuccess;
+    ok = ok && hipFuncSetAttribute(reinterpret_cast<const void *>(kAttn1Kernels[M->aq_idx]),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)M->lds_max) == hipSuccess;
     if (!ok) return fail(set_error(MLLM_ERR_HIP, "LDS attribute"));
   }
   *out = M;
@@ -1484,7 +2098,9 @@ extern "C" int mllm_max_pass_tokens(const mllm_model *M) { return M ? M->max_pas
 
 extern "C" int mllm_set_exec_mode(mllm_model *M, int mode) {
   MLLM_CHECK(M, "null model");
-  MLLM_CHECK(mode == 1 || mode == 2, "exec mode %d (1: graph replay, 2: direct launches)", mode);
+  MLLM_CHECK(mode >= 1 && mode <= 3, "exec mode %d (1: graph replay, 2: direct launches, 3: persistent kernel)",
+             mode);
+  if (mode == 3 && !M->flow_grid) return set_error(MLLM_ERR_UNSUPPORTED, "persistent kernel unavailable on this device");
   M->exec_mode = mode;
   return 0;
 }
@@ -1553,7 +2169,9 @@ extern "C" int mllm_decode_chain(mllm_model *M, int32_t first, int n_steps, int3
   s.tok[0] = first;
   if (int rc = upload_state(M)) return rc;
   MLLM_HIP(hipEventRecord(M->ev0, M->stream));
-  if (M->exec_mode == 2) {
+  if (M->exec_mode == 3) {
+    if (int rc = launch_flow(M, n_steps)) return rc;
+  } else if (M->exec_mode == 2) {
     for (int i = 0; i < n_steps; ++i)
       if (int rc = enqueue_pass_phases(M, 1, true)) return rc;
   } else {
@@ -1579,7 +2197,7 @@ extern "C" int mllm_profile_decode(mllm_model *M, int32_t first, int n_steps, fl
   MLLM_CHECK(n_steps > 0, "n_steps %d", n_steps);
   MLLM_CHECK(M->cache_len + n_steps <= M->cfg.max_seq_len, "profile run exceeds the context");
   if (int rc = check_ids(M, &first, 1)) return rc;
-  const auto phases = pass_phases(M, true);
+  const auto phases = pass_phases(M, true, 1);
   const int per_step = (int)phases.size();
   if ((int)M->prof_ev.size() < 2 * per_step) {
     for (hipEvent_t e : M->prof_ev) (void)hipEventDestroy(e);

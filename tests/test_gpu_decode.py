@@ -12,6 +12,7 @@ import mllm
 from mllm import pgw
 
 gpu = pytest.mark.gpu
+MODES = [1, 2, 3]  # graph replay, direct launches, persistent kernel
 LOGIT_TOL = 1e-2
 MARGIN = 1e-2
 
@@ -44,7 +45,7 @@ def build(arch="llama", seed=1, **over):
 
 @gpu
 @pytest.mark.parametrize("arch", ["llama", "gpt2"])
-@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("mode", MODES)
 def test_small_teacher_forced_vs_oracle(oracle_lib, arch, mode):
     bundle = build(arch, seed=3)
     print(f"decode small {arch} mode={mode}", flush=True)
@@ -61,14 +62,15 @@ def test_small_teacher_forced_vs_oracle(oracle_lib, arch, mode):
 def test_exec_modes_bit_identical():
     bundle = build("llama", seed=5)
     outs = []
-    for mode in (1, 2):
+    for mode in MODES:
         g = mllm.PetitGPT(bundle, exec_mode=mode)
         rows = [g.forwardPrompt([1, 2, 3, 4, 5]).copy()]
         for t in (6, 7, 8):
             rows.append(g.forwardDecode(t).copy())
         outs.append(np.stack(rows))
         g.destroy()
-    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    for o in outs[1:]:
+        assert np.array_equal(outs[0].view(np.uint32), o.view(np.uint32))
 
 
 @gpu
@@ -90,7 +92,7 @@ def test_verify_rows_bit_identical_to_decode(n):
 
 
 @gpu
-@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("mode", MODES)
 def test_chain_equals_host_greedy(mode):
     bundle = build("llama", seed=7)
     g = mllm.PetitGPT(bundle, exec_mode=mode)
@@ -102,7 +104,7 @@ def test_chain_equals_host_greedy(mode):
 
 
 @gpu
-@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("mode", MODES)
 def test_chain_stops_at_eos(mode):
     bundle = build("llama", seed=7)
     g = mllm.PetitGPT(bundle, exec_mode=mode)
@@ -116,7 +118,7 @@ def test_chain_stops_at_eos(mode):
 
 
 @gpu
-@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("mode", MODES)
 def test_gpt2_chain_penalty_equals_host_argmax_gpt2(mode):
     """Device argmaxGpt2 (3-gram block + 1.15 penalty) == host rule on host logits."""
     bundle = build("gpt2", seed=8)
@@ -130,7 +132,7 @@ def test_gpt2_chain_penalty_equals_host_argmax_gpt2(mode):
 
 
 @gpu
-@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("mode", MODES)
 def test_long_context_splits_vs_oracle(oracle_lib, mode):
     """Context beyond one 256-position attention split (several splits merged)."""
     bundle = build("llama", seed=9, max_seq_len=1024)
@@ -144,9 +146,10 @@ def test_long_context_splits_vs_oracle(oracle_lib, mode):
 
 
 @gpu
-def test_fp16_kv_within_tolerance(oracle_lib):
+@pytest.mark.parametrize("mode", [1, 3])
+def test_fp16_kv_within_tolerance(oracle_lib, mode):
     bundle = build("llama", seed=10, max_seq_len=512)
-    g = mllm.PetitGPT(bundle, kv_fp16=True)
+    g = mllm.PetitGPT(bundle, kv_fp16=True, exec_mode=mode)
     ref = oracle_lib.OracleModel(bundle)
     rng = np.random.default_rng(3)
     prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 300)]
@@ -167,11 +170,12 @@ def test_model_gemv_plug_point(oracle_lib):
 
 
 @gpu
-def test_smollm2_135m_prefill_decode_vs_oracle(oracle_lib):
+@pytest.mark.parametrize("mode", [1, 3])
+def test_smollm2_135m_prefill_decode_vs_oracle(oracle_lib, mode):
     """Config 1 shape at full size: 32-token prompt then 4 greedy steps."""
     cfg = pgw.CONFIGS["smollm2-135m"]
     bundle = pgw.parse_pgw(pgw.make_llama(cfg, seed=0))
-    g = mllm.PetitGPT(bundle)
+    g = mllm.PetitGPT(bundle, exec_mode=mode)
     ref = oracle_lib.OracleModel(bundle)
     rng = np.random.default_rng(1)
     prompt = [int(v) for v in rng.integers(0, cfg.vocab_size, 32)]
@@ -191,3 +195,28 @@ def test_gpt2_124m_prefill_decode_vs_oracle(oracle_lib):
     worst, agree = teacher_forced(g, ref, prompt, 3, None)
     g.destroy()
     assert worst < LOGIT_TOL and agree, worst
+
+
+@gpu
+@pytest.mark.parametrize("arch", ["llama", "gpt2"])
+def test_full_size_chain_persistent_equals_graph(arch):
+    """Config 1 / config 4 shapes: a long chained decode in one persistent
+    launch gives the token sequence of the graph replay, and the last step's
+    logits bit for bit."""
+    name = "smollm2-135m" if arch == "llama" else "gpt2-124m"
+    cfg = pgw.CONFIGS[name]
+    bundle = pgw.parse_pgw(pgw.make_model(cfg, seed=0))
+    rng = np.random.default_rng(1)
+    prompt = [int(v) for v in rng.integers(0, cfg.vocab_size, 32)]
+    outs = []
+    for mode in (1, 3):
+        print(f"chain {name} mode={mode}", flush=True)
+        g = mllm.PetitGPT(bundle, exec_mode=mode)
+        first = int(np.argmax(g.forwardPrompt(prompt)))
+        hist = [first] if arch == "gpt2" else None
+        ids = g.decodeChain(first, 96, hist=hist)
+        last = g.forwardDecode(ids[-1]).copy()
+        outs.append((ids, last))
+        g.destroy()
+    assert outs[0][0] == outs[1][0]
+    assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))
