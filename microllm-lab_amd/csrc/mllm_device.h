@@ -38,6 +38,8 @@ __device__ __forceinline__ int tid() {
   return t;
 }
 
+__device__ __forceinline__ int lane_id64() { return tid() & 63; }
+
 struct Q4Mat {
   const uint4 *q;  // packed nibbles, as 16-byte chunks
   const float *s;  // one scale per chunk
@@ -249,6 +251,86 @@ __device__ __forceinline__ void coh_sth(void *base, uint32_t off, unsigned short
 // barrier alone does not wait for them.
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0) */ }
 
+// ---------------------------------------------------------------- integer group dots
+// The decode engine's GEMVs take their activations quantised per 32-element
+// group (the Q4 group) to int16: xi = rint(x * 32767 / amax), scale
+// sx = amax / 32767 (amax = max |x| of the group; 0 for an all-zero group).
+// Splitting xi = 256 * hi + lo (hi signed, lo unsigned bytes) turns the
+// group's dot with the nibbles into byte dot products that are exact in
+// int32:
+//   sum_k (q_k - 8) * xi_k = 256 * sdot4(q, hi) + udot4(q, lo) - 8 * sum_k xi_k
+// A packed dword of the weights holds elements 8j .. 8j+7 (byte b: element
+// 8j+2b in the low nibble, 8j+2b+1 in the high one), so the activations are
+// stored per group as a QX record of QXR dwords:
+//   [0..3]  high bytes of the even elements 8j, 8j+2, 8j+4, 8j+6 (dword j)
+//   [4..7]  high bytes of the odd elements
+//   [8..11] low bytes of the even elements, [12..15] of the odd ones
+//   [16] sx (float bits), [17] sum of xi, [18..19] padding
+// The group's contribution to a row is then ((float)dot * sx) * w_scale:
+// about 34 VALU operations per 32 weights instead of 80 for float
+// dequantisation.  The only rounding is that of x to 16 bits (relative
+// 1.5e-5 per element).
+constexpr int QXR = 20;
+
+__device__ __forceinline__ float q4_qx_part(const uint4 w, const uint32_t *__restrict__ rec, float ws) {
+  const uint4 he = *reinterpret_cast<const uint4 *>(rec), ho = *reinterpret_cast<const uint4 *>(rec + 4);
+  const uint4 le = *reinterpret_cast<const uint4 *>(rec + 8), lo = *reinterpret_cast<const uint4 *>(rec + 12);
+  const uint2 sc = *reinterpret_cast<const uint2 *>(rec + 16);
+  const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
+  const uint32_t xhe[4] = {he.x, he.y, he.z, he.w}, xho[4] = {ho.x, ho.y, ho.z, ho.w};
+  const uint32_t xle[4] = {le.x, le.y, le.z, le.w}, xlo[4] = {lo.x, lo.y, lo.z, lo.w};
+  int h = 0;
+  uint32_t l = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t ev = dw[j] & 0x0F0F0F0Fu, od = (dw[j] >> 4) & 0x0F0F0F0Fu;
+    h = __builtin_amdgcn_sdot4((int)ev, (int)xhe[j], h, false);
+    h = __builtin_amdgcn_sdot4((int)od, (int)xho[j], h, false);
+    l = __builtin_amdgcn_udot4(ev, xle[j], l, false);
+    l = __builtin_amdgcn_udot4(od, xlo[j], l, false);
+  }
+  const int dot = h * 256 + (int)l - 8 * (int)sc.y;
+  return ((float)dot * __uint_as_float(sc.x)) * ws;
+}
+
+// The same with the group's record held in registers (x16: dwords 0..15,
+// sx, xs = sum of xi), e.g. for the gate and up rows of one unit.
+struct QxRec {
+  uint32_t d[16];
+  float sx;
+  int xs;
+};
+__device__ __forceinline__ QxRec qx_load(const uint32_t *__restrict__ rec) {
+  QxRec r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint4 v = *reinterpret_cast<const uint4 *>(rec + 4 * k);
+    r.d[4 * k] = v.x;
+    r.d[4 * k + 1] = v.y;
+    r.d[4 * k + 2] = v.z;
+    r.d[4 * k + 3] = v.w;
+  }
+  const uint2 sc = *reinterpret_cast<const uint2 *>(rec + 16);
+  r.sx = __uint_as_float(sc.x);
+  r.xs = (int)sc.y;
+  return r;
+}
+__device__ __forceinline__ float q4_qx_part_reg(const uint4 w, const QxRec &r, float ws) {
+  const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
+  int h = 0;
+  uint32_t l = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t ev = dw[j] & 0x0F0F0F0Fu, od = (dw[j] >> 4) & 0x0F0F0F0Fu;
+    h = __builtin_amdgcn_sdot4((int)ev, (int)r.d[j], h, false);
+    h = __builtin_amdgcn_sdot4((int)od, (int)r.d[4 + j], h, false);
+    l = __builtin_amdgcn_udot4(ev, r.d[8 + j], l, false);
+    l = __builtin_amdgcn_udot4(od, r.d[12 + j], l, false);
+  }
+  const int dot = h * 256 + (int)l - 8 * r.xs;
+  return ((float)dot * r.sx) * ws;
+}
+
 // Cross-lane moves through DPP (a VALU operand modifier) instead of
 // ds_bpermute, which goes through the LDS crossbar and costs an LDS round
 // trip per step.  Control codes (GFX9 DPP16): quad_perm(1,0,3,2) = 0xB1,
@@ -459,6 +541,71 @@ __device__ __forceinline__ float row_sum(const float *p, int n) {
   return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
 }
 
+// ---------------------------------------------------------------- activation staging (QX)
+// Max / sum over the 8 lanes of each half-row (lanes 8k .. 8k+7).
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  return fmaxf(v, dpp_f<0x141>(v));
+}
+__device__ __forceinline__ int sum8i(int v) {
+  v = v + dpp_i<0xB1>(v);
+  v = v + dpp_i<0x4E>(v);
+  return v + dpp_i<0x141>(v);
+}
+__device__ __forceinline__ float qx_inv(float amax) { return amax > 0.f ? 32767.0f / amax : 0.f; }
+__device__ __forceinline__ int qx_round(float v, float inv) { return (int)__builtin_rintf(v * inv); }
+
+// A row staged by one thread per float4 column q (elements 4q .. 4q+3, the
+// group's columns on 8 neighbouring lanes): the QX records of the row's
+// groups at qx.  Called by whole waves (DPP); `in` marks real columns.
+__device__ __forceinline__ void qx_stage_col(float4 y, bool in, int q, uint32_t *qx) {
+  if (!in) y = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float a = max8(fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+  const float inv = qx_inv(a);
+  const int x0 = qx_round(y.x, inv), x1 = qx_round(y.y, inv), x2 = qx_round(y.z, inv), x3 = qx_round(y.w, inv);
+  const int s = sum8i((x0 + x1) + (x2 + x3));
+  if (in) {
+    uint32_t *rec = qx + (q >> 3) * QXR;
+    uint8_t *rb = reinterpret_cast<uint8_t *>(rec);
+    const int off = 4 * ((q & 7) >> 1) + 2 * (q & 1);  // even/odd element slots of this column
+    *reinterpret_cast<unsigned short *>(rb + off) = (unsigned short)(((x0 >> 8) & 255) | (((x2 >> 8) & 255) << 8));
+    *reinterpret_cast<unsigned short *>(rb + 16 + off) = (unsigned short)(((x1 >> 8) & 255) | (((x3 >> 8) & 255) << 8));
+    *reinterpret_cast<unsigned short *>(rb + 32 + off) = (unsigned short)((x0 & 255) | ((x2 & 255) << 8));
+    *reinterpret_cast<unsigned short *>(rb + 48 + off) = (unsigned short)((x1 & 255) | ((x3 & 255) << 8));
+    if ((q & 7) == 0) {
+      rec[16] = __float_as_uint(a / 32767.0f);
+      rec[17] = (uint32_t)s;
+    }
+  }
+}
+
+// 64 values, one per lane of the calling wave (lane r: element r & 31 of
+// group r >> 5): the two QX records at qx.  Called by the whole wave.
+__device__ __forceinline__ void qx_stage_lanes(float v, uint32_t *qx) {
+  const int r = lane_id64(), k = r & 31;
+  const float m16 = row16_max(fabsf(v));
+  const float a = r < 32 ? fmaxf(readlane_f(m16, 0), readlane_f(m16, 16))
+                         : fmaxf(readlane_f(m16, 32), readlane_f(m16, 48));
+  const int xi = qx_round(v, qx_inv(a));
+  int s16 = xi;
+  s16 = s16 + dpp_i<0xB1>(s16);
+  s16 = s16 + dpp_i<0x4E>(s16);
+  s16 = s16 + dpp_i<0x141>(s16);
+  s16 = s16 + dpp_i<0x140>(s16);
+  const int s = r < 32 ? __builtin_amdgcn_readlane(s16, 0) + __builtin_amdgcn_readlane(s16, 16)
+                       : __builtin_amdgcn_readlane(s16, 32) + __builtin_amdgcn_readlane(s16, 48);
+  uint32_t *rec = qx + (r >> 5) * QXR;
+  uint8_t *rb = reinterpret_cast<uint8_t *>(rec);
+  const int off = 16 * (k & 1) + 4 * (k >> 3) + ((k & 7) >> 1);
+  rb[off] = (uint8_t)((xi >> 8) & 255);
+  rb[32 + off] = (uint8_t)(xi & 255);
+  if (k == 0) {
+    rec[16] = __float_as_uint(a / 32767.0f);
+    rec[17] = (uint32_t)s;
+  }
+}
+
 // ---------------------------------------------------------------- tiles
 // A tile is up to two contiguous row ranges [r0a, r0a+na) and [r0b, r0b+nb)
 // of one matrix (two ranges let a QKV tile hold both RoPE partners d and
@@ -528,6 +675,37 @@ __device__ __forceinline__ void tile_compute(const TileRegs<C> &R, int nrows, in
         const float d = q4_chunk_dot(R.w[j], xs + (t * ng + gj[j]) * XS);
         part[t * nch + c] = (d - 8.f * xsum[t * ng + gj[j]]) * R.s[j];
       }
+    }
+  }
+  __syncthreads();
+  for (int i = tid(); i < nrows * m; i += NT) {
+    const int t = i / nrows, r = i - t * nrows;
+    out[t * ostride + r] = row_sum(part + t * nch + r * ng, ng);
+  }
+  __syncthreads();
+}
+
+// tile_compute with the activations staged as QX records (m tokens x ng
+// groups).
+template <int C, int NT = WG>
+__device__ __forceinline__ void tile_compute_qx(const TileRegs<C> &R, int nrows, int ng, int nch, int m,
+                                                const uint32_t *qx, int gfirst, int gstep, float *part, float *out,
+                                                int ostride) {
+  int gj[C];
+  {
+    int g = gfirst;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      gj[j] = g;
+      g += gstep;
+      if (g >= ng) g -= ng;
+    }
+  }
+  for (int t = 0; t < m; ++t) {
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const int c = tid() + j * NT;
+      if (c < nch) part[t * nch + c] = q4_qx_part(R.w[j], qx + (t * ng + gj[j]) * QXR, R.s[j]);
     }
   }
   __syncthreads();

@@ -123,7 +123,6 @@ struct DecParams {
   float *opart;   // [MAXT][NH][D] per-head partials of W_o . att
   float *dpart;   // [MAXT][nchunk][D] per-chunk partials of W_2 . h
   float *xn;      // [MAXT][D] final-normed rows for the lm_head
-  float *xnsum;   // [MAXT][32] their group sums
   float *q;       // [MAXT][NH*HD] queries after RoPE
   void *kv;       // [L][2][NKV][max_seq][HD] (f32 or f16)
   float *attp;    // [MAXT][NH][nsplit_max][APS]
@@ -154,7 +153,6 @@ struct NoWait {
 };
 
 // ---------------------------------------------------------------- helpers
-__device__ __forceinline__ int skew(int i) { return (i >> 5) * XS + (i & 31); }
 
 // LDS regions read or written as float4 start on a 16-byte boundary.
 __host__ __device__ __forceinline__ size_t al4(size_t n) { return (n + 3) & ~(size_t)3; }
@@ -271,15 +269,13 @@ __device__ __forceinline__ void resid_blocks(const float *pt, int nq, int np, fl
 // x * (1/sqrt(mean(x^2) + eps)) * w) or LayerNorm (infer.js:147-164,
 // eps 1e-5): each wave sums its columns with DPP, the waves' sums are added
 // in order.  1/sqrt is the hardware reciprocal square root.  The
-// normalised row goes to xs_t (skewed) and the sum of every 32-element
-// group (8 neighbouring lanes x 4) to xsum_t.  The gains (LayerNorm:
+// normalised row is staged as QX records at qx_t (when set).  The gains (LayerNorm:
 // gamma || beta) and the bias are in gl[0, 2D) and gl[2D, 3D).  Every
 // thread of the workgroup must call it (it holds barriers); red needs
 // 2 x 16 floats.
 struct ColOut {
-  float *x;     // the residual row (coherent store), or null
-  float *y;     // the normalised row (coherent store), or null
-  float *ysum;  // its group sums (coherent store), or null
+  float *x;  // the residual row (coherent store), or null
+  float *y;  // the normalised row (coherent store), or null
 };
 
 __device__ __forceinline__ float4 col_finish(const float *blk, int nq, int np, float4 base, const float *gl, int D,
@@ -305,8 +301,8 @@ __device__ __forceinline__ float waves_sum(float v, int nw, float *red) {
   return t;
 }
 
-__device__ __forceinline__ void col_norm(const DecParams &P, float4 x, const float *gl, float *red, float *xs_t,
-                                         float *xsum_t, const ColOut &o) {
+__device__ __forceinline__ void col_norm(const DecParams &P, float4 x, const float *gl, float *red, uint32_t *qx_t,
+                                         const ColOut &o) {
   const int D = P.D, nq = D >> 2, q = tid(), nw = (nq + 63) >> 6;
   const bool in = q < nq;
   if (!in) x = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -330,20 +326,8 @@ __device__ __forceinline__ void col_norm(const DecParams &P, float4 x, const flo
     y = make_float4(x.x * r * g.x, x.y * r * g.y, x.z * r * g.z, x.w * r * g.w);
   }
   if (!in) y = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (wave_id() < nw) {
-    float v = (y.x + y.y) + (y.z + y.w);
-    v = v + dpp_f<0xB1>(v);   // pairs
-    v = v + dpp_f<0x4E>(v);   // quads
-    v = v + dpp_f<0x141>(v);  // 8 lanes (half-row mirror)
-    if (in) {
-      if (xs_t) *reinterpret_cast<float4 *>(xs_t + (q >> 3) * XS + ((4 * q) & 31)) = y;
-      if (o.y) coh_st4(o.y, 16u * q, y);
-      if ((q & 7) == 0) {
-        if (xsum_t) xsum_t[q >> 3] = v;
-        if (o.ysum) coh_stf(o.ysum, 4u * (q >> 3), v);
-      }
-    }
-  }
+  if (o.y && in) coh_st4(o.y, 16u * q, y);
+  if (qx_t && wave_id() < nw) qx_stage_col(y, in, q, qx_t);
 }
 
 // The base column of this thread (coherent load, branch-free).
@@ -354,8 +338,8 @@ __device__ __forceinline__ float4 col_base_load(const float *base, int nq) {
 // Per-chunk partials of a tile in registers for m staged tokens:
 // part[t*nch + c] (the arithmetic of tile_compute); no barrier.
 template <int C>
-__device__ __forceinline__ void tile_partials(const TileRegs<C> &R, int ng, int nch, int m, const float *xs,
-                                              const float *xsum, float *part) {
+__device__ __forceinline__ void tile_partials(const TileRegs<C> &R, int ng, int nch, int m, const uint32_t *qx,
+                                              float *part) {
   int gj[C];
   {
     int g = tid() % ng;
@@ -371,10 +355,7 @@ __device__ __forceinline__ void tile_partials(const TileRegs<C> &R, int ng, int 
 #pragma unroll
     for (int j = 0; j < C; ++j) {
       const int c = tid() + j * 1024;
-      if (c < nch) {
-        const float d = q4_chunk_dot_lean(R.w[j], xs + (t * ng + gj[j]) * XS);
-        part[t * nch + c] = (d - 8.f * xsum[t * ng + gj[j]]) * R.s[j];
-      }
+      if (c < nch) part[t * nch + c] = q4_qx_part(R.w[j], qx + (t * ng + gj[j]) * QXR, R.s[j]);
       // one chunk at a time: the activations of several chunks in flight at
       // once would not fit beside the registers the caller holds (the other
       // waves of the SIMD hide the LDS latency)
@@ -397,19 +378,18 @@ __device__ __forceinline__ void slice_load(const Q4Mat &W, int g0, int rows, Til
   }
 }
 
-// The slice against two staged groups v (skewed, 2 x XS) with sums vsum[2]:
+// The slice against two staged groups (QX records v, v + QXR):
 // out[r] = part(group g0) + part(group g0 + 1), the row_sum order of two
 // groups (coherent stores).  Neighbouring lanes hold the pair; every lane
 // takes part in the shuffle.
 template <int C, int NT>
-__device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const float *v, const float *vsum,
-                                           float *out) {
+__device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const uint32_t *v, float *out) {
 #pragma unroll
   for (int k = 0; k < C; ++k) {
     const int c = tid() + k * NT;
     const int j = c & 1;
     float p = 0.f;
-    if (c < 2 * rows) p = (q4_chunk_dot(R.w[k], v + j * XS) - 8.f * vsum[j]) * R.s[k];
+    if (c < 2 * rows) p = q4_qx_part(R.w[k], v + j * QXR, R.s[k]);
     const float sum = p + lane_xor1(p);
     if (c < 2 * rows && j == 0) coh_stf(out, 4u * (c >> 1), sum);
   }
@@ -493,7 +473,8 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
   const int pos0 = st.pos0;
   const bool gpt2 = P.arch == 1;
   const int nb = (P.nchunk + PB - 1) / PB;
-  float *gl = smem, *xs = gl + al4(3 * D), *xsum = xs + m * ng * XS, *part = xsum + al4(m * ng);
+  float *gl = smem, *part = gl + al4(3 * D) + m * ng * QXR;
+  uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // m x ng QX records
   float *blk = part + m * nch;  // 2 x nb * D (alternating tokens), then red
   const float *rbias = gpt2 && li > 0 ? Lw.prev_mproj_b : nullptr;
   QkvPre Q;
@@ -521,7 +502,7 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
     if (li > 0) resid_blocks_rest(P.dpart, nq, P.nchunk, R0, blk);
     gains_store(P, rbias, GR, gl);
   }
-  // stage every token: x, the norm, xs and xsum
+  // stage every token: x, the norm, its QX records
   for (int t = 0; t < m; ++t) {
     float *bt = blk + (t & 1) * nb * D;
     if (li == 0) {
@@ -533,10 +514,10 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
     }
     __syncthreads();
     const float4 x = li == 0 ? base : col_finish(bt, nq, P.nchunk, base, gl, D, rbias != nullptr);
-    col_norm(P, x, gl, red, xs + t * ng * XS, xsum + t * ng, ColOut{head == 0 ? P.xa + (size_t)t * D : nullptr});
+    col_norm(P, x, gl, red, qx + t * ng * QXR, ColOut{head == 0 ? P.xa + (size_t)t * D : nullptr});
   }
   __syncthreads();
-  tile_partials<QC>(Q.R, ng, nch, m, xs, xsum, part);
+  tile_partials<QC>(Q.R, ng, nch, m, qx, part);
   __syncthreads();
   // epilogue on the token's wave: lane d is head dimension d
   for (int t = wv; t < m; t += NWV) {
@@ -577,12 +558,11 @@ struct AttnLds {
   float *sc;    // 256: scores
   float *pv;    // 64 x 64
   float *pv2;   // 4 x 64
-  float *own;   // 64: this split's P.V
-  float *att;   // 2 x XS: merged head output, skewed
-  float *asum;  // 2
+  float *own;      // 64: this split's P.V
+  uint32_t *attq;  // 2 x QXR: merged head output, staged for the W_o slice
   int *flag;
 };
-constexpr int ATT_LDS = HD + 2 * ACH + 64 * HD + 4 * HD + HD + 2 * XS + 2 + 2;  // floats
+constexpr int ATT_LDS = HD + 2 * ACH + 64 * HD + 4 * HD + HD + 2 * QXR + 4;  // floats
 
 __device__ __forceinline__ AttnLds attn_lds(float *base) {
   AttnLds A;
@@ -592,9 +572,8 @@ __device__ __forceinline__ AttnLds attn_lds(float *base) {
   A.pv = A.sc + ACH;
   A.pv2 = A.pv + 64 * HD;
   A.own = A.pv2 + 4 * HD;
-  A.att = A.own + HD;
-  A.asum = A.att + 2 * XS;
-  A.flag = reinterpret_cast<int *>(A.asum + 2);
+  A.attq = reinterpret_cast<uint32_t *>(A.own + HD);
+  A.flag = reinterpret_cast<int *>(A.attq + 2 * QXR);
   return A;
 }
 
@@ -645,13 +624,16 @@ __device__ __forceinline__ void attn_v_load(const DecParams &P, int li, int kvh,
 }
 
 // Scores, split-local softmax statistics, P.V, the merge and the head's
-// W_o slice, with the query staged in A.qs and the keys in kr/vr.  Ro holds
-// the slice when ro_loaded; the merging split of a multi-split head loads it
-// otherwise.  Returns true in the workgroup that wrote the head's output.
+// W_o slice, with the query staged in A.qs and the keys in kr/vr; key knew
+// of the split (when >= 0) is taken from LDS instead (kvn: K row then V
+// row), selected where it is used so that no load of kr/vr is waited for
+// early.  Ro holds the slice when ro_loaded; the merging split of a
+// multi-split head loads it otherwise.  Returns true in the workgroup that
+// wrote the head's output.
 template <int C>
 __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, int h, int ns, int cnt,
-                          const float4 (&kr)[4], const float4 (&vr)[4], TileRegs<C> &Ro, bool ro_loaded,
-                          const AttnLds &A) {
+                          const float4 (&kr)[4], const float4 (&vr)[4], int knew, const float *kvn, TileRegs<C> &Ro,
+                          bool ro_loaded, const AttnLds &A) {
   const int D = P.D;
   const bool solo = ns == 1;
   const int kp = tid() >> 2, ku = tid() & 3;
@@ -661,12 +643,14 @@ __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, i
   if (kp < cnt) {
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
     const float *qq = A.qs + 16 * ku;
+    const bool nk = kp == knew;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      a0 = __builtin_fmaf(qq[4 * j + 0], kr[j].x, a0);
-      a1 = __builtin_fmaf(qq[4 * j + 1], kr[j].y, a1);
-      a2 = __builtin_fmaf(qq[4 * j + 2], kr[j].z, a2);
-      a3 = __builtin_fmaf(qq[4 * j + 3], kr[j].w, a3);
+      const float4 kk = nk ? reinterpret_cast<const float4 *>(kvn)[4 * ku + j] : kr[j];
+      a0 = __builtin_fmaf(qq[4 * j + 0], kk.x, a0);
+      a1 = __builtin_fmaf(qq[4 * j + 1], kk.y, a1);
+      a2 = __builtin_fmaf(qq[4 * j + 2], kk.z, a2);
+      a3 = __builtin_fmaf(qq[4 * j + 3], kk.w, a3);
     }
     part = (a0 + a1) + (a2 + a3);
   }
@@ -696,10 +680,11 @@ __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, i
     const int k = kg + 64 * j;
     if (k < cnt) {
       const float ek = A.es[k];
-      acc.x = __builtin_fmaf(ek, vr[j].x, acc.x);
-      acc.y = __builtin_fmaf(ek, vr[j].y, acc.y);
-      acc.z = __builtin_fmaf(ek, vr[j].z, acc.z);
-      acc.w = __builtin_fmaf(ek, vr[j].w, acc.w);
+      const float4 vv = k == knew ? reinterpret_cast<const float4 *>(kvn + HD)[d4] : vr[j];
+      acc.x = __builtin_fmaf(ek, vv.x, acc.x);
+      acc.y = __builtin_fmaf(ek, vv.y, acc.y);
+      acc.z = __builtin_fmaf(ek, vv.z, acc.z);
+      acc.w = __builtin_fmaf(ek, vv.w, acc.w);
     }
   }
   *reinterpret_cast<float4 *>(A.pv + kg * HD + 4 * d4) = acc;
@@ -760,15 +745,10 @@ __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, i
       }
       v = as / ls;
     }
-    A.att[skew(d)] = v;
-    // the two group sums of the head output (lanes 0-31, 32-63)
-    const float rs = row16_sum(v);
-    const float ga = readlane_f(rs, 0) + readlane_f(rs, 16), gb = readlane_f(rs, 32) + readlane_f(rs, 48);
-    if (d == 0) A.asum[0] = ga;
-    if (d == 32) A.asum[1] = gb;
+    qx_stage_lanes(v, A.attq);  // the head output: two groups, wave 0
   }
   __syncthreads();
-  slice_gemv<C, AT>(Ro, D, A.att, A.asum, P.opart + (size_t)(t * P.NH + h) * D);
+  slice_gemv<C, AT>(Ro, D, A.attq, P.opart + (size_t)(t * P.NH + h) * D);
   return true;
 }
 
@@ -799,7 +779,7 @@ __device__ bool phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, 
   attn_v_load(P, li, h / (P.NH / P.NKV), s0, cnt, vr);
   const bool ro = FLOW || ns == 1;
   if (!FLOW && ns == 1) slice_load<SC, AT>(Lw.proj, 2 * h, P.D, Ro);  // behind the K/V loads
-  return attn_core<SC>(P, Lw, t, sp, h, ns, cnt, kr, vr, Ro, ro, A);
+  return attn_core<SC>(P, Lw, t, sp, h, ns, cnt, kr, vr, -1, A.qs, Ro, ro, A);  // no key from LDS
 }
 
 // Weights and other inputs of a fused decode attention item that do not
@@ -846,7 +826,8 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   const bool gpt2 = P.arch == 1;
   const float *rbias = gpt2 && li > 0 ? Lw.prev_mproj_b : nullptr;
   const int nb = (P.nchunk + PB - 1) / PB;
-  float *gl = smem, *xs = gl + al4(3 * D), *xsum = xs + ng * XS, *part = xsum + al4(ng);
+  float *gl = smem, *part = gl + al4(3 * D) + ng * QXR;
+  uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // ng QX records
   float *blk = part + nch, *red = blk + nb * D, *kvn = red + 32;  // kvn: the new K row (64) then V row (64)
   const AttnLds A = attn_lds(kvn + 2 * HD);
   const int wv = wave_id(), lane = lane_id();
@@ -892,9 +873,9 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   if (li == 0) base = embed_col(P, min(max(st_ld(P, ST_OFF(tok)), 0), P.V - 1), min(pos, P.max_seq - 1));
   __syncthreads();
   const float4 x = li == 0 ? base : col_finish(blk, nq, P.nchunk, base, gl, D, rbias != nullptr);
-  col_norm(P, x, gl, red, xs, xsum, ColOut{item == 0 ? P.xa : nullptr});
+  col_norm(P, x, gl, red, qx, ColOut{item == 0 ? P.xa : nullptr});
   __syncthreads();
-  tile_partials<AQC>(Wt, ng, nch, 1, xs, xsum, part);
+  tile_partials<AQC>(Wt, ng, nch, 1, qx, part);
   __builtin_amdgcn_sched_barrier(0);
   attn_v_load(P, li, kvh, s0, last ? cnt - 1 : cnt, vr);
   __builtin_amdgcn_sched_barrier(0);
@@ -923,19 +904,8 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
       kvn[(wv - 1) * HD + lane] = r;
     }
   }
-  __syncthreads();
-  if (last) {
-    // the current position (key cnt - 1 of this split) from LDS
-    const int kp = tid() >> 2, ku = tid() & 3, d4 = tid() & 15, kg = tid() >> 4;
-    if (kp == cnt - 1) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) kr[j] = reinterpret_cast<const float4 *>(kvn)[4 * ku + j];
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (kg + 64 * j == cnt - 1) vr[j] = reinterpret_cast<const float4 *>(kvn + HD)[d4];
-  }
-  return attn_core<SC>(P, Lw, 0, sp, h, ns, cnt, kr, vr, Ro, true, A);
+  // the current position (key cnt - 1 of the last split) comes from LDS
+  return attn_core<SC>(P, Lw, 0, sp, h, ns, cnt, kr, vr, last ? cnt - 1 : -1, kvn, Ro, true, A);
 }
 
 // Hidden units [item*UNITS, (item+1)*UNITS): gate/up (or fc) rows, the
@@ -964,8 +934,10 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item,
   const int nch = UNITS * ng;
   const int S = (MT / ng) * ng;
   const int nb = (P.NH + PB - 1) / PB;
-  float *gl = smem, *xs = gl + al4(3 * D), *xsum = xs + m * ng * XS, *part = xsum + al4(m * ng);  // part: 2 x (gate || up)
-  float *hs = part + 4 * nch, *hsum = hs + m * 2 * XS, *blk = hsum + al4(2 * m);  // blk: 2 x nb * D, then red
+  float *gl = smem, *part = gl + al4(3 * D) + m * ng * QXR;  // part: 2 x (gate || up)
+  uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // m x ng QX records
+  uint32_t *hq = reinterpret_cast<uint32_t *>(part + 4 * nch);   // m x 2 QX records of h
+  float *blk = reinterpret_cast<float *>(hq + m * 2 * QXR);     // 2 x nb * D, then red
   float *red = blk + 2 * nb * D;
   const float *rbias = gpt2 ? Lw.proj_b : nullptr;
   MlpPre M;
@@ -996,7 +968,7 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item,
       resid_blocks(P.opart + (size_t)t * P.NH * D, nq, P.NH, bt);
     }
     __syncthreads();
-    col_norm(P, col_finish(bt, nq, P.NH, base, gl, D, gpt2), gl, red, xs + t * ng * XS, xsum + t * ng,
+    col_norm(P, col_finish(bt, nq, P.NH, base, gl, D, gpt2), gl, red, qx + t * ng * QXR,
              ColOut{item == 0 ? P.xb + (size_t)t * D : nullptr});
   }
   if (!FLOW) slice_load<MC, MT>(Lw.w2, 2 * item, D, M.Rd);  // needed last: behind everything the prologue reads
@@ -1007,17 +979,13 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item,
     // tile_compute), one barrier, then the token's wave (unit r = lane)
     // forms the rows, the activation and the two group sums of h
     float *pt = part + (t & 1) * 2 * nch;
-    float xr[32];
-    load_group(xs + (t * ng + g) * XS, xr);
-    const float xsg = 8.f * xsum[t * ng + g];
+    const QxRec xr = qx_load(qx + (t * ng + g) * QXR);
 #pragma unroll
     for (int k = 0; k < MC; ++k) {
       const int c = tid() + k * S;
       if ((int)tid() < S && c < nch) {
-        float dg, du;
-        q4_chunk_dot2_reg(M.Rg.w[k], gpt2 ? M.Rg.w[k] : M.Ru.w[k], xr, dg, du);
-        pt[c] = (dg - xsg) * M.Rg.s[k];
-        if (!gpt2) pt[nch + c] = (du - xsg) * M.Ru.s[k];
+        pt[c] = q4_qx_part_reg(M.Rg.w[k], xr, M.Rg.s[k]);
+        if (!gpt2) pt[nch + c] = q4_qx_part_reg(M.Ru.w[k], xr, M.Ru.s[k]);
       }
     }
     __syncthreads();
@@ -1031,34 +999,29 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item,
       } else {
         h = (gv / (1.0f + expf(-gv))) * row_sum(pt + nch + r * ng, ng);
       }
-      hs[t * 2 * XS + skew(r)] = h;
-      const float rs = row16_sum(h);
-      const float ga = readlane_f(rs, 0) + readlane_f(rs, 16), gb = readlane_f(rs, 32) + readlane_f(rs, 48);
-      if (r == 0) hsum[2 * t] = ga;
-      if (r == 32) hsum[2 * t + 1] = gb;
+      qx_stage_lanes(h, hq + t * 2 * QXR);
     }
   }
   __syncthreads();
   for (int t = 0; t < m; ++t)
-    slice_gemv<MC, MT>(M.Rd, D, hs + t * 2 * XS, hsum + 2 * t, P.dpart + ((size_t)t * P.nchunk + item) * D);
+    slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * QXR, P.dpart + ((size_t)t * P.nchunk + item) * D);
 }
 
-// The last layer's residual and the final norm of token t, on wave 0:
-// xs/xsum (LDS) for the lm_head of the persistent kernel, or xn/xnsum
-// (coherent stores) for the lm_head kernel.  blk needs nb * D floats; the
+// The last layer's residual and the final norm of token t: QX records (LDS)
+// for the lm_head of the persistent kernel, or xn (coherent stores) for the
+// lm_head kernel.  blk needs nb * D floats; the
 // caller has staged the norm_f gains in gl.
-__device__ __forceinline__ void final_row(const DecParams &P, int t, float *blk, const float *gl, float *xs,
-                                          float *xsum, bool to_global) {
+__device__ __forceinline__ void final_row(const DecParams &P, int t, float *blk, const float *gl, uint32_t *qx,
+                                          bool to_global) {
   const int D = P.D, nq = D >> 2;
   const float4 base = col_base_load(P.xb + (size_t)t * D, nq);
   resid_blocks(P.dpart + (size_t)t * P.nchunk * D, nq, P.nchunk, blk);
   __syncthreads();
   const float4 x = col_finish(blk, nq, P.nchunk, base, gl, D, P.arch == 1);
-  col_norm(P, x, gl, blk + ((P.nchunk + PB - 1) / PB) * D, xs, xsum,
-           ColOut{nullptr, to_global ? P.xn + (size_t)t * D : nullptr, to_global ? P.xnsum + t * 32 : nullptr});
+  col_norm(P, x, gl, blk + ((P.nchunk + PB - 1) / PB) * D, qx, ColOut{nullptr, to_global ? P.xn + (size_t)t * D : nullptr});
 }
 
-// Kernel-per-phase mode: item t writes xn[t], xnsum[t] (only the rows the
+// Kernel-per-phase mode: item t writes xn[t] (only the rows the
 // lm_head reads).
 __device__ void phase_final(const DecParams &P, int m, int item, const Step &st, float *smem) {
   const int lm_rows = st_ld(P, ST_OFF(lm_rows));
@@ -1071,7 +1034,7 @@ __device__ void phase_final(const DecParams &P, int m, int item, const Step &st,
   GainsReg GR;
   gains_load(P, P.norm_f, rbias, GR);
   gains_store(P, rbias, GR, gl);
-  final_row(P, t, blk, gl, nullptr, nullptr, true);
+  final_row(P, t, blk, gl, nullptr, true);
 }
 
 // argmaxGpt2 (infer.js:252-287) adjustment of one logit given the banned and
@@ -1086,7 +1049,8 @@ __device__ __forceinline__ float gpt2_adjust(float v, int i, const int *ban, int
 }
 
 struct LmLds {
-  float *xs, *xsum, *part, *out;
+  uint32_t *qx;  // the normed rows, QX records
+  float *part, *out;
   int *lists;
 };
 
@@ -1106,7 +1070,7 @@ __device__ __forceinline__ void lm_tile(const DecParams &P, const LmGeom &L, con
                                         int m, const LmLds &s, bool penal, int nban, int nrec) {
   const int ng = P.D >> 5, rpt = L.rpt;
   const int r0 = tile * rpt, nr = min(rpt, P.V - r0);
-  tile_compute<TCN, NT>(R, nr, ng, nr * ng, m, s.xs, s.xsum, tid() % ng, NT % ng, s.part, s.out, rpt);
+  tile_compute_qx<TCN, NT>(R, nr, ng, nr * ng, m, s.qx, tid() % ng, NT % ng, s.part, s.out, rpt);
   for (int e = tid(); e < m * nr; e += NT) {
     const int t = e / nr, r = e - t * nr;
     P.logits[(size_t)(tb + t) * P.V + r0 + r] = s.out[t * rpt + r];
@@ -1156,8 +1120,9 @@ __device__ __forceinline__ void gpt2_lists(const DecParams &P, int *lists) {
   lists[1] = nrec;
 }
 
-// Kernel-per-phase lm_head: row tiles wg, wg + nwg, ...; the normed rows and
-// their group sums come from FINAL (xn, xnsum); the next tile's weights are
+// Kernel-per-phase lm_head: row tiles wg, wg + nwg, ...; the normed rows come
+// from FINAL (xn) and are staged here as in the persistent kernel; the next
+// tile's weights are
 // loaded while the current one is computed (two register sets used in turn,
 // each with constant indices so both stay in VGPRs).
 __device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, const Step &st, float *smem) {
@@ -1170,23 +1135,19 @@ __device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, const S
   const int D = P.D, ng = D >> 5, nq = D >> 2;
   TileRegs<TC> Ra, Rb;
   int tile = wg;
-  // the normed rows first, then the weights (loads retire in issue order)
+  // the normed rows first, then the weights (loads retire in issue order);
+  // thread f of a round stages column f % nq of token f / nq (a token's row
+  // is a multiple of 8 columns, so a group's columns are 8 neighbouring lanes)
   float4 xv[4];
-  float sv = 0.f;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int f = min(tid() + k * LT, m * nq - 1);  // branch-free; extra lanes unused
     xv[k] = coh_ld4(P.xn + (size_t)tb * D, 16u * f);
   }
-  {
-    const int f = min(tid(), m * ng - 1);
-    sv = coh_ldf(P.xnsum, 4u * ((tb + f / ng) * 32 + f % ng));
-  }
   lm_load<TC, LT>(P, L, tile, Ra);
   LmLds s;
-  s.xs = smem;
-  s.xsum = s.xs + m * ng * XS;
-  s.part = s.xsum + al4(m * ng);
+  s.qx = reinterpret_cast<uint32_t *>(smem);
+  s.part = smem + m * ng * QXR;
   s.out = s.part + m * TC * LT;
   s.lists = reinterpret_cast<int *>(s.out + m * L.rpt);  // [0]: nban, [1]: nrec, [2..34): rec, then ban
   const bool penal = P.arch == 1 && st_ld(P, ST_OFF(chain)) != 0;
@@ -1201,14 +1162,10 @@ __device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, const S
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int f = base + tid() + k * LT;
-      if (f < m * nq) {
-        const int t = f / nq, i = 4 * (f - t * nq);
-        *reinterpret_cast<float4 *>(s.xs + (t * ng + (i >> 5)) * XS + (i & 31)) = xv[k];
-      }
+      const int fc = min(f, m * nq - 1), t = fc / nq;
+      qx_stage_col(xv[k], f < m * nq, fc - t * nq, s.qx + t * ng * QXR);
     }
   }
-  if (tid() < m * ng) s.xsum[tid()] = sv;
-  for (int f = tid() + LT; f < m * ng; f += LT) s.xsum[f] = coh_ldf(P.xnsum, 4u * ((tb + f / ng) * 32 + f % ng));
   __syncthreads();
   const int nban = penal ? s.lists[0] : 0, nrec = penal ? s.lists[1] : 0;
   while (tile < L.ntiles) {
@@ -1393,6 +1350,10 @@ __device__ __forceinline__ void flag_st(int *f, int v) {
 // once another workgroup has failed, st->err is set and the wait returns
 // (the host then reports the error; every later wait of the launch returns
 // at once, so the grid drains).
+// A nonzero `sleep` spaces the polls (s_sleep units of 64 clocks): waits
+// that are known to be long poll slowly, so that the flags' memory channel
+// is not flooded while other workgroups publish through it.
+template <int SLEEP = 0>
 __device__ void flow_wait(const DecParams &P, const int *f0, int n0, const int *f1, int n1, const int *f2, int n2,
                           int e) {
   if (tid() < 64) {
@@ -1405,6 +1366,7 @@ __device__ void flow_wait(const DecParams &P, const int *f0, int n0, const int *
       for (int i = lane; i < n1; i += 64) ok &= flag_ld(f1 + i) >= e;
       for (int i = lane; i < n2; i += 64) ok &= flag_ld(f2 + i) >= e;
       if (__all(ok)) break;
+      if (SLEEP) __builtin_amdgcn_s_sleep(SLEEP);
       ++spins;
       if ((spins & 15) == 0) failed = __builtin_amdgcn_readfirstlane(st_ld(P, ST_OFF(err))) != 0;
       if (spins > kSpinLimit) {
@@ -1432,15 +1394,16 @@ struct FlowCtl {
   int e;
   bool pending;  // the step's ARGMAX wait is still due
   bool done;
+  template <int SLEEP = 0>
   __device__ bool wait(const int *f0, int n0, const int *f1 = nullptr, int n1 = 0, const int *f2 = nullptr,
                        int n2 = 0) {
     if (pending) {
-      flow_wait(P, am_flag, 1, nullptr, 0, nullptr, 0, e - 1);
+      flow_wait<SLEEP>(P, am_flag, 1, nullptr, 0, nullptr, 0, e - 1);
       pending = false;
       done = st_ld(P, ST_OFF(done)) != 0;
     }
     if (done) return true;
-    if (n0 + n1 + n2) flow_wait(P, f0, n0, f1, n1, f2, n2, e);
+    if (n0 + n1 + n2) flow_wait<SLEEP>(P, f0, n0, f1, n1, f2, n2, e);
     return false;
   }
 };
@@ -1457,9 +1420,8 @@ __device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, co
   lm_load<FTC, FLT>(P, L, tile, Ra);
   LmLds s;
   float *gl = smem;
-  s.xs = gl + al4(3 * D);
-  s.xsum = s.xs + ng * XS;
-  s.part = s.xsum + al4(ng);
+  s.qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));
+  s.part = gl + al4(3 * D) + ng * QXR;
   s.out = s.part + FTC * FLT;
   s.lists = reinterpret_cast<int *>(s.out + L.rpt);
   float *blk = reinterpret_cast<float *>(s.lists + 34 + P.max_seq);
@@ -1470,7 +1432,7 @@ __device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, co
   if (wait()) return false;
   const bool penal = P.arch == 1 && st_ld(P, ST_OFF(chain)) != 0;
   if (penal && tid() == 0) gpt2_lists(P, s.lists);
-  final_row(P, 0, blk, gl, s.xs, s.xsum, false);
+  final_row(P, 0, blk, gl, s.qx, false);
   __syncthreads();
   const int nban = penal ? s.lists[0] : 0, nrec = penal ? s.lists[1] : 0;
   while (tile < L.ntiles) {
@@ -1526,6 +1488,12 @@ __global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
       }
     }
     if (!C.done && w < nlm) {
+      // the lm_head waits through the whole layer stack: first slowly on
+      // earlier layers, then closely on the last one
+      if (P.L > 4) {
+        C.wait<127>(F.flags + (P.L - 4) * stride + P.NH, F.nm);
+        C.wait<16>(F.flags + (P.L - 2) * stride + P.NH, F.nm);
+      }
       const int *dep = F.flags + (P.L - 1) * stride + P.NH;
       const bool did = flow_lm(P, lg, w, G, st, smem, [&] { return C.wait(dep, F.nm); });
       if (did && !C.done) {
@@ -1616,15 +1584,14 @@ size_t lds_floats(const DecParams &P, int ph, int m) {
   const size_t ngd = P.D / 32, D = P.D;
   const size_t nbo = (P.NH + PB - 1) / PB, nbd = (P.nchunk + PB - 1) / PB;
   switch (ph) {
-  case PH_QKV: return al4(3 * D) + m * ngd * XS + al4(m * ngd) + (size_t)m * HD * ngd + 2 * nbd * D + 32;
+  case PH_QKV: return al4(3 * D) + m * ngd * QXR + (size_t)m * HD * ngd + 2 * nbd * D + 32;
   case PH_ATTN:
-    if (m == 1) return al4(3 * D) + ngd * XS + al4(ngd) + 3 * HD * ngd + nbd * D + 32 + 2 * HD + ATT_LDS;
+    if (m == 1) return al4(3 * D) + ngd * QXR + 3 * HD * ngd + nbd * D + 32 + 2 * HD + ATT_LDS;
     return ATT_LDS;
   case PH_MLP:
-    return al4(3 * D) + m * ngd * XS + al4(m * ngd) + 4 * UNITS * ngd + (size_t)m * 2 * XS + al4(2 * m) + 2 * nbo * D +
-           32;
+    return al4(3 * D) + m * ngd * QXR + 4 * UNITS * ngd + (size_t)m * 2 * QXR + 2 * nbo * D + 32;
   case PH_FINAL: return al4(3 * D) + nbd * D + 32;
-  case PH_LM: return m * ngd * XS + al4(m * ngd) + (size_t)m * TC * LT + (size_t)m * P.lm_rpt + 34 + P.max_seq;
+  case PH_LM: return m * ngd * QXR + (size_t)m * TC * LT + (size_t)m * P.lm_rpt + 34 + P.max_seq;
   default: return 2 * (LT / 64);
   }
 }
@@ -1636,7 +1603,7 @@ size_t flow_lds_bytes(const DecParams &P, const FlowGeom &F) {
   size_t f = 2 * (FLT / 64);
   for (int ph = PH_QKV; ph <= PH_FINAL; ++ph) f = std::max(f, lds_floats(P, ph, 1));
   const size_t nbd = (P.nchunk + PB - 1) / PB;
-  f = std::max(f, al4(3 * (size_t)P.D) + ngd * XS + al4(ngd) + (size_t)FTC * FLT + (size_t)F.lm_rpt + 34 + P.max_seq +
+  f = std::max(f, al4(3 * (size_t)P.D) + ngd * QXR + (size_t)FTC * FLT + (size_t)F.lm_rpt + 34 + P.max_seq +
                       nbd * P.D + 32);
   return f * sizeof(float);
 }
@@ -1998,7 +1965,6 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   if (!rc) rc = dev_alloc(M, (void **)&P.opart, sizeof(float) * MAXT * NH * D);
   if (!rc) rc = dev_alloc(M, (void **)&P.dpart, sizeof(float) * MAXT * P.nchunk * D);
   if (!rc) rc = dev_alloc(M, (void **)&P.xn, sizeof(float) * MAXT * D);
-  if (!rc) rc = dev_alloc(M, (void **)&P.xnsum, sizeof(float) * MAXT * 32);
   if (!rc) rc = dev_alloc(M, (void **)&P.q, sizeof(float) * MAXT * NH * HD);
   if (!rc) rc = dev_alloc(M, &P.kv, kv_elems * (c.kv_fp16 ? 2 : 4));
   if (!rc) rc = dev_alloc(M, (void **)&P.attp, sizeof(float) * MAXT * NH * P.nsplit_max * APS);
