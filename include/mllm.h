@@ -173,11 +173,14 @@ int mllm_decode_chain(mllm_model *model, int32_t first, int n_steps, int32_t eos
 /* model.gemv(name, x, y) (infer.js:338-346): host x [cols] -> host y [rows]. */
 int mllm_model_gemv(mllm_model *model, const char *name, const float *x, float *y);
 
-/* Execution mode of the decode step: 1 (default) = one kernel per phase, a
- * chained decode step replayed from a HIP graph; 2 = the same kernels
- * launched directly (for profilers); 0 = one persistent cooperative kernel per
- * launch with grid barriers between phases.  Results are bit-identical
- * across modes. */
+/* Execution mode of the single-token decode step.  3 (the default where the
+ * device can co-schedule one workgroup per CU) = one persistent cooperative
+ * kernel per decode call or chain, its workgroups ordered by per-item epoch
+ * flags instead of grid barriers; 1 (the default otherwise) = one kernel per
+ * phase, a chained step replayed from a HIP graph; 2 = the phase kernels
+ * launched directly (for profilers).  Multi-token passes (prefill, verify)
+ * always use the phase kernels.  Results are bit-identical across modes.
+ * Returns MLLM_ERR_UNSUPPORTED for mode 3 where it is unavailable. */
 int mllm_set_exec_mode(mllm_model *model, int mode);
 
 /* GpuPetitGPT.lastTiming {n, gpuMs} (webgpu.js:1143-1160): the time between

@@ -2013,6 +2013,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       if (int rc = dev_alloc(M, (void **)&F.flags, sizeof(int) * nflags)) return fail(rc);
       if (hipMemset(F.flags, 0, sizeof(int) * nflags) != hipSuccess) return fail(set_error(MLLM_ERR_HIP, "memset"));
       M->flow_grid = G;
+      M->exec_mode = 3;
     }
     (void)hipGetLastError();
   }

@@ -62,7 +62,8 @@ def argmax_gpt2(logits: np.ndarray, history: List[int], no_repeat_ngram: int = 3
 class PetitGPT:
     """infer.js PetitGPT on the MI355X decode step."""
 
-    def __init__(self, bundle: Bundle, norm_eps: float = 1e-6, kv_fp16: bool = False, exec_mode: int = 1):
+    def __init__(self, bundle: Bundle, norm_eps: float = 1e-6, kv_fp16: bool = False,
+                 exec_mode: Optional[int] = None):
         self.bundle = bundle
         self.cfg = bundle.cfg
         self.kind = bundle.kind
@@ -88,7 +89,9 @@ class PetitGPT:
         self._h = h
         self._logits = np.zeros(c.vocab_size, np.float32)
         self.max_pass = abi.lib().mllm_max_pass_tokens(h)
-        self.set_exec_mode(exec_mode)
+        self.exec_mode = None
+        if exec_mode is not None:
+            self.set_exec_mode(exec_mode)
         self.lastTiming = None
 
     # ---------------------------------------------------------------- state
