@@ -1,20 +1,15 @@
 // mllm_device.h -- device building blocks shared by the operator kernels and
-// the decode engine (gfx950, wave64, 256-thread workgroups).
+// the decode engine (gfx950, wave64).
 //
-// GEMV scheme for group-32 Q4 at batch 1 (no MFMA):
-//   * A row-major [m][n/2] nibble matrix is one contiguous byte stream, and the
-//     16-byte "chunk" c (= 32 weights = one quant group) has its scale at
-//     scale[c].  Consecutive threads take consecutive chunks, so every 128-bit
-//     load of a wavefront covers 1 KiB of contiguous HBM.
-//   * The activation vector x is staged once per workgroup in LDS as
-//     [group][36] floats (32 used, 4 of skew so neighbouring lanes' 128-bit LDS
-//     reads land in different banks), with the per-group sum xsum[g].
-//   * In registers a chunk is unpacked as two masked dwords per 8 weights
-//     (v_cvt_f32_ubyte0..3 on (d & 0x0f0f0f0f) and ((d >> 4) & 0x0f0f0f0f));
-//     the "-8" is applied once per group as  sum(q*x) - 8*sum(x), then * scale.
-//   * Per-chunk partials go to LDS and each row is summed over its groups in
-//     ascending order by one thread: a fixed order, so a row's result does not
-//     depend on how many tokens share the pass (the verify pass relies on it).
+// Q4 group-32 weights at batch 1 are read as 16-byte "chunks" (the 32
+// nibbles of one group of one row; scale[c] belongs to chunk c), so every
+// 128-bit load of a wavefront covers 1 KiB of contiguous memory.  The
+// activations are quantised per group to integers and dotted with the
+// nibbles by the byte/nibble dot instructions (no MFMA): the decode engine
+// uses 16-bit records (QX, below), the standalone GEMV of mllm_ops.hip 24-bit
+// ones.  Per-chunk partials are summed per row in a fixed order that does not
+// depend on how rows or tokens are split across workgroups, so a row's value
+// is the same in every launch shape (the verify pass relies on it).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -24,8 +19,7 @@ namespace mllm {
 
 constexpr int WG = 256;          // threads per workgroup
 constexpr int XS = 36;           // LDS floats per staged 32-float group
-constexpr int CPT = 4;           // chunks per thread per sub-tile
-constexpr int SUB_CH = WG * CPT; // chunks per sub-tile
+constexpr int SUB_CH = WG * 4;   // chunks per sub-tile of the Q8 GEMV
 
 // The thread index as a value the compiler cannot move.  Inside the
 // persistent decode kernel's loops it would otherwise hoist every
@@ -46,142 +40,7 @@ struct Q4Mat {
   int rows, cols;  // cols % 32 == 0
 };
 
-// AND through inline asm: the mask stays opaque to the known-bits combiner,
-// so (float)((v >> 8k) & 0xff) below selects v_cvt_f32_ubyte{k} on the masked
-// dword instead of a v_bfe_u32 per weight.
-__device__ __forceinline__ uint32_t and_opaque(uint32_t v, uint32_t mask) {
-  uint32_t r;
-  asm("v_and_b32 %0, %1, %2" : "=v"(r) : "s"(mask), "v"(v));
-  return r;
-}
-
 __device__ __forceinline__ float ubyte(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xFFu); }
-
-// One 16-byte chunk (32 weights of one group) against 32 staged floats:
-// returns sum_k q_k * x_k with q_k the raw nibble (0..15).  Even elements are
-// the low nibbles; odd elements are taken in place (16 * q) and rescaled by
-// 1/16 (exact) at the end: 2 ANDs + 8 conversions + 8 FMAs per 8 weights.
-__device__ __forceinline__ float q4_chunk_dot(const uint4 w, const float *__restrict__ xg) {
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-  const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t lo = and_opaque(dw[j], 0x0F0F0F0Fu);
-    const uint32_t hi = and_opaque(dw[j], 0xF0F0F0F0u);
-    const float4 xa = *reinterpret_cast<const float4 *>(xg + 8 * j);
-    const float4 xb = *reinterpret_cast<const float4 *>(xg + 8 * j + 4);
-    a0 = __builtin_fmaf(ubyte(lo, 0), xa.x, a0);
-    a1 = __builtin_fmaf(ubyte(hi, 0), xa.y, a1);
-    a2 = __builtin_fmaf(ubyte(lo, 1), xa.z, a2);
-    a3 = __builtin_fmaf(ubyte(hi, 1), xa.w, a3);
-    a0 = __builtin_fmaf(ubyte(lo, 2), xb.x, a0);
-    a1 = __builtin_fmaf(ubyte(hi, 2), xb.y, a1);
-    a2 = __builtin_fmaf(ubyte(lo, 3), xb.z, a2);
-    a3 = __builtin_fmaf(ubyte(hi, 3), xb.w, a3);
-  }
-  return (a0 + a2) + (a1 + a3) * 0.0625f;
-}
-
-// q4_chunk_dot with the activations read in two halves, so only 16 of them
-// are live at a time (same operations in the same order: the same bits).
-__device__ __forceinline__ float q4_chunk_dot_lean(const uint4 w, const float *__restrict__ xg) {
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-  const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (j == 2) __builtin_amdgcn_sched_barrier(0);
-    const uint32_t lo = and_opaque(dw[j], 0x0F0F0F0Fu);
-    const uint32_t hi = and_opaque(dw[j], 0xF0F0F0F0u);
-    const float4 xa = *reinterpret_cast<const float4 *>(xg + 8 * j);
-    const float4 xb = *reinterpret_cast<const float4 *>(xg + 8 * j + 4);
-    a0 = __builtin_fmaf(ubyte(lo, 0), xa.x, a0);
-    a1 = __builtin_fmaf(ubyte(hi, 0), xa.y, a1);
-    a2 = __builtin_fmaf(ubyte(lo, 1), xa.z, a2);
-    a3 = __builtin_fmaf(ubyte(hi, 1), xa.w, a3);
-    a0 = __builtin_fmaf(ubyte(lo, 2), xb.x, a0);
-    a1 = __builtin_fmaf(ubyte(hi, 2), xb.y, a1);
-    a2 = __builtin_fmaf(ubyte(lo, 3), xb.z, a2);
-    a3 = __builtin_fmaf(ubyte(hi, 3), xb.w, a3);
-  }
-  return (a0 + a2) + (a1 + a3) * 0.0625f;
-}
-
-// Two chunks of the same group (e.g. the gate and up rows of one hidden
-// unit) against one read of the 32 staged activations: each result has the
-// arithmetic of q4_chunk_dot.
-__device__ __forceinline__ void q4_chunk_dot2(const uint4 wa, const uint4 wb, const float *__restrict__ xg, float &da,
-                                              float &db) {
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
-  const uint32_t dwa[4] = {wa.x, wa.y, wa.z, wa.w}, dwb[4] = {wb.x, wb.y, wb.z, wb.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float4 xa = *reinterpret_cast<const float4 *>(xg + 8 * j);
-    const float4 xb = *reinterpret_cast<const float4 *>(xg + 8 * j + 4);
-    const uint32_t la = and_opaque(dwa[j], 0x0F0F0F0Fu), ha = and_opaque(dwa[j], 0xF0F0F0F0u);
-    const uint32_t lb = and_opaque(dwb[j], 0x0F0F0F0Fu), hb = and_opaque(dwb[j], 0xF0F0F0F0u);
-    a0 = __builtin_fmaf(ubyte(la, 0), xa.x, a0);
-    a1 = __builtin_fmaf(ubyte(ha, 0), xa.y, a1);
-    a2 = __builtin_fmaf(ubyte(la, 1), xa.z, a2);
-    a3 = __builtin_fmaf(ubyte(ha, 1), xa.w, a3);
-    a0 = __builtin_fmaf(ubyte(la, 2), xb.x, a0);
-    a1 = __builtin_fmaf(ubyte(ha, 2), xb.y, a1);
-    a2 = __builtin_fmaf(ubyte(la, 3), xb.z, a2);
-    a3 = __builtin_fmaf(ubyte(ha, 3), xb.w, a3);
-    b0 = __builtin_fmaf(ubyte(lb, 0), xa.x, b0);
-    b1 = __builtin_fmaf(ubyte(hb, 0), xa.y, b1);
-    b2 = __builtin_fmaf(ubyte(lb, 1), xa.z, b2);
-    b3 = __builtin_fmaf(ubyte(hb, 1), xa.w, b3);
-    b0 = __builtin_fmaf(ubyte(lb, 2), xb.x, b0);
-    b1 = __builtin_fmaf(ubyte(hb, 2), xb.y, b1);
-    b2 = __builtin_fmaf(ubyte(lb, 3), xb.z, b2);
-    b3 = __builtin_fmaf(ubyte(hb, 3), xb.w, b3);
-  }
-  da = (a0 + a2) + (a1 + a3) * 0.0625f;
-  db = (b0 + b2) + (b1 + b3) * 0.0625f;
-}
-
-// q4_chunk_dot2 with the group's 32 activations in registers.
-__device__ __forceinline__ void q4_chunk_dot2_reg(const uint4 wa, const uint4 wb, const float (&x)[32], float &da,
-                                                  float &db) {
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
-  const uint32_t dwa[4] = {wa.x, wa.y, wa.z, wa.w}, dwb[4] = {wb.x, wb.y, wb.z, wb.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float *xg = x + 8 * j;
-    const uint32_t la = and_opaque(dwa[j], 0x0F0F0F0Fu), ha = and_opaque(dwa[j], 0xF0F0F0F0u);
-    const uint32_t lb = and_opaque(dwb[j], 0x0F0F0F0Fu), hb = and_opaque(dwb[j], 0xF0F0F0F0u);
-    a0 = __builtin_fmaf(ubyte(la, 0), xg[0], a0);
-    a1 = __builtin_fmaf(ubyte(ha, 0), xg[1], a1);
-    a2 = __builtin_fmaf(ubyte(la, 1), xg[2], a2);
-    a3 = __builtin_fmaf(ubyte(ha, 1), xg[3], a3);
-    a0 = __builtin_fmaf(ubyte(la, 2), xg[4], a0);
-    a1 = __builtin_fmaf(ubyte(ha, 2), xg[5], a1);
-    a2 = __builtin_fmaf(ubyte(la, 3), xg[6], a2);
-    a3 = __builtin_fmaf(ubyte(ha, 3), xg[7], a3);
-    b0 = __builtin_fmaf(ubyte(lb, 0), xg[0], b0);
-    b1 = __builtin_fmaf(ubyte(hb, 0), xg[1], b1);
-    b2 = __builtin_fmaf(ubyte(lb, 1), xg[2], b2);
-    b3 = __builtin_fmaf(ubyte(hb, 1), xg[3], b3);
-    b0 = __builtin_fmaf(ubyte(lb, 2), xg[4], b0);
-    b1 = __builtin_fmaf(ubyte(hb, 2), xg[5], b1);
-    b2 = __builtin_fmaf(ubyte(lb, 3), xg[6], b2);
-    b3 = __builtin_fmaf(ubyte(hb, 3), xg[7], b3);
-  }
-  da = (a0 + a2) + (a1 + a3) * 0.0625f;
-  db = (b0 + b2) + (b1 + b3) * 0.0625f;
-}
-
-// The 32 staged activations of one group (skewed layout) into registers.
-__device__ __forceinline__ void load_group(const float *xg, float (&x)[32]) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float4 v = *reinterpret_cast<const float4 *>(xg + 4 * j);
-    x[4 * j] = v.x;
-    x[4 * j + 1] = v.y;
-    x[4 * j + 2] = v.z;
-    x[4 * j + 3] = v.w;
-  }
-}
 
 // 16 signed 8-bit weights against 16 floats: sum((u - 128) * x) with
 // u = q ^ 0x80 converted by v_cvt_f32_ubyte; the -128 is folded by the caller.
@@ -460,20 +319,6 @@ __device__ __forceinline__ void wave_argmax(float &v, int &i) {
   i = bi;
 }
 
-// Per-group sums of the staged activations: xsum[t*ng+g] = sum_k xs[(t*ng+g)*XS+k]
-// in ascending k.  Call after xs is complete (a barrier follows inside).
-template <int NT = WG>
-__device__ __forceinline__ void stage_group_sums(const float *xs, float *xsum, int m, int ng) {
-  for (int i = tid(); i < m * ng; i += NT) {
-    const float *p = xs + i * XS;
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < 32; ++k) s += p[k];
-    xsum[i] = s;
-  }
-  __syncthreads();
-}
-
 // Copy m rows x[t*ldx + i] (i < n, n % 32 == 0, 16-byte aligned rows) into
 // the skewed layout.  Loads go out in batches of 4 float4 per thread before
 // any LDS store, so a batch costs one memory latency, not one per element.
@@ -518,14 +363,6 @@ __device__ __forceinline__ void stage_rows(const float *__restrict__ x, int ldx,
     stage_rows_load<NT>(x, ldx, m, n, base, v);
     stage_rows_store<NT>(m, n, base, v, xs);
   }
-}
-
-// Plain staging of m vectors x[t*ldx + i] (i < n) into the skewed layout.
-__device__ __forceinline__ void stage_plain(const float *__restrict__ x, int ldx, int m, int n, float *xs,
-                                            float *xsum) {
-  stage_rows(x, ldx, m, n, xs);
-  __syncthreads();
-  stage_group_sums(xs, xsum, m, n >> 5);
 }
 
 // Sum of a row's n group partials in a fixed order: eight interleaved
@@ -648,43 +485,6 @@ __device__ __forceinline__ void tile_load_strided(const Q4Mat &W, int r0, int nr
   }
 }
 
-// out[t*ostride + r] for tile row r in [0, nrows): rows of range a first.
-// part needs m*nch floats of LDS.  gfirst = tid() % ng, gstep = NT % ng.
-template <int C, int NT = WG>
-__device__ __forceinline__ void tile_compute(const TileRegs<C> &R, int nrows, int ng, int nch, int m,
-                                             const float *xs, const float *xsum, int gfirst, int gstep,
-                                             float *part, float *out, int ostride) {
-  // Group index of each register chunk, computed once; the token loop is the
-  // outer one so every R.w[j] / R.s[j] access has a constant index and the
-  // tile stays in VGPRs (a runtime index would move it to scratch memory).
-  int gj[C];
-  {
-    int g = gfirst;
-#pragma unroll
-    for (int j = 0; j < C; ++j) {
-      gj[j] = g;
-      g += gstep;
-      if (g >= ng) g -= ng;
-    }
-  }
-  for (int t = 0; t < m; ++t) {
-#pragma unroll
-    for (int j = 0; j < C; ++j) {
-      const int c = tid() + j * NT;
-      if (c < nch) {
-        const float d = q4_chunk_dot(R.w[j], xs + (t * ng + gj[j]) * XS);
-        part[t * nch + c] = (d - 8.f * xsum[t * ng + gj[j]]) * R.s[j];
-      }
-    }
-  }
-  __syncthreads();
-  for (int i = tid(); i < nrows * m; i += NT) {
-    const int t = i / nrows, r = i - t * nrows;
-    out[t * ostride + r] = row_sum(part + t * nch + r * ng, ng);
-  }
-  __syncthreads();
-}
-
 // tile_compute with the activations staged as QX records (m tokens x ng
 // groups).
 template <int C, int NT = WG>
@@ -714,20 +514,6 @@ __device__ __forceinline__ void tile_compute_qx(const TileRegs<C> &R, int nrows,
     out[t * ostride + r] = row_sum(part + t * nch + r * ng, ng);
   }
   __syncthreads();
-}
-
-// Q4 GEMV over rows [row0, row0 + nrows) of W for m staged vectors, in
-// sub-tiles of at most SUB_CH chunks: out[t*ostride + r].
-__device__ __forceinline__ void gemv_q4_rows(const Q4Mat &W, int row0, int nrows, int m, const float *xs,
-                                             const float *xsum, int ng, int gfirst, int gstep, float *part,
-                                             float *out, int ostride) {
-  const int rows_per_sub = SUB_CH / ng > 0 ? SUB_CH / ng : 1;
-  for (int rs = 0; rs < nrows; rs += rows_per_sub) {
-    const int nr = min(rows_per_sub, nrows - rs);
-    TileRegs<CPT> R;
-    tile_load<CPT>(W, row0 + rs, nr, 0, ng, nr * ng, R);
-    tile_compute<CPT>(R, nr, ng, nr * ng, m, xs, xsum, gfirst, gstep, part, out + rs, ostride);
-  }
 }
 
 }  // namespace mllm

@@ -1556,6 +1556,7 @@ struct mllm_model {
   // persistent kernel (exec mode 3)
   FlowGeom flow{};
   int flow_grid = 0;      // 0: not available on this device
+  bool flow_default = false;  // mode 3 was chosen by default, not by mllm_set_exec_mode
   size_t flow_lds = 0;
   int flow_epoch = 0;     // epochs used so far (flags hold epochs, never cleared)
   int aq_idx = 0;         // instance of the decode attention item / persistent kernel (tile size 4, 5, 6)
@@ -1684,17 +1685,31 @@ int launch_phase(mllm_model *M, int ph, int li, int m, hipEvent_t e0 = nullptr, 
 }
 
 // One cooperative launch of the persistent kernel: `steps` single-token
-// steps (chained when the pass state says so).
+// steps (chained when the pass state says so).  Returns kFlowFellBack when
+// the runtime refuses the cooperative launch (e.g. another process holds
+// the device's cooperative-launch resources) and mode 3 was only the
+// default: the model then switches to mode 1 for good and the caller
+// enqueues the phase kernels instead (same results, bit for bit).
+constexpr int kFlowFellBack = -1;
 int launch_flow(mllm_model *M, int steps) {
   FlowGeom F = M->flow;
   F.ep0 = M->flow_epoch + 1;
   F.steps = steps;
-  M->flow_epoch += steps;
   void *args[] = {&M->P, &F};
-  MLLM_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(kFlowKernels[M->aq_idx]), dim3(M->flow_grid),
-                                      dim3(FLT), args,
-                                      M->flow_lds, M->stream));
-  return 0;
+  const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(kFlowKernels[M->aq_idx]),
+                                                  dim3(M->flow_grid), dim3(FLT), args, M->flow_lds, M->stream);
+  if (e == hipSuccess) {
+    M->flow_epoch += steps;
+    return 0;
+  }
+  if (M->flow_default && (e == hipErrorIllegalState || e == hipErrorNotSupported ||
+                          e == hipErrorCooperativeLaunchTooLarge)) {
+    (void)hipGetLastError();
+    M->exec_mode = 1;
+    M->flow_grid = 0;
+    return kFlowFellBack;
+  }
+  return hip_fail(e, "hipLaunchCooperativeKernel(k_flow)", __FILE__, __LINE__);
 }
 
 // The phases of one pass in order: (phase, layer) pairs.
@@ -1772,11 +1787,9 @@ int run_pass(mllm_model *M, const int32_t *ids, int m, int pos0, int lm_rows) {
   for (int i = 0; i < m; ++i) s.tok[i] = ids[i];
   if (int rc = upload_state(M)) return rc;
   MLLM_HIP(hipEventRecord(M->ev0, M->stream));
-  if (M->exec_mode == 3 && m == 1 && lm_rows == 1) {
-    if (int rc = launch_flow(M, 1)) return rc;
-  } else {
-    if (int rc = enqueue_pass_phases(M, m, lm_rows != 0)) return rc;
-  }
+  int rc = M->exec_mode == 3 && m == 1 && lm_rows == 1 ? launch_flow(M, 1) : kFlowFellBack;
+  if (rc == kFlowFellBack) rc = enqueue_pass_phases(M, m, lm_rows != 0);
+  if (rc) return rc;
   MLLM_HIP(hipEventRecord(M->ev1, M->stream));
   MLLM_HIP(hipStreamSynchronize(M->stream));
   MLLM_HIP(hipEventElapsedTime(&M->last_ms, M->ev0, M->ev1));
@@ -2014,6 +2027,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       if (hipMemset(F.flags, 0, sizeof(int) * nflags) != hipSuccess) return fail(set_error(MLLM_ERR_HIP, "memset"));
       M->flow_grid = G;
       M->exec_mode = 3;
+      M->flow_default = true;
     }
     (void)hipGetLastError();
   }
@@ -2069,6 +2083,7 @@ extern "C" int mllm_set_exec_mode(mllm_model *M, int mode) {
              mode);
   if (mode == 3 && !M->flow_grid) return set_error(MLLM_ERR_UNSUPPORTED, "persistent kernel unavailable on this device");
   M->exec_mode = mode;
+  M->flow_default = false;
   return 0;
 }
 
@@ -2136,16 +2151,17 @@ extern "C" int mllm_decode_chain(mllm_model *M, int32_t first, int n_steps, int3
   s.tok[0] = first;
   if (int rc = upload_state(M)) return rc;
   MLLM_HIP(hipEventRecord(M->ev0, M->stream));
-  if (M->exec_mode == 3) {
-    if (int rc = launch_flow(M, n_steps)) return rc;
-  } else if (M->exec_mode == 2) {
-    for (int i = 0; i < n_steps; ++i)
-      if (int rc = enqueue_pass_phases(M, 1, true)) return rc;
-  } else {
-    if (!M->chain_graph)
-      if (int rc = build_chain_graph(M)) return rc;
-    for (int i = 0; i < n_steps; ++i) MLLM_HIP(hipGraphLaunch(M->chain_graph, M->stream));
+  int rc = M->exec_mode == 3 ? launch_flow(M, n_steps) : kFlowFellBack;
+  if (rc == kFlowFellBack) {
+    rc = 0;
+    if (M->exec_mode == 2) {
+      for (int i = 0; i < n_steps && !rc; ++i) rc = enqueue_pass_phases(M, 1, true);
+    } else {
+      if (!M->chain_graph) rc = build_chain_graph(M);
+      for (int i = 0; i < n_steps && !rc; ++i) MLLM_HIP(hipGraphLaunch(M->chain_graph, M->stream));
+    }
   }
+  if (rc) return rc;
   MLLM_HIP(hipEventRecord(M->ev1, M->stream));
   MLLM_HIP(hipStreamSynchronize(M->stream));
   MLLM_HIP(hipEventElapsedTime(&M->last_ms, M->ev0, M->ev1));

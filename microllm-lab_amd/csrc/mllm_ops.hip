@@ -41,45 +41,183 @@ extern "C" const char *mllm_last_error(void) { return mllm::g_err.c_str(); }
 extern "C" int mllm_kernel_version(void) { return 1; }
 
 // ---------------------------------------------------------------- Q4 GEMV
-// Tiles of rows_per_tile rows; each workgroup stages the m vectors once and
-// walks tiles grid-stride.  y[t][rows] row-major.
-__global__ __launch_bounds__(WG) void k_gemv_q4(Q4Mat W, const float *__restrict__ x, float *__restrict__ y,
-                                                 int m, int rows_per_tile, int ntiles) {
-  extern __shared__ float4 smem4[];
-  float *smem = reinterpret_cast<float *>(smem4);
-  const int ng = W.cols >> 5;
-  float *xs = smem;
-  float *xsum = xs + m * ng * XS;
-  float *part = xsum + m * ng;
-  stage_plain(x, W.cols, m, W.cols, xs, xsum);
-  const int gfirst = threadIdx.x % ng, gstep = WG % ng;
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int row0 = tile * rows_per_tile;
-    const int nr = min(rows_per_tile, W.rows - row0);
-    gemv_q4_rows(W, row0, nr, m, xs, xsum, ng, gfirst, gstep, part, y + row0, W.rows);
+// The activations are taken as 24-bit integers per 32-element group (the Q4
+// group): xi = rint(x * XMAX / amax), sx = amax / XMAX (amax = max |x| of
+// the group).  Each xi is held as six signed 4-bit digits,
+// xi = sum_k 16^k d_k with d_k in [-8, 7], and flipping bit 3 of a stored
+// nibble q gives the signed nibble q - 8, so one dot8 (eight 4-bit
+// products) per 8 weights and digit plane yields
+//   dot = sum_k 16^k sum_e (q_e - 8) d_{k,e} = sum_e (q_e - 8) xi_e,
+// exact in int32: |dot| <= 32 * 8 * XMAX < 2^31 (the Horner partial sums
+// may wrap; the final value does not).  A group adds (float)dot * sx *
+// w_scale to its row.  Rounding x to 24 bits moves it by at most
+// amax / (2 XMAX) = 6.4e-8 amax, the size of one float32 rounding.
+//
+// Digits: with u = xi + C (C = 8 (16^6 - 1) / 15, so u >= 0), digit k of xi
+// is hex digit k of u minus 8, i.e. its 4-bit pattern is bfe(u, 4k, 4) ^ 8.
+//
+// Work split: thread t < rpp * ng keeps group g = t % ng of rows
+// rpp * p + t / ng of its tile for p < P, so each thread reads one group
+// record and the loads of a pass are contiguous across the workgroup; the
+// row sums go through LDS in a fixed order that depends only on ng.
+constexpr int Q6R = 28;              // dwords per group record: 6 digit planes x 4 dwords, sx, padding
+constexpr int Q6C = 8947848;         // 8 * (16^6 - 1) / 15
+constexpr float Q6MAX = 7829360.0f;  // below 7 * (16^6 - 1) / 15 = 7829367 by more than the rcp rounding
+constexpr int GX_BATCH = 4;          // float4s of x per thread loaded ahead of the weights
+
+// Stage the float4 column q of the activations (elements 4q .. 4q+3 of
+// group q >> 3; a group is 8 neighbouring lanes).  Whole waves call it.
+__device__ __forceinline__ void q6_stage_col(float4 y, bool in, int q, uint32_t *rec0) {
+  if (!in) y = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float a = max8(fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+  const float inv = a > 0.f ? Q6MAX * __builtin_amdgcn_rcpf(a) : 0.f;
+  const uint32_t u0 = (uint32_t)((int)__builtin_rintf(y.x * inv) + Q6C);
+  const uint32_t u1 = (uint32_t)((int)__builtin_rintf(y.y * inv) + Q6C);
+  const uint32_t u2 = (uint32_t)((int)__builtin_rintf(y.z * inv) + Q6C);
+  const uint32_t u3 = (uint32_t)((int)__builtin_rintf(y.w * inv) + Q6C);
+  if (!in) return;
+  uint32_t *rec = rec0 + (q >> 3) * Q6R;
+  uint8_t *rb = reinterpret_cast<uint8_t *>(rec);
+  // elements 8j .. 8j+7 of the group are dword j of a plane, nibble i = element 8j + i
+  const int off = 4 * ((q & 7) >> 1) + 2 * (q & 1);
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    const uint32_t v = __builtin_amdgcn_ubfe(u0, 4 * k, 4) | (__builtin_amdgcn_ubfe(u1, 4 * k, 4) << 4) |
+                       (__builtin_amdgcn_ubfe(u2, 4 * k, 4) << 8) | (__builtin_amdgcn_ubfe(u3, 4 * k, 4) << 12);
+    *reinterpret_cast<unsigned short *>(rb + 16 * k + off) = (unsigned short)(v ^ 0x8888u);
+  }
+  if ((q & 7) == 0) rec[24] = __float_as_uint(a * (1.0f / Q6MAX));
+}
+
+// One 16-byte chunk (the 32 weights of one group of one row) against the
+// group's record xr (24 digit dwords) with activation scale sx and weight
+// scale ws.
+__device__ __forceinline__ float q4_dot6(const uint4 w, const uint32_t *xr, float sx, float ws) {
+  const int d[4] = {(int)(w.x ^ 0x88888888u), (int)(w.y ^ 0x88888888u), (int)(w.z ^ 0x88888888u),
+                    (int)(w.w ^ 0x88888888u)};
+  int acc = 0;
+#pragma unroll
+  for (int k = 5; k >= 0; --k) {
+    if (k < 5) acc = (int)((uint32_t)acc << 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_sdot8(d[j], (int)xr[4 * k + j], acc, false);
+  }
+  return ((float)acc * sx) * ws;
+}
+
+// Sum over lpr (a power of two <= 64) neighbouring lanes; whole lpr-lane
+// segments are active.
+__device__ __forceinline__ float seg_sum(float a, int lpr) {
+  if (lpr > 1) a += dpp_f<0xB1>(a);    // lane ^ 1
+  if (lpr > 2) a += dpp_f<0x4E>(a);    // lane ^ 2
+  if (lpr > 4) a += dpp_f<0x141>(a);   // mirror within 8
+  if (lpr > 8) a += dpp_f<0x140>(a);   // mirror within 16
+  if (lpr > 16) a += __shfl_xor(a, 16);
+  if (lpr > 32) a += __shfl_xor(a, 32);
+  return a;
+}
+
+struct GemvGeom {
+  int rows, cols, m;  // matrix shape; tokens
+  int rpp, lpr;       // rows per pass; lanes per row sum (power of two <= 64)
+  int ystride;        // y[t * ystride + r]
+};
+
+// One tile (P passes of rpp rows) of y = W x for m tokens.
+template <int WGT, int P>
+__device__ __forceinline__ void q4_gemv_tile(const uint8_t *__restrict__ packed, const float *__restrict__ scale,
+                                             const float *__restrict__ x, float *__restrict__ y, const GemvGeom &G,
+                                             int tile, uint32_t *lds) {
+  const int ng = G.cols >> 5, nq = G.cols >> 2, nx = G.m * nq;
+  const int ngp = 4 * ((ng + 3) >> 2), RT = G.rpp * P;
+  uint32_t *rec = lds;                                          // [m][ng][Q6R]
+  float *part = reinterpret_cast<float *>(lds + G.m * ng * Q6R);  // [m][RT][ngp]
+  const int t = threadIdx.x;
+  const int rr0 = t / ng;
+  const bool act = rr0 < G.rpp;
+  const int rr = act ? rr0 : 0, g = act ? t - rr0 * ng : 0;
+  const int row0 = tile * RT;
+  // x ahead of the weights: loads retire in order, so the staging below
+  // waits for x alone while the weights are in flight
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  float4 xv[GX_BATCH];
+#pragma unroll
+  for (int i = 0; i < GX_BATCH; ++i) {
+    const int q = t + i * WGT;
+    xv[i] = x4[q < nx ? q : 0];
+  }
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(packed), (short)0,
+                                                                      0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(scale), (short)0,
+                                                                      0x7fffffff, 0x00020000);
+  uint4 w[P];
+  float s[P];
+  const int last = G.rows - 1;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int row = min(row0 + p * G.rpp + rr, last);
+    const uint32_t c = (uint32_t)(row * ng + g);
+    w[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(c * 16), 0, 0));
+    s[p] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(c * 4), 0, 0));
+  }
+#pragma unroll
+  for (int i = 0; i < GX_BATCH; ++i)
+    if (i * WGT < nx) q6_stage_col(xv[i], t + i * WGT < nx, t + i * WGT, rec);
+  for (int base = GX_BATCH * WGT; base < nx; base += WGT) {
+    const int q = base + t;
+    q6_stage_col(x4[q < nx ? q : 0], q < nx, q, rec);
+  }
+  __syncthreads();
+  if (act) {
+    for (int tok = 0; tok < G.m; ++tok) {
+      const uint32_t *r = rec + (tok * ng + g) * Q6R;
+      uint32_t xr[24];
+#pragma unroll
+      for (int k = 0; k < 6; ++k) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(r + 4 * k);
+        xr[4 * k] = v.x;
+        xr[4 * k + 1] = v.y;
+        xr[4 * k + 2] = v.z;
+        xr[4 * k + 3] = v.w;
+      }
+      const float sx = __uint_as_float(r[24]);
+      float *pp = part + (tok * RT + rr) * ngp + g;
+#pragma unroll
+      for (int p = 0; p < P; ++p) pp[p * G.rpp * ngp] = q4_dot6(w[p], xr, sx, s[p]);
+    }
+  }
+  __syncthreads();
+  // row sums: lpr lanes per row, lane l adds float4s 4l, 4l + 4 lpr, ...
+  const int nr = min(RT, G.rows - row0);
+  for (int i = t; i < G.m * RT * G.lpr; i += WGT) {
+    const int r = i / G.lpr, l = i - r * G.lpr;
+    const int tok = r / RT, rl = r - tok * RT;
+    float a = 0.f;
+    for (int gi = 4 * l; gi < ng; gi += 4 * G.lpr) {
+      const float4 v = *reinterpret_cast<const float4 *>(part + r * ngp + gi);
+      a += ((v.x + (gi + 1 < ng ? v.y : 0.f)) + ((gi + 2 < ng ? v.z : 0.f) + (gi + 3 < ng ? v.w : 0.f)));
+    }
+    a = seg_sum(a, G.lpr);
+    if (l == 0 && rl < nr) y[tok * G.ystride + row0 + rl] = a;
   }
 }
 
-// One launch over `count` same-shape matrices: blockIdx.y selects the matrix.
-__global__ __launch_bounds__(WG) void k_gemv_q4_batched(const uint8_t *const *__restrict__ packed,
-                                                         const float *const *__restrict__ scale,
-                                                         const float *const *__restrict__ xv, float *const *__restrict__ yv,
-                                                         int rows, int cols, int rows_per_tile, int ntiles) {
+template <int WGT, int P>
+__global__ __launch_bounds__(WGT) void k_gemv_q4(const uint8_t *__restrict__ packed, const float *__restrict__ scale,
+                                                 const float *__restrict__ x, float *__restrict__ y, GemvGeom G) {
   extern __shared__ float4 smem4[];
-  float *smem = reinterpret_cast<float *>(smem4);
+  q4_gemv_tile<WGT, P>(packed, scale, x, y, G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4));
+}
+
+// One launch over same-shape matrices: blockIdx.y selects the matrix.
+template <int WGT, int P>
+__global__ __launch_bounds__(WGT) void k_gemv_q4_batched(const uint8_t *const *__restrict__ packed,
+                                                         const float *const *__restrict__ scale,
+                                                         const float *const *__restrict__ xv,
+                                                         float *const *__restrict__ yv, GemvGeom G) {
+  extern __shared__ float4 smem4[];
   const int b = blockIdx.y;
-  Q4Mat W{reinterpret_cast<const uint4 *>(packed[b]), scale[b], rows, cols};
-  const int ng = cols >> 5;
-  float *xs = smem;
-  float *xsum = xs + ng * XS;
-  float *part = xsum + ng;
-  stage_plain(xv[b], cols, 1, cols, xs, xsum);
-  const int gfirst = threadIdx.x % ng, gstep = WG % ng;
-  float *y = yv[b];
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int row0 = tile * rows_per_tile;
-    gemv_q4_rows(W, row0, min(rows_per_tile, rows - row0), 1, xs, xsum, ng, gfirst, gstep, part, y + row0, rows);
-  }
+  q4_gemv_tile<WGT, P>(packed[b], scale[b], xv[b], yv[b], G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4));
 }
 
 // ---------------------------------------------------------------- Q8 GEMV
@@ -207,10 +345,37 @@ int device_wg_cap() {
   return cap;
 }
 
-constexpr int kMaxCols = 16384;  // staged x must fit LDS: 144 B per 32 columns
-constexpr int kMaxTok = 8;       // tokens per gemm launch
+constexpr int kMaxCols = 16384;              // staged x must fit LDS
+constexpr int kMaxTok = 8;                   // tokens per gemm launch
+constexpr size_t kQ4LdsMax = 96 * 1024;      // LDS budget of one Q4 GEMV workgroup
 
-size_t q4_lds_bytes(int m, int ng) { return sizeof(float) * ((size_t)m * ng * XS + (size_t)m * ng + (size_t)m * SUB_CH); }
+// Geometry of the Q4 GEMV for a column count: workgroup size, rows per pass
+// (one group per thread), lanes per row sum.
+struct Q4Plan {
+  int wgt, rpp, lpr, ngp;
+};
+Q4Plan q4_plan(int cols) {
+  const int ng = cols / 32;
+  Q4Plan p;
+  p.wgt = ng <= 256 ? 256 : 512;
+  p.rpp = p.wgt / ng;
+  p.lpr = 1;
+  while (p.lpr < 64 && p.lpr * 4 < ng) p.lpr <<= 1;
+  p.ngp = 4 * ((ng + 3) / 4);
+  return p;
+}
+size_t q4_lds_bytes(const Q4Plan &pl, int ng, int m, int P) {
+  return sizeof(float) * ((size_t)m * ng * Q6R + (size_t)m * pl.rpp * P * pl.ngp);
+}
+// Passes per tile: the largest P in {8, 4, 2, 1} that still gives at least
+// 4 workgroups per CU, so every load of a launch is in flight at once while
+// the per-workgroup staging of x is spread over several passes.
+int q4_pick_p(int rows, int rpp, int count) {
+  const long target = 4L * (device_wg_cap() / 8);
+  int P = 8;
+  while (P > 1 && (long)((rows + rpp * P - 1) / (rpp * P)) * count < target) P >>= 1;
+  return P;
+}
 
 template <typename K>
 int launch_dyn(K kernel, dim3 grid, size_t lds, hipStream_t st, const char *name) {
@@ -228,20 +393,50 @@ int check_q4_shape(int m, int n, int group) {
   return 0;
 }
 
+template <int WGT, int P>
+int q4_launch_one(dim3 grid, size_t lds, hipStream_t st, const uint8_t *packed, const float *scale, const float *x,
+                  float *y, const GemvGeom &G) {
+  if (int rc = launch_dyn(k_gemv_q4<WGT, P>, grid, lds, st, "k_gemv_q4")) return rc;
+  hipLaunchKernelGGL((k_gemv_q4<WGT, P>), grid, dim3(WGT), lds, st, packed, scale, x, y, G);
+  MLLM_HIP(hipGetLastError());
+  return 0;
+}
+
+template <int WGT, int P>
+int q4_launch_batched(dim3 grid, size_t lds, hipStream_t st, const uint8_t *const *packed, const float *const *scale,
+                      const float *const *x, float *const *y, const GemvGeom &G) {
+  if (int rc = launch_dyn(k_gemv_q4_batched<WGT, P>, grid, lds, st, "k_gemv_q4_batched")) return rc;
+  hipLaunchKernelGGL((k_gemv_q4_batched<WGT, P>), grid, dim3(WGT), lds, st, packed, scale, x, y, G);
+  MLLM_HIP(hipGetLastError());
+  return 0;
+}
+
+// Run F<WGT, P>(args...) for the runtime (wgt, P) of a plan.
+#define MLLM_Q4_DISPATCH(F, wgt, P, ...)                                     \
+  ((wgt) == 256 ? ((P) == 8 ? F<256, 8>(__VA_ARGS__)                         \
+                   : (P) == 4 ? F<256, 4>(__VA_ARGS__)                       \
+                   : (P) == 2 ? F<256, 2>(__VA_ARGS__)                       \
+                              : F<256, 1>(__VA_ARGS__))                      \
+                : ((P) == 8 ? F<512, 8>(__VA_ARGS__)                         \
+                   : (P) == 4 ? F<512, 4>(__VA_ARGS__)                       \
+                   : (P) == 2 ? F<512, 2>(__VA_ARGS__)                       \
+                              : F<512, 1>(__VA_ARGS__)))
+
 int q4_gemm(int t, int m, int n, const uint8_t *packed, const float *scale, const float *x, float *y,
             hipStream_t st) {
+  MLLM_CHECK((size_t)m * n / 2 < (1ull << 31), "matrix of %zu bytes exceeds 2 GiB", (size_t)m * n / 2);
   const int ng = n / 32;
-  const int rpt = SUB_CH / ng > 0 ? SUB_CH / ng : 1;
-  const int ntiles = (m + rpt - 1) / rpt;
-  const int grid = ntiles < device_wg_cap() ? ntiles : device_wg_cap();
-  Q4Mat W{reinterpret_cast<const uint4 *>(packed), scale, m, n};
-  for (int t0 = 0; t0 < t; t0 += kMaxTok) {
-    const int mt = t - t0 < kMaxTok ? t - t0 : kMaxTok;
-    const size_t lds = q4_lds_bytes(mt, ng);
-    if (int rc = launch_dyn(k_gemv_q4, grid, lds, st, "k_gemv_q4")) return rc;
-    hipLaunchKernelGGL(k_gemv_q4, dim3(grid), dim3(WG), lds, st, W, x + (size_t)t0 * n, y + (size_t)t0 * m, mt, rpt,
-                       ntiles);
-    MLLM_HIP(hipGetLastError());
+  const Q4Plan pl = q4_plan(n);
+  const int P = q4_pick_p(m, pl.rpp, 1);
+  const int ntiles = (m + pl.rpp * P - 1) / (pl.rpp * P);
+  for (int t0 = 0; t0 < t;) {
+    int mt = t - t0 < kMaxTok ? t - t0 : kMaxTok;
+    while (mt > 1 && q4_lds_bytes(pl, ng, mt, P) > kQ4LdsMax) --mt;
+    const GemvGeom G{m, n, mt, pl.rpp, pl.lpr, m};
+    if (int rc = MLLM_Q4_DISPATCH(q4_launch_one, pl.wgt, P, dim3(ntiles), q4_lds_bytes(pl, ng, mt, P), st, packed,
+                                  scale, x + (size_t)t0 * n, y + (size_t)t0 * m, G))
+      return rc;
+    t0 += mt;
   }
   return 0;
 }
@@ -270,18 +465,14 @@ extern "C" int mllm_gemv_q4_batched(int count, int m, int n, const uint8_t *cons
   if (int rc = check_q4_shape(m, n, 32)) return rc;
   MLLM_CHECK(count > 0 && count <= 65535, "count=%d", count);
   MLLM_CHECK(packed && scale && x && y, "null pointer");
+  MLLM_CHECK((size_t)m * n / 2 < (1ull << 31), "matrix of %zu bytes exceeds 2 GiB", (size_t)m * n / 2);
   const int ng = n / 32;
-  const int rpt = SUB_CH / ng > 0 ? SUB_CH / ng : 1;
-  const int ntiles = (m + rpt - 1) / rpt;
-  int gx = device_wg_cap() / count;
-  if (gx < 1) gx = 1;
-  if (gx > ntiles) gx = ntiles;
-  const size_t lds = q4_lds_bytes(1, ng);
-  hipStream_t st = as_stream(stream);
-  if (int rc = launch_dyn(k_gemv_q4_batched, dim3(gx, count), lds, st, "k_gemv_q4_batched")) return rc;
-  hipLaunchKernelGGL(k_gemv_q4_batched, dim3(gx, count), dim3(WG), lds, st, packed, scale, x, y, m, n, rpt, ntiles);
-  MLLM_HIP(hipGetLastError());
-  return 0;
+  const Q4Plan pl = q4_plan(n);
+  const int P = q4_pick_p(m, pl.rpp, count);
+  const int ntiles = (m + pl.rpp * P - 1) / (pl.rpp * P);
+  const GemvGeom G{m, n, 1, pl.rpp, pl.lpr, m};
+  return MLLM_Q4_DISPATCH(q4_launch_batched, pl.wgt, P, dim3(ntiles, count), q4_lds_bytes(pl, ng, 1, P),
+                          as_stream(stream), packed, scale, x, y, G);
 }
 
 static int q8_common(int m, int n, const int8_t *q, const float *scale, const float *x, float *y, int per_row,
