@@ -1,38 +1,43 @@
 // mllm_engine.hip -- the fused single-token Q4 decode step on MI355X and the
 // engine-level C ABI (PetitGPT API of engine/infer.js:289-647).
 //
-// One decode step = L x [QKV, ATTN, MLP] + FINAL + LM + ARGMAX kernels
-// (the graph of engine/infer.js:579-601; the reference GPU runs it as 244
-// dispatches, engine/webgpu-metal.js:1242-1322):
-//   QKV    16-row tiles of blocks.i.attn.qkv holding RoPE partner rows d, d+32
-//          prologue: embed (layer 0) or x = xb + sum of the previous layer's
-//          down-projection partials; RMSNorm/LayerNorm in LDS
+// One decode step = L x [QKV, ATTN, MLP] + FINAL + LM + ARGMAX (the graph
+// of engine/infer.js:579-601; the reference GPU runs it as 244 dispatches,
+// engine/webgpu-metal.js:1242-1322):
+//   QKV    (multi-token passes) one head's 64 q, k or v rows per workgroup;
+//          prologue: embed (layer 0) or the residual sum of the previous
+//          layer's down-projection partials, then RMSNorm/LayerNorm;
 //          epilogue: bias (gpt2), RoPE (llama), q -> scratch, k/v -> KV cache
 //   ATTN   one workgroup per (token, 256-position split, head): scores,
-//          split-local softmax statistics and P.V.  The last split of a
-//          (token, head) to finish (the only one below 256 positions) merges
-//          the splits and multiplies the head's attention output by its
-//          64-column slice of attn.proj: a per-head partial of W_o . att.
-//   MLP    one workgroup per 64 hidden units: x = xa + sum of the per-head
+//          split-local softmax statistics and P.V; the last split of a
+//          (token, head) merges the splits and multiplies the head output by
+//          its 64-column slice of attn.proj, a per-head partial of W_o . att.
+//          At one token (decode) the head's q/k/v rows are computed inside
+//          the item itself (QKV fused in): residual sum, norm, q/k/v GEMV,
+//          RoPE, KV-cache write, then attention.
+//   MLP    one workgroup per 64 hidden units: residual sum of the per-head
 //          partials (+ proj bias), norm2, gate and up rows of its units ->
 //          silu(g)*u (gpt2: fc + bias -> GELU-tanh), then those units'
 //          64-column slice of the down projection: a per-chunk partial of
 //          W_2 . h
-//   FINAL  per token: x = xb + the down partials (+ bias), final norm
-//   LM     grid-stride row tiles of the tied lm_head with the next tile's
-//          weights in flight; logits + per-tile argmax (gpt2 chain: 3-gram
-//          block and repetition penalty of infer.js:252-287)
-//   ARGMAX one workgroup: first maximum over tiles; chained decode feeds it
-//          back as the next input token (CHAIN_TOK, webgpu-metal.js:609-610).
+//   FINAL  per token: residual sum of the down partials (+ bias), final norm
+//   LM     row tiles of the tied lm_head; logits + per-tile argmax (gpt2
+//          chain: 3-gram block and repetition penalty of infer.js:252-287)
+//   ARGMAX first maximum over tiles; chained decode feeds it back as the
+//          next input token (CHAIN_TOK, webgpu-metal.js:609-610).
 // The split-K partials are summed by their consumer in a fixed order, so
 // every result is deterministic.  Every GEMV issues its weight loads before
-// it stages its activations, so the two memory latencies overlap.
+// it stages its activations, so the two memory latencies overlap.  The GEMVs
+// take their activations as 16-bit integer records per 32-element group and
+// use byte dot products (QX, mllm_device.h).
 //
-// Execution: mode 1 (default) replays a HIP graph of one kernel per phase;
-// mode 2 launches the same kernels directly.  Both run the same kernels.  (A
-// persistent kernel with grid barriers between phases measured slower than
-// graph replay here: one barrier over 256 workgroups cost ~17 us against
-// ~1.6 us per graph node.)
+// Execution modes, all running the same per-item device code:
+//   3 (default where the device co-schedules one 1024-thread workgroup per
+//     CU) one persistent cooperative kernel per decode call or chain; items
+//     are ordered by per-item epoch flags, not barriers (k_flow below);
+//   1 a HIP graph of one kernel per phase, replayed per token;
+//   2 the phase kernels launched directly (for profilers).
+// Multi-token passes (prefill, verify) always run the phase kernels.
 //
 // Every per-token computation (norm, GEMV row, attention split, merge, the
 // partial sums, argmax) runs the same instruction sequence whatever the
