@@ -106,9 +106,29 @@ __device__ __forceinline__ void coh_sti(void *base, uint32_t off, int v) {
 __device__ __forceinline__ void coh_sth(void *base, uint32_t off, unsigned short v) {
   __builtin_amdgcn_raw_buffer_store_b16(v, coh_rsrc(base), (int)off, 0, CP_SC1);
 }
+__device__ __forceinline__ void coh_st8(void *base, uint32_t off, uint2 v) {
+  const u32x2_t u = {v.x, v.y};
+  __builtin_amdgcn_raw_buffer_store_b64(u, coh_rsrc(base), (int)off, 0, CP_SC1);
+}
+__device__ __forceinline__ void coh_st16(void *base, uint32_t off, uint4 v) {
+  const u32x4_t u = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(u, coh_rsrc(base), (int)off, 0, CP_SC1);
+}
 // Wait until this thread's stores (and loads) have completed: a workgroup
 // barrier alone does not wait for them.
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0) */ }
+
+// Tagged values.  A value handed from one workgroup to another inside the
+// persistent kernel travels with the tag of the (step, layer) that wrote it,
+// as one naturally aligned 64-bit (float bits, tag) pair: a 64-bit access is
+// single-copy atomic, so a reader that sees the tag it waits for also sees
+// that writer's value, and polling the data replaces a completion wait plus
+// a flag.  Tags grow across launches and are compared modulo 2^32.
+__device__ __forceinline__ bool tag_ok(uint32_t tag, int want) { return (int)(tag - (uint32_t)want) >= 0; }
+__device__ __forceinline__ uint2 tagged(float v, int tag) { return make_uint2(__float_as_uint(v), (uint32_t)tag); }
+// A compiler barrier for polling loops: the loads after it are issued again
+// on every iteration instead of being hoisted out of the loop.
+__device__ __forceinline__ void poll_fence() { asm volatile("" ::: "memory"); }
 
 // ---------------------------------------------------------------- integer group dots
 // The decode engine's GEMVs take their activations quantised per 32-element

@@ -112,6 +112,7 @@ struct PassState {
   int n_hist;    // tokens in hist[] (gpt2 argmax history / chain output)
   int err;       // device-side error flag (reported by the next host check)
   int bad_tok;   // ARGMAX found no finite maximum (chain fed token 0 instead)
+  int tag0;      // tag base of a kernel-per-phase pass (below every later persistent-kernel tag)
   int tok[MAXT];
   int res[MAXT];  // argmax per lm row
 };
@@ -123,10 +124,10 @@ struct DecParams {
   Q4Mat lm;
   const float *norm_f, *wpe, *sf, *rope_cos, *rope_sin;
   const float *last_mproj_b;  // gpt2: mlp.proj bias of the last layer
-  float *xa;      // [MAXT][D] residual entering the attention block
-  float *xb;      // [MAXT][D] residual entering the MLP block
-  float *opart;   // [MAXT][NH][D] per-head partials of W_o . att
-  float *dpart;   // [MAXT][nchunk][D] per-chunk partials of W_2 . h
+  uint2 *xa;      // [MAXT][D] tagged residual entering the attention block
+  uint2 *xb;      // [MAXT][D] tagged residual entering the MLP block
+  uint2 *opart;   // [MAXT][NH][D] tagged per-head partials of W_o . att
+  uint2 *dpart;   // [MAXT][nchunk][D] tagged per-chunk partials of W_2 . h
   float *xn;      // [MAXT][D] final-normed rows for the lm_head
   float *q;       // [MAXT][NH*HD] queries after RoPE
   void *kv;       // [L][2][NKV][max_seq][HD] (f32 or f16)
@@ -144,7 +145,9 @@ struct DecParams {
 struct Step {
   int pos0;   // position of token 0
   bool done;  // a chained decode already emitted eos: issue the first loads, store nothing
+  int tag;    // tag of layer 0's handoff values; layer li writes tag + li
 };
+constexpr int TAGL = 128;  // tags per step (layers < TAGL)
 
 // The pass state is read and written with coherent access: inside the
 // persistent kernel ARGMAX updates it for workgroups on other XCDs.
@@ -210,25 +213,53 @@ __device__ __forceinline__ void gains_store(const DecParams &P, const float *bia
 //   x = base + (((B_0 + B_1) + ... + B_{nb-1}) + bias)
 // where B_b sums parts[p] for p in [b*PB, min(np, (b+1)*PB)) in ascending p
 // (from +0).  The order of every addition is fixed by np alone.
-// The block sums use every thread of a 1024-thread workgroup: item
-// it = b * nq + c (round it / 1024) forms B_b of float4 column c into blk[it]
-// (LDS).  A round's loads all go out before its first add, so a round costs
-// one memory latency; round 0 can be loaded ahead (resid_blocks_load) so its
-// latency overlaps the weight loads.  Branch-free: an item or partial past
-// the end reads partial 0 of column 0 (valid memory) and is left out.
+// The partials are tagged (value, tag) pairs; a 16-byte load carries two
+// neighbouring columns.  The block sums use every thread of a 1024-thread
+// workgroup: item it = b * nq2 + c (nq2 = D / 2 column pairs, round
+// it / 1024) forms B_b of columns 2c, 2c+1 into blk[b*D + 2c ..] (LDS).  A
+// round's loads all go out before its first add, so a round costs one
+// memory latency; round 0 can be loaded ahead (resid_blocks_load) so its
+// latency overlaps the weight loads.  With POLL (persistent kernel) a round
+// is loaded again until every pair carries a tag of at least `want`.
+// Branch-free: an item or partial past the end reads partial 0 of column 0
+// (valid memory) and is left out.
 struct ResidReg {
-  float4 v[PB];
+  uint4 v[PB];
 };
 
-__device__ __forceinline__ void resid_blocks_load(const float *pt, int nq, int np, int round, ResidReg &R) {
-  const int nitems = nq * ((np + PB - 1) / PB);
+// Spin bound of the data polls: as kSpinLimit for flags; on time-out (or
+// once another workgroup failed) the error is recorded and the wait returns.
+__device__ __forceinline__ bool poll_give_up(const DecParams &P, unsigned spins);
+
+template <bool POLL>
+__device__ __forceinline__ void resid_blocks_load(const DecParams &P, const uint2 *pt, int nq2, int np, int round,
+                                                  int want, ResidReg &R) {
+  const int nitems = nq2 * ((np + PB - 1) / PB);
   const int it = tid() + round * 1024;
-  const int b = it / nq, c = it - b * nq;
+  const int b = it / nq2, c = it - b * nq2;
 #pragma unroll
   for (int k = 0; k < PB; ++k) {
     const int p = b * PB + k;
     const bool ok = it < nitems && p < np;
-    R.v[k] = coh_ld4(pt, 16u * (ok ? (uint32_t)(p * nq + c) : 0u));
+    R.v[k] = coh_ld16(pt, 16u * (ok ? (uint32_t)(p * nq2 + c) : 0u));
+  }
+  if (POLL) {
+    for (unsigned spins = 1;; ++spins) {
+      bool ready = true;
+#pragma unroll
+      for (int k = 0; k < PB; ++k) {
+        const bool ok = it < nitems && b * PB + k < np;
+        ready &= !ok || (tag_ok(R.v[k].y, want) && tag_ok(R.v[k].w, want));
+      }
+      if (ready || poll_give_up(P, spins)) break;
+      poll_fence();
+#pragma unroll
+      for (int k = 0; k < PB; ++k) {
+        const int p = b * PB + k;
+        const bool ok = it < nitems && p < np;
+        R.v[k] = coh_ld16(pt, 16u * (ok ? (uint32_t)(p * nq2 + c) : 0u));
+      }
+    }
   }
 }
 
@@ -236,35 +267,40 @@ __device__ __forceinline__ void resid_blocks_load(const float *pt, int nq, int n
 // conditional): a load consumed inside a divergent branch leaves the
 // compiler unsure it has completed, and it then waits for every load in
 // flight before the register is reused.
-__device__ __forceinline__ void resid_blocks_add(int nq, int np, int round, const ResidReg &R, float *blk) {
-  const int nitems = nq * ((np + PB - 1) / PB);
+__device__ __forceinline__ void resid_blocks_add(int nq2, int np, int round, const ResidReg &R, float *blk) {
+  const int nitems = nq2 * ((np + PB - 1) / PB);
   const int it = tid() + round * 1024;
-  const int b = it / nq;
-  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int b = it / nq2;
+  float2 a = make_float2(0.f, 0.f);
 #pragma unroll
   for (int k = 0; k < PB; ++k) {
-    const float4 w = R.v[k];
+    const uint4 w = R.v[k];
     const bool use = b * PB + k < np;
-    a = add4(a, make_float4(use ? w.x : 0.f, use ? w.y : 0.f, use ? w.z : 0.f, use ? w.w : 0.f));
+    a.x = a.x + (use ? __uint_as_float(w.x) : 0.f);
+    a.y = a.y + (use ? __uint_as_float(w.z) : 0.f);
   }
-  if (it < nitems) reinterpret_cast<float4 *>(blk)[it] = a;
+  if (it < nitems) reinterpret_cast<float2 *>(blk)[it] = a;
 }
 
-// Every round of the block sums, round 0 already loaded into R0 (at most
-// two rounds: nq * nb <= 2048).
-__device__ __forceinline__ void resid_blocks_rest(const float *pt, int nq, int np, const ResidReg &R0, float *blk) {
-  resid_blocks_add(nq, np, 0, R0, blk);
-  if (nq * ((np + PB - 1) / PB) > 1024) {
+// Every round of the block sums, round 0 already loaded into R0.
+template <bool POLL>
+__device__ __forceinline__ void resid_blocks_rest(const DecParams &P, const uint2 *pt, int nq2, int np, int want,
+                                                  const ResidReg &R0, float *blk) {
+  resid_blocks_add(nq2, np, 0, R0, blk);
+  const int nitems = nq2 * ((np + PB - 1) / PB);
+  for (int round = 1; round * 1024 < nitems; ++round) {
     ResidReg R1;
-    resid_blocks_load(pt, nq, np, 1, R1);
-    resid_blocks_add(nq, np, 1, R1, blk);
+    resid_blocks_load<POLL>(P, pt, nq2, np, round, want, R1);
+    resid_blocks_add(nq2, np, round, R1, blk);
   }
 }
 
-__device__ __forceinline__ void resid_blocks(const float *pt, int nq, int np, float *blk) {
+template <bool POLL>
+__device__ __forceinline__ void resid_blocks(const DecParams &P, const uint2 *pt, int nq2, int np, int want,
+                                             float *blk) {
   ResidReg R0;
-  resid_blocks_load(pt, nq, np, 0, R0);
-  resid_blocks_rest(pt, nq, np, R0, blk);
+  resid_blocks_load<POLL>(P, pt, nq2, np, 0, want, R0);
+  resid_blocks_rest<POLL>(P, pt, nq2, np, want, R0, blk);
 }
 
 // One token's residual and norm, one float4 column q < nq per thread
@@ -279,7 +315,8 @@ __device__ __forceinline__ void resid_blocks(const float *pt, int nq, int np, fl
 // thread of the workgroup must call it (it holds barriers); red needs
 // 2 x 16 floats.
 struct ColOut {
-  float *x;  // the residual row (coherent store), or null
+  uint2 *x;  // the residual row (tagged coherent stores), or null
+  int tag;   // its tag
   float *y;  // the normalised row (coherent store), or null
 };
 
@@ -311,7 +348,10 @@ __device__ __forceinline__ void col_norm(const DecParams &P, float4 x, const flo
   const int D = P.D, nq = D >> 2, q = tid(), nw = (nq + 63) >> 6;
   const bool in = q < nq;
   if (!in) x = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (o.x && in) coh_st4(o.x, 16u * q, x);
+  if (o.x && in) {
+    coh_st16(o.x, 32u * q, make_uint4(__float_as_uint(x.x), (uint32_t)o.tag, __float_as_uint(x.y), (uint32_t)o.tag));
+    coh_st16(o.x, 32u * q + 16u, make_uint4(__float_as_uint(x.z), (uint32_t)o.tag, __float_as_uint(x.w), (uint32_t)o.tag));
+  }
   const float inv_d = 1.0f / (float)D;
   const float4 *g4 = reinterpret_cast<const float4 *>(gl);
   const int qc = min(q, nq - 1);
@@ -335,9 +375,22 @@ __device__ __forceinline__ void col_norm(const DecParams &P, float4 x, const flo
   if (qx_t && wave_id() < nw) qx_stage_col(y, in, q, qx_t);
 }
 
-// The base column of this thread (coherent load, branch-free).
-__device__ __forceinline__ float4 col_base_load(const float *base, int nq) {
-  return coh_ld4(base, 16u * min(tid(), nq - 1));
+// The base column of this thread from a tagged row (coherent loads,
+// branch-free); with POLL, loaded again until its tags reach `want`.
+template <bool POLL>
+__device__ __forceinline__ float4 col_base_load(const DecParams &P, const uint2 *base, int nq, int want) {
+  const uint32_t q = (uint32_t)min(tid(), nq - 1);
+  uint4 a = coh_ld16(base, 32u * q), b = coh_ld16(base, 32u * q + 16u);
+  if (POLL && tid() < nq) {
+    for (unsigned spins = 1; !(tag_ok(a.y, want) && tag_ok(a.w, want) && tag_ok(b.y, want) && tag_ok(b.w, want)) &&
+                             !poll_give_up(P, spins);
+         ++spins) {
+      poll_fence();
+      a = coh_ld16(base, 32u * q);
+      b = coh_ld16(base, 32u * q + 16u);
+    }
+  }
+  return make_float4(__uint_as_float(a.x), __uint_as_float(a.z), __uint_as_float(b.x), __uint_as_float(b.z));
 }
 
 // Per-chunk partials of a tile in registers for m staged tokens:
@@ -388,7 +441,7 @@ __device__ __forceinline__ void slice_load(const Q4Mat &W, int g0, int rows, Til
 // groups (coherent stores).  Neighbouring lanes hold the pair; every lane
 // takes part in the shuffle.
 template <int C, int NT>
-__device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const uint32_t *v, float *out) {
+__device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const uint32_t *v, uint2 *out, int tag) {
 #pragma unroll
   for (int k = 0; k < C; ++k) {
     const int c = tid() + k * NT;
@@ -396,7 +449,7 @@ __device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const
     float p = 0.f;
     if (c < 2 * rows) p = q4_qx_part(R.w[k], v + j * QXR, R.s[k]);
     const float sum = p + lane_xor1(p);
-    if (c < 2 * rows && j == 0) coh_stf(out, 4u * (c >> 1), sum);
+    if (c < 2 * rows && j == 0) coh_st8(out, 8u * (c >> 1), tagged(sum, tag));
   }
 }
 
@@ -498,13 +551,13 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
     // loads retire in issue order: everything the prologue reads goes out
     // before the weight tile, so the prologue never waits for the weights
     if (li > 0) {
-      base = col_base_load(P.xb, nq);
-      resid_blocks_load(P.dpart, nq, P.nchunk, 0, R0);
+      base = col_base_load<false>(P, P.xb, nq, 0);
+      resid_blocks_load<false>(P, P.dpart, D >> 1, P.nchunk, 0, 0, R0);
     }
     gains_load(P, Lw.n1, rbias, GR);
     qkv_pre(P, Lw, head, pos0, Q);
     if (st.done) return;  // a chained decode that reached eos: loads only, no stores
-    if (li > 0) resid_blocks_rest(P.dpart, nq, P.nchunk, R0, blk);
+    if (li > 0) resid_blocks_rest<false>(P, P.dpart, D >> 1, P.nchunk, 0, R0, blk);
     gains_store(P, rbias, GR, gl);
   }
   // stage every token: x, the norm, its QX records
@@ -514,12 +567,12 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
       const int tok = min(max(st_ld(P, ST_OFF(tok) + 4u * t), 0), P.V - 1);  // host and ARGMAX keep it in range
       base = embed_col(P, tok, min(pos0 + t, P.max_seq - 1));
     } else if (FLOW || t > 0) {
-      base = col_base_load(P.xb + (size_t)t * D, nq);
-      resid_blocks(P.dpart + (size_t)t * P.nchunk * D, nq, P.nchunk, bt);
+      base = col_base_load<FLOW>(P, P.xb + (size_t)t * D, nq, st.tag + li - 1);
+      resid_blocks<FLOW>(P, P.dpart + (size_t)t * P.nchunk * D, D >> 1, P.nchunk, st.tag + li - 1, bt);
     }
     __syncthreads();
     const float4 x = li == 0 ? base : col_finish(bt, nq, P.nchunk, base, gl, D, rbias != nullptr);
-    col_norm(P, x, gl, red, qx + t * ng * QXR, ColOut{head == 0 ? P.xa + (size_t)t * D : nullptr});
+    col_norm(P, x, gl, red, qx + t * ng * QXR, ColOut{head == 0 ? P.xa + (size_t)t * D : nullptr, st.tag + li});
   }
   __syncthreads();
   tile_partials<QC>(Q.R, ng, nch, m, qx, part);
@@ -638,7 +691,7 @@ __device__ __forceinline__ void attn_v_load(const DecParams &P, int li, int kvh,
 template <int C>
 __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, int h, int ns, int cnt,
                           const float4 (&kr)[4], const float4 (&vr)[4], int knew, const float *kvn, TileRegs<C> &Ro,
-                          bool ro_loaded, const AttnLds &A) {
+                          bool ro_loaded, const AttnLds &A, int tag) {
   const int D = P.D;
   const bool solo = ns == 1;
   const int kp = tid() >> 2, ku = tid() & 3;
@@ -752,8 +805,11 @@ __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, i
     }
     qx_stage_lanes(v, A.attq);  // the head output: two groups, wave 0
   }
+  // the item's earlier stores (its K/V cache row) complete before the head's
+  // output becomes visible, so whoever sees the output also sees them
+  wait_stores();
   __syncthreads();
-  slice_gemv<C, AT>(Ro, D, A.attq, P.opart + (size_t)(t * P.NH + h) * D);
+  slice_gemv<C, AT>(Ro, D, A.attq, P.opart + (size_t)(t * P.NH + h) * D, tag);
   return true;
 }
 
@@ -784,7 +840,7 @@ __device__ bool phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, 
   attn_v_load(P, li, h / (P.NH / P.NKV), s0, cnt, vr);
   const bool ro = FLOW || ns == 1;
   if (!FLOW && ns == 1) slice_load<SC, AT>(Lw.proj, 2 * h, P.D, Ro);  // behind the K/V loads
-  return attn_core<SC>(P, Lw, t, sp, h, ns, cnt, kr, vr, -1, A.qs, Ro, ro, A);  // no key from LDS
+  return attn_core<SC>(P, Lw, t, sp, h, ns, cnt, kr, vr, -1, A.qs, Ro, ro, A, st.tag + li);  // no key from LDS
 }
 
 // Weights and other inputs of a fused decode attention item that do not
@@ -856,17 +912,17 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
     gains_store(P, rbias, GR, gl);
     if (wait()) return false;
     if (li > 0) {
-      base = col_base_load(P.xb, nq);
-      resid_blocks(P.dpart, nq, P.nchunk, blk);
+      base = col_base_load<true>(P, P.xb, nq, st.tag + li - 1);
+      resid_blocks<true>(P, P.dpart, D >> 1, P.nchunk, st.tag + li - 1, blk);
     }
   } else {
     // activations first, then the weights (loads retire in issue order)
     if (li > 0) {
-      base = col_base_load(P.xb, nq);
-      resid_blocks_load(P.dpart, nq, P.nchunk, 0, R0);
+      base = col_base_load<false>(P, P.xb, nq, 0);
+      resid_blocks_load<false>(P, P.dpart, D >> 1, P.nchunk, 0, 0, R0);
     }
     attn1_pre(P, Lw, rq, rk, rv, h, pos, row_own, rbias, Wt, Ro, c_own, s_own, GR);
-    if (li > 0) resid_blocks_rest(P.dpart, nq, P.nchunk, R0, blk);
+    if (li > 0) resid_blocks_rest<false>(P, P.dpart, D >> 1, P.nchunk, 0, R0, blk);
     gains_store(P, rbias, GR, gl);
   }
   // stage boundaries are fixed (sched_barrier) so that the tile, the K rows
@@ -878,7 +934,7 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   if (li == 0) base = embed_col(P, min(max(st_ld(P, ST_OFF(tok)), 0), P.V - 1), min(pos, P.max_seq - 1));
   __syncthreads();
   const float4 x = li == 0 ? base : col_finish(blk, nq, P.nchunk, base, gl, D, rbias != nullptr);
-  col_norm(P, x, gl, red, qx, ColOut{item == 0 ? P.xa : nullptr});
+  col_norm(P, x, gl, red, qx, ColOut{item == 0 ? P.xa : nullptr, st.tag + li});
   __syncthreads();
   tile_partials<AQC>(Wt, ng, nch, 1, qx, part);
   __builtin_amdgcn_sched_barrier(0);
@@ -910,7 +966,7 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
     }
   }
   // the current position (key cnt - 1 of the last split) comes from LDS
-  return attn_core<SC>(P, Lw, 0, sp, h, ns, cnt, kr, vr, last ? cnt - 1 : -1, kvn, Ro, true, A);
+  return attn_core<SC>(P, Lw, 0, sp, h, ns, cnt, kr, vr, last ? cnt - 1 : -1, kvn, Ro, true, A, st.tag + li);
 }
 
 // Hidden units [item*UNITS, (item+1)*UNITS): gate/up (or fc) rows, the
@@ -932,7 +988,7 @@ __device__ __forceinline__ void mlp_pre_up(const DecParams &P, const LayerW &Lw,
 }
 
 template <bool FLOW, class W>
-__device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item, const Step &st, float *smem,
+__device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, int item, const Step &st, float *smem,
                           W &&wait) {
   const int D = P.D, ng = D >> 5, nq = D >> 2;
   const bool gpt2 = P.arch == 1;
@@ -956,25 +1012,26 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item,
   }
   const int wv = wave_id(), lane = lane_id();
   float4 base = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int want = st.tag + li;  // the attention block of this layer
   if (!FLOW) {
-    base = col_base_load(P.xa, nq);
+    base = col_base_load<false>(P, P.xa, nq, 0);
     ResidReg R0;
-    resid_blocks_load(P.opart, nq, P.NH, 0, R0);
+    resid_blocks_load<false>(P, P.opart, D >> 1, P.NH, 0, 0, R0);
     gains_load(P, Lw.n2, rbias, GR);
     mlp_pre_up(P, Lw, item, M);  // before the down slice (loads retire in issue order)
     if (st.done) return;
-    resid_blocks_rest(P.opart, nq, P.NH, R0, blk);
+    resid_blocks_rest<false>(P, P.opart, D >> 1, P.NH, 0, R0, blk);
     gains_store(P, rbias, GR, gl);
   }
   for (int t = 0; t < m; ++t) {
     float *bt = blk + (t & 1) * nb * D;
     if (FLOW || t > 0) {
-      base = col_base_load(P.xa + (size_t)t * D, nq);
-      resid_blocks(P.opart + (size_t)t * P.NH * D, nq, P.NH, bt);
+      base = col_base_load<FLOW>(P, P.xa + (size_t)t * D, nq, want);
+      resid_blocks<FLOW>(P, P.opart + (size_t)t * P.NH * D, D >> 1, P.NH, want, bt);
     }
     __syncthreads();
     col_norm(P, col_finish(bt, nq, P.NH, base, gl, D, gpt2), gl, red, qx + t * ng * QXR,
-             ColOut{item == 0 ? P.xb + (size_t)t * D : nullptr});
+             ColOut{item == 0 ? P.xb + (size_t)t * D : nullptr, want});
   }
   if (!FLOW) slice_load<MC, MT>(Lw.w2, 2 * item, D, M.Rd);  // needed last: behind everything the prologue reads
   __syncthreads();
@@ -1009,21 +1066,22 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int item,
   }
   __syncthreads();
   for (int t = 0; t < m; ++t)
-    slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * QXR, P.dpart + ((size_t)t * P.nchunk + item) * D);
+    slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * QXR, P.dpart + ((size_t)t * P.nchunk + item) * D, want);
 }
 
 // The last layer's residual and the final norm of token t: QX records (LDS)
 // for the lm_head of the persistent kernel, or xn (coherent stores) for the
 // lm_head kernel.  blk needs nb * D floats; the
 // caller has staged the norm_f gains in gl.
+template <bool POLL>
 __device__ __forceinline__ void final_row(const DecParams &P, int t, float *blk, const float *gl, uint32_t *qx,
-                                          bool to_global) {
+                                          bool to_global, int want) {
   const int D = P.D, nq = D >> 2;
-  const float4 base = col_base_load(P.xb + (size_t)t * D, nq);
-  resid_blocks(P.dpart + (size_t)t * P.nchunk * D, nq, P.nchunk, blk);
+  const float4 base = col_base_load<POLL>(P, P.xb + (size_t)t * D, nq, want);
+  resid_blocks<POLL>(P, P.dpart + (size_t)t * P.nchunk * D, D >> 1, P.nchunk, want, blk);
   __syncthreads();
   const float4 x = col_finish(blk, nq, P.nchunk, base, gl, D, P.arch == 1);
-  col_norm(P, x, gl, blk + ((P.nchunk + PB - 1) / PB) * D, qx, ColOut{nullptr, to_global ? P.xn + (size_t)t * D : nullptr});
+  col_norm(P, x, gl, blk + ((P.nchunk + PB - 1) / PB) * D, qx, ColOut{nullptr, 0, to_global ? P.xn + (size_t)t * D : nullptr});
 }
 
 // Kernel-per-phase mode: item t writes xn[t] (only the rows the
@@ -1039,7 +1097,7 @@ __device__ void phase_final(const DecParams &P, int m, int item, const Step &st,
   GainsReg GR;
   gains_load(P, P.norm_f, rbias, GR);
   gains_store(P, rbias, GR, gl);
-  final_row(P, t, blk, gl, nullptr, true);
+  final_row<false>(P, t, blk, gl, nullptr, true, 0);
 }
 
 // argmaxGpt2 (infer.js:252-287) adjustment of one logit given the banned and
@@ -1279,13 +1337,13 @@ template <int PH, int ONE>
 __global__ __launch_bounds__(phase_threads(PH)) void k_phase(DecParams P, LayerW Lw, int li, int m) {
   extern __shared__ float4 smem4[];
   float *smem = reinterpret_cast<float *>(smem4);
-  const Step st{st_ld(P, ST_OFF(pos0)), st_ld(P, ST_OFF(done)) != 0};
+  const Step st{st_ld(P, ST_OFF(pos0)), st_ld(P, ST_OFF(done)) != 0, st_ld(P, ST_OFF(tag0))};
   const int mm = ONE ? 1 : m;
   const int item = blockIdx.x;
   switch (PH) {
   case PH_QKV: phase_qkv<false>(P, Lw, mm, li, item, st, smem, NoWait{}); break;
   case PH_ATTN: phase_attn<false>(P, Lw, mm, li, item, st, smem, NoWait{}); break;
-  case PH_MLP: phase_mlp<false>(P, Lw, mm, item, st, smem, NoWait{}); break;
+  case PH_MLP: phase_mlp<false>(P, Lw, mm, li, item, st, smem, NoWait{}); break;
   case PH_FINAL: phase_final(P, mm, item, st, smem); break;
   case PH_LM: phase_lm(P, mm, item, gridDim.x, st, smem); break;
   default: phase_argmax<LT>(P, P.lm_tiles, st, smem); break;
@@ -1297,7 +1355,7 @@ template <int AQC>
 __global__ __launch_bounds__(AT) void k_attn1(DecParams P, LayerW Lw, int li, int m) {
   extern __shared__ float4 smem4[];
   float *smem = reinterpret_cast<float *>(smem4);
-  const Step st{st_ld(P, ST_OFF(pos0)), st_ld(P, ST_OFF(done)) != 0};
+  const Step st{st_ld(P, ST_OFF(pos0)), st_ld(P, ST_OFF(done)) != 0, st_ld(P, ST_OFF(tag0))};
   (void)m;
   phase_attn1<false, AQC>(P, Lw, li, blockIdx.x, st, smem, NoWait{});
 }
@@ -1322,17 +1380,21 @@ static const char *const kPhaseNames[PH_COUNT] = {"QKV", "ATTN", "MLP", "FINAL",
 // layer, forms the final norm itself (no separate FINAL step) and computes
 // the tile; the last workgroup to finish its tile takes the argmax.
 //
-// Ordering is by per-item epoch flags instead of kernel boundaries: when an
-// item's outputs are stored (coherent stores, then a wait for their
-// completion) the item's flag is set to the step's epoch; a consumer polls
-// the flags of exactly the items it reads.  Dependencies:
+// Ordering is by tags carried in the data instead of kernel boundaries: an
+// item stores its outputs as (value, tag) pairs, tag = step epoch * TAGL +
+// layer, and a consumer polls exactly the values it reads until they carry
+// the tag it needs (the residual, the per-head or per-chunk partials).
+// Dependencies:
 //   ATTN(l)     <- MLP(l-1), every chunk     (l = 0: the previous step's ARGMAX)
-//   MLP(l)      <- ATTN(l), every head (set by the split that merged the head)
+//   MLP(l)      <- ATTN(l), every head (written by the split that merged the head)
 //   LM          <- MLP(L-1), every chunk;   ARGMAX: the last LM workgroup
-// Every item depends only on items earlier in the order (layer, stage) and
-// every workgroup runs its items in that order, so with all workgroups
-// resident (a cooperative launch) the grid always makes progress.  Flags
-// hold epochs, which grow across launches, so they are never cleared.
+// A buffer is rewritten only by items that depend, through these edges, on
+// every reader of its previous contents.  Every item depends only on items
+// earlier in the order (layer, stage) and every workgroup runs its items in
+// that order, so with all workgroups resident (a cooperative launch) the
+// grid always makes progress.  Epochs and tags grow across launches, so
+// nothing is ever cleared; they are compared modulo 2^32.  The ARGMAX and
+// lm_head counters still use flags (set after a completion wait).
 struct FlowGeom {
   int *flags;             // [L][NH + nm] attention heads and MLP chunks, LM counter, ARGMAX
   int ep0, steps;         // epoch of the launch's first step; chained steps
@@ -1342,6 +1404,14 @@ struct FlowGeom {
 
 constexpr int FLT = 1024;               // threads per workgroup of the persistent kernel
 constexpr unsigned kSpinLimit = 1u << 22;  // polls before a wait gives up (seconds)
+
+__device__ __forceinline__ bool poll_give_up(const DecParams &P, unsigned spins) {
+  if (spins > kSpinLimit) {
+    st_st(P, ST_OFF(err), 1);
+    return true;
+  }
+  return (spins & 255) == 0 && st_ld(P, ST_OFF(err)) != 0;
+}
 
 __device__ __forceinline__ int flag_ld(const int *f) {
   return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1367,9 +1437,9 @@ __device__ void flow_wait(const DecParams &P, const int *f0, int n0, const int *
     bool failed = __builtin_amdgcn_readfirstlane(st_ld(P, ST_OFF(err))) != 0;
     while (!failed) {
       bool ok = true;
-      for (int i = lane; i < n0; i += 64) ok &= flag_ld(f0 + i) >= e;
-      for (int i = lane; i < n1; i += 64) ok &= flag_ld(f1 + i) >= e;
-      for (int i = lane; i < n2; i += 64) ok &= flag_ld(f2 + i) >= e;
+      for (int i = lane; i < n0; i += 64) ok &= tag_ok((uint32_t)flag_ld(f0 + i), e);
+      for (int i = lane; i < n1; i += 64) ok &= tag_ok((uint32_t)flag_ld(f1 + i), e);
+      for (int i = lane; i < n2; i += 64) ok &= tag_ok((uint32_t)flag_ld(f2 + i), e);
       if (__all(ok)) break;
       if (SLEEP) __builtin_amdgcn_s_sleep(SLEEP);
       ++spins;
@@ -1437,7 +1507,7 @@ __device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, co
   if (wait()) return false;
   const bool penal = P.arch == 1 && st_ld(P, ST_OFF(chain)) != 0;
   if (penal && tid() == 0) gpt2_lists(P, s.lists);
-  final_row(P, 0, blk, gl, s.qx, false);
+  final_row<true>(P, 0, blk, gl, s.qx, false, st.tag + P.L - 1);
   __syncthreads();
   const int nban = penal ? s.lists[0] : 0, nrec = penal ? s.lists[1] : 0;
   while (tile < L.ntiles) {
@@ -1467,7 +1537,7 @@ __global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
   for (int step = 0; step < F.steps; ++step) {
     FlowCtl C{P, am_flag, F.ep0 + step, step > 0, false};
     const int e = C.e;
-    const Step st{pos_start + step, false};
+    const Step st{pos_start + step, false, (int)((uint32_t)e * (uint32_t)TAGL)};
     for (int lv = 0; lv < P.L && !C.done; ++lv) {
       // the layer and item indices are made opaque to the compiler: it would
       // otherwise hoist per-thread addresses out of the loops and keep them
@@ -1479,16 +1549,17 @@ __global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
       for (int jv = w; jv < F.ni && !C.done; jv += G) {
         int j = jv;
         asm volatile("" : "+s"(j));
+        // items poll their inputs' tags (the previous layer's residual and
+        // down partials, or this layer's attention partials); the waits
+        // below only take the step's ARGMAX and `done`
         if (j < F.na) {
-          const int h = j % P.NH;
-          const int *dep = fl - stride + P.NH;  // MLP chunks of the previous layer
-          const int ndep = li > 0 ? F.nm : 0;
-          const bool merged = phase_attn1<true, AQC>(P, Lw, li, j, st, smem, [&] { return C.wait(dep, ndep); });
-          if (merged && !C.done) flow_publish(fl + h, e);
+          phase_attn1<true, AQC>(P, Lw, li, j, st, smem, [&] { return C.wait(nullptr, 0); });
         } else {
           const int it = j - F.na;
-          phase_mlp<true>(P, Lw, 1, it, st, smem, [&] { return C.wait(fl, P.NH); });
-          if (!C.done) flow_publish(fl + P.NH + it, e);
+          phase_mlp<true>(P, Lw, 1, li, it, st, smem, [&] { return C.wait(nullptr, 0); });
+          // a hint for the lm_head's coarse waits, set without waiting for the
+          // stores: the data itself carries the tags that decide
+          if (!C.done && tid() == 0) flag_st(fl + P.NH + it, e);
         }
       }
     }
@@ -1658,6 +1729,9 @@ int get_f32(mllm_model *M, const std::string &n, size_t count, const float **out
 }
 
 int upload_state(mllm_model *M) {
+  // kernel-per-phase passes tag their handoff values below every tag a later
+  // persistent launch waits for (its epochs start at flow_epoch + 1)
+  M->h_st->tag0 = (int)((uint32_t)M->flow_epoch * (uint32_t)TAGL);
   MLLM_HIP(hipMemcpyAsync(M->d_st, M->h_st, sizeof(PassState), hipMemcpyHostToDevice, M->stream));
   return 0;
 }
@@ -1840,6 +1914,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
                  c.vocab_size > 0 && c.max_seq_len > 0,
              "invalid config");
   MLLM_CHECK(c.d_model % c.n_heads == 0 && c.n_heads % c.n_kv_heads == 0, "heads do not divide");
+  if (c.n_layers >= TAGL) return set_error(MLLM_ERR_UNSUPPORTED, "%d layers (at most %d)", c.n_layers, TAGL - 1);
   // coherent loads and stores address the KV cache with 32-bit byte offsets
   MLLM_CHECK((uint64_t)c.n_layers * 2 * c.n_kv_heads * c.max_seq_len * HD * (c.kv_fp16 ? 2 : 4) < (1ull << 31),
              "KV cache of %d layers x %d positions exceeds 2 GiB", c.n_layers, c.max_seq_len);
@@ -1978,10 +2053,12 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
 
   // activations, KV cache, scratch
   const size_t kv_elems = (size_t)L * 2 * NKV * c.max_seq_len * HD;
-  int rc = dev_alloc(M, (void **)&P.xa, sizeof(float) * MAXT * D);
-  if (!rc) rc = dev_alloc(M, (void **)&P.xb, sizeof(float) * MAXT * D);
-  if (!rc) rc = dev_alloc(M, (void **)&P.opart, sizeof(float) * MAXT * NH * D);
-  if (!rc) rc = dev_alloc(M, (void **)&P.dpart, sizeof(float) * MAXT * P.nchunk * D);
+  const size_t tagged_bytes[4] = {sizeof(uint2) * MAXT * D, sizeof(uint2) * MAXT * D, sizeof(uint2) * MAXT * NH * D,
+                                   sizeof(uint2) * MAXT * P.nchunk * D};
+  int rc = dev_alloc(M, (void **)&P.xa, tagged_bytes[0]);
+  if (!rc) rc = dev_alloc(M, (void **)&P.xb, tagged_bytes[1]);
+  if (!rc) rc = dev_alloc(M, (void **)&P.opart, tagged_bytes[2]);
+  if (!rc) rc = dev_alloc(M, (void **)&P.dpart, tagged_bytes[3]);
   if (!rc) rc = dev_alloc(M, (void **)&P.xn, sizeof(float) * MAXT * D);
   if (!rc) rc = dev_alloc(M, (void **)&P.q, sizeof(float) * MAXT * NH * HD);
   if (!rc) rc = dev_alloc(M, &P.kv, kv_elems * (c.kv_fp16 ? 2 : 4));
@@ -1998,6 +2075,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   if (hipHostMalloc((void **)&M->h_st, sizeof(PassState), hipHostMallocDefault) != hipSuccess)
     return fail(set_error(MLLM_ERR_HIP, "pinned state"));
   if (hipMemset(M->d_st, 0, sizeof(PassState)) != hipSuccess ||
+      hipMemset(P.xa, 0, tagged_bytes[0]) != hipSuccess || hipMemset(P.xb, 0, tagged_bytes[1]) != hipSuccess ||
+      hipMemset(P.opart, 0, tagged_bytes[2]) != hipSuccess || hipMemset(P.dpart, 0, tagged_bytes[3]) != hipSuccess ||
       hipMemset(P.cnt, 0, sizeof(unsigned) * MAXT * NH) != hipSuccess ||
       hipMemset(P.kv, 0, kv_elems * (c.kv_fp16 ? 2 : 4)) != hipSuccess)
     return fail(set_error(MLLM_ERR_HIP, "memset"));
