@@ -87,7 +87,15 @@ constexpr int QC = 2;      // chunk registers per thread of a QKV item: one head
 // Chunk registers per thread of the fused q/k/v tile of a decode attention
 // item (3 x 64 rows x d_model/32 chunks over 1024 threads): 4 up to d_model
 // 672, 5 up to 832, 6 up to 1024.  The kernels are instantiated for each.
-constexpr int aqc_for(int ng) { return (3 * HD * ng + 1023) / 1024 <= 4 ? 4 : (3 * HD * ng + 1023) / 1024; }
+// (chunk c of the tile is taken by thread c % S, S = ng * (1024 / ng) the
+// largest multiple of ng that fits the workgroup, so all of a thread's
+// chunks are of one group)
+constexpr int fixed_stride(int ng) { return (1024 / ng) * ng; }
+constexpr int aqc_for(int ng) {
+  return (3 * HD * ng + fixed_stride(ng) - 1) / fixed_stride(ng) <= 4
+             ? 4
+             : (3 * HD * ng + fixed_stride(ng) - 1) / fixed_stride(ng);
+}
 constexpr int FTC = 4;     // chunk registers per thread of a persistent-kernel lm_head tile (FTC * 1024 chunks)
 constexpr int PB = 8;      // partials per block of the fixed-order partial sums
 constexpr int NBMAX = 8;   // blocks per partial sum (<= PB * NBMAX partials: heads, 64-unit chunks)
@@ -422,6 +430,24 @@ __device__ __forceinline__ void tile_partials(const TileRegs<C> &R, int ng, int 
   }
 }
 
+// The same partials for one token, chunk c taken by thread c % S (S =
+// fixed_stride(ng), chunks loaded by tile_load3): every chunk of a thread is
+// of group tid % ng, so its activation record is read from LDS once.  The
+// partials have the arithmetic of tile_partials (q4_qx_part_reg).
+template <int C>
+__device__ __forceinline__ void tile_partials_fixed(const TileRegs<C> &R, int ng, int nch, const uint32_t *qx,
+                                                    float *part) {
+  const int S = fixed_stride(ng);
+  if ((int)tid() < S) {
+    const QxRec xr = qx_load(qx + (tid() % ng) * QXR);
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const int c = tid() + j * S;
+      if (c < nch) part[c] = q4_qx_part_reg(R.w[j], xr, R.s[j]);
+    }
+  }
+}
+
 // A two-group column slice of a matrix with ng groups per row: chunk
 // c = 2r + j (r < rows, j < 2) is row r, group g0 + j.
 template <int C, int NT>
@@ -458,10 +484,10 @@ __device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const
 // last chunk (unused).
 template <int C>
 __device__ __forceinline__ void tile_load3(const Q4Mat &W, int r0, int r1, int r2, int ng, TileRegs<C> &R) {
-  const int per = HD * ng, nch = 3 * per;
+  const int per = HD * ng, nch = 3 * per, S = fixed_stride(ng);
 #pragma unroll
   for (int j = 0; j < C; ++j) {
-    const int c = min(tid() + j * 1024, nch - 1);
+    const int c = min(min((int)tid(), S - 1) + j * S, nch - 1);
     const int k = c / per, cc = c - k * per;
     // arithmetic, not a select chain (which the compiler turns into a table
     // in scratch memory)
@@ -936,7 +962,7 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   const float4 x = li == 0 ? base : col_finish(blk, nq, P.nchunk, base, gl, D, rbias != nullptr);
   col_norm(P, x, gl, red, qx, ColOut{item == 0 ? P.xa : nullptr, st.tag + li});
   __syncthreads();
-  tile_partials<AQC>(Wt, ng, nch, 1, qx, part);
+  tile_partials_fixed<AQC>(Wt, ng, nch, qx, part);
   __builtin_amdgcn_sched_barrier(0);
   attn_v_load(P, li, kvh, s0, last ? cnt - 1 : cnt, vr);
   __builtin_amdgcn_sched_barrier(0);
@@ -2039,7 +2065,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   // buffer of phase_lm.
   P.lm_grid = (P.lm_tiles + MLLM_LM_TILES_PER_WG - 1) / MLLM_LM_TILES_PER_WG;
   M->aq_idx = aqc_for(ngd) - 4;
-  if (HD * ngd > QC * QT || UNITS * ngd > MC * ((MT / ngd) * ngd) || 2 * D > MC * MT || 2 * D > SC * AT ||
+  if (aqc_for(ngd) > 6 || HD * ngd > QC * QT || UNITS * ngd > MC * ((MT / ngd) * ngd) || 2 * D > MC * MT || 2 * D > SC * AT ||
       16 * ngd > TC * LT)
     return fail(set_error(MLLM_ERR_UNSUPPORTED, "tiles exceed the chunk registers (d_model %d)", D));
 
