@@ -410,6 +410,12 @@ __device__ __forceinline__ int sum8i(int v) {
   v = v + dpp_i<0x4E>(v);
   return v + dpp_i<0x141>(v);
 }
+// Sum over the 8 lanes of each half-row, the same bits in all 8 lanes.
+__device__ __forceinline__ float sum8f(float v) {
+  v = v + dpp_f<0xB1>(v);
+  v = v + dpp_f<0x4E>(v);
+  return v + dpp_f<0x141>(v);
+}
 __device__ __forceinline__ float qx_inv(float amax) { return amax > 0.f ? 32767.0f / amax : 0.f; }
 __device__ __forceinline__ int qx_round(float v, float inv) { return (int)__builtin_rintf(v * inv); }
 

@@ -1026,6 +1026,7 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
   uint32_t *hq = reinterpret_cast<uint32_t *>(part + 4 * nch);   // m x 2 QX records of h
   float *blk = reinterpret_cast<float *>(hq + m * 2 * QXR);     // 2 x nb * D, then red
   float *red = blk + 2 * nb * D;
+  float *rsum = red + 32;  // 2 x (gate || up) row sums, by token parity
   const float *rbias = gpt2 ? Lw.proj_b : nullptr;
   MlpPre M;
   GainsReg GR;
@@ -1062,11 +1063,13 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
   if (!FLOW) slice_load<MC, MT>(Lw.w2, 2 * item, D, M.Rd);  // needed last: behind everything the prologue reads
   __syncthreads();
   const int g = tid() % ng;
+  static_assert(2 * UNITS * 8 == MT, "one 8-lane row sum per gate and up row");
   for (int t = 0; t < m; ++t) {
-    // gate and up chunk partials of token t (the arithmetic of
-    // tile_compute), one barrier, then the token's wave (unit r = lane)
-    // forms the rows, the activation and the two group sums of h
+    // gate and up chunk partials of token t, then the row sums on every
+    // wave (8 lanes per row), then the token's wave (unit r = lane) forms
+    // the activation and the two group records of h
     float *pt = part + (t & 1) * 2 * nch;
+    float *rt = rsum + (t & 1) * 2 * UNITS;
     const QxRec xr = qx_load(qx + (t * ng + g) * QXR);
 #pragma unroll
     for (int k = 0; k < MC; ++k) {
@@ -1077,15 +1080,28 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
       }
     }
     __syncthreads();
+    {
+      // row r (gate rows, then up rows): lane s adds partials s, s + 8, ...
+      // in order, then a fixed 8-lane tree
+      const int r = tid() >> 3, s = tid() & 7;
+      const int nrows = gpt2 ? UNITS : 2 * UNITS;
+      const float *pr = pt + (r < UNITS ? 0 : nch) + (r & (UNITS - 1)) * ng;
+      float a = 0.f;
+      if (r < nrows)
+        for (int k = s; k < ng; k += 8) a = a + pr[k];
+      a = sum8f(a);
+      if (s == 0 && r < nrows) rt[r] = a;
+    }
+    __syncthreads();
     if (wv == (t & (NWV - 1))) {
       const int r = lane;
-      const float gv = row_sum(pt + r * ng, ng);
+      const float gv = rt[r];
       float h;
       if (gpt2) {
         const float v = gv + M.fcb;
         h = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
       } else {
-        h = (gv / (1.0f + expf(-gv))) * row_sum(pt + nch + r * ng, ng);
+        h = (gv / (1.0f + expf(-gv))) * rt[UNITS + r];
       }
       qx_stage_lanes(h, hq + t * 2 * QXR);
     }
@@ -1692,7 +1708,7 @@ size_t lds_floats(const DecParams &P, int ph, int m) {
     if (m == 1) return al4(3 * D) + ngd * QXR + 3 * HD * ngd + nbd * D + 32 + 2 * HD + ATT_LDS;
     return ATT_LDS;
   case PH_MLP:
-    return al4(3 * D) + m * ngd * QXR + 4 * UNITS * ngd + (size_t)m * 2 * QXR + 2 * nbo * D + 32;
+    return al4(3 * D) + m * ngd * QXR + 4 * UNITS * ngd + (size_t)m * 2 * QXR + 2 * nbo * D + 32 + 4 * UNITS;
   case PH_FINAL: return al4(3 * D) + nbd * D + 32;
   case PH_LM: return m * ngd * QXR + (size_t)m * TC * LT + (size_t)m * P.lm_rpt + 34 + P.max_seq;
   default: return 2 * (LT / 64);
