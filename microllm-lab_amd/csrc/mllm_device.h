@@ -410,6 +410,16 @@ __device__ __forceinline__ int sum8i(int v) {
   v = v + dpp_i<0x4E>(v);
   return v + dpp_i<0x141>(v);
 }
+// The sum of a row's ng partials p[0 .. ng) on 4 lanes (s = lane & 3):
+// lane s adds partials s, s + 4, ... in order (from +0), then a fixed 4-lane
+// tree; the same bits in all 4 lanes.  Called with the whole quad active.
+__device__ __forceinline__ float row_sum4(const float *p, int ng, int s) {
+  float a = 0.f;
+  for (int k = s; k < ng; k += 4) a = a + p[k];
+  a = a + dpp_f<0xB1>(a);
+  return a + dpp_f<0x4E>(a);
+}
+
 // Sum over the 8 lanes of each half-row, the same bits in all 8 lanes.
 __device__ __forceinline__ float sum8f(float v) {
   v = v + dpp_f<0xB1>(v);

@@ -603,10 +603,19 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
   __syncthreads();
   tile_partials<QC>(Q.R, ng, nch, m, qx, part);
   __syncthreads();
+  // the m x 64 row sums, four lanes each (the decode attention item's order)
+  float *rs = red + 32;
+  for (int base = 0; base < m * HD; base += 256) {
+    const int r = base + (int)(tid() >> 2);
+    const int rr = min(r, m * HD - 1), tr = rr / HD;
+    const float a = row_sum4(part + tr * nch + (rr - tr * HD) * ng, ng, tid() & 3);
+    if ((tid() & 3) == 0 && r < m * HD) rs[r] = a;
+  }
+  __syncthreads();
   // epilogue on the token's wave: lane d is head dimension d
   for (int t = wv; t < m; t += NWV) {
     const int d = lane;
-    float v = row_sum(part + t * nch + d * ng, ng);
+    float v = rs[t * HD + d];
     const int pos = pos0 + t;
     const bool is_q = head < P.NH, is_k = !is_q && head < P.NH + P.NKV;
     if (gpt2) {
@@ -916,7 +925,8 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   float *gl = smem, *part = gl + al4(3 * D) + ng * QXR;
   uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // ng QX records
   float *blk = part + nch, *red = blk + nb * D, *kvn = red + 32;  // kvn: the new K row (64) then V row (64)
-  const AttnLds A = attn_lds(kvn + 2 * HD);
+  float *rs = kvn + 2 * HD;  // 3 x 64 row sums: q, k, v
+  const AttnLds A = attn_lds(rs + 3 * HD);
   const int wv = wave_id(), lane = lane_id();
   // rows of the fused tile: [q head h | K head kvh | V head kvh], 64 each
   const int rq = h * HD, rk = (P.NH + kvh) * HD, rv = (P.NH + P.NKV + kvh) * HD;
@@ -967,9 +977,16 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   attn_v_load(P, li, kvh, s0, last ? cnt - 1 : cnt, vr);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
+  {
+    // the 192 row sums, four lanes each
+    const int r = tid() >> 2;
+    const float a = row_sum4(part + min(r, 3 * HD - 1) * ng, ng, tid() & 3);
+    if ((tid() & 3) == 0 && r < 3 * HD) rs[r] = a;
+  }
+  __syncthreads();
   // rows: wave 0 the query, wave 1 the key, wave 2 the value (lane d)
   if (wv < 3) {
-    float v = row_sum(part + (wv * HD + lane) * ng, ng);
+    float v = rs[wv * HD + lane];
     if (gpt2) {
       v = v + c_own;  // the bias
     } else if (wv < 2) {
@@ -1703,9 +1720,9 @@ size_t lds_floats(const DecParams &P, int ph, int m) {
   const size_t ngd = P.D / 32, D = P.D;
   const size_t nbo = (P.NH + PB - 1) / PB, nbd = (P.nchunk + PB - 1) / PB;
   switch (ph) {
-  case PH_QKV: return al4(3 * D) + m * ngd * QXR + (size_t)m * HD * ngd + 2 * nbd * D + 32;
+  case PH_QKV: return al4(3 * D) + m * ngd * QXR + (size_t)m * HD * ngd + 2 * nbd * D + 32 + (size_t)m * HD;
   case PH_ATTN:
-    if (m == 1) return al4(3 * D) + ngd * QXR + 3 * HD * ngd + nbd * D + 32 + 2 * HD + ATT_LDS;
+    if (m == 1) return al4(3 * D) + ngd * QXR + 3 * HD * ngd + nbd * D + 32 + 2 * HD + 3 * HD + ATT_LDS;
     return ATT_LDS;
   case PH_MLP:
     return al4(3 * D) + m * ngd * QXR + 4 * UNITS * ngd + (size_t)m * 2 * QXR + 2 * nbo * D + 32 + 4 * UNITS;
