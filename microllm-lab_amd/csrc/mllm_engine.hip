@@ -134,8 +134,8 @@ struct DecParams {
   const float *last_mproj_b;  // gpt2: mlp.proj bias of the last layer
   uint2 *xa;      // [MAXT][D] tagged residual entering the attention block
   uint2 *xb;      // [MAXT][D] tagged residual entering the MLP block
-  uint2 *opart;   // [MAXT][NH][D] tagged per-head partials of W_o . att
-  uint2 *dpart;   // [MAXT][nchunk][D] tagged per-chunk partials of W_2 . h
+  uint4 *opart;   // [MAXT][NH][nquads(D)] per-head partials of W_o . att, tagged quads
+  uint4 *dpart;   // [MAXT][nchunk][nquads(D)] per-chunk partials of W_2 . h, tagged quads
   float *xn;      // [MAXT][D] final-normed rows for the lm_head
   float *q;       // [MAXT][NH*HD] queries after RoPE
   void *kv;       // [L][2][NKV][max_seq][HD] (f32 or f16)
@@ -156,6 +156,11 @@ struct Step {
   int tag;    // tag of layer 0's handoff values; layer li writes tag + li
 };
 constexpr int TAGL = 128;  // tags per step (layers < TAGL)
+// A tagged quad holds three consecutive values of a partial row and their
+// tag, (v0, v1, v2, tag): one 16-byte store by one lane, read by 16-byte loads
+// (a lane's aligned 16 bytes travel as one request to one cache line).  A
+// row of D values is nquads(D) quads; values past D are 0.
+__host__ __device__ constexpr int nquads(int D) { return (D + 2) / 3; }
 
 // The pass state is read and written with coherent access: inside the
 // persistent kernel ARGMAX updates it for workgroups on other XCDs.
@@ -221,14 +226,13 @@ __device__ __forceinline__ void gains_store(const DecParams &P, const float *bia
 //   x = base + (((B_0 + B_1) + ... + B_{nb-1}) + bias)
 // where B_b sums parts[p] for p in [b*PB, min(np, (b+1)*PB)) in ascending p
 // (from +0).  The order of every addition is fixed by np alone.
-// The partials are tagged (value, tag) pairs; a 16-byte load carries two
-// neighbouring columns.  The block sums use every thread of a 1024-thread
-// workgroup: item it = b * nq2 + c (nq2 = D / 2 column pairs, round
-// it / 1024) forms B_b of columns 2c, 2c+1 into blk[b*D + 2c ..] (LDS).  A
-// round's loads all go out before its first add, so a round costs one
-// memory latency; round 0 can be loaded ahead (resid_blocks_load) so its
+// The partials are rows of tagged quads (nq3 = nquads(D) per row).  The
+// block sums use every thread of a 1024-thread workgroup: item it = b * nq3
+// + c (round it / 1024) forms B_b of values 3c .. 3c+2 into blk[b*D + 3c ..]
+// (LDS).  A round's loads all go out before its first add, so a round costs
+// one memory latency; round 0 can be loaded ahead (resid_blocks_load) so its
 // latency overlaps the weight loads.  With POLL (persistent kernel) a round
-// is loaded again until every pair carries a tag of at least `want`.
+// is loaded again until every quad carries a tag of at least `want`.
 // Branch-free: an item or partial past the end reads partial 0 of column 0
 // (valid memory) and is left out.
 struct ResidReg {
@@ -240,32 +244,29 @@ struct ResidReg {
 __device__ __forceinline__ bool poll_give_up(const DecParams &P, unsigned spins);
 
 template <bool POLL>
-__device__ __forceinline__ void resid_blocks_load(const DecParams &P, const uint2 *pt, int nq2, int np, int round,
+__device__ __forceinline__ void resid_blocks_load(const DecParams &P, const uint4 *pt, int nq3, int np, int round,
                                                   int want, ResidReg &R) {
-  const int nitems = nq2 * ((np + PB - 1) / PB);
+  const int nitems = nq3 * ((np + PB - 1) / PB);
   const int it = tid() + round * 1024;
-  const int b = it / nq2, c = it - b * nq2;
+  const int b = it / nq3, c = it - b * nq3;
 #pragma unroll
   for (int k = 0; k < PB; ++k) {
     const int p = b * PB + k;
     const bool ok = it < nitems && p < np;
-    R.v[k] = coh_ld16(pt, 16u * (ok ? (uint32_t)(p * nq2 + c) : 0u));
+    R.v[k] = coh_ld16(pt, 16u * (ok ? (uint32_t)(p * nq3 + c) : 0u));
   }
   if (POLL) {
     for (unsigned spins = 1;; ++spins) {
       bool ready = true;
 #pragma unroll
-      for (int k = 0; k < PB; ++k) {
-        const bool ok = it < nitems && b * PB + k < np;
-        ready &= !ok || (tag_ok(R.v[k].y, want) && tag_ok(R.v[k].w, want));
-      }
+      for (int k = 0; k < PB; ++k) ready &= !(it < nitems && b * PB + k < np) || tag_ok(R.v[k].w, want);
       if (ready || poll_give_up(P, spins)) break;
       poll_fence();
 #pragma unroll
       for (int k = 0; k < PB; ++k) {
         const int p = b * PB + k;
         const bool ok = it < nitems && p < np;
-        R.v[k] = coh_ld16(pt, 16u * (ok ? (uint32_t)(p * nq2 + c) : 0u));
+        R.v[k] = coh_ld16(pt, 16u * (ok ? (uint32_t)(p * nq3 + c) : 0u));
       }
     }
   }
@@ -275,40 +276,46 @@ __device__ __forceinline__ void resid_blocks_load(const DecParams &P, const uint
 // conditional): a load consumed inside a divergent branch leaves the
 // compiler unsure it has completed, and it then waits for every load in
 // flight before the register is reused.
-__device__ __forceinline__ void resid_blocks_add(int nq2, int np, int round, const ResidReg &R, float *blk) {
-  const int nitems = nq2 * ((np + PB - 1) / PB);
+__device__ __forceinline__ void resid_blocks_add(int D, int nq3, int np, int round, const ResidReg &R, float *blk) {
+  const int nitems = nq3 * ((np + PB - 1) / PB);
   const int it = tid() + round * 1024;
-  const int b = it / nq2;
-  float2 a = make_float2(0.f, 0.f);
+  const int b = it / nq3, c = it - b * nq3;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f;
 #pragma unroll
   for (int k = 0; k < PB; ++k) {
     const uint4 w = R.v[k];
     const bool use = b * PB + k < np;
-    a.x = a.x + (use ? __uint_as_float(w.x) : 0.f);
-    a.y = a.y + (use ? __uint_as_float(w.z) : 0.f);
+    a0 = a0 + (use ? __uint_as_float(w.x) : 0.f);
+    a1 = a1 + (use ? __uint_as_float(w.y) : 0.f);
+    a2 = a2 + (use ? __uint_as_float(w.z) : 0.f);
   }
-  if (it < nitems) reinterpret_cast<float2 *>(blk)[it] = a;
+  if (it < nitems) {
+    float *o = blk + b * D + 3 * c;
+    o[0] = a0;
+    if (3 * c + 1 < D) o[1] = a1;
+    if (3 * c + 2 < D) o[2] = a2;
+  }
 }
 
 // Every round of the block sums, round 0 already loaded into R0.
 template <bool POLL>
-__device__ __forceinline__ void resid_blocks_rest(const DecParams &P, const uint2 *pt, int nq2, int np, int want,
+__device__ __forceinline__ void resid_blocks_rest(const DecParams &P, const uint4 *pt, int np, int want,
                                                   const ResidReg &R0, float *blk) {
-  resid_blocks_add(nq2, np, 0, R0, blk);
-  const int nitems = nq2 * ((np + PB - 1) / PB);
+  const int D = P.D, nq3 = nquads(D);
+  resid_blocks_add(D, nq3, np, 0, R0, blk);
+  const int nitems = nq3 * ((np + PB - 1) / PB);
   for (int round = 1; round * 1024 < nitems; ++round) {
     ResidReg R1;
-    resid_blocks_load<POLL>(P, pt, nq2, np, round, want, R1);
-    resid_blocks_add(nq2, np, round, R1, blk);
+    resid_blocks_load<POLL>(P, pt, nq3, np, round, want, R1);
+    resid_blocks_add(D, nq3, np, round, R1, blk);
   }
 }
 
 template <bool POLL>
-__device__ __forceinline__ void resid_blocks(const DecParams &P, const uint2 *pt, int nq2, int np, int want,
-                                             float *blk) {
+__device__ __forceinline__ void resid_blocks(const DecParams &P, const uint4 *pt, int np, int want, float *blk) {
   ResidReg R0;
-  resid_blocks_load<POLL>(P, pt, nq2, np, 0, want, R0);
-  resid_blocks_rest<POLL>(P, pt, nq2, np, want, R0, blk);
+  resid_blocks_load<POLL>(P, pt, nquads(P.D), np, 0, want, R0);
+  resid_blocks_rest<POLL>(P, pt, np, want, R0, blk);
 }
 
 // One token's residual and norm, one float4 column q < nq per thread
@@ -450,32 +457,45 @@ __device__ __forceinline__ void tile_partials_fixed(const TileRegs<C> &R, int ng
 
 // A two-group column slice of a matrix with ng groups per row: chunk
 // c = 2r + j (r < rows, j < 2) is row r, group g0 + j.
+// A slice is two groups (64 columns, groups g0 and g0 + 1) of every row of
+// W.  Wave-slot ws = wave + (NT / 64) k (register k) takes rows
+// [RPW ws, RPW ws + RPW): lane L < 2 RPW holds the chunk of row RPW ws + L / 2,
+// group g0 + (L & 1).  RPW is a multiple of 3, so a wave-slot's rows make
+// whole tagged quads.
+constexpr int RPW = 30;
 template <int C, int NT>
 __device__ __forceinline__ void slice_load(const Q4Mat &W, int g0, int rows, TileRegs<C> &R) {
   const int ng = W.cols >> 5;
+  const int L = lane_id(), wv = wave_id();
 #pragma unroll
   for (int k = 0; k < C; ++k) {
-    const int c = min((int)tid() + k * NT, 2 * rows - 1);  // branch-free; extra lanes unused
-    const size_t gc = (size_t)(c >> 1) * ng + g0 + (c & 1);
+    const int ws = wv + k * (NT / 64);
+    const int r = min(RPW * ws + (min(L, 2 * RPW - 1) >> 1), rows - 1);  // branch-free; extra lanes unused
+    const size_t gc = (size_t)r * ng + g0 + (L & 1);
     R.w[k] = W.q[gc];
     R.s[k] = W.s[gc];
   }
 }
 
 // The slice against two staged groups (QX records v, v + QXR):
-// out[r] = part(group g0) + part(group g0 + 1), the row_sum order of two
-// groups (coherent stores).  Neighbouring lanes hold the pair; every lane
-// takes part in the shuffle.
+// row r = part(group g0) + part(group g0 + 1), the row_sum order of two
+// groups, stored as tagged quads (coherent 16-byte stores): lane 6Q of a
+// wave-slot stores the rows of lanes 6Q, 6Q + 2, 6Q + 4.  Every lane takes
+// part in the shuffles.
 template <int C, int NT>
-__device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const uint32_t *v, uint2 *out, int tag) {
+__device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const uint32_t *v, uint4 *out, int tag) {
+  const int L = lane_id(), wv = wave_id();
 #pragma unroll
   for (int k = 0; k < C; ++k) {
-    const int c = tid() + k * NT;
-    const int j = c & 1;
+    const int ws = wv + k * (NT / 64);
+    const int r = RPW * ws + (L >> 1);
     float p = 0.f;
-    if (c < 2 * rows) p = q4_qx_part(R.w[k], v + j * QXR, R.s[k]);
-    const float sum = p + lane_xor1(p);
-    if (c < 2 * rows && j == 0) coh_st8(out, 8u * (c >> 1), tagged(sum, tag));
+    if (L < 2 * RPW && r < rows) p = q4_qx_part(R.w[k], v + (L & 1) * QXR, R.s[k]);
+    const float sum = p + lane_xor1(p);  // rows past the end are 0
+    const float s1 = __shfl(sum, min(L + 2, 63)), s2 = __shfl(sum, min(L + 4, 63));
+    if (L % 6 == 0 && L < 2 * RPW && r < rows)
+      coh_st16(out, 16u * (uint32_t)((RPW / 3) * ws + L / 6),
+               make_uint4(__float_as_uint(sum), __float_as_uint(s1), __float_as_uint(s2), (uint32_t)tag));
   }
 }
 
@@ -578,12 +598,12 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
     // before the weight tile, so the prologue never waits for the weights
     if (li > 0) {
       base = col_base_load<false>(P, P.xb, nq, 0);
-      resid_blocks_load<false>(P, P.dpart, D >> 1, P.nchunk, 0, 0, R0);
+      resid_blocks_load<false>(P, P.dpart, nquads(D), P.nchunk, 0, 0, R0);
     }
     gains_load(P, Lw.n1, rbias, GR);
     qkv_pre(P, Lw, head, pos0, Q);
     if (st.done) return;  // a chained decode that reached eos: loads only, no stores
-    if (li > 0) resid_blocks_rest<false>(P, P.dpart, D >> 1, P.nchunk, 0, R0, blk);
+    if (li > 0) resid_blocks_rest<false>(P, P.dpart, P.nchunk, 0, R0, blk);
     gains_store(P, rbias, GR, gl);
   }
   // stage every token: x, the norm, its QX records
@@ -594,7 +614,7 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
       base = embed_col(P, tok, min(pos0 + t, P.max_seq - 1));
     } else if (FLOW || t > 0) {
       base = col_base_load<FLOW>(P, P.xb + (size_t)t * D, nq, st.tag + li - 1);
-      resid_blocks<FLOW>(P, P.dpart + (size_t)t * P.nchunk * D, D >> 1, P.nchunk, st.tag + li - 1, bt);
+      resid_blocks<FLOW>(P, P.dpart + (size_t)t * P.nchunk * nquads(D), P.nchunk, st.tag + li - 1, bt);
     }
     __syncthreads();
     const float4 x = li == 0 ? base : col_finish(bt, nq, P.nchunk, base, gl, D, rbias != nullptr);
@@ -844,7 +864,7 @@ __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, i
   // output becomes visible, so whoever sees the output also sees them
   wait_stores();
   __syncthreads();
-  slice_gemv<C, AT>(Ro, D, A.attq, P.opart + (size_t)(t * P.NH + h) * D, tag);
+  slice_gemv<C, AT>(Ro, D, A.attq, P.opart + (size_t)(t * P.NH + h) * nquads(D), tag);
   return true;
 }
 
@@ -949,16 +969,16 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
     if (wait()) return false;
     if (li > 0) {
       base = col_base_load<true>(P, P.xb, nq, st.tag + li - 1);
-      resid_blocks<true>(P, P.dpart, D >> 1, P.nchunk, st.tag + li - 1, blk);
+      resid_blocks<true>(P, P.dpart, P.nchunk, st.tag + li - 1, blk);
     }
   } else {
     // activations first, then the weights (loads retire in issue order)
     if (li > 0) {
       base = col_base_load<false>(P, P.xb, nq, 0);
-      resid_blocks_load<false>(P, P.dpart, D >> 1, P.nchunk, 0, 0, R0);
+      resid_blocks_load<false>(P, P.dpart, nquads(D), P.nchunk, 0, 0, R0);
     }
     attn1_pre(P, Lw, rq, rk, rv, h, pos, row_own, rbias, Wt, Ro, c_own, s_own, GR);
-    if (li > 0) resid_blocks_rest<false>(P, P.dpart, D >> 1, P.nchunk, 0, R0, blk);
+    if (li > 0) resid_blocks_rest<false>(P, P.dpart, P.nchunk, 0, R0, blk);
     gains_store(P, rbias, GR, gl);
   }
   // stage boundaries are fixed (sched_barrier) so that the tile, the K rows
@@ -1060,18 +1080,18 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
   if (!FLOW) {
     base = col_base_load<false>(P, P.xa, nq, 0);
     ResidReg R0;
-    resid_blocks_load<false>(P, P.opart, D >> 1, P.NH, 0, 0, R0);
+    resid_blocks_load<false>(P, P.opart, nquads(D), P.NH, 0, 0, R0);
     gains_load(P, Lw.n2, rbias, GR);
     mlp_pre_up(P, Lw, item, M);  // before the down slice (loads retire in issue order)
     if (st.done) return;
-    resid_blocks_rest<false>(P, P.opart, D >> 1, P.NH, 0, R0, blk);
+    resid_blocks_rest<false>(P, P.opart, P.NH, 0, R0, blk);
     gains_store(P, rbias, GR, gl);
   }
   for (int t = 0; t < m; ++t) {
     float *bt = blk + (t & 1) * nb * D;
     if (FLOW || t > 0) {
       base = col_base_load<FLOW>(P, P.xa + (size_t)t * D, nq, want);
-      resid_blocks<FLOW>(P, P.opart + (size_t)t * P.NH * D, D >> 1, P.NH, want, bt);
+      resid_blocks<FLOW>(P, P.opart + (size_t)t * P.NH * nquads(D), P.NH, want, bt);
     }
     __syncthreads();
     col_norm(P, col_finish(bt, nq, P.NH, base, gl, D, gpt2), gl, red, qx + t * ng * QXR,
@@ -1125,7 +1145,7 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
   }
   __syncthreads();
   for (int t = 0; t < m; ++t)
-    slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * QXR, P.dpart + ((size_t)t * P.nchunk + item) * D, want);
+    slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * QXR, P.dpart + ((size_t)t * P.nchunk + item) * nquads(D), want);
 }
 
 // The last layer's residual and the final norm of token t: QX records (LDS)
@@ -1137,7 +1157,7 @@ __device__ __forceinline__ void final_row(const DecParams &P, int t, float *blk,
                                           bool to_global, int want) {
   const int D = P.D, nq = D >> 2;
   const float4 base = col_base_load<POLL>(P, P.xb + (size_t)t * D, nq, want);
-  resid_blocks<POLL>(P, P.dpart + (size_t)t * P.nchunk * D, D >> 1, P.nchunk, want, blk);
+  resid_blocks<POLL>(P, P.dpart + (size_t)t * P.nchunk * nquads(D), P.nchunk, want, blk);
   __syncthreads();
   const float4 x = col_finish(blk, nq, P.nchunk, base, gl, D, P.arch == 1);
   col_norm(P, x, gl, blk + ((P.nchunk + PB - 1) / PB) * D, qx, ColOut{nullptr, 0, to_global ? P.xn + (size_t)t * D : nullptr});
@@ -2098,7 +2118,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   // buffer of phase_lm.
   P.lm_grid = (P.lm_tiles + MLLM_LM_TILES_PER_WG - 1) / MLLM_LM_TILES_PER_WG;
   M->aq_idx = aqc_for(ngd) - 4;
-  if (aqc_for(ngd) > 6 || HD * ngd > QC * QT || UNITS * ngd > MC * ((MT / ngd) * ngd) || 2 * D > MC * MT || 2 * D > SC * AT ||
+  if (aqc_for(ngd) > 6 || HD * ngd > QC * QT || UNITS * ngd > MC * ((MT / ngd) * ngd) || D > RPW * (MT / 64) * MC ||
+      D > RPW * (AT / 64) * SC ||
       16 * ngd > TC * LT)
     return fail(set_error(MLLM_ERR_UNSUPPORTED, "tiles exceed the chunk registers (d_model %d)", D));
 
@@ -2112,8 +2133,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
 
   // activations, KV cache, scratch
   const size_t kv_elems = (size_t)L * 2 * NKV * c.max_seq_len * HD;
-  const size_t tagged_bytes[4] = {sizeof(uint2) * MAXT * D, sizeof(uint2) * MAXT * D, sizeof(uint2) * MAXT * NH * D,
-                                   sizeof(uint2) * MAXT * P.nchunk * D};
+  const size_t tagged_bytes[4] = {sizeof(uint2) * MAXT * D, sizeof(uint2) * MAXT * D,
+                                   sizeof(uint4) * MAXT * NH * nquads(D), sizeof(uint4) * MAXT * P.nchunk * nquads(D)};
   int rc = dev_alloc(M, (void **)&P.xa, tagged_bytes[0]);
   if (!rc) rc = dev_alloc(M, (void **)&P.xb, tagged_bytes[1]);
   if (!rc) rc = dev_alloc(M, (void **)&P.opart, tagged_bytes[2]);
