@@ -183,6 +183,20 @@ int mllm_model_gemv(mllm_model *model, const char *name, const float *x, float *
  * Returns MLLM_ERR_UNSUPPORTED for mode 3 where it is unavailable. */
 int mllm_set_exec_mode(mllm_model *model, int mode);
 
+/* Prompts of at least min_tokens tokens (default 64; 0 = never) are
+ * processed in batches (no counterpart in the reference, whose GPU path runs
+ * a prompt token by token, webgpu.js:1178-1187): tokens 0 .. n-2 go through
+ * every layer as Q4 GEMMs on the int8 matrix cores and one causal attention
+ * kernel per layer, in chunks of up to 2048 tokens, and write the KV cache;
+ * the last token runs as a decode step and yields the logits.  Shorter
+ * prompts run in passes of mllm_max_pass_tokens() tokens through the decode
+ * phases.  The two agree to the logits tolerance, not bit for bit (the
+ * batched path quantises activations per token instead of per group).
+ * chunk_tokens (1 .. 2048 or max_seq_len if smaller; 0 = the largest) bounds
+ * the tokens per chunk; later chunks read the earlier ones' keys from the
+ * cache. */
+int mllm_set_prefill(mllm_model *model, int min_tokens, int chunk_tokens);
+
 /* GpuPetitGPT.lastTiming {n, gpuMs} (webgpu.js:1143-1160): the time between
  * HIP events recorded on the model's stream immediately before and after the
  * kernels of the last forward / chain call, and the tokens it produced. */

@@ -32,7 +32,7 @@ LIB = os.path.join(PKG, "libmllm.so")
 NAPI_SRC = os.path.join(PKG, "js", "napi", "mllm_napi.cc")
 NAPI_OUT = os.path.join(PKG, "js", "mllm_napi.node")
 
-HIP_SOURCES = ["mllm_ops.hip", "mllm_engine.hip"]
+HIP_SOURCES = ["mllm_ops.hip", "mllm_engine.hip", "mllm_prefill.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("MLLM_OFFLOAD_ARCH", "gfx950")
 HIP_FLAGS = [

@@ -57,6 +57,7 @@
 
 #include "mllm_device.h"
 #include "mllm_host.h"
+#include "mllm_prefill.h"
 
 namespace mllm {
 
@@ -1719,6 +1720,13 @@ struct mllm_model {
   std::vector<hipEvent_t> prof_ev;          // mllm_profile_decode
   float last_ms = 0.f;
   int last_tokens = 0;
+  // batched prompt processing (mllm_prefill.hip): prompts of at least
+  // pf_min tokens (0: never) run their first n - 1 tokens through it
+  PfArgs pf{};
+  std::vector<PfLayer> pf_layer;
+  int pf_min = 0;
+  int pf_tc_max = 0;  // tokens the work buffers hold
+  hipEvent_t ev_pf = nullptr;
   std::vector<void *> allocs;
 };
 
@@ -2021,7 +2029,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   M->num_cus = prop.multiProcessorCount;
   if (hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking) != hipSuccess)
     return fail(set_error(MLLM_ERR_HIP, "stream create"));
-  if (hipEventCreate(&M->ev0) != hipSuccess || hipEventCreate(&M->ev1) != hipSuccess)
+  if (hipEventCreate(&M->ev0) != hipSuccess || hipEventCreate(&M->ev1) != hipSuccess ||
+      hipEventCreate(&M->ev_pf) != hipSuccess)
     return fail(set_error(MLLM_ERR_HIP, "event create"));
 
   // weights: the payload as-is (16-byte aligned tensors, PGW1 layout)
@@ -2164,6 +2173,52 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   P.hist = M->d_hist;
   P.st = M->d_st;
 
+  // batched prompt processing: the weights as PGW1 matrices, work buffers
+  // for up to 2048 tokens per chunk
+  {
+    PfArgs &A = M->pf;
+    auto mat = [](const Q4Mat &w) { return PfMat{reinterpret_cast<const uint8_t *>(w.q), w.s, w.rows, w.cols}; };
+    A.arch = c.arch;
+    A.L = L;
+    A.D = D;
+    A.NH = NH;
+    A.NKV = NKV;
+    A.FF = FF;
+    A.max_seq = c.max_seq_len;
+    A.kv_fp16 = P.kv_fp16;
+    A.eps = P.eps;
+    A.attn_scale = P.attn_scale;
+    A.emb = mat(P.lm);
+    A.wpe = P.wpe;
+    A.sf = P.sf;
+    A.rope_cos = P.rope_cos;
+    A.rope_sin = P.rope_sin;
+    A.kv = P.kv;
+    M->pf_layer.resize(L);
+    for (int i = 0; i < L; ++i) {
+      const LayerW &w = M->layers[i];
+      PfLayer &f = M->pf_layer[i];
+      f.qkv = mat(w.qkv);
+      f.proj = mat(w.proj);
+      f.w1 = mat(w.w1);
+      f.w3 = mat(w.w3);
+      f.w2 = mat(w.w2);
+      f.n1 = w.n1;
+      f.n2 = w.n2;
+      f.qkv_b = w.qkv_b;
+      f.proj_b = w.proj_b;
+      f.fc_b = w.fc_b;
+      f.mproj_b = w.mproj_b;
+    }
+    A.layers = M->pf_layer.data();
+    const int tc = std::min(c.max_seq_len, 2048);
+    void *buf = nullptr;
+    if (int rc = dev_alloc(M, &buf, pf_buffer_bytes(A, tc))) return fail(rc);
+    pf_carve(A, buf, tc);
+    M->pf_tc_max = tc;
+    M->pf_min = 64;
+  }
+
   // persistent kernel: geometry, LDS, one resident workgroup set, flags
   {
     FlowGeom &F = M->flow;
@@ -2219,6 +2274,7 @@ extern "C" int mllm_model_destroy(mllm_model *M) {
   for (hipEvent_t e : M->prof_ev) (void)hipEventDestroy(e);
   if (M->ev0) hipEventDestroy(M->ev0);
   if (M->ev1) hipEventDestroy(M->ev1);
+  if (M->ev_pf) hipEventDestroy(M->ev_pf);
   if (M->stream) hipStreamDestroy(M->stream);
   delete M;
   return 0;
@@ -2251,6 +2307,16 @@ extern "C" int mllm_set_exec_mode(mllm_model *M, int mode) {
   return 0;
 }
 
+extern "C" int mllm_set_prefill(mllm_model *M, int min_tokens, int chunk_tokens) {
+  MLLM_CHECK(M, "null model");
+  MLLM_CHECK(min_tokens >= 0, "prefill threshold %d", min_tokens);
+  MLLM_CHECK(chunk_tokens >= 0 && chunk_tokens <= M->pf_tc_max, "prefill chunk %d (at most %d)", chunk_tokens,
+             M->pf_tc_max);
+  M->pf_min = min_tokens;
+  M->pf.tc = chunk_tokens ? chunk_tokens : M->pf_tc_max;
+  return 0;
+}
+
 extern "C" uint64_t mllm_model_device_bytes(const mllm_model *M) { return M ? M->device_bytes : 0; }
 
 static int fetch_outputs(mllm_model *M, int row, int nrows, float *logits, int32_t *argmax) {
@@ -2265,6 +2331,18 @@ extern "C" int mllm_forward_prompt(mllm_model *M, const int32_t *ids, int n, flo
   MLLM_CHECK(M && ids, "null argument");
   MLLM_CHECK(n > 0 && n <= M->cfg.max_seq_len, "prompt length %d out of range", n);
   if (int rc = check_ids(M, ids, n)) return rc;
+  if (M->pf_min > 0 && n >= M->pf_min) {
+    // tokens 0 .. n-2 write their K and V in chunks; the last one is a
+    // decode step, which forms the logits
+    MLLM_HIP(hipEventRecord(M->ev_pf, M->stream));
+    for (int p0 = 0; p0 < n - 1; p0 += M->pf.tc)
+      if (int rc = pf_layers(M->pf, ids + p0, std::min(M->pf.tc, n - 1 - p0), p0, M->stream)) return rc;
+    if (int rc = run_pass(M, ids + n - 1, 1, n - 1, 1)) return rc;
+    MLLM_HIP(hipEventElapsedTime(&M->last_ms, M->ev_pf, M->ev1));
+    M->last_tokens = n;
+    M->cache_len = n;
+    return fetch_outputs(M, 0, 1, logits, argmax);
+  }
   int last_rows = 0;
   for (int p0 = 0; p0 < n; p0 += M->max_pass) {
     const int m = std::min(M->max_pass, n - p0);

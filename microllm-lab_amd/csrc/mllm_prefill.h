@@ -1,0 +1,56 @@
+// mllm_prefill.h -- batched prompt processing (infer.js:553-577 forwardPrompt):
+// every layer of a chunk of prompt tokens as a few wide kernels (Q4 GEMMs on
+// int8 matrix cores, one causal attention kernel), writing the KV cache.
+// The engine runs the prompt's last token through its decode step, which
+// produces the logits from that cache.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mllm {
+
+// A Q4 group-32 matrix as stored in the PGW1 payload: packed nibbles
+// [rows][cols / 2] (byte k/2 of a group holds element k in the low nibble,
+// k + 1 in the high one) and scales [rows][cols / 32].
+struct PfMat {
+  const uint8_t *q;
+  const float *s;
+  int rows, cols;
+};
+
+struct PfLayer {
+  PfMat qkv, proj, w1, w3, w2;             // gpt2: w1 = mlp.fc, w2 = mlp.proj, no w3
+  const float *n1, *n2;                    // RMS gains; gpt2: LayerNorm gamma || beta
+  const float *qkv_b, *proj_b, *fc_b, *mproj_b;  // gpt2 biases (proj_b / mproj_b may be null)
+};
+
+struct PfArgs {
+  int arch, L, D, NH, NKV, FF, max_seq, kv_fp16;
+  float eps, attn_scale;
+  const PfLayer *layers;  // host array of L layers
+  PfMat emb;              // tied lm_head: the embedding rows
+  const float *wpe, *sf, *rope_cos, *rope_sin;
+  void *kv;               // [L][2][NKV][max_seq][64], f32 or f16
+  // work buffers for up to tc tokens
+  int tc;
+  int32_t *ids;  // [tc]
+  float *x;      // [tc][D] residual stream
+  float *q;      // [tc][D] roped queries
+  float *att;    // [tc][D] attention output
+  float *h;      // [tc][FF] MLP activation
+  float *sx;     // [tc] per-token activation scale
+  uint8_t *px;   // [tc][max(D, FF) / 32][64] int8 activation planes
+};
+
+// Bytes of work buffers for tc tokens (one allocation, carved by pf_carve).
+size_t pf_buffer_bytes(const PfArgs &A, int tc);
+void pf_carve(PfArgs &A, void *base, int tc);
+
+// Tokens ids[0 .. n) at positions pos0 .. pos0 + n (n <= tc, pos0 + n <=
+// max_seq) through every layer: their K and V are written to the cache.  The
+// residual stream after the last layer is not formed (nothing reads it).
+// Returns 0 or an MLLM_ERR_* code with the message set.
+int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, hipStream_t stream);
+
+}  // namespace mllm

@@ -44,6 +44,7 @@ SIGNATURES = {
     "mllm_decode_chain": ([P, C.c_int32, I, C.c_int32, P, I, P, P], I),
     "mllm_model_gemv": ([P, C.c_char_p, P, P], I),
     "mllm_set_exec_mode": ([P, I], I),
+    "mllm_set_prefill": ([P, I, I], I),
     "mllm_model_device_bytes": ([P], C.c_uint64),
     "mllm_last_timing": ([P, P, P], I),
     "mllm_profile_decode": ([P, C.c_int32, I, P], I),

@@ -110,6 +110,11 @@ class PetitGPT:
         abi.call("mllm_set_exec_mode", self._h, int(mode))
         self.exec_mode = int(mode)
 
+    def set_prefill(self, min_tokens: int, chunk_tokens: int = 0):
+        """Prompts of at least min_tokens tokens take the batched path (0: never),
+        in chunks of at most chunk_tokens (0: the largest)."""
+        abi.call("mllm_set_prefill", self._h, int(min_tokens), int(chunk_tokens))
+
     def last_timing(self):
         """(gpu_ms, tokens) of the last call, from HIP events on the model stream."""
         ms = C.c_float(0)

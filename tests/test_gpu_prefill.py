@@ -1,0 +1,123 @@
+"""GPU parity of the batched prompt path (mllm_set_prefill; forwardPrompt,
+infer.js:553-577) against the oracle and against the 16-token pass path.
+
+Bars: the prompt's last-token logits, and the logits of decode steps that
+read the batched path's KV cache, within LOGIT_TOL (max-abs 1e-2) of the
+fp64-accumulating oracle; greedy argmax identical wherever the oracle's top-2
+margin exceeds MARGIN.  Against the pass path (activations quantised per
+group instead of per token) the logits agree within PASS_TOL.
+"""
+import numpy as np
+import pytest
+
+import mllm
+from mllm import pgw
+
+gpu = pytest.mark.gpu
+LOGIT_TOL = 1e-2
+MARGIN = 1e-2
+PASS_TOL = 5e-3
+
+
+def margin(logits):
+    top2 = np.partition(logits, -2)[-2:]
+    return float(top2[1] - top2[0])
+
+
+def build(arch="llama", seed=1, **over):
+    cfg = pgw.small_config(arch, **over)
+    return pgw.parse_pgw(pgw.make_model(cfg, seed=seed))
+
+
+def vs_oracle(g, ref, prompt, steps, rng):
+    lg = g.forwardPrompt(prompt).copy()
+    lr = ref.forward_prompt(prompt)
+    worst = float(np.abs(lg - lr).max())
+    agree = [int(np.argmax(lg)) == int(np.argmax(lr)) or margin(lr) <= MARGIN]
+    for _ in range(steps):
+        tok = int(rng.integers(0, g.cfg.vocab_size))
+        lg = g.forwardDecode(tok).copy()
+        lr = ref.forward_decode(tok)
+        worst = max(worst, float(np.abs(lg - lr).max()))
+        agree.append(int(np.argmax(lg)) == int(np.argmax(lr)) or margin(lr) <= MARGIN)
+    return worst, all(agree)
+
+
+@gpu
+@pytest.mark.parametrize("arch", ["llama", "gpt2"])
+@pytest.mark.parametrize("chunk", [0, 40])
+def test_batched_prompt_vs_oracle(oracle_lib, arch, chunk):
+    """A 150-token prompt in one chunk, and in chunks of 40 (later chunks read
+    the earlier keys from the cache; 149 = 3 x 40 + 29 ragged)."""
+    bundle = build(arch, seed=21, max_seq_len=256)
+    print(f"prefill {arch} chunk={chunk}", flush=True)
+    g = mllm.PetitGPT(bundle)
+    g.set_prefill(64, chunk)
+    ref = oracle_lib.OracleModel(bundle)
+    rng = np.random.default_rng(5)
+    prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 150)]
+    worst, agree = vs_oracle(g, ref, prompt, 5, rng)
+    assert g.cacheLen == 150 + 5
+    g.destroy()
+    assert worst < LOGIT_TOL and agree, worst
+
+
+@gpu
+@pytest.mark.parametrize("kv_fp16", [False, True])
+def test_batched_prompt_long_context_vs_oracle(oracle_lib, kv_fp16):
+    """700 tokens: many 64-key blocks per query block, every query block
+    masked on its diagonal; f32 and f16 KV."""
+    bundle = build("llama", seed=22, max_seq_len=1024)
+    print(f"prefill long kv_fp16={kv_fp16}", flush=True)
+    g = mllm.PetitGPT(bundle, kv_fp16=kv_fp16)
+    ref = oracle_lib.OracleModel(bundle)
+    rng = np.random.default_rng(6)
+    prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 700)]
+    worst, agree = vs_oracle(g, ref, prompt, 3, rng)
+    g.destroy()
+    assert worst < LOGIT_TOL and agree, worst
+
+
+@gpu
+@pytest.mark.parametrize("n", [64, 65, 97, 128])
+def test_batched_equals_pass_path(n):
+    """Prompt lengths around the 32-token GEMM tile and the 64-query attention
+    block: the batched path and the pass path give the same logits within
+    PASS_TOL, and the same greedy continuation."""
+    bundle = build("llama", seed=23, max_seq_len=256)
+    rng = np.random.default_rng(n)
+    prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, n)]
+    outs = []
+    for pf_min in (64, 0):
+        print(f"prefill n={n} pf_min={pf_min}", flush=True)
+        g = mllm.PetitGPT(bundle)
+        g.set_prefill(pf_min)
+        lg = g.forwardPrompt(prompt).copy()
+        ids = g.generate(prompt, maxNewTokens=8, mode="greedy")["generatedIds"]
+        outs.append((lg, ids))
+        g.destroy()
+    assert np.abs(outs[0][0] - outs[1][0]).max() < PASS_TOL
+    if margin(outs[1][0]) > MARGIN:
+        assert outs[0][1][0] == outs[1][1][0]
+
+
+@gpu
+def test_smollm2_135m_batched_prompt_vs_pass_path():
+    """Config 1 shape at full size, a 300-token prompt: the batched path's
+    logits and its KV cache (read by 8 greedy steps) against the pass path."""
+    cfg = pgw.CONFIGS["smollm2-135m"]
+    bundle = pgw.parse_pgw(pgw.make_llama(cfg, seed=0))
+    rng = np.random.default_rng(7)
+    prompt = [int(v) for v in rng.integers(0, cfg.vocab_size, 300)]
+    follow = [int(v) for v in rng.integers(0, cfg.vocab_size, 8)]
+    outs = []
+    for pf_min in (64, 0):
+        print(f"prefill 135m pf_min={pf_min}", flush=True)
+        g = mllm.PetitGPT(bundle)
+        g.set_prefill(pf_min)
+        steps = [g.forwardPrompt(prompt).copy()]
+        for tok in follow:
+            steps.append(g.forwardDecode(tok).copy())
+        outs.append(np.stack(steps))
+        g.destroy()
+    assert np.abs(outs[0] - outs[1]).max() < PASS_TOL
