@@ -27,10 +27,10 @@
 // 9 .. 15, odd).  The activation planes are stored in that order, 64 bytes
 // per (token, group): hi of half 0, hi of half 1, lo of half 0, lo of half 1.
 //
-// Attention: causal, f32, one (64-query block, query head) per workgroup,
-// 64-key blocks staged in LDS with an online softmax (running max and sum,
-// rescaled per block); the softmax of infer.js:422-504 without the decode
-// path's single pass.
+// Attention: causal, one (32-query tile, KV head) per workgroup, 32-key
+// blocks staged in LDS, S = Q K^T and O = P V on the f16 matrix cores with
+// hi/lo splits for f32 accuracy, an online softmax (running max and sum,
+// rescaled per block); the softmax of infer.js:422-504.
 //
 // Per layer: norm + quantise, QKV GEMM (bias or RoPE, K/V to the cache, q to
 // a buffer), attention, quantise, O GEMM (+ residual), norm + quantise,
@@ -50,8 +50,6 @@ namespace {
 constexpr int PX_MAX = 32639;   // |xi| bound of the 16-bit activations
 constexpr int PX_GROUP = 64;    // bytes per (token, group) of the planes
 constexpr int PF_HD = 64;       // head dimension
-constexpr int AQ = 64, AK = 64; // attention query and key block
-constexpr int KS = 68;          // LDS row stride (floats) of the key / weight tiles
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -298,142 +296,181 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
 }
 
 // ---------------------------------------------------------------- attention
-// Workgroup (query block, query head): 64 queries x 64 dimensions in LDS;
-// per 64-key block, S = Q K^T (thread (ti, tj): queries 4ti .. 4ti+3, keys
-// tj + 16b), the online softmax over the 16 threads of a query row, then
-// O += P V (thread (ti, tj): queries 4ti .. 4ti+3, dimensions 4tj .. 4tj+3).
-__global__ __launch_bounds__(WG) void k_pf_attn(PfArgs A, int li, int n, int pos0) {
-  __shared__ float Qs[AQ * PF_HD];
-  __shared__ float KP[AK * KS];  // keys, then the block's weights P
-  __shared__ float Vs[AK * PF_HD];
-  const int hq = blockIdx.y, qb = gridDim.x - 1 - blockIdx.x;  // the longest rows first
-  const int T0 = qb * AQ;
-  const int kvh = hq / (A.NH / A.NKV);
-  const int ti = tid() >> 4, tj = tid() & 15;
-  // the query block (zeros past the chunk)
-  for (int i = tid(); i < AQ * PF_HD / 4; i += WG) {
-    const int r = i >> 4, c = i & 15;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (T0 + r < n) v = reinterpret_cast<const float4 *>(A.q + (size_t)(T0 + r) * A.D + hq * PF_HD)[c];
-    reinterpret_cast<float4 *>(Qs)[i] = v;
+// Workgroup (32-query tile, KV head), one wave per query head of the KV
+// head (GQA: the waves share the staged keys and values).  Per 32-key block,
+// on the f16 matrix cores (v_mfma_f32_32x32x16_f16, f32 accumulation):
+//   S^T = K Q^T   A = the keys (lane: key j, 8 dimensions), B = the queries;
+//                 out lane (query j, half hh) holds keys 8(v/4) + 4hh + v%4
+//   O^T += V^T P^T  A = the values transposed (lane: dimension j), B = the
+//                 weights P straight from the S^T registers: slot s of half
+//                 hh is key 8(s/4) + 4hh + s%4 (+16 for the block's second
+//                 half), so V^T takes the same keys per slot
+// so every lane holds one query's scores and output column, and the online
+// softmax (running max and sum, per-block rescaling) needs one exchange with
+// the lane 32 apart.  f32 accuracy from f16 operands: the scaled query and
+// the weights are split as hi + lo halves (v = hi + lo to ~2^-22), and so are
+// f32 keys and values (an f16 cache is exact as is); the dropped lo x lo
+// terms are below 2^-40 relative.  The scores are formed in the log2 domain
+// (the query scaled by attn_scale * log2 e) for v_exp_f32.
+constexpr int QTL = 32;   // queries per wave
+constexpr int KBL = 32;   // keys per block
+constexpr int KROW = 72;  // halves per staged key row (64 + pad)
+constexpr int VROW = 40;  // halves per staged value column (32 keys + pad)
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ void load8(const PfArgs &A, size_t off, float (&v)[8]) {
+  if (A.kv_fp16) {
+    const uint4 u = *reinterpret_cast<const uint4 *>(reinterpret_cast<const __half *>(A.kv) + off);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const __half2 h = *reinterpret_cast<const __half2 *>(&w[i]);
+      v[2 * i] = __low2float(h);
+      v[2 * i + 1] = __high2float(h);
+    }
+  } else {
+    const float4 a = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(A.kv) + off);
+    const float4 b = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(A.kv) + off + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
   }
-  const int qlast = pos0 + min(T0 + AQ, n) - 1;  // last key any query of the block sees
-  const int nkb = qlast / AK + 1;
+}
+
+template <bool SPLIT_KV>
+__global__ __launch_bounds__(1024) void k_pf_attn(PfArgs A, int li, int n, int pos0) {
+  __shared__ __attribute__((aligned(16))) _Float16 Kh[KBL * KROW], Kl[SPLIT_KV ? KBL * KROW : 8];
+  __shared__ __attribute__((aligned(16))) _Float16 Vh[PF_HD * VROW], Vl[SPLIT_KV ? PF_HD * VROW : 8];
+  const int rep = A.NH / A.NKV;
+  const int T0 = (gridDim.x - 1 - blockIdx.x) * QTL, kvh = blockIdx.y;  // the longest tiles first
+  const int lane = tid() & 63, j = lane & 31, hh = lane >> 5;
+  const int hq = kvh * rep + (tid() >> 6);
+  v8h qh[4], ql[4];
+  {
+    const float c = A.attn_scale * 1.4426950408889634f;
+    const float *qr = A.q + (size_t)min(T0 + j, n - 1) * A.D + hq * PF_HD + 8 * hh;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = qr[16 * m + i] * c;
+        const _Float16 h = (_Float16)v;
+        qh[m][i] = h;
+        ql[m][i] = (_Float16)(v - (float)h);
+      }
+  }
+  const int qpos = pos0 + T0 + j;
+  const int qlast = pos0 + min(T0 + QTL, n) - 1;  // last key any query of the tile sees
+  const int nkb = qlast / KBL + 1;
   const size_t kbase = pf_kv_index(A, li, 0, kvh, 0), vbase = pf_kv_index(A, li, 1, kvh, 0);
-  float m[4], l[4], o[4][4];
+  float m_run = -INFINITY, l_run = 0.f;
+  v16f o0, o1;
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    m[a] = -INFINITY;
-    l[a] = 0.f;
-    o[a][0] = o[a][1] = o[a][2] = o[a][3] = 0.f;
-  }
+  for (int v = 0; v < 16; ++v) o0[v] = o1[v] = 0.f;
   for (int kb = 0; kb < nkb; ++kb) {
-    const int k0 = kb * AK;
-    __syncthreads();  // the previous block's P and V are consumed
-    for (int i = tid(); i < AK * PF_HD / 4; i += WG) {
-      const int r = i >> 4, c = i & 15;
-      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-      if (k0 + r <= qlast) {
-        const size_t ko = kbase + (size_t)(k0 + r) * PF_HD + 4 * c, vo = vbase + (size_t)(k0 + r) * PF_HD + 4 * c;
-        if (A.kv_fp16) {
-          const __half *h = reinterpret_cast<const __half *>(A.kv);
-          const uint2 ku = *reinterpret_cast<const uint2 *>(h + ko), vu = *reinterpret_cast<const uint2 *>(h + vo);
-          const __half2 k01 = *reinterpret_cast<const __half2 *>(&ku.x), k23 = *reinterpret_cast<const __half2 *>(&ku.y);
-          const __half2 v01 = *reinterpret_cast<const __half2 *>(&vu.x), v23 = *reinterpret_cast<const __half2 *>(&vu.y);
-          kv = make_float4(__low2float(k01), __high2float(k01), __low2float(k23), __high2float(k23));
-          vv = make_float4(__low2float(v01), __high2float(v01), __low2float(v23), __high2float(v23));
-        } else {
-          const float *f = reinterpret_cast<const float *>(A.kv);
-          kv = *reinterpret_cast<const float4 *>(f + ko);
-          vv = *reinterpret_cast<const float4 *>(f + vo);
+    const int k0 = kb * KBL;
+    __syncthreads();  // the previous block is consumed
+    for (int c = tid(); c < KBL * 8; c += blockDim.x) {
+      const int kk = c >> 3, d0 = (c & 7) * 8;
+      float kv[8], vv[8];
+      if (k0 + kk <= qlast) {
+        load8(A, kbase + (size_t)(k0 + kk) * PF_HD + d0, kv);
+        load8(A, vbase + (size_t)(k0 + kk) * PF_HD + d0, vv);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kv[i] = vv[i] = 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const _Float16 kh = (_Float16)kv[i], vh = (_Float16)vv[i];
+        Kh[kk * KROW + d0 + i] = kh;
+        Vh[(d0 + i) * VROW + kk] = vh;
+        if (SPLIT_KV) {
+          Kl[kk * KROW + d0 + i] = (_Float16)(kv[i] - (float)kh);
+          Vl[(d0 + i) * VROW + kk] = (_Float16)(vv[i] - (float)vh);
         }
       }
-      *reinterpret_cast<float4 *>(KP + r * KS + 4 * c) = kv;
-      reinterpret_cast<float4 *>(Vs)[i] = vv;
     }
     __syncthreads();
-    float s[4][4];
+    v16f s;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) s[a][0] = s[a][1] = s[a][2] = s[a][3] = 0.f;
-#pragma unroll 4
-    for (int d = 0; d < PF_HD; d += 4) {
-      float4 qa[4], kk[4];
+    for (int v = 0; v < 16; ++v) s[v] = 0.f;
 #pragma unroll
-      for (int a = 0; a < 4; ++a) qa[a] = *reinterpret_cast<const float4 *>(Qs + (4 * ti + a) * PF_HD + d);
-#pragma unroll
-      for (int b = 0; b < 4; ++b) kk[b] = *reinterpret_cast<const float4 *>(KP + (tj + 16 * b) * KS + d);
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          float z = s[a][b];
-          z = __builtin_fmaf(qa[a].x, kk[b].x, z);
-          z = __builtin_fmaf(qa[a].y, kk[b].y, z);
-          z = __builtin_fmaf(qa[a].z, kk[b].z, z);
-          z = __builtin_fmaf(qa[a].w, kk[b].w, z);
-          s[a][b] = z;
-        }
-    }
-    __syncthreads();  // every thread is done with the keys: KP becomes P
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int qpos = pos0 + T0 + 4 * ti + a;
-      float mb = -INFINITY;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        s[a][b] = k0 + tj + 16 * b <= qpos ? s[a][b] * A.attn_scale : -INFINITY;
-        mb = fmaxf(mb, s[a][b]);
+    for (int m = 0; m < 4; ++m) {
+      const v8h ka = *reinterpret_cast<const v8h *>(Kh + j * KROW + 16 * m + 8 * hh);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[m], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[m], s, 0, 0, 0);
+      if (SPLIT_KV) {
+        const v8h kl = *reinterpret_cast<const v8h *>(Kl + j * KROW + 16 * m + 8 * hh);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[m], s, 0, 0, 0);
       }
-      // the 16 threads of the row are lanes 16k .. 16k+15 of the wave
-      mb = fmaxf(mb, __shfl_xor(mb, 8, 16));
-      mb = fmaxf(mb, __shfl_xor(mb, 4, 16));
-      mb = fmaxf(mb, __shfl_xor(mb, 2, 16));
-      mb = fmaxf(mb, __shfl_xor(mb, 1, 16));
-      const float mn = fmaxf(m[a], mb);  // finite: key 0 is in block 0 for every query
-      const float alpha = expf(m[a] - mn);
-      float ps = 0.f;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const float p = expf(s[a][b] - mn);
-        KP[(4 * ti + a) * KS + tj + 16 * b] = p;
-        ps += p;
-      }
-      ps += __shfl_xor(ps, 8, 16);
-      ps += __shfl_xor(ps, 4, 16);
-      ps += __shfl_xor(ps, 2, 16);
-      ps += __shfl_xor(ps, 1, 16);
-      l[a] = l[a] * alpha + ps;
-      m[a] = mn;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) o[a][c] *= alpha;
     }
-    __syncthreads();
-#pragma unroll 4
-    for (int k = 0; k < AK; k += 4) {
-      float4 pa[4], vk[4];
+    float mx = -INFINITY;
 #pragma unroll
-      for (int a = 0; a < 4; ++a) pa[a] = *reinterpret_cast<const float4 *>(KP + (4 * ti + a) * KS + k);
+    for (int v = 0; v < 16; ++v) {
+      if (k0 + 8 * (v >> 2) + 4 * hh + (v & 3) > qpos) s[v] = -INFINITY;
+      mx = fmaxf(mx, s[v]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m_run, mx);  // finite: block 0 holds key 0 for every query
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+    v8h ph[2], pl[2];
+    float ps = 0.f;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) vk[u] = *reinterpret_cast<const float4 *>(Vs + (k + u) * PF_HD + 4 * tj);
+    for (int v = 0; v < 16; ++v) {
+      const float p = __builtin_amdgcn_exp2f(s[v] - mn);
+      ps += p;
+      const _Float16 h = (_Float16)p;
+      ph[v >> 3][v & 7] = h;
+      pl[v >> 3][v & 7] = (_Float16)(p - (float)h);
+    }
+    ps += __shfl_xor(ps, 32);
+    l_run = l_run * alpha + ps;
+    m_run = mn;
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const float pp[4] = {pa[a].x, pa[a].y, pa[a].z, pa[a].w};
+    for (int v = 0; v < 16; ++v) {
+      o0[v] *= alpha;
+      o1[v] *= alpha;
+    }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          o[a][0] = __builtin_fmaf(pp[u], vk[u].x, o[a][0]);
-          o[a][1] = __builtin_fmaf(pp[u], vk[u].y, o[a][1]);
-          o[a][2] = __builtin_fmaf(pp[u], vk[u].z, o[a][2]);
-          o[a][3] = __builtin_fmaf(pp[u], vk[u].w, o[a][3]);
-        }
+    for (int u = 0; u < 2; ++u) {
+      const int kc = 16 * u + 4 * hh;
+      v8h va, vb;
+      {
+        const v4h a0 = *reinterpret_cast<const v4h *>(Vh + j * VROW + kc);
+        const v4h a1 = *reinterpret_cast<const v4h *>(Vh + j * VROW + kc + 8);
+        const v4h b0 = *reinterpret_cast<const v4h *>(Vh + (32 + j) * VROW + kc);
+        const v4h b1 = *reinterpret_cast<const v4h *>(Vh + (32 + j) * VROW + kc + 8);
+        va = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+        vb = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+      o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph[u], o0, 0, 0, 0);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl[u], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb, ph[u], o1, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb, pl[u], o1, 0, 0, 0);
+      if (SPLIT_KV) {
+        const v4h a0 = *reinterpret_cast<const v4h *>(Vl + j * VROW + kc);
+        const v4h a1 = *reinterpret_cast<const v4h *>(Vl + j * VROW + kc + 8);
+        const v4h b0 = *reinterpret_cast<const v4h *>(Vl + (32 + j) * VROW + kc);
+        const v4h b1 = *reinterpret_cast<const v4h *>(Vl + (32 + j) * VROW + kc + 8);
+        o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7), ph[u], o0,
+                                                    0, 0, 0);
+        o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7), ph[u], o1,
+                                                    0, 0, 0);
       }
     }
   }
+  // lane (query j, half hh): dimensions 8g + 4hh .. +3 (o0), 32 + the same (o1)
+  if (T0 + j < n) {
+    float *out = A.att + (size_t)(T0 + j) * A.D + hq * PF_HD + 4 * hh;
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int t = T0 + 4 * ti + a;
-    if (t < n)
-      *reinterpret_cast<float4 *>(A.att + (size_t)t * A.D + hq * PF_HD + 4 * tj) =
-          make_float4(o[a][0] / l[a], o[a][1] / l[a], o[a][2] / l[a], o[a][3] / l[a]);
+    for (int g = 0; g < 4; ++g) {
+      *reinterpret_cast<float4 *>(out + 8 * g) =
+          make_float4(o0[4 * g] / l_run, o0[4 * g + 1] / l_run, o0[4 * g + 2] / l_run, o0[4 * g + 3] / l_run);
+      *reinterpret_cast<float4 *>(out + 32 + 8 * g) =
+          make_float4(o1[4 * g] / l_run, o1[4 * g + 1] / l_run, o1[4 * g + 2] / l_run, o1[4 * g + 3] / l_run);
+    }
   }
 }
 
@@ -497,12 +534,13 @@ int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, hipStream_t 
   if (n <= 0) return 0;
   MLLM_CHECK(n <= A.tc && pos0 >= 0 && pos0 + n <= A.max_seq, "prefill chunk of %d tokens at %d out of range", n,
              pos0);
-  MLLM_CHECK(A.D == A.NH * PF_HD && A.D % 64 == 0 && A.FF % 64 == 0 && A.D <= 16384 && A.FF <= 16384,
+  MLLM_CHECK(A.D == A.NH * PF_HD && A.NH % A.NKV == 0 && A.NH / A.NKV <= 16 && A.FF % 64 == 0 && A.D <= 8192 &&
+                 A.FF <= 8192,
              "prefill shapes unsupported (d_model %d, d_ff %d)", A.D, A.FF);
   MLLM_HIP(hipMemcpyAsync(A.ids, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, s));
   const bool gpt2 = A.arch == 1;
   hipLaunchKernelGGL(k_pf_embed, dim3(n), dim3(WG), 0, s, A, n, pos0);
-  const int nqb = (n + AQ - 1) / AQ;
+  const int nqt = (n + QTL - 1) / QTL, rep = A.NH / A.NKV;
   for (int li = 0; li < A.L; ++li) {
     const PfLayer &W = A.layers[li];
     if (gpt2)
@@ -514,7 +552,10 @@ int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, hipStream_t 
     G.pos0 = pos0;
     launch_gemm<EPI_QKV>(A, G, s);
     if (li == A.L - 1) break;  // the last layer's K and V are all the cache needs
-    hipLaunchKernelGGL(k_pf_attn, dim3(nqb, A.NH), dim3(WG), 0, s, A, li, n, pos0);
+    if (A.kv_fp16)
+      hipLaunchKernelGGL(k_pf_attn<false>, dim3(nqt, A.NKV), dim3(64 * rep), 0, s, A, li, n, pos0);
+    else
+      hipLaunchKernelGGL(k_pf_attn<true>, dim3(nqt, A.NKV), dim3(64 * rep), 0, s, A, li, n, pos0);
     launch_quant<NORM_NONE>(A, A.att, A.D, nullptr, n, s);
     launch_gemm<EPI_RESID>(A, gemm_same(W.proj, n, gpt2 ? W.proj_b : nullptr, A.x, A.D), s);
     if (gpt2)
