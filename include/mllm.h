@@ -194,7 +194,9 @@ int mllm_set_exec_mode(mllm_model *model, int mode);
  * batched path quantises activations per token instead of per group).
  * chunk_tokens (1 .. 2048 or max_seq_len if smaller; 0 = the largest) bounds
  * the tokens per chunk; later chunks read the earlier ones' keys from the
- * cache. */
+ * cache.  Models with more than 4 query heads per KV head, or d_model / d_ff
+ * not multiples of 64, keep the pass path (min_tokens > 0 then returns
+ * MLLM_ERR_UNSUPPORTED). */
 int mllm_set_prefill(mllm_model *model, int min_tokens, int chunk_tokens);
 
 /* GpuPetitGPT.lastTiming {n, gpuMs} (webgpu.js:1143-1160): the time between

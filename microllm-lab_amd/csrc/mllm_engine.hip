@@ -2211,12 +2211,29 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       f.mproj_b = w.mproj_b;
     }
     A.layers = M->pf_layer.data();
-    const int tc = std::min(c.max_seq_len, 2048);
-    void *buf = nullptr;
-    if (int rc = dev_alloc(M, &buf, pf_buffer_bytes(A, tc))) return fail(rc);
-    pf_carve(A, buf, tc);
-    M->pf_tc_max = tc;
-    M->pf_min = 64;
+    if (pf_supported(A)) {
+      const int tc = std::min(c.max_seq_len, 2048);
+      void *buf = nullptr;
+      if (int rc = dev_alloc(M, &buf, pf_buffer_bytes(A, tc))) return fail(rc);
+      pf_carve(A, buf, tc);
+      // the layer matrices as tiled copies (about the payload's size again)
+      size_t tiled = 0;
+      for (PfLayer &f : M->pf_layer)
+        for (PfMat *w : {&f.qkv, &f.proj, &f.w1, &f.w3, &f.w2})
+          if (w->q) tiled += pf_tiled_bytes(*w);
+      uint8_t *tb = nullptr;
+      if (int rc = dev_alloc(M, (void **)&tb, tiled)) return fail(rc);
+      for (PfLayer &f : M->pf_layer)
+        for (PfMat *w : {&f.qkv, &f.proj, &f.w1, &f.w3, &f.w2})
+          if (w->q) {
+            const size_t b = pf_tiled_bytes(*w);
+            if (int rc = pf_tile(*w, tb, w, M->stream)) return fail(rc);
+            tb += b;
+          }
+      if (hipStreamSynchronize(M->stream) != hipSuccess) return fail(set_error(MLLM_ERR_HIP, "weight tiling"));
+      M->pf_tc_max = tc;
+      M->pf_min = 64;
+    }
   }
 
   // persistent kernel: geometry, LDS, one resident workgroup set, flags
@@ -2310,6 +2327,7 @@ extern "C" int mllm_set_exec_mode(mllm_model *M, int mode) {
 extern "C" int mllm_set_prefill(mllm_model *M, int min_tokens, int chunk_tokens) {
   MLLM_CHECK(M, "null model");
   MLLM_CHECK(min_tokens >= 0, "prefill threshold %d", min_tokens);
+  if (min_tokens > 0 && !M->pf_tc_max) return set_error(MLLM_ERR_UNSUPPORTED, "batched prompts unsupported for this model");
   MLLM_CHECK(chunk_tokens >= 0 && chunk_tokens <= M->pf_tc_max, "prefill chunk %d (at most %d)", chunk_tokens,
              M->pf_tc_max);
   M->pf_min = min_tokens;

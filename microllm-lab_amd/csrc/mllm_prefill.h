@@ -19,6 +19,7 @@ struct PfMat {
   int rows, cols;
 };
 
+// The layer matrices are tiled copies (pf_tile); the embedding is not.
 struct PfLayer {
   PfMat qkv, proj, w1, w3, w2;             // gpt2: w1 = mlp.fc, w2 = mlp.proj, no w3
   const float *n1, *n2;                    // RMS gains; gpt2: LayerNorm gamma || beta
@@ -40,8 +41,20 @@ struct PfArgs {
   float *att;    // [tc][D] attention output
   float *h;      // [tc][FF] MLP activation
   float *sx;     // [tc] per-token activation scale
-  uint8_t *px;   // [tc][max(D, FF) / 32][64] int8 activation planes
+  uint8_t *px;   // [tc / 32][max(D, FF) / 32][2][64 lanes][16] int8 activation planes
 };
+
+// The tiled copy of a Q4 matrix that the prefill GEMMs read (rows and cols
+// multiples of 32): for row tile rt and group g, 64 lane operands of 8 bytes
+// (lane 32 hh + j: bytes 8hh .. 8hh+7 of the group in row 32 rt + j), then the
+// scales per (row tile, group) as 32 floats.  pf_tile enqueues the copy on
+// `stream` into dst (pf_tiled_bytes(W) bytes) and describes it in *out.
+size_t pf_tiled_bytes(const PfMat &W);
+int pf_tile(const PfMat &W, void *dst, PfMat *out, hipStream_t stream);
+
+// Shapes the kernels take: head_dim 64, at most 4 query heads per KV head,
+// d_model and d_ff multiples of 64 up to 8192.
+bool pf_supported(const PfArgs &A);
 
 // Bytes of work buffers for tc tokens (one allocation, carved by pf_carve).
 size_t pf_buffer_bytes(const PfArgs &A, int tc);

@@ -40,6 +40,8 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <algorithm>
+
 #include "mllm_device.h"
 #include "mllm_host.h"
 #include "mllm_prefill.h"
@@ -48,7 +50,7 @@ namespace mllm {
 namespace {
 
 constexpr int PX_MAX = 32639;   // |xi| bound of the 16-bit activations
-constexpr int PX_GROUP = 64;    // bytes per (token, group) of the planes
+constexpr int PX_TILE = 2048;   // bytes per (32-token tile, group) of the planes
 constexpr int PF_HD = 64;       // head dimension
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -137,7 +139,8 @@ __global__ __launch_bounds__(WG) void k_pf_quant(const float *src, int K, const 
   am = block_max<WG>(am, red);  // its barriers also order the y4 stores above
   const float inv = am > 0.f ? (float)PX_MAX / am : 0.f;
   if (tid() == 0) sx[t] = am / (float)PX_MAX;
-  uint8_t *rowp = px + (size_t)t * ng * PX_GROUP;
+  // token t is row j = t % 32 of token tile t / 32
+  uint8_t *tile = px + (size_t)(t >> 5) * ng * PX_TILE + 16 * (t & 31);
   for (int q = tid(); q < nq; q += WG) {
     const float4 v = y4[q];
     const int x0 = (int)__builtin_rintf(v.x * inv), x1 = (int)__builtin_rintf(v.y * inv);
@@ -150,11 +153,11 @@ __global__ __launch_bounds__(WG) void k_pf_quant(const float *src, int K, const 
     // p, p+1 of the half, odd ones at p+8, p+9
     const int e0 = 4 * (q & 7), hh = e0 >> 4, kk = e0 & 15;
     const int p = (kk >> 3) * 4 + ((kk & 7) >> 1);
-    uint8_t *rec = rowp + (q >> 3) * PX_GROUP + 16 * hh;
+    uint8_t *rec = tile + (size_t)(q >> 3) * PX_TILE + 512 * hh;  // lane 32 hh + j of the hi plane
     *reinterpret_cast<unsigned short *>(rec + p) = (unsigned short)((h0 & 255) | ((h2 & 255) << 8));
     *reinterpret_cast<unsigned short *>(rec + 8 + p) = (unsigned short)((h1 & 255) | ((h3 & 255) << 8));
-    *reinterpret_cast<unsigned short *>(rec + 32 + p) = (unsigned short)((l0 & 255) | ((l2 & 255) << 8));
-    *reinterpret_cast<unsigned short *>(rec + 40 + p) = (unsigned short)((l1 & 255) | ((l3 & 255) << 8));
+    *reinterpret_cast<unsigned short *>(rec + 1024 + p) = (unsigned short)((l0 & 255) | ((l2 & 255) << 8));
+    *reinterpret_cast<unsigned short *>(rec + 1032 + p) = (unsigned short)((l1 & 255) | ((l3 & 255) << 8));
   }
 }
 
@@ -189,6 +192,8 @@ __device__ __forceinline__ v4i pf_unpack(uint2 w) {
   return r;
 }
 
+constexpr int GPF = 4;  // groups of loads in flight per wave
+
 struct GemmLd {
   uint2 w0, w1;
   float c0, c1;
@@ -202,28 +207,37 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
   if (R >= G.rows) return;  // no barriers below
   const int T0 = blockIdx.y * 32;
   const int ng = G.ng;
-  const int ra = min(R + j, G.rows - 1), rb = min(R + G.off1 + j, G.rows - 1);
-  const uint8_t *wa = G.q0 + (size_t)ra * ng * 16 + 8 * hh;
-  const uint8_t *wb = G.q1 + (size_t)rb * ng * 16 + 8 * hh;
-  const float *sa = G.s0 + (size_t)ra * ng, *sb = G.s1 + (size_t)rb * ng;
-  const uint8_t *xa = A.px + (size_t)min(T0 + j, G.n - 1) * ng * PX_GROUP + 16 * hh;
+  // tiled operands (every row tile and token tile whole): per group, the
+  // wave's weights are 512 contiguous bytes, its scales 128, its
+  // activations 2 x 1024
+  const size_t ta = (size_t)(R >> 5) * ng, tb = (size_t)((R + G.off1) >> 5) * ng;
+  const uint8_t *wa = G.q0 + ta * 512 + 8 * lane, *wb = G.q1 + tb * 512 + 8 * lane;
+  const float *sa = G.s0 + ta * 32 + j, *sb = G.s1 + tb * 32 + j;
+  const uint8_t *xa = A.px + (size_t)blockIdx.y * ng * PX_TILE + 16 * lane;
   auto load = [&](int g) {
     GemmLd L;
-    L.w0 = *reinterpret_cast<const uint2 *>(wa + 16 * g);
-    L.w1 = *reinterpret_cast<const uint2 *>(wb + 16 * g);
-    L.c0 = sa[g];
-    L.c1 = sb[g];
-    L.ah = *reinterpret_cast<const v4i *>(xa + PX_GROUP * g);
-    L.al = *reinterpret_cast<const v4i *>(xa + PX_GROUP * g + 32);
+    L.w0 = *reinterpret_cast<const uint2 *>(wa + 512 * g);
+    L.w1 = *reinterpret_cast<const uint2 *>(wb + 512 * g);
+    L.c0 = sa[32 * g];
+    L.c1 = sb[32 * g];
+    L.ah = *reinterpret_cast<const v4i *>(xa + PX_TILE * g);
+    L.al = *reinterpret_cast<const v4i *>(xa + PX_TILE * g + 1024);
     return L;
   };
   float acc0[16], acc1[16];
 #pragma unroll
   for (int v = 0; v < 16; ++v) acc0[v] = acc1[v] = 0.f;
   const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  GemmLd cur = load(0);
-  for (int g = 0; g < ng; ++g) {
-    const GemmLd nxt = load(min(g + 1, ng - 1));
+  // the loads of group g + GPF go out before group g is computed
+  GemmLd ring[GPF];
+#pragma unroll
+  for (int i = 0; i < GPF; ++i) ring[i] = load(min(i, ng - 1));
+  for (int g0 = 0; g0 < ng; g0 += GPF)
+#pragma unroll
+    for (int i = 0; i < GPF; ++i) {
+    if (g0 + i >= ng) break;
+    const GemmLd cur = ring[i];
+    ring[i] = load(min(g0 + i + GPF, ng - 1));
     const v4i b0 = pf_unpack(cur.w0), b1 = pf_unpack(cur.w1);
     const v16i h0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.ah, b0, zero, 0, 0, 0);
     const v16i l0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.al, b0, zero, 0, 0, 0);
@@ -234,9 +248,8 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
       acc0[v] = __builtin_fmaf((float)(h0[v] * 256 + l0[v]), cur.c0, acc0[v]);
       acc1[v] = __builtin_fmaf((float)(h1[v] * 256 + l1[v]), cur.c1, acc1[v]);
     }
-    cur = nxt;
   }
-  // epilogue: value v is token T0 + 8(v/4) + 4hh + v%4, rows ra / rb
+  // epilogue: value v is token T0 + 8(v/4) + 4hh + v%4, rows r0 / r1
   const int r0 = R + j, r1 = R + G.off1 + j;
   const bool in0 = r0 < G.rows, in1 = r1 < G.rows;
 #pragma unroll
@@ -321,25 +334,43 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ void load8(const PfArgs &A, size_t off, float (&v)[8]) {
-  if (A.kv_fp16) {
-    const uint4 u = *reinterpret_cast<const uint4 *>(reinterpret_cast<const __half *>(A.kv) + off);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+// Eight consecutive cache values as loaded (f16: one 16-byte load, f32: two),
+// widened to f32 when staged.
+struct Raw8 {
+  uint4 a, b;
+};
+template <bool F32>
+__device__ __forceinline__ Raw8 load8(const PfArgs &A, size_t off) {
+  Raw8 r;
+  if (F32) {
+    r.a = *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(A.kv) + off);
+    r.b = *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(A.kv) + off + 4);
+  } else {
+    r.a = *reinterpret_cast<const uint4 *>(reinterpret_cast<const __half *>(A.kv) + off);
+    r.b = make_uint4(0u, 0u, 0u, 0u);
+  }
+  return r;
+}
+template <bool F32>
+__device__ __forceinline__ void widen8(const Raw8 &r, float (&v)[8]) {
+  if (F32) {
+    const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w[i]);
+  } else {
+    const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const __half2 h = *reinterpret_cast<const __half2 *>(&w[i]);
       v[2 * i] = __low2float(h);
       v[2 * i + 1] = __high2float(h);
     }
-  } else {
-    const float4 a = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(A.kv) + off);
-    const float4 b = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(A.kv) + off + 4);
-    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
   }
 }
+constexpr int SCH = 4;  // staged 8-value chunks per thread and block (KBL * 8 chunks, >= 64 threads)
 
 template <bool SPLIT_KV>
-__global__ __launch_bounds__(1024) void k_pf_attn(PfArgs A, int li, int n, int pos0) {
+__global__ __launch_bounds__(256) void k_pf_attn(PfArgs A, int li, int n, int pos0) {
   __shared__ __attribute__((aligned(16))) _Float16 Kh[KBL * KROW], Kl[SPLIT_KV ? KBL * KROW : 8];
   __shared__ __attribute__((aligned(16))) _Float16 Vh[PF_HD * VROW], Vl[SPLIT_KV ? PF_HD * VROW : 8];
   const int rep = A.NH / A.NKV;
@@ -368,19 +399,32 @@ __global__ __launch_bounds__(1024) void k_pf_attn(PfArgs A, int li, int n, int p
   v16f o0, o1;
 #pragma unroll
   for (int v = 0; v < 16; ++v) o0[v] = o1[v] = 0.f;
+  // the block's chunks c = tid + i * blockDim (key c / 8, dimensions 8 (c % 8)
+  // .. +7), loaded one block ahead of their use
+  Raw8 rk[SCH], rv[SCH];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < SCH; ++i) {
+      const int c = tid() + i * (int)blockDim.x, kk = c >> 3, d0 = (c & 7) * 8;
+      if (c < KBL * 8 && k0 + kk <= qlast) {
+        rk[i] = load8<SPLIT_KV>(A, kbase + (size_t)(k0 + kk) * PF_HD + d0);
+        rv[i] = load8<SPLIT_KV>(A, vbase + (size_t)(k0 + kk) * PF_HD + d0);
+      } else {
+        rk[i].a = rk[i].b = rv[i].a = rv[i].b = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+  fetch(0);
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * KBL;
     __syncthreads();  // the previous block is consumed
-    for (int c = tid(); c < KBL * 8; c += blockDim.x) {
-      const int kk = c >> 3, d0 = (c & 7) * 8;
-      float kv[8], vv[8];
-      if (k0 + kk <= qlast) {
-        load8(A, kbase + (size_t)(k0 + kk) * PF_HD + d0, kv);
-        load8(A, vbase + (size_t)(k0 + kk) * PF_HD + d0, vv);
-      } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) kv[i] = vv[i] = 0.f;
-      }
+    for (int ci = 0; ci < SCH; ++ci) {
+      const int c = tid() + ci * (int)blockDim.x, kk = c >> 3, d0 = (c & 7) * 8;
+      if (c >= KBL * 8) break;
+      float kv[8], vv[8];
+      widen8<SPLIT_KV>(rk[ci], kv);
+      widen8<SPLIT_KV>(rv[ci], vv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const _Float16 kh = (_Float16)kv[i], vh = (_Float16)vv[i];
@@ -392,6 +436,7 @@ __global__ __launch_bounds__(1024) void k_pf_attn(PfArgs A, int li, int n, int p
         }
       }
     }
+    if (kb + 1 < nkb) fetch(k0 + KBL);
     __syncthreads();
     v16f s;
 #pragma unroll
@@ -474,6 +519,24 @@ __global__ __launch_bounds__(1024) void k_pf_attn(PfArgs A, int li, int n, int p
   }
 }
 
+// ---------------------------------------------------------------- weight tiling
+// The prefill GEMMs read a tiled copy of each Q4 matrix: for row tile rt
+// (rows 32 rt .. 32 rt + 31) and group g, the 64 lanes' 8-byte weight
+// operands in lane order (lane 32 hh + j: bytes 8hh .. 8hh+7 of the group in
+// row 32 rt + j), then separately the 32 rows' scales.
+__global__ __launch_bounds__(WG) void k_pf_tile(PfMat W, uint8_t *q, float *s) {
+  const int ng = W.cols >> 5;
+  const size_t units = (size_t)(W.rows >> 5) * ng * 64;  // (row tile, group, lane)
+  for (size_t u = (size_t)blockIdx.x * WG + tid(); u < units; u += (size_t)gridDim.x * WG) {
+    const int lane = (int)(u & 63), j = lane & 31, hh = lane >> 5;
+    const size_t tg = u >> 6;  // rt * ng + g
+    const int g = (int)(tg % ng), r = (int)(tg / ng) * 32 + j;
+    const uint8_t *src = W.q + (size_t)r * ng * 16 + 16 * g + 8 * hh;
+    *reinterpret_cast<uint2 *>(q + u * 8) = *reinterpret_cast<const uint2 *>(src);
+    if (hh == 0) s[tg * 32 + j] = W.s[(size_t)r * ng + g];
+  }
+}
+
 // ---------------------------------------------------------------- host
 template <int NORM>
 void launch_quant(const PfArgs &A, const float *src, int K, const float *g, int n, hipStream_t s) {
@@ -503,11 +566,33 @@ PfGemm gemm_same(const PfMat &W, int n, const float *bias, float *out, int ldo) 
 
 }  // namespace
 
+size_t pf_tiled_bytes(const PfMat &W) {
+  const size_t packed = ((size_t)W.rows * W.cols / 2 + 255) & ~(size_t)255;
+  return (packed + (size_t)W.rows * (W.cols / 32) * sizeof(float) + 255) & ~(size_t)255;
+}
+
+int pf_tile(const PfMat &W, void *dst, PfMat *out, hipStream_t s) {
+  MLLM_CHECK(W.rows % 32 == 0 && W.cols % 32 == 0, "matrix %d x %d cannot be tiled", W.rows, W.cols);
+  uint8_t *q = static_cast<uint8_t *>(dst);
+  float *sc = reinterpret_cast<float *>(q + (((size_t)W.rows * W.cols / 2 + 255) & ~(size_t)255));
+  const size_t units = (size_t)(W.rows / 32) * (W.cols / 32) * 64;
+  const int blocks = (int)std::min<size_t>((units + WG - 1) / WG, 4096);
+  hipLaunchKernelGGL(k_pf_tile, dim3(blocks), dim3(WG), 0, s, W, q, sc);
+  MLLM_HIP(hipGetLastError());
+  *out = PfMat{q, sc, W.rows, W.cols};
+  return 0;
+}
+
+bool pf_supported(const PfArgs &A) {
+  return A.D == A.NH * PF_HD && A.NH % A.NKV == 0 && A.NH / A.NKV <= 4 && A.FF % 64 == 0 && A.D <= 8192 &&
+         A.FF <= 8192;
+}
+
 size_t pf_buffer_bytes(const PfArgs &A, int tc) {
   const size_t kmax = (size_t)(A.D > A.FF ? A.D : A.FF);
   auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
   return al(sizeof(int32_t) * tc) + 3 * al(sizeof(float) * tc * A.D) + al(sizeof(float) * tc * A.FF) +
-         al(sizeof(float) * tc) + al((size_t)tc * (kmax / 32) * PX_GROUP);
+         al(sizeof(float) * tc) + al((size_t)((tc + 31) / 32) * (kmax / 32) * PX_TILE);
 }
 
 void pf_carve(PfArgs &A, void *base, int tc) {
@@ -534,9 +619,8 @@ int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, hipStream_t 
   if (n <= 0) return 0;
   MLLM_CHECK(n <= A.tc && pos0 >= 0 && pos0 + n <= A.max_seq, "prefill chunk of %d tokens at %d out of range", n,
              pos0);
-  MLLM_CHECK(A.D == A.NH * PF_HD && A.NH % A.NKV == 0 && A.NH / A.NKV <= 16 && A.FF % 64 == 0 && A.D <= 8192 &&
-                 A.FF <= 8192,
-             "prefill shapes unsupported (d_model %d, d_ff %d)", A.D, A.FF);
+  MLLM_CHECK(pf_supported(A), "prefill shapes unsupported (d_model %d, d_ff %d, %d heads, %d KV heads)", A.D, A.FF,
+             A.NH, A.NKV);
   MLLM_HIP(hipMemcpyAsync(A.ids, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, s));
   const bool gpt2 = A.arch == 1;
   hipLaunchKernelGGL(k_pf_embed, dim3(n), dim3(WG), 0, s, A, n, pos0);
