@@ -326,9 +326,7 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
 // terms are below 2^-40 relative.  The scores are formed in the log2 domain
 // (the query scaled by attn_scale * log2 e) for v_exp_f32.
 constexpr int QTL = 32;   // queries per wave
-constexpr int KBL = 32;   // keys per block
 constexpr int KROW = 72;  // halves per staged key row (64 + pad)
-constexpr int VROW = 40;  // halves per staged value column (32 keys + pad)
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
@@ -367,16 +365,27 @@ __device__ __forceinline__ void widen8(const Raw8 &r, float (&v)[8]) {
     }
   }
 }
-constexpr int SCH = 4;  // staged 8-value chunks per thread and block (KBL * 8 chunks, >= 64 threads)
+constexpr int SCH = 4;   // staged 8-value chunks per thread and super-block (64 keys x 8 chunks, >= 128 threads)
+constexpr int KSB = 64;  // keys per super-block: two 32-key blocks, one per wave set
+constexpr int VROW2 = 68;  // halves per staged value column (64 keys + pad)
 
+// The tile's key blocks alternate between two sets of waves (block 2i to set
+// 0, 2i + 1 to set 1; a wave per query head in each set), so two waves share
+// each SIMD; set 1's running (max, sum, output) is merged into set 0's at the
+// end through LDS.
 template <bool SPLIT_KV>
-__global__ __launch_bounds__(256) void k_pf_attn(PfArgs A, int li, int n, int pos0) {
-  __shared__ __attribute__((aligned(16))) _Float16 Kh[KBL * KROW], Kl[SPLIT_KV ? KBL * KROW : 8];
-  __shared__ __attribute__((aligned(16))) _Float16 Vh[PF_HD * VROW], Vl[SPLIT_KV ? PF_HD * VROW : 8];
+__global__ __launch_bounds__(512) void k_pf_attn(PfArgs A, int li, int n, int pos0) {
+  constexpr int KB_BYTES = KSB * KROW * 2, VB_BYTES = PF_HD * VROW2 * 2;
+  constexpr int STAGE = (SPLIT_KV ? 2 : 1) * (KB_BYTES + VB_BYTES);
+  constexpr int MERGE = 4 * 64 * 34 * 4;  // up to 4 heads x 64 lanes x (32 outputs, max, sum)
+  __shared__ __attribute__((aligned(16))) uint8_t smem[STAGE > MERGE ? STAGE : MERGE];
+  _Float16 *Kh = reinterpret_cast<_Float16 *>(smem), *Vh = Kh + KSB * KROW;
+  _Float16 *Kl = Vh + PF_HD * VROW2, *Vl = Kl + KSB * KROW;  // SPLIT_KV only
   const int rep = A.NH / A.NKV;
   const int T0 = (gridDim.x - 1 - blockIdx.x) * QTL, kvh = blockIdx.y;  // the longest tiles first
   const int lane = tid() & 63, j = lane & 31, hh = lane >> 5;
-  const int hq = kvh * rep + (tid() >> 6);
+  const int wv = tid() >> 6, set = wv / rep, hsel = wv - set * rep;
+  const int hq = kvh * rep + hsel;
   v8h qh[4], ql[4];
   {
     const float c = A.attn_scale * 1.4426950408889634f;
@@ -393,20 +402,20 @@ __global__ __launch_bounds__(256) void k_pf_attn(PfArgs A, int li, int n, int po
   }
   const int qpos = pos0 + T0 + j;
   const int qlast = pos0 + min(T0 + QTL, n) - 1;  // last key any query of the tile sees
-  const int nkb = qlast / KBL + 1;
+  const int nsb = qlast / KSB + 1;
   const size_t kbase = pf_kv_index(A, li, 0, kvh, 0), vbase = pf_kv_index(A, li, 1, kvh, 0);
   float m_run = -INFINITY, l_run = 0.f;
   v16f o0, o1;
 #pragma unroll
   for (int v = 0; v < 16; ++v) o0[v] = o1[v] = 0.f;
-  // the block's chunks c = tid + i * blockDim (key c / 8, dimensions 8 (c % 8)
-  // .. +7), loaded one block ahead of their use
+  // chunks c = tid + i * blockDim (key c / 8 of the super-block, dimensions
+  // 8 (c % 8) .. +7), loaded one super-block ahead of their use
   Raw8 rk[SCH], rv[SCH];
   auto fetch = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < SCH; ++i) {
       const int c = tid() + i * (int)blockDim.x, kk = c >> 3, d0 = (c & 7) * 8;
-      if (c < KBL * 8 && k0 + kk <= qlast) {
+      if (c < KSB * 8 && k0 + kk <= qlast) {
         rk[i] = load8<SPLIT_KV>(A, kbase + (size_t)(k0 + kk) * PF_HD + d0);
         rv[i] = load8<SPLIT_KV>(A, vbase + (size_t)(k0 + kk) * PF_HD + d0);
       } else {
@@ -415,39 +424,47 @@ __global__ __launch_bounds__(256) void k_pf_attn(PfArgs A, int li, int n, int po
     }
   };
   fetch(0);
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int k0 = kb * KBL;
-    __syncthreads();  // the previous block is consumed
+  for (int sb = 0; sb < nsb; ++sb) {
+    __syncthreads();  // the previous super-block is consumed
 #pragma unroll
     for (int ci = 0; ci < SCH; ++ci) {
       const int c = tid() + ci * (int)blockDim.x, kk = c >> 3, d0 = (c & 7) * 8;
-      if (c >= KBL * 8) break;
-      float kv[8], vv[8];
-      widen8<SPLIT_KV>(rk[ci], kv);
-      widen8<SPLIT_KV>(rv[ci], vv);
+      if (c >= KSB * 8) break;
+      if (SPLIT_KV) {
+        float kv[8], vv[8];
+        widen8<true>(rk[ci], kv);
+        widen8<true>(rv[ci], vv);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const _Float16 kh = (_Float16)kv[i], vh = (_Float16)vv[i];
-        Kh[kk * KROW + d0 + i] = kh;
-        Vh[(d0 + i) * VROW + kk] = vh;
-        if (SPLIT_KV) {
+        for (int i = 0; i < 8; ++i) {
+          const _Float16 kh = (_Float16)kv[i], vh = (_Float16)vv[i];
+          Kh[kk * KROW + d0 + i] = kh;
+          Vh[(d0 + i) * VROW2 + kk] = vh;
           Kl[kk * KROW + d0 + i] = (_Float16)(kv[i] - (float)kh);
-          Vl[(d0 + i) * VROW + kk] = (_Float16)(vv[i] - (float)vh);
+          Vl[(d0 + i) * VROW2 + kk] = (_Float16)(vv[i] - (float)vh);
         }
+      } else {  // an f16 cache is staged as is
+        *reinterpret_cast<uint4 *>(Kh + kk * KROW + d0) = rk[ci].a;
+        const uint32_t w[4] = {rv[ci].a.x, rv[ci].a.y, rv[ci].a.z, rv[ci].a.w};
+        unsigned short *vt = reinterpret_cast<unsigned short *>(Vh);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vt[(d0 + i) * VROW2 + kk] = (unsigned short)(w[i >> 1] >> (16 * (i & 1)));
       }
     }
-    if (kb + 1 < nkb) fetch(k0 + KBL);
+    if (sb + 1 < nsb) fetch((sb + 1) * KSB);
     __syncthreads();
+    const int k0 = sb * KSB + 32 * set;  // this set's block
+    if (k0 > qlast) continue;            // past every query of the tile (uniform)
+    const int kr = 32 * set;             // its rows / columns in the staged super-block
     v16f s;
 #pragma unroll
     for (int v = 0; v < 16; ++v) s[v] = 0.f;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      const v8h ka = *reinterpret_cast<const v8h *>(Kh + j * KROW + 16 * m + 8 * hh);
+      const v8h ka = *reinterpret_cast<const v8h *>(Kh + (kr + j) * KROW + 16 * m + 8 * hh);
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[m], s, 0, 0, 0);
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[m], s, 0, 0, 0);
       if (SPLIT_KV) {
-        const v8h kl = *reinterpret_cast<const v8h *>(Kl + j * KROW + 16 * m + 8 * hh);
+        const v8h kl = *reinterpret_cast<const v8h *>(Kl + (kr + j) * KROW + 16 * m + 8 * hh);
         s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[m], s, 0, 0, 0);
       }
     }
@@ -458,13 +475,15 @@ __global__ __launch_bounds__(256) void k_pf_attn(PfArgs A, int li, int n, int po
       mx = fmaxf(mx, s[v]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mn = fmaxf(m_run, mx);  // finite: block 0 holds key 0 for every query
-    const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+    const float mn = fmaxf(m_run, mx);
+    // a query with no key yet in this set: everything stays zero
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mref);
     v8h ph[2], pl[2];
     float ps = 0.f;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const float p = __builtin_amdgcn_exp2f(s[v] - mn);
+      const float p = __builtin_amdgcn_exp2f(s[v] - mref);
       ps += p;
       const _Float16 h = (_Float16)p;
       ph[v >> 3][v & 7] = h;
@@ -480,41 +499,58 @@ __global__ __launch_bounds__(256) void k_pf_attn(PfArgs A, int li, int n, int po
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int kc = 16 * u + 4 * hh;
-      v8h va, vb;
-      {
-        const v4h a0 = *reinterpret_cast<const v4h *>(Vh + j * VROW + kc);
-        const v4h a1 = *reinterpret_cast<const v4h *>(Vh + j * VROW + kc + 8);
-        const v4h b0 = *reinterpret_cast<const v4h *>(Vh + (32 + j) * VROW + kc);
-        const v4h b1 = *reinterpret_cast<const v4h *>(Vh + (32 + j) * VROW + kc + 8);
-        va = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
-        vb = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
+      const int kc = kr + 16 * u + 4 * hh;
+      const v4h a0 = *reinterpret_cast<const v4h *>(Vh + j * VROW2 + kc);
+      const v4h a1 = *reinterpret_cast<const v4h *>(Vh + j * VROW2 + kc + 8);
+      const v4h b0 = *reinterpret_cast<const v4h *>(Vh + (32 + j) * VROW2 + kc);
+      const v4h b1 = *reinterpret_cast<const v4h *>(Vh + (32 + j) * VROW2 + kc + 8);
+      const v8h va = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+      const v8h vb = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
       o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph[u], o0, 0, 0, 0);
       o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl[u], o0, 0, 0, 0);
       o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb, ph[u], o1, 0, 0, 0);
       o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb, pl[u], o1, 0, 0, 0);
       if (SPLIT_KV) {
-        const v4h a0 = *reinterpret_cast<const v4h *>(Vl + j * VROW + kc);
-        const v4h a1 = *reinterpret_cast<const v4h *>(Vl + j * VROW + kc + 8);
-        const v4h b0 = *reinterpret_cast<const v4h *>(Vl + (32 + j) * VROW + kc);
-        const v4h b1 = *reinterpret_cast<const v4h *>(Vl + (32 + j) * VROW + kc + 8);
-        o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7), ph[u], o0,
+        const v4h c0 = *reinterpret_cast<const v4h *>(Vl + j * VROW2 + kc);
+        const v4h c1 = *reinterpret_cast<const v4h *>(Vl + j * VROW2 + kc + 8);
+        const v4h d0 = *reinterpret_cast<const v4h *>(Vl + (32 + j) * VROW2 + kc);
+        const v4h d1 = *reinterpret_cast<const v4h *>(Vl + (32 + j) * VROW2 + kc + 8);
+        o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_shufflevector(c0, c1, 0, 1, 2, 3, 4, 5, 6, 7), ph[u], o0,
                                                     0, 0, 0);
-        o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7), ph[u], o1,
+        o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_shufflevector(d0, d1, 0, 1, 2, 3, 4, 5, 6, 7), ph[u], o1,
                                                     0, 0, 0);
       }
     }
   }
-  // lane (query j, half hh): dimensions 8g + 4hh .. +3 (o0), 32 + the same (o1)
-  if (T0 + j < n) {
+  // merge: set 1 hands (outputs, max, sum) to set 0 through LDS
+  float *mrg = reinterpret_cast<float *>(smem) + (size_t)(hsel * 64 + lane) * 34;
+  __syncthreads();  // the staging area is free
+  if (set == 1) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      mrg[v] = o0[v];
+      mrg[16 + v] = o1[v];
+    }
+    mrg[32] = m_run;
+    mrg[33] = l_run;
+  }
+  __syncthreads();
+  if (set == 0 && T0 + j < n) {
+    const float m1 = mrg[32], l1 = mrg[33];
+    const float M = fmaxf(m_run, m1);  // finite: set 0 holds key 0
+    const float a0 = __builtin_amdgcn_exp2f(m_run - M), a1 = __builtin_amdgcn_exp2f(m1 - M);
+    const float l = l_run * a0 + l1 * a1;
     float *out = A.att + (size_t)(T0 + j) * A.D + hq * PF_HD + 4 * hh;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      *reinterpret_cast<float4 *>(out + 8 * g) =
-          make_float4(o0[4 * g] / l_run, o0[4 * g + 1] / l_run, o0[4 * g + 2] / l_run, o0[4 * g + 3] / l_run);
-      *reinterpret_cast<float4 *>(out + 32 + 8 * g) =
-          make_float4(o1[4 * g] / l_run, o1[4 * g + 1] / l_run, o1[4 * g + 2] / l_run, o1[4 * g + 3] / l_run);
+      float r[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        r[e] = (o0[4 * g + e] * a0 + mrg[4 * g + e] * a1) / l;
+        r[4 + e] = (o1[4 * g + e] * a0 + mrg[16 + 4 * g + e] * a1) / l;
+      }
+      *reinterpret_cast<float4 *>(out + 8 * g) = make_float4(r[0], r[1], r[2], r[3]);
+      *reinterpret_cast<float4 *>(out + 32 + 8 * g) = make_float4(r[4], r[5], r[6], r[7]);
     }
   }
 }
@@ -637,9 +673,9 @@ int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, hipStream_t 
     launch_gemm<EPI_QKV>(A, G, s);
     if (li == A.L - 1) break;  // the last layer's K and V are all the cache needs
     if (A.kv_fp16)
-      hipLaunchKernelGGL(k_pf_attn<false>, dim3(nqt, A.NKV), dim3(64 * rep), 0, s, A, li, n, pos0);
+      hipLaunchKernelGGL(k_pf_attn<false>, dim3(nqt, A.NKV), dim3(128 * rep), 0, s, A, li, n, pos0);
     else
-      hipLaunchKernelGGL(k_pf_attn<true>, dim3(nqt, A.NKV), dim3(64 * rep), 0, s, A, li, n, pos0);
+      hipLaunchKernelGGL(k_pf_attn<true>, dim3(nqt, A.NKV), dim3(128 * rep), 0, s, A, li, n, pos0);
     launch_quant<NORM_NONE>(A, A.att, A.D, nullptr, n, s);
     launch_gemm<EPI_RESID>(A, gemm_same(W.proj, n, gpt2 ? W.proj_b : nullptr, A.x, A.D), s);
     if (gpt2)
