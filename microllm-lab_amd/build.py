@@ -33,6 +33,9 @@ NAPI_SRC = os.path.join(PKG, "js", "napi", "mllm_napi.cc")
 NAPI_OUT = os.path.join(PKG, "js", "mllm_napi.node")
 
 HIP_SOURCES = ["mllm_ops.hip", "mllm_engine.hip", "mllm_prefill.hip"]
+# per-source flags: the prefill kernels consume their matrix-core results in
+# VALU epilogues, so the results go to VGPRs (no AGPR-to-VGPR copies)
+EXTRA_FLAGS = {"mllm_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("MLLM_OFFLOAD_ARCH", "gfx950")
 HIP_FLAGS = [
@@ -75,7 +78,8 @@ def build_lib(verbose: bool = False) -> str:
 
     def compile_one(src):
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-        lines = _run([HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", os.path.join(CSRC, src),
+        lines = _run([HIPCC, *HIP_FLAGS, *EXTRA_FLAGS.get(src, []), "-Rpass-analysis=kernel-resource-usage", "-c",
+                      os.path.join(CSRC, src),
                       "-o", obj])
         return obj, _resource_usage(lines)
 

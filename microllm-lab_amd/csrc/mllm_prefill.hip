@@ -165,7 +165,10 @@ __global__ __launch_bounds__(WG) void k_pf_quant(const float *src, int K, const 
 // A wave computes two 32-row sub-tiles (sub-tile 1 is either the next 32
 // rows of the same matrix -- a 64-row head of attn.qkv, 64 rows of the
 // others -- or the same rows of a second matrix: mlp.w3 beside mlp.w1) for
-// 32 tokens.  Workgroup: 4 waves on consecutive row ranges, one token tile.
+// 32 tokens.  Workgroup: 4 waves, one token tile; with KS > 1, KS waves
+// share a row range and take consecutive slices of the groups, and their
+// sums are added in slice order through LDS (deterministic) before the
+// epilogue -- more waves for the GEMMs with few row ranges.
 struct PfGemm {
   const uint8_t *q0, *q1;
   const float *s0, *s1;
@@ -200,13 +203,15 @@ struct GemmLd {
   v4i ah, al;
 };
 
-template <int EPI>
+template <int EPI, int KS>
 __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
+  __shared__ float red[KS > 1 ? WG * 32 : 1];
   const int wv = tid() >> 6, lane = tid() & 63, j = lane & 31, hh = lane >> 5;
-  const int R = (blockIdx.x * (WG / 64) + wv) * G.rstep;
-  if (R >= G.rows) return;  // no barriers below
+  const int ks = wv % KS;
+  const int R = (blockIdx.x * (WG / 64 / KS) + wv / KS) * G.rstep;
+  const bool active = R < G.rows;
   const int T0 = blockIdx.y * 32;
-  const int ng = G.ng;
+  const int ng = G.ng, gb = ng * ks / KS, ge = ng * (ks + 1) / KS;  // this wave's groups
   // tiled operands (every row tile and token tile whole): per group, the
   // wave's weights are 512 contiguous bytes, its scales 128, its
   // activations 2 x 1024
@@ -230,14 +235,17 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
   const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   // the loads of group g + GPF go out before group g is computed
   GemmLd ring[GPF];
+  if (active) {
+  // (groups past ge are loaded and not used: the tiled matrices and the
+  // planes carry GPF groups of padding)
 #pragma unroll
-  for (int i = 0; i < GPF; ++i) ring[i] = load(min(i, ng - 1));
-  for (int g0 = 0; g0 < ng; g0 += GPF)
+  for (int i = 0; i < GPF; ++i) ring[i] = load(gb + i);
+  for (int g0 = gb; g0 < ge; g0 += GPF)
 #pragma unroll
     for (int i = 0; i < GPF; ++i) {
-    if (g0 + i >= ng) break;
+    if (g0 + i >= ge) break;
     const GemmLd cur = ring[i];
-    ring[i] = load(min(g0 + i + GPF, ng - 1));
+    ring[i] = load(g0 + i + GPF);
     const v4i b0 = pf_unpack(cur.w0), b1 = pf_unpack(cur.w1);
     const v16i h0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.ah, b0, zero, 0, 0, 0);
     const v16i l0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.al, b0, zero, 0, 0, 0);
@@ -249,6 +257,29 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
       acc1[v] = __builtin_fmaf((float)(h1[v] * 256 + l1[v]), cur.c1, acc1[v]);
     }
   }
+  }
+  if (KS > 1) {
+    float *mine = red + (size_t)tid() * 32;
+    if (ks > 0) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        mine[v] = acc0[v];
+        mine[16 + v] = acc1[v];
+      }
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int k = 1; k < KS; ++k) {
+      const float *o = mine + (size_t)k * 64 * 32;  // the same lane of slice k's wave
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        acc0[v] = acc0[v] + o[v];
+        acc1[v] = acc1[v] + o[16 + v];
+      }
+    }
+  }
+  if (!active) return;
   // epilogue: value v is token T0 + 8(v/4) + 4hh + v%4, rows r0 / r1
   const int r0 = R + j, r1 = R + G.off1 + j;
   const bool in0 = r0 < G.rows, in1 = r1 < G.rows;
@@ -579,10 +610,18 @@ void launch_quant(const PfArgs &A, const float *src, int K, const float *g, int 
   hipLaunchKernelGGL(k_pf_quant<NORM>, dim3(n), dim3(WG), (size_t)K * sizeof(float), s, src, K, g, A.eps, A.px, A.sx);
 }
 
+// Group slices per row range: the fewest (1, 2 or 4) that give at least
+// 2048 waves (two per SIMD on 256 CUs), keeping >= 8 groups per slice.
 template <int EPI>
 void launch_gemm(const PfArgs &A, const PfGemm &G, hipStream_t s) {
-  const int per_wg = (WG / 64) * G.rstep;
-  hipLaunchKernelGGL(k_pf_gemm<EPI>, dim3((G.rows + per_wg - 1) / per_wg, (G.n + 31) / 32), dim3(WG), 0, s, A, G);
+  const int tt = (G.n + 31) / 32, rw = (G.rows + G.rstep - 1) / G.rstep;
+  int ks = 1;
+  while (ks < 4 && rw * tt * ks < 2048 && G.ng / (2 * ks) >= 8) ks *= 2;
+  const int per_wg = (WG / 64 / ks) * G.rstep;
+  const dim3 grid((G.rows + per_wg - 1) / per_wg, tt);
+  if (ks == 1) hipLaunchKernelGGL((k_pf_gemm<EPI, 1>), grid, dim3(WG), 0, s, A, G);
+  if (ks == 2) hipLaunchKernelGGL((k_pf_gemm<EPI, 2>), grid, dim3(WG), 0, s, A, G);
+  if (ks == 4) hipLaunchKernelGGL((k_pf_gemm<EPI, 4>), grid, dim3(WG), 0, s, A, G);
 }
 
 PfGemm gemm_same(const PfMat &W, int n, const float *bias, float *out, int ldo) {
@@ -603,8 +642,9 @@ PfGemm gemm_same(const PfMat &W, int n, const float *bias, float *out, int ldo) 
 }  // namespace
 
 size_t pf_tiled_bytes(const PfMat &W) {
+  // + GPF groups of padding after the scales (read ahead, never used)
   const size_t packed = ((size_t)W.rows * W.cols / 2 + 255) & ~(size_t)255;
-  return (packed + (size_t)W.rows * (W.cols / 32) * sizeof(float) + 255) & ~(size_t)255;
+  return (packed + (size_t)W.rows * (W.cols / 32) * sizeof(float) + GPF * 512 + 255) & ~(size_t)255;
 }
 
 int pf_tile(const PfMat &W, void *dst, PfMat *out, hipStream_t s) {
@@ -628,7 +668,7 @@ size_t pf_buffer_bytes(const PfArgs &A, int tc) {
   const size_t kmax = (size_t)(A.D > A.FF ? A.D : A.FF);
   auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
   return al(sizeof(int32_t) * tc) + 3 * al(sizeof(float) * tc * A.D) + al(sizeof(float) * tc * A.FF) +
-         al(sizeof(float) * tc) + al((size_t)((tc + 31) / 32) * (kmax / 32) * PX_TILE);
+         al(sizeof(float) * tc) + al((size_t)(((tc + 31) / 32) * (kmax / 32) + GPF) * PX_TILE);
 }
 
 void pf_carve(PfArgs &A, void *base, int tc) {
