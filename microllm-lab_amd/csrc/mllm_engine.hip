@@ -2194,6 +2194,9 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
     A.rope_cos = P.rope_cos;
     A.rope_sin = P.rope_sin;
     A.kv = P.kv;
+    A.norm_f = P.norm_f;
+    A.logits = M->d_logits;
+    A.res = &M->d_st->res[0];
     M->pf_layer.resize(L);
     for (int i = 0; i < L; ++i) {
       const LayerW &w = M->layers[i];
@@ -2350,12 +2353,14 @@ extern "C" int mllm_forward_prompt(mllm_model *M, const int32_t *ids, int n, flo
   MLLM_CHECK(n > 0 && n <= M->cfg.max_seq_len, "prompt length %d out of range", n);
   if (int rc = check_ids(M, ids, n)) return rc;
   if (M->pf_min > 0 && n >= M->pf_min) {
-    // tokens 0 .. n-2 write their K and V in chunks; the last one is a
-    // decode step, which forms the logits
+    // the prompt in chunks; the last one also forms the logits
     MLLM_HIP(hipEventRecord(M->ev_pf, M->stream));
-    for (int p0 = 0; p0 < n - 1; p0 += M->pf.tc)
-      if (int rc = pf_layers(M->pf, ids + p0, std::min(M->pf.tc, n - 1 - p0), p0, M->stream)) return rc;
-    if (int rc = run_pass(M, ids + n - 1, 1, n - 1, 1)) return rc;
+    for (int p0 = 0; p0 < n; p0 += M->pf.tc) {
+      const int m = std::min(M->pf.tc, n - p0);
+      if (int rc = pf_layers(M->pf, ids + p0, m, p0, p0 + m == n, M->stream)) return rc;
+    }
+    MLLM_HIP(hipEventRecord(M->ev1, M->stream));
+    MLLM_HIP(hipStreamSynchronize(M->stream));
     MLLM_HIP(hipEventElapsedTime(&M->last_ms, M->ev_pf, M->ev1));
     M->last_tokens = n;
     M->cache_len = n;

@@ -32,7 +32,10 @@ struct PfArgs {
   const PfLayer *layers;  // host array of L layers
   PfMat emb;              // tied lm_head: the embedding rows
   const float *wpe, *sf, *rope_cos, *rope_sin;
+  const float *norm_f;    // final norm gains (gpt2: ln_f gamma || beta)
   void *kv;               // [L][2][NKV][max_seq][64], f32 or f16
+  float *logits;          // [V] the last token's logits
+  int *res;               // its argmax
   // work buffers for up to tc tokens
   int tc;
   int32_t *ids;  // [tc]
@@ -53,7 +56,7 @@ size_t pf_tiled_bytes(const PfMat &W);
 int pf_tile(const PfMat &W, void *dst, PfMat *out, hipStream_t stream);
 
 // Shapes the kernels take: head_dim 64, at most 4 query heads per KV head,
-// d_model and d_ff multiples of 64 up to 8192.
+// d_model and d_ff multiples of 64 up to 4096.
 bool pf_supported(const PfArgs &A);
 
 // Bytes of work buffers for tc tokens (one allocation, carved by pf_carve).
@@ -61,9 +64,11 @@ size_t pf_buffer_bytes(const PfArgs &A, int tc);
 void pf_carve(PfArgs &A, void *base, int tc);
 
 // Tokens ids[0 .. n) at positions pos0 .. pos0 + n (n <= tc, pos0 + n <=
-// max_seq) through every layer: their K and V are written to the cache.  The
-// residual stream after the last layer is not formed (nothing reads it).
-// Returns 0 or an MLLM_ERR_* code with the message set.
-int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, hipStream_t stream);
+// max_seq) through every layer: their K and V are written to the cache.
+// With `last` (the chunk ends the prompt) the last token's logits and argmax
+// are formed as well (the last layer's attention and MLP for its 32-token
+// tile, the final norm, the lm_head); otherwise the last layer stops after
+// its K and V.  Returns 0 or an MLLM_ERR_* code with the message set.
+int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, bool last, hipStream_t stream);
 
 }  // namespace mllm

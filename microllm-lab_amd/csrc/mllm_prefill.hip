@@ -89,76 +89,209 @@ __global__ __launch_bounds__(WG) void k_pf_embed(PfArgs A, int n, int pos0) {
 }
 
 // ---------------------------------------------------------------- norm + quantise
-// One token row of K floats per workgroup: optional RMSNorm / LayerNorm
-// (the decode engine's formulas), then the 16-bit planes and the scale.
+// One token row of K floats per wave (tokens t0 .. t1-1): optional RMSNorm /
+// LayerNorm (the decode engine's formulas), then the 16-bit planes and the
+// scale.  Wave reductions only; the row is re-read from cache per pass.
 template <int NORM>
-__global__ __launch_bounds__(WG) void k_pf_quant(const float *src, int K, const float *g, float eps, uint8_t *px,
-                                                 float *sx) {
-  extern __shared__ float ys[];  // K floats
-  __shared__ float red[WG / 64];
-  const int t = blockIdx.x, nq = K >> 2, ng = K >> 5;
-  const float4 *xr = reinterpret_cast<const float4 *>(src + (size_t)t * K);
-  float4 *y4 = reinterpret_cast<float4 *>(ys);
-  const float inv_k = 1.0f / (float)K;
-  float s1 = 0.f;
-  for (int q = tid(); q < nq; q += WG) {
-    const float4 v = xr[q];
-    y4[q] = v;
-    if (NORM == NORM_RMS) s1 += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
-    if (NORM == NORM_LN) s1 += (v.x + v.y) + (v.z + v.w);
-  }
+__device__ __forceinline__ float4 pf_norm_col(const float4 *xr, const float4 *g4, int nq, int q, float r, float mean) {
+  const float4 v = xr[q];
   if (NORM == NORM_RMS) {
-    const float r = __builtin_amdgcn_rsqf(block_sum<WG>(s1, red) * inv_k + eps);
-    const float4 *g4 = reinterpret_cast<const float4 *>(g);
-    for (int q = tid(); q < nq; q += WG) {
-      const float4 v = y4[q], w = g4[q];
-      y4[q] = make_float4(v.x * r * w.x, v.y * r * w.y, v.z * r * w.z, v.w * r * w.w);
+    const float4 w = g4[q];
+    return make_float4(v.x * r * w.x, v.y * r * w.y, v.z * r * w.z, v.w * r * w.w);
+  }
+  if (NORM == NORM_LN) {
+    const float4 w = g4[q], b = g4[nq + q];
+    const float4 d = make_float4(v.x - mean, v.y - mean, v.z - mean, v.w - mean);
+    return make_float4(__builtin_fmaf(d.x * r, w.x, b.x), __builtin_fmaf(d.y * r, w.y, b.y),
+                       __builtin_fmaf(d.z * r, w.z, b.z), __builtin_fmaf(d.w * r, w.w, b.w));
+  }
+  return v;
+}
+
+template <int NORM>
+__device__ __forceinline__ void pf_norm_stats(const float4 *xr, int K, float eps, float &r, float &mean) {
+  const int lane = tid() & 63, nq = K >> 2;
+  const float inv_k = 1.0f / (float)K;
+  r = 1.f;
+  mean = 0.f;
+  if (NORM == NORM_RMS) {
+    float s1 = 0.f;
+    for (int q = lane; q < nq; q += 64) {
+      const float4 v = xr[q];
+      s1 += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
     }
+    r = __builtin_amdgcn_rsqf(wave_sum(s1) * inv_k + eps);
   } else if (NORM == NORM_LN) {
-    const float mean = block_sum<WG>(s1, red) * inv_k;
+    float s1 = 0.f;
+    for (int q = lane; q < nq; q += 64) {
+      const float4 v = xr[q];
+      s1 += (v.x + v.y) + (v.z + v.w);
+    }
+    mean = wave_sum(s1) * inv_k;
     float s2 = 0.f;
-    for (int q = tid(); q < nq; q += WG) {
-      const float4 v = y4[q];
+    for (int q = lane; q < nq; q += 64) {
+      const float4 v = xr[q];
       const float4 d = make_float4(v.x - mean, v.y - mean, v.z - mean, v.w - mean);
       s2 += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
     }
-    const float r = __builtin_amdgcn_rsqf(block_sum<WG>(s2, red) * inv_k + 1e-5f);
-    const float4 *g4 = reinterpret_cast<const float4 *>(g);
-    for (int q = tid(); q < nq; q += WG) {
-      const float4 v = y4[q], w = g4[q], b = g4[nq + q];
-      const float4 d = make_float4(v.x - mean, v.y - mean, v.z - mean, v.w - mean);
-      y4[q] = make_float4(__builtin_fmaf(d.x * r, w.x, b.x), __builtin_fmaf(d.y * r, w.y, b.y),
-                          __builtin_fmaf(d.z * r, w.z, b.z), __builtin_fmaf(d.w * r, w.w, b.w));
+    r = __builtin_amdgcn_rsqf(wave_sum(s2) * inv_k + 1e-5f);
+  }
+}
+
+// Lane u of the wave owns (group u / 2, half u % 2) of the row -- 16
+// consecutive elements, PPL such units per lane (K <= 1024 PPL) -- held in
+// registers from one load, and writes the unit's hi and lo operands as two
+// 16-byte stores.
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) | ((uint32_t)d << 24);
+}
+
+template <int NORM, int PPL>
+__global__ __launch_bounds__(WG) void k_pf_quant(const float *src, int K, const float *g, float eps, uint8_t *px,
+                                                 float *sx, int t0, int t1) {
+  const int t = t0 + (int)blockIdx.x * (WG / 64) + (tid() >> 6);
+  if (t >= t1) return;  // no barriers below
+  const int lane = tid() & 63, nu = K >> 4, ng = K >> 5;
+  const float4 *xr = reinterpret_cast<const float4 *>(src + (size_t)t * K);
+  const float4 *g4 = reinterpret_cast<const float4 *>(g);
+  const float inv_k = 1.0f / (float)K;
+  float4 y[PPL][4];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) {
+    const int u = lane + 64 * i;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) y[i][c] = u < nu ? xr[4 * u + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (NORM == NORM_RMS) {
+    float s1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float4 v = y[i][c];
+        s1 += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+      }
+    const float r = __builtin_amdgcn_rsqf(wave_sum(s1) * inv_k + eps);
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+      const int u = lane + 64 * i;
+      if (u < nu)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float4 v = y[i][c], w = g4[4 * u + c];
+          y[i][c] = make_float4(v.x * r * w.x, v.y * r * w.y, v.z * r * w.z, v.w * r * w.w);
+        }
+    }
+  } else if (NORM == NORM_LN) {
+    float s1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) s1 += (y[i][c].x + y[i][c].y) + (y[i][c].z + y[i][c].w);
+    const float mean = wave_sum(s1) * inv_k;
+    float s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+      const int u = lane + 64 * i;
+      if (u < nu)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float4 d = make_float4(y[i][c].x - mean, y[i][c].y - mean, y[i][c].z - mean, y[i][c].w - mean);
+          s2 += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+        }
+    }
+    const float r = __builtin_amdgcn_rsqf(wave_sum(s2) * inv_k + 1e-5f);
+    const int nq = K >> 2;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+      const int u = lane + 64 * i;
+      if (u < nu)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float4 w = g4[4 * u + c], b = g4[nq + 4 * u + c];
+          const float4 d = make_float4(y[i][c].x - mean, y[i][c].y - mean, y[i][c].z - mean, y[i][c].w - mean);
+          y[i][c] = make_float4(__builtin_fmaf(d.x * r, w.x, b.x), __builtin_fmaf(d.y * r, w.y, b.y),
+                                __builtin_fmaf(d.z * r, w.z, b.z), __builtin_fmaf(d.w * r, w.w, b.w));
+        }
     }
   }
   float am = 0.f;
-  for (int q = tid(); q < nq; q += WG) {
-    const float4 v = y4[q];
-    am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-  }
-  am = block_max<WG>(am, red);  // its barriers also order the y4 stores above
+#pragma unroll
+  for (int i = 0; i < PPL; ++i)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4 v = y[i][c];
+      am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+  am = wave_max(am);
   const float inv = am > 0.f ? (float)PX_MAX / am : 0.f;
-  if (tid() == 0) sx[t] = am / (float)PX_MAX;
+  if (lane == 0) sx[t] = am / (float)PX_MAX;
   // token t is row j = t % 32 of token tile t / 32
   uint8_t *tile = px + (size_t)(t >> 5) * ng * PX_TILE + 16 * (t & 31);
-  for (int q = tid(); q < nq; q += WG) {
-    const float4 v = y4[q];
-    const int x0 = (int)__builtin_rintf(v.x * inv), x1 = (int)__builtin_rintf(v.y * inv);
-    const int x2 = (int)__builtin_rintf(v.z * inv), x3 = (int)__builtin_rintf(v.w * inv);
-    // signed split: lo = low byte sign-extended, hi = (x - lo) / 256
-    const int l0 = (int)(signed char)(x0 & 255), l1 = (int)(signed char)(x1 & 255);
-    const int l2 = (int)(signed char)(x2 & 255), l3 = (int)(signed char)(x3 & 255);
-    const int h0 = (x0 - l0) >> 8, h1 = (x1 - l1) >> 8, h2 = (x2 - l2) >> 8, h3 = (x3 - l3) >> 8;
-    // elements e0 .. e0+3 of group q/8: half e0/16; even elements at bytes
-    // p, p+1 of the half, odd ones at p+8, p+9
-    const int e0 = 4 * (q & 7), hh = e0 >> 4, kk = e0 & 15;
-    const int p = (kk >> 3) * 4 + ((kk & 7) >> 1);
-    uint8_t *rec = tile + (size_t)(q >> 3) * PX_TILE + 512 * hh;  // lane 32 hh + j of the hi plane
-    *reinterpret_cast<unsigned short *>(rec + p) = (unsigned short)((h0 & 255) | ((h2 & 255) << 8));
-    *reinterpret_cast<unsigned short *>(rec + 8 + p) = (unsigned short)((h1 & 255) | ((h3 & 255) << 8));
-    *reinterpret_cast<unsigned short *>(rec + 1024 + p) = (unsigned short)((l0 & 255) | ((l2 & 255) << 8));
-    *reinterpret_cast<unsigned short *>(rec + 1032 + p) = (unsigned short)((l1 & 255) | ((l3 & 255) << 8));
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) {
+    const int u = lane + 64 * i;
+    if (u >= nu) break;
+    int hi[16], lo[16];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float e[4] = {y[i][c].x, y[i][c].y, y[i][c].z, y[i][c].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int x = (int)__builtin_rintf(e[k] * inv);
+        // signed split: lo = low byte sign-extended, hi = (x - lo) / 256
+        const int l = (int)(signed char)(x & 255);
+        lo[4 * c + k] = l;
+        hi[4 * c + k] = (x - l) >> 8;
+      }
+    }
+    // operand order: elements 0 2 4 6 | 8 10 12 14 | 1 3 5 7 | 9 11 13 15
+    const uint4 h = make_uint4(pack4(hi[0], hi[2], hi[4], hi[6]), pack4(hi[8], hi[10], hi[12], hi[14]),
+                               pack4(hi[1], hi[3], hi[5], hi[7]), pack4(hi[9], hi[11], hi[13], hi[15]));
+    const uint4 l = make_uint4(pack4(lo[0], lo[2], lo[4], lo[6]), pack4(lo[8], lo[10], lo[12], lo[14]),
+                               pack4(lo[1], lo[3], lo[5], lo[7]), pack4(lo[9], lo[11], lo[13], lo[15]));
+    uint8_t *rec = tile + (size_t)(u >> 1) * PX_TILE + 512 * (u & 1);  // lane 32 hh + j of the hi plane
+    *reinterpret_cast<uint4 *>(rec) = h;
+    *reinterpret_cast<uint4 *>(rec + 1024) = l;
   }
+}
+
+// The final norm of token t's row (one wave) into xn.
+template <int NORM>
+__global__ __launch_bounds__(64) void k_pf_final(const float *x, int K, int t, const float *g, float eps, float *xn) {
+  const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)t * K);
+  float r, mean;
+  pf_norm_stats<NORM>(xr, K, eps, r, mean);
+  for (int q = tid(); q < (K >> 2); q += 64)
+    reinterpret_cast<float4 *>(xn)[q] = pf_norm_col<NORM>(xr, reinterpret_cast<const float4 *>(g), K >> 2, q, r, mean);
+}
+
+// Greedy argmax (infer.js:240-250): the first index of the maximum.
+__global__ __launch_bounds__(1024) void k_pf_argmax(const float *v, int n, int *res) {
+  __shared__ float bv[1024];
+  __shared__ int bi[1024];
+  float best = -INFINITY;
+  int idx = 0x7fffffff;
+  for (int i = tid(); i < n; i += 1024)
+    if (v[i] > best) {  // ascending per thread: ties keep the first
+      best = v[i];
+      idx = i;
+    }
+  bv[tid()] = best;
+  bi[tid()] = idx;
+  __syncthreads();
+  for (int w = 512; w > 0; w >>= 1) {
+    if (tid() < w) {
+      const float o = bv[tid() + w];
+      const int oi = bi[tid() + w];
+      if (o > bv[tid()] || (o == bv[tid()] && oi < bi[tid()])) {
+        bv[tid()] = o;
+        bi[tid()] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (tid() == 0) *res = bi[0] == 0x7fffffff ? 0 : bi[0];
 }
 
 // ---------------------------------------------------------------- Q4 GEMM
@@ -177,6 +310,7 @@ struct PfGemm {
   int rstep;  // rows per wave (64 or 32)
   int ng;     // groups per row
   int n;      // tokens
+  int tt0;    // first token tile
   int li, pos0;
   const float *bias0, *bias1;  // per row of each matrix, or null
   float *out;                  // EPI_RESID: the residual rows; SWIGLU/GELU: the MLP activation
@@ -210,7 +344,7 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
   const int ks = wv % KS;
   const int R = (blockIdx.x * (WG / 64 / KS) + wv / KS) * G.rstep;
   const bool active = R < G.rows;
-  const int T0 = blockIdx.y * 32;
+  const int T0 = (G.tt0 + blockIdx.y) * 32;
   const int ng = G.ng, gb = ng * ks / KS, ge = ng * (ks + 1) / KS;  // this wave's groups
   // tiled operands (every row tile and token tile whole): per group, the
   // wave's weights are 512 contiguous bytes, its scales 128, its
@@ -218,7 +352,7 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
   const size_t ta = (size_t)(R >> 5) * ng, tb = (size_t)((R + G.off1) >> 5) * ng;
   const uint8_t *wa = G.q0 + ta * 512 + 8 * lane, *wb = G.q1 + tb * 512 + 8 * lane;
   const float *sa = G.s0 + ta * 32 + j, *sb = G.s1 + tb * 32 + j;
-  const uint8_t *xa = A.px + (size_t)blockIdx.y * ng * PX_TILE + 16 * lane;
+  const uint8_t *xa = A.px + (size_t)(G.tt0 + blockIdx.y) * ng * PX_TILE + 16 * lane;
   auto load = [&](int g) {
     GemmLd L;
     L.w0 = *reinterpret_cast<const uint2 *>(wa + 512 * g);
@@ -405,7 +539,7 @@ constexpr int VROW2 = 68;  // halves per staged value column (64 keys + pad)
 // each SIMD; set 1's running (max, sum, output) is merged into set 0's at the
 // end through LDS.
 template <bool SPLIT_KV>
-__global__ __launch_bounds__(512) void k_pf_attn(PfArgs A, int li, int n, int pos0) {
+__global__ __launch_bounds__(512) void k_pf_attn(PfArgs A, int li, int n, int pos0, int tt0) {
   constexpr int KB_BYTES = KSB * KROW * 2, VB_BYTES = PF_HD * VROW2 * 2;
   constexpr int STAGE = (SPLIT_KV ? 2 : 1) * (KB_BYTES + VB_BYTES);
   constexpr int MERGE = 4 * 64 * 34 * 4;  // up to 4 heads x 64 lanes x (32 outputs, max, sum)
@@ -413,7 +547,7 @@ __global__ __launch_bounds__(512) void k_pf_attn(PfArgs A, int li, int n, int po
   _Float16 *Kh = reinterpret_cast<_Float16 *>(smem), *Vh = Kh + KSB * KROW;
   _Float16 *Kl = Vh + PF_HD * VROW2, *Vl = Kl + KSB * KROW;  // SPLIT_KV only
   const int rep = A.NH / A.NKV;
-  const int T0 = (gridDim.x - 1 - blockIdx.x) * QTL, kvh = blockIdx.y;  // the longest tiles first
+  const int T0 = (tt0 + gridDim.x - 1 - blockIdx.x) * QTL, kvh = blockIdx.y;  // the longest tiles first
   const int lane = tid() & 63, j = lane & 31, hh = lane >> 5;
   const int wv = tid() >> 6, set = wv / rep, hsel = wv - set * rep;
   const int hq = kvh * rep + hsel;
@@ -606,15 +740,22 @@ __global__ __launch_bounds__(WG) void k_pf_tile(PfMat W, uint8_t *q, float *s) {
 
 // ---------------------------------------------------------------- host
 template <int NORM>
-void launch_quant(const PfArgs &A, const float *src, int K, const float *g, int n, hipStream_t s) {
-  hipLaunchKernelGGL(k_pf_quant<NORM>, dim3(n), dim3(WG), (size_t)K * sizeof(float), s, src, K, g, A.eps, A.px, A.sx);
+void launch_quant(const PfArgs &A, const float *src, int K, const float *g, int t0, int t1, hipStream_t s) {
+  const int per = WG / 64;
+  const dim3 grid((t1 - t0 + per - 1) / per);
+  if (K <= 1024)
+    hipLaunchKernelGGL((k_pf_quant<NORM, 1>), grid, dim3(WG), 0, s, src, K, g, A.eps, A.px, A.sx, t0, t1);
+  else if (K <= 2048)
+    hipLaunchKernelGGL((k_pf_quant<NORM, 2>), grid, dim3(WG), 0, s, src, K, g, A.eps, A.px, A.sx, t0, t1);
+  else
+    hipLaunchKernelGGL((k_pf_quant<NORM, 4>), grid, dim3(WG), 0, s, src, K, g, A.eps, A.px, A.sx, t0, t1);
 }
 
 // Group slices per row range: the fewest (1, 2 or 4) that give at least
 // 2048 waves (two per SIMD on 256 CUs), keeping >= 8 groups per slice.
 template <int EPI>
 void launch_gemm(const PfArgs &A, const PfGemm &G, hipStream_t s) {
-  const int tt = (G.n + 31) / 32, rw = (G.rows + G.rstep - 1) / G.rstep;
+  const int tt = (G.n + 31) / 32 - G.tt0, rw = (G.rows + G.rstep - 1) / G.rstep;
   int ks = 1;
   while (ks < 4 && rw * tt * ks < 2048 && G.ng / (2 * ks) >= 8) ks *= 2;
   const int per_wg = (WG / 64 / ks) * G.rstep;
@@ -660,8 +801,8 @@ int pf_tile(const PfMat &W, void *dst, PfMat *out, hipStream_t s) {
 }
 
 bool pf_supported(const PfArgs &A) {
-  return A.D == A.NH * PF_HD && A.NH % A.NKV == 0 && A.NH / A.NKV <= 4 && A.FF % 64 == 0 && A.D <= 8192 &&
-         A.FF <= 8192;
+  return A.D == A.NH * PF_HD && A.NH % A.NKV == 0 && A.NH / A.NKV <= 4 && A.FF % 64 == 0 && A.D <= 4096 &&
+         A.FF <= 4096;
 }
 
 size_t pf_buffer_bytes(const PfArgs &A, int tc) {
@@ -691,7 +832,7 @@ void pf_carve(PfArgs &A, void *base, int tc) {
   A.px = p;
 }
 
-int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, hipStream_t s) {
+int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, bool last, hipStream_t s) {
   if (n <= 0) return 0;
   MLLM_CHECK(n <= A.tc && pos0 >= 0 && pos0 + n <= A.max_seq, "prefill chunk of %d tokens at %d out of range", n,
              pos0);
@@ -704,26 +845,34 @@ int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, hipStream_t 
   for (int li = 0; li < A.L; ++li) {
     const PfLayer &W = A.layers[li];
     if (gpt2)
-      launch_quant<NORM_LN>(A, A.x, A.D, W.n1, n, s);
+      launch_quant<NORM_LN>(A, A.x, A.D, W.n1, 0, n, s);
     else
-      launch_quant<NORM_RMS>(A, A.x, A.D, W.n1, n, s);
+      launch_quant<NORM_RMS>(A, A.x, A.D, W.n1, 0, n, s);
     PfGemm G = gemm_same(W.qkv, n, gpt2 ? W.qkv_b : nullptr, nullptr, 0);
     G.li = li;
     G.pos0 = pos0;
     launch_gemm<EPI_QKV>(A, G, s);
-    if (li == A.L - 1) break;  // the last layer's K and V are all the cache needs
+    // the last layer: only the K and V, or (for the prompt's last token) the
+    // rest of it for the last token tile alone
+    const bool final_layer = li == A.L - 1;
+    if (final_layer && !last) break;
+    const int tt0 = final_layer ? nqt - 1 : 0, t0 = tt0 * QTL;
     if (A.kv_fp16)
-      hipLaunchKernelGGL(k_pf_attn<false>, dim3(nqt, A.NKV), dim3(128 * rep), 0, s, A, li, n, pos0);
+      hipLaunchKernelGGL(k_pf_attn<false>, dim3(nqt - tt0, A.NKV), dim3(128 * rep), 0, s, A, li, n, pos0, tt0);
     else
-      hipLaunchKernelGGL(k_pf_attn<true>, dim3(nqt, A.NKV), dim3(128 * rep), 0, s, A, li, n, pos0);
-    launch_quant<NORM_NONE>(A, A.att, A.D, nullptr, n, s);
-    launch_gemm<EPI_RESID>(A, gemm_same(W.proj, n, gpt2 ? W.proj_b : nullptr, A.x, A.D), s);
+      hipLaunchKernelGGL(k_pf_attn<true>, dim3(nqt - tt0, A.NKV), dim3(128 * rep), 0, s, A, li, n, pos0, tt0);
+    launch_quant<NORM_NONE>(A, A.att, A.D, nullptr, t0, n, s);
+    PfGemm O = gemm_same(W.proj, n, gpt2 ? W.proj_b : nullptr, A.x, A.D);
+    O.tt0 = tt0;
+    launch_gemm<EPI_RESID>(A, O, s);
     if (gpt2)
-      launch_quant<NORM_LN>(A, A.x, A.D, W.n2, n, s);
+      launch_quant<NORM_LN>(A, A.x, A.D, W.n2, t0, n, s);
     else
-      launch_quant<NORM_RMS>(A, A.x, A.D, W.n2, n, s);
+      launch_quant<NORM_RMS>(A, A.x, A.D, W.n2, t0, n, s);
     if (gpt2) {
-      launch_gemm<EPI_GELU>(A, gemm_same(W.w1, n, W.fc_b, A.h, A.FF), s);
+      PfGemm F = gemm_same(W.w1, n, W.fc_b, A.h, A.FF);
+      F.tt0 = tt0;
+      launch_gemm<EPI_GELU>(A, F, s);
     } else {
       PfGemm U{};
       U.q0 = W.w1.q;
@@ -735,12 +884,26 @@ int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, hipStream_t 
       U.rstep = 32;
       U.ng = W.w1.cols >> 5;
       U.n = n;
+      U.tt0 = tt0;
       U.out = A.h;
       U.ldo = A.FF;
       launch_gemm<EPI_SWIGLU>(A, U, s);
     }
-    launch_quant<NORM_NONE>(A, A.h, A.FF, nullptr, n, s);
-    launch_gemm<EPI_RESID>(A, gemm_same(W.w2, n, gpt2 ? W.mproj_b : nullptr, A.x, A.D), s);
+    launch_quant<NORM_NONE>(A, A.h, A.FF, nullptr, t0, n, s);
+    PfGemm Dn = gemm_same(W.w2, n, gpt2 ? W.mproj_b : nullptr, A.x, A.D);
+    Dn.tt0 = tt0;
+    launch_gemm<EPI_RESID>(A, Dn, s);
+  }
+  if (last) {
+    // the final norm of the last token, the lm_head (the standalone Q4 GEMV)
+    // and the greedy argmax
+    float *xn = A.att;  // free once the layers are done
+    if (gpt2)
+      hipLaunchKernelGGL(k_pf_final<NORM_LN>, dim3(1), dim3(64), 0, s, A.x, A.D, n - 1, A.norm_f, A.eps, xn);
+    else
+      hipLaunchKernelGGL(k_pf_final<NORM_RMS>, dim3(1), dim3(64), 0, s, A.x, A.D, n - 1, A.norm_f, A.eps, xn);
+    if (int rc = mllm_gemv_q4(A.emb.rows, A.emb.cols, A.emb.q, A.emb.s, 32, xn, A.logits, s)) return rc;
+    hipLaunchKernelGGL(k_pf_argmax, dim3(1), dim3(1024), 0, s, A.logits, A.emb.rows, A.res);
   }
   MLLM_HIP(hipGetLastError());
   return 0;
