@@ -23,7 +23,12 @@ One JSON line on stdout carries, besides the driver's fields:
                 (warm = MALL-resident, cold = rotating >= 1 GiB of copies,
                 stacked = 32 matrices per launch)
   configs       config 3 (prompt-lookup speculation, k = 4 / 8), config 4
-                (GPT-2 124M), config 5 (362M, fp16 KV, 1536-token prefill)
+                (GPT-2 124M), config 5 (362M, fp16 KV: the 1536-token prompt
+                through the batched path, and through the 16-token passes of
+                the decode phases for comparison; then 511 decode steps)
+
+    python bench.py --prefill-only   config 5's prompt through the batched
+                                     path three times (for profilers)
 """
 from __future__ import annotations
 
@@ -367,15 +372,27 @@ def bench_configs(mllm, pgw, args):
     cfg = pgw.CONFIGS["smollm2-360m"]
     g = mllm.PetitGPT(pgw.parse_pgw(pgw.make_llama(cfg, seed=0)), kv_fp16=True, exec_mode=args.exec_mode)
     prompt = [int(v) for v in np.random.default_rng(5).integers(0, cfg.vocab_size, 1536)]
+    # the prompt through the 16-token passes of the decode phases (the path
+    # shorter prompts take), then the batched path twice (the second is timed)
+    g.set_prefill(0)
+    t0 = time.perf_counter()
+    g.forwardPrompt(prompt)
+    pass_s = time.perf_counter() - t0
+    g.set_prefill(64)
+    g.forwardPrompt(prompt)
     t0 = time.perf_counter()
     g.forwardPrompt(prompt)
     ttft = time.perf_counter() - t0
+    prefill_gpu_ms, _ = g.last_timing()
     first = g.last_argmax
     t0 = time.perf_counter()
     ids = g.decodeChain(first, 511)
     dt = time.perf_counter() - t0
     mean_seq = 1536 + 256
-    res["smollm2_360m_fp16kv"] = {"prefill_ms": round(ttft * 1e3, 1), "decode_tok_s": round(len(ids) / dt, 1),
+    res["smollm2_360m_fp16kv"] = {"prefill_ms": round(ttft * 1e3, 2), "prefill_gpu_ms": round(prefill_gpu_ms, 2),
+                                  "prefill_tok_s": round(1536 / ttft, 1),
+                                  "prefill_pass_path_ms": round(pass_s * 1e3, 1),
+                                  "decode_tok_s": round(len(ids) / dt, 1),
                                   "decode_step_gbs": round(token_bytes(cfg, mean_seq, 2) / (dt / len(ids)) / 1e9, 1)}
     g.destroy()
     return res
@@ -392,6 +409,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true", help="config 5's prompt, batched, three times")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (counter calibration for the traffic figure)")
     args = ap.parse_args()
@@ -415,6 +433,18 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration(torch)
+        return
+    if args.prefill_only:
+        cfg = pgw.CONFIGS["smollm2-360m"]
+        g = mllm.PetitGPT(pgw.parse_pgw(pgw.make_llama(cfg, seed=0)), kv_fp16=True, exec_mode=args.exec_mode)
+        prompt = [int(v) for v in np.random.default_rng(5).integers(0, cfg.vocab_size, 1536)]
+        runs = []
+        for _ in range(3):
+            g.forwardPrompt(prompt)
+            runs.append(round(g.last_timing()[0], 3))
+            log(f"[bench] prefill 1536 tokens: {runs[-1]} ms (GPU)")
+        g.destroy()
+        print(json.dumps({"prefill_gpu_ms": runs, "tokens": 1536, "workload": "smollm2-360m fp16 KV (config 5)"}))
         return
     dec = bench_decode(mllm, pgw, torch, args)
     log(f"[bench] decode {dec['value']:.1f} tok/s, phases {dec['phase_us']}")
