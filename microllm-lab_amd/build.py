@@ -2,6 +2,7 @@
 
     python microllm-lab_amd/build.py            # everything
     python microllm-lab_amd/build.py lib        # libmllm.so only
+    python microllm-lab_amd/build.py convert    # the PGW1 converter (host C++)
 
 hipcc cross-compiles for gfx950 without a GPU.  All HIP code is built with
 packed-FP32 instructions disabled (-Xclang -target-feature -Xclang
@@ -30,6 +31,9 @@ INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libmllm.so")
 NAPI_SRC = os.path.join(PKG, "js", "napi", "mllm_napi.cc")
+CONVERT_SRC = os.path.join(PKG, "convert", "pgw_convert.cc")
+CONVERT_LIB = os.path.join(PKG, "convert", "libpgwconvert.so")
+CONVERT_BIN = os.path.join(PKG, "convert", "pgw_convert")
 NAPI_OUT = os.path.join(PKG, "js", "mllm_napi.node")
 
 HIP_SOURCES = ["mllm_ops.hip", "mllm_engine.hip", "mllm_prefill.hip"]
@@ -120,9 +124,25 @@ def build_napi(verbose: bool = False) -> str:
     return NAPI_OUT
 
 
+def build_convert(verbose: bool = False) -> str:
+    """The PGW1 converter (host C++): libpgwconvert.so and the pgw_convert command."""
+    cxx = shutil.which("g++") or "g++"
+    flags = ["-O2", "-std=c++17", "-Wall", "-Wextra", f"-I{INCLUDE}"]
+    tmp = CONVERT_LIB + ".tmp"
+    _run([cxx, *flags, "-shared", "-fPIC", CONVERT_SRC, "-o", tmp])
+    os.replace(tmp, CONVERT_LIB)
+    tmp = CONVERT_BIN + ".tmp"
+    _run([cxx, *flags, "-DPGW_CONVERT_MAIN", CONVERT_SRC, "-o", tmp])
+    os.replace(tmp, CONVERT_BIN)
+    if verbose:
+        print(f"built {CONVERT_LIB} and {CONVERT_BIN}")
+    return CONVERT_LIB
+
+
 def build_all(verbose: bool = False):
     build_lib(verbose)
     build_napi(verbose)
+    build_convert(verbose)
 
 
 if __name__ == "__main__":
@@ -131,5 +151,7 @@ if __name__ == "__main__":
         build_lib(True)
     elif what == "napi":
         build_napi(True)
+    elif what == "convert":
+        build_convert(True)
     else:
         build_all(True)

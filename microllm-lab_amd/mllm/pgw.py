@@ -310,3 +310,32 @@ def small_config(arch: str = "llama", **over) -> Config:
     for k, v in over.items():
         setattr(c, k, v)
     return c
+
+
+# --------------------------------------------------------------------------
+# checkpoint conversion (the C++ converter, libpgwconvert.so)
+# --------------------------------------------------------------------------
+def convert_checkpoint(hf_dir: str, out_path: str, arch: str = "llama", max_seq: Optional[int] = None,
+                       scale_factors: Optional[np.ndarray] = None) -> None:
+    """A HuggingFace checkpoint directory (config.json + safetensors) to a PGW1
+    file, as tools/convert_hf_to_pgw.py (arch "llama") or
+    tools/convert_gpt2_to_pgw.py after its calibration (arch "gpt2", with the
+    calibrated channel scales) write it; see include/pgw_convert.h."""
+    import ctypes as C
+    import os
+
+    lib_path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "convert",
+                            "libpgwconvert.so")
+    lib = C.CDLL(lib_path)
+    lib.pgwc_last_error.restype = C.c_char_p
+    if arch == "llama":
+        rc = lib.pgwc_convert_llama(hf_dir.encode(), out_path.encode(), C.c_int(max_seq or 2048))
+    elif arch == "gpt2":
+        sf = None if scale_factors is None else np.ascontiguousarray(scale_factors, np.float32)
+        rc = lib.pgwc_convert_gpt2(hf_dir.encode(), out_path.encode(), C.c_int(max_seq or 1024),
+                                   C.c_void_p(None if sf is None else sf.ctypes.data),
+                                   C.c_int(0 if sf is None else sf.size))
+    else:
+        raise ValueError(f"arch {arch!r}")
+    if rc:
+        raise RuntimeError(f"pgw_convert: {lib.pgwc_last_error().decode()}")
