@@ -169,3 +169,52 @@ def test_gemv_q4_linearity_full_lm_head():
         torch.cuda.synchronize()
         outs.append(host(dy))
     assert np.abs(outs[2] - (outs[0] + outs[1])).max() < 1e-4
+
+
+@gpu
+def test_gpu_abi_against_the_oracle_abi_on_the_same_arguments(oracle_lib):
+    """Each operator of include/mllm.h and its host-pointer counterpart in the
+    oracle (oracle/mllm_cpu.h, kernels.rs semantics) on one argument list:
+    dequant bit-exact, the rest within the row bound."""
+    lib = C.CDLL(oracle_lib.build())
+    rng = np.random.default_rng(42)
+    m, n, t = 300, 960, 3
+    w = (rng.standard_normal((m, n)) * 0.02).astype(np.float32)
+    packed, sc = pgw.quant_q4(w)
+    W = oracle_lib.dequant_q4(packed, sc)
+    x = rng.standard_normal((t, n)).astype(np.float32)
+    hp = lambda a: C.c_void_p(a.ctypes.data)  # noqa: E731
+    print("cpu abi: gemv_q4 / gemm_q4 / dequant_q4", flush=True)
+    y_cpu = np.zeros((t, m), np.float32)
+    assert lib.mllm_cpu_gemm_q4(t, m, n, hp(packed), hp(sc), 32, hp(x), hp(y_cpu), None) == 0
+    dy = torch.empty((t, m), dtype=torch.float32, device="cuda")
+    abi.call("mllm_gemm_q4", t, m, n, ptr(dev(packed)), ptr(dev(sc)), 32, ptr(dev(x)), ptr(dy), None)
+    for i in range(t):
+        assert (np.abs(host(dy)[i] - y_cpu[i]) <= 2 * row_bound(W, x[i])).all()
+    y1 = np.zeros(m, np.float32)
+    assert lib.mllm_cpu_gemv_q4(m, n, hp(packed), hp(sc), 32, hp(x[0]), hp(y1), None) == 0
+    assert np.array_equal(y1, y_cpu[0])
+    d_cpu = np.zeros((m, n), np.float32)
+    assert lib.mllm_cpu_dequant_q4(m, n, hp(packed), hp(sc), 32, hp(d_cpu), None) == 0
+    dd = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    abi.call("mllm_dequant_q4", m, n, ptr(dev(packed)), ptr(dev(sc)), 32, ptr(dd), None)
+    assert np.array_equal(host(dd).view(np.uint32), d_cpu.view(np.uint32))
+    print("cpu abi: rms_norm / silu_mul / gemv_f32", flush=True)
+    g = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    o_cpu = np.zeros((t, n), np.float32)
+    assert lib.mllm_cpu_rms_norm(n, hp(x), hp(g), hp(o_cpu), t, C.c_float(1e-6), None) == 0
+    do = torch.empty((t, n), dtype=torch.float32, device="cuda")
+    abi.call("mllm_rms_norm", n, ptr(dev(x)), ptr(dev(g)), ptr(do), t, C.c_float(1e-6), None)
+    assert np.abs(host(do) - o_cpu).max() <= 1e-5 * np.abs(o_cpu).max()
+    a = rng.standard_normal(n).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    a_cpu = a.copy()
+    assert lib.mllm_cpu_silu_mul(n, hp(a_cpu), hp(b), None) == 0
+    da = dev(a)
+    abi.call("mllm_silu_mul", n, ptr(da), ptr(dev(b)), None)
+    assert np.abs(host(da) - a_cpu).max() <= 1e-5 * np.abs(a_cpu).max() + 1e-6
+    f_cpu = np.zeros(m, np.float32)
+    assert lib.mllm_cpu_gemv_f32(m, n, hp(w), hp(x[0]), hp(f_cpu), None) == 0
+    df = torch.empty(m, dtype=torch.float32, device="cuda")
+    abi.call("mllm_gemv_f32", m, n, ptr(dev(w)), ptr(dev(x[0])), ptr(df), None)
+    assert (np.abs(host(df) - f_cpu) <= 2 * row_bound(w, x[0])).all()
