@@ -187,8 +187,11 @@ def test_gpu_abi_against_the_oracle_abi_on_the_same_arguments(oracle_lib):
     print("cpu abi: gemv_q4 / gemm_q4 / dequant_q4", flush=True)
     y_cpu = np.zeros((t, m), np.float32)
     assert lib.mllm_cpu_gemm_q4(t, m, n, hp(packed), hp(sc), 32, hp(x), hp(y_cpu), None) == 0
+    # device copies held for the whole test: a temporary's memory may be
+    # reused by the next allocation before the kernel runs
+    dp, ds, dx = dev(packed), dev(sc), dev(x)
     dy = torch.empty((t, m), dtype=torch.float32, device="cuda")
-    abi.call("mllm_gemm_q4", t, m, n, ptr(dev(packed)), ptr(dev(sc)), 32, ptr(dev(x)), ptr(dy), None)
+    abi.call("mllm_gemm_q4", t, m, n, ptr(dp), ptr(ds), 32, ptr(dx), ptr(dy), None)
     for i in range(t):
         assert (np.abs(host(dy)[i] - y_cpu[i]) <= 2 * row_bound(W, x[i])).all()
     y1 = np.zeros(m, np.float32)
@@ -197,24 +200,26 @@ def test_gpu_abi_against_the_oracle_abi_on_the_same_arguments(oracle_lib):
     d_cpu = np.zeros((m, n), np.float32)
     assert lib.mllm_cpu_dequant_q4(m, n, hp(packed), hp(sc), 32, hp(d_cpu), None) == 0
     dd = torch.empty((m, n), dtype=torch.float32, device="cuda")
-    abi.call("mllm_dequant_q4", m, n, ptr(dev(packed)), ptr(dev(sc)), 32, ptr(dd), None)
+    abi.call("mllm_dequant_q4", m, n, ptr(dp), ptr(ds), 32, ptr(dd), None)
     assert np.array_equal(host(dd).view(np.uint32), d_cpu.view(np.uint32))
     print("cpu abi: rms_norm / silu_mul / gemv_f32", flush=True)
     g = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
     o_cpu = np.zeros((t, n), np.float32)
     assert lib.mllm_cpu_rms_norm(n, hp(x), hp(g), hp(o_cpu), t, C.c_float(1e-6), None) == 0
+    dg = dev(g)
     do = torch.empty((t, n), dtype=torch.float32, device="cuda")
-    abi.call("mllm_rms_norm", n, ptr(dev(x)), ptr(dev(g)), ptr(do), t, C.c_float(1e-6), None)
+    abi.call("mllm_rms_norm", n, ptr(dx), ptr(dg), ptr(do), t, C.c_float(1e-6), None)
     assert np.abs(host(do) - o_cpu).max() <= 1e-5 * np.abs(o_cpu).max()
     a = rng.standard_normal(n).astype(np.float32)
     b = rng.standard_normal(n).astype(np.float32)
     a_cpu = a.copy()
     assert lib.mllm_cpu_silu_mul(n, hp(a_cpu), hp(b), None) == 0
-    da = dev(a)
-    abi.call("mllm_silu_mul", n, ptr(da), ptr(dev(b)), None)
+    da, db = dev(a), dev(b)
+    abi.call("mllm_silu_mul", n, ptr(da), ptr(db), None)
     assert np.abs(host(da) - a_cpu).max() <= 1e-5 * np.abs(a_cpu).max() + 1e-6
     f_cpu = np.zeros(m, np.float32)
     assert lib.mllm_cpu_gemv_f32(m, n, hp(w), hp(x[0]), hp(f_cpu), None) == 0
+    dw, dx0 = dev(w), dev(x[0])
     df = torch.empty(m, dtype=torch.float32, device="cuda")
-    abi.call("mllm_gemv_f32", m, n, ptr(dev(w)), ptr(dev(x[0])), ptr(df), None)
+    abi.call("mllm_gemv_f32", m, n, ptr(dw), ptr(dx0), ptr(df), None)
     assert (np.abs(host(df) - f_cpu) <= 2 * row_bound(w, x[0])).all()
