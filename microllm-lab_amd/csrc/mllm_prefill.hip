@@ -634,11 +634,13 @@ __global__ __launch_bounds__(512) void k_pf_attn(PfArgs A, int li, int n, int po
       }
     }
     float mx = -INFINITY;
+    if (k0 + 31 > pos0 + T0) {  // the block reaches past a query of the tile: mask
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      if (k0 + 8 * (v >> 2) + 4 * hh + (v & 3) > qpos) s[v] = -INFINITY;
-      mx = fmaxf(mx, s[v]);
+      for (int v = 0; v < 16; ++v)
+        if (k0 + 8 * (v >> 2) + 4 * hh + (v & 3) > qpos) s[v] = -INFINITY;
     }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[v]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float mn = fmaxf(m_run, mx);
     // a query with no key yet in this set: everything stays zero
@@ -656,12 +658,15 @@ __global__ __launch_bounds__(512) void k_pf_attn(PfArgs A, int li, int n, int po
     }
     ps += __shfl_xor(ps, 32);
     l_run = l_run * alpha + ps;
-    m_run = mn;
+    // rescale the outputs unless no lane's running max moved (alpha = 1)
+    if (__builtin_amdgcn_read_exec() & __ballot(mn != m_run)) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      o0[v] *= alpha;
-      o1[v] *= alpha;
+      for (int v = 0; v < 16; ++v) {
+        o0[v] *= alpha;
+        o1[v] *= alpha;
+      }
     }
+    m_run = mn;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int kc = kr + 16 * u + 4 * hh;
