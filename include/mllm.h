@@ -183,7 +183,7 @@ int mllm_model_gemv(mllm_model *model, const char *name, const float *x, float *
  * Returns MLLM_ERR_UNSUPPORTED for mode 3 where it is unavailable. */
 int mllm_set_exec_mode(mllm_model *model, int mode);
 
-/* Prompts of at least min_tokens tokens (default 64; 0 = never) are
+/* Prompts of at least min_tokens tokens (default 2; 0 = never) are
  * processed in batches (no counterpart in the reference, whose GPU path runs
  * a prompt token by token, webgpu.js:1178-1187): tokens 0 .. n-2 go through
  * every layer as Q4 GEMMs on the int8 matrix cores and one causal attention

@@ -2235,7 +2235,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
           }
       if (hipStreamSynchronize(M->stream) != hipSuccess) return fail(set_error(MLLM_ERR_HIP, "weight tiling"));
       M->pf_tc_max = tc;
-      M->pf_min = 64;
+      M->pf_min = 2;  // faster than the passes from 2 tokens on (one token: the decode step)
     }
   }
 
