@@ -220,3 +220,22 @@ def test_full_size_chain_persistent_equals_graph(arch):
         g.destroy()
     assert outs[0][0] == outs[1][0]
     assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))
+
+
+@gpu
+def test_long_context_persistent_equals_graph():
+    """600-token context (3 attention splits per head, merged by the last
+    split to finish): the persistent kernel's logits bit-identical to the
+    graph-replayed phase kernels'."""
+    bundle = build("llama", seed=13, max_seq_len=1024)
+    rng = np.random.default_rng(8)
+    prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 600)]
+    follow = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 6)]
+    outs = []
+    for mode in (1, 3):
+        print(f"long context mode={mode}", flush=True)
+        g = mllm.PetitGPT(bundle, exec_mode=mode)
+        g.forwardPrompt(prompt)
+        outs.append(np.stack([g.forwardDecode(t).copy() for t in follow]))
+        g.destroy()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
