@@ -21,7 +21,7 @@ import pytest
 from mllm import tokenizer as T
 
 REF_MODELS = "/root/reference/models"
-MODELS = ["gpt2", "l20-edu-135m", "minimind2", "smollm2-135m-instruct"]
+MODELS = ["gpt2", "l20-edu-135m", "minimind2", "smollm2-135m-instruct", "petitgpt"]
 
 TEXTS = [
     "Hello! How can I help you today?",
@@ -171,3 +171,22 @@ def test_templates():
         T.encode_chat(tok, [{"role": "tool", "content": "x"}])
     with pytest.raises(ValueError, match="empty"):
         T.encode_chat(tok, [{"role": "user", "content": ""}])
+
+
+def test_templates_with_the_reference_cards():
+    """The cards shipped beside the models (card.json): petitgpt's template with
+    its own role ids, chatml with SmolLM2's <|im_start|> / <|im_end|>."""
+    import json
+
+    tok, _ = hf_or_skip("petitgpt")
+    card = json.load(open(os.path.join(REF_MODELS, "petitgpt", "card.json")))
+    conv = [{"role": "system", "content": "Be brief."}, {"role": "user", "content": "What is 2 + 2?"}]
+    ids = T.encode_messages(tok, conv, card)
+    sp = card["specials"]
+    assert ids == ([card["bosId"], sp["<|system|>"]] + tok.encode("Be brief.") + [sp["<|user|>"]] +
+                   tok.encode("What is 2 + 2?") + [sp["<|assistant|>"]])
+    tok2, _ = hf_or_skip("smollm2-135m-instruct")
+    card2 = dict(json.load(open(os.path.join(REF_MODELS, "smollm2-135m-instruct", "card.json"))), template="chatml")
+    ids2 = T.encode_messages(tok2, conv[1:], card2)
+    assert ids2[0] == tok2.special["<|im_start|>"] == 1 and ids2.count(tok2.special["<|im_end|>"]) == 1
+    assert tok2.decode(ids2) == "<|im_start|>user\nWhat is 2 + 2?<|im_end|>\n<|im_start|>assistant\n"
