@@ -63,6 +63,8 @@ export class HipPetitGPT {
     this._logits = new Float32Array(c.vocabSize);
     this.maxPass = native.maxPassTokens(this._h);
     if (o.execMode !== undefined) native.setExecMode(this._h, o.execMode);
+    // prompts of at least prefillMin ids run batched (mllm_set_prefill; 0 = 16-token passes)
+    if (o.prefillMin !== undefined) native.setPrefill(this._h, o.prefillMin, o.prefillChunk || 0);
     this.mode = `hip-${bundle.kind}`;
     this.lastArgmax = 0;
     this.lastTiming = null;

@@ -328,6 +328,15 @@ napi_value SetExecMode(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+napi_value SetPrefill(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!get_args(env, info, 3, argv)) return nullptr;
+  Handle *h = get_handle(env, argv[0]);
+  if (!h) return nullptr;
+  MLLM_OK_OR_THROW("mllm_set_prefill", mllm_set_prefill(h->model, get_i32(env, argv[1]), get_i32(env, argv[2])));
+  return nullptr;
+}
+
 napi_value LastTiming(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!get_args(env, info, 1, argv)) return nullptr;
@@ -373,7 +382,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"createModel", CreateModel}, {"destroy", Destroy},           {"resetCache", ResetCache},
       {"cacheLen", CacheLen},       {"setCacheLen", SetCacheLen},   {"forwardPrompt", ForwardPrompt},
       {"forwardDecode", ForwardDecode}, {"forwardVerify", ForwardVerify}, {"decodeChain", DecodeChain},
-      {"gemv", Gemv},               {"setExecMode", SetExecMode},   {"lastTiming", LastTiming},
+      {"gemv", Gemv},               {"setExecMode", SetExecMode},   {"setPrefill", SetPrefill},   {"lastTiming", LastTiming},
       {"deviceBytes", DeviceBytes}, {"maxPassTokens", MaxPass},     {"version", Version},
   };
   for (const auto &f : fns) {

@@ -2,7 +2,7 @@
  * Drive HipPetitGPT on a .pgw file (the flow of engine/worker.js:34-181:
  * load -> new engine -> generate with streaming onToken).
  *   node run_generate.mjs <model.pgw> <spec.json>   -> prints one JSON line
- * spec: { prompt: [...], maxNewTokens, eosId, mode, specK, kvFp16, execMode,
+ * spec: { prompt: [...], maxNewTokens, eosId, mode, specK, kvFp16, execMode, prefillMin,
  *         decodeLogits: [ids...] }  (decodeLogits: teacher-forced tokens whose
  *         logits are returned for comparison)
  */
@@ -14,7 +14,7 @@ async function main() {
   const [, , pgwPath, specPath] = process.argv;
   const spec = JSON.parse(fs.readFileSync(specPath, "utf8"));
   const bundle = parsePgw(fs.readFileSync(pgwPath));
-  const model = new HipPetitGPT(bundle, { kvFp16: !!spec.kvFp16, execMode: spec.execMode });
+  const model = new HipPetitGPT(bundle, { kvFp16: !!spec.kvFp16, execMode: spec.execMode, prefillMin: spec.prefillMin });
   const streamed = [];
   const res = await model.generate(spec.prompt, {
     maxNewTokens: spec.maxNewTokens,
