@@ -121,3 +121,21 @@ def test_smollm2_135m_batched_prompt_vs_pass_path():
         outs.append(np.stack(steps))
         g.destroy()
     assert np.abs(outs[0] - outs[1]).max() < PASS_TOL
+
+
+@gpu
+def test_set_prefill_arguments():
+    """Threshold and chunk are checked; a chunk at the buffers' limit works."""
+    bundle = build("llama", seed=24, max_seq_len=256)
+    g = mllm.PetitGPT(bundle)
+    with pytest.raises(Exception, match="threshold"):
+        g.set_prefill(-1)
+    with pytest.raises(Exception, match="chunk"):
+        g.set_prefill(2, 257)
+    g.set_prefill(2, 256)
+    prompt = list(range(1, 101))
+    a = g.forwardPrompt(prompt).copy()
+    g.set_prefill(2, 33)  # 100 = 3 x 33 + 1
+    b = g.forwardPrompt(prompt).copy()
+    g.destroy()
+    assert np.abs(a - b).max() < PASS_TOL
