@@ -81,7 +81,8 @@ def phase_bytes(cfg, seq, kv_bytes=4):
 
 
 def token_bytes(cfg, seq, kv_bytes=4):
-    """BASELINE.md's per-token algorithmic bytes: Q4 weights + norms + KV read."""
+    """Algorithmic bytes of one decode token: the Q4 weights, the norm gains
+    and the KV rows read at context mean_seq."""
     D, FF = cfg.d_model, cfg.d_ff
     hd = D // cfg.n_heads
     kvd = cfg.n_kv_heads * hd
@@ -416,7 +417,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
-              "the decode step is batch-1 and single-device, see DESIGN.md for how it would shard", file=sys.stderr)
+              "the decode step is batch-1 on one device; data-parallel sequences would each run their own", file=sys.stderr)
         sys.exit(2)
     if args.steps < 1 or args.steps + args.warmup + 40 > 2048:
         print("--steps/--warmup out of range for a 2048 context", file=sys.stderr)
