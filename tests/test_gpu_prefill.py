@@ -139,3 +139,28 @@ def test_set_prefill_arguments():
     b = g.forwardPrompt(prompt).copy()
     g.destroy()
     assert np.abs(a - b).max() < PASS_TOL
+
+
+@gpu
+@pytest.mark.parametrize("name,kv16", [("gpt2-124m", False), ("smollm2-360m", True)])
+def test_full_size_batched_prompt_vs_pass_path(name, kv16):
+    """Config 4 and config 5 shapes at full size, a 200-token prompt then 4
+    decode steps: the batched path (GELU / LayerNorm / bias epilogues for
+    GPT-2; d_model 960, 5 KV heads, f16 KV for the 360M) against the pass
+    path within PASS_TOL."""
+    cfg = pgw.CONFIGS[name]
+    bundle = pgw.parse_pgw(pgw.make_model(cfg, seed=0))
+    rng = np.random.default_rng(9)
+    prompt = [int(v) for v in rng.integers(0, cfg.vocab_size, 200)]
+    follow = [int(v) for v in rng.integers(0, cfg.vocab_size, 4)]
+    outs = []
+    for pf_min in (2, 0):
+        print(f"prefill {name} pf_min={pf_min}", flush=True)
+        g = mllm.PetitGPT(bundle, kv_fp16=kv16)
+        g.set_prefill(pf_min)
+        steps = [g.forwardPrompt(prompt).copy()]
+        for tok in follow:
+            steps.append(g.forwardDecode(tok).copy())
+        outs.append(np.stack(steps))
+        g.destroy()
+    assert np.abs(outs[0] - outs[1]).max() < PASS_TOL
