@@ -120,10 +120,13 @@ __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F7
 
 // Tagged values.  A value handed from one workgroup to another inside the
 // persistent kernel travels with the tag of the (step, layer) that wrote it,
-// as one naturally aligned 64-bit (float bits, tag) pair: a 64-bit access is
-// single-copy atomic, so a reader that sees the tag it waits for also sees
-// that writer's value, and polling the data replaces a completion wait plus
-// a flag.  Tags grow across launches and are compared modulo 2^32.
+// in the same naturally aligned access: a 64-bit (float bits, tag) pair, or a
+// 16-byte quad of three floats and the tag (the residual partials).  Such an
+// access reaches memory whole, so a reader that sees the tag it waits for also
+// sees that writer's values, and polling the data replaces a completion wait
+// plus a flag.  (For the quads this rests on the 16-byte stores and loads
+// being observed whole on this device; torn quads were searched for and not
+// seen.)  Tags grow across launches and are compared modulo 2^32.
 __device__ __forceinline__ bool tag_ok(uint32_t tag, int want) { return (int)(tag - (uint32_t)want) >= 0; }
 __device__ __forceinline__ uint2 tagged(float v, int tag) { return make_uint2(__float_as_uint(v), (uint32_t)tag); }
 // A compiler barrier for polling loops: the loads after it are issued again
