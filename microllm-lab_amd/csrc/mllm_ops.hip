@@ -359,16 +359,17 @@ long q4_target() { return (long)MLLM_Q4_WG_PER_CU * (device_wg_cap() / 8); }
 
 // Geometry of the Q4 GEMV for a shape and matrix count: workgroup size, rows
 // per pass (one group per thread), lanes per row sum.  256-thread workgroups
-// up to 256 groups per row; 512 above that, and also where even one-pass
-// tiles of 256 threads leave the launch below its workgroup target (the
-// small layer matrices: fewer, wider workgroups then measure faster, e.g.
-// 960 x 2560 in 3.8 instead of 4.5 us).  The per-row arithmetic and its
-// summation order do not depend on the workgroup size.
+// up to 256 groups per row; 512 above that, and also for long rows (>= 64
+// groups) where even one-pass tiles of 256 threads leave the launch below its
+// workgroup target: every workgroup stages all of x, and twice the rows
+// share that staging (960 x 2560: 4.4 instead of 4.7 us of kernel time; at
+// 960 columns the 256-thread tiles stay faster).  The per-row arithmetic and
+// its summation order do not depend on the workgroup size.
 Q4Plan q4_plan(int cols, int rows, int count) {
   const int ng = cols / 32;
   Q4Plan p;
   p.wgt = ng <= 256 ? 256 : 512;
-  if (p.wgt == 256 && (long)((rows + 256 / ng - 1) / (256 / ng)) * count < q4_target()) p.wgt = 512;
+  if (p.wgt == 256 && ng >= 64 && (long)((rows + 256 / ng - 1) / (256 / ng)) * count < q4_target()) p.wgt = 512;
   p.rpp = p.wgt / ng;
   p.lpr = 1;
   while (p.lpr < 64 && p.lpr * 4 < ng) p.lpr <<= 1;
