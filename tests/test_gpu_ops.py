@@ -89,6 +89,26 @@ def test_gemv_q4_batched_matches_single():
 
 
 @gpu
+def test_gemv_q4_rows_do_not_depend_on_the_workgroup_width():
+    """960 x 2560 alone launches 512-thread one-pass tiles; 32 of them stacked
+    launch 256-thread eight-pass tiles.  Every row must carry the same bits."""
+    rng = np.random.default_rng(8)
+    count, m, n = 32, 960, 2560
+    packed, sc = pgw.quant_q4((rng.standard_normal((m, n)) * 0.02).astype(np.float32))
+    dp, ds = dev(packed), dev(sc)
+    xs = [dev(rng.standard_normal(n).astype(np.float32)) for _ in range(count)]
+    ys = [torch.empty(m, dtype=torch.float32, device="cuda") for _ in range(count)]
+    table = lambda ts: dev(np.array([t.data_ptr() for t in ts], np.uint64))  # noqa: E731
+    tp, ts_, tx, ty = table([dp] * count), table([ds] * count), table(xs), table(ys)
+    abi.call("mllm_gemv_q4_batched", count, m, n, ptr(tp), ptr(ts_), ptr(tx), ptr(ty), None)
+    torch.cuda.synchronize()
+    for i in range(count):
+        d1 = torch.empty(m, dtype=torch.float32, device="cuda")
+        abi.call("mllm_gemv_q4", m, n, ptr(dp), ptr(ds), 32, ptr(xs[i]), ptr(d1), None)
+        assert np.array_equal(host(d1).view(np.uint32), host(ys[i]).view(np.uint32)), i
+
+
+@gpu
 @pytest.mark.parametrize("m,n", [(96, 64), (960, 960), (2560, 960), (49152, 960)])
 def test_gemv_q8_row_and_g32_vs_oracle(oracle_lib, m, n):
     rng = np.random.default_rng(m + n)
