@@ -89,11 +89,13 @@ def test_gemv_q4_batched_matches_single():
 
 
 @gpu
-def test_gemv_q4_rows_do_not_depend_on_the_workgroup_width():
-    """960 x 2560 alone launches 512-thread one-pass tiles; 32 of them stacked
-    launch 256-thread eight-pass tiles.  Every row must carry the same bits."""
+@pytest.mark.parametrize("n", [2048, 2560, 4096, 8192])
+def test_gemv_q4_rows_do_not_depend_on_the_workgroup_width(n):
+    """960 x n alone (64 to 256 groups per row) launches 512-thread one-pass
+    tiles; 32 of them stacked launch 256-thread multi-pass tiles.  Every row
+    must carry the same bits."""
     rng = np.random.default_rng(8)
-    count, m, n = 32, 960, 2560
+    count, m = 32, 960
     packed, sc = pgw.quant_q4((rng.standard_normal((m, n)) * 0.02).astype(np.float32))
     dp, ds = dev(packed), dev(sc)
     xs = [dev(rng.standard_normal(n).astype(np.float32)) for _ in range(count)]
@@ -109,7 +111,7 @@ def test_gemv_q4_rows_do_not_depend_on_the_workgroup_width():
 
 
 @gpu
-@pytest.mark.parametrize("m,n", [(96, 64), (960, 960), (2560, 960), (49152, 960)])
+@pytest.mark.parametrize("m,n", [(96, 64), (960, 960), (320, 960), (2560, 960), (960, 2560), (49152, 960)])
 def test_gemv_q8_row_and_g32_vs_oracle(oracle_lib, m, n):
     rng = np.random.default_rng(m + n)
     w = (rng.standard_normal((m, n)) * 0.02).astype(np.float32)

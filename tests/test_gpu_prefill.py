@@ -164,3 +164,31 @@ def test_full_size_batched_prompt_vs_pass_path(name, kv16):
         outs.append(np.stack(steps))
         g.destroy()
     assert np.abs(outs[0] - outs[1]).max() < PASS_TOL
+
+
+@gpu
+@pytest.mark.parametrize("pf_min", [2, 0])
+@pytest.mark.parametrize("mode", [1, 3])
+def test_gpt2_smoothquant_descale_and_biases_vs_oracle(oracle_lib, pf_min, mode):
+    """GPT-2 with non-unit SmoothQuant channel scales (the embedding row is
+    divided by scale_factors, infer.js:416-419, webgpu-gpt2.js:132-147) and
+    non-zero biases in every layer: the batched prompt (pf_min 2) and the pass
+    path (pf_min 0), then decode steps in graph-replay and persistent modes,
+    against the oracle.  The scales follow the converter's shape
+    (convert_gpt2_to_pgw.py:126-129): positive, median 1, spread over about
+    a factor of 10."""
+    cfg = pgw.small_config("gpt2", max_seq_len=128)
+    srng = np.random.default_rng(31)
+    sf = np.exp(srng.standard_normal(cfg.d_model) * 0.8).astype(np.float32)
+    sf = (sf / np.median(sf)).astype(np.float32)
+    bundle = pgw.parse_pgw(pgw.make_gpt2(cfg, seed=31, scale_factors=sf, bias_std=0.02))
+    print(f"gpt2 smoothquant pf_min={pf_min} mode={mode}", flush=True)
+    g = mllm.PetitGPT(bundle, exec_mode=mode)
+    g.set_prefill(pf_min)
+    ref = oracle_lib.OracleModel(bundle)
+    rng = np.random.default_rng(32)
+    prompt = [int(v) for v in rng.integers(0, cfg.vocab_size, 40)]
+    worst, agree = vs_oracle(g, ref, prompt, 6, rng)
+    g.destroy()
+    ref.close()
+    assert worst < LOGIT_TOL and agree, worst

@@ -91,29 +91,89 @@ def test_dequant_error_bound_and_requant(oracle_lib, rng):
 
 
 def test_dequant_exhaustive_bytes(oracle_lib):
-    """All 256 byte values x scale edge cases: element 2k = low nibble, 2k+1 = high."""
-    packed = np.tile(np.arange(256, dtype=np.uint8), (4, 1))[:, :256].reshape(4, 256)
+    """All 256 byte values x scale edge cases (1, 0, the smallest subnormal, a
+    large finite value): element 2k = low nibble, 2k+1 = high nibble, each
+    (nib - 8) * sc rounded once to float32."""
+    packed = np.tile(np.arange(256, dtype=np.uint8), (4, 1))
     scales = np.array([[1.0] * 16, [0.0] * 16, [1.4e-45] * 16, [3.0e38] * 16], np.float32)
     d = oracle_lib.dequant_q4(packed, scales)
-    for r in range(4):
-        for b in (0, 1, 0x0F, 0xF0, 0x87, 0x78, 0xFF):
-            lo = (b & 15) - 8
-            hi = (b >> 4) - 8
-            assert d[r, 2 * b] == np.float32(np.float64(lo) * np.float64(scales[r, 0]))
-            assert d[r, 2 * b + 1] == np.float32(np.float64(hi) * np.float64(scales[r, 0]))
+    b = np.arange(256)
+    lo = ((b & 15) - 8).astype(np.float64)
+    hi = ((b >> 4) - 8).astype(np.float64)
+    with np.errstate(over="ignore"):
+        for r in range(4):
+            s = np.float64(scales[r, 0])
+            want = np.empty(512, np.float32)
+            want[0::2] = (lo * s).astype(np.float32)
+            want[1::2] = (hi * s).astype(np.float32)
+            assert np.array_equal(d[r].view(np.uint32), want.view(np.uint32)), r
+    # the closed form at the ends: byte 0x80 -> (-8, 0), byte 0x7F -> (7, -1)
+    assert d[0, 2 * 0x80] == -8.0 and d[0, 2 * 0x80 + 1] == 0.0
+    assert d[0, 2 * 0x7F] == 7.0 and d[0, 2 * 0x7F + 1] == -1.0
+    assert np.isinf(d[3, 0]) and d[3, 0] < 0  # -8 * 3e38 overflows float32
+
+
+def _q8_brute(x, sc):
+    """The nearest of the 255 levels q * sc (q in [-127, 127]) to each x, ties
+    to the even q; levels and distances in float64."""
+    q = np.arange(-127, 128, dtype=np.float64)
+    lv = q * np.float64(sc)
+    out = np.empty(x.size, np.int64)
+    for i, v in enumerate(x.astype(np.float64)):
+        err = np.abs(lv - v)
+        best = np.flatnonzero(err == err.min())
+        if best.size > 1:  # an exact tie between two levels: the even one
+            best = best[(q[best] % 2) == 0]
+        out[i] = int(q[best[0]])
+    return out
 
 
 def test_quant_q8_rules(oracle_lib, rng):
-    """Build-defined Q8 (no reference quantiser; parity unpinned): stated rule only."""
+    """Build-defined Q8 (the reference ships no Q8 quantiser): the scale is
+    float32(amax / 127) exactly (amax = max |x| of the span; 1 when amax is 0),
+    the element of largest magnitude maps to +-127, and every other element
+    to the nearest level (brute force over all 255 levels).  A scale of
+    amax / 126 or amax / 128, a truncating rounding or a clip at 128 fails
+    one of these."""
     x = (rng.standard_normal((4, 64)) * 0.02).astype(np.float32)
+    x[1, 5] = -np.abs(x[1]).max() * 1.5  # a negative maximum magnitude
+    x[2, :32] = 0.0  # an all-zero group
+    for quant, span in ((oracle_lib.quant_q8g32, 32), (oracle_lib.quant_q8row, 64)):
+        q, s = quant(x)
+        s = s.reshape(4, -1)
+        for r in range(4):
+            for g in range(64 // span):
+                xs = x[r, g * span:(g + 1) * span]
+                qs = q[r, g * span:(g + 1) * span].astype(np.int64)
+                amax = np.abs(xs).max()
+                if amax == 0:
+                    assert s[r, g] == 1.0 and (qs == 0).all()
+                    continue
+                assert s[r, g] == np.float32(np.float64(amax) / 127.0)
+                assert s[r, g] != np.float32(np.float64(amax) / 126.0)
+                k = int(np.argmax(np.abs(xs)))
+                assert qs[k] == (127 if xs[k] > 0 else -127)
+                # the division x / sc is float32 as in rintf(x / sc); brute
+                # force over levels agrees except where that float32 quotient
+                # lands on the other side of a half level (none in this data)
+                assert np.array_equal(qs, _q8_brute(xs, s[r, g]))
     q, s = oracle_lib.quant_q8g32(x)
-    assert q.dtype == np.int8 and np.abs(q).max() <= 127
-    d = oracle_lib.dequant_q8g32(q, s)
-    assert (np.abs(d - x) <= np.repeat(s, 32, axis=1) * 0.5000001).all()
     q2, s2 = pgw.quant_q8g32(x)
     assert np.array_equal(q, q2) and np.array_equal(s, s2)
     qr, sr = oracle_lib.quant_q8row(x)
     qr2, sr2 = pgw.quant_q8row(x)
     assert np.array_equal(qr, qr2) and np.array_equal(sr, sr2)
+    d = oracle_lib.dequant_q8g32(q, s)
+    assert (np.abs(d - x) <= np.repeat(s, 32, axis=1) * 0.5000001).all()
     dr = oracle_lib.dequant_q8row(qr, sr)
     assert (np.abs(dr - x) <= sr[:, None] * 0.5000001).all()
+
+
+def test_quant_q8_ties_to_even(oracle_lib):
+    """amax 127 gives sc = 1, so x = k + 0.5 is an exact tie: rint rounds to
+    the even neighbour (0.5 -> 0, 1.5 -> 2, -2.5 -> -2), and 127 -> 127."""
+    x = np.zeros((1, 32), np.float32)
+    x[0, :6] = [127.0, 0.5, 1.5, -2.5, 3.5, -0.5]
+    q, s = oracle_lib.quant_q8g32(x)
+    assert s[0, 0] == 1.0
+    assert list(q[0, :6]) == [127, 0, 2, -2, 4, 0]
