@@ -4,10 +4,9 @@
 // Q4 group-32 weights at batch 1 are read as 16-byte "chunks" (the 32
 // nibbles of one group of one row; scale[c] belongs to chunk c), so every
 // 128-bit load of a wavefront covers 1 KiB of contiguous memory.  The
-// activations are quantised per group to integers and dotted with the
-// nibbles by the byte/nibble dot instructions (no MFMA): the decode engine
-// uses 16-bit records (QX, below), the standalone GEMV of mllm_ops.hip 24-bit
-// ones.  Per-chunk partials are summed per row in a fixed order that does not
+// activations are quantised per group to 24-bit integers (Q6 records, below)
+// and dotted with the nibbles by the 4-bit dot instruction (no MFMA), in the
+// decode engine and in the standalone GEMV alike.  Per-chunk partials are summed per row in a fixed order that does not
 // depend on how rows or tokens are split across workgroups, so a row's value
 // is the same in every launch shape (the verify pass relies on it).
 #pragma once
@@ -120,97 +119,128 @@ __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F7
 
 // Tagged values.  A value handed from one workgroup to another inside the
 // persistent kernel travels with the tag of the (step, layer) that wrote it,
-// in the same naturally aligned access: a 64-bit (float bits, tag) pair, or a
-// 16-byte quad of three floats and the tag (the residual partials).  Such an
-// access reaches memory whole, so a reader that sees the tag it waits for also
-// sees that writer's values, and polling the data replaces a completion wait
-// plus a flag.  (For the quads this rests on the 16-byte stores and loads
-// being observed whole on this device; torn quads were searched for and not
-// seen.)  Tags grow across launches and are compared modulo 2^32.
+// as one naturally aligned 64-bit (float bits, tag) pair, written by one
+// 64-bit store and read by one 64-bit load with the device-scope (sc1)
+// policy.  That pair of instructions is what the AMDGPU memory model (the
+// GFX942-family mapping LLVM implements for gfx950) emits for a relaxed
+// agent-scope atomic 64-bit store and load -- "buffer/global/flat_store
+// sc1=1", "buffer/global/flat_load sc1=1" -- so each access is single-copy
+// atomic: a reader that sees the tag it waits for also sees the value written
+// with it, and polling the data replaces a completion wait plus a flag.
+// (The buffer form keeps the wave-uniform base in scalar registers; a
+// __hip_atomic_load of the same address compiles to the global form of the
+// same instruction but holds a 64-bit address per value in VGPRs.)  Tags grow
+// across launches and are compared modulo 2^32.
 __device__ __forceinline__ bool tag_ok(uint32_t tag, int want) { return (int)(tag - (uint32_t)want) >= 0; }
-__device__ __forceinline__ uint2 tagged(float v, int tag) { return make_uint2(__float_as_uint(v), (uint32_t)tag); }
+// Element i of a row of pairs at a wave-uniform base.
+__device__ __forceinline__ uint2 tag_ld(const uint2 *base, uint32_t i) { return coh_ld8(base, i * 8u); }
+__device__ __forceinline__ void tag_st(uint2 *base, uint32_t i, float v, int tag) {
+  coh_st8(base, i * 8u, make_uint2(__float_as_uint(v), (uint32_t)tag));
+}
 // A compiler barrier for polling loops: the loads after it are issued again
 // on every iteration instead of being hoisted out of the loop.
 __device__ __forceinline__ void poll_fence() { asm volatile("" ::: "memory"); }
 
-// ---------------------------------------------------------------- integer group dots
-// The decode engine's GEMVs take their activations quantised per 32-element
-// group (the Q4 group) to int16: xi = rint(x * 32767 / amax), scale
-// sx = amax / 32767 (amax = max |x| of the group; 0 for an all-zero group).
-// Splitting xi = 256 * hi + lo (hi signed, lo unsigned bytes) turns the
-// group's dot with the nibbles into byte dot products that are exact in
-// int32:
-//   sum_k (q_k - 8) * xi_k = 256 * sdot4(q, hi) + udot4(q, lo) - 8 * sum_k xi_k
-// A packed dword of the weights holds elements 8j .. 8j+7 (byte b: element
-// 8j+2b in the low nibble, 8j+2b+1 in the high one), so the activations are
-// stored per group as a QX record of QXR dwords:
-//   [0..3]  high bytes of the even elements 8j, 8j+2, 8j+4, 8j+6 (dword j)
-//   [4..7]  high bytes of the odd elements
-//   [8..11] low bytes of the even elements, [12..15] of the odd ones
-//   [16] sx (float bits), [17] sum of xi, [18..19] padding
-// The group's contribution to a row is then ((float)dot * sx) * w_scale:
-// about 34 VALU operations per 32 weights instead of 80 for float
-// dequantisation.  The only rounding is that of x to 16 bits (relative
-// 1.5e-5 per element).
-constexpr int QXR = 20;
+// ---------------------------------------------------------------- integer group dots (Q6 records)
+// Every Q4 GEMV of this library takes its activations as 24-bit integers
+// per 32-element group (the Q4 group): xi = rint(x * Q6MAX / amax), with the
+// group's scale sx = amax / Q6MAX (amax = max |x| of the group; 0 for an
+// all-zero group).  Rounding x to 24 bits moves it by at most
+// amax / (2 Q6MAX) = 6.4e-8 amax: the size of one float32 rounding of the
+// group's largest element, so the products keep float32 accuracy.
+//
+// Each xi is held as six signed 4-bit digits, xi = sum_k 16^k d_k with
+// d_k in [-8, 7].  Flipping bit 3 of a stored nibble q gives the signed
+// nibble q - 8, so one v_dot8_i32_i4 per 8 weights and digit plane yields
+//   dot = sum_k 16^k sum_e (q_e - 8) d_{k,e} = sum_e (q_e - 8) xi_e,
+// exact in int32: |dot| <= 32 * 8 * Q6MAX < 2^31 (the Horner partial sums may
+// wrap; the final value does not).  The group adds ((float)dot * sx) * w_scale
+// to its row: 4 XOR, 24 dot8, 5 shifts, a convert and 2 multiplies per 32
+// weights.
+//
+// Digits: with u = xi + Q6C (Q6C = 8 (16^6 - 1) / 15, so u >= 0), digit k of
+// xi is hex digit k of u minus 8, i.e. its 4-bit pattern is bfe(u, 4k, 4) ^ 8.
+//
+// A group's record is Q6R dwords: plane k (k = 0 .. 5) is dwords 4k .. 4k+3,
+// dword j of a plane holding the digits of elements 8j .. 8j+7 (element 8j+i
+// in nibble i, the weights' own nibble order); dword 24 is sx; 25 .. 27 pad
+// the record to 16-byte alignment.
+constexpr int Q6R = 28;
+constexpr int Q6C = 8947848;         // 8 * (16^6 - 1) / 15
+constexpr float Q6MAX = 7829360.0f;  // below 7 * (16^6 - 1) / 15 = 7829367 by more than the rcp rounding
 
-__device__ __forceinline__ float q4_qx_part(const uint4 w, const uint32_t *__restrict__ rec, float ws) {
-  const uint4 he = *reinterpret_cast<const uint4 *>(rec), ho = *reinterpret_cast<const uint4 *>(rec + 4);
-  const uint4 le = *reinterpret_cast<const uint4 *>(rec + 8), lo = *reinterpret_cast<const uint4 *>(rec + 12);
-  const uint2 sc = *reinterpret_cast<const uint2 *>(rec + 16);
-  const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
-  const uint32_t xhe[4] = {he.x, he.y, he.z, he.w}, xho[4] = {ho.x, ho.y, ho.z, ho.w};
-  const uint32_t xle[4] = {le.x, le.y, le.z, le.w}, xlo[4] = {lo.x, lo.y, lo.z, lo.w};
-  int h = 0;
-  uint32_t l = 0;
+__device__ __forceinline__ float q6_inv(float amax) { return amax > 0.f ? Q6MAX * __builtin_amdgcn_rcpf(amax) : 0.f; }
+__device__ __forceinline__ uint32_t q6_u(float v, float inv) { return (uint32_t)((int)__builtin_rintf(v * inv) + Q6C); }
+
+// One 16-byte chunk (the 32 weights of one group of one row) against a
+// group's digit planes xr[24], activation scale sx and weight scale ws.
+__device__ __forceinline__ float q4_dot6(const uint4 w, const uint32_t (&xr)[24], float sx, float ws) {
+  const int d[4] = {(int)(w.x ^ 0x88888888u), (int)(w.y ^ 0x88888888u), (int)(w.z ^ 0x88888888u),
+                    (int)(w.w ^ 0x88888888u)};
+  int acc = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t ev = dw[j] & 0x0F0F0F0Fu, od = (dw[j] >> 4) & 0x0F0F0F0Fu;
-    h = __builtin_amdgcn_sdot4((int)ev, (int)xhe[j], h, false);
-    h = __builtin_amdgcn_sdot4((int)od, (int)xho[j], h, false);
-    l = __builtin_amdgcn_udot4(ev, xle[j], l, false);
-    l = __builtin_amdgcn_udot4(od, xlo[j], l, false);
+  for (int k = 5; k >= 0; --k) {
+    if (k < 5) acc = (int)((uint32_t)acc << 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_sdot8(d[j], (int)xr[4 * k + j], acc, false);
   }
-  const int dot = h * 256 + (int)l - 8 * (int)sc.y;
-  return ((float)dot * __uint_as_float(sc.x)) * ws;
+  return ((float)acc * sx) * ws;
 }
 
-// The same with the group's record held in registers (x16: dwords 0..15,
-// sx, xs = sum of xi), e.g. for the gate and up rows of one unit.
-struct QxRec {
-  uint32_t d[16];
+// A group's record held in registers (e.g. a thread's one group of a tile).
+struct Q6Rec {
+  uint32_t d[24];
   float sx;
-  int xs;
 };
-__device__ __forceinline__ QxRec qx_load(const uint32_t *__restrict__ rec) {
-  QxRec r;
+__device__ __forceinline__ Q6Rec q6_load(const uint32_t *__restrict__ rec) {
+  Q6Rec r;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < 6; ++k) {
     const uint4 v = *reinterpret_cast<const uint4 *>(rec + 4 * k);
     r.d[4 * k] = v.x;
     r.d[4 * k + 1] = v.y;
     r.d[4 * k + 2] = v.z;
     r.d[4 * k + 3] = v.w;
   }
-  const uint2 sc = *reinterpret_cast<const uint2 *>(rec + 16);
-  r.sx = __uint_as_float(sc.x);
-  r.xs = (int)sc.y;
+  r.sx = __uint_as_float(rec[24]);
   return r;
 }
-__device__ __forceinline__ float q4_qx_part_reg(const uint4 w, const QxRec &r, float ws) {
-  const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
-  int h = 0;
-  uint32_t l = 0;
+__device__ __forceinline__ float q4_dot6(const uint4 w, const Q6Rec &r, float ws) { return q4_dot6(w, r.d, r.sx, ws); }
+
+// C chunks of one group against that group's record in LDS, taken digit
+// plane by digit plane, so that at most one plane of the record is held in
+// registers beside the chunks: out[j] is q4_dot6 of chunk j, bit for bit
+// (the same dot instructions in the same order).
+template <int C>
+__device__ __forceinline__ void q4_dot6_planes(const uint4 (&w)[C], const float (&ws)[C],
+                                               const uint32_t *__restrict__ rec, float (&out)[C]) {
+  int acc[C];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t ev = dw[j] & 0x0F0F0F0Fu, od = (dw[j] >> 4) & 0x0F0F0F0Fu;
-    h = __builtin_amdgcn_sdot4((int)ev, (int)r.d[j], h, false);
-    h = __builtin_amdgcn_sdot4((int)od, (int)r.d[4 + j], h, false);
-    l = __builtin_amdgcn_udot4(ev, r.d[8 + j], l, false);
-    l = __builtin_amdgcn_udot4(od, r.d[12 + j], l, false);
+  for (int j = 0; j < C; ++j) acc[j] = 0;
+#pragma unroll
+  for (int k = 5; k >= 0; --k) {
+    const uint4 v = *reinterpret_cast<const uint4 *>(rec + 4 * k);
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      if (k < 5) acc[j] = (int)((uint32_t)acc[j] << 4);
+      acc[j] = __builtin_amdgcn_sdot8((int)(w[j].x ^ 0x88888888u), (int)v.x, acc[j], false);
+      acc[j] = __builtin_amdgcn_sdot8((int)(w[j].y ^ 0x88888888u), (int)v.y, acc[j], false);
+      acc[j] = __builtin_amdgcn_sdot8((int)(w[j].z ^ 0x88888888u), (int)v.z, acc[j], false);
+      acc[j] = __builtin_amdgcn_sdot8((int)(w[j].w ^ 0x88888888u), (int)v.w, acc[j], false);
+    }
   }
-  const int dot = h * 256 + (int)l - 8 * r.xs;
-  return ((float)dot * r.sx) * ws;
+  const float sx = __uint_as_float(rec[24]);
+#pragma unroll
+  for (int j = 0; j < C; ++j) out[j] = ((float)acc[j] * sx) * ws[j];
+}
+
+// One chunk against a record in LDS.
+__device__ __forceinline__ float q4_dot6(const uint4 w, const uint32_t *__restrict__ rec, float ws) {
+  const uint4 wa[1] = {w};
+  const float sa[1] = {ws};
+  float o[1];
+  q4_dot6_planes<1>(wa, sa, rec, o);
+  return o[0];
 }
 
 // Cross-lane moves through DPP (a VALU operand modifier) instead of
@@ -401,17 +431,12 @@ __device__ __forceinline__ float row_sum(const float *p, int n) {
   return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
 }
 
-// ---------------------------------------------------------------- activation staging (QX)
-// Max / sum over the 8 lanes of each half-row (lanes 8k .. 8k+7).
+// ---------------------------------------------------------------- activation staging (Q6 records)
+// Max over the 8 lanes of each half-row (lanes 8k .. 8k+7).
 __device__ __forceinline__ float max8(float v) {
   v = fmaxf(v, dpp_f<0xB1>(v));
   v = fmaxf(v, dpp_f<0x4E>(v));
   return fmaxf(v, dpp_f<0x141>(v));
-}
-__device__ __forceinline__ int sum8i(int v) {
-  v = v + dpp_i<0xB1>(v);
-  v = v + dpp_i<0x4E>(v);
-  return v + dpp_i<0x141>(v);
 }
 // The sum of a row's ng partials p[0 .. ng) on 4 lanes (s = lane & 3):
 // lane s adds partials s, s + 4, ... in order (from +0), then a fixed 4-lane
@@ -429,56 +454,47 @@ __device__ __forceinline__ float sum8f(float v) {
   v = v + dpp_f<0x4E>(v);
   return v + dpp_f<0x141>(v);
 }
-__device__ __forceinline__ float qx_inv(float amax) { return amax > 0.f ? 32767.0f / amax : 0.f; }
-__device__ __forceinline__ int qx_round(float v, float inv) { return (int)__builtin_rintf(v * inv); }
 
-// A row staged by one thread per float4 column q (elements 4q .. 4q+3, the
-// group's columns on 8 neighbouring lanes): the QX records of the row's
-// groups at qx.  Called by whole waves (DPP); `in` marks real columns.
-__device__ __forceinline__ void qx_stage_col(float4 y, bool in, int q, uint32_t *qx) {
+// A row staged by one thread per float4 column q (elements 4q .. 4q+3 of
+// group q >> 3; a group's columns are 8 neighbouring lanes): the Q6 records
+// of the row's groups at rec0.  Called by whole waves (DPP); `in` marks real
+// columns (lanes past the row take part in the max with zeros).
+__device__ __forceinline__ void q6_stage_col(float4 y, bool in, int q, uint32_t *rec0) {
   if (!in) y = make_float4(0.f, 0.f, 0.f, 0.f);
   const float a = max8(fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
-  const float inv = qx_inv(a);
-  const int x0 = qx_round(y.x, inv), x1 = qx_round(y.y, inv), x2 = qx_round(y.z, inv), x3 = qx_round(y.w, inv);
-  const int s = sum8i((x0 + x1) + (x2 + x3));
-  if (in) {
-    uint32_t *rec = qx + (q >> 3) * QXR;
-    uint8_t *rb = reinterpret_cast<uint8_t *>(rec);
-    const int off = 4 * ((q & 7) >> 1) + 2 * (q & 1);  // even/odd element slots of this column
-    *reinterpret_cast<unsigned short *>(rb + off) = (unsigned short)(((x0 >> 8) & 255) | (((x2 >> 8) & 255) << 8));
-    *reinterpret_cast<unsigned short *>(rb + 16 + off) = (unsigned short)(((x1 >> 8) & 255) | (((x3 >> 8) & 255) << 8));
-    *reinterpret_cast<unsigned short *>(rb + 32 + off) = (unsigned short)((x0 & 255) | ((x2 & 255) << 8));
-    *reinterpret_cast<unsigned short *>(rb + 48 + off) = (unsigned short)((x1 & 255) | ((x3 & 255) << 8));
-    if ((q & 7) == 0) {
-      rec[16] = __float_as_uint(a / 32767.0f);
-      rec[17] = (uint32_t)s;
-    }
+  const float inv = q6_inv(a);
+  const uint32_t u0 = q6_u(y.x, inv), u1 = q6_u(y.y, inv), u2 = q6_u(y.z, inv), u3 = q6_u(y.w, inv);
+  if (!in) return;
+  uint32_t *rec = rec0 + (q >> 3) * Q6R;
+  uint8_t *rb = reinterpret_cast<uint8_t *>(rec);
+  // column q holds elements 4(q & 7) .. +3: dword (q & 7) >> 1 of a plane, its
+  // low or high 16 bits
+  const int off = 4 * ((q & 7) >> 1) + 2 * (q & 1);
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    const uint32_t v = __builtin_amdgcn_ubfe(u0, 4 * k, 4) | (__builtin_amdgcn_ubfe(u1, 4 * k, 4) << 4) |
+                       (__builtin_amdgcn_ubfe(u2, 4 * k, 4) << 8) | (__builtin_amdgcn_ubfe(u3, 4 * k, 4) << 12);
+    *reinterpret_cast<unsigned short *>(rb + 16 * k + off) = (unsigned short)(v ^ 0x8888u);
   }
+  if ((q & 7) == 0) rec[24] = __float_as_uint(a * (1.0f / Q6MAX));
 }
 
 // 64 values, one per lane of the calling wave (lane r: element r & 31 of
-// group r >> 5): the two QX records at qx.  Called by the whole wave.
-__device__ __forceinline__ void qx_stage_lanes(float v, uint32_t *qx) {
-  const int r = lane_id64(), k = r & 31;
+// group r >> 5): the two Q6 records at rec0.  Called by the whole wave.
+__device__ __forceinline__ void q6_stage_lanes(float v, uint32_t *rec0) {
+  const int r = lane_id64(), e = r & 31;
   const float m16 = row16_max(fabsf(v));
   const float a = r < 32 ? fmaxf(readlane_f(m16, 0), readlane_f(m16, 16))
                          : fmaxf(readlane_f(m16, 32), readlane_f(m16, 48));
-  const int xi = qx_round(v, qx_inv(a));
-  int s16 = xi;
-  s16 = s16 + dpp_i<0xB1>(s16);
-  s16 = s16 + dpp_i<0x4E>(s16);
-  s16 = s16 + dpp_i<0x141>(s16);
-  s16 = s16 + dpp_i<0x140>(s16);
-  const int s = r < 32 ? __builtin_amdgcn_readlane(s16, 0) + __builtin_amdgcn_readlane(s16, 16)
-                       : __builtin_amdgcn_readlane(s16, 32) + __builtin_amdgcn_readlane(s16, 48);
-  uint32_t *rec = qx + (r >> 5) * QXR;
-  uint8_t *rb = reinterpret_cast<uint8_t *>(rec);
-  const int off = 16 * (k & 1) + 4 * (k >> 3) + ((k & 7) >> 1);
-  rb[off] = (uint8_t)((xi >> 8) & 255);
-  rb[32 + off] = (uint8_t)(xi & 255);
-  if (k == 0) {
-    rec[16] = __float_as_uint(a / 32767.0f);
-    rec[17] = (uint32_t)s;
+  const uint32_t u = q6_u(v, q6_inv(a));
+  const uint32_t uo = (uint32_t)dpp_i<0xB1>((int)u);  // the odd neighbour's (lane ^ 1)
+  if ((e & 1) == 0) {
+    // elements e, e + 1: byte (e & 7) >> 1 of dword e >> 3 of each plane
+    uint8_t *rb = reinterpret_cast<uint8_t *>(rec0 + (r >> 5) * Q6R) + 4 * (e >> 3) + ((e & 7) >> 1);
+#pragma unroll
+    for (int k = 0; k < 6; ++k)
+      rb[16 * k] = (uint8_t)((__builtin_amdgcn_ubfe(u, 4 * k, 4) | (__builtin_amdgcn_ubfe(uo, 4 * k, 4) << 4)) ^ 0x88u);
+    if (e == 0) rec0[(r >> 5) * Q6R + 24] = __float_as_uint(a * (1.0f / Q6MAX));
   }
 }
 
@@ -524,10 +540,10 @@ __device__ __forceinline__ void tile_load_strided(const Q4Mat &W, int r0, int nr
   }
 }
 
-// tile_compute with the activations staged as QX records (m tokens x ng
-// groups).
+// A tile against activations staged as Q6 records (m tokens x ng groups):
+// chunk partials to part, then the row sums in row_sum's order to out.
 template <int C, int NT = WG>
-__device__ __forceinline__ void tile_compute_qx(const TileRegs<C> &R, int nrows, int ng, int nch, int m,
+__device__ __forceinline__ void tile_compute_q6(const TileRegs<C> &R, int nrows, int ng, int nch, int m,
                                                 const uint32_t *qx, int gfirst, int gstep, float *part, float *out,
                                                 int ostride) {
   int gj[C];
@@ -544,7 +560,7 @@ __device__ __forceinline__ void tile_compute_qx(const TileRegs<C> &R, int nrows,
 #pragma unroll
     for (int j = 0; j < C; ++j) {
       const int c = tid() + j * NT;
-      if (c < nch) part[t * nch + c] = q4_qx_part(R.w[j], qx + (t * ng + gj[j]) * QXR, R.s[j]);
+      if (c < nch) part[t * nch + c] = q4_dot6(R.w[j], qx + (t * ng + gj[j]) * Q6R, R.s[j]);
     }
   }
   __syncthreads();

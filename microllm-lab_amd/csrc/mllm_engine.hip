@@ -28,8 +28,8 @@
 // The split-K partials are summed by their consumer in a fixed order, so
 // every result is deterministic.  Every GEMV issues its weight loads before
 // it stages its activations, so the two memory latencies overlap.  The GEMVs
-// take their activations as 16-bit integer records per 32-element group and
-// use byte dot products (QX, mllm_device.h).
+// take their activations as 24-bit integer records per 32-element group and
+// use 4-bit dot products (Q6 records, mllm_device.h).
 //
 // Execution modes, all running the same per-item device code:
 //   3 (default where the device co-schedules one 1024-thread workgroup per
@@ -135,8 +135,8 @@ struct DecParams {
   const float *last_mproj_b;  // gpt2: mlp.proj bias of the last layer
   uint2 *xa;      // [MAXT][D] tagged residual entering the attention block
   uint2 *xb;      // [MAXT][D] tagged residual entering the MLP block
-  uint4 *opart;   // [MAXT][NH][nquads(D)] per-head partials of W_o . att, tagged quads
-  uint4 *dpart;   // [MAXT][nchunk][nquads(D)] per-chunk partials of W_2 . h, tagged quads
+  uint2 *opart;   // [MAXT][NH][D] per-head partials of W_o . att, tagged pairs
+  uint2 *dpart;   // [MAXT][nchunk][D] per-chunk partials of W_2 . h, tagged pairs
   float *xn;      // [MAXT][D] final-normed rows for the lm_head
   float *q;       // [MAXT][NH*HD] queries after RoPE
   void *kv;       // [L][2][NKV][max_seq][HD] (f32 or f16)
@@ -157,11 +157,6 @@ struct Step {
   int tag;    // tag of layer 0's handoff values; layer li writes tag + li
 };
 constexpr int TAGL = 128;  // tags per step (layers < TAGL)
-// A tagged quad holds three consecutive values of a partial row and their
-// tag, (v0, v1, v2, tag): one 16-byte store by one lane, read by 16-byte loads
-// (a lane's aligned 16 bytes travel as one request to one cache line).  A
-// row of D values is nquads(D) quads; values past D are 0.
-__host__ __device__ constexpr int nquads(int D) { return (D + 2) / 3; }
 
 // The pass state is read and written with coherent access: inside the
 // persistent kernel ARGMAX updates it for workgroups on other XCDs.
@@ -227,17 +222,19 @@ __device__ __forceinline__ void gains_store(const DecParams &P, const float *bia
 //   x = base + (((B_0 + B_1) + ... + B_{nb-1}) + bias)
 // where B_b sums parts[p] for p in [b*PB, min(np, (b+1)*PB)) in ascending p
 // (from +0).  The order of every addition is fixed by np alone.
-// The partials are rows of tagged quads (nq3 = nquads(D) per row).  The
-// block sums use every thread of a 1024-thread workgroup: item it = b * nq3
-// + c (round it / 1024) forms B_b of values 3c .. 3c+2 into blk[b*D + 3c ..]
-// (LDS).  A round's loads all go out before its first add, so a round costs
-// one memory latency; round 0 can be loaded ahead (resid_blocks_load) so its
-// latency overlaps the weight loads.  With POLL (persistent kernel) a round
-// is loaded again until every quad carries a tag of at least `want`.
-// Branch-free: an item or partial past the end reads partial 0 of column 0
+// The partials are rows of D tagged pairs.  The block sums use every thread
+// of a 1024-thread workgroup: item it = b * (D / 2) + c (round it / 1024)
+// forms B_b of columns c and c + D / 2 into blk[b*D + c] and
+// blk[b*D + c + D/2] (LDS), so each load instruction of a wave reads 64
+// consecutive pairs.  A round's
+// loads all go out before its first add, so a round costs one memory
+// latency; round 0 can be loaded ahead (resid_blocks_load) so its latency
+// overlaps the weight loads.  With POLL (persistent kernel) a round is loaded
+// again until every pair carries a tag of at least `want`.
+// Branch-free: an item or partial past the end reads pair 0 of partial 0
 // (valid memory) and is left out.
 struct ResidReg {
-  uint4 v[PB];
+  uint2 v[2 * PB];
 };
 
 // Spin bound of the data polls: as kSpinLimit for flags; on time-out (or
@@ -245,30 +242,31 @@ struct ResidReg {
 __device__ __forceinline__ bool poll_give_up(const DecParams &P, unsigned spins);
 
 template <bool POLL>
-__device__ __forceinline__ void resid_blocks_load(const DecParams &P, const uint4 *pt, int nq3, int np, int round,
-                                                  int want, ResidReg &R) {
-  const int nitems = nq3 * ((np + PB - 1) / PB);
+__device__ __forceinline__ void resid_blocks_load(const DecParams &P, const uint2 *pt, int np, int round, int want,
+                                                  ResidReg &R) {
+  const int D = P.D, nc2 = D >> 1, nitems = nc2 * ((np + PB - 1) / PB);
   const int it = tid() + round * 1024;
-  const int b = it / nq3, c = it - b * nq3;
+  const int b = it / nc2, c = it - b * nc2;
+  auto load = [&] {
 #pragma unroll
-  for (int k = 0; k < PB; ++k) {
-    const int p = b * PB + k;
-    const bool ok = it < nitems && p < np;
-    R.v[k] = coh_ld16(pt, 16u * (ok ? (uint32_t)(p * nq3 + c) : 0u));
-  }
+    for (int k = 0; k < PB; ++k) {
+      const int p = b * PB + k;
+      const bool ok = it < nitems && p < np;
+      const uint32_t e = ok ? (uint32_t)(p * D + c) : 0u;
+      R.v[2 * k] = tag_ld(pt, e);
+      R.v[2 * k + 1] = tag_ld(pt, e + (ok ? (uint32_t)nc2 : 0u));
+    }
+  };
+  load();
   if (POLL) {
     for (unsigned spins = 1;; ++spins) {
       bool ready = true;
 #pragma unroll
-      for (int k = 0; k < PB; ++k) ready &= !(it < nitems && b * PB + k < np) || tag_ok(R.v[k].w, want);
+      for (int k = 0; k < PB; ++k)
+        ready &= !(it < nitems && b * PB + k < np) || (tag_ok(R.v[2 * k].y, want) && tag_ok(R.v[2 * k + 1].y, want));
       if (ready || poll_give_up(P, spins)) break;
       poll_fence();
-#pragma unroll
-      for (int k = 0; k < PB; ++k) {
-        const int p = b * PB + k;
-        const bool ok = it < nitems && p < np;
-        R.v[k] = coh_ld16(pt, 16u * (ok ? (uint32_t)(p * nq3 + c) : 0u));
-      }
+      load();
     }
   }
 }
@@ -277,45 +275,41 @@ __device__ __forceinline__ void resid_blocks_load(const DecParams &P, const uint
 // conditional): a load consumed inside a divergent branch leaves the
 // compiler unsure it has completed, and it then waits for every load in
 // flight before the register is reused.
-__device__ __forceinline__ void resid_blocks_add(int D, int nq3, int np, int round, const ResidReg &R, float *blk) {
-  const int nitems = nq3 * ((np + PB - 1) / PB);
+__device__ __forceinline__ void resid_blocks_add(int D, int np, int round, const ResidReg &R, float *blk) {
+  const int nc2 = D >> 1, nitems = nc2 * ((np + PB - 1) / PB);
   const int it = tid() + round * 1024;
-  const int b = it / nq3, c = it - b * nq3;
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+  const int b = it / nc2, c = it - b * nc2;
+  float a0 = 0.f, a1 = 0.f;
 #pragma unroll
   for (int k = 0; k < PB; ++k) {
-    const uint4 w = R.v[k];
     const bool use = b * PB + k < np;
-    a0 = a0 + (use ? __uint_as_float(w.x) : 0.f);
-    a1 = a1 + (use ? __uint_as_float(w.y) : 0.f);
-    a2 = a2 + (use ? __uint_as_float(w.z) : 0.f);
+    a0 = a0 + (use ? __uint_as_float(R.v[2 * k].x) : 0.f);
+    a1 = a1 + (use ? __uint_as_float(R.v[2 * k + 1].x) : 0.f);
   }
   if (it < nitems) {
-    float *o = blk + b * D + 3 * c;
-    o[0] = a0;
-    if (3 * c + 1 < D) o[1] = a1;
-    if (3 * c + 2 < D) o[2] = a2;
+    blk[b * D + c] = a0;
+    blk[b * D + c + nc2] = a1;
   }
 }
 
 // Every round of the block sums, round 0 already loaded into R0.
 template <bool POLL>
-__device__ __forceinline__ void resid_blocks_rest(const DecParams &P, const uint4 *pt, int np, int want,
+__device__ __forceinline__ void resid_blocks_rest(const DecParams &P, const uint2 *pt, int np, int want,
                                                   const ResidReg &R0, float *blk) {
-  const int D = P.D, nq3 = nquads(D);
-  resid_blocks_add(D, nq3, np, 0, R0, blk);
-  const int nitems = nq3 * ((np + PB - 1) / PB);
+  const int D = P.D;
+  resid_blocks_add(D, np, 0, R0, blk);
+  const int nitems = (D >> 1) * ((np + PB - 1) / PB);
   for (int round = 1; round * 1024 < nitems; ++round) {
     ResidReg R1;
-    resid_blocks_load<POLL>(P, pt, nq3, np, round, want, R1);
-    resid_blocks_add(D, nq3, np, round, R1, blk);
+    resid_blocks_load<POLL>(P, pt, np, round, want, R1);
+    resid_blocks_add(D, np, round, R1, blk);
   }
 }
 
 template <bool POLL>
-__device__ __forceinline__ void resid_blocks(const DecParams &P, const uint4 *pt, int np, int want, float *blk) {
+__device__ __forceinline__ void resid_blocks(const DecParams &P, const uint2 *pt, int np, int want, float *blk) {
   ResidReg R0;
-  resid_blocks_load<POLL>(P, pt, nquads(P.D), np, 0, want, R0);
+  resid_blocks_load<POLL>(P, pt, np, 0, want, R0);
   resid_blocks_rest<POLL>(P, pt, np, want, R0, blk);
 }
 
@@ -326,7 +320,7 @@ __device__ __forceinline__ void resid_blocks(const DecParams &P, const uint4 *pt
 // x * (1/sqrt(mean(x^2) + eps)) * w) or LayerNorm (infer.js:147-164,
 // eps 1e-5): each wave sums its columns with DPP, the waves' sums are added
 // in order.  1/sqrt is the hardware reciprocal square root.  The
-// normalised row is staged as QX records at qx_t (when set).  The gains (LayerNorm:
+// normalised row is staged as Q6 records at qx_t (when set).  The gains (LayerNorm:
 // gamma || beta) and the bias are in gl[0, 2D) and gl[2D, 3D).  Every
 // thread of the workgroup must call it (it holds barriers); red needs
 // 2 x 16 floats.
@@ -364,9 +358,11 @@ __device__ __forceinline__ void col_norm(const DecParams &P, float4 x, const flo
   const int D = P.D, nq = D >> 2, q = tid(), nw = (nq + 63) >> 6;
   const bool in = q < nq;
   if (!in) x = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (o.x && in) {
-    coh_st16(o.x, 32u * q, make_uint4(__float_as_uint(x.x), (uint32_t)o.tag, __float_as_uint(x.y), (uint32_t)o.tag));
-    coh_st16(o.x, 32u * q + 16u, make_uint4(__float_as_uint(x.z), (uint32_t)o.tag, __float_as_uint(x.w), (uint32_t)o.tag));
+  if (o.x && in) {  // element 4q + j at pair j * nq + q (col_base_load)
+    tag_st(o.x, q, x.x, o.tag);
+    tag_st(o.x, nq + q, x.y, o.tag);
+    tag_st(o.x, 2 * nq + q, x.z, o.tag);
+    tag_st(o.x, 3 * nq + q, x.w, o.tag);
   }
   const float inv_d = 1.0f / (float)D;
   const float4 *g4 = reinterpret_cast<const float4 *>(gl);
@@ -388,25 +384,29 @@ __device__ __forceinline__ void col_norm(const DecParams &P, float4 x, const flo
   }
   if (!in) y = make_float4(0.f, 0.f, 0.f, 0.f);
   if (o.y && in) coh_st4(o.y, 16u * q, y);
-  if (qx_t && wave_id() < nw) qx_stage_col(y, in, q, qx_t);
+  if (qx_t && wave_id() < nw) q6_stage_col(y, in, q, qx_t);
 }
 
-// The base column of this thread from a tagged row (coherent loads,
-// branch-free); with POLL, loaded again until its tags reach `want`.
+// The base column of this thread from a tagged row (branch-free); with POLL,
+// loaded again until its tags reach `want`.  A residual row of D pairs
+// keeps element 4q + j at pair j * nq + q (nq = D / 4), so each of the four
+// load instructions of a wave reads 64 consecutive pairs.
 template <bool POLL>
 __device__ __forceinline__ float4 col_base_load(const DecParams &P, const uint2 *base, int nq, int want) {
-  const uint32_t q = (uint32_t)min(tid(), nq - 1);
-  uint4 a = coh_ld16(base, 32u * q), b = coh_ld16(base, 32u * q + 16u);
+  const uint32_t b = (uint32_t)min(tid(), nq - 1), n = (uint32_t)nq;
+  uint2 v0 = tag_ld(base, b), v1 = tag_ld(base, b + n), v2 = tag_ld(base, b + 2 * n), v3 = tag_ld(base, b + 3 * n);
   if (POLL && tid() < nq) {
-    for (unsigned spins = 1; !(tag_ok(a.y, want) && tag_ok(a.w, want) && tag_ok(b.y, want) && tag_ok(b.w, want)) &&
+    for (unsigned spins = 1; !(tag_ok(v0.y, want) && tag_ok(v1.y, want) && tag_ok(v2.y, want) && tag_ok(v3.y, want)) &&
                              !poll_give_up(P, spins);
          ++spins) {
       poll_fence();
-      a = coh_ld16(base, 32u * q);
-      b = coh_ld16(base, 32u * q + 16u);
+      v0 = tag_ld(base, b);
+      v1 = tag_ld(base, b + n);
+      v2 = tag_ld(base, b + 2 * n);
+      v3 = tag_ld(base, b + 3 * n);
     }
   }
-  return make_float4(__uint_as_float(a.x), __uint_as_float(a.z), __uint_as_float(b.x), __uint_as_float(b.z));
+  return make_float4(__uint_as_float(v0.x), __uint_as_float(v1.x), __uint_as_float(v2.x), __uint_as_float(v3.x));
 }
 
 // Per-chunk partials of a tile in registers for m staged tokens:
@@ -429,7 +429,7 @@ __device__ __forceinline__ void tile_partials(const TileRegs<C> &R, int ng, int 
 #pragma unroll
     for (int j = 0; j < C; ++j) {
       const int c = tid() + j * 1024;
-      if (c < nch) part[t * nch + c] = q4_qx_part(R.w[j], qx + (t * ng + gj[j]) * QXR, R.s[j]);
+      if (c < nch) part[t * nch + c] = q4_dot6(R.w[j], qx + (t * ng + gj[j]) * Q6R, R.s[j]);
       // one chunk at a time: the activations of several chunks in flight at
       // once would not fit beside the registers the caller holds (the other
       // waves of the SIMD hide the LDS latency)
@@ -441,29 +441,27 @@ __device__ __forceinline__ void tile_partials(const TileRegs<C> &R, int ng, int 
 // The same partials for one token, chunk c taken by thread c % S (S =
 // fixed_stride(ng), chunks loaded by tile_load3): every chunk of a thread is
 // of group tid % ng, so its activation record is read from LDS once.  The
-// partials have the arithmetic of tile_partials (q4_qx_part_reg).
+// partials have the arithmetic of tile_partials (q4_dot6).
 template <int C>
 __device__ __forceinline__ void tile_partials_fixed(const TileRegs<C> &R, int ng, int nch, const uint32_t *qx,
                                                     float *part) {
   const int S = fixed_stride(ng);
   if ((int)tid() < S) {
-    const QxRec xr = qx_load(qx + (tid() % ng) * QXR);
+    float o[C];
+    q4_dot6_planes<C>(R.w, R.s, qx + (tid() % ng) * Q6R, o);
 #pragma unroll
     for (int j = 0; j < C; ++j) {
       const int c = tid() + j * S;
-      if (c < nch) part[c] = q4_qx_part_reg(R.w[j], xr, R.s[j]);
+      if (c < nch) part[c] = o[j];
     }
   }
 }
 
-// A two-group column slice of a matrix with ng groups per row: chunk
-// c = 2r + j (r < rows, j < 2) is row r, group g0 + j.
 // A slice is two groups (64 columns, groups g0 and g0 + 1) of every row of
 // W.  Wave-slot ws = wave + (NT / 64) k (register k) takes rows
-// [RPW ws, RPW ws + RPW): lane L < 2 RPW holds the chunk of row RPW ws + L / 2,
-// group g0 + (L & 1).  RPW is a multiple of 3, so a wave-slot's rows make
-// whole tagged quads.
-constexpr int RPW = 30;
+// [RPW ws, RPW ws + RPW): lane L holds the chunk of row RPW ws + L / 2,
+// group g0 + (L & 1).
+constexpr int RPW = 32;
 template <int C, int NT>
 __device__ __forceinline__ void slice_load(const Q4Mat &W, int g0, int rows, TileRegs<C> &R) {
   const int ng = W.cols >> 5;
@@ -471,32 +469,28 @@ __device__ __forceinline__ void slice_load(const Q4Mat &W, int g0, int rows, Til
 #pragma unroll
   for (int k = 0; k < C; ++k) {
     const int ws = wv + k * (NT / 64);
-    const int r = min(RPW * ws + (min(L, 2 * RPW - 1) >> 1), rows - 1);  // branch-free; extra lanes unused
+    const int r = min(RPW * ws + (L >> 1), rows - 1);  // branch-free; rows past the end unused
     const size_t gc = (size_t)r * ng + g0 + (L & 1);
     R.w[k] = W.q[gc];
     R.s[k] = W.s[gc];
   }
 }
 
-// The slice against two staged groups (QX records v, v + QXR):
+// The slice against two staged groups (Q6 records v, v + Q6R):
 // row r = part(group g0) + part(group g0 + 1), the row_sum order of two
-// groups, stored as tagged quads (coherent 16-byte stores): lane 6Q of a
-// wave-slot stores the rows of lanes 6Q, 6Q + 2, 6Q + 4.  Every lane takes
-// part in the shuffles.
+// groups, stored as a tagged pair by the even lane of the row.  Every lane
+// takes part in the shuffle.
 template <int C, int NT>
-__device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const uint32_t *v, uint4 *out, int tag) {
+__device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const uint32_t *v, uint2 *out, int tag) {
   const int L = lane_id(), wv = wave_id();
 #pragma unroll
   for (int k = 0; k < C; ++k) {
     const int ws = wv + k * (NT / 64);
     const int r = RPW * ws + (L >> 1);
     float p = 0.f;
-    if (L < 2 * RPW && r < rows) p = q4_qx_part(R.w[k], v + (L & 1) * QXR, R.s[k]);
+    if (r < rows) p = q4_dot6(R.w[k], v + (L & 1) * Q6R, R.s[k]);
     const float sum = p + lane_xor1(p);  // rows past the end are 0
-    const float s1 = __shfl(sum, min(L + 2, 63)), s2 = __shfl(sum, min(L + 4, 63));
-    if (L % 6 == 0 && L < 2 * RPW && r < rows)
-      coh_st16(out, 16u * (uint32_t)((RPW / 3) * ws + L / 6),
-               make_uint4(__float_as_uint(sum), __float_as_uint(s1), __float_as_uint(s2), (uint32_t)tag));
+    if ((L & 1) == 0 && r < rows) tag_st(out, (uint32_t)r, sum, tag);
   }
 }
 
@@ -578,8 +572,8 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
   const int pos0 = st.pos0;
   const bool gpt2 = P.arch == 1;
   const int nb = (P.nchunk + PB - 1) / PB;
-  float *gl = smem, *part = gl + al4(3 * D) + m * ng * QXR;
-  uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // m x ng QX records
+  float *gl = smem, *part = gl + al4(3 * D) + m * ng * Q6R;
+  uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // m x ng Q6 records
   float *blk = part + m * nch;  // 2 x nb * D (alternating tokens), then red
   const float *rbias = gpt2 && li > 0 ? Lw.prev_mproj_b : nullptr;
   QkvPre Q;
@@ -599,7 +593,7 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
     // before the weight tile, so the prologue never waits for the weights
     if (li > 0) {
       base = col_base_load<false>(P, P.xb, nq, 0);
-      resid_blocks_load<false>(P, P.dpart, nquads(D), P.nchunk, 0, 0, R0);
+      resid_blocks_load<false>(P, P.dpart, P.nchunk, 0, 0, R0);
     }
     gains_load(P, Lw.n1, rbias, GR);
     qkv_pre(P, Lw, head, pos0, Q);
@@ -607,7 +601,7 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
     if (li > 0) resid_blocks_rest<false>(P, P.dpart, P.nchunk, 0, R0, blk);
     gains_store(P, rbias, GR, gl);
   }
-  // stage every token: x, the norm, its QX records
+  // stage every token: x, the norm, its Q6 records
   for (int t = 0; t < m; ++t) {
     float *bt = blk + (t & 1) * nb * D;
     if (li == 0) {
@@ -615,11 +609,11 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
       base = embed_col(P, tok, min(pos0 + t, P.max_seq - 1));
     } else if (FLOW || t > 0) {
       base = col_base_load<FLOW>(P, P.xb + (size_t)t * D, nq, st.tag + li - 1);
-      resid_blocks<FLOW>(P, P.dpart + (size_t)t * P.nchunk * nquads(D), P.nchunk, st.tag + li - 1, bt);
+      resid_blocks<FLOW>(P, P.dpart + (size_t)t * P.nchunk * D, P.nchunk, st.tag + li - 1, bt);
     }
     __syncthreads();
     const float4 x = li == 0 ? base : col_finish(bt, nq, P.nchunk, base, gl, D, rbias != nullptr);
-    col_norm(P, x, gl, red, qx + t * ng * QXR, ColOut{head == 0 ? P.xa + (size_t)t * D : nullptr, st.tag + li});
+    col_norm(P, x, gl, red, qx + t * ng * Q6R, ColOut{head == 0 ? P.xa + (size_t)t * D : nullptr, st.tag + li});
   }
   __syncthreads();
   tile_partials<QC>(Q.R, ng, nch, m, qx, part);
@@ -673,10 +667,10 @@ struct AttnLds {
   float *pv;    // 64 x 64
   float *pv2;   // 4 x 64
   float *own;      // 64: this split's P.V
-  uint32_t *attq;  // 2 x QXR: merged head output, staged for the W_o slice
+  uint32_t *attq;  // 2 x Q6R: merged head output, staged for the W_o slice
   int *flag;
 };
-constexpr int ATT_LDS = HD + 2 * ACH + 64 * HD + 4 * HD + HD + 2 * QXR + 4;  // floats
+constexpr int ATT_LDS = HD + 2 * ACH + 64 * HD + 4 * HD + HD + 2 * Q6R + 4;  // floats
 
 __device__ __forceinline__ AttnLds attn_lds(float *base) {
   AttnLds A;
@@ -687,7 +681,7 @@ __device__ __forceinline__ AttnLds attn_lds(float *base) {
   A.pv2 = A.pv + 64 * HD;
   A.own = A.pv2 + 4 * HD;
   A.attq = reinterpret_cast<uint32_t *>(A.own + HD);
-  A.flag = reinterpret_cast<int *>(A.attq + 2 * QXR);
+  A.flag = reinterpret_cast<int *>(A.attq + 2 * Q6R);
   return A;
 }
 
@@ -859,13 +853,13 @@ __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, i
       }
       v = as / ls;
     }
-    qx_stage_lanes(v, A.attq);  // the head output: two groups, wave 0
+    q6_stage_lanes(v, A.attq);  // the head output: two groups, wave 0
   }
   // the item's earlier stores (its K/V cache row) complete before the head's
   // output becomes visible, so whoever sees the output also sees them
   wait_stores();
   __syncthreads();
-  slice_gemv<C, AT>(Ro, D, A.attq, P.opart + (size_t)(t * P.NH + h) * nquads(D), tag);
+  slice_gemv<C, AT>(Ro, D, A.attq, P.opart + (size_t)(t * P.NH + h) * D, tag);
   return true;
 }
 
@@ -943,8 +937,8 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   const bool gpt2 = P.arch == 1;
   const float *rbias = gpt2 && li > 0 ? Lw.prev_mproj_b : nullptr;
   const int nb = (P.nchunk + PB - 1) / PB;
-  float *gl = smem, *part = gl + al4(3 * D) + ng * QXR;
-  uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // ng QX records
+  float *gl = smem, *part = gl + al4(3 * D) + ng * Q6R;
+  uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // ng Q6 records
   float *blk = part + nch, *red = blk + nb * D, *kvn = red + 32;  // kvn: the new K row (64) then V row (64)
   float *rs = kvn + 2 * HD;  // 3 x 64 row sums: q, k, v
   const AttnLds A = attn_lds(rs + 3 * HD);
@@ -976,7 +970,7 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
     // activations first, then the weights (loads retire in issue order)
     if (li > 0) {
       base = col_base_load<false>(P, P.xb, nq, 0);
-      resid_blocks_load<false>(P, P.dpart, nquads(D), P.nchunk, 0, 0, R0);
+      resid_blocks_load<false>(P, P.dpart, P.nchunk, 0, 0, R0);
     }
     attn1_pre(P, Lw, rq, rk, rv, h, pos, row_own, rbias, Wt, Ro, c_own, s_own, GR);
     if (li > 0) resid_blocks_rest<false>(P, P.dpart, P.nchunk, 0, R0, blk);
@@ -1059,10 +1053,10 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
   const int nch = UNITS * ng;
   const int S = (MT / ng) * ng;
   const int nb = (P.NH + PB - 1) / PB;
-  float *gl = smem, *part = gl + al4(3 * D) + m * ng * QXR;  // part: 2 x (gate || up)
-  uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // m x ng QX records
-  uint32_t *hq = reinterpret_cast<uint32_t *>(part + 4 * nch);   // m x 2 QX records of h
-  float *blk = reinterpret_cast<float *>(hq + m * 2 * QXR);     // 2 x nb * D, then red
+  float *gl = smem, *part = gl + al4(3 * D) + m * ng * Q6R;  // part: 2 x (gate || up)
+  uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // m x ng Q6 records
+  uint32_t *hq = reinterpret_cast<uint32_t *>(part + 4 * nch);   // m x 2 Q6 records of h
+  float *blk = reinterpret_cast<float *>(hq + m * 2 * Q6R);     // 2 x nb * D, then red
   float *red = blk + 2 * nb * D;
   float *rsum = red + 32;  // 2 x (gate || up) row sums, by token parity
   const float *rbias = gpt2 ? Lw.proj_b : nullptr;
@@ -1081,7 +1075,7 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
   if (!FLOW) {
     base = col_base_load<false>(P, P.xa, nq, 0);
     ResidReg R0;
-    resid_blocks_load<false>(P, P.opart, nquads(D), P.NH, 0, 0, R0);
+    resid_blocks_load<false>(P, P.opart, P.NH, 0, 0, R0);
     gains_load(P, Lw.n2, rbias, GR);
     mlp_pre_up(P, Lw, item, M);  // before the down slice (loads retire in issue order)
     if (st.done) return;
@@ -1092,10 +1086,10 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
     float *bt = blk + (t & 1) * nb * D;
     if (FLOW || t > 0) {
       base = col_base_load<FLOW>(P, P.xa + (size_t)t * D, nq, want);
-      resid_blocks<FLOW>(P, P.opart + (size_t)t * P.NH * nquads(D), P.NH, want, bt);
+      resid_blocks<FLOW>(P, P.opart + (size_t)t * P.NH * D, P.NH, want, bt);
     }
     __syncthreads();
-    col_norm(P, col_finish(bt, nq, P.NH, base, gl, D, gpt2), gl, red, qx + t * ng * QXR,
+    col_norm(P, col_finish(bt, nq, P.NH, base, gl, D, gpt2), gl, red, qx + t * ng * Q6R,
              ColOut{item == 0 ? P.xb + (size_t)t * D : nullptr, want});
   }
   if (!FLOW) slice_load<MC, MT>(Lw.w2, 2 * item, D, M.Rd);  // needed last: behind everything the prologue reads
@@ -1108,13 +1102,25 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
     // the activation and the two group records of h
     float *pt = part + (t & 1) * 2 * nch;
     float *rt = rsum + (t & 1) * 2 * UNITS;
-    const QxRec xr = qx_load(qx + (t * ng + g) * QXR);
+    {
+      // gate chunks then up chunks against the thread's one group record
+      uint4 w[2 * MC];
+      float ws[2 * MC], o[2 * MC];
 #pragma unroll
-    for (int k = 0; k < MC; ++k) {
-      const int c = tid() + k * S;
-      if ((int)tid() < S && c < nch) {
-        pt[c] = q4_qx_part_reg(M.Rg.w[k], xr, M.Rg.s[k]);
-        if (!gpt2) pt[nch + c] = q4_qx_part_reg(M.Ru.w[k], xr, M.Ru.s[k]);
+      for (int k = 0; k < MC; ++k) {
+        w[k] = M.Rg.w[k];
+        ws[k] = M.Rg.s[k];
+        w[MC + k] = M.Ru.w[k];
+        ws[MC + k] = M.Ru.s[k];
+      }
+      q4_dot6_planes<2 * MC>(w, ws, qx + (t * ng + g) * Q6R, o);
+#pragma unroll
+      for (int k = 0; k < MC; ++k) {
+        const int c = tid() + k * S;
+        if ((int)tid() < S && c < nch) {
+          pt[c] = o[k];
+          if (!gpt2) pt[nch + c] = o[MC + k];
+        }
       }
     }
     __syncthreads();
@@ -1141,15 +1147,15 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
       } else {
         h = (gv / (1.0f + expf(-gv))) * rt[UNITS + r];
       }
-      qx_stage_lanes(h, hq + t * 2 * QXR);
+      q6_stage_lanes(h, hq + t * 2 * Q6R);
     }
   }
   __syncthreads();
   for (int t = 0; t < m; ++t)
-    slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * QXR, P.dpart + ((size_t)t * P.nchunk + item) * nquads(D), want);
+    slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * Q6R, P.dpart + ((size_t)t * P.nchunk + item) * D, want);
 }
 
-// The last layer's residual and the final norm of token t: QX records (LDS)
+// The last layer's residual and the final norm of token t: Q6 records (LDS)
 // for the lm_head of the persistent kernel, or xn (coherent stores) for the
 // lm_head kernel.  blk needs nb * D floats; the
 // caller has staged the norm_f gains in gl.
@@ -1158,7 +1164,7 @@ __device__ __forceinline__ void final_row(const DecParams &P, int t, float *blk,
                                           bool to_global, int want) {
   const int D = P.D, nq = D >> 2;
   const float4 base = col_base_load<POLL>(P, P.xb + (size_t)t * D, nq, want);
-  resid_blocks<POLL>(P, P.dpart + (size_t)t * P.nchunk * nquads(D), P.nchunk, want, blk);
+  resid_blocks<POLL>(P, P.dpart + (size_t)t * P.nchunk * D, P.nchunk, want, blk);
   __syncthreads();
   const float4 x = col_finish(blk, nq, P.nchunk, base, gl, D, P.arch == 1);
   col_norm(P, x, gl, blk + ((P.nchunk + PB - 1) / PB) * D, qx, ColOut{nullptr, 0, to_global ? P.xn + (size_t)t * D : nullptr});
@@ -1192,7 +1198,7 @@ __device__ __forceinline__ float gpt2_adjust(float v, int i, const int *ban, int
 }
 
 struct LmLds {
-  uint32_t *qx;  // the normed rows, QX records
+  uint32_t *qx;  // the normed rows, Q6 records
   float *part, *out;
   int *lists;
 };
@@ -1213,7 +1219,7 @@ __device__ __forceinline__ void lm_tile(const DecParams &P, const LmGeom &L, con
                                         int m, const LmLds &s, bool penal, int nban, int nrec) {
   const int ng = P.D >> 5, rpt = L.rpt;
   const int r0 = tile * rpt, nr = min(rpt, P.V - r0);
-  tile_compute_qx<TCN, NT>(R, nr, ng, nr * ng, m, s.qx, tid() % ng, NT % ng, s.part, s.out, rpt);
+  tile_compute_q6<TCN, NT>(R, nr, ng, nr * ng, m, s.qx, tid() % ng, NT % ng, s.part, s.out, rpt);
   for (int e = tid(); e < m * nr; e += NT) {
     const int t = e / nr, r = e - t * nr;
     P.logits[(size_t)(tb + t) * P.V + r0 + r] = s.out[t * rpt + r];
@@ -1290,7 +1296,7 @@ __device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, const S
   lm_load<TC, LT>(P, L, tile, Ra);
   LmLds s;
   s.qx = reinterpret_cast<uint32_t *>(smem);
-  s.part = smem + m * ng * QXR;
+  s.part = smem + m * ng * Q6R;
   s.out = s.part + m * TC * LT;
   s.lists = reinterpret_cast<int *>(s.out + m * L.rpt);  // [0]: nban, [1]: nrec, [2..34): rec, then ban
   const bool penal = P.arch == 1 && st_ld(P, ST_OFF(chain)) != 0;
@@ -1306,7 +1312,7 @@ __device__ void phase_lm(const DecParams &P, int m_all, int wg, int nwg, const S
     for (int k = 0; k < 4; ++k) {
       const int f = base + tid() + k * LT;
       const int fc = min(f, m * nq - 1), t = fc / nq;
-      qx_stage_col(xv[k], f < m * nq, fc - t * nq, s.qx + t * ng * QXR);
+      q6_stage_col(xv[k], f < m * nq, fc - t * nq, s.qx + t * ng * Q6R);
     }
   }
   __syncthreads();
@@ -1576,7 +1582,7 @@ __device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, co
   LmLds s;
   float *gl = smem;
   s.qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));
-  s.part = gl + al4(3 * D) + ng * QXR;
+  s.part = gl + al4(3 * D) + ng * Q6R;
   s.out = s.part + FTC * FLT;
   s.lists = reinterpret_cast<int *>(s.out + L.rpt);
   float *blk = reinterpret_cast<float *>(s.lists + 34 + P.max_seq);
@@ -1748,14 +1754,14 @@ size_t lds_floats(const DecParams &P, int ph, int m) {
   const size_t ngd = P.D / 32, D = P.D;
   const size_t nbo = (P.NH + PB - 1) / PB, nbd = (P.nchunk + PB - 1) / PB;
   switch (ph) {
-  case PH_QKV: return al4(3 * D) + m * ngd * QXR + (size_t)m * HD * ngd + 2 * nbd * D + 32 + (size_t)m * HD;
+  case PH_QKV: return al4(3 * D) + m * ngd * Q6R + (size_t)m * HD * ngd + 2 * nbd * D + 32 + (size_t)m * HD;
   case PH_ATTN:
-    if (m == 1) return al4(3 * D) + ngd * QXR + 3 * HD * ngd + nbd * D + 32 + 2 * HD + 3 * HD + ATT_LDS;
+    if (m == 1) return al4(3 * D) + ngd * Q6R + 3 * HD * ngd + nbd * D + 32 + 2 * HD + 3 * HD + ATT_LDS;
     return ATT_LDS;
   case PH_MLP:
-    return al4(3 * D) + m * ngd * QXR + 4 * UNITS * ngd + (size_t)m * 2 * QXR + 2 * nbo * D + 32 + 4 * UNITS;
+    return al4(3 * D) + m * ngd * Q6R + 4 * UNITS * ngd + (size_t)m * 2 * Q6R + 2 * nbo * D + 32 + 4 * UNITS;
   case PH_FINAL: return al4(3 * D) + nbd * D + 32;
-  case PH_LM: return m * ngd * QXR + (size_t)m * TC * LT + (size_t)m * P.lm_rpt + 34 + P.max_seq;
+  case PH_LM: return m * ngd * Q6R + (size_t)m * TC * LT + (size_t)m * P.lm_rpt + 34 + P.max_seq;
   default: return 2 * (LT / 64);
   }
 }
@@ -1767,7 +1773,7 @@ size_t flow_lds_bytes(const DecParams &P, const FlowGeom &F) {
   size_t f = 2 * (FLT / 64);
   for (int ph = PH_QKV; ph <= PH_FINAL; ++ph) f = std::max(f, lds_floats(P, ph, 1));
   const size_t nbd = (P.nchunk + PB - 1) / PB;
-  f = std::max(f, al4(3 * (size_t)P.D) + ngd * QXR + (size_t)FTC * FLT + (size_t)F.lm_rpt + 34 + P.max_seq +
+  f = std::max(f, al4(3 * (size_t)P.D) + ngd * Q6R + (size_t)FTC * FLT + (size_t)F.lm_rpt + 34 + P.max_seq +
                       nbd * P.D + 32);
   return f * sizeof(float);
 }
@@ -2142,8 +2148,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
 
   // activations, KV cache, scratch
   const size_t kv_elems = (size_t)L * 2 * NKV * c.max_seq_len * HD;
-  const size_t tagged_bytes[4] = {sizeof(uint2) * MAXT * D, sizeof(uint2) * MAXT * D,
-                                   sizeof(uint4) * MAXT * NH * nquads(D), sizeof(uint4) * MAXT * P.nchunk * nquads(D)};
+  const size_t tagged_bytes[4] = {sizeof(uint2) * MAXT * D, sizeof(uint2) * MAXT * D, sizeof(uint2) * MAXT * NH * D,
+                                   sizeof(uint2) * MAXT * P.nchunk * D};
   int rc = dev_alloc(M, (void **)&P.xa, tagged_bytes[0]);
   if (!rc) rc = dev_alloc(M, (void **)&P.xb, tagged_bytes[1]);
   if (!rc) rc = dev_alloc(M, (void **)&P.opart, tagged_bytes[2]);

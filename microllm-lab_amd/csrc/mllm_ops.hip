@@ -41,69 +41,15 @@ extern "C" const char *mllm_last_error(void) { return mllm::g_err.c_str(); }
 extern "C" int mllm_kernel_version(void) { return 1; }
 
 // ---------------------------------------------------------------- Q4 GEMV
-// The activations are taken as 24-bit integers per 32-element group (the Q4
-// group): xi = rint(x * XMAX / amax), sx = amax / XMAX (amax = max |x| of
-// the group).  Each xi is held as six signed 4-bit digits,
-// xi = sum_k 16^k d_k with d_k in [-8, 7], and flipping bit 3 of a stored
-// nibble q gives the signed nibble q - 8, so one dot8 (eight 4-bit
-// products) per 8 weights and digit plane yields
-//   dot = sum_k 16^k sum_e (q_e - 8) d_{k,e} = sum_e (q_e - 8) xi_e,
-// exact in int32: |dot| <= 32 * 8 * XMAX < 2^31 (the Horner partial sums
-// may wrap; the final value does not).  A group adds (float)dot * sx *
-// w_scale to its row.  Rounding x to 24 bits moves it by at most
-// amax / (2 XMAX) = 6.4e-8 amax, the size of one float32 rounding.
-//
-// Digits: with u = xi + C (C = 8 (16^6 - 1) / 15, so u >= 0), digit k of xi
-// is hex digit k of u minus 8, i.e. its 4-bit pattern is bfe(u, 4k, 4) ^ 8.
+// The activations are taken as Q6 records (24-bit integers per 32-element
+// group, mllm_device.h): one v_dot8 per 8 weights and digit plane, exact in
+// int32; a group adds (float)dot * sx * w_scale to its row.
 //
 // Work split: thread t < rpp * ng keeps group g = t % ng of rows
 // rpp * p + t / ng of its tile for p < P, so each thread reads one group
 // record and the loads of a pass are contiguous across the workgroup; the
 // row sums go through LDS in a fixed order that depends only on ng.
-constexpr int Q6R = 28;              // dwords per group record: 6 digit planes x 4 dwords, sx, padding
-constexpr int Q6C = 8947848;         // 8 * (16^6 - 1) / 15
-constexpr float Q6MAX = 7829360.0f;  // below 7 * (16^6 - 1) / 15 = 7829367 by more than the rcp rounding
 constexpr int GX_BATCH = 4;          // float4s of x per thread loaded ahead of the weights
-
-// Stage the float4 column q of the activations (elements 4q .. 4q+3 of
-// group q >> 3; a group is 8 neighbouring lanes).  Whole waves call it.
-__device__ __forceinline__ void q6_stage_col(float4 y, bool in, int q, uint32_t *rec0) {
-  if (!in) y = make_float4(0.f, 0.f, 0.f, 0.f);
-  const float a = max8(fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
-  const float inv = a > 0.f ? Q6MAX * __builtin_amdgcn_rcpf(a) : 0.f;
-  const uint32_t u0 = (uint32_t)((int)__builtin_rintf(y.x * inv) + Q6C);
-  const uint32_t u1 = (uint32_t)((int)__builtin_rintf(y.y * inv) + Q6C);
-  const uint32_t u2 = (uint32_t)((int)__builtin_rintf(y.z * inv) + Q6C);
-  const uint32_t u3 = (uint32_t)((int)__builtin_rintf(y.w * inv) + Q6C);
-  if (!in) return;
-  uint32_t *rec = rec0 + (q >> 3) * Q6R;
-  uint8_t *rb = reinterpret_cast<uint8_t *>(rec);
-  // elements 8j .. 8j+7 of the group are dword j of a plane, nibble i = element 8j + i
-  const int off = 4 * ((q & 7) >> 1) + 2 * (q & 1);
-#pragma unroll
-  for (int k = 0; k < 6; ++k) {
-    const uint32_t v = __builtin_amdgcn_ubfe(u0, 4 * k, 4) | (__builtin_amdgcn_ubfe(u1, 4 * k, 4) << 4) |
-                       (__builtin_amdgcn_ubfe(u2, 4 * k, 4) << 8) | (__builtin_amdgcn_ubfe(u3, 4 * k, 4) << 12);
-    *reinterpret_cast<unsigned short *>(rb + 16 * k + off) = (unsigned short)(v ^ 0x8888u);
-  }
-  if ((q & 7) == 0) rec[24] = __float_as_uint(a * (1.0f / Q6MAX));
-}
-
-// One 16-byte chunk (the 32 weights of one group of one row) against the
-// group's record xr (24 digit dwords) with activation scale sx and weight
-// scale ws.
-__device__ __forceinline__ float q4_dot6(const uint4 w, const uint32_t *xr, float sx, float ws) {
-  const int d[4] = {(int)(w.x ^ 0x88888888u), (int)(w.y ^ 0x88888888u), (int)(w.z ^ 0x88888888u),
-                    (int)(w.w ^ 0x88888888u)};
-  int acc = 0;
-#pragma unroll
-  for (int k = 5; k >= 0; --k) {
-    if (k < 5) acc = (int)((uint32_t)acc << 4);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_sdot8(d[j], (int)xr[4 * k + j], acc, false);
-  }
-  return ((float)acc * sx) * ws;
-}
 
 // Sum over lpr (a power of two <= 64) neighbouring lanes; whole lpr-lane
 // segments are active.
@@ -170,20 +116,10 @@ __device__ __forceinline__ void q4_gemv_tile(const uint8_t *__restrict__ packed,
   __syncthreads();
   if (act) {
     for (int tok = 0; tok < G.m; ++tok) {
-      const uint32_t *r = rec + (tok * ng + g) * Q6R;
-      uint32_t xr[24];
-#pragma unroll
-      for (int k = 0; k < 6; ++k) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(r + 4 * k);
-        xr[4 * k] = v.x;
-        xr[4 * k + 1] = v.y;
-        xr[4 * k + 2] = v.z;
-        xr[4 * k + 3] = v.w;
-      }
-      const float sx = __uint_as_float(r[24]);
+      const Q6Rec xr = q6_load(rec + (tok * ng + g) * Q6R);
       float *pp = part + (tok * RT + rr) * ngp + g;
 #pragma unroll
-      for (int p = 0; p < P; ++p) pp[p * G.rpp * ngp] = q4_dot6(w[p], xr, sx, s[p]);
+      for (int p = 0; p < P; ++p) pp[p * G.rpp * ngp] = q4_dot6(w[p], xr, s[p]);
     }
   }
   __syncthreads();

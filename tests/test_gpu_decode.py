@@ -239,3 +239,57 @@ def test_long_context_persistent_equals_graph():
         outs.append(np.stack([g.forwardDecode(t).copy() for t in follow]))
         g.destroy()
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+# Decode at the reference's precision: the GEMVs take 24-bit activations
+# (rounding x by at most 6.4e-8 amax per group, one float32 rounding), so a
+# decode step's logits stay within float32 accumulation error of the oracle's
+# fp64 arithmetic.  DECODE_TOL bounds that error relative to the logits'
+# scale; 16-bit activations (1.5e-5 amax per group) exceed it by an order of
+# magnitude on these models.
+DECODE_TOL = 2e-6
+
+
+@gpu
+@pytest.mark.parametrize("arch", ["llama", "gpt2"])
+@pytest.mark.parametrize("mode", MODES)
+def test_decode_precision_vs_oracle(oracle_lib, arch, mode):
+    """Prompt through the pass path (the decode kernels, 24-bit activations),
+    then teacher-forced decode steps: max-abs logits error <= DECODE_TOL x
+    max |logit| of the oracle row (plus a 1e-7 floor)."""
+    bundle = build(arch, seed=14, max_seq_len=128)
+    g = mllm.PetitGPT(bundle, exec_mode=mode)
+    g.set_prefill(0)
+    ref = oracle_lib.OracleModel(bundle)
+    rng = np.random.default_rng(15)
+    prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 20)]
+    rows = [(g.forwardPrompt(prompt).copy(), ref.forward_prompt(prompt))]
+    for _ in range(10):
+        tok = int(rng.integers(0, bundle.cfg.vocab_size))
+        rows.append((g.forwardDecode(tok).copy(), ref.forward_decode(tok)))
+    g.destroy()
+    ref.close()
+    rel = max(float(np.abs(a - b).max()) / (float(np.abs(b).max()) + 1e-7 / DECODE_TOL) for a, b in rows)
+    print(f"decode precision {arch} mode={mode}: max-abs error / max|logit| = {rel:.2e}", flush=True)
+    assert rel <= DECODE_TOL, rel
+
+
+@gpu
+def test_decode_precision_full_size_135m(oracle_lib):
+    """Config 1's model at full size (30 layers, vocabulary 49152): the same
+    bound on the prompt's and 3 decode steps' logits."""
+    cfg = pgw.CONFIGS["smollm2-135m"]
+    bundle = pgw.parse_pgw(pgw.make_llama(cfg, seed=0))
+    g = mllm.PetitGPT(bundle)
+    g.set_prefill(0)
+    ref = oracle_lib.OracleModel(bundle)
+    prompt = [int(v) for v in np.random.default_rng(1).integers(0, cfg.vocab_size, 32)]
+    rows = [(g.forwardPrompt(prompt).copy(), ref.forward_prompt(prompt))]
+    for _ in range(3):
+        tok = int(np.argmax(rows[-1][1]))
+        rows.append((g.forwardDecode(tok).copy(), ref.forward_decode(tok)))
+    g.destroy()
+    ref.close()
+    rel = max(float(np.abs(a - b).max()) / float(np.abs(b).max()) for a, b in rows)
+    print(f"decode precision 135m: max-abs error / max|logit| = {rel:.2e}", flush=True)
+    assert rel <= DECODE_TOL, rel
