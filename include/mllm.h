@@ -68,6 +68,16 @@ int mllm_gemv_q8(int m, int n, const int8_t *q, const float *scale, const float 
 int mllm_gemv_q4(int m, int n, const uint8_t *packed, const float *scale, int group, const float *x, float *y,
                  void *stream);
 
+/* infer.js:597-600 (the lm_head GEMV of the last row) followed by argmax,
+ * infer.js:240-250 (GPU: webgpu-metal.js:786-813): y = W x as mllm_gemv_q4
+ * computes it (bit-identical), and *argmax = the first index of the maximum
+ * of y (best = 0, bestV = y[0], then each later row strictly larger; NaN
+ * rows never win).  argmax is a device pointer.  The per-workgroup maxima and
+ * a completion counter live in a scratch buffer that the library allocates
+ * per device on first use; calls on one device must not overlap. */
+int mllm_gemv_q4_argmax(int m, int n, const uint8_t *packed, const float *scale, int group, const float *x, float *y,
+                        int32_t *argmax, void *stream);
+
 /* No reference counterpart (BASELINE config 2 asks for it; the reference's Q8
  * is per-row only): Q8 group-32, q [m][n] i8 + scale [m][n/32] f32. */
 int mllm_gemv_q8_g32(int m, int n, const int8_t *q, const float *scale, const float *x, float *y, void *stream);
@@ -182,6 +192,11 @@ int mllm_model_gemv(mllm_model *model, const char *name, const float *x, float *
  * always use the phase kernels.  Results are bit-identical across modes.
  * Returns MLLM_ERR_UNSUPPORTED for mode 3 where it is unavailable. */
 int mllm_set_exec_mode(mllm_model *model, int mode);
+
+/* No reference counterpart: the execution mode the next decode call will use
+ * (after a refused cooperative launch, a default mode 3 has fallen back to
+ * 1); -1 for a null model. */
+int mllm_get_exec_mode(const mllm_model *model);
 
 /* Prompts of at least min_tokens tokens (default 2; 0 = never) are
  * processed in batches (no counterpart in the reference, whose GPU path runs

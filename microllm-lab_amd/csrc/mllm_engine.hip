@@ -2333,6 +2333,8 @@ extern "C" int mllm_set_exec_mode(mllm_model *M, int mode) {
   return 0;
 }
 
+extern "C" int mllm_get_exec_mode(const mllm_model *M) { return M ? M->exec_mode : -1; }
+
 extern "C" int mllm_set_prefill(mllm_model *M, int min_tokens, int chunk_tokens) {
   MLLM_CHECK(M, "null model");
   MLLM_CHECK(min_tokens >= 0, "prefill threshold %d", min_tokens);

@@ -8,6 +8,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "mllm_device.h"
@@ -69,11 +70,20 @@ struct GemvGeom {
   int ystride;        // y[t * ystride + r]
 };
 
+// The first maximum of the rows this thread wrote (one token), for the
+// argmax launches: (value, row) under amax_better, NaN rows left out, and
+// whether row 0 is NaN.
+struct RowMax {
+  float v = -INFINITY;
+  int i = 0x7fffffff;
+  bool nan0 = false;
+};
+
 // One tile (P passes of rpp rows) of y = W x for m tokens.
-template <int WGT, int P>
+template <int WGT, int P, bool AMX = false>
 __device__ __forceinline__ void q4_gemv_tile(const uint8_t *__restrict__ packed, const float *__restrict__ scale,
                                              const float *__restrict__ x, float *__restrict__ y, const GemvGeom &G,
-                                             int tile, uint32_t *lds) {
+                                             int tile, uint32_t *lds, RowMax *rm = nullptr) {
   const int ng = G.cols >> 5, nq = G.cols >> 2, nx = G.m * nq;
   const int ngp = 4 * ((ng + 3) >> 2), RT = G.rpp * P;
   uint32_t *rec = lds;                                          // [m][ng][Q6R]
@@ -134,7 +144,17 @@ __device__ __forceinline__ void q4_gemv_tile(const uint8_t *__restrict__ packed,
       a += ((v.x + (gi + 1 < ng ? v.y : 0.f)) + ((gi + 2 < ng ? v.z : 0.f) + (gi + 3 < ng ? v.w : 0.f)));
     }
     a = seg_sum(a, G.lpr);
-    if (l == 0 && rl < nr) y[tok * G.ystride + row0 + rl] = a;
+    if (l == 0 && rl < nr) {
+      y[tok * G.ystride + row0 + rl] = a;
+      if (AMX) {
+        const int row = row0 + rl;
+        if (amax_better(a, row, rm->v, rm->i)) {  // false for a NaN row
+          rm->v = a;
+          rm->i = row;
+        }
+        if (row == 0) rm->nan0 = a != a;
+      }
+    }
   }
 }
 
@@ -154,6 +174,85 @@ __global__ __launch_bounds__(WGT) void k_gemv_q4_batched(const uint8_t *const *_
   extern __shared__ float4 smem4[];
   const int b = blockIdx.y;
   q4_gemv_tile<WGT, P>(packed[b], scale[b], xv[b], yv[b], G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4));
+}
+
+// y = W x (one token) and the first index of its maximum, in one launch
+// (infer.js:597-600 + argmax, infer.js:240-250: best = 0, bestV = y[0], then
+// every later row that is strictly larger; a NaN row never wins, and a NaN
+// y[0] keeps index 0).  Each workgroup reduces its tile's rows to a (value,
+// row) pair in the scratch buffer; the last workgroup to finish (a counter in
+// the scratch) reduces the pairs and writes the index.  Scratch layout
+// (bytes): [0, 4) the counter, which every completed launch leaves at 0;
+// [4, 8) row 0 is NaN (tile 0 writes it); [64, 64 + 4 ntiles) the tiles'
+// values, then ntiles rows.  Two launches that share a scratch buffer must
+// not overlap.
+constexpr size_t kAmxHead = 64;
+__host__ __device__ constexpr size_t amx_scratch_bytes(int ntiles) { return kAmxHead + 8 * (size_t)ntiles; }
+
+template <int WGT, int P>
+__global__ __launch_bounds__(WGT) void k_gemv_q4_argmax(const uint8_t *__restrict__ packed,
+                                                        const float *__restrict__ scale, const float *__restrict__ x,
+                                                        float *__restrict__ y, GemvGeom G, unsigned char *scratch,
+                                                        int32_t *out) {
+  extern __shared__ float4 smem4[];
+  __shared__ float wv[WGT / 64];
+  __shared__ int wi[WGT / 64], last;
+  unsigned *cnt = reinterpret_cast<unsigned *>(scratch);
+  int *nan0 = reinterpret_cast<int *>(scratch + 4);
+  float *tv = reinterpret_cast<float *>(scratch + kAmxHead);
+  int *ti = reinterpret_cast<int *>(scratch + kAmxHead + 4 * (size_t)gridDim.x);
+  RowMax rm;
+  q4_gemv_tile<WGT, P, true>(packed, scale, x, y, G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4), &rm);
+  const int t = threadIdx.x;
+  float v = rm.v;
+  int i = rm.i;
+  wave_argmax(v, i);
+  if ((t & 63) == 0) {
+    wv[t >> 6] = v;
+    wi[t >> 6] = i;
+  }
+  if (blockIdx.x == 0 && t == 0) coh_sti(nan0, 0, rm.nan0 ? 1 : 0);  // thread 0 of tile 0 summed row 0
+  __syncthreads();
+  if (t == 0) {
+    for (int w = 1; w < WGT / 64; ++w)
+      if (amax_better(wv[w], wi[w], v, i)) {
+        v = wv[w];
+        i = wi[w];
+      }
+    coh_stf(tv, 4u * blockIdx.x, v);
+    coh_sti(ti, 4u * blockIdx.x, i);
+    wait_stores();  // the pair (and nan0) are visible before the count is
+    last = atomicAdd(cnt, 1u) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  v = -INFINITY;
+  i = 0x7fffffff;
+  for (int k = t; k < (int)gridDim.x; k += WGT) {
+    const float kv = coh_ldf(tv, 4u * k);
+    const int ki = coh_ldi(ti, 4u * k);
+    if (amax_better(kv, ki, v, i)) {
+      v = kv;
+      i = ki;
+    }
+  }
+  wave_argmax(v, i);
+  __syncthreads();
+  if ((t & 63) == 0) {
+    wv[t >> 6] = v;
+    wi[t >> 6] = i;
+  }
+  __syncthreads();
+  if (t == 0) {
+    for (int w = 1; w < WGT / 64; ++w)
+      if (amax_better(wv[w], wi[w], v, i)) {
+        v = wv[w];
+        i = wi[w];
+      }
+    // every row NaN leaves i at INT_MAX; row 0 NaN wins in any case
+    *out = coh_ldi(nan0, 0) || i == 0x7fffffff ? 0 : i;
+    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // ---------------------------------------------------------------- Q8 GEMV
@@ -370,6 +469,75 @@ int q4_launch_batched(dim3 grid, size_t lds, hipStream_t st, const uint8_t *cons
                    : (P) == 2 ? F<512, 2>(__VA_ARGS__)                       \
                               : F<512, 1>(__VA_ARGS__)))
 
+template <int WGT, int P>
+int q4_launch_argmax(dim3 grid, size_t lds, hipStream_t st, const uint8_t *packed, const float *scale, const float *x,
+                     float *y, const GemvGeom &G, unsigned char *scratch, int32_t *out) {
+  if (int rc = launch_dyn(k_gemv_q4_argmax<WGT, P>, grid, lds, st, "k_gemv_q4_argmax")) return rc;
+  hipLaunchKernelGGL((k_gemv_q4_argmax<WGT, P>), grid, dim3(WGT), lds, st, packed, scale, x, y, G, scratch, out);
+  MLLM_HIP(hipGetLastError());
+  return 0;
+}
+
+// The GEMV + argmax plan: the tiles of mllm_gemv_q4 for one token, so y is
+// bit-identical to mllm_gemv_q4's.
+struct AmxPlan {
+  Q4Plan pl;
+  int P, ntiles;
+};
+AmxPlan amx_plan(int m, int n) {
+  AmxPlan a;
+  a.pl = q4_plan(n, m, 1);
+  a.P = q4_pick_p(m, a.pl.rpp, 1);
+  a.ntiles = (m + a.pl.rpp * a.P - 1) / (a.pl.rpp * a.P);
+  return a;
+}
+
+int gemv_q4_argmax_run(const AmxPlan &a, int m, int n, const uint8_t *packed, const float *scale, const float *x,
+                       float *y, int32_t *out, unsigned char *scratch, hipStream_t st) {
+  const GemvGeom G{m, n, 1, a.pl.rpp, a.pl.lpr, m};
+  return MLLM_Q4_DISPATCH(q4_launch_argmax, a.pl.wgt, a.P, dim3(a.ntiles), q4_lds_bytes(a.pl, n / 32, 1, a.P), st,
+                          packed, scale, x, y, G, scratch, out);
+}
+
+int check_argmax_args(int m, int n, int group, const uint8_t *packed, const float *scale, const float *x, float *y,
+                      int32_t *argmax) {
+  if (int rc = check_q4_shape(m, n, group)) return rc;
+  MLLM_CHECK(packed && scale && x && y && argmax, "null pointer");
+  MLLM_CHECK((((uintptr_t)packed | (uintptr_t)x) & 15) == 0, "packed and x must be 16-byte aligned");
+  MLLM_CHECK((size_t)m * n / 2 < (1ull << 31), "matrix of %zu bytes exceeds 2 GiB", (size_t)m * n / 2);
+  return 0;
+}
+
+// The library's argmax scratch, one buffer per device, allocated on the first
+// call that needs it and grown (after the device is idle) when a call needs
+// more; its counter is zeroed once at allocation.
+constexpr int kMaxDevices = 64;
+struct DevScratch {
+  unsigned char *p = nullptr;
+  size_t bytes = 0;
+};
+DevScratch g_amx_scratch[kMaxDevices];
+std::mutex g_amx_mu;
+
+int amx_scratch_for(int dev, size_t need, unsigned char **out) {
+  std::lock_guard<std::mutex> lk(g_amx_mu);
+  DevScratch &d = g_amx_scratch[dev];
+  if (d.bytes < need) {
+    if (d.p) {
+      MLLM_HIP(hipDeviceSynchronize());
+      MLLM_HIP(hipFree(d.p));
+      d.p = nullptr;
+      d.bytes = 0;
+    }
+    const size_t bytes = need < 65536 ? 65536 : need;
+    MLLM_HIP(hipMalloc(reinterpret_cast<void **>(&d.p), bytes));
+    MLLM_HIP(hipMemset(d.p, 0, bytes));
+    d.bytes = bytes;
+  }
+  *out = d.p;
+  return 0;
+}
+
 int q4_gemm(int t, int m, int n, const uint8_t *packed, const float *scale, const float *x, float *y,
             hipStream_t st) {
   MLLM_CHECK((size_t)m * n / 2 < (1ull << 31), "matrix of %zu bytes exceeds 2 GiB", (size_t)m * n / 2);
@@ -421,6 +589,18 @@ extern "C" int mllm_gemv_q4_batched(int count, int m, int n, const uint8_t *cons
   const GemvGeom G{m, n, 1, pl.rpp, pl.lpr, m};
   return MLLM_Q4_DISPATCH(q4_launch_batched, pl.wgt, P, dim3(ntiles, count), q4_lds_bytes(pl, ng, 1, P),
                           as_stream(stream), packed, scale, x, y, G);
+}
+
+extern "C" int mllm_gemv_q4_argmax(int m, int n, const uint8_t *packed, const float *scale, int group,
+                                   const float *x, float *y, int32_t *argmax, void *stream) {
+  if (int rc = check_argmax_args(m, n, group, packed, scale, x, y, argmax)) return rc;
+  int dev = 0;
+  MLLM_HIP(hipGetDevice(&dev));
+  MLLM_CHECK(dev >= 0 && dev < kMaxDevices, "device %d beyond %d", dev, kMaxDevices);
+  const AmxPlan a = amx_plan(m, n);
+  unsigned char *scratch = nullptr;
+  if (int rc = amx_scratch_for(dev, amx_scratch_bytes(a.ntiles), &scratch)) return rc;
+  return gemv_q4_argmax_run(a, m, n, packed, scale, x, y, argmax, scratch, as_stream(stream));
 }
 
 static int q8_common(int m, int n, const int8_t *q, const float *scale, const float *x, float *y, int per_row,

@@ -29,6 +29,7 @@ SIGNATURES = {
     "mllm_gemv_q8_g32": ([I, I, P, P, P, P, P], I),
     "mllm_gemm_q4": ([I, I, I, P, P, I, P, P, P], I),
     "mllm_gemv_q4_batched": ([I, I, I, P, P, P, P, P], I),
+    "mllm_gemv_q4_argmax": ([I, I, P, P, I, P, P, P, P], I),
     "mllm_rms_norm": ([I, P, P, P, I, C.c_float, P], I),
     "mllm_silu_mul": ([I, P, P, P], I),
     "mllm_dequant_q4": ([I, I, P, P, I, P, P], I),
@@ -44,6 +45,7 @@ SIGNATURES = {
     "mllm_decode_chain": ([P, C.c_int32, I, C.c_int32, P, I, P, P], I),
     "mllm_model_gemv": ([P, C.c_char_p, P, P], I),
     "mllm_set_exec_mode": ([P, I], I),
+    "mllm_get_exec_mode": ([P], I),
     "mllm_set_prefill": ([P, I, I], I),
     "mllm_model_device_bytes": ([P], C.c_uint64),
     "mllm_last_timing": ([P, P, P], I),

@@ -110,6 +110,11 @@ class PetitGPT:
         abi.call("mllm_set_exec_mode", self._h, int(mode))
         self.exec_mode = int(mode)
 
+    @property
+    def execMode(self) -> int:
+        """The execution mode the next decode call uses (mllm_get_exec_mode)."""
+        return int(abi.lib().mllm_get_exec_mode(self._h))
+
     def set_prefill(self, min_tokens: int, chunk_tokens: int = 0):
         """Prompts of at least min_tokens tokens take the batched path (0: never),
         in chunks of at most chunk_tokens (0: the largest)."""

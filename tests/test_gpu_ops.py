@@ -245,3 +245,52 @@ def test_gpu_abi_against_the_oracle_abi_on_the_same_arguments(oracle_lib):
     df = torch.empty(m, dtype=torch.float32, device="cuda")
     abi.call("mllm_gemv_f32", m, n, ptr(dw), ptr(dx0), ptr(df), None)
     assert (np.abs(host(df) - f_cpu) <= 2 * row_bound(w, x[0])).all()
+
+
+def host_argmax(y):
+    """infer.js:240-250: best = 0, bestV = y[0]; a later row wins only when
+    strictly larger (so NaN rows never win and a NaN y[0] keeps 0)."""
+    best, bv = 0, y[0]
+    for i in range(1, y.size):
+        if y[i] > bv:
+            best, bv = i, y[i]
+    return best
+
+
+def argmax_case(rng, m, n, kind):
+    w = (rng.standard_normal((m, n)) * 0.02).astype(np.float32)
+    x = rng.standard_normal(n).astype(np.float32)
+    if kind == "tie":  # three equal maximal rows: the first one wins
+        w[[m // 3, m // 2, m - 1]] = w[m // 2] * 3
+    packed, sc = pgw.quant_q4(w)
+    if kind == "nan0":  # row 0 NaN keeps index 0
+        sc[0, 0] = np.nan
+    if kind == "nan_rows":  # NaN rows elsewhere never win
+        sc[1:m:7, 0] = np.nan
+    if kind == "all_nan":
+        x[:] = np.nan
+    if kind == "last":  # the maximum in the last row (the last tile)
+        w[-1] = np.abs(w[-1]) * np.sign(x) * 4
+        packed, sc = pgw.quant_q4(w)
+    return packed, sc, x
+
+
+@gpu
+@pytest.mark.parametrize("m,n,kind", [(49152, 960, "rand"), (49152, 576, "tie"), (50257, 768, "last"),
+                                      (2000, 960, "nan0"), (2000, 960, "nan_rows"), (300, 64, "all_nan"),
+                                      (7, 32, "rand")])
+def test_gemv_q4_argmax(m, n, kind):
+    """y bit-identical to mllm_gemv_q4, and the index equal to the reference
+    argmax rule over y (first maximum, NaN rules of infer.js:240-250)."""
+    rng = np.random.default_rng(m + n)
+    packed, sc, x = argmax_case(rng, m, n, kind)
+    dp, ds, dx = dev(packed), dev(sc), dev(x)
+    dy = torch.empty(m, dtype=torch.float32, device="cuda")
+    dy1 = torch.empty(m, dtype=torch.float32, device="cuda")
+    di = torch.full((1,), -5, dtype=torch.int32, device="cuda")
+    print(f"gemv_q4_argmax m={m} n={n} {kind}", flush=True)
+    abi.call("mllm_gemv_q4_argmax", m, n, ptr(dp), ptr(ds), 32, ptr(dx), ptr(dy), ptr(di), None)
+    abi.call("mllm_gemv_q4", m, n, ptr(dp), ptr(ds), 32, ptr(dx), ptr(dy1), None)
+    y = host(dy)
+    assert np.array_equal(y.view(np.uint32), host(dy1).view(np.uint32))
+    assert int(host(di)[0]) == host_argmax(y)
