@@ -78,6 +78,16 @@ int mllm_gemv_q4(int m, int n, const uint8_t *packed, const float *scale, int gr
 int mllm_gemv_q4_argmax(int m, int n, const uint8_t *packed, const float *scale, int group, const float *x, float *y,
                         int32_t *argmax, void *stream);
 
+/* No counterpart in the reference.  mllm_gemv_q4_argmax for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid hipMalloc): the same kernel and results, with its scratch in a
+ * fixed 128 KiB device array (one per GPU, held until the process ends), so
+ * the call allocates nothing.  At most 16376 workgroup tiles (the 49152-row
+ * lm_head takes 1536); larger shapes return MLLM_ERR_UNSUPPORTED.  Every
+ * call on a GPU shares that GPU's array: calls that overlap on one GPU race. */
+int mllm_gemv_q4_argmax_noalloc(int m, int n, const uint8_t *packed, const float *scale, int group, const float *x,
+                                float *y, int32_t *argmax, void *stream);
+
 /* No reference counterpart (BASELINE config 2 asks for it; the reference's Q8
  * is per-row only): Q8 group-32, q [m][n] i8 + scale [m][n/32] f32. */
 int mllm_gemv_q8_g32(int m, int n, const int8_t *q, const float *scale, const float *x, float *y, void *stream);

@@ -603,6 +603,52 @@ extern "C" int mllm_gemv_q4_argmax(int m, int n, const uint8_t *packed, const fl
   return gemv_q4_argmax_run(a, m, n, packed, scale, x, y, argmax, scratch, as_stream(stream));
 }
 
+// ---------------------------------------------------------------- no-allocation variant
+// mllm_gemv_q4_argmax_noalloc keeps the argmax scratch in a file-scope device
+// array of fixed size instead of memory the library allocates: every call on
+// a device shares that device's copy, which keeps the last call's contents
+// (the counter, which every completed call leaves at 0, is the only part read
+// before it is written).  Calls that overlap on one device race.  In host code
+// `scratch` names a host-side stand-in, not the device array: its device
+// address is looked up once per device (hipGetSymbolAddress, with that device
+// current) and only that address is passed to kernels.
+constexpr size_t kNoallocScratchBytes = 128 * 1024;
+constexpr int kNoallocMaxTiles = (int)((kNoallocScratchBytes - kAmxHead) / 8);
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+namespace {
+unsigned char *g_noalloc_ptr[kMaxDevices];
+std::mutex g_noalloc_mu;
+
+int noalloc_scratch(int dev, unsigned char **out) {
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void *p = nullptr;
+    MLLM_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return set_error(MLLM_ERR_HIP, "hipGetSymbolAddress(scratch) returned no address");
+    g_noalloc_ptr[dev] = static_cast<unsigned char *>(p);
+  }
+  *out = g_noalloc_ptr[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" int mllm_gemv_q4_argmax_noalloc(int m, int n, const uint8_t *packed, const float *scale, int group,
+                                           const float *x, float *y, int32_t *argmax, void *stream) {
+  if (int rc = check_argmax_args(m, n, group, packed, scale, x, y, argmax)) return rc;
+  const AmxPlan a = amx_plan(m, n);
+  if (a.ntiles > kNoallocMaxTiles)
+    return set_error(MLLM_ERR_UNSUPPORTED,
+                     "m=%d n=%d needs %d argmax tiles; the no-allocation scratch (%zu bytes) holds at most %d", m, n,
+                     a.ntiles, kNoallocScratchBytes, kNoallocMaxTiles);
+  int dev = 0;
+  MLLM_HIP(hipGetDevice(&dev));
+  MLLM_CHECK(dev >= 0 && dev < kMaxDevices, "device %d beyond %d", dev, kMaxDevices);
+  unsigned char *sp = nullptr;
+  if (int rc = noalloc_scratch(dev, &sp)) return rc;
+  return gemv_q4_argmax_run(a, m, n, packed, scale, x, y, argmax, sp, as_stream(stream));
+}
+
 static int q8_common(int m, int n, const int8_t *q, const float *scale, const float *x, float *y, int per_row,
                      hipStream_t st) {
   MLLM_CHECK(m > 0 && n > 0 && n % 32 == 0, "invalid shape m=%d n=%d (n %% 32 == 0 required)", m, n);

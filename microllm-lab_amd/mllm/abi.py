@@ -30,6 +30,7 @@ SIGNATURES = {
     "mllm_gemm_q4": ([I, I, I, P, P, I, P, P, P], I),
     "mllm_gemv_q4_batched": ([I, I, I, P, P, P, P, P], I),
     "mllm_gemv_q4_argmax": ([I, I, P, P, I, P, P, P, P], I),
+    "mllm_gemv_q4_argmax_noalloc": ([I, I, P, P, I, P, P, P, P], I),
     "mllm_rms_norm": ([I, P, P, P, I, C.c_float, P], I),
     "mllm_silu_mul": ([I, P, P, P], I),
     "mllm_dequant_q4": ([I, I, P, P, I, P, P], I),
