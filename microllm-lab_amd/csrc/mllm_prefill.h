@@ -43,8 +43,7 @@ struct PfArgs {
   float *q;      // [tc][D] roped queries
   float *att;    // [tc][D] attention output
   float *h;      // [tc][FF] MLP activation
-  float *sx;     // [tc] per-token activation scale
-  uint8_t *px;   // [tc / 32][max(D, FF) / 32][2][64 lanes][16] int8 activation planes
+  uint8_t *px;   // [tc / 32][max(D, FF) / 32]: 3 x [64 lanes][16] int8 activation planes, [32] f32 group scales
 };
 
 // The tiled copy of a Q4 matrix that the prefill GEMMs read (rows and cols

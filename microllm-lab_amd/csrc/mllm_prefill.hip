@@ -2,19 +2,21 @@
 // (infer.js:553-577): a chunk of T prompt tokens goes through every layer as
 // a handful of wide kernels instead of 16-token passes of the decode phases.
 //
-// Q4 GEMMs on int8 matrix cores.  Activations are quantised per token to
-// 16-bit integers, xi = rint(x * 32639 / amax) (amax = max |x| of the
-// token's row; sx = amax / 32639), and split into two signed bytes,
-// xi = 256 * hi + lo with lo = the low byte sign-extended (|xi| <= 32639
-// keeps hi within [-127, 127]).  With the weights as signed nibbles q - 8 the
-// group's dot product is exact in int32:
-//   sum_k (q_k - 8) xi_k = 256 * sum_k (q_k - 8) hi_k + sum_k (q_k - 8) lo_k,
-// two v_mfma_i32_32x32x32_i8 per 32-row x 32-token x 32-column group (K =
-// 32 = one Q4 group).  The group's float contribution is added as
-//   acc = fma((float)dot, w_scale, acc)
-// in group order, and the row is multiplied by sx at the end.  The VALU
-// epilogue (three operations per output and group) bounds these GEMMs, not
-// the matrix cores.
+// Q4 GEMMs on int8 matrix cores.  Activations are quantised per token and
+// 32-element group (the Q4 group) to 24-bit integers, xi = rint(x * Q3MAX /
+// amax) (amax = max |x| of the group; sx = amax / Q3MAX), which moves x by at
+// most 6.0e-8 amax: one float32 rounding of the group's largest element.  xi
+// is split into three signed bytes, xi = 65536 h + 256 m + l (l and m the
+// low bytes sign-extended, |xi| <= Q3MAX keeps h within [-128, 127]).  With
+// the weights as signed nibbles q - 8 the group's dot product is exact:
+//   sum_k (q_k - 8) xi_k = 65536 sum (q-8) h + 256 sum (q-8) m + sum (q-8) l,
+// three v_mfma_i32_32x32x32_i8 per 32-row x 32-token x 32-column group (K =
+// 32 = one Q4 group), combined in 32-bit wrapping arithmetic (the exact sum
+// is below 2^31 in magnitude: 32 * 8 * Q3MAX).  The group's float
+// contribution is added as
+//   acc = fma((float)dot, w_scale * sx, acc)
+// in group order.  The VALU epilogue (five operations per output and group)
+// and the matrix cores bound these GEMMs together.
 //
 // Operand layouts (v_mfma_i32_32x32x32_i8, checked on gfx950): A (the
 // activations) lane l holds row l % 32 (a token), 16 bytes of k; B (the
@@ -24,8 +26,9 @@
 // 16hh .. 16hh+15 in the order its weight bytes unpack: the low nibbles of
 // packed bytes 8hh .. 8hh+3 (elements 0, 2, 4, 6), of bytes 8hh+4 .. 8hh+7
 // (elements 8 .. 14), then the high nibbles of each (elements 1 .. 7 and
-// 9 .. 15, odd).  The activation planes are stored in that order, 64 bytes
-// per (token, group): hi of half 0, hi of half 1, lo of half 0, lo of half 1.
+// 9 .. 15, odd).  The activation planes are stored in that order, PX_TILE
+// bytes per (32-token tile, group): the h plane (half 0 then half 1, 16 bytes
+// per token each), the m plane, the l plane, then the 32 tokens' scales.
 //
 // Attention: causal, one (32-query tile, KV head) per workgroup, 32-key
 // blocks staged in LDS, S = Q K^T and O = P V on the f16 matrix cores with
@@ -49,8 +52,10 @@
 namespace mllm {
 namespace {
 
-constexpr int PX_MAX = 32639;   // |xi| bound of the 16-bit activations
-constexpr int PX_TILE = 2048;   // bytes per (32-token tile, group) of the planes
+constexpr float Q3MAX = 8355000.0f;  // |xi| bound of the 24-bit activations (three signed bytes need < 8355712)
+constexpr int PX_PLANE = 1024;  // bytes per plane of a (32-token tile, group)
+constexpr int PX_SC = 3 * PX_PLANE;  // offset of the 32 tokens' scales
+constexpr int PX_TILE = PX_SC + 128;  // bytes per (32-token tile, group)
 constexpr int PF_HD = 64;       // head dimension
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -90,8 +95,8 @@ __global__ __launch_bounds__(WG) void k_pf_embed(PfArgs A, int n, int pos0) {
 
 // ---------------------------------------------------------------- norm + quantise
 // One token row of K floats per wave (tokens t0 .. t1-1): optional RMSNorm /
-// LayerNorm (the decode engine's formulas), then the 16-bit planes and the
-// scale.  Wave reductions only; the row is re-read from cache per pass.
+// LayerNorm (the decode engine's formulas), then the 24-bit planes and the
+// group scales.  Wave reductions only; the row is re-read from cache per pass.
 template <int NORM>
 __device__ __forceinline__ float4 pf_norm_col(const float4 *xr, const float4 *g4, int nq, int q, float r, float mean) {
   const float4 v = xr[q];
@@ -140,15 +145,16 @@ __device__ __forceinline__ void pf_norm_stats(const float4 *xr, int K, float eps
 
 // Lane u of the wave owns (group u / 2, half u % 2) of the row -- 16
 // consecutive elements, PPL such units per lane (K <= 1024 PPL) -- held in
-// registers from one load, and writes the unit's hi and lo operands as two
-// 16-byte stores.
+// registers from one load; the two halves of a group are neighbouring lanes
+// (their amax is joined with one DPP step).  The unit's h, m and l operands
+// go out as three 16-byte stores.
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
   return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) | ((uint32_t)d << 24);
 }
 
 template <int NORM, int PPL>
 __global__ __launch_bounds__(WG) void k_pf_quant(const float *src, int K, const float *g, float eps, uint8_t *px,
-                                                 float *sx, int t0, int t1) {
+                                                 int t0, int t1) {
   const int t = t0 + (int)blockIdx.x * (WG / 64) + (tid() >> 6);
   if (t >= t1) return;  // no barriers below
   const int lane = tid() & 63, nu = K >> 4, ng = K >> 5;
@@ -215,44 +221,47 @@ __global__ __launch_bounds__(WG) void k_pf_quant(const float *src, int K, const 
         }
     }
   }
-  float am = 0.f;
-#pragma unroll
-  for (int i = 0; i < PPL; ++i)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float4 v = y[i][c];
-      am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-  am = wave_max(am);
-  const float inv = am > 0.f ? (float)PX_MAX / am : 0.f;
-  if (lane == 0) sx[t] = am / (float)PX_MAX;
   // token t is row j = t % 32 of token tile t / 32
-  uint8_t *tile = px + (size_t)(t >> 5) * ng * PX_TILE + 16 * (t & 31);
+  uint8_t *tile = px + (size_t)(t >> 5) * ng * PX_TILE;
 #pragma unroll
   for (int i = 0; i < PPL; ++i) {
     const int u = lane + 64 * i;
-    if (u >= nu) break;
-    int hi[16], lo[16];
+    float am = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4 v = y[i][c];  // zero past the row
+      am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    am = fmaxf(am, dpp_f<0xB1>(am));  // the other half of the group (lane ^ 1)
+    if (u >= nu) continue;            // whole waves took part in the DPP step
+    const float inv = am > 0.f ? Q3MAX * __builtin_amdgcn_rcpf(am) : 0.f;
+    int hq[16], mq[16], lq[16];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const float e[4] = {y[i][c].x, y[i][c].y, y[i][c].z, y[i][c].w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int x = (int)__builtin_rintf(e[k] * inv);
-        // signed split: lo = low byte sign-extended, hi = (x - lo) / 256
+        // balanced bytes: l, then m, sign-extended low bytes; h the rest
         const int l = (int)(signed char)(x & 255);
-        lo[4 * c + k] = l;
-        hi[4 * c + k] = (x - l) >> 8;
+        const int x1 = (x - l) >> 8;
+        const int m = (int)(signed char)(x1 & 255);
+        lq[4 * c + k] = l;
+        mq[4 * c + k] = m;
+        hq[4 * c + k] = (x1 - m) >> 8;
       }
     }
     // operand order: elements 0 2 4 6 | 8 10 12 14 | 1 3 5 7 | 9 11 13 15
-    const uint4 h = make_uint4(pack4(hi[0], hi[2], hi[4], hi[6]), pack4(hi[8], hi[10], hi[12], hi[14]),
-                               pack4(hi[1], hi[3], hi[5], hi[7]), pack4(hi[9], hi[11], hi[13], hi[15]));
-    const uint4 l = make_uint4(pack4(lo[0], lo[2], lo[4], lo[6]), pack4(lo[8], lo[10], lo[12], lo[14]),
-                               pack4(lo[1], lo[3], lo[5], lo[7]), pack4(lo[9], lo[11], lo[13], lo[15]));
-    uint8_t *rec = tile + (size_t)(u >> 1) * PX_TILE + 512 * (u & 1);  // lane 32 hh + j of the hi plane
-    *reinterpret_cast<uint4 *>(rec) = h;
-    *reinterpret_cast<uint4 *>(rec + 1024) = l;
+    auto plane = [](const int (&v)[16]) {
+      return make_uint4(pack4(v[0], v[2], v[4], v[6]), pack4(v[8], v[10], v[12], v[14]),
+                        pack4(v[1], v[3], v[5], v[7]), pack4(v[9], v[11], v[13], v[15]));
+    };
+    uint8_t *grp = tile + (size_t)(u >> 1) * PX_TILE;
+    uint8_t *rec = grp + 512 * (u & 1) + 16 * (t & 31);  // lane 32 hh + j of each plane
+    *reinterpret_cast<uint4 *>(rec) = plane(hq);
+    *reinterpret_cast<uint4 *>(rec + PX_PLANE) = plane(mq);
+    *reinterpret_cast<uint4 *>(rec + 2 * PX_PLANE) = plane(lq);
+    if ((u & 1) == 0) reinterpret_cast<float *>(grp + PX_SC)[t & 31] = am * (1.0f / Q3MAX);
   }
 }
 
@@ -334,12 +343,33 @@ constexpr int GPF = 4;  // groups of loads in flight per wave
 struct GemmLd {
   uint2 w0, w1;
   float c0, c1;
-  v4i ah, al;
+  v4i ah, am, al;
 };
+
+constexpr int PF_NGMAX = 128;  // groups per row (d_model, d_ff <= 4096)
+
+// One sub-tile's group: the three plane products combined into the exact
+// integer dot (32-bit wrapping arithmetic), then acc += dot * (w_scale * sx)
+// for the lane's 16 tokens.
+__device__ __forceinline__ void pf_group_acc(const v4i &ah, const v4i &am, const v4i &al, const v4i &b, float c,
+                                             const float4 (&sx)[4], float (&acc)[16]) {
+  const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  const v16i H = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, b, zero, 0, 0, 0);
+  const v16i M = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, b, zero, 0, 0, 0);
+  const v16i L = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, b, zero, 0, 0, 0);
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const uint32_t d = ((uint32_t)H[v] << 16) + ((uint32_t)M[v] << 8) + (uint32_t)L[v];
+    const float4 s4 = sx[v >> 2];
+    const float sv = (v & 3) == 0 ? s4.x : (v & 3) == 1 ? s4.y : (v & 3) == 2 ? s4.z : s4.w;
+    acc[v] = __builtin_fmaf((float)(int)d, c * sv, acc[v]);
+  }
+}
 
 template <int EPI, int KS>
 __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
   __shared__ float red[KS > 1 ? WG * 32 : 1];
+  __shared__ float4 sxs[PF_NGMAX * 8];  // the token tile's group scales: [group][32 tokens]
   const int wv = tid() >> 6, lane = tid() & 63, j = lane & 31, hh = lane >> 5;
   const int ks = wv % KS;
   const int R = (blockIdx.x * (WG / 64 / KS) + wv / KS) * G.rstep;
@@ -352,7 +382,11 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
   const size_t ta = (size_t)(R >> 5) * ng, tb = (size_t)((R + G.off1) >> 5) * ng;
   const uint8_t *wa = G.q0 + ta * 512 + 8 * lane, *wb = G.q1 + tb * 512 + 8 * lane;
   const float *sa = G.s0 + ta * 32 + j, *sb = G.s1 + tb * 32 + j;
-  const uint8_t *xa = A.px + (size_t)(G.tt0 + blockIdx.y) * ng * PX_TILE + 16 * lane;
+  const uint8_t *xt = A.px + (size_t)(G.tt0 + blockIdx.y) * ng * PX_TILE, *xa = xt + 16 * lane;
+  // every wave of the workgroup takes the same token tile: its scales to LDS
+  for (int i = tid(); i < ng * 8; i += WG)
+    sxs[i] = *reinterpret_cast<const float4 *>(xt + (size_t)(i >> 3) * PX_TILE + PX_SC + 16 * (i & 7));
+  __syncthreads();
   auto load = [&](int g) {
     GemmLd L;
     L.w0 = *reinterpret_cast<const uint2 *>(wa + 512 * g);
@@ -360,13 +394,13 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
     L.c0 = sa[32 * g];
     L.c1 = sb[32 * g];
     L.ah = *reinterpret_cast<const v4i *>(xa + PX_TILE * g);
-    L.al = *reinterpret_cast<const v4i *>(xa + PX_TILE * g + 1024);
+    L.am = *reinterpret_cast<const v4i *>(xa + PX_TILE * g + PX_PLANE);
+    L.al = *reinterpret_cast<const v4i *>(xa + PX_TILE * g + 2 * PX_PLANE);
     return L;
   };
   float acc0[16], acc1[16];
 #pragma unroll
   for (int v = 0; v < 16; ++v) acc0[v] = acc1[v] = 0.f;
-  const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   // the loads of group g + GPF go out before group g is computed
   GemmLd ring[GPF];
   if (active) {
@@ -380,16 +414,13 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
     if (g0 + i >= ge) break;
     const GemmLd cur = ring[i];
     ring[i] = load(g0 + i + GPF);
-    const v4i b0 = pf_unpack(cur.w0), b1 = pf_unpack(cur.w1);
-    const v16i h0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.ah, b0, zero, 0, 0, 0);
-    const v16i l0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.al, b0, zero, 0, 0, 0);
-    const v16i h1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.ah, b1, zero, 0, 0, 0);
-    const v16i l1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.al, b1, zero, 0, 0, 0);
+    // value v of this lane is token 8(v/4) + 4hh + v%4 of the tile
+    float4 sx[4];
+    const float4 *sg = sxs + (g0 + i) * 8 + hh;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      acc0[v] = __builtin_fmaf((float)(h0[v] * 256 + l0[v]), cur.c0, acc0[v]);
-      acc1[v] = __builtin_fmaf((float)(h1[v] * 256 + l1[v]), cur.c1, acc1[v]);
-    }
+    for (int k = 0; k < 4; ++k) sx[k] = sg[2 * k];
+    pf_group_acc(cur.ah, cur.am, cur.al, pf_unpack(cur.w0), cur.c0, sx, acc0);
+    pf_group_acc(cur.ah, cur.am, cur.al, pf_unpack(cur.w1), cur.c1, sx, acc1);
   }
   }
   if (KS > 1) {
@@ -421,8 +452,7 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
   for (int v = 0; v < 16; ++v) {
     const int t = T0 + 8 * (v >> 2) + 4 * hh + (v & 3);
     if (t >= G.n) continue;
-    const float s = A.sx[t];
-    float y0 = acc0[v] * s, y1 = acc1[v] * s;
+    float y0 = acc0[v], y1 = acc1[v];
     if (EPI == EPI_QKV) {
       // rows R .. R+63 are one head: query head, K head or V head
       const int head = R >> 6, pos = G.pos0 + t;
@@ -749,11 +779,11 @@ void launch_quant(const PfArgs &A, const float *src, int K, const float *g, int 
   const int per = WG / 64;
   const dim3 grid((t1 - t0 + per - 1) / per);
   if (K <= 1024)
-    hipLaunchKernelGGL((k_pf_quant<NORM, 1>), grid, dim3(WG), 0, s, src, K, g, A.eps, A.px, A.sx, t0, t1);
+    hipLaunchKernelGGL((k_pf_quant<NORM, 1>), grid, dim3(WG), 0, s, src, K, g, A.eps, A.px, t0, t1);
   else if (K <= 2048)
-    hipLaunchKernelGGL((k_pf_quant<NORM, 2>), grid, dim3(WG), 0, s, src, K, g, A.eps, A.px, A.sx, t0, t1);
+    hipLaunchKernelGGL((k_pf_quant<NORM, 2>), grid, dim3(WG), 0, s, src, K, g, A.eps, A.px, t0, t1);
   else
-    hipLaunchKernelGGL((k_pf_quant<NORM, 4>), grid, dim3(WG), 0, s, src, K, g, A.eps, A.px, A.sx, t0, t1);
+    hipLaunchKernelGGL((k_pf_quant<NORM, 4>), grid, dim3(WG), 0, s, src, K, g, A.eps, A.px, t0, t1);
 }
 
 // Group slices per row range: the fewest (1, 2 or 4) that give at least
@@ -806,15 +836,15 @@ int pf_tile(const PfMat &W, void *dst, PfMat *out, hipStream_t s) {
 }
 
 bool pf_supported(const PfArgs &A) {
-  return A.D == A.NH * PF_HD && A.NH % A.NKV == 0 && A.NH / A.NKV <= 4 && A.FF % 64 == 0 && A.D <= 4096 &&
-         A.FF <= 4096;
+  return A.D == A.NH * PF_HD && A.NH % A.NKV == 0 && A.NH / A.NKV <= 4 && A.FF % 64 == 0 &&
+         A.D <= 32 * PF_NGMAX && A.FF <= 32 * PF_NGMAX;
 }
 
 size_t pf_buffer_bytes(const PfArgs &A, int tc) {
   const size_t kmax = (size_t)(A.D > A.FF ? A.D : A.FF);
   auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
   return al(sizeof(int32_t) * tc) + 3 * al(sizeof(float) * tc * A.D) + al(sizeof(float) * tc * A.FF) +
-         al(sizeof(float) * tc) + al((size_t)(((tc + 31) / 32) * (kmax / 32) + GPF) * PX_TILE);
+         al((size_t)(((tc + 31) / 32) * (kmax / 32) + GPF) * PX_TILE);
 }
 
 void pf_carve(PfArgs &A, void *base, int tc) {
@@ -832,8 +862,6 @@ void pf_carve(PfArgs &A, void *base, int tc) {
   p += al(sizeof(float) * tc * A.D);
   A.h = reinterpret_cast<float *>(p);
   p += al(sizeof(float) * tc * A.FF);
-  A.sx = reinterpret_cast<float *>(p);
-  p += al(sizeof(float) * tc);
   A.px = p;
 }
 

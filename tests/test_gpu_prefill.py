@@ -4,8 +4,11 @@ infer.js:553-577) against the oracle and against the 16-token pass path.
 Bars: the prompt's last-token logits, and the logits of decode steps that
 read the batched path's KV cache, within LOGIT_TOL (max-abs 1e-2) of the
 fp64-accumulating oracle; greedy argmax identical wherever the oracle's top-2
-margin exceeds MARGIN.  Against the pass path (activations quantised per
-group instead of per token) the logits agree within PASS_TOL.
+margin exceeds MARGIN; at the reference's precision, within PREFILL_TOL of the
+oracle relative to the logits' scale.  Against the pass path (the decode
+kernels, a different summation order) the logits agree within PASS_TOL with
+an f32 KV cache; with an f16 cache the two paths can round a K or V element
+to neighbouring f16 values, so PASS_TOL_F16KV.
 """
 import numpy as np
 import pytest
@@ -16,7 +19,8 @@ from mllm import pgw
 gpu = pytest.mark.gpu
 LOGIT_TOL = 1e-2
 MARGIN = 1e-2
-PASS_TOL = 5e-3
+PASS_TOL = 2e-5
+PASS_TOL_F16KV = 5e-3
 
 
 def margin(logits):
@@ -163,7 +167,7 @@ def test_full_size_batched_prompt_vs_pass_path(name, kv16):
             steps.append(g.forwardDecode(tok).copy())
         outs.append(np.stack(steps))
         g.destroy()
-    assert np.abs(outs[0] - outs[1]).max() < PASS_TOL
+    assert np.abs(outs[0] - outs[1]).max() < (PASS_TOL_F16KV if kv16 else PASS_TOL)
 
 
 @gpu
@@ -192,3 +196,51 @@ def test_gpt2_smoothquant_descale_and_biases_vs_oracle(oracle_lib, pf_min, mode)
     g.destroy()
     ref.close()
     assert worst < LOGIT_TOL and agree, worst
+
+
+# The batched prompt at the reference's precision: 24-bit activations per
+# group in the GEMMs, f16 hi/lo splits in the attention; the prompt's logits
+# (and the decode steps that read its KV cache) stay within PREFILL_TOL of the
+# oracle relative to the logits' scale.
+PREFILL_TOL = 2e-6
+
+
+@gpu
+@pytest.mark.parametrize("arch", ["llama", "gpt2"])
+def test_batched_prompt_precision_vs_oracle(oracle_lib, arch):
+    bundle = build(arch, seed=25, max_seq_len=256)
+    g = mllm.PetitGPT(bundle)
+    g.set_prefill(2)
+    ref = oracle_lib.OracleModel(bundle)
+    rng = np.random.default_rng(26)
+    prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 130)]
+    rows = [(g.forwardPrompt(prompt).copy(), ref.forward_prompt(prompt))]
+    for _ in range(4):
+        tok = int(rng.integers(0, bundle.cfg.vocab_size))
+        rows.append((g.forwardDecode(tok).copy(), ref.forward_decode(tok)))
+    g.destroy()
+    ref.close()
+    rel = [float(np.abs(a - b).max()) / float(np.abs(b).max()) for a, b in rows]
+    print(f"batched prompt precision {arch}: prompt {rel[0]:.2e}, decode max {max(rel[1:]):.2e}", flush=True)
+    assert max(rel) <= PREFILL_TOL, rel
+
+
+@gpu
+def test_batched_prompt_precision_full_size_360m(oracle_lib):
+    """The 360M shape at full depth (f32 KV cache, as the oracle's), a 64-token
+    prompt through the batched path: its last-token logits within PREFILL_TOL
+    of the oracle relative to their scale.  (With the f16 cache of config 5
+    the rounding of K and V to 11 bits adds about 1e-3 here, inside the 1e-2
+    parity bar that test_gpu_config5 checks.)"""
+    cfg = pgw.CONFIGS["smollm2-360m"]
+    bundle = pgw.parse_pgw(pgw.make_llama(cfg, seed=0))
+    g = mllm.PetitGPT(bundle)
+    ref = oracle_lib.OracleModel(bundle)
+    prompt = [int(v) for v in np.random.default_rng(27).integers(0, cfg.vocab_size, 64)]
+    lg = g.forwardPrompt(prompt).copy()
+    lr = ref.forward_prompt(prompt)
+    g.destroy()
+    ref.close()
+    rel = float(np.abs(lg - lr).max()) / float(np.abs(lr).max())
+    print(f"batched prompt precision 360m: {rel:.2e}", flush=True)
+    assert rel <= PREFILL_TOL, rel
