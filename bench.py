@@ -15,10 +15,14 @@ One JSON line on stdout carries, besides the driver's fields:
                 bytes are the per-token Q4 weights + norms + KV reads summed
                 over the chain's steps, divided by the chain's duration from
                 HIP events on the model's stream; in modes 1/2 the dominant
-                phase kernel
+                phase kernel (mode 4: k_flow through an ordinary launch, for
+                profilers)
+  precision     what the arithmetic is: 24-bit activations per 32-element
+                group, exact int32 group dots, f32 across groups
   gemv_roofline the lm_head-shaped Q4 GEMV (49152 x 960, config 2) read cold
   cpu_baseline  the oracle (C restatement of engine/infer.js, fp64 accumulate,
-                1 thread) on a bounded sample of the same decode
+                1 thread) on a bounded sample of the same decode, with the
+                host CPU model; configs 2-5 carry their own CPU figures
   gemv_sweep    config 2: Q4 / Q8 group-32 GEMV GB/s on the 360M shapes
                 (warm = MALL-resident, cold = rotating >= 1 GiB of copies,
                 stacked = 32 matrices per launch)
@@ -137,6 +141,7 @@ def bench_decode(mllm, pgw, torch, args):
     log(f"[bench] 135M model generated in {time.time() - t:.1f}s")
     prompt = [int(v) for v in np.random.default_rng(1).integers(0, cfg.vocab_size, 32)]
     g = mllm.PetitGPT(bundle, exec_mode=args.exec_mode)
+    mode = g.execMode  # the mode the engine really uses (a refused cooperative launch falls back to 1)
     # warmup: W chained steps after a prefill
     g.resetCache()
     g.forwardPrompt(prompt)
@@ -154,6 +159,12 @@ def bench_decode(mllm, pgw, torch, args):
     gpu_ms, n = g.last_timing()
     assert n == args.steps == len(ids)
     wall = t1 - t0
+    mode = g.execMode
+    # reference-style rate (worker.js:166,176): n / totalMs of a whole
+    # generate call, prompt included -- 128 tokens after the 32-token prompt
+    r = g.generate(prompt, maxNewTokens=128, mode="chain", chainChunk=128)
+    r = g.generate(prompt, maxNewTokens=128, mode="chain", chainChunk=128)
+    ref_style = len(r["generatedIds"]) / (r["totalMs"] / 1e3)
     # per-phase kernel times (events around each launch, same stream)
     g.resetCache()
     g.forwardPrompt(prompt)
@@ -162,7 +173,7 @@ def bench_decode(mllm, pgw, torch, args):
     pb = phase_bytes(cfg, seq_mean)
     per_token_us = {ph: us * (cfg.n_layers if ph in LAYER_PHASES else 1) for ph, us in prof.items()}
     dom = max(per_token_us, key=per_token_us.get)
-    if args.exec_mode == 3:
+    if mode >= 3:
         # one k_flow launch ran the whole timed chain: step i attends over
         # len(prompt) + 1 + i cached positions
         kname = flow_kernel_name(cfg)
@@ -209,6 +220,9 @@ def bench_decode(mllm, pgw, torch, args):
     step_bytes = token_bytes(cfg, mean_seq)
     return {
         "value": args.steps / wall,
+        "exec_mode": mode,
+        "ref_style_tok_s": round(ref_style, 1),
+        "ttft_ms": round(r["ttftMs"], 3),
         "ms_per_step": wall / args.steps * 1e3,
         "kernel_ms_per_step": gpu_ms / args.steps,
         "first_ids": ids[:8],
@@ -220,36 +234,93 @@ def bench_decode(mllm, pgw, torch, args):
     }
 
 
-def bench_cpu(pgw, oracle, budget_s):
-    """The oracle (infer.js arithmetic in C, one thread) on the same model:
-    prefill 32 tokens untimed, then time greedy decode steps for ~budget_s."""
-    cfg = pgw.CONFIGS["smollm2-135m"]
-    bundle = pgw.parse_pgw(pgw.make_llama(cfg, seed=0))
-    prompt = [int(v) for v in np.random.default_rng(1).integers(0, cfg.vocab_size, 32)]
+def host_cpu():
+    """The host CPU's model name (/proc/cpuinfo) and logical CPU count."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return name, os.cpu_count()
+
+
+def cpu_decode_rate(oracle, bundle, budget_s, prompt=None, context=None, gpt2=False, max_steps=256):
+    """Greedy decode steps of the oracle (one thread) timed for ~budget_s: after
+    a real prompt, or with the cache length set to `context` directly (the
+    cached values are then not computed: a step's cost does not depend on
+    them).  Returns (tok/s, steps, prompt seconds or None)."""
     m = oracle.OracleModel(bundle)
-    lg = m.forward_prompt(prompt)
-    tok = oracle.argmax(lg)
+    pre = None
+    if prompt is not None:
+        t0 = time.perf_counter()
+        lg = m.forward_prompt(prompt)
+        pre = time.perf_counter() - t0
+        hist = []
+        tok = oracle.argmax_gpt2(lg, hist) if gpt2 else oracle.argmax(lg)
+    else:
+        m.cache_len = context
+        tok, hist = 1, []
     n = 0
     t0 = time.perf_counter()
     while True:
-        tok = oracle.argmax(m.forward_decode(tok))
+        lg = m.forward_decode(tok)
+        hist.append(tok)
+        tok = oracle.argmax_gpt2(lg, hist) if gpt2 else oracle.argmax(lg)
         n += 1
-        if time.perf_counter() - t0 > budget_s or n >= 256:
+        if time.perf_counter() - t0 > budget_s or n >= max_steps:
             break
     dt = time.perf_counter() - t0
     m.close()
+    return n / dt, n, pre
+
+
+def bench_cpu(pgw, oracle, budget_s):
+    """The oracle (infer.js arithmetic in C, one thread) on the same model:
+    prefill 32 tokens (timed for the reference-style n / totalMs), then time
+    greedy decode steps for ~budget_s."""
+    cfg = pgw.CONFIGS["smollm2-135m"]
+    bundle = pgw.parse_pgw(pgw.make_llama(cfg, seed=0))
+    prompt = [int(v) for v in np.random.default_rng(1).integers(0, cfg.vocab_size, 32)]
+    rate, n, pre = cpu_decode_rate(oracle, bundle, budget_s, prompt=prompt)
+    cpu, nproc = host_cpu()
     return {
-        "value": round(n / dt, 3),
+        "value": round(rate, 3),
         "unit": "tok/s",
         "cores": 1,
         "kind": "port",
+        "host_cpu": cpu,
+        "host_nproc": nproc,
+        # 128 tokens: the prompt's token, then 127 steps at the measured rate
+        "ref_style_tok_s": round(128 / (pre + 127 / rate), 3),
+        "prompt_ms": round(pre * 1e3, 1),
         "sample": f"135M Q4 greedy decode, {n} steps after a 32-token prompt, oracle/mllm_oracle.c "
-                  f"(engine/infer.js fp64 arithmetic), 1 thread, host nproc={os.cpu_count()}",
+                  f"(engine/infer.js fp64 arithmetic), 1 thread",
     }
 
 
 # ---------------------------------------------------------------- GEMV sweep
-def bench_gemv(torch, abi, pgw):
+def cpu_gemv_q4(oracle, pgw, m, n, budget_s=1.0):
+    """The CPU baseline of config 2: the C restatement of kernels.rs gemv_q4
+    (f32 accumulation in the reference's order, scalar, one thread) on a
+    matrix of the shape; GB/s of the same algorithmic bytes."""
+    rng = np.random.default_rng(m + n)
+    packed, sc = pgw.quant_q4((rng.standard_normal((m, n)) * 0.02).astype(np.float32))
+    x = rng.standard_normal(n).astype(np.float32)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.gemv_q4(packed, sc, x, mode="wasm")
+        reps += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    us = (time.perf_counter() - t0) / reps * 1e6
+    return {"us": round(us, 1), "gbs": round((m * n // 2 + m * n // 8 + 4 * n + 4 * m) / us / 1e3, 2), "reps": reps}
+
+
+def bench_gemv(torch, abi, pgw, oracle=None):
     shapes = [(960, 960), (320, 960), (2560, 960), (960, 2560), (49152, 960)]
     stream = torch.cuda.current_stream()
     sp = C.c_void_p(stream.cuda_stream)
@@ -320,6 +391,8 @@ def bench_gemv(torch, abi, pgw):
                 res["stacked32_gbs"] = round(cnt * algo / us / 1e3, 1)
                 del tabs
             res["cold_frac_hbm"] = round(res["cold_gbs"] / HBM_PEAK_GBS, 4)
+            if fmt == "q4" and oracle is not None:
+                res["cpu_kernels_rs"] = cpu_gemv_q4(oracle, pgw, m, n)
             out.append(res)
             del W, S
             torch.cuda.empty_cache()
@@ -340,11 +413,29 @@ def spans_prompt(rng, vocab, length, copy_frac=0.4):
     return out[:length]
 
 
-def bench_configs(mllm, pgw, args):
+def verify_pass_us(g, prompt, m, reps=20):
+    """GPU time of one (k+1)-row verify pass of m tokens at the end of the
+    prompt: the rows are a copy span of the prompt (forced drafts, so the pass
+    is the full k+1 rows whatever the model would accept), rolled back after
+    each pass."""
+    g.forwardPrompt(prompt)
+    base = g.cacheLen
+    span = prompt[100:100 + m]
+    times = []
+    for _ in range(reps):
+        g.forwardVerify(span)
+        times.append(g.last_timing()[0])
+        g.cacheLen = base
+    return round(float(np.median(times)) * 1e3, 1)
+
+
+def bench_configs(mllm, pgw, args, oracle=None):
     res = {}
+    cpu_s = 0.0 if oracle is None else max(3.0, args.cpu_seconds / 3)
     # config 3: prompt-lookup speculation on the 135M shape
     cfg = pgw.CONFIGS["smollm2-135m"]
-    g = mllm.PetitGPT(pgw.parse_pgw(pgw.make_llama(cfg, seed=0)), exec_mode=args.exec_mode)
+    bundle = pgw.parse_pgw(pgw.make_llama(cfg, seed=0))
+    g = mllm.PetitGPT(bundle, exec_mode=args.exec_mode)
     prompt = spans_prompt(np.random.default_rng(3), cfg.vocab_size, 512)
     base = g.generate(prompt, maxNewTokens=256, mode="chain")
     base = g.generate(prompt, maxNewTokens=256, mode="chain")
@@ -358,7 +449,20 @@ def bench_configs(mllm, pgw, args):
             "specTries": r["specTries"],
             "same_as_greedy": r["generatedIds"] == base["generatedIds"],
         }
+    # the synthetic model's greedy output repeats one token, so lookupDraft
+    # only finds 1-token drafts (the most recent match of the last 3 tokens
+    # overlaps them); the verify pass itself at M = k + 1 rows, forced drafts:
+    spec3["verify_pass_us"] = {f"m{m}": verify_pass_us(g, prompt, m) for m in (1, 5, 9)}
+    spec3["note"] = ("greedy output of the synthetic model repeats one token: every draft is 1 token long; "
+                     "verify_pass_us times M-row passes with forced drafts")
     g.destroy()
+    if oracle is not None:
+        # the reference's CPU path has no speculation (it is in the GPU engine
+        # only, webgpu.js:1239-1270): greedy decode at the prompt's context
+        rate, n, _ = cpu_decode_rate(oracle, bundle, cpu_s, context=512)
+        spec3["cpu"] = {"value": round(rate, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+                        "sample": f"{n} greedy decode steps from context 512 (cache length set directly; "
+                                  "the reference CPU path has no speculation)"}
     res["spec_135m"] = spec3
     # config 4: GPT-2 124M, 16-token prompt, 256 tokens with argmaxGpt2
     cfg = pgw.CONFIGS["gpt2-124m"]
@@ -367,7 +471,13 @@ def bench_configs(mllm, pgw, args):
     r = g.generate(prompt, maxNewTokens=256, mode="chain")
     r = g.generate(prompt, maxNewTokens=256, mode="chain")
     res["gpt2_124m"] = {"decode_tok_s": round(255 / ((r["totalMs"] - r["ttftMs"]) / 1e3), 1),
-                        "ttft_ms": round(r["ttftMs"], 2), "distinct_ids": len(set(r["generatedIds"]))}
+                        "ttft_ms": round(r["ttftMs"], 2), "distinct_ids": len(set(r["generatedIds"])),
+                        "ref_style_tok_s": round(len(r["generatedIds"]) / (r["totalMs"] / 1e3), 1)}
+    if oracle is not None:
+        rate, n, pre = cpu_decode_rate(oracle, g.bundle, cpu_s, prompt=prompt, gpt2=True)
+        res["gpt2_124m"]["cpu"] = {"value": round(rate, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+                                   "ref_style_tok_s": round(256 / (pre + 255 / rate), 3),
+                                   "sample": f"{n} decode steps (argmaxGpt2) after the 16-token prompt"}
     g.destroy()
     # config 5: 362M, fp16 KV, 1536-token prefill then 512 decode steps to 2048
     cfg = pgw.CONFIGS["smollm2-360m"]
@@ -395,6 +505,13 @@ def bench_configs(mllm, pgw, args):
                                   "prefill_pass_path_ms": round(pass_s * 1e3, 1),
                                   "decode_tok_s": round(len(ids) / dt, 1),
                                   "decode_step_gbs": round(token_bytes(cfg, mean_seq, 2) / (dt / len(ids)) / 1e9, 1)}
+    if oracle is not None:
+        # the oracle keeps an f32 cache (the reference's); 1536 prompt tokens
+        # would take minutes, so the cache length is set to 1792 directly
+        rate, n, _ = cpu_decode_rate(oracle, g.bundle, cpu_s, context=1792, max_steps=64)
+        res["smollm2_360m_fp16kv"]["cpu"] = {"value": round(rate, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+                                             "sample": f"{n} decode steps from context 1792 (f32 cache, length set "
+                                                       "directly; the 1536-token prompt is not run on the CPU)"}
     g.destroy()
     return res
 
@@ -404,8 +521,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=127, help="decode steps timed (tokens 2..K+1)")
     ap.add_argument("--warmup", type=int, default=32)
-    ap.add_argument("--exec-mode", type=int, default=3, choices=(1, 2, 3),
-                    help="3 persistent kernel (default), 1 graph replay, 2 direct launches")
+    ap.add_argument("--exec-mode", type=int, default=3, choices=(1, 2, 3, 4),
+                    help="3 persistent kernel (default), 1 graph replay, 2 direct launches, "
+                         "4 persistent kernel through an ordinary launch (for profilers)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
@@ -461,21 +579,31 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
+        "precision": {"weights": "q4 group-32 nibbles, f32 scales (PGW1)",
+                      "activations": "24-bit integers per 32-element group, rounding <= 6.4e-8 x the group's "
+                                     "max |x| (one f32 rounding of its largest element)",
+                      "accumulation": "exact int32 per group, f32 across groups",
+                      "measured": "decode logits within 2e-6 x max|logit| of the fp64 oracle (tests)"},
         "data": "synthetic: N(0,0.02) weights (seed 0) quantised by quant_q4; 32 prompt ids uniform (seed 1)",
         "config": {"workload": "smollm2-135m-q4 greedy decode, 32-token prompt, batch 1 (BASELINE config 1)",
-                   "weights": "q4 group-32 (PGW1)", "exec_mode": args.exec_mode, "kv_cache": "f32"},
+                   "weights": "q4 group-32 (PGW1)", "exec_mode": dec["exec_mode"], "kv_cache": "f32",
+                   "norm_eps": 1e-6,
+                   "norm_eps_note": "the reference's constant (infer.js:8); BASELINE config 1 states 1e-5"},
         "roofline": dec["roofline"],
         "kernel_ms_per_step": round(dec["kernel_ms_per_step"], 4),
         "phase_us": dec["phase_us"],
         "decode_step_gbs": dec["decode_step_gbs"],
         "decode_step_bytes": dec["decode_step_bytes"],
         "host_loop_tok_s": dec["host_loop_tok_s"],
+        "ref_style_tok_s": dec["ref_style_tok_s"],
+        "ttft_ms": dec["ttft_ms"],
     }
-    if not args.no_cpu:
-        line["cpu_baseline"] = bench_cpu(pgw, __import__("oracle"), args.cpu_seconds)
+    oracle = None if args.no_cpu else __import__("oracle")
+    if oracle is not None:
+        line["cpu_baseline"] = bench_cpu(pgw, oracle, args.cpu_seconds)
         line["speedup_vs_cpu"] = round(line["value"] / line["cpu_baseline"]["value"], 1)
     if not args.no_sweep:
-        sweep = bench_gemv(torch, abi, pgw)
+        sweep = bench_gemv(torch, abi, pgw, oracle)
         line["gemv_sweep"] = sweep
         best = max(r["cold_gbs"] for r in sweep if r["fmt"] == "q4")
         line["gemv_q4_best_cold_frac_hbm"] = round(best / HBM_PEAK_GBS, 4)
@@ -485,7 +613,7 @@ def main():
                                  "frac": lm["cold_frac_hbm"], "bytes_per_launch": lm["bytes"],
                                  "us_per_launch": lm["cold_us"]}
     if not args.no_configs:
-        line["configs"] = bench_configs(mllm, pgw, args)
+        line["configs"] = bench_configs(mllm, pgw, args, oracle)
     print(json.dumps(line), flush=True)
 
 

@@ -198,9 +198,13 @@ int mllm_model_gemv(mllm_model *model, const char *name, const float *x, float *
  * kernel per decode call or chain, its workgroups ordered by per-item epoch
  * flags instead of grid barriers; 1 (the default otherwise) = one kernel per
  * phase, a chained step replayed from a HIP graph; 2 = the phase kernels
- * launched directly (for profilers).  Multi-token passes (prefill, verify)
- * always use the phase kernels.  Results are bit-identical across modes.
- * Returns MLLM_ERR_UNSUPPORTED for mode 3 where it is unavailable. */
+ * launched directly (for profilers); 4 = mode 3's kernel and grid through an
+ * ordinary (not cooperative) launch, for profilers that do not follow
+ * cooperative launches -- every workgroup is resident only while the device
+ * runs nothing else, so it is not a serving mode.  Multi-token passes
+ * (prefill, verify) always use the phase kernels.  Results are bit-identical
+ * across modes.  Returns MLLM_ERR_UNSUPPORTED for modes 3 and 4 where the
+ * persistent kernel is unavailable. */
 int mllm_set_exec_mode(mllm_model *model, int mode);
 
 /* No reference counterpart: the execution mode the next decode call will use

@@ -1868,6 +1868,16 @@ int launch_flow(mllm_model *M, int steps) {
   F.ep0 = M->flow_epoch + 1;
   F.steps = steps;
   void *args[] = {&M->P, &F};
+  if (M->exec_mode == 4) {
+    // the same kernel and grid through an ordinary launch (profilers that do
+    // not follow cooperative launches): every workgroup is resident only if
+    // the device runs nothing else meanwhile; a wait that times out is
+    // reported as an error, as in mode 3
+    hipLaunchKernelGGL(kFlowKernels[M->aq_idx], dim3(M->flow_grid), dim3(FLT), M->flow_lds, M->stream, M->P, F);
+    MLLM_HIP(hipGetLastError());
+    M->flow_epoch += steps;
+    return 0;
+  }
   const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(kFlowKernels[M->aq_idx]),
                                                   dim3(M->flow_grid), dim3(FLT), args, M->flow_lds, M->stream);
   if (e == hipSuccess) {
@@ -1959,7 +1969,7 @@ int run_pass(mllm_model *M, const int32_t *ids, int m, int pos0, int lm_rows) {
   for (int i = 0; i < m; ++i) s.tok[i] = ids[i];
   if (int rc = upload_state(M)) return rc;
   MLLM_HIP(hipEventRecord(M->ev0, M->stream));
-  int rc = M->exec_mode == 3 && m == 1 && lm_rows == 1 ? launch_flow(M, 1) : kFlowFellBack;
+  int rc = M->exec_mode >= 3 && m == 1 && lm_rows == 1 ? launch_flow(M, 1) : kFlowFellBack;
   if (rc == kFlowFellBack) rc = enqueue_pass_phases(M, m, lm_rows != 0);
   if (rc) return rc;
   MLLM_HIP(hipEventRecord(M->ev1, M->stream));
@@ -2325,9 +2335,11 @@ extern "C" int mllm_max_pass_tokens(const mllm_model *M) { return M ? M->max_pas
 
 extern "C" int mllm_set_exec_mode(mllm_model *M, int mode) {
   MLLM_CHECK(M, "null model");
-  MLLM_CHECK(mode >= 1 && mode <= 3, "exec mode %d (1: graph replay, 2: direct launches, 3: persistent kernel)",
+  MLLM_CHECK(mode >= 1 && mode <= 4,
+             "exec mode %d (1: graph replay, 2: direct launches, 3: persistent kernel, 4: persistent kernel, "
+             "ordinary launch)",
              mode);
-  if (mode == 3 && !M->flow_grid) return set_error(MLLM_ERR_UNSUPPORTED, "persistent kernel unavailable on this device");
+  if (mode >= 3 && !M->flow_grid) return set_error(MLLM_ERR_UNSUPPORTED, "persistent kernel unavailable on this device");
   M->exec_mode = mode;
   M->flow_default = false;
   return 0;
@@ -2424,7 +2436,7 @@ extern "C" int mllm_decode_chain(mllm_model *M, int32_t first, int n_steps, int3
   s.tok[0] = first;
   if (int rc = upload_state(M)) return rc;
   MLLM_HIP(hipEventRecord(M->ev0, M->stream));
-  int rc = M->exec_mode == 3 ? launch_flow(M, n_steps) : kFlowFellBack;
+  int rc = M->exec_mode >= 3 ? launch_flow(M, n_steps) : kFlowFellBack;
   if (rc == kFlowFellBack) {
     rc = 0;
     if (M->exec_mode == 2) {

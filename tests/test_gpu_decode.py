@@ -60,9 +60,11 @@ def test_small_teacher_forced_vs_oracle(oracle_lib, arch, mode):
 
 @gpu
 def test_exec_modes_bit_identical():
+    """Modes 1-3 and mode 4 (the persistent kernel through an ordinary
+    launch, for profilers) give the same logits bit for bit."""
     bundle = build("llama", seed=5)
     outs = []
-    for mode in MODES:
+    for mode in MODES + [4]:
         g = mllm.PetitGPT(bundle, exec_mode=mode)
         rows = [g.forwardPrompt([1, 2, 3, 4, 5]).copy()]
         for t in (6, 7, 8):
