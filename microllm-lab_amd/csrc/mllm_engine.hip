@@ -653,42 +653,61 @@ __device__ void phase_qkv(const DecParams &P, const LayerW &Lw, int m, int li, i
 }
 
 // ---------------------------------------------------------------- attention
-// One (token, split, head) item, 1024 threads.  Every K/V load of the item
-// is issued at once: the score of key p of the split is formed by the four
-// lanes 4p .. 4p+3 (16 dimensions each, joined with DPP); thread (kg, d4)
-// owns V[kg + 64j][4*d4 .. 4*d4+3] for j < 4.  The last split of (token,
-// head) to finish -- counted in P.cnt; a single split is its own last --
-// merges the splits (flash-decoding merge in split order) and writes the
-// head's partial of the attention output projection to P.opart.
+// One (token, split, head) item, 1024 threads: wave w takes keys
+// 16w .. 16w+15 of the split.  Every K/V load of the item is issued at once:
+// the score of key p is formed by the four lanes 4p .. 4p+3 (16 dimensions
+// each, joined with DPP), and lane d of wave w holds V[16w + k][d] for
+// k < 16.  Each wave forms its keys' softmax statistics (max, sum of
+// weights) and its P.V for the 64 dimensions by itself, with no exchange
+// between waves; wave 0 merges the 16 wave partials in wave order (the
+// flash-decoding merge).  The last split of (token, head) to finish --
+// counted in P.cnt; a single split is its own last -- merges the splits the
+// same way, in split order, and writes the head's partial of the attention
+// output projection to P.opart.
+constexpr int AW = AT / 64;  // waves of an attention item; 16 keys each (AW * 16 == ACH)
+static_assert(AW * 16 == ACH, "one wave per 16 keys of a split");
 struct AttnLds {
-  float *qs;    // 64: the query
-  float *es;    // 256: exp weights
-  float *sc;    // 256: scores
-  float *pv;    // 64 x 64
-  float *pv2;   // 4 x 64
-  float *own;      // 64: this split's P.V
+  float *qs;       // 64: the query
+  float *wm, *wl;  // AW: each wave's score maximum and sum of weights
+  float *wacc;     // AW x 64: each wave's P.V
   uint32_t *attq;  // 2 x Q6R: merged head output, staged for the W_o slice
   int *flag;
 };
-constexpr int ATT_LDS = HD + 2 * ACH + 64 * HD + 4 * HD + HD + 2 * Q6R + 4;  // floats
+constexpr int ATT_LDS = HD + 2 * AW + AW * HD + 2 * Q6R + 4;  // floats
 
 __device__ __forceinline__ AttnLds attn_lds(float *base) {
   AttnLds A;
   A.qs = base;
-  A.es = A.qs + HD;
-  A.sc = A.es + ACH;
-  A.pv = A.sc + ACH;
-  A.pv2 = A.pv + 64 * HD;
-  A.own = A.pv2 + 4 * HD;
-  A.attq = reinterpret_cast<uint32_t *>(A.own + HD);
+  A.wm = A.qs + HD;
+  A.wl = A.wm + AW;
+  A.wacc = A.wl + AW;
+  A.attq = reinterpret_cast<uint32_t *>(A.wacc + AW * HD);
   A.flag = reinterpret_cast<int *>(A.attq + 2 * Q6R);
   return A;
 }
 
-// K rows of keys kp < nkeys (four lanes per key) and V rows (thread (kg, d4))
-// of the split starting at position s0 (coherent loads).  Keys at and past
-// nkeys are not loaded (at short contexts most lanes have none; duplicated
-// clamped loads measured slower here).
+// K rows of keys kp < nkeys (four lanes per key) and V rows (lane d of wave
+// w: dimension d of keys 16w .. 16w+15) of the split starting at position s0.
+// Keys at and past nkeys are not loaded (at short contexts most lanes have
+// none; duplicated clamped loads measured slower here).
+//
+// These are ordinary (L2-cached) loads, not device-coherent ones: a cached
+// row never changes once written, and it is first read -- on any XCD -- only
+// after its writer's tagged output has been seen, which follows the row's
+// completed stores (the item waits for them before it publishes).  The
+// cache line (128 B; a row is 256 B in f32, 128 B in f16, line-aligned)
+// therefore cannot be in a reader's L2 from before the write, except from an
+// earlier launch, and the persistent kernel opens with an agent-scope acquire
+// that drops such lines.  Each attention item runs on the same workgroup in
+// every step, so from the second step on its rows come from its XCD's L2.
+__device__ __forceinline__ float4 kv_ld4(const void *base, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(coh_rsrc(base), (int)off, 0, 0);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+__device__ __forceinline__ uint4 kv_ld16(const void *base, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(coh_rsrc(base), (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ void attn_k_load(const DecParams &P, int li, int kvh, int s0, int nkeys, float4 (&kr)[4]) {
   const uint32_t kbase = (uint32_t)kv_index(P, li, 0, kvh, s0);
   const int kp = tid() >> 2, ku = tid() & 3;
@@ -697,7 +716,7 @@ __device__ __forceinline__ void attn_k_load(const DecParams &P, int li, int kvh,
       const uint32_t off = 2u * (kbase + kp * HD + 16 * ku);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const uint4 u = coh_ld16(P.kv, off + 16u * j);
+        const uint4 u = kv_ld16(P.kv, off + 16u * j);
         const __half2 *hp = reinterpret_cast<const __half2 *>(&u);
         const float2 f0 = __half22float2(hp[0]), f1 = __half22float2(hp[1]);
         const float2 f2 = __half22float2(hp[2]), f3 = __half22float2(hp[3]);
@@ -707,45 +726,42 @@ __device__ __forceinline__ void attn_k_load(const DecParams &P, int li, int kvh,
     } else {
       const uint32_t off = 4u * (kbase + kp * HD + 16 * ku);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) kr[j] = coh_ld4(P.kv, off + 16u * j);
+      for (int j = 0; j < 4; ++j) kr[j] = kv_ld4(P.kv, off + 16u * j);
     }
   }
 }
 
-__device__ __forceinline__ void attn_v_load(const DecParams &P, int li, int kvh, int s0, int nkeys, float4 (&vr)[4]) {
-  const uint32_t vbase = (uint32_t)kv_index(P, li, 1, kvh, s0);
-  const int d4 = tid() & 15, kg = tid() >> 4;
+__device__ __forceinline__ void attn_v_load(const DecParams &P, int li, int kvh, int s0, int nkeys, float (&vr)[16]) {
+  const uint32_t vbase = (uint32_t)kv_index(P, li, 1, kvh, s0) + (uint32_t)lane_id();
+  const int k0 = 16 * wave_id();
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int k = kg + 64 * j;
-    if (k < nkeys) {
-      if (P.kv_fp16) {
-        const uint2 u = coh_ld8(P.kv, 2u * (vbase + k * HD + 4 * d4));
-        const __half2 *hp = reinterpret_cast<const __half2 *>(&u);
-        const float2 f0 = __half22float2(hp[0]), f1 = __half22float2(hp[1]);
-        vr[j] = make_float4(f0.x, f0.y, f1.x, f1.y);
-      } else {
-        vr[j] = coh_ld4(P.kv, 4u * (vbase + k * HD + 4 * d4));
-      }
+  for (int k = 0; k < 16; ++k) {
+    vr[k] = 0.f;
+    if (k0 + k < nkeys) {
+      const uint32_t e = vbase + (uint32_t)(k0 + k) * HD;
+      if (P.kv_fp16)
+        vr[k] = __half2float(__ushort_as_half(
+            __builtin_amdgcn_raw_buffer_load_b16(coh_rsrc(P.kv), (int)(2u * e), 0, 0)));
+      else
+        vr[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(coh_rsrc(P.kv), (int)(4u * e), 0, 0));
     }
   }
 }
 
-// Scores, split-local softmax statistics, P.V, the merge and the head's
-// W_o slice, with the query staged in A.qs and the keys in kr/vr; key knew
-// of the split (when >= 0) is taken from LDS instead (kvn: K row then V
-// row), selected where it is used so that no load of kr/vr is waited for
-// early.  Ro holds the slice when ro_loaded; the merging split of a
-// multi-split head loads it otherwise.  Returns true in the workgroup that
-// wrote the head's output.
+// Scores, softmax statistics, P.V, the merge and the head's W_o slice, with
+// the query staged in A.qs and the keys in kr/vr; key knew of the split (when
+// >= 0) is taken from LDS instead (kvn: K row then V row), selected where it
+// is used so that no load of kr/vr is waited for early.  Ro holds the slice
+// when ro_loaded; the merging split of a multi-split head loads it otherwise.
+// Returns true in the workgroup that wrote the head's output.
 template <int C>
 __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, int h, int ns, int cnt,
-                          const float4 (&kr)[4], const float4 (&vr)[4], int knew, const float *kvn, TileRegs<C> &Ro,
+                          const float4 (&kr)[4], const float (&vr)[16], int knew, const float *kvn, TileRegs<C> &Ro,
                           bool ro_loaded, const AttnLds &A, int tag) {
   const int D = P.D;
   const bool solo = ns == 1;
   const int kp = tid() >> 2, ku = tid() & 3;
-  const int d4 = tid() & 15, kg = tid() >> 4;
+  const int lane = lane_id(), wv = wave_id();
   __syncthreads();
   float part = 0.f;
   if (kp < cnt) {
@@ -766,57 +782,55 @@ __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, i
   part = part + dpp_f<0xB1>(part);
   part = part + dpp_f<0x4E>(part);
   const float score = kp < cnt ? part * P.attn_scale : -INFINITY;
-  // softmax statistics, reduced by every wave itself (no cross-wave
-  // exchange): the scores, then the weights, go through LDS once each
-  const int lane = tid() & 63;
-  if (ku == 0) A.sc[kp] = score;
+  // the wave's 16 keys: maximum, weights, their sum and P.V (lane = dimension)
+  const float mw = wave_max(score);  // -inf in a wave with no key
+  const float e = kp < cnt ? expf(score - mw) : 0.f;
+  const float lw = wave_sum(ku == 0 ? e : 0.f);
+  // branch-free: the new key's value is read from LDS once, and selected
+  const float vnew = kvn[HD + lane];
+  float acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int key = 16 * wv + k;
+    const float ek = readlane_f(e, 4 * k);
+    float vv = key == knew ? vnew : vr[k];
+    vv = key < cnt ? vv : 0.f;
+    acc = __builtin_fmaf(ek, vv, acc);
+  }
+  A.wacc[wv * HD + lane] = acc;
+  if (lane == 0) {
+    A.wm[wv] = mw;
+    A.wl[wv] = lw;
+  }
   __syncthreads();
-  float ml = -INFINITY;
+  // wave 0: the split's maximum, sum and P.V from the wave partials, added
+  // in wave order.  Lane w < AW forms wave w's weight expf(m_w - max) (a
+  // wave with no key has m_w = -inf and weight 0; wave 0 always has key 0);
+  // the weights reach every lane as scalars.
+  float mx = 0.f, l = 0.f, own = 0.f;
+  if (wv == 0) {
+    const float wm = lane < AW ? A.wm[lane] : -INFINITY;
+    const float wl = lane < AW ? A.wl[lane] : 0.f;
+    mx = wave_max(wm);
+    const float f = lane < AW ? expf(wm - mx) : 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) ml = fmaxf(ml, A.sc[lane + 64 * j]);  // -inf past cnt
-  const float mx = wave_max(ml);
-  const float e = kp < cnt ? expf(score - mx) : 0.f;
-  if (ku == 0) A.es[kp] = e;
-  __syncthreads();
-  float ll = 0.f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) ll += A.es[lane + 64 * j];
-  const float l = wave_sum(ll);
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int k = kg + 64 * j;
-    if (k < cnt) {
-      const float ek = A.es[k];
-      const float4 vv = k == knew ? reinterpret_cast<const float4 *>(kvn + HD)[d4] : vr[j];
-      acc.x = __builtin_fmaf(ek, vv.x, acc.x);
-      acc.y = __builtin_fmaf(ek, vv.y, acc.y);
-      acc.z = __builtin_fmaf(ek, vv.z, acc.z);
-      acc.w = __builtin_fmaf(ek, vv.w, acc.w);
+    for (int w = 0; w < AW; ++w) {
+      const float fw = readlane_f(f, w);
+      l = __builtin_fmaf(readlane_f(wl, w), fw, l);
+      own = __builtin_fmaf(A.wacc[w * HD + lane], fw, own);
     }
   }
-  *reinterpret_cast<float4 *>(A.pv + kg * HD + 4 * d4) = acc;
-  __syncthreads();
-  if (tid() < 4 * HD) {  // key groups 16q .. 16q+15 of dimension d
-    const int d = tid() & (HD - 1), q = tid() >> 6;
-    float a = 0.f;
-#pragma unroll
-    for (int g = 0; g < 16; ++g) a += A.pv[(16 * q + g) * HD + d];
-    A.pv2[q * HD + d] = a;
-  }
-  __syncthreads();
-  if (tid() < HD)
-    A.own[tid()] = (A.pv2[tid()] + A.pv2[HD + tid()]) + (A.pv2[2 * HD + tid()] + A.pv2[3 * HD + tid()]);
   // split partials of (t, h): [nsplit_max][APS] floats (m, l, pad, pad, acc[64])
   const float *parts = P.attp + (size_t)(t * P.NH + h) * P.nsplit_max * APS;
   if (!solo) {
     // publish this split, then count it; the last one merges
     float *dst = P.attp + ((size_t)(t * P.NH + h) * P.nsplit_max + sp) * APS;
-    __syncthreads();
-    if (tid() < HD) coh_stf(dst, 4u * (4 + tid()), A.own[tid()]);
-    if (tid() == 0) {
-      coh_stf(dst, 0, mx);
-      coh_stf(dst, 4, l);
+    if (wv == 0) {
+      coh_stf(dst, 4u * (4 + lane), own);
+      if (lane == 0) {
+        coh_stf(dst, 0, mx);
+        coh_stf(dst, 4, l);
+      }
     }
     wait_stores();
     __syncthreads();
@@ -830,23 +844,22 @@ __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, i
     if (!A.flag[0]) return false;
     if (!ro_loaded) slice_load<C, AT>(Lw.proj, 2 * h, D, Ro);
   }
-  __syncthreads();
-  if (tid() < HD) {
-    const int d = tid();
+  if (wv == 0) {
+    const int d = lane;
     float v;
     if (solo) {
-      v = A.own[d] / l;  // the merge below with one split: weight expf(0) = 1
+      v = own / l;  // the merge below with one split: weight expf(0) = 1
     } else {
       float M = sp == 0 ? mx : coh_ldf(parts, 0);
       for (int j = 1; j < ns; ++j) M = fmaxf(M, j == sp ? mx : coh_ldf(parts, 4u * (j * APS)));
       const float m0 = sp == 0 ? mx : coh_ldf(parts, 0), l0 = sp == 0 ? l : coh_ldf(parts, 4),
-                  a0 = sp == 0 ? A.own[d] : coh_ldf(parts, 4u * (4 + d));
+                  a0 = sp == 0 ? own : coh_ldf(parts, 4u * (4 + d));
       const float w0 = expf(m0 - M);
       float ls = __builtin_fmaf(l0, w0, 0.f), as = __builtin_fmaf(a0, w0, 0.f);
       for (int j = 1; j < ns; ++j) {
         const float mj = j == sp ? mx : coh_ldf(parts, 4u * (j * APS));
         const float lj = j == sp ? l : coh_ldf(parts, 4u * (j * APS + 1));
-        const float aj = j == sp ? A.own[d] : coh_ldf(parts, 4u * (j * APS + 4 + d));
+        const float aj = j == sp ? own : coh_ldf(parts, 4u * (j * APS + 4 + d));
         const float w = expf(mj - M);
         ls = __builtin_fmaf(lj, w, ls);
         as = __builtin_fmaf(aj, w, as);
@@ -884,7 +897,8 @@ __device__ bool phase_attn(const DecParams &P, const LayerW &Lw, int m, int li, 
   }
   const int cnt = min(ACH, pos + 1 - s0);
   const AttnLds A = attn_lds(smem);
-  float4 kr[4], vr[4];
+  float4 kr[4];
+  float vr[16];
   if (tid() < HD) A.qs[tid()] = coh_ldf(P.q, 4u * ((t * P.NH + h) * HD + tid()));
   attn_k_load(P, li, h / (P.NH / P.NKV), s0, cnt, kr);
   attn_v_load(P, li, h / (P.NH / P.NKV), s0, cnt, vr);
@@ -941,7 +955,7 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // ng Q6 records
   float *blk = part + nch, *red = blk + nb * D, *kvn = red + 32;  // kvn: the new K row (64) then V row (64)
   float *rs = kvn + 2 * HD;  // 3 x 64 row sums: q, k, v
-  const AttnLds A = attn_lds(rs + 3 * HD);
+  const AttnLds A = attn_lds(rs + 3 * HD);  // 16-byte aligned: every region before it is a multiple of 4 floats
   const int wv = wave_id(), lane = lane_id();
   // rows of the fused tile: [q head h | K head kvh | V head kvh], 64 each
   const int rq = h * HD, rk = (P.NH + kvh) * HD, rv = (P.NH + P.NKV + kvh) * HD;
@@ -949,7 +963,8 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   TileRegs<SC> Ro;
   GainsReg GR;
   float c_own = 0.f, s_own = 0.f;
-  float4 kr[4], vr[4];
+  float4 kr[4];
+  float vr[16];
   ResidReg R0;
   float4 base = make_float4(0.f, 0.f, 0.f, 0.f);
   // wave w < 3 forms row (w: q, k, v) lane d of the tile: its RoPE entries
@@ -980,6 +995,7 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   // and the V rows are not all held at once
   __builtin_amdgcn_sched_barrier(0);
   attn_k_load(P, li, kvh, s0, last ? cnt - 1 : cnt, kr);  // cached positions: written by earlier steps
+  attn_v_load(P, li, kvh, s0, last ? cnt - 1 : cnt, vr);
   __builtin_amdgcn_sched_barrier(0);
   // the residual (layer 0: the embedding) and the norm
   if (li == 0) base = embed_col(P, min(max(st_ld(P, ST_OFF(tok)), 0), P.V - 1), min(pos, P.max_seq - 1));
@@ -988,8 +1004,6 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   col_norm(P, x, gl, red, qx, ColOut{item == 0 ? P.xa : nullptr, st.tag + li});
   __syncthreads();
   tile_partials_fixed<AQC>(Wt, ng, nch, qx, part);
-  __builtin_amdgcn_sched_barrier(0);
-  attn_v_load(P, li, kvh, s0, last ? cnt - 1 : cnt, vr);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
   {
@@ -1612,6 +1626,9 @@ template <int AQC>
 __global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
   extern __shared__ float4 smem4[];
   float *smem = reinterpret_cast<float *>(smem4);
+  // lines of the KV cache that an XCD's L2 may still hold from before the
+  // launch are dropped before any ordinary load of the cache (kv_ld4)
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   const int w = blockIdx.x, G = gridDim.x;
   const int stride = P.NH + F.nm;
   int *const lm_cnt = F.flags + P.L * stride;
