@@ -212,6 +212,12 @@ int mllm_set_exec_mode(mllm_model *model, int mode);
  * 1); -1 for a null model. */
 int mllm_get_exec_mode(const mllm_model *model);
 
+/* No reference counterpart: the most tokens a verify pass (mllm_forward_verify)
+ * runs as one step of the persistent kernel in exec modes 3 and 4; longer
+ * passes, and every pass in modes 1 and 2, run the phase kernels (the same
+ * results, bit for bit).  0 when the persistent kernel is not in use. */
+int mllm_flow_verify_tokens(const mllm_model *model);
+
 /* Prompts of at least min_tokens tokens (default 2; 0 = never) are
  * processed in batches (no counterpart in the reference, whose GPU path runs
  * a prompt token by token, webgpu.js:1178-1187): tokens 0 .. n-2 go through

@@ -138,6 +138,8 @@ struct DecParams {
   uint2 *opart;   // [MAXT][NH][D] per-head partials of W_o . att, tagged pairs
   uint2 *dpart;   // [MAXT][nchunk][D] per-chunk partials of W_2 . h, tagged pairs
   float *xn;      // [MAXT][D] final-normed rows for the lm_head
+  uint2 *rec;     // [2][MAXT][D/32 * Q6R] verify step: normed rows as tagged Q6 record dwords (attention, MLP)
+  uint2 *qkvr;    // [L][MAXT][(NH + 2 NKV) * HD] verify step: q/k/v rows as tagged pairs, per layer
   float *q;       // [MAXT][NH*HD] queries after RoPE
   void *kv;       // [L][2][NKV][max_seq][HD] (f32 or f16)
   float *attp;    // [MAXT][NH][nsplit_max][APS]
@@ -1238,23 +1240,21 @@ __device__ __forceinline__ void lm_tile(const DecParams &P, const LmGeom &L, con
     const int t = e / nr, r = e - t * nr;
     P.logits[(size_t)(tb + t) * P.V + r0 + r] = s.out[t * rpt + r];
   }
-  if (tid() < 64) {
-    for (int t = 0; t < m; ++t) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int r = tid(); r < nr; r += 64) {
-        float v = s.out[t * rpt + r];
-        if (penal) v = gpt2_adjust(v, r0 + r, s.lists + 34, nban, s.lists + 2, nrec);
-        if (amax_better(v, r0 + r, bv, bi)) {
-          bv = v;
-          bi = r0 + r;
-        }
+  for (int t = wave_id(); t < m; t += NT / 64) {  // token t on wave t % (NT / 64)
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int r = lane_id(); r < nr; r += 64) {
+      float v = s.out[t * rpt + r];
+      if (penal) v = gpt2_adjust(v, r0 + r, s.lists + 34, nban, s.lists + 2, nrec);
+      if (amax_better(v, r0 + r, bv, bi)) {
+        bv = v;
+        bi = r0 + r;
       }
-      wave_argmax(bv, bi);
-      if (tid() == 0) {
-        coh_stf(P.amv, 4u * ((tb + t) * P.lm_tiles + tile), bv);
-        coh_sti(P.ami, 4u * ((tb + t) * P.lm_tiles + tile), bi);
-      }
+    }
+    wave_argmax(bv, bi);
+    if (lane_id() == 0) {
+      coh_stf(P.amv, 4u * ((tb + t) * P.lm_tiles + tile), bv);
+      coh_sti(P.ami, 4u * ((tb + t) * P.lm_tiles + tile), bi);
     }
   }
   __syncthreads();
@@ -1498,6 +1498,8 @@ static const char *const kPhaseNames[PH_COUNT] = {"QKV", "ATTN", "MLP", "FINAL",
 struct FlowGeom {
   int *flags;             // [L][NH + nm] attention heads and MLP chunks, LM counter, ARGMAX
   int ep0, steps;         // epoch of the launch's first step; chained steps
+  int m;                  // tokens of a verify step (k_flowm; the decode kernel takes 1)
+  int tq, ta, mt;         // k_flowm: tokens per QKV, attention and MLP item (the items of a stage are x token group)
   int na, nm, ni;         // items per layer: attention (split, head) items, MLP chunks; ni = na + nm
   int lm_rpt, lm_tiles;   // lm_head tiles of the 1024-thread role (one per workgroup w < lm_tiles, then w + G ...)
 };
@@ -1696,8 +1698,592 @@ __global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
   }
 }
 
+// ---------------------------------------------------------------- verify step
+// The persistent kernel's m-token verify step (k_flowm: speculation's k + 1
+// rows, webgpu.js:568-685).  Each layer runs five stages of items; the token
+// work of a stage is spread over its items and over the workgroup instead of
+// being taken one token at a time:
+//   NA(t)  token t's residual (layer 0: the embedding) and attention norm:
+//          the residual row xa[t] and the normed row's Q6 records rec[0][t];
+//   QKV    (row head, token group): 64 rows of attn.qkv for the group's
+//          tokens, the q/k/v rows to P.qkvr, the K/V rows to the cache;
+//   ATT    (split, head, token group): the group's scores and P.V over the
+//          split, the merges, the W_o slice;
+//   NM(t)  token t's residual after attention xb[t] and the MLP norm's
+//          records rec[1][t];
+//   MLP    (unit block, token group): gate/up rows, activation and the
+//          down-projection slice of the group's tokens.
+// After the last layer NA(t) forms the final norm's records for the lm_head
+// tiles.  A residual is summed once per token rather than once per consumer
+// item, so each partial row is read once per token and layer.  Every token's
+// arithmetic is the single-token step's (the same functions in the same
+// order), so each row of a verify step is, bit for bit, the decode step at
+// that position.  The records are tagged pairs like every other handoff, with
+// tag st.tag + layer (st.tag + L for the final norm).
+constexpr int VQB = 4;  // tokens per batch of the attention item's q/k/v rows
+constexpr int VMB = 4;  // tokens per batch of the MLP item's gate/up rows
+constexpr int VLB = 4;  // tokens per pass over an lm_head tile
+
+// The n dwords at LDS src as tagged pairs at dst.
+__device__ __forceinline__ void rec_put(uint2 *dst, const uint32_t *src, int n, int tag) {
+  for (int i = tid(); i < n; i += 1024) coh_st8(dst, (uint32_t)i * 8u, make_uint2(src[i], (uint32_t)tag));
+}
+
+// n tagged dwords into LDS dst, loaded again until every tag reaches want:
+// eight pairs per thread in flight.  Branch-free loads (lanes past n read the
+// last pair).
+__device__ __forceinline__ void rec_get(const DecParams &P, const uint2 *src, int n, int want, uint32_t *dst) {
+  for (int b = 0; b < n; b += 8 * 1024) {
+    uint2 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = tag_ld(src, (uint32_t)min(b + (int)tid() + k * 1024, n - 1));
+    for (unsigned spins = 1;; ++spins) {
+      bool ready = true;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ready &= tag_ok(v[k].y, want);
+      if (ready || poll_give_up(P, spins)) break;
+      poll_fence();
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = tag_ld(src, (uint32_t)min(b + (int)tid() + k * 1024, n - 1));
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = b + (int)tid() + k * 1024;
+      if (i < n) dst[i] = v[k].x;
+    }
+  }
+}
+
+__device__ __forceinline__ uint2 *rec_row(const DecParams &P, int side, int t) {
+  return P.rec + ((size_t)side * MAXT + t) * (P.D >> 5) * Q6R;
+}
+
+// Norm item t.  side 0 at layer li < L: the attention norm (phase_attn1's
+// residual and norm); li == L: the final norm (final_row's), no residual row
+// written; side 1: the MLP norm (phase_mlp's).
+__device__ void flowm_norm(const DecParams &P, int li, int t, int side, const Step &st, float *smem) {
+  const int D = P.D, ng = D >> 5, nq = D >> 2;
+  const bool gpt2 = P.arch == 1, fin = li == P.L;
+  const LayerW &Lw = P.layers[min(li, P.L - 1)];
+  const float *gain = side ? Lw.n2 : fin ? P.norm_f : Lw.n1;
+  const float *rbias = !gpt2 ? nullptr : side ? Lw.proj_b : li == 0 ? nullptr : fin ? P.last_mproj_b : Lw.prev_mproj_b;
+  const int np = side ? P.NH : P.nchunk;
+  const int want = st.tag + li - (side ? 0 : 1);  // the inputs' tag
+  float *gl = smem;
+  uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // ng Q6 records
+  float *blk = gl + al4(3 * D) + al4(ng * Q6R), *red = blk + ((np + PB - 1) / PB) * D;
+  GainsReg GR;
+  gains_load(P, gain, rbias, GR);
+  gains_store(P, rbias, GR, gl);
+  float4 x;
+  if (side == 0 && li == 0) {
+    const int tok = min(max(st_ld(P, ST_OFF(tok) + 4u * t), 0), P.V - 1);
+    x = embed_col(P, tok, min(st.pos0 + t, P.max_seq - 1));
+    __syncthreads();
+  } else {
+    const uint2 *brow = (side ? P.xa : P.xb) + (size_t)t * D;
+    const uint2 *prow = side ? P.opart + (size_t)t * P.NH * D : P.dpart + (size_t)t * P.nchunk * D;
+    const float4 base = col_base_load<true>(P, brow, nq, want);
+    resid_blocks<true>(P, prow, np, want, blk);
+    __syncthreads();
+    x = col_finish(blk, nq, np, base, gl, D, rbias != nullptr);
+  }
+  col_norm(P, x, gl, red, qx, ColOut{fin ? nullptr : (side ? P.xb : P.xa) + (size_t)t * D, st.tag + li});
+  __syncthreads();
+  rec_put(rec_row(P, side, t), qx, ng * Q6R, st.tag + li);
+}
+
+// QKV item of the verify step: rows [rh*64, rh*64 + 64) of attn.qkv (query
+// head rh, K head rh - NH or V head rh - NH - NKV) for tokens [t0, t0 + nt):
+// phase_qkv's arithmetic (tile_partials, four-lane row sums, RoPE or the
+// bias), which is the single-token step's.  The rows go to P.qkvr as tagged
+// pairs (K and V rows rounded as the cache stores them), the K and V rows
+// also to the cache.  nt <= VQT.
+constexpr int VQT = 8;  // tokens per QKV item at most (its LDS)
+__device__ void flowm_qkv(const DecParams &P, const LayerW &Lw, int li, int rh, int t0, int nt, const Step &st,
+                          float *smem) {
+  const int D = P.D, ng = D >> 5, nch = HD * ng;
+  const int nrow = (P.NH + 2 * P.NKV) * HD;
+  const bool gpt2 = P.arch == 1;
+  const bool is_q = rh < P.NH, is_k = !is_q && rh < P.NH + P.NKV;
+  uint32_t *qx = reinterpret_cast<uint32_t *>(smem);  // nt x ng Q6 records
+  float *part = smem + al4(nt * ng * Q6R);            // nt x nch chunk partials
+  float *rs = part + nt * nch;                        // nt x 64 row sums
+  float *rt = rs + nt * HD;                           // nt x (cos, sin) (gpt2: the bias)
+  TileRegs<QC> R;
+  tile_load<QC, QT>(Lw.qkv, rh * HD, HD, 0, ng, nch, R);
+  if ((int)tid() < nt * HD) {
+    const int tt = tid() / HD, d = tid() - tt * HD;
+    if (gpt2) {
+      rt[tt * 2 * HD + d] = Lw.qkv_b[rh * HD + d];
+    } else {
+      const size_t ri = (size_t)min(st.pos0 + t0 + tt, P.max_seq - 1) * HD + d;
+      rt[tt * 2 * HD + d] = P.rope_cos[ri];
+      rt[tt * 2 * HD + HD + d] = P.rope_sin[ri];
+    }
+  }
+  rec_get(P, rec_row(P, 0, t0), nt * ng * Q6R, st.tag + li, qx);
+  __syncthreads();
+  tile_partials<QC>(R, ng, nch, nt, qx, part);
+  __syncthreads();
+  // the nt x 64 row sums, four lanes each (the decode attention item's order)
+  for (int base = 0; base < nt * HD; base += 256) {
+    const int r = base + (int)(tid() >> 2);
+    const int rr = min(r, nt * HD - 1), tr = rr / HD;
+    const float a = row_sum4(part + tr * nch + (rr - tr * HD) * ng, ng, tid() & 3);
+    if ((tid() & 3) == 0 && r < nt * HD) rs[r] = a;
+  }
+  __syncthreads();
+  // token t0 + tt on wave tt, lane d = head dimension d
+  for (int tt = wave_id(); tt < nt; tt += NWV) {
+    const int d = lane_id(), t = t0 + tt, pos = st.pos0 + t;
+    float v = rs[tt * HD + d];
+    if (gpt2) {
+      v = v + rt[tt * 2 * HD + d];  // the bias
+    } else if (is_q || is_k) {
+      const float mate = __shfl_xor(v, 32);  // rotate-half partner d +- 32
+      v = __builtin_fmaf(v, rt[tt * 2 * HD + d], (d < 32 ? -mate : mate) * rt[tt * 2 * HD + HD + d]);
+    }
+    float r = v;
+    if (!is_q) {
+      const int kvh = is_k ? rh - P.NH : rh - P.NH - P.NKV;
+      const size_t k = kv_index(P, li, is_k ? 0 : 1, kvh, pos) + d;
+      if (P.kv_fp16) {
+        const __half hv = __float2half_rn(v);
+        r = __half2float(hv);
+        coh_sth(P.kv, 2u * (uint32_t)k, __half_as_ushort(hv));
+      } else {
+        coh_stf(P.kv, 4u * (uint32_t)k, v);
+      }
+    }
+    tag_st(P.qkvr, (uint32_t)((li * MAXT + t) * nrow + rh * HD + d), r, st.tag + li);
+  }
+}
+
+// The q rows of tokens [u0, u1) of head h and the K and V rows of tokens
+// [0, u1) of KV head kvh from layer li's P.qkvr into LDS (qrows: row t; kvn:
+// row t = K then V), each pair loaded again until its tag reaches want.  An
+// attention item reads the K/V rows of earlier token groups, whose items may
+// run a layer ahead: each layer keeps its own rows, so none is overwritten
+// within the pass.
+__device__ __forceinline__ void qkv_rows_get(const DecParams &P, int li, int want, int u0, int u1, int h, int kvh,
+                                             float *qrows, float *kvn) {
+  const int nrow = (P.NH + 2 * P.NKV) * HD;
+  const int nqr = (u1 - u0) * HD, n = nqr + u1 * 2 * HD;  // <= 3 x 16 x 64
+  uint32_t src[3];
+  float *dst[3];
+  uint2 v[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int i = min((int)tid() + k * 1024, n - 1);
+    int t, col;
+    if (i < nqr) {
+      t = u0 + i / HD;
+      col = h * HD + (i - (i / HD) * HD);
+      dst[k] = qrows + t * HD + (col - h * HD);
+    } else {
+      const int j = i - nqr, tk = j / (2 * HD), e = j - tk * 2 * HD;  // e < 64: K, else V
+      t = tk;
+      col = (e < HD ? P.NH + kvh : P.NH + P.NKV + kvh) * HD + (e & (HD - 1));
+      dst[k] = kvn + tk * 2 * HD + e;
+    }
+    src[k] = (uint32_t)((li * MAXT + t) * nrow + col);
+    v[k] = tag_ld(P.qkvr, src[k]);
+  }
+  for (unsigned spins = 1;; ++spins) {
+    bool ready = true;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) ready &= tag_ok(v[k].y, want);
+    if (ready || poll_give_up(P, spins)) break;
+    poll_fence();
+#pragma unroll
+    for (int k = 0; k < 3; ++k) v[k] = tag_ld(P.qkvr, src[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+    if ((int)tid() + k * 1024 < n) *dst[k] = __uint_as_float(v[k].x);
+}
+
+// Attention item (split sp, head h, tokens [u0, u1)) of the verify step: the
+// scores, softmax statistics and P.V of every token of the range whose
+// position reaches the split (attn_core's arithmetic), the merges (wave w
+// takes tokens ta + w, ta + w + 16, ...) and the W_o slice of each token
+// this item completes.  Cached keys (< pos0) come from the cache; the pass's
+// own K/V rows come from the QKV items (rounded as the cache holds them).
+__device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int item, int u0, int u1, const Step &st,
+                           int m, float *smem) {
+  const int sp = item / P.NH, h = item - sp * P.NH;
+  const int pos0 = st.pos0, s0 = sp * ACH;
+  if (s0 > pos0 + u1 - 1) return;  // no token of the range reaches this split
+  const int rep = P.NH / P.NKV, kvh = h / rep;
+  const int D = P.D;
+  const int ta = max(u0, s0 - pos0);  // the first token of the range whose position reaches this split
+  const int knew = pos0 - s0;         // keys from knew on are the pass's own rows (LDS row key - knew)
+  const int ncached = min(max(knew, 0), ACH);
+  const int wv = wave_id(), lane = lane_id();
+  float *kvn = smem;                  // m x (K row, V row)
+  float *qrows = kvn + m * 2 * HD;    // m x 64 queries
+  float *wacc = qrows + m * HD, *wm = wacc + m * AW * HD, *wl = wm + m * AW;  // per token: AW x 64 P.V, AW maxima, sums
+  uint32_t *attq = reinterpret_cast<uint32_t *>(wl + m * AW);  // m x 2 Q6 records: the head outputs
+  int *flag = reinterpret_cast<int *>(attq + m * 2 * Q6R);     // m: this item writes token t's output
+  TileRegs<SC> Ro;
+  slice_load<SC, AT>(Lw.proj, 2 * h, D, Ro);
+  float4 kr[4];
+  float vr[16];
+  attn_k_load(P, li, kvh, s0, ncached, kr);  // cached positions: written by earlier steps
+  attn_v_load(P, li, kvh, s0, ncached, vr);
+  qkv_rows_get(P, li, st.tag + li, u0, u1, h, kvh, qrows, kvn);
+  __syncthreads();
+  // this thread's K quarter and V values of the split, cached or the pass's
+  // own (row key - knew, clamped: keys past the range's last row are past
+  // every count of the range)
+  const int kp = tid() >> 2, ku = tid() & 3;
+  float4 kk[4];
+  float vs[16];
+  {
+    const float4 *kn = reinterpret_cast<const float4 *>(kvn + 2 * HD * min(max(kp - knew, 0), u1 - 1));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kk[j] = kp >= knew ? kn[4 * ku + j] : kr[j];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int key = 16 * wv + k;
+      vs[k] = key >= knew ? kvn[2 * HD * min(max(key - knew, 0), u1 - 1) + HD + lane] : vr[k];
+    }
+  }
+  // every token's scores, wave statistics and P.V (attn_core's arithmetic;
+  // keys past the count have weight 0 and finite values, which changes at
+  // most the sign of a zero sum, and the Q6 staging of the output drops it)
+  for (int t = ta; t < u1; ++t) {
+    const int cnt = min(ACH, pos0 + t + 1 - s0);
+    float pt = 0.f;
+    if (kp < cnt) {
+      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+      const float *qq = qrows + t * HD + 16 * ku;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a0 = __builtin_fmaf(qq[4 * j + 0], kk[j].x, a0);
+        a1 = __builtin_fmaf(qq[4 * j + 1], kk[j].y, a1);
+        a2 = __builtin_fmaf(qq[4 * j + 2], kk[j].z, a2);
+        a3 = __builtin_fmaf(qq[4 * j + 3], kk[j].w, a3);
+      }
+      pt = (a0 + a1) + (a2 + a3);
+    }
+    pt = pt + dpp_f<0xB1>(pt);
+    pt = pt + dpp_f<0x4E>(pt);
+    const float score = kp < cnt ? pt * P.attn_scale : -INFINITY;
+    const float mw = wave_max(score);
+    const float e = kp < cnt ? expf(score - mw) : 0.f;
+    const float lw = wave_sum(ku == 0 ? e : 0.f);
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc = __builtin_fmaf(readlane_f(e, 4 * k), vs[k], acc);
+    wacc[(t * AW + wv) * HD + lane] = acc;
+    if (lane == 0) {
+      wm[t * AW + wv] = mw;
+      wl[t * AW + wv] = lw;
+    }
+  }
+  __syncthreads();
+  // each token's split statistics from its wave partials, in wave order; a
+  // solo split stages its output, the others publish their partials
+  for (int t = ta + wv; t < u1; t += NWV) {
+    const int ns = (pos0 + t) / ACH + 1;
+    const float wmv = lane < AW ? wm[t * AW + lane] : -INFINITY;
+    const float wlv = lane < AW ? wl[t * AW + lane] : 0.f;
+    const float mx = wave_max(wmv);
+    const float f = lane < AW ? expf(wmv - mx) : 0.f;
+    float l = 0.f, own = 0.f;
+#pragma unroll
+    for (int w = 0; w < AW; ++w) {
+      const float fw = readlane_f(f, w);
+      l = __builtin_fmaf(readlane_f(wlv, w), fw, l);
+      own = __builtin_fmaf(wacc[(t * AW + w) * HD + lane], fw, own);
+    }
+    if (ns == 1) {
+      q6_stage_lanes(own / l, attq + t * 2 * Q6R);
+    } else {
+      float *dst = P.attp + ((size_t)(t * P.NH + h) * P.nsplit_max + sp) * APS;
+      coh_stf(dst, 4u * (4 + lane), own);
+      if (lane == 0) {
+        coh_stf(dst, 0, mx);
+        coh_stf(dst, 4, l);
+      }
+      // kept for the merge, should this split finish last
+      wacc[t * AW * HD + lane] = own;
+      if (lane == 0) {
+        wm[t * AW] = mx;
+        wl[t * AW] = l;
+      }
+    }
+  }
+  wait_stores();
+  __syncthreads();
+  if ((int)tid() < m) {
+    const int t = tid();
+    int mine = 0;
+    if (t >= ta && t < u1) {
+      const int ns = (pos0 + t) / ACH + 1;
+      if (ns == 1) {
+        mine = 1;
+      } else {
+        // count this split; the last of (t, h) merges
+        unsigned *c = P.cnt + t * P.NH + h;
+        const unsigned arrived = atomicAdd(c, 1u);
+        mine = arrived == (unsigned)(ns - 1);
+        if (mine) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    flag[t] = mine;
+  }
+  __syncthreads();
+  for (int t = ta + wv; t < u1; t += NWV) {
+    const int ns = (pos0 + t) / ACH + 1;
+    if (ns == 1 || !flag[t]) continue;
+    // the splits of (t, h) in split order, this one's from LDS
+    const float *parts = P.attp + (size_t)(t * P.NH + h) * P.nsplit_max * APS;
+    const float mx = wm[t * AW], l = wl[t * AW], own = wacc[t * AW * HD + lane];
+    const int d = lane;
+    float M = sp == 0 ? mx : coh_ldf(parts, 0);
+    for (int j = 1; j < ns; ++j) M = fmaxf(M, j == sp ? mx : coh_ldf(parts, 4u * (j * APS)));
+    const float m0 = sp == 0 ? mx : coh_ldf(parts, 0), l0 = sp == 0 ? l : coh_ldf(parts, 4),
+                a0 = sp == 0 ? own : coh_ldf(parts, 4u * (4 + d));
+    const float w0 = expf(m0 - M);
+    float ls = __builtin_fmaf(l0, w0, 0.f), as = __builtin_fmaf(a0, w0, 0.f);
+    for (int j = 1; j < ns; ++j) {
+      const float mj = j == sp ? mx : coh_ldf(parts, 4u * (j * APS));
+      const float lj = j == sp ? l : coh_ldf(parts, 4u * (j * APS + 1));
+      const float aj = j == sp ? own : coh_ldf(parts, 4u * (j * APS + 4 + d));
+      const float w = expf(mj - M);
+      ls = __builtin_fmaf(lj, w, ls);
+      as = __builtin_fmaf(aj, w, as);
+    }
+    q6_stage_lanes(as / ls, attq + t * 2 * Q6R);
+  }
+  // the item's K/V cache rows are complete before any head output it writes
+  // becomes visible
+  wait_stores();
+  __syncthreads();
+  for (int t = ta; t < u1; ++t)
+    if (flag[t]) slice_gemv<SC, AT>(Ro, D, attq + t * 2 * Q6R, P.opart + (size_t)(t * P.NH + h) * D, st.tag + li);
+}
+
+// MLP item of the verify step: hidden units [item*UNITS, (item+1)*UNITS) of
+// tokens [ta, ta + m) (phase_mlp's arithmetic), VMB tokens per batch, then
+// the units' slice of the down projection for each of them.
+__device__ void flowm_mlp(const DecParams &P, const LayerW &Lw, int li, int item, const Step &st, int ta, int m,
+                          float *smem) {
+  const int D = P.D, ng = D >> 5, nch = UNITS * ng, S = (MT / ng) * ng;
+  const bool gpt2 = P.arch == 1;
+  uint32_t *qx = reinterpret_cast<uint32_t *>(smem);                   // m x ng Q6 records
+  float *part = smem + al4(m * ng * Q6R);                              // VMB x (gate || up) chunk partials
+  float *rsum = part + VMB * 2 * nch;                                  // VMB x (gate || up) row sums
+  uint32_t *hq = reinterpret_cast<uint32_t *>(rsum + VMB * 2 * UNITS);  // m x 2 Q6 records of h
+  MlpPre M;
+  mlp_pre_up(P, Lw, item, M);
+  slice_load<MC, MT>(Lw.w2, 2 * item, D, M.Rd);
+  const int want = st.tag + li;
+  rec_get(P, rec_row(P, 1, ta), m * ng * Q6R, want, qx);
+  __syncthreads();
+  const int wv = wave_id(), lane = lane_id(), g = tid() % ng;
+  for (int t0 = 0; t0 < m; t0 += VMB) {
+    const int nt = min(VMB, m - t0);
+    for (int tt = 0; tt < nt; ++tt) {
+      // gate chunks then up chunks against the thread's one group record
+      float *pt = part + tt * 2 * nch;
+      uint4 w[2 * MC];
+      float ws[2 * MC], o[2 * MC];
+#pragma unroll
+      for (int k = 0; k < MC; ++k) {
+        w[k] = M.Rg.w[k];
+        ws[k] = M.Rg.s[k];
+        w[MC + k] = M.Ru.w[k];
+        ws[MC + k] = M.Ru.s[k];
+      }
+      q4_dot6_planes<2 * MC>(w, ws, qx + ((t0 + tt) * ng + g) * Q6R, o);
+#pragma unroll
+      for (int k = 0; k < MC; ++k) {
+        const int c = tid() + k * S;
+        if ((int)tid() < S && c < nch) {
+          pt[c] = o[k];
+          if (!gpt2) pt[nch + c] = o[MC + k];
+        }
+      }
+    }
+    __syncthreads();
+    for (int tt = 0; tt < nt; ++tt) {
+      // row r (gate rows, then up rows): lane s adds partials s, s + 8, ...
+      // in order, then a fixed 8-lane tree
+      const float *pt = part + tt * 2 * nch;
+      const int r = tid() >> 3, s = tid() & 7;
+      const int nrows = gpt2 ? UNITS : 2 * UNITS;
+      const float *pr = pt + (r < UNITS ? 0 : nch) + (r & (UNITS - 1)) * ng;
+      float a = 0.f;
+      if (r < nrows)
+        for (int k = s; k < ng; k += 8) a = a + pr[k];
+      a = sum8f(a);
+      if (s == 0 && r < nrows) rsum[tt * 2 * UNITS + r] = a;
+    }
+    __syncthreads();
+    // token t0 + tt's activation on wave tt (unit = lane); the next batch's
+    // row sums overwrite rsum only after its partials' barrier
+    for (int tt = wv; tt < nt; tt += NWV) {
+      const float *rt = rsum + tt * 2 * UNITS;
+      const float gv = rt[lane];
+      float hv;
+      if (gpt2) {
+        const float v = gv + M.fcb;
+        hv = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+      } else {
+        hv = (gv / (1.0f + expf(-gv))) * rt[UNITS + lane];
+      }
+      q6_stage_lanes(hv, hq + (t0 + tt) * 2 * Q6R);
+    }
+  }
+  __syncthreads();
+  for (int t = 0; t < m; ++t)
+    slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * Q6R, P.dpart + ((size_t)(ta + t) * P.nchunk + item) * D, want);
+}
+
+// lm_head share of the verify step (tiles wg, wg + nwg, ...): every token's
+// logits rows and tile maxima against the final norm's records, VLB tokens
+// per pass over a tile (no penalties: a verify pass is greedy).  Returns
+// true when this workgroup computed at least one tile.
+__device__ bool flowm_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, const Step &st, int m, float *smem) {
+  if (wg >= L.ntiles) return false;
+  const int ng = P.D >> 5;
+  TileRegs<FTC> R;
+  int tile = wg;
+  lm_load<FTC, FLT>(P, L, tile, R);
+  LmLds s;
+  s.qx = reinterpret_cast<uint32_t *>(smem);
+  s.part = smem + al4(m * ng * Q6R);
+  s.out = s.part + VLB * FTC * FLT;
+  s.lists = nullptr;
+  rec_get(P, rec_row(P, 0, 0), m * ng * Q6R, st.tag + P.L, s.qx);
+  __syncthreads();
+  for (;;) {
+    for (int t0 = 0; t0 < m; t0 += VLB) {
+      LmLds u = s;
+      u.qx = s.qx + t0 * ng * Q6R;
+      lm_tile<FTC, FLT>(P, L, R, tile, t0, min(VLB, m - t0), u, false, 0, 0);
+    }
+    tile += nwg;
+    if (tile >= L.ntiles) break;
+    lm_load<FTC, FLT>(P, L, tile, R);
+  }
+  return true;
+}
+
+// Every row's first maximum over the tile maxima, one wave per row (the
+// relation is a total order on (value, index), so the order of the
+// comparisons does not change the result).
+__device__ void flowm_argmax(const DecParams &P, int ntiles, int m) {
+  for (int t = wave_id(); t < m; t += NWV) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int base = 0; base < ntiles; base += 8 * 64) {
+      float vv[8];
+      int iv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {  // all loads of the batch before any compare
+        const int k = min(base + lane_id() + j * 64, ntiles - 1);
+        vv[j] = coh_ldf(P.amv, 4u * (t * P.lm_tiles + k));
+        iv[j] = coh_ldi(P.ami, 4u * (t * P.lm_tiles + k));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (amax_better(vv[j], iv[j], bv, bi)) {
+          bv = vv[j];
+          bi = iv[j];
+        }
+    }
+    wave_argmax(bv, bi);
+    if (lane_id() == 0) st_st(P, ST_OFF(res) + 4u * t, bi);
+  }
+}
+
+// One verify step of m tokens in one launch (the stages above), then every
+// row's argmax.  Items are numbered per layer [NA(t) | QKV (row head, token
+// group of F.tq) | ATT (split, head, token group of F.ta) | NM(t) | MLP (unit
+// block, token group of F.mt)] and item j runs on workgroup j % G, each
+// workgroup taking its items layer by layer in order; an item waits only for
+// items of earlier stages or layers, so every wait ends.  The step is not
+// chained.
+__global__ __launch_bounds__(FLT) void k_flowm(DecParams P, FlowGeom F) {
+  extern __shared__ float4 smem4[];
+  float *smem = reinterpret_cast<float *>(smem4);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // as in k_flow: no stale cache lines of the KV cache
+  const int w = blockIdx.x, G = gridDim.x, m = F.m;
+  const int stride = P.NH + F.nm;
+  int *const lm_cnt = F.flags + P.L * stride;
+  int *const am_flag = lm_cnt + 1;
+  const int nlm = min(G, F.lm_tiles);
+  const LmGeom lg{F.lm_rpt, F.lm_tiles};
+  int *const red = reinterpret_cast<int *>(smem);
+  FlowCtl C{P, am_flag, F.ep0, false, false};
+  const int e = C.e;
+  const Step st{st_ld(P, ST_OFF(pos0)), false, (int)((uint32_t)e * (uint32_t)TAGL)};
+  const int nrh = P.NH + 2 * P.NKV;
+  const int ngq = (m + F.tq - 1) / F.tq, nga = (m + F.ta - 1) / F.ta, ngm = (m + F.mt - 1) / F.mt;  // token groups
+  const int iq = m, ia = iq + nrh * ngq, inm = ia + F.na * nga, im = inm + m, ni = im + F.nm * ngm;
+  for (int lv = 0; lv < P.L; ++lv) {
+    int li = lv;
+    asm volatile("" : "+s"(li));
+    const LayerW &Lw = P.layers[li];
+    int *const fl = F.flags + li * stride;
+    for (int jv = w; jv < ni; jv += G) {
+      int j = jv;
+      asm volatile("" : "+s"(j));
+      __syncthreads();  // the previous item's LDS is free
+      if (j < iq) {
+        flowm_norm(P, li, j, 0, st, smem);
+      } else if (j < ia) {
+        const int tg = (j - iq) / nrh, rh = (j - iq) - tg * nrh;
+        flowm_qkv(P, Lw, li, rh, tg * F.tq, min(F.tq, m - tg * F.tq), st, smem);
+      } else if (j < inm) {
+        const int tg = (j - ia) / F.na, it = (j - ia) - tg * F.na;
+        flowm_attn(P, Lw, li, it, tg * F.ta, min(m, (tg + 1) * F.ta), st, m, smem);
+      } else if (j < im) {
+        flowm_norm(P, li, j - inm, 1, st, smem);
+      } else {
+        const int tg = (j - im) / F.nm, it = (j - im) - tg * F.nm;
+        flowm_mlp(P, Lw, li, it, st, tg * F.mt, min(F.mt, m - tg * F.mt), smem);
+        // a hint for the lm_head's coarse waits (the records carry the tags that decide)
+        if (tid() == 0) flag_st(fl + P.NH + it, e);
+      }
+    }
+  }
+  if (w < m) {
+    __syncthreads();
+    flowm_norm(P, P.L, w, 0, st, smem);  // the final norm of token w
+  }
+  if (w < nlm) {
+    if (P.L > 4) {
+      C.wait<127>(F.flags + (P.L - 4) * stride + P.NH, F.nm);
+      C.wait<16>(F.flags + (P.L - 2) * stride + P.NH, F.nm);
+    }
+    __syncthreads();
+    if (flowm_lm(P, lg, w, G, st, m, smem)) {
+      // the last lm_head workgroup to finish takes every row's argmax
+      wait_stores();
+      __syncthreads();
+      if (tid() == 0) {
+        const int arrived = atomicAdd(lm_cnt, 1);
+        red[0] = arrived == nlm - 1;
+        if (red[0]) __hip_atomic_store(lm_cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (red[0]) {
+        flowm_argmax(P, F.lm_tiles, m);
+        flow_publish(am_flag, e);
+      }
+    }
+  }
+}
+
 using FlowKernel = void (*)(DecParams, FlowGeom);
 static const FlowKernel kFlowKernels[3] = {k_flow<4>, k_flow<5>, k_flow<6>};
+
 
 }  // namespace mllm
 
@@ -1735,6 +2321,8 @@ struct mllm_model {
   // persistent kernel (exec mode 3)
   FlowGeom flow{};
   int flow_grid = 0;      // 0: not available on this device
+  int flowm_max = 0;      // most tokens of a verify step in the persistent kernel (0: verify uses the phase kernels)
+  size_t flowm_lds = 0;
   bool flow_default = false;  // mode 3 was chosen by default, not by mllm_set_exec_mode
   size_t flow_lds = 0;
   int flow_epoch = 0;     // epochs used so far (flags hold epochs, never cleared)
@@ -1792,6 +2380,20 @@ size_t flow_lds_bytes(const DecParams &P, const FlowGeom &F) {
   const size_t nbd = (P.nchunk + PB - 1) / PB;
   f = std::max(f, al4(3 * (size_t)P.D) + ngd * Q6R + (size_t)FTC * FLT + (size_t)F.lm_rpt + 34 + P.max_seq +
                       nbd * P.D + 32);
+  return f * sizeof(float);
+}
+
+// The verify kernel for m tokens: the largest of its items' LDS (k_flowm).
+size_t flowm_lds_bytes(const DecParams &P, const FlowGeom &F, int m) {
+  const size_t ngd = P.D / 32, D = P.D, mm = m, mq = std::min(m, VQT);
+  const size_t nbd = (std::max(P.nchunk, P.NH) + PB - 1) / PB;
+  const size_t rec = al4(mm * ngd * Q6R);
+  size_t f = 2 * (FLT / 64);
+  f = std::max(f, al4(3 * D) + al4(ngd * Q6R) + nbd * D + 32);                       // norm items
+  f = std::max(f, al4(mq * ngd * Q6R) + mq * (HD * ngd + 3 * HD));                    // QKV items
+  f = std::max(f, mm * (3 * HD + AW * HD + 2 * AW + 2 * Q6R) + al4(mm));             // attention items
+  f = std::max(f, rec + VMB * (2 * UNITS * ngd + 2 * UNITS) + mm * 2 * Q6R);          // MLP items
+  f = std::max(f, rec + (size_t)VLB * FTC * FLT + (size_t)VLB * F.lm_rpt);            // lm_head share
   return f * sizeof(float);
 }
 
@@ -1880,10 +2482,12 @@ int launch_phase(mllm_model *M, int ph, int li, int m, hipEvent_t e0 = nullptr, 
 // default: the model then switches to mode 1 for good and the caller
 // enqueues the phase kernels instead (same results, bit for bit).
 constexpr int kFlowFellBack = -1;
+int launch_flowm(mllm_model *M, int m, int pos0);
 int launch_flow(mllm_model *M, int steps) {
   FlowGeom F = M->flow;
   F.ep0 = M->flow_epoch + 1;
   F.steps = steps;
+  F.m = 1;
   void *args[] = {&M->P, &F};
   if (M->exec_mode == 4) {
     // the same kernel and grid through an ordinary launch (profilers that do
@@ -1909,6 +2513,37 @@ int launch_flow(mllm_model *M, int steps) {
     return kFlowFellBack;
   }
   return hip_fail(e, "hipLaunchCooperativeKernel(k_flow)", __FILE__, __LINE__);
+}
+
+// One verify step of m tokens at positions pos0 .. pos0+m-1 in the
+// persistent kernel (k_flowm), launched as mode 3 (cooperative) or mode 4
+// launches k_flow.  Only the attention splits that the pass reaches get
+// items, and the stages' token groups are as small as the grid allows (every
+// item of a layer on its own workgroup).
+int launch_flowm(mllm_model *M, int m, int pos0) {
+  FlowGeom F = M->flow;
+  F.ep0 = M->flow_epoch + 1;
+  F.steps = 1;
+  F.m = m;
+  F.na = M->P.NH * ((pos0 + m - 1) / ACH + 1);
+  const int nrh = M->P.NH + 2 * M->P.NKV;
+  for (int tpi = 1; tpi <= m; ++tpi) {
+    F.ta = F.mt = tpi;
+    F.tq = std::min(tpi, VQT);
+    const auto groups = [m](int per) { return (m + per - 1) / per; };
+    const int ni = 2 * m + nrh * groups(F.tq) + F.na * groups(F.ta) + F.nm * groups(F.mt);
+    if (ni <= M->flow_grid) break;
+  }
+  const void *k = reinterpret_cast<const void *>(k_flowm);
+  if (M->exec_mode == 4) {
+    hipLaunchKernelGGL(k_flowm, dim3(M->flow_grid), dim3(FLT), M->flowm_lds, M->stream, M->P, F);
+    MLLM_HIP(hipGetLastError());
+  } else {
+    void *args[] = {&M->P, &F};
+    MLLM_HIP(hipLaunchCooperativeKernel(k, dim3(M->flow_grid), dim3(FLT), args, M->flowm_lds, M->stream));
+  }
+  M->flow_epoch += 1;
+  return 0;
 }
 
 // The phases of one pass in order: (phase, layer) pairs.
@@ -1986,7 +2621,9 @@ int run_pass(mllm_model *M, const int32_t *ids, int m, int pos0, int lm_rows) {
   for (int i = 0; i < m; ++i) s.tok[i] = ids[i];
   if (int rc = upload_state(M)) return rc;
   MLLM_HIP(hipEventRecord(M->ev0, M->stream));
-  int rc = M->exec_mode >= 3 && m == 1 && lm_rows == 1 ? launch_flow(M, 1) : kFlowFellBack;
+  int rc = kFlowFellBack;
+  if (M->exec_mode >= 3 && m == 1 && lm_rows == 1) rc = launch_flow(M, 1);
+  else if (M->exec_mode >= 3 && m <= M->flowm_max && lm_rows == 2) rc = launch_flowm(M, m, pos0);
   if (rc == kFlowFellBack) rc = enqueue_pass_phases(M, m, lm_rows != 0);
   if (rc) return rc;
   MLLM_HIP(hipEventRecord(M->ev1, M->stream));
@@ -2182,6 +2819,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   if (!rc) rc = dev_alloc(M, (void **)&P.opart, tagged_bytes[2]);
   if (!rc) rc = dev_alloc(M, (void **)&P.dpart, tagged_bytes[3]);
   if (!rc) rc = dev_alloc(M, (void **)&P.xn, sizeof(float) * MAXT * D);
+  if (!rc) rc = dev_alloc(M, (void **)&P.rec, sizeof(uint2) * 2 * MAXT * ngd * Q6R);
+  if (!rc) rc = dev_alloc(M, (void **)&P.qkvr, sizeof(uint2) * L * MAXT * (NH + 2 * NKV) * HD);
   if (!rc) rc = dev_alloc(M, (void **)&P.q, sizeof(float) * MAXT * NH * HD);
   if (!rc) rc = dev_alloc(M, &P.kv, kv_elems * (c.kv_fp16 ? 2 : 4));
   if (!rc) rc = dev_alloc(M, (void **)&P.attp, sizeof(float) * MAXT * NH * P.nsplit_max * APS);
@@ -2200,6 +2839,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       hipMemset(P.xa, 0, tagged_bytes[0]) != hipSuccess || hipMemset(P.xb, 0, tagged_bytes[1]) != hipSuccess ||
       hipMemset(P.opart, 0, tagged_bytes[2]) != hipSuccess || hipMemset(P.dpart, 0, tagged_bytes[3]) != hipSuccess ||
       hipMemset(P.cnt, 0, sizeof(unsigned) * MAXT * NH) != hipSuccess ||
+      hipMemset(P.rec, 0, sizeof(uint2) * 2 * MAXT * ngd * Q6R) != hipSuccess ||
+      hipMemset(P.qkvr, 0, sizeof(uint2) * L * MAXT * (NH + 2 * NKV) * HD) != hipSuccess ||
       hipMemset(P.kv, 0, kv_elems * (c.kv_fp16 ? 2 : 4)) != hipSuccess)
     return fail(set_error(MLLM_ERR_HIP, "memset"));
   P.logits = M->d_logits;
@@ -2300,6 +2941,21 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       M->flow_grid = G;
       M->exec_mode = 3;
       M->flow_default = true;
+      // the verify kernel: the most tokens whose LDS still lets the same grid
+      // be resident (one workgroup per CU)
+      const void *km = reinterpret_cast<const void *>(k_flowm);
+      for (int mm = std::min(MAXT, M->max_pass); mm >= 2; --mm) {
+        const size_t b = flowm_lds_bytes(P, F, mm);
+        int pc = 0;
+        if (b <= lds_cap &&
+            (b <= 64 * 1024 || hipFuncSetAttribute(km, hipFuncAttributeMaxDynamicSharedMemorySize, (int)b) ==
+                                   hipSuccess) &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, km, FLT, b) == hipSuccess && pc * M->num_cus >= G) {
+          M->flowm_max = mm;
+          M->flowm_lds = b;
+          break;
+        }
+      }
     }
     (void)hipGetLastError();
   }
@@ -2363,6 +3019,8 @@ extern "C" int mllm_set_exec_mode(mllm_model *M, int mode) {
 }
 
 extern "C" int mllm_get_exec_mode(const mllm_model *M) { return M ? M->exec_mode : -1; }
+
+extern "C" int mllm_flow_verify_tokens(const mllm_model *M) { return M && M->exec_mode >= 3 ? M->flowm_max : 0; }
 
 extern "C" int mllm_set_prefill(mllm_model *M, int min_tokens, int chunk_tokens) {
   MLLM_CHECK(M, "null model");

@@ -115,6 +115,11 @@ class PetitGPT:
         """The execution mode the next decode call uses (mllm_get_exec_mode)."""
         return int(abi.lib().mllm_get_exec_mode(self._h))
 
+    @property
+    def flowVerifyTokens(self) -> int:
+        """Most tokens a verify pass runs in the persistent kernel (0: phase kernels)."""
+        return int(abi.lib().mllm_flow_verify_tokens(self._h))
+
     def set_prefill(self, min_tokens: int, chunk_tokens: int = 0):
         """Prompts of at least min_tokens tokens take the batched path (0: never),
         in chunks of at most chunk_tokens (0: the largest)."""

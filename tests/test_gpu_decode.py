@@ -76,12 +76,18 @@ def test_exec_modes_bit_identical():
 
 
 @gpu
-@pytest.mark.parametrize("n", [2, 5, 9])
-def test_verify_rows_bit_identical_to_decode(n):
+@pytest.mark.parametrize("mode", [1, 3, 4])
+@pytest.mark.parametrize("n", [1, 2, 5, 9, 16])
+def test_verify_rows_bit_identical_to_decode(n, mode):
+    """A (k+1)-row verify pass -- one step of the persistent kernel in modes
+    3 and 4 (k_flowm), the phase kernels in mode 1 -- gives every row's
+    logits and argmax bit for bit as single-token decode at that position."""
     bundle = build("llama", seed=6)
-    g = mllm.PetitGPT(bundle)
+    g = mllm.PetitGPT(bundle, exec_mode=mode)
+    if mode >= 3:
+        assert g.flowVerifyTokens >= n
     prompt = [3, 1, 4, 1, 5, 9, 2, 6]
-    extra = [5, 3, 5, 8, 9, 7, 9, 3, 2][:n]
+    extra = [5, 3, 5, 8, 9, 7, 9, 3, 2, 3, 8, 4, 6, 2, 6, 4][:n]
     g.forwardPrompt(prompt)
     am, lg = g.forwardVerify(extra, want_logits=True)
     assert g.cacheLen == len(prompt) + n
@@ -295,3 +301,25 @@ def test_decode_precision_full_size_135m(oracle_lib):
     rel = max(float(np.abs(a - b).max()) / float(np.abs(b).max()) for a, b in rows)
     print(f"decode precision 135m: max-abs error / max|logit| = {rel:.2e}", flush=True)
     assert rel <= DECODE_TOL, rel
+
+
+@gpu
+@pytest.mark.parametrize("kv_fp16", [False, True])
+def test_verify_across_splits_bit_identical_to_decode(kv_fp16):
+    """Verify rows whose positions straddle a 256-position attention split
+    (250 .. 258) and reach past it, in the persistent kernel, against
+    single-token decode at each position."""
+    bundle = build("llama", seed=16, max_seq_len=512)
+    g = mllm.PetitGPT(bundle, kv_fp16=kv_fp16)
+    assert g.flowVerifyTokens >= 9
+    rng = np.random.default_rng(17)
+    prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 250)]
+    extra = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 9)]
+    g.forwardPrompt(prompt)
+    am, lg = g.forwardVerify(extra, want_logits=True)
+    g.forwardPrompt(prompt)
+    for i, t in enumerate(extra):
+        row = g.forwardDecode(t).copy()
+        assert np.array_equal(row.view(np.uint32), lg[i].view(np.uint32)), i
+        assert am[i] == g.last_argmax
+    g.destroy()
