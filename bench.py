@@ -429,6 +429,37 @@ def verify_pass_us(g, prompt, m, reps=20):
     return round(float(np.median(times)) * 1e3, 1)
 
 
+def batched_pass_us(g, prompt, m, reps=20):
+    """GPU time of the batched prompt path (int8 matrix-core GEMMs) over the
+    same m rows, as a prompt at position 0 (its lm_head forms the last row
+    only): the matrix-core alternative to a verify pass of m rows.  Prompts
+    of two tokens or more take that path by default."""
+    times = []
+    for _ in range(reps):
+        g.forwardPrompt(prompt[100:100 + m])
+        times.append(g.last_timing()[0])
+    return round(float(np.median(times)) * 1e3, 1)
+
+
+def bench_verify(mllm, pgw, args):
+    """Config 3's verify passes alone (for kernel traces): M = 1, 5, 9 rows with
+    forced drafts after a 512-token prompt, and the batched matrix-core path
+    over the same rows."""
+    cfg = pgw.CONFIGS["smollm2-135m"]
+    g = mllm.PetitGPT(pgw.parse_pgw(pgw.make_llama(cfg, seed=0)), exec_mode=args.exec_mode)
+    prompt = spans_prompt(np.random.default_rng(3), cfg.vocab_size, 512)
+    out = {"workload": "smollm2-135m q4: verify passes of M rows after a 512-token prompt (forced drafts)",
+           "exec_mode": g.execMode, "flow_verify_tokens": g.flowVerifyTokens}
+    out["verify_pass_us"] = {}
+    for m in (1, 5, 9):
+        out["verify_pass_us"][f"m{m}"] = verify_pass_us(g, prompt, m)
+        log(f"[bench] verify M = {m}: {out['verify_pass_us'][f'm{m}']} us")
+    out["batched_prompt_us"] = {f"m{m}": batched_pass_us(g, prompt, m) for m in (5, 9)}
+    log(f"[bench] batched path: {out['batched_prompt_us']}")
+    g.destroy()
+    return out
+
+
 def bench_configs(mllm, pgw, args, oracle=None):
     res = {}
     cpu_s = 0.0 if oracle is None else max(3.0, args.cpu_seconds / 3)
@@ -529,6 +560,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
     ap.add_argument("--prefill-only", action="store_true", help="config 5's prompt, batched, three times")
+    ap.add_argument("--verify-only", action="store_true",
+                    help="only config 3's verify passes at M = 1, 5, 9 (and the batched path at M = 5, 9)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (counter calibration for the traffic figure)")
     args = ap.parse_args()
@@ -552,6 +585,9 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration(torch)
+        return
+    if args.verify_only:
+        print(json.dumps(bench_verify(mllm, pgw, args)))
         return
     if args.prefill_only:
         cfg = pgw.CONFIGS["smollm2-360m"]
