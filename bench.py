@@ -560,6 +560,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
     ap.add_argument("--prefill-only", action="store_true", help="config 5's prompt, batched, three times")
+    ap.add_argument("--sweep-only", action="store_true",
+                    help="only the Q4 / Q8 GEMV sweep (config 2), no decode and no cooperative launch")
     ap.add_argument("--verify-only", action="store_true",
                     help="only config 3's verify passes at M = 1, 5, 9 (and the batched path at M = 5, 9)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -585,6 +587,9 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration(torch)
+        return
+    if args.sweep_only:
+        print(json.dumps({"gemv_sweep": bench_gemv(torch, abi, pgw)}))
         return
     if args.verify_only:
         print(json.dumps(bench_verify(mllm, pgw, args)))

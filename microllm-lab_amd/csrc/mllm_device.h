@@ -17,8 +17,6 @@
 namespace mllm {
 
 constexpr int WG = 256;          // threads per workgroup
-constexpr int XS = 36;           // LDS floats per staged 32-float group
-constexpr int SUB_CH = WG * 4;   // chunks per sub-tile of the Q8 GEMV
 
 // The thread index as a value the compiler cannot move.  Inside the
 // persistent decode kernel's loops it would otherwise hoist every
@@ -38,24 +36,6 @@ struct Q4Mat {
   const float *s;  // one scale per chunk
   int rows, cols;  // cols % 32 == 0
 };
-
-__device__ __forceinline__ float ubyte(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xFFu); }
-
-// 16 signed 8-bit weights against 16 floats: sum((u - 128) * x) with
-// u = q ^ 0x80 converted by v_cvt_f32_ubyte; the -128 is folded by the caller.
-__device__ __forceinline__ float q8_chunk_dot(const uint4 w, const float *__restrict__ xg) {
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-  const uint32_t dw[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u, w.w ^ 0x80808080u};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float4 xa = *reinterpret_cast<const float4 *>(xg + 4 * j);
-    a0 = __builtin_fmaf(ubyte(dw[j], 0), xa.x, a0);
-    a1 = __builtin_fmaf(ubyte(dw[j], 1), xa.y, a1);
-    a2 = __builtin_fmaf(ubyte(dw[j], 2), xa.z, a2);
-    a3 = __builtin_fmaf(ubyte(dw[j], 3), xa.w, a3);
-  }
-  return (a0 + a1) + (a2 + a3);
-}
 
 // ---------------------------------------------------------------- coherent access
 // Values one workgroup hands to another (activations, partial sums, the KV
@@ -370,52 +350,6 @@ __device__ __forceinline__ void wave_argmax(float &v, int &i) {
   }
   v = bv;
   i = bi;
-}
-
-// Copy m rows x[t*ldx + i] (i < n, n % 32 == 0, 16-byte aligned rows) into
-// the skewed layout.  Loads go out in batches of 4 float4 per thread before
-// any LDS store, so a batch costs one memory latency, not one per element.
-// stage_rows_load / stage_rows_store split one batch (float4 index base +
-// tid + k*NT) so a caller can issue it ahead of other loads; stage_rows
-// then copies the batches from `from` on.
-// Loads here are branch-free: an out-of-range lane reads a valid element
-// (its index clamped) and the value is ignored where it is used.  A load
-// inside a divergent branch makes the compiler wait for it at the join,
-// which would serialise loads meant to be in flight together.
-template <int NT = WG>
-__device__ __forceinline__ void stage_rows_load(const float *__restrict__ x, int ldx, int m, int n, int base,
-                                                float4 (&v)[4]) {
-  const int nq = n >> 2, total = m * nq;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int f = min(base + (int)tid() + k * NT, total - 1);
-    const int t = f / nq, q = f - t * nq;
-    v[k] = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + 4 * q);
-  }
-}
-
-template <int NT = WG>
-__device__ __forceinline__ void stage_rows_store(int m, int n, int base, const float4 (&v)[4], float *xs) {
-  const int nq = n >> 2, total = m * nq, ng = n >> 5;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int f = base + tid() + k * NT;
-    if (f < total) {
-      const int t = f / nq, i = 4 * (f - t * nq);
-      *reinterpret_cast<float4 *>(xs + (t * ng + (i >> 5)) * XS + (i & 31)) = v[k];
-    }
-  }
-}
-
-template <int NT = WG>
-__device__ __forceinline__ void stage_rows(const float *__restrict__ x, int ldx, int m, int n, float *xs,
-                                           int from = 0) {
-  const int nq = n >> 2, total = m * nq;
-  for (int base = from; base < total; base += 4 * NT) {
-    float4 v[4];
-    stage_rows_load<NT>(x, ldx, m, n, base, v);
-    stage_rows_store<NT>(m, n, base, v, xs);
-  }
 }
 
 // Sum of a row's n group partials in a fixed order: eight interleaved

@@ -255,49 +255,133 @@ __global__ __launch_bounds__(WGT) void k_gemv_q4_argmax(const uint8_t *__restric
   }
 }
 
-// ---------------------------------------------------------------- Q8 GEMV
-// 16-byte chunk = 16 int8 weights.  per_row: one scale per row applied to the
-// row sum (kernels.rs:41-57); otherwise one scale per 32 (two chunks).
-__global__ __launch_bounds__(WG) void k_gemv_q8(const uint4 *__restrict__ q, const float *__restrict__ scale,
-                                                 const float *__restrict__ x, float *__restrict__ y, int rows, int cols,
-                                                 int per_row, int rows_per_tile, int ntiles) {
-  extern __shared__ float4 smem4[];
-  float *smem = reinterpret_cast<float *>(smem4);
-  const int ng = cols >> 5, nc = cols >> 4;  // groups of 32, chunks of 16
-  float *xs = smem;
-  float *xsum16 = xs + ng * XS;
-  float *part = xsum16 + nc;
-  stage_rows(x, cols, 1, cols, xs);
-  __syncthreads();
-  for (int c = threadIdx.x; c < nc; c += WG) {
-    const float *p = xs + (c >> 1) * XS + (c & 1) * 16;
-    float s = 0.f;
+// ---------------------------------------------------------------- Q8 GEMV (integer dots)
+// The activations as 24-bit integers per 32-element group, xi = rint(x *
+// Q3MAX / amax) with sx = amax / Q3MAX (the rounding of the Q4 path's Q6
+// records, |xi| <= Q3MAX), split into three signed bytes, xi = 65536 h +
+// 256 m + l (l, m the low bytes sign-extended; |xi| <= Q3MAX keeps h in
+// [-128, 127]).  A group's record (Q6R dwords, as a Q6 record) holds the h,
+// m and l planes at dwords 0-7, 8-15 and 16-23 (byte e of the plane is
+// element e, the weights' byte order) and sx at dword 24.  One v_dot4 per
+// 4 weights and plane, exact in int32 (a plane's sum is at most 32 * 127 *
+// 128 in magnitude); the planes combine exactly in 64 bits (the group's dot
+// reaches 32 * 127 * Q3MAX, past int32), converted to float once.  The
+// group adds ((float)dot * sx) * w_scale to its row (g32), or the row sum is
+// multiplied by the row's scale (kernels.rs:41-57).
+constexpr float Q3MAX = 8355000.0f;
+
+// A row staged by one thread per float4 column q (as q6_stage_col).
+__device__ __forceinline__ void q3_stage_col(float4 y, bool in, int q, uint32_t *rec0) {
+  if (!in) y = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float a = max8(fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+  const float inv = a > 0.f ? Q3MAX * __builtin_amdgcn_rcpf(a) : 0.f;
+  const float v[4] = {y.x, y.y, y.z, y.w};
+  uint32_t ph = 0, pm = 0, pl = 0;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) s += p[k];
-    xsum16[c] = s;
+  for (int e = 0; e < 4; ++e) {
+    const int xi = (int)__builtin_rintf(v[e] * inv);
+    const int l = (int)(int8_t)(xi & 0xFF);
+    const int r1 = (xi - l) >> 8;
+    const int m = (int)(int8_t)(r1 & 0xFF);
+    const int h = (r1 - m) >> 8;
+    ph |= (uint32_t)(h & 0xFF) << (8 * e);
+    pm |= (uint32_t)(m & 0xFF) << (8 * e);
+    pl |= (uint32_t)(l & 0xFF) << (8 * e);
+  }
+  if (!in) return;
+  uint32_t *rec = rec0 + (q >> 3) * Q6R;
+  const int j = q & 7;  // elements 4j .. 4j+3 of the group: dword j of each plane
+  rec[j] = ph;
+  rec[8 + j] = pm;
+  rec[16 + j] = pl;
+  if (j == 0) rec[24] = __float_as_uint(a * (1.0f / Q3MAX));
+}
+
+// One group (32 int8 weights in wa, wb) against a Q3 record in registers.
+__device__ __forceinline__ float q8_dot3(const uint4 wa, const uint4 wb, const Q6Rec &r, float ws) {
+  const int wd[8] = {(int)wa.x, (int)wa.y, (int)wa.z, (int)wa.w, (int)wb.x, (int)wb.y, (int)wb.z, (int)wb.w};
+  int H = 0, M = 0, L = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    H = __builtin_amdgcn_sdot4(wd[j], (int)r.d[j], H, false);
+    M = __builtin_amdgcn_sdot4(wd[j], (int)r.d[8 + j], M, false);
+    L = __builtin_amdgcn_sdot4(wd[j], (int)r.d[16 + j], L, false);
+  }
+  const long long dot = (long long)H * 65536 + (long long)M * 256 + (long long)L;
+  return ((float)dot * r.sx) * ws;
+}
+
+// One tile of y = W x (one token) for Q8 weights: q4_gemv_tile's layout and
+// row-sum order with 32-byte chunks.
+template <int WGT, int P, bool PERROW>
+__device__ __forceinline__ void q8_gemv_tile(const int8_t *__restrict__ q, const float *__restrict__ scale,
+                                             const float *__restrict__ x, float *__restrict__ y, const GemvGeom &G,
+                                             int tile, uint32_t *lds) {
+  const int ng = G.cols >> 5, nq = G.cols >> 2, nx = nq;
+  const int ngp = 4 * ((ng + 3) >> 2), RT = G.rpp * P;
+  uint32_t *rec = lds;                                    // [ng][Q6R]
+  float *part = reinterpret_cast<float *>(lds + ng * Q6R);  // [RT][ngp]
+  const int t = threadIdx.x;
+  const int rr0 = t / ng;
+  const bool act = rr0 < G.rpp;
+  const int rr = act ? rr0 : 0, g = act ? t - rr0 * ng : 0;
+  const int row0 = tile * RT;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  float4 xv[GX_BATCH];
+#pragma unroll
+  for (int i = 0; i < GX_BATCH; ++i) {
+    const int qq = t + i * WGT;
+    xv[i] = x4[qq < nx ? qq : 0];
+  }
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(q), (short)0, 0x7fffffff,
+                                                                      0x00020000);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(scale), (short)0,
+                                                                      0x7fffffff, 0x00020000);
+  uint4 wa[P], wb[P];
+  float s[P];
+  const int last = G.rows - 1;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int row = min(row0 + p * G.rpp + rr, last);
+    const uint32_t c = (uint32_t)(row * ng + g);
+    wa[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(c * 32), 0, 0));
+    wb[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(c * 32 + 16), 0, 0));
+    s[p] = PERROW ? 1.f : __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(c * 4), 0, 0));
+  }
+#pragma unroll
+  for (int i = 0; i < GX_BATCH; ++i)
+    if (i * WGT < nx) q3_stage_col(xv[i], t + i * WGT < nx, t + i * WGT, rec);
+  for (int base = GX_BATCH * WGT; base < nx; base += WGT) {
+    const int qq = base + t;
+    q3_stage_col(x4[qq < nx ? qq : 0], qq < nx, qq, rec);
   }
   __syncthreads();
-  const int tid = threadIdx.x;
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int row0 = tile * rows_per_tile;
-    const int nr = min(rows_per_tile, rows - row0);
-    const int nch = nr * nc;
-    const size_t cbase = (size_t)row0 * nc;
-    for (int c = tid; c < nch; c += WG) {
-      const uint4 w = q[cbase + c];
-      const int cc = c % nc;
-      const float d = q8_chunk_dot(w, xs + (cc >> 1) * XS + (cc & 1) * 16) - 128.f * xsum16[cc];
-      part[c] = per_row ? d : d * scale[(cbase + c) >> 1];
-    }
-    __syncthreads();
-    for (int r = tid; r < nr; r += WG) {
-      const float *p = part + r * nc;
-      float acc = 0.f;
-      for (int k = 0; k < nc; ++k) acc += p[k];
-      y[row0 + r] = per_row ? acc * scale[row0 + r] : acc;
-    }
-    __syncthreads();
+  if (act) {
+    const Q6Rec xr = q6_load(rec + g * Q6R);
+    float *pp = part + rr * ngp + g;
+#pragma unroll
+    for (int p = 0; p < P; ++p) pp[p * G.rpp * ngp] = q8_dot3(wa[p], wb[p], xr, s[p]);
   }
+  __syncthreads();
+  // row sums: q4_gemv_tile's order
+  const int nr = min(RT, G.rows - row0);
+  for (int i = t; i < RT * G.lpr; i += WGT) {
+    const int r = i / G.lpr, l = i - r * G.lpr;
+    float a = 0.f;
+    for (int gi = 4 * l; gi < ng; gi += 4 * G.lpr) {
+      const float4 v = *reinterpret_cast<const float4 *>(part + r * ngp + gi);
+      a += ((v.x + (gi + 1 < ng ? v.y : 0.f)) + ((gi + 2 < ng ? v.z : 0.f) + (gi + 3 < ng ? v.w : 0.f)));
+    }
+    a = seg_sum(a, G.lpr);
+    if (l == 0 && r < nr) y[row0 + r] = PERROW ? a * scale[row0 + r] : a;
+  }
+}
+
+template <int WGT, int P, bool PERROW>
+__global__ __launch_bounds__(WGT) void k_gemv_q8i(const int8_t *__restrict__ q, const float *__restrict__ scale,
+                                                  const float *__restrict__ x, float *__restrict__ y, GemvGeom G) {
+  extern __shared__ float4 smem4[];
+  q8_gemv_tile<WGT, P, PERROW>(q, scale, x, y, G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4));
 }
 
 // ---------------------------------------------------------------- f32 GEMV
@@ -649,22 +733,36 @@ extern "C" int mllm_gemv_q4_argmax_noalloc(int m, int n, const uint8_t *packed, 
   return gemv_q4_argmax_run(a, m, n, packed, scale, x, y, argmax, sp, as_stream(stream));
 }
 
+template <int WGT, int P>
+int q8_launch(dim3 grid, size_t lds, hipStream_t st, const int8_t *q, const float *scale, const float *x, float *y,
+              const GemvGeom &G, int per_row) {
+  if (per_row) {
+    if (int rc = launch_dyn(k_gemv_q8i<WGT, P, true>, grid, lds, st, "k_gemv_q8i")) return rc;
+    hipLaunchKernelGGL((k_gemv_q8i<WGT, P, true>), grid, dim3(WGT), lds, st, q, scale, x, y, G);
+  } else {
+    if (int rc = launch_dyn(k_gemv_q8i<WGT, P, false>, grid, lds, st, "k_gemv_q8i")) return rc;
+    hipLaunchKernelGGL((k_gemv_q8i<WGT, P, false>), grid, dim3(WGT), lds, st, q, scale, x, y, G);
+  }
+  MLLM_HIP(hipGetLastError());
+  return 0;
+}
+
+// The Q8 GEMVs on integer dots, with the Q4 path's tile plan (the chunk of a
+// (row, group) is 32 bytes instead of 16).
 static int q8_common(int m, int n, const int8_t *q, const float *scale, const float *x, float *y, int per_row,
                      hipStream_t st) {
   MLLM_CHECK(m > 0 && n > 0 && n % 32 == 0, "invalid shape m=%d n=%d (n %% 32 == 0 required)", m, n);
   if (n > kMaxCols) return set_error(MLLM_ERR_UNSUPPORTED, "n=%d exceeds %d", n, kMaxCols);
   MLLM_CHECK(q && scale && x && y, "null pointer");
   MLLM_CHECK((((uintptr_t)q | (uintptr_t)x) & 15) == 0, "q and x must be 16-byte aligned");
-  const int nc = n / 16, ng = n / 32;
-  const int rpt = SUB_CH / nc > 0 ? SUB_CH / nc : 1;
-  const int ntiles = (m + rpt - 1) / rpt;
-  const int grid = ntiles < device_wg_cap() ? ntiles : device_wg_cap();
-  const size_t lds = sizeof(float) * ((size_t)ng * XS + nc + (size_t)rpt * nc);
-  if (int rc = launch_dyn(k_gemv_q8, grid, lds, st, "k_gemv_q8")) return rc;
-  hipLaunchKernelGGL(k_gemv_q8, dim3(grid), dim3(WG), lds, st, reinterpret_cast<const uint4 *>(q), scale, x, y, m, n,
-                     per_row, rpt, ntiles);
-  MLLM_HIP(hipGetLastError());
-  return 0;
+  MLLM_CHECK((size_t)m * n < (1ull << 31), "matrix of %zu bytes exceeds 2 GiB", (size_t)m * n);
+  const int ng = n / 32;
+  const Q4Plan pl = q4_plan(n, m, 1);
+  const int P = q4_pick_p(m, pl.rpp, 1);
+  const int ntiles = (m + pl.rpp * P - 1) / (pl.rpp * P);
+  const GemvGeom G{m, n, 1, pl.rpp, pl.lpr, m};
+  return MLLM_Q4_DISPATCH(q8_launch, pl.wgt, P, dim3(ntiles), q4_lds_bytes(pl, ng, 1, P), st, q, scale, x, y, G,
+                          per_row);
 }
 
 extern "C" int mllm_gemv_q8(int m, int n, const int8_t *q, const float *scale, const float *x, float *y,
