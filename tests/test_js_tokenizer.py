@@ -1,0 +1,121 @@
+"""The Node host's tokenizer (microllm-lab_amd/js/tokenizer.mjs) against the
+Python tokenizer (mllm/tokenizer.py), which test_tokenizer.py pins to the
+HuggingFace `tokenizers` library on the reference's tokenizer files.
+
+The same texts (fixed, seeded random Unicode, long and surrogate-cut
+strings), id lists and conversations go through both; encode ids, decoded
+text and template ids must be equal.  The models' tokenizer files are read
+from the reference checkout when present; hand-made tokenizers cover the
+merge order, specials and templates without it."""
+import json
+import os
+import random
+import shutil
+import subprocess
+
+import pytest
+
+from mllm import tokenizer as T
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CLI = os.path.join(ROOT, "microllm-lab_amd", "js", "tokenize_cli.mjs")
+NODE = shutil.which("node")
+pytestmark = pytest.mark.skipif(NODE is None, reason="node not installed")
+REF_MODELS = "/root/reference/models"
+MODELS = ["gpt2", "l20-edu-135m", "minimind2", "smollm2-135m-instruct", "petitgpt"]
+
+TEXTS = [
+    "Hello! How can I help you today?",
+    "  leading spaces and   runs\n\n\tof whitespace  ",
+    "def add(a, b):\n    return a + b  # 42\n",
+    "ünïcödé café naïve — “quotes” ‘single’ … ½ ² ℃",
+    "日本語のテキストと中文混合 한국어",
+    "emoji 😀🎉👍🏽 family 👨‍👩‍👧 flags 🇫🇷",
+    "<|im_start|>user\nhi<|im_end|>\n<|im_start|>assistant\n",
+    "<|endoftext|>after<|endoftext|><|endoftext|>",
+    "don't won't I'm you're they've we'll he'd 'S 'LL",
+    "tabs\tand\rcarriage\x0breturns\x0cff \x85 \x1c ﻿﻿",
+    "  nbsp  emspace 　ideo  ls",
+    "x",
+    "",
+]
+
+
+def random_texts(seed, n=40):
+    rng = random.Random(seed)
+    pools = [range(0x20, 0x7F), range(0xA0, 0x250), range(0x400, 0x4FF), range(0x4E00, 0x4F00),
+             range(0x3040, 0x30FF), [0x20, 0x20, 0x0A, 0x09], range(0x1F600, 0x1F650)]
+    return ["".join(chr(rng.choice(rng.choice(pools))) for _ in range(rng.randint(1, 60))) for _ in range(n)]
+
+
+def run_js(tmp_path, cases):
+    f = tmp_path / "cases.json"
+    f.write_text(json.dumps(cases, ensure_ascii=False), encoding="utf-8")
+    r = subprocess.run([NODE, CLI, str(f)], capture_output=True, text=True, encoding="utf-8", timeout=300)
+    assert r.returncode == 0, r.stderr
+    # one line: split on "\n" only (decoded text may hold U+2028, U+0085 and
+    # U+001C, at which str.splitlines would also split)
+    return json.loads(r.stdout.rstrip("\n").split("\n")[-1])
+
+
+def py_messages(tok, msgs, card):
+    try:
+        return T.encode_messages(tok, msgs, card)
+    except ValueError as e:
+        return {"error": str(e)}
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_js_tokenizer_equals_python_on_the_reference_models(tmp_path, name):
+    path = os.path.join(REF_MODELS, name, "tokenizer.json")
+    if not os.path.exists(path):
+        pytest.skip("the reference's tokenizer files are not present")
+    tok = T.load_tokenizer(path)
+    texts = TEXTS + random_texts(hash(name) & 0xFFFF)
+    ids = [tok.encode(t) for t in texts]
+    # past 32768 UTF-16 units: the cut lands on the low half of a surrogate
+    # pair (42000 - 32768 = 9232 = 4 mod 6), and at a character boundary
+    cut = ["ab \U0001F600 " * 7000, ("x1 yz " * 7000)[:40000]]
+    cases = {"tokenizer": path, "encode": texts + cut, "decode": ids + [[10 ** 9], ids[3][:1]],
+             "decodeSkip": ids[6:8]}
+    out = run_js(tmp_path, cases)
+    assert out["encode"][:len(texts)] == ids
+    assert out["encode"][len(texts):] == [tok.encode(t) for t in cut]
+    assert out["decode"] == [tok.decode(i) for i in cases["decode"]]
+    assert out["decodeSkip"] == [tok.decode(i, skip_special=True) for i in cases["decodeSkip"]]
+
+
+def toy_spec(merges, extra_vocab=(), added=()):
+    vocab = {}
+    for sym in [T.BYTE_TO_CHAR[b] for b in range(256)] + list(extra_vocab):
+        vocab.setdefault(sym, len(vocab))
+    return {"model": {"type": "BPE", "vocab": vocab, "merges": merges},
+            "added_tokens": [dict(content=c, id=i, special=s) for c, i, s in added]}
+
+
+def test_js_tokenizer_merges_specials_and_templates(tmp_path):
+    spec = toy_spec(["a a", "b c", "a b", "a a"], ["aa", "bc", "ab", "aaa"],
+                    [("<s>", 900, True), ("<s><s>", 901, True), ("<x>", 902, False),
+                     ("<|im_start|>", 500, True), ("<|im_end|>", 501, True)])
+    tok = T.load_tokenizer(spec)
+    texts = ["aaa", "abc", "aab", "aaaa", "<s><s>a<s>", "<x>", "ab<|im_start|>c", "zzz"]
+    convs = [
+        ([{"role": "User", "content": "hi"}], {"template": "chatml", "defaultSystem": "sys"}),
+        ([{"role": "user", "content": "q"}], {"template": "completion"}),
+        ([{"role": "user", "content": "a"}, {"role": "assistant", "content": "b"}, {"role": "user", "content": "c"}],
+         {"template": "petitgpt"}),
+        ([{"role": "user", "content": "a"}, {"role": "assistant", "content": "b"}], {"template": "petitgpt"}),
+        ([{"role": "tool", "content": "x"}], {"template": "petitgpt"}),
+        ([{"role": "user", "content": ""}], {"template": "petitgpt"}),
+        ([{"role": "system", "content": "s"}, {"role": "user", "content": "u"}],
+         {"template": "petitgpt", "bosId": 7, "eosId": 8, "specials": {"<|user|>": 11, "<|assistant|>": 12}}),
+    ]
+    out = run_js(tmp_path, {"tokenizer": spec, "encode": texts,
+                            "messages": [{"messages": m, "card": c} for m, c in convs]})
+    assert out["encode"] == [tok.encode(t) for t in texts]
+    for got, (m, c) in zip(out["messages"], convs):
+        want = py_messages(tok, m, c)
+        if isinstance(want, dict):
+            assert isinstance(got, dict) and got["error"] == want["error"]
+        else:
+            assert got == want
