@@ -320,6 +320,27 @@ def cpu_gemv_q4(oracle, pgw, m, n, budget_s=1.0):
     return {"us": round(us, 1), "gbs": round((m * n // 2 + m * n // 8 + 4 * n + 4 * m) / us / 1e3, 2), "reps": reps}
 
 
+def graph_us(torch, enqueue, n_launch, replays=5):
+    """Microseconds per launch of n_launch launches captured in one graph
+    (enqueue(stream_handle) issues them), replayed `replays` times; the
+    launches allocate nothing and clear nothing, so they capture as is."""
+    cs = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cs):
+        enqueue(C.c_void_p(cs.cuda_stream))
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (replays * n_launch)
+    del g
+    return round(us, 3)
+
+
 def bench_gemv(torch, abi, pgw, oracle=None):
     shapes = [(960, 960), (320, 960), (2560, 960), (960, 2560), (49152, 960)]
     stream = torch.cuda.current_stream()
@@ -337,13 +358,13 @@ def bench_gemv(torch, abi, pgw, oracle=None):
             x = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).cuda()
             y = torch.empty(m, dtype=torch.float32, device="cuda")
 
-            def launch(i):
+            def launch(i, s=sp):
                 if fmt == "q4":
                     rc = abi.lib().mllm_gemv_q4(m, n, W[i].data_ptr(), S[i].data_ptr(), 32, x.data_ptr(),
-                                                y.data_ptr(), sp)
+                                                y.data_ptr(), s)
                 else:
                     rc = abi.lib().mllm_gemv_q8_g32(m, n, W[i].data_ptr(), S[i].data_ptr(), x.data_ptr(),
-                                                    y.data_ptr(), sp)
+                                                    y.data_ptr(), s)
                 abi.check("gemv", rc)
 
             res = {"fmt": fmt, "shape": [m, n], "bytes": algo}
@@ -360,6 +381,10 @@ def bench_gemv(torch, abi, pgw, oracle=None):
                 us = e0.elapsed_time(e1) * 1e3 / reps
                 res[f"{mode}_us"] = round(us, 3)
                 res[f"{mode}_gbs"] = round(algo / us / 1e3, 1)
+            # the cold launches again, replayed from a captured graph: kernel
+            # time without the host's per-call cost (ctypes, launch)
+            res["cold_graph_us"] = graph_us(torch, lambda s: [launch(i % copies, s) for i in range(reps)], reps)
+            res["cold_graph_gbs"] = round(algo / res["cold_graph_us"] / 1e3, 1)
             if fmt == "q4":
                 # layer-stacked: 32 distinct matrices per launch
                 cnt = 32
@@ -389,6 +414,14 @@ def bench_gemv(torch, abi, pgw, oracle=None):
                 us = e0.elapsed_time(e1) * 1e3 / reps
                 res["stacked32_us"] = round(us, 3)
                 res["stacked32_gbs"] = round(cnt * algo / us / 1e3, 1)
+
+                def stacked(s):
+                    for i in range(reps):
+                        tp, ts, tx, ty, _ = tabs[i % len(tabs)]
+                        abi.check("batched", abi.lib().mllm_gemv_q4_batched(cnt, m, n, tp.data_ptr(), ts.data_ptr(),
+                                                                            tx.data_ptr(), ty.data_ptr(), s))
+                res["stacked32_graph_us"] = graph_us(torch, stacked, reps)
+                res["stacked32_graph_gbs"] = round(cnt * algo / res["stacked32_graph_us"] / 1e3, 1)
                 del tabs
             res["cold_frac_hbm"] = round(res["cold_gbs"] / HBM_PEAK_GBS, 4)
             if fmt == "q4" and oracle is not None:

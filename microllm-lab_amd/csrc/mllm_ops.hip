@@ -481,7 +481,7 @@ long q4_target() { return (long)MLLM_Q4_WG_PER_CU * (device_wg_cap() / 8); }
 // up to 256 groups per row; 512 above that, and also for long rows (>= 64
 // groups) where even one-pass tiles of 256 threads leave the launch below its
 // workgroup target: every workgroup stages all of x, and twice the rows
-// share that staging (960 x 2560: 4.4 instead of 4.7 us of kernel time; at
+// share that staging (960 x 2560 cold: 4.24 instead of 4.72 us of kernel time; at
 // 960 columns the 256-thread tiles stay faster).  The per-row arithmetic and
 // its summation order do not depend on the workgroup size.
 Q4Plan q4_plan(int cols, int rows, int count) {
