@@ -484,7 +484,7 @@ def bench_verify(mllm, pgw, args):
     out = {"workload": "smollm2-135m q4: verify passes of M rows after a 512-token prompt (forced drafts)",
            "exec_mode": g.execMode, "flow_verify_tokens": g.flowVerifyTokens}
     out["verify_pass_us"] = {}
-    for m in (1, 5, 9):
+    for m in (1, 2, 3, 4, 5, 9):
         out["verify_pass_us"][f"m{m}"] = verify_pass_us(g, prompt, m)
         log(f"[bench] verify M = {m}: {out['verify_pass_us'][f'm{m}']} us")
     out["batched_prompt_us"] = {f"m{m}": batched_pass_us(g, prompt, m) for m in (5, 9)}

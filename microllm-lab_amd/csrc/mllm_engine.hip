@@ -1500,6 +1500,7 @@ struct FlowGeom {
   int ep0, steps;         // epoch of the launch's first step; chained steps
   int m;                  // tokens of a verify step (k_flowm; the decode kernel takes 1)
   int tq, ta, mt;         // k_flowm: tokens per QKV, attention and MLP item (the items of a stage are x token group)
+  int fuse;               // k_flowm: no norm items; the QKV, MLP and lm_head items form their tokens' norms
   int na, nm, ni;         // items per layer: attention (split, head) items, MLP chunks; ni = na + nm
   int lm_rpt, lm_tiles;   // lm_head tiles of the 1024-thread role (one per workgroup w < lm_tiles, then w + G ...)
 };
@@ -1758,20 +1759,26 @@ __device__ __forceinline__ uint2 *rec_row(const DecParams &P, int side, int t) {
   return P.rec + ((size_t)side * MAXT + t) * (P.D >> 5) * Q6R;
 }
 
-// Norm item t.  side 0 at layer li < L: the attention norm (phase_attn1's
-// residual and norm); li == L: the final norm (final_row's), no residual row
-// written; side 1: the MLP norm (phase_mlp's).
-__device__ void flowm_norm(const DecParams &P, int li, int t, int side, const Step &st, float *smem) {
-  const int D = P.D, ng = D >> 5, nq = D >> 2;
+// Token t's residual and norm into the Q6 records at LDS qx.  side 0 at
+// layer li < L: the attention norm (phase_attn1's residual and norm); li ==
+// L: the final norm (final_row's); side 1: the MLP norm (phase_mlp's).  The
+// residual row (xa[t], side 0, or xb[t], side 1; none for the final norm) is
+// written when write_x.  scratch holds the gains, the block sums and the
+// reduction (norm_scratch floats).  Every thread calls it (it holds
+// barriers); the records are complete after the caller's next barrier.
+__host__ __device__ inline size_t norm_scratch(size_t D, size_t nbd) { return al4(3 * D) + nbd * D + 32; }
+__device__ __forceinline__ void resid_norm(const DecParams &P, int li, int t, int side, const Step &st, float *scratch,
+                                           uint32_t *qx,
+                           bool write_x) {
+  const int D = P.D, nq = D >> 2;
   const bool gpt2 = P.arch == 1, fin = li == P.L;
   const LayerW &Lw = P.layers[min(li, P.L - 1)];
   const float *gain = side ? Lw.n2 : fin ? P.norm_f : Lw.n1;
   const float *rbias = !gpt2 ? nullptr : side ? Lw.proj_b : li == 0 ? nullptr : fin ? P.last_mproj_b : Lw.prev_mproj_b;
   const int np = side ? P.NH : P.nchunk;
   const int want = st.tag + li - (side ? 0 : 1);  // the inputs' tag
-  float *gl = smem;
-  uint32_t *qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));  // ng Q6 records
-  float *blk = gl + al4(3 * D) + al4(ng * Q6R), *red = blk + ((np + PB - 1) / PB) * D;
+  float *gl = scratch;
+  float *blk = gl + al4(3 * D), *red = blk + ((np + PB - 1) / PB) * D;
   GainsReg GR;
   gains_load(P, gain, rbias, GR);
   gains_store(P, rbias, GR, gl);
@@ -1788,7 +1795,16 @@ __device__ void flowm_norm(const DecParams &P, int li, int t, int side, const St
     __syncthreads();
     x = col_finish(blk, nq, np, base, gl, D, rbias != nullptr);
   }
-  col_norm(P, x, gl, red, qx, ColOut{fin ? nullptr : (side ? P.xb : P.xa) + (size_t)t * D, st.tag + li});
+  uint2 *xo = write_x && !fin ? (side ? P.xb : P.xa) + (size_t)t * D : nullptr;
+  col_norm(P, x, gl, red, qx, ColOut{xo, st.tag + li});
+}
+
+// Norm item t (the five-stage step): resid_norm, then the records to
+// P.rec for the stage's consumers.
+__device__ void flowm_norm(const DecParams &P, int li, int t, int side, const Step &st, float *smem) {
+  const int ng = P.D >> 5;
+  uint32_t *qx = reinterpret_cast<uint32_t *>(smem);  // ng Q6 records
+  resid_norm(P, li, t, side, st, smem + al4(ng * Q6R), qx, true);
   __syncthreads();
   rec_put(rec_row(P, side, t), qx, ng * Q6R, st.tag + li);
 }
@@ -1801,7 +1817,7 @@ __device__ void flowm_norm(const DecParams &P, int li, int t, int side, const St
 // also to the cache.  nt <= VQT.
 constexpr int VQT = 8;  // tokens per QKV item at most (its LDS)
 __device__ void flowm_qkv(const DecParams &P, const LayerW &Lw, int li, int rh, int t0, int nt, const Step &st,
-                          float *smem) {
+                          bool fused, float *smem) {
   const int D = P.D, ng = D >> 5, nch = HD * ng;
   const int nrow = (P.NH + 2 * P.NKV) * HD;
   const bool gpt2 = P.arch == 1;
@@ -1822,7 +1838,13 @@ __device__ void flowm_qkv(const DecParams &P, const LayerW &Lw, int li, int rh, 
       rt[tt * 2 * HD + HD + d] = P.rope_sin[ri];
     }
   }
-  rec_get(P, rec_row(P, 0, t0), nt * ng * Q6R, st.tag + li, qx);
+  if (fused) {
+    // each token's residual and norm here (the row head 0 item writes xa)
+    float *scratch = rt + al4(nt * 2 * HD);
+    for (int tt = 0; tt < nt; ++tt) resid_norm(P, li, t0 + tt, 0, st, scratch, qx + tt * ng * Q6R, rh == 0);
+  } else {
+    rec_get(P, rec_row(P, 0, t0), nt * ng * Q6R, st.tag + li, qx);
+  }
   __syncthreads();
   tile_partials<QC>(R, ng, nch, nt, qx, part);
   __syncthreads();
@@ -2071,7 +2093,7 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
 // tokens [ta, ta + m) (phase_mlp's arithmetic), VMB tokens per batch, then
 // the units' slice of the down projection for each of them.
 __device__ void flowm_mlp(const DecParams &P, const LayerW &Lw, int li, int item, const Step &st, int ta, int m,
-                          float *smem) {
+                          bool fused, float *smem) {
   const int D = P.D, ng = D >> 5, nch = UNITS * ng, S = (MT / ng) * ng;
   const bool gpt2 = P.arch == 1;
   uint32_t *qx = reinterpret_cast<uint32_t *>(smem);                   // m x ng Q6 records
@@ -2082,7 +2104,13 @@ __device__ void flowm_mlp(const DecParams &P, const LayerW &Lw, int li, int item
   mlp_pre_up(P, Lw, item, M);
   slice_load<MC, MT>(Lw.w2, 2 * item, D, M.Rd);
   const int want = st.tag + li;
-  rec_get(P, rec_row(P, 1, ta), m * ng * Q6R, want, qx);
+  if (fused) {
+    // each token's residual and norm here (the unit block 0 item writes xb)
+    float *scratch = reinterpret_cast<float *>(hq + m * 2 * Q6R);
+    for (int tt = 0; tt < m; ++tt) resid_norm(P, li, ta + tt, 1, st, scratch, qx + tt * ng * Q6R, item == 0);
+  } else {
+    rec_get(P, rec_row(P, 1, ta), m * ng * Q6R, want, qx);
+  }
   __syncthreads();
   const int wv = wave_id(), lane = lane_id(), g = tid() % ng;
   for (int t0 = 0; t0 < m; t0 += VMB) {
@@ -2148,7 +2176,8 @@ __device__ void flowm_mlp(const DecParams &P, const LayerW &Lw, int li, int item
 // logits rows and tile maxima against the final norm's records, VLB tokens
 // per pass over a tile (no penalties: a verify pass is greedy).  Returns
 // true when this workgroup computed at least one tile.
-__device__ bool flowm_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, const Step &st, int m, float *smem) {
+__device__ bool flowm_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, const Step &st, int m, bool fused,
+                         float *smem) {
   if (wg >= L.ntiles) return false;
   const int ng = P.D >> 5;
   TileRegs<FTC> R;
@@ -2159,7 +2188,13 @@ __device__ bool flowm_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, c
   s.part = smem + al4(m * ng * Q6R);
   s.out = s.part + VLB * FTC * FLT;
   s.lists = nullptr;
-  rec_get(P, rec_row(P, 0, 0), m * ng * Q6R, st.tag + P.L, s.qx);
+  if (fused) {
+    // each token's final norm here
+    float *scratch = s.out + VLB * L.rpt;
+    for (int t = 0; t < m; ++t) resid_norm(P, P.L, t, 0, st, scratch, s.qx + t * ng * Q6R, false);
+  } else {
+    rec_get(P, rec_row(P, 0, 0), m * ng * Q6R, st.tag + P.L, s.qx);
+  }
   __syncthreads();
   for (;;) {
     for (int t0 = 0; t0 < m; t0 += VLB) {
@@ -2225,6 +2260,8 @@ __global__ __launch_bounds__(FLT) void k_flowm(DecParams P, FlowGeom F) {
   const Step st{st_ld(P, ST_OFF(pos0)), false, (int)((uint32_t)e * (uint32_t)TAGL)};
   const int nrh = P.NH + 2 * P.NKV;
   const int ngq = (m + F.tq - 1) / F.tq, nga = (m + F.ta - 1) / F.ta, ngm = (m + F.mt - 1) / F.mt;  // token groups
+  // norm items per stage; a fused step leaves them idle (its QKV, MLP and
+  // lm_head items form their tokens' norms)
   const int iq = m, ia = iq + nrh * ngq, inm = ia + F.na * nga, im = inm + m, ni = im + F.nm * ngm;
   for (int lv = 0; lv < P.L; ++lv) {
     int li = lv;
@@ -2236,24 +2273,24 @@ __global__ __launch_bounds__(FLT) void k_flowm(DecParams P, FlowGeom F) {
       asm volatile("" : "+s"(j));
       __syncthreads();  // the previous item's LDS is free
       if (j < iq) {
-        flowm_norm(P, li, j, 0, st, smem);
+        if (!F.fuse) flowm_norm(P, li, j, 0, st, smem);
       } else if (j < ia) {
         const int tg = (j - iq) / nrh, rh = (j - iq) - tg * nrh;
-        flowm_qkv(P, Lw, li, rh, tg * F.tq, min(F.tq, m - tg * F.tq), st, smem);
+        flowm_qkv(P, Lw, li, rh, tg * F.tq, min(F.tq, m - tg * F.tq), st, F.fuse, smem);
       } else if (j < inm) {
         const int tg = (j - ia) / F.na, it = (j - ia) - tg * F.na;
         flowm_attn(P, Lw, li, it, tg * F.ta, min(m, (tg + 1) * F.ta), st, m, smem);
       } else if (j < im) {
-        flowm_norm(P, li, j - inm, 1, st, smem);
+        if (!F.fuse) flowm_norm(P, li, j - inm, 1, st, smem);
       } else {
         const int tg = (j - im) / F.nm, it = (j - im) - tg * F.nm;
-        flowm_mlp(P, Lw, li, it, st, tg * F.mt, min(F.mt, m - tg * F.mt), smem);
+        flowm_mlp(P, Lw, li, it, st, tg * F.mt, min(F.mt, m - tg * F.mt), F.fuse, smem);
         // a hint for the lm_head's coarse waits (the records carry the tags that decide)
         if (tid() == 0) flag_st(fl + P.NH + it, e);
       }
     }
   }
-  if (w < m) {
+  if (!F.fuse && w < m) {
     __syncthreads();
     flowm_norm(P, P.L, w, 0, st, smem);  // the final norm of token w
   }
@@ -2263,7 +2300,7 @@ __global__ __launch_bounds__(FLT) void k_flowm(DecParams P, FlowGeom F) {
       C.wait<16>(F.flags + (P.L - 2) * stride + P.NH, F.nm);
     }
     __syncthreads();
-    if (flowm_lm(P, lg, w, G, st, m, smem)) {
+    if (flowm_lm(P, lg, w, G, st, m, F.fuse, smem)) {
       // the last lm_head workgroup to finish takes every row's argmax
       wait_stores();
       __syncthreads();
@@ -2322,6 +2359,7 @@ struct mllm_model {
   FlowGeom flow{};
   int flow_grid = 0;      // 0: not available on this device
   int flowm_max = 0;      // most tokens of a verify step in the persistent kernel (0: verify uses the phase kernels)
+  int verify_fuse = 9;    // verify steps of at most this many tokens run fused (MLLM_VERIFY_FUSE); faster at every M <= 9 measured
   size_t flowm_lds = 0;
   bool flow_default = false;  // mode 3 was chosen by default, not by mllm_set_exec_mode
   size_t flow_lds = 0;
@@ -2383,17 +2421,18 @@ size_t flow_lds_bytes(const DecParams &P, const FlowGeom &F) {
   return f * sizeof(float);
 }
 
-// The verify kernel for m tokens: the largest of its items' LDS (k_flowm).
+// The verify kernel for m tokens: the largest of its items' LDS (k_flowm),
+// with the norm scratch the fused step's QKV, MLP and lm_head items add.
 size_t flowm_lds_bytes(const DecParams &P, const FlowGeom &F, int m) {
   const size_t ngd = P.D / 32, D = P.D, mm = m, mq = std::min(m, VQT);
   const size_t nbd = (std::max(P.nchunk, P.NH) + PB - 1) / PB;
-  const size_t rec = al4(mm * ngd * Q6R);
+  const size_t rec = al4(mm * ngd * Q6R), ns = norm_scratch(D, nbd);
   size_t f = 2 * (FLT / 64);
-  f = std::max(f, al4(3 * D) + al4(ngd * Q6R) + nbd * D + 32);                       // norm items
-  f = std::max(f, al4(mq * ngd * Q6R) + mq * (HD * ngd + 3 * HD));                    // QKV items
-  f = std::max(f, mm * (3 * HD + AW * HD + 2 * AW + 2 * Q6R) + al4(mm));             // attention items
-  f = std::max(f, rec + VMB * (2 * UNITS * ngd + 2 * UNITS) + mm * 2 * Q6R);          // MLP items
-  f = std::max(f, rec + (size_t)VLB * FTC * FLT + (size_t)VLB * F.lm_rpt);            // lm_head share
+  f = std::max(f, al4(ngd * Q6R) + ns);                                                 // norm items
+  f = std::max(f, al4(mq * ngd * Q6R) + mq * (HD * ngd + HD) + al4(mq * 2 * HD) + ns);  // QKV items
+  f = std::max(f, mm * (3 * HD + AW * HD + 2 * AW + 2 * Q6R) + al4(mm));               // attention items
+  f = std::max(f, rec + VMB * (2 * UNITS * ngd + 2 * UNITS) + mm * 2 * Q6R + ns);       // MLP items
+  f = std::max(f, rec + (size_t)VLB * FTC * FLT + (size_t)VLB * F.lm_rpt + ns);         // lm_head share
   return f * sizeof(float);
 }
 
@@ -2527,12 +2566,16 @@ int launch_flowm(mllm_model *M, int m, int pos0) {
   F.m = m;
   F.na = M->P.NH * ((pos0 + m - 1) / ACH + 1);
   const int nrh = M->P.NH + 2 * M->P.NKV;
+  // up to verify_fuse tokens: three stages per layer, one token per item,
+  // every item forming its token's norm; past that, five stages with norm
+  // items and token groups as small as the grid allows
+  F.fuse = m <= M->verify_fuse;
   for (int tpi = 1; tpi <= m; ++tpi) {
     F.ta = F.mt = tpi;
     F.tq = std::min(tpi, VQT);
     const auto groups = [m](int per) { return (m + per - 1) / per; };
     const int ni = 2 * m + nrh * groups(F.tq) + F.na * groups(F.ta) + F.nm * groups(F.mt);
-    if (ni <= M->flow_grid) break;
+    if (F.fuse || ni <= M->flow_grid) break;
   }
   const void *k = reinterpret_cast<const void *>(k_flowm);
   if (M->exec_mode == 4) {
@@ -2622,7 +2665,8 @@ int run_pass(mllm_model *M, const int32_t *ids, int m, int pos0, int lm_rows) {
   if (int rc = upload_state(M)) return rc;
   MLLM_HIP(hipEventRecord(M->ev0, M->stream));
   int rc = kFlowFellBack;
-  if (M->exec_mode >= 3 && m == 1 && lm_rows == 1) rc = launch_flow(M, 1);
+  // one row, with or without "every row's" logits, is the decode step
+  if (M->exec_mode >= 3 && m == 1 && lm_rows != 0) rc = launch_flow(M, 1);
   else if (M->exec_mode >= 3 && m <= M->flowm_max && lm_rows == 2) rc = launch_flowm(M, m, pos0);
   if (rc == kFlowFellBack) rc = enqueue_pass_phases(M, m, lm_rows != 0);
   if (rc) return rc;
@@ -2943,6 +2987,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       M->flow_default = true;
       // the verify kernel: the most tokens whose LDS still lets the same grid
       // be resident (one workgroup per CU)
+      if (const char *v = getenv("MLLM_VERIFY_FUSE")) M->verify_fuse = atoi(v);
       const void *km = reinterpret_cast<const void *>(k_flowm);
       for (int mm = std::min(MAXT, M->max_pass); mm >= 2; --mm) {
         const size_t b = flowm_lds_bytes(P, F, mm);

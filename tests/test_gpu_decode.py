@@ -77,7 +77,7 @@ def test_exec_modes_bit_identical():
 
 @gpu
 @pytest.mark.parametrize("mode", [1, 3, 4])
-@pytest.mark.parametrize("n", [1, 2, 5, 9, 16])
+@pytest.mark.parametrize("n", [1, 2, 4, 5, 9, 16])
 def test_verify_rows_bit_identical_to_decode(n, mode):
     """A (k+1)-row verify pass -- one step of the persistent kernel in modes
     3 and 4 (k_flowm), the phase kernels in mode 1 -- gives every row's
@@ -304,11 +304,14 @@ def test_decode_precision_full_size_135m(oracle_lib):
 
 
 @gpu
+@pytest.mark.parametrize("fuse", [0, 16])
 @pytest.mark.parametrize("kv_fp16", [False, True])
-def test_verify_across_splits_bit_identical_to_decode(kv_fp16):
+def test_verify_across_splits_bit_identical_to_decode(kv_fp16, fuse, monkeypatch):
     """Verify rows whose positions straddle a 256-position attention split
-    (250 .. 258) and reach past it, in the persistent kernel, against
+    (250 .. 258) and reach past it, in the persistent kernel -- the five-stage
+    step (fuse 0) and the fused three-stage step (fuse 16) -- against
     single-token decode at each position."""
+    monkeypatch.setenv("MLLM_VERIFY_FUSE", str(fuse))
     bundle = build("llama", seed=16, max_seq_len=512)
     g = mllm.PetitGPT(bundle, kv_fp16=kv_fp16)
     assert g.flowVerifyTokens >= 9
