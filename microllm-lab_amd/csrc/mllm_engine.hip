@@ -231,8 +231,9 @@ __device__ __forceinline__ void gains_store(const DecParams &P, const float *bia
 // consecutive pairs.  A round's
 // loads all go out before its first add, so a round costs one memory
 // latency; round 0 can be loaded ahead (resid_blocks_load) so its latency
-// overlaps the weight loads.  With POLL (persistent kernel) a round is loaded
-// again until every pair carries a tag of at least `want`.
+// overlaps the weight loads.  With POLL (persistent kernels) a round is
+// polled until every pair carries a tag of at least `want`: POLL 1 loads the
+// whole round again, POLL 2 only the pairs still missing.
 // Branch-free: an item or partial past the end reads pair 0 of partial 0
 // (valid memory) and is left out.
 struct ResidReg {
@@ -243,7 +244,7 @@ struct ResidReg {
 // once another workgroup failed) the error is recorded and the wait returns.
 __device__ __forceinline__ bool poll_give_up(const DecParams &P, unsigned spins);
 
-template <bool POLL>
+template <int POLL>
 __device__ __forceinline__ void resid_blocks_load(const DecParams &P, const uint2 *pt, int np, int round, int want,
                                                   ResidReg &R) {
   const int D = P.D, nc2 = D >> 1, nitems = nc2 * ((np + PB - 1) / PB);
@@ -268,7 +269,22 @@ __device__ __forceinline__ void resid_blocks_load(const DecParams &P, const uint
         ready &= !(it < nitems && b * PB + k < np) || (tag_ok(R.v[2 * k].y, want) && tag_ok(R.v[2 * k + 1].y, want));
       if (ready || poll_give_up(P, spins)) break;
       poll_fence();
-      load();
+      if (POLL == 1) {
+        load();
+        continue;
+      }
+      // POLL 2: only the pairs whose tag is not there yet are loaded again:
+      // once most producers are done, a round carries the few missing pairs
+      // instead of the whole gather (a CU's outstanding coherent loads bound
+      // its rate)
+#pragma unroll
+      for (int k = 0; k < PB; ++k) {
+        const int p = b * PB + k;
+        const bool ok = it < nitems && p < np;
+        const uint32_t e = ok ? (uint32_t)(p * D + c) : 0u;
+        if (ok && !tag_ok(R.v[2 * k].y, want)) R.v[2 * k] = tag_ld(pt, e);
+        if (ok && !tag_ok(R.v[2 * k + 1].y, want)) R.v[2 * k + 1] = tag_ld(pt, e + (uint32_t)nc2);
+      }
     }
   }
 }
@@ -295,7 +311,7 @@ __device__ __forceinline__ void resid_blocks_add(int D, int np, int round, const
 }
 
 // Every round of the block sums, round 0 already loaded into R0.
-template <bool POLL>
+template <int POLL>
 __device__ __forceinline__ void resid_blocks_rest(const DecParams &P, const uint2 *pt, int np, int want,
                                                   const ResidReg &R0, float *blk) {
   const int D = P.D;
@@ -308,7 +324,7 @@ __device__ __forceinline__ void resid_blocks_rest(const DecParams &P, const uint
   }
 }
 
-template <bool POLL>
+template <int POLL>
 __device__ __forceinline__ void resid_blocks(const DecParams &P, const uint2 *pt, int np, int want, float *blk) {
   ResidReg R0;
   resid_blocks_load<POLL>(P, pt, np, 0, want, R0);
@@ -981,7 +997,7 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
     if (wait()) return false;
     if (li > 0) {
       base = col_base_load<true>(P, P.xb, nq, st.tag + li - 1);
-      resid_blocks<true>(P, P.dpart, P.nchunk, st.tag + li - 1, blk);
+      resid_blocks<2>(P, P.dpart, P.nchunk, st.tag + li - 1, blk);
     }
   } else {
     // activations first, then the weights (loads retire in issue order)
@@ -1102,7 +1118,7 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
     float *bt = blk + (t & 1) * nb * D;
     if (FLOW || t > 0) {
       base = col_base_load<FLOW>(P, P.xa + (size_t)t * D, nq, want);
-      resid_blocks<FLOW>(P, P.opart + (size_t)t * P.NH * D, P.NH, want, bt);
+      resid_blocks<FLOW ? 2 : 0>(P, P.opart + (size_t)t * P.NH * D, P.NH, want, bt);
     }
     __syncthreads();
     col_norm(P, col_finish(bt, nq, P.NH, base, gl, D, gpt2), gl, red, qx + t * ng * Q6R,
@@ -1175,11 +1191,11 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
 // for the lm_head of the persistent kernel, or xn (coherent stores) for the
 // lm_head kernel.  blk needs nb * D floats; the
 // caller has staged the norm_f gains in gl.
-template <bool POLL>
+template <int POLL>
 __device__ __forceinline__ void final_row(const DecParams &P, int t, float *blk, const float *gl, uint32_t *qx,
                                           bool to_global, int want) {
   const int D = P.D, nq = D >> 2;
-  const float4 base = col_base_load<POLL>(P, P.xb + (size_t)t * D, nq, want);
+  const float4 base = col_base_load<(POLL != 0)>(P, P.xb + (size_t)t * D, nq, want);
   resid_blocks<POLL>(P, P.dpart + (size_t)t * P.nchunk * D, P.nchunk, want, blk);
   __syncthreads();
   const float4 x = col_finish(blk, nq, P.nchunk, base, gl, D, P.arch == 1);
@@ -1610,7 +1626,7 @@ __device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, co
   if (wait()) return false;
   const bool penal = P.arch == 1 && st_ld(P, ST_OFF(chain)) != 0;
   if (penal && tid() == 0) gpt2_lists(P, s.lists);
-  final_row<true>(P, 0, blk, gl, s.qx, false, st.tag + P.L - 1);
+  final_row<2>(P, 0, blk, gl, s.qx, false, st.tag + P.L - 1);
   __syncthreads();
   const int nban = penal ? s.lists[0] : 0, nrec = penal ? s.lists[1] : 0;
   while (tile < L.ntiles) {
