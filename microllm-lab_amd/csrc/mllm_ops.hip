@@ -52,6 +52,26 @@ extern "C" int mllm_kernel_version(void) { return 1; }
 // row sums go through LDS in a fixed order that depends only on ng.
 constexpr int GX_BATCH = 4;          // float4s of x per thread loaded ahead of the weights
 
+// x through buffer loads, like the weights: vector-memory loads of one kind
+// complete in issue order, so the staging waits for x alone (vmcnt) while the
+// weights are in flight.  A load through a generic pointer is a flat load,
+// which may complete out of order with them: the compiler then waits for every
+// load in flight before the first use of x.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t x_rsrc(const float *x) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(x), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ float4 x_ld4(__amdgpu_buffer_rsrc_t r, int q) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, q * 16, 0, 0));
+}
+// Called once the weights' loads are issued: from here on x is the value in
+// these registers, so the compiler cannot load it again behind the weights
+// (it would rather re-load x than keep it live across them, and the staging
+// would then wait for every weight).
+__device__ __forceinline__ void x_pin(float4 (&xv)[GX_BATCH]) {
+#pragma unroll
+  for (int i = 0; i < GX_BATCH; ++i) asm volatile("" : "+v"(xv[i].x), "+v"(xv[i].y), "+v"(xv[i].z), "+v"(xv[i].w));
+}
+
 // Sum over lpr (a power of two <= 64) neighbouring lanes; whole lpr-lane
 // segments are active.
 __device__ __forceinline__ float seg_sum(float a, int lpr) {
@@ -95,12 +115,12 @@ __device__ __forceinline__ void q4_gemv_tile(const uint8_t *__restrict__ packed,
   const int row0 = tile * RT;
   // x ahead of the weights: loads retire in order, so the staging below
   // waits for x alone while the weights are in flight
-  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  const __amdgpu_buffer_rsrc_t rx = x_rsrc(x);
   float4 xv[GX_BATCH];
 #pragma unroll
   for (int i = 0; i < GX_BATCH; ++i) {
     const int q = t + i * WGT;
-    xv[i] = x4[q < nx ? q : 0];
+    xv[i] = x_ld4(rx, q < nx ? q : 0);
   }
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(packed), (short)0,
                                                                       0x7fffffff, 0x00020000);
@@ -115,16 +135,29 @@ __device__ __forceinline__ void q4_gemv_tile(const uint8_t *__restrict__ packed,
     const uint32_t c = (uint32_t)(row * ng + g);
     w[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(c * 16), 0, 0));
     s[p] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(c * 4), 0, 0));
+    __builtin_amdgcn_sched_barrier(0);  // chunk p's loads (weights, scale) before chunk p + 1's
   }
+  x_pin(xv);
 #pragma unroll
   for (int i = 0; i < GX_BATCH; ++i)
     if (i * WGT < nx) q6_stage_col(xv[i], t + i * WGT < nx, t + i * WGT, rec);
   for (int base = GX_BATCH * WGT; base < nx; base += WGT) {
     const int q = base + t;
-    q6_stage_col(x4[q < nx ? q : 0], q < nx, q, rec);
+    q6_stage_col(x_ld4(rx, q < nx ? q : 0), q < nx, q, rec);
   }
   __syncthreads();
-  if (act) {
+  if (act && G.m == 1) {
+    // one token: chunk by chunk, in the loads' order, so each dot waits only
+    // for its own chunk and the dots run while later chunks stream in (inside
+    // a token loop the compiler would prepare every chunk before the first)
+    const Q6Rec xr = q6_load(rec + g * Q6R);
+    float *pp = part + rr * ngp + g;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      pp[p * G.rpp * ngp] = q4_dot6(w[p], xr, s[p]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else if (act) {
     for (int tok = 0; tok < G.m; ++tok) {
       const Q6Rec xr = q6_load(rec + (tok * ng + g) * Q6R);
       float *pp = part + (tok * RT + rr) * ngp + g;
@@ -326,12 +359,12 @@ __device__ __forceinline__ void q8_gemv_tile(const int8_t *__restrict__ q, const
   const bool act = rr0 < G.rpp;
   const int rr = act ? rr0 : 0, g = act ? t - rr0 * ng : 0;
   const int row0 = tile * RT;
-  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  const __amdgpu_buffer_rsrc_t rx = x_rsrc(x);
   float4 xv[GX_BATCH];
 #pragma unroll
   for (int i = 0; i < GX_BATCH; ++i) {
     const int qq = t + i * WGT;
-    xv[i] = x4[qq < nx ? qq : 0];
+    xv[i] = x_ld4(rx, qq < nx ? qq : 0);
   }
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(q), (short)0, 0x7fffffff,
                                                                       0x00020000);
@@ -347,20 +380,25 @@ __device__ __forceinline__ void q8_gemv_tile(const int8_t *__restrict__ q, const
     wa[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(c * 32), 0, 0));
     wb[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(c * 32 + 16), 0, 0));
     s[p] = PERROW ? 1.f : __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(c * 4), 0, 0));
+    __builtin_amdgcn_sched_barrier(0);  // chunk p's loads before chunk p + 1's
   }
+  x_pin(xv);
 #pragma unroll
   for (int i = 0; i < GX_BATCH; ++i)
     if (i * WGT < nx) q3_stage_col(xv[i], t + i * WGT < nx, t + i * WGT, rec);
   for (int base = GX_BATCH * WGT; base < nx; base += WGT) {
     const int qq = base + t;
-    q3_stage_col(x4[qq < nx ? qq : 0], qq < nx, qq, rec);
+    q3_stage_col(x_ld4(rx, qq < nx ? qq : 0), qq < nx, qq, rec);
   }
   __syncthreads();
   if (act) {
     const Q6Rec xr = q6_load(rec + g * Q6R);
     float *pp = part + rr * ngp + g;
 #pragma unroll
-    for (int p = 0; p < P; ++p) pp[p * G.rpp * ngp] = q8_dot3(wa[p], wb[p], xr, s[p]);
+    for (int p = 0; p < P; ++p) {
+      pp[p * G.rpp * ngp] = q8_dot3(wa[p], wb[p], xr, s[p]);  // chunk by chunk, as q4_gemv_tile
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   __syncthreads();
   // row sums: q4_gemv_tile's order
