@@ -99,23 +99,35 @@ __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F7
 
 // Tagged values.  A value handed from one workgroup to another inside the
 // persistent kernel travels with the tag of the (step, layer) that wrote it,
-// as one naturally aligned 64-bit (float bits, tag) pair, written by one
-// 64-bit store and read by one 64-bit load with the device-scope (sc1)
-// policy.  That pair of instructions is what the AMDGPU memory model (the
-// GFX942-family mapping LLVM implements for gfx950) emits for a relaxed
-// agent-scope atomic 64-bit store and load -- "buffer/global/flat_store
-// sc1=1", "buffer/global/flat_load sc1=1" -- so each access is single-copy
-// atomic: a reader that sees the tag it waits for also sees the value written
-// with it, and polling the data replaces a completion wait plus a flag.
-// (The buffer form keeps the wave-uniform base in scalar registers; a
-// __hip_atomic_load of the same address compiles to the global form of the
-// same instruction but holds a 64-bit address per value in VGPRs.)  Tags grow
-// across launches and are compared modulo 2^32.
+// as one naturally aligned 8-byte pair (x, y) = (v, v ^ tag) of float bits v,
+// stored by one 8-byte device-scope (sc1) store.  Readers load pairs with
+// sc1 loads of 8 or 16 bytes (two neighbouring pairs) and accept a pair only
+// when x ^ y equals the tag they wait for exactly; the value is then x.
+// The argument needs nothing wider than single-copy atomic dwords:
+//  - a location is rewritten only after every reader of its previous version
+//    is done (each buffer's writers depend, through the data edges, on all of
+//    its readers), so a polling reader sees one of two versions of a pair:
+//    the old (v0, v0 ^ t0) with t0 != want, or the new (v1, v1 ^ want);
+//  - a read that returns both dwords of one version passes the check exactly
+//    when that version is the new one;
+//  - a read that mixes the versions' dwords passes only with a value that is
+//    the new one's: (v1, v0 ^ t0) passes iff v1 ^ v0 ^ t0 == want, and then
+//    x = v1; (v0, v1 ^ want) passes iff v0 == v1, and then x = v0 = v1.
+// So a reader that sees the tag it waits for holds the value stored with it,
+// whether or not the hardware moves a lane's 8 or 16 bytes in one piece, and
+// polling the data replaces a completion wait plus a flag.  Every writer of
+// these buffers (decode, verify and phase kernels) uses the encoding, so no
+// stale pair can pass either.  Tags grow across launches (32-bit, wrapping
+// after 2^25 steps); buffers start zeroed (tag 0, below every tag waited for).
+__device__ __forceinline__ uint32_t pair_tag(uint2 p) { return p.x ^ p.y; }
+__device__ __forceinline__ bool pair_ok(uint2 p, int want) { return (p.x ^ p.y) == (uint32_t)want; }
+// Flags (single dwords) are compared modulo 2^32: at least e.
 __device__ __forceinline__ bool tag_ok(uint32_t tag, int want) { return (int)(tag - (uint32_t)want) >= 0; }
 // Element i of a row of pairs at a wave-uniform base.
 __device__ __forceinline__ uint2 tag_ld(const uint2 *base, uint32_t i) { return coh_ld8(base, i * 8u); }
+__device__ __forceinline__ uint2 tag_pair(uint32_t bits, int tag) { return make_uint2(bits, bits ^ (uint32_t)tag); }
 __device__ __forceinline__ void tag_st(uint2 *base, uint32_t i, float v, int tag) {
-  coh_st8(base, i * 8u, make_uint2(__float_as_uint(v), (uint32_t)tag));
+  coh_st8(base, i * 8u, tag_pair(__float_as_uint(v), tag));
 }
 // A compiler barrier for polling loops: the loads after it are issued again
 // on every iteration instead of being hoisted out of the loop.

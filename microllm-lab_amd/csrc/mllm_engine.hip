@@ -226,13 +226,17 @@ __device__ __forceinline__ void gains_store(const DecParams &P, const float *bia
 // (from +0).  The order of every addition is fixed by np alone.
 // The partials are rows of D tagged pairs.  The block sums use every thread
 // of a 1024-thread workgroup: item it = b * (D / 2) + c (round it / 1024)
-// forms B_b of columns c and c + D / 2 into blk[b*D + c] and
-// blk[b*D + c + D/2] (LDS), so each load instruction of a wave reads 64
-// consecutive pairs.  A round's
+// forms B_b of two columns.  With W16 these are columns 2c and 2c + 1, read
+// as one 16-byte load (two neighbouring pairs) per partial, so each load
+// instruction of a wave reads 1 KB contiguous; without it, columns c and
+// c + D / 2 by two 8-byte loads.  A workgroup's gather rate is bound by its
+// load instructions (16-byte loads move a 110 KB gather in about half the
+// time of 8-byte ones), and the gather of the down partials is the larger part
+// of a handoff.  A round's
 // loads all go out before its first add, so a round costs one memory
 // latency; round 0 can be loaded ahead (resid_blocks_load) so its latency
 // overlaps the weight loads.  With POLL (persistent kernels) a round is
-// polled until every pair carries a tag of at least `want`: POLL 1 loads the
+// polled until every pair carries the tag `want`: POLL 1 loads the
 // whole round again, POLL 2 only the pairs still missing.
 // Branch-free: an item or partial past the end reads pair 0 of partial 0
 // (valid memory) and is left out.
@@ -244,33 +248,47 @@ struct ResidReg {
 // once another workgroup failed) the error is recorded and the wait returns.
 __device__ __forceinline__ bool poll_give_up(const DecParams &P, unsigned spins);
 
-template <int POLL>
+// With W16, pairs 2c and 2c + 1 of a partial come from one 16-byte load (1 KB
+// contiguous per wave instruction, half the load instructions); without it,
+// pairs c and c + D / 2 come from two 8-byte loads.
+template <bool W16>
+__device__ __forceinline__ void resid_pair2(const uint2 *pt, int D, int p, int c, bool ok, uint2 &lo, uint2 &hi) {
+  if (W16) {
+    const uint4 u = coh_ld16(pt, (ok ? (uint32_t)(p * D + 2 * c) : 0u) * 8u);
+    lo = make_uint2(u.x, u.y);
+    hi = make_uint2(u.z, u.w);
+  } else {
+    const uint32_t e = ok ? (uint32_t)(p * D + c) : 0u;
+    lo = tag_ld(pt, e);
+    hi = tag_ld(pt, e + (ok ? (uint32_t)(D >> 1) : 0u));
+  }
+}
+
+template <int POLL, bool W16 = false>
 __device__ __forceinline__ void resid_blocks_load(const DecParams &P, const uint2 *pt, int np, int round, int want,
                                                   ResidReg &R) {
   const int D = P.D, nc2 = D >> 1, nitems = nc2 * ((np + PB - 1) / PB);
   const int it = tid() + round * 1024;
   const int b = it / nc2, c = it - b * nc2;
-  auto load = [&] {
 #pragma unroll
-    for (int k = 0; k < PB; ++k) {
-      const int p = b * PB + k;
-      const bool ok = it < nitems && p < np;
-      const uint32_t e = ok ? (uint32_t)(p * D + c) : 0u;
-      R.v[2 * k] = tag_ld(pt, e);
-      R.v[2 * k + 1] = tag_ld(pt, e + (ok ? (uint32_t)nc2 : 0u));
-    }
-  };
-  load();
+  for (int k = 0; k < PB; ++k) {
+    const int p = b * PB + k;
+    resid_pair2<W16>(pt, D, p, c, it < nitems && p < np, R.v[2 * k], R.v[2 * k + 1]);
+  }
   if (POLL) {
     for (unsigned spins = 1;; ++spins) {
       bool ready = true;
 #pragma unroll
       for (int k = 0; k < PB; ++k)
-        ready &= !(it < nitems && b * PB + k < np) || (tag_ok(R.v[2 * k].y, want) && tag_ok(R.v[2 * k + 1].y, want));
+        ready &= !(it < nitems && b * PB + k < np) || (pair_ok(R.v[2 * k], want) && pair_ok(R.v[2 * k + 1], want));
       if (ready || poll_give_up(P, spins)) break;
       poll_fence();
       if (POLL == 1) {
-        load();
+#pragma unroll
+        for (int k = 0; k < PB; ++k) {
+          const int p = b * PB + k;
+          resid_pair2<W16>(pt, D, p, c, it < nitems && p < np, R.v[2 * k], R.v[2 * k + 1]);
+        }
         continue;
       }
       // POLL 2: only the pairs whose tag is not there yet are loaded again:
@@ -281,9 +299,8 @@ __device__ __forceinline__ void resid_blocks_load(const DecParams &P, const uint
       for (int k = 0; k < PB; ++k) {
         const int p = b * PB + k;
         const bool ok = it < nitems && p < np;
-        const uint32_t e = ok ? (uint32_t)(p * D + c) : 0u;
-        if (ok && !tag_ok(R.v[2 * k].y, want)) R.v[2 * k] = tag_ld(pt, e);
-        if (ok && !tag_ok(R.v[2 * k + 1].y, want)) R.v[2 * k + 1] = tag_ld(pt, e + (uint32_t)nc2);
+        const bool miss = !(pair_ok(R.v[2 * k], want) && pair_ok(R.v[2 * k + 1], want));
+        if (ok && miss) resid_pair2<W16>(pt, D, p, c, true, R.v[2 * k], R.v[2 * k + 1]);
       }
     }
   }
@@ -293,6 +310,7 @@ __device__ __forceinline__ void resid_blocks_load(const DecParams &P, const uint
 // conditional): a load consumed inside a divergent branch leaves the
 // compiler unsure it has completed, and it then waits for every load in
 // flight before the register is reused.
+template <bool W16 = false>
 __device__ __forceinline__ void resid_blocks_add(int D, int np, int round, const ResidReg &R, float *blk) {
   const int nc2 = D >> 1, nitems = nc2 * ((np + PB - 1) / PB);
   const int it = tid() + round * 1024;
@@ -305,30 +323,34 @@ __device__ __forceinline__ void resid_blocks_add(int D, int np, int round, const
     a1 = a1 + (use ? __uint_as_float(R.v[2 * k + 1].x) : 0.f);
   }
   if (it < nitems) {
-    blk[b * D + c] = a0;
-    blk[b * D + c + nc2] = a1;
+    if (W16) {
+      *reinterpret_cast<float2 *>(blk + b * D + 2 * c) = make_float2(a0, a1);
+    } else {
+      blk[b * D + c] = a0;
+      blk[b * D + c + nc2] = a1;
+    }
   }
 }
 
 // Every round of the block sums, round 0 already loaded into R0.
-template <int POLL>
+template <int POLL, bool W16 = false>
 __device__ __forceinline__ void resid_blocks_rest(const DecParams &P, const uint2 *pt, int np, int want,
                                                   const ResidReg &R0, float *blk) {
   const int D = P.D;
-  resid_blocks_add(D, np, 0, R0, blk);
+  resid_blocks_add<W16>(D, np, 0, R0, blk);
   const int nitems = (D >> 1) * ((np + PB - 1) / PB);
   for (int round = 1; round * 1024 < nitems; ++round) {
     ResidReg R1;
-    resid_blocks_load<POLL>(P, pt, np, round, want, R1);
-    resid_blocks_add(D, np, round, R1, blk);
+    resid_blocks_load<POLL, W16>(P, pt, np, round, want, R1);
+    resid_blocks_add<W16>(D, np, round, R1, blk);
   }
 }
 
-template <int POLL>
+template <int POLL, bool W16 = false>
 __device__ __forceinline__ void resid_blocks(const DecParams &P, const uint2 *pt, int np, int want, float *blk) {
   ResidReg R0;
-  resid_blocks_load<POLL>(P, pt, np, 0, want, R0);
-  resid_blocks_rest<POLL>(P, pt, np, want, R0, blk);
+  resid_blocks_load<POLL, W16>(P, pt, np, 0, want, R0);
+  resid_blocks_rest<POLL, W16>(P, pt, np, want, R0, blk);
 }
 
 // One token's residual and norm, one float4 column q < nq per thread
@@ -414,7 +436,7 @@ __device__ __forceinline__ float4 col_base_load(const DecParams &P, const uint2 
   const uint32_t b = (uint32_t)min(tid(), nq - 1), n = (uint32_t)nq;
   uint2 v0 = tag_ld(base, b), v1 = tag_ld(base, b + n), v2 = tag_ld(base, b + 2 * n), v3 = tag_ld(base, b + 3 * n);
   if (POLL && tid() < nq) {
-    for (unsigned spins = 1; !(tag_ok(v0.y, want) && tag_ok(v1.y, want) && tag_ok(v2.y, want) && tag_ok(v3.y, want)) &&
+    for (unsigned spins = 1; !(pair_ok(v0, want) && pair_ok(v1, want) && pair_ok(v2, want) && pair_ok(v3, want)) &&
                              !poll_give_up(P, spins);
          ++spins) {
       poll_fence();
@@ -943,6 +965,37 @@ __device__ __forceinline__ void attn1_pre(const DecParams &P, const LayerW &Lw, 
   gains_load(P, Lw.n1, rbias, GR);
 }
 
+// Deferred K/V-row stores of the persistent kernel.  Only later steps read
+// a position's cached K/V row from memory (the query heads of the group form
+// the row themselves, and the current position lies in the last split only),
+// so the writer keeps the row's two stores -- one word per lane of waves 1
+// (K) and 2 (V) -- in LDS slots of its own (byte offset, bits; offset ~0: none)
+// and issues them when the workgroup starts its next attention item.  A slot
+// with nothing pending points at a pad word past the end of the cache
+// (kv_pad), so the store is issued unconditionally.  That
+// item's output, and any later one, waits for the workgroup's stores before it
+// becomes visible (attn_core), and every reader of the row in a later step
+// depends through the data edges on the workgroup's next item of the same step
+// (or, past the last layer, of the next step); the kernel issues what is left
+// when it ends.  The writer therefore never waits for the acknowledgement of
+// a row it has just stored, and the output it publishes does not wait either.
+__device__ __forceinline__ uint2 *kv_slot(float *smem, int kvp) {
+  return reinterpret_cast<uint2 *>(smem + kvp) + (tid() - 64);
+}
+__device__ __forceinline__ uint2 kv_pad(const DecParams &P) {
+  return make_uint2((uint32_t)kv_index(P, P.L, 0, 0, 0) * (P.kv_fp16 ? 2u : 4u), 0u);
+}
+__device__ __forceinline__ void kv_flush(const DecParams &P, float *smem, int kvp) {
+  const int wv = wave_id();
+  if (wv == 1 || wv == 2) {
+    uint2 *slot = kv_slot(smem, kvp);
+    const uint2 e = *slot;
+    if (P.kv_fp16) coh_sth(P.kv, e.x, (unsigned short)e.y);
+    else coh_sti(P.kv, e.x, (int)e.y);
+    *slot = kv_pad(P);
+  }
+}
+
 // Single-token attention item (split sp, head h) with the QKV projection
 // fused in: the item forms its own query head and its K/V head's rows of
 // attn.qkv from the residual (the K/V rows are formed again by every query
@@ -953,7 +1006,7 @@ __device__ __forceinline__ void attn1_pre(const DecParams &P, const LayerW &Lw, 
 // order), so the step matches a multi-token pass bit for bit.
 template <bool FLOW, int AQC, class W>
 __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int item, const Step &st, float *smem,
-                            W &&wait) {
+                            W &&wait, int kvp = 0) {
   const int sp = item / P.NH, h = item - sp * P.NH;
   if (st.done) return false;
   const int pos = st.pos0;
@@ -992,12 +1045,13 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   // (their registers are then free), the V rows once the q/k/v tile is
   // consumed; their latency overlaps the norm, the q/k/v rows and the scores.
   if (FLOW) {
+    kv_flush(P, smem, kvp);  // the previous item's K/V row
     attn1_pre(P, Lw, rq, rk, rv, h, pos, row_own, rbias, Wt, Ro, c_own, s_own, GR);
     gains_store(P, rbias, GR, gl);
     if (wait()) return false;
     if (li > 0) {
       base = col_base_load<true>(P, P.xb, nq, st.tag + li - 1);
-      resid_blocks<2>(P, P.dpart, P.nchunk, st.tag + li - 1, blk);
+      resid_blocks<2, true>(P, P.dpart, P.nchunk, st.tag + li - 1, blk);
     }
   } else {
     // activations first, then the weights (loads retire in issue order)
@@ -1045,10 +1099,15 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
     } else {
       const size_t k = kv_index(P, li, wv - 1, kvh, pos) + lane;
       float r = v;
+      // FLOW: the row's stores are issued by the workgroup's next attention item
+      uint2 *slot = kv_slot(smem, kvp);
       if (P.kv_fp16) {
         const __half hv = __float2half_rn(v);
         r = __half2float(hv);
-        if (writer) coh_sth(P.kv, 2u * (uint32_t)k, __half_as_ushort(hv));
+        if (writer && FLOW) *slot = make_uint2(2u * (uint32_t)k, __half_as_ushort(hv));
+        else if (writer) coh_sth(P.kv, 2u * (uint32_t)k, __half_as_ushort(hv));
+      } else if (writer && FLOW) {
+        *slot = make_uint2(4u * (uint32_t)k, __float_as_uint(v));
       } else if (writer) {
         coh_stf(P.kv, 4u * (uint32_t)k, v);
       }
@@ -1118,7 +1177,7 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
     float *bt = blk + (t & 1) * nb * D;
     if (FLOW || t > 0) {
       base = col_base_load<FLOW>(P, P.xa + (size_t)t * D, nq, want);
-      resid_blocks<FLOW ? 2 : 0>(P, P.opart + (size_t)t * P.NH * D, P.NH, want, bt);
+      resid_blocks<FLOW ? 2 : 0, FLOW>(P, P.opart + (size_t)t * P.NH * D, P.NH, want, bt);
     }
     __syncthreads();
     col_norm(P, col_finish(bt, nq, P.NH, base, gl, D, gpt2), gl, red, qx + t * ng * Q6R,
@@ -1196,7 +1255,7 @@ __device__ __forceinline__ void final_row(const DecParams &P, int t, float *blk,
                                           bool to_global, int want) {
   const int D = P.D, nq = D >> 2;
   const float4 base = col_base_load<(POLL != 0)>(P, P.xb + (size_t)t * D, nq, want);
-  resid_blocks<POLL>(P, P.dpart + (size_t)t * P.nchunk * D, P.nchunk, want, blk);
+  resid_blocks<POLL, POLL == 2>(P, P.dpart + (size_t)t * P.nchunk * D, P.nchunk, want, blk);
   __syncthreads();
   const float4 x = col_finish(blk, nq, P.nchunk, base, gl, D, P.arch == 1);
   col_norm(P, x, gl, blk + ((P.nchunk + PB - 1) / PB) * D, qx, ColOut{nullptr, 0, to_global ? P.xn + (size_t)t * D : nullptr});
@@ -1519,6 +1578,7 @@ struct FlowGeom {
   int fuse;               // k_flowm: no norm items; the QKV, MLP and lm_head items form their tokens' norms
   int na, nm, ni;         // items per layer: attention (split, head) items, MLP chunks; ni = na + nm
   int lm_rpt, lm_tiles;   // lm_head tiles of the 1024-thread role (one per workgroup w < lm_tiles, then w + G ...)
+  int kvp;                // k_flow: LDS float offset of the deferred K/V-row slots (kv_flush)
 };
 
 constexpr int FLT = 1024;               // threads per workgroup of the persistent kernel
@@ -1656,6 +1716,7 @@ __global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
   const LmGeom lg{F.lm_rpt, F.lm_tiles};
   const int pos_start = st_ld(P, ST_OFF(pos0));
   int *const red = reinterpret_cast<int *>(smem);
+  if (wave_id() == 1 || wave_id() == 2) *kv_slot(smem, F.kvp) = kv_pad(P);  // no deferred K/V row yet
   for (int step = 0; step < F.steps; ++step) {
     FlowCtl C{P, am_flag, F.ep0 + step, step > 0, false};
     const int e = C.e;
@@ -1675,7 +1736,7 @@ __global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
         // down partials, or this layer's attention partials); the waits
         // below only take the step's ARGMAX and `done`
         if (j < F.na) {
-          phase_attn1<true, AQC>(P, Lw, li, j, st, smem, [&] { return C.wait(nullptr, 0); });
+          phase_attn1<true, AQC>(P, Lw, li, j, st, smem, [&] { return C.wait(nullptr, 0); }, F.kvp);
         } else {
           const int it = j - F.na;
           phase_mlp<true>(P, Lw, 1, li, it, st, smem, [&] { return C.wait(nullptr, 0); });
@@ -1713,6 +1774,7 @@ __global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
     }
     if (C.done) break;
   }
+  kv_flush(P, smem, F.kvp);
 }
 
 // ---------------------------------------------------------------- verify step
@@ -1743,7 +1805,7 @@ constexpr int VLB = 4;  // tokens per pass over an lm_head tile
 
 // The n dwords at LDS src as tagged pairs at dst.
 __device__ __forceinline__ void rec_put(uint2 *dst, const uint32_t *src, int n, int tag) {
-  for (int i = tid(); i < n; i += 1024) coh_st8(dst, (uint32_t)i * 8u, make_uint2(src[i], (uint32_t)tag));
+  for (int i = tid(); i < n; i += 1024) coh_st8(dst, (uint32_t)i * 8u, tag_pair(src[i], tag));
 }
 
 // n tagged dwords into LDS dst, loaded again until every tag reaches want:
@@ -1757,7 +1819,7 @@ __device__ __forceinline__ void rec_get(const DecParams &P, const uint2 *src, in
     for (unsigned spins = 1;; ++spins) {
       bool ready = true;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) ready &= tag_ok(v[k].y, want);
+      for (int k = 0; k < 8; ++k) ready &= pair_ok(v[k], want);
       if (ready || poll_give_up(P, spins)) break;
       poll_fence();
 #pragma unroll
@@ -1931,7 +1993,7 @@ __device__ __forceinline__ void qkv_rows_get(const DecParams &P, int li, int wan
   for (unsigned spins = 1;; ++spins) {
     bool ready = true;
 #pragma unroll
-    for (int k = 0; k < 3; ++k) ready &= tag_ok(v[k].y, want);
+    for (int k = 0; k < 3; ++k) ready &= pair_ok(v[k], want);
     if (ready || poll_give_up(P, spins)) break;
     poll_fence();
 #pragma unroll
@@ -2882,7 +2944,9 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   if (!rc) rc = dev_alloc(M, (void **)&P.rec, sizeof(uint2) * 2 * MAXT * ngd * Q6R);
   if (!rc) rc = dev_alloc(M, (void **)&P.qkvr, sizeof(uint2) * L * MAXT * (NH + 2 * NKV) * HD);
   if (!rc) rc = dev_alloc(M, (void **)&P.q, sizeof(float) * MAXT * NH * HD);
-  if (!rc) rc = dev_alloc(M, &P.kv, kv_elems * (c.kv_fp16 ? 2 : 4));
+  // + a pad word that the persistent kernel's deferred K/V stores write when
+  // nothing is pending
+  if (!rc) rc = dev_alloc(M, &P.kv, kv_elems * (c.kv_fp16 ? 2 : 4) + 256);
   if (!rc) rc = dev_alloc(M, (void **)&P.attp, sizeof(float) * MAXT * NH * P.nsplit_max * APS);
   if (!rc) rc = dev_alloc(M, (void **)&P.cnt, sizeof(unsigned) * MAXT * NH);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_logits, sizeof(float) * MAXT * (size_t)V);
@@ -2981,7 +3045,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
     F.ni = F.na + F.nm;
     F.lm_rpt = std::min(V, std::max(1, (FTC * FLT) / ngd));
     F.lm_tiles = (V + F.lm_rpt - 1) / F.lm_rpt;
-    M->flow_lds = flow_lds_bytes(P, F);
+    F.kvp = (int)al4(flow_lds_bytes(P, F) / sizeof(float));
+    M->flow_lds = ((size_t)F.kvp + 2 * 128) * sizeof(float);  // + the deferred K/V-row slots
     int per_cu = 0;
     const bool lds_ok = M->flow_lds <= lds_cap &&
                         (M->flow_lds <= 64 * 1024 ||
