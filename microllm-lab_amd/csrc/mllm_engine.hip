@@ -788,6 +788,46 @@ __device__ __forceinline__ void attn_v_load(const DecParams &P, int li, int kvh,
   }
 }
 
+// One wave's merge of a split's AW wave partials, every lane taking part:
+// mx = max_w m_w, f_w = expf(m_w - mx) (0 for a wave with no key), and
+// l = sum_w l_w f_w, own = sum_w acc_w[lane] f_w, each accumulated in
+// ascending w by FMA from +0.  The weights go back to LDS in place of the
+// maxima and return as broadcast reads, and every operand is loaded before
+// the first FMA: the chain then waits for LDS once, not once per pair of
+// waves, and needs no lane reads.  wm, wl: AW floats each (16-byte aligned);
+// wacc: AW rows of HD floats.
+__device__ __forceinline__ void split_merge(float *wm, const float *wl, const float *wacc, float &mx, float &l,
+                                            float &own) {
+  const int lane = lane_id();
+  const float wmv = lane < AW ? wm[lane] : -INFINITY;
+  mx = wave_max(wmv);
+  const float f = lane < AW ? expf(wmv - mx) : 0.f;
+  if (lane < AW) wm[lane] = f;  // the same wave reads it back: LDS operations of a wave complete in order
+  float av[AW], fv[AW], lv[AW];
+#pragma unroll
+  for (int w = 0; w < AW; ++w) av[w] = wacc[w * HD + lane];
+#pragma unroll
+  for (int w = 0; w < AW; w += 4) {
+    const float4 a = *reinterpret_cast<const float4 *>(wm + w);
+    const float4 b = *reinterpret_cast<const float4 *>(wl + w);
+    fv[w] = a.x;
+    fv[w + 1] = a.y;
+    fv[w + 2] = a.z;
+    fv[w + 3] = a.w;
+    lv[w] = b.x;
+    lv[w + 1] = b.y;
+    lv[w + 2] = b.z;
+    lv[w + 3] = b.w;
+  }
+  l = 0.f;
+  own = 0.f;
+#pragma unroll
+  for (int w = 0; w < AW; ++w) {
+    l = __builtin_fmaf(lv[w], fv[w], l);
+    own = __builtin_fmaf(av[w], fv[w], own);
+  }
+}
+
 // Scores, softmax statistics, P.V, the merge and the head's W_o slice, with
 // the query staged in A.qs and the keys in kr/vr; key knew of the split (when
 // >= 0) is taken from LDS instead (kvn: K row then V row), selected where it
@@ -844,22 +884,10 @@ __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, i
   }
   __syncthreads();
   // wave 0: the split's maximum, sum and P.V from the wave partials, added
-  // in wave order.  Lane w < AW forms wave w's weight expf(m_w - max) (a
-  // wave with no key has m_w = -inf and weight 0; wave 0 always has key 0);
-  // the weights reach every lane as scalars.
+  // in wave order (a wave with no key has m_w = -inf and weight 0; wave 0
+  // always has key 0)
   float mx = 0.f, l = 0.f, own = 0.f;
-  if (wv == 0) {
-    const float wm = lane < AW ? A.wm[lane] : -INFINITY;
-    const float wl = lane < AW ? A.wl[lane] : 0.f;
-    mx = wave_max(wm);
-    const float f = lane < AW ? expf(wm - mx) : 0.f;
-#pragma unroll
-    for (int w = 0; w < AW; ++w) {
-      const float fw = readlane_f(f, w);
-      l = __builtin_fmaf(readlane_f(wl, w), fw, l);
-      own = __builtin_fmaf(A.wacc[w * HD + lane], fw, own);
-    }
-  }
+  if (wv == 0) split_merge(A.wm, A.wl, A.wacc, mx, l, own);
   // split partials of (t, h): [nsplit_max][APS] floats (m, l, pad, pad, acc[64])
   const float *parts = P.attp + (size_t)(t * P.NH + h) * P.nsplit_max * APS;
   if (!solo) {
@@ -2088,17 +2116,8 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
   // solo split stages its output, the others publish their partials
   for (int t = ta + wv; t < u1; t += NWV) {
     const int ns = (pos0 + t) / ACH + 1;
-    const float wmv = lane < AW ? wm[t * AW + lane] : -INFINITY;
-    const float wlv = lane < AW ? wl[t * AW + lane] : 0.f;
-    const float mx = wave_max(wmv);
-    const float f = lane < AW ? expf(wmv - mx) : 0.f;
-    float l = 0.f, own = 0.f;
-#pragma unroll
-    for (int w = 0; w < AW; ++w) {
-      const float fw = readlane_f(f, w);
-      l = __builtin_fmaf(readlane_f(wlv, w), fw, l);
-      own = __builtin_fmaf(wacc[(t * AW + w) * HD + lane], fw, own);
-    }
+    float mx, l, own;
+    split_merge(wm + t * AW, wl + t * AW, wacc + t * AW * HD, mx, l, own);
     if (ns == 1) {
       q6_stage_lanes(own / l, attq + t * 2 * Q6R);
     } else {
