@@ -147,6 +147,7 @@ struct DecParams {
   float *logits;  // [MAXT][V]
   float *amv;     // [MAXT][lm_tiles]
   int *ami;
+  uint2 *amt;     // [2][lm_tiles][2] persistent decode: each lm_head tile's first maximum (value, row) as tagged pairs, by step parity
   int lm_rpt, lm_tiles, lm_grid;
   PassState *st;
   int *hist;      // [max_seq + 1]
@@ -1010,6 +1011,12 @@ __device__ __forceinline__ void attn1_pre(const DecParams &P, const LayerW &Lw, 
 __device__ __forceinline__ uint2 *kv_slot(float *smem, int kvp) {
   return reinterpret_cast<uint2 *>(smem + kvp) + (tid() - 64);
 }
+// The persistent kernel's broadcast slots (LDS, past the deferred K/V slots):
+// [0] the step's input token, [1] the chain is done, [2] workgroup 0's count
+// of history tokens, [3] the eos id (-1: none), [4] chained decode, [5, 21)
+// eight waves' (value, row) maxima (flow_tiles_argmax).
+__device__ __forceinline__ int *flow_slots(float *smem, int kvp) { return reinterpret_cast<int *>(smem + kvp + 256); }
+
 __device__ __forceinline__ uint2 kv_pad(const DecParams &P) {
   return make_uint2((uint32_t)kv_index(P, P.L, 0, 0, 0) * (P.kv_fp16 ? 2u : 4u), 0u);
 }
@@ -1098,7 +1105,11 @@ __device__ bool phase_attn1(const DecParams &P, const LayerW &Lw, int li, int it
   attn_v_load(P, li, kvh, s0, last ? cnt - 1 : cnt, vr);
   __builtin_amdgcn_sched_barrier(0);
   // the residual (layer 0: the embedding) and the norm
-  if (li == 0) base = embed_col(P, min(max(st_ld(P, ST_OFF(tok)), 0), P.V - 1), min(pos, P.max_seq - 1));
+  if (li == 0) {
+    // the persistent kernel takes the step's token from its slot
+    const int tok = FLOW ? flow_slots(smem, kvp)[0] : min(max(st_ld(P, ST_OFF(tok)), 0), P.V - 1);
+    base = embed_col(P, tok, min(pos, P.max_seq - 1));
+  }
   __syncthreads();
   const float4 x = li == 0 ? base : col_finish(blk, nq, P.nchunk, base, gl, D, rbias != nullptr);
   col_norm(P, x, gl, red, qx, ColOut{item == 0 ? P.xa : nullptr, st.tag + li});
@@ -1333,9 +1344,12 @@ struct LmGeom {
 // One lm_head tile whose weights are in R: logits rows [r0, r0+nr) of the m
 // tokens from tb, then the tile's first maximum per token (gpt2 chain: with
 // the argmaxGpt2 adjustments).
+// With amt (one token), the tile's first maximum goes out as two tagged pairs
+// (value, row) at amt[2 tile] instead of to amv / ami.
 template <int TCN, int NT>
 __device__ __forceinline__ void lm_tile(const DecParams &P, const LmGeom &L, const TileRegs<TCN> &R, int tile, int tb,
-                                        int m, const LmLds &s, bool penal, int nban, int nrec) {
+                                        int m, const LmLds &s, bool penal, int nban, int nrec, uint2 *amt = nullptr,
+                                        int amtag = 0) {
   const int ng = P.D >> 5, rpt = L.rpt;
   const int r0 = tile * rpt, nr = min(rpt, P.V - r0);
   tile_compute_q6<TCN, NT>(R, nr, ng, nr * ng, m, s.qx, tid() % ng, NT % ng, s.part, s.out, rpt);
@@ -1356,8 +1370,13 @@ __device__ __forceinline__ void lm_tile(const DecParams &P, const LmGeom &L, con
     }
     wave_argmax(bv, bi);
     if (lane_id() == 0) {
-      coh_stf(P.amv, 4u * ((tb + t) * P.lm_tiles + tile), bv);
-      coh_sti(P.ami, 4u * ((tb + t) * P.lm_tiles + tile), bi);
+      if (amt) {
+        const uint2 pv = tag_pair(__float_as_uint(bv), amtag), pi = tag_pair((uint32_t)bi, amtag);
+        coh_st16(amt, 16u * tile, make_uint4(pv.x, pv.y, pi.x, pi.y));
+      } else {
+        coh_stf(P.amv, 4u * ((tb + t) * P.lm_tiles + tile), bv);
+        coh_sti(P.ami, 4u * ((tb + t) * P.lm_tiles + tile), bi);
+      }
     }
   }
   __syncthreads();
@@ -1668,22 +1687,130 @@ __device__ __forceinline__ void flow_publish(int *f, int e) {
   if (tid() == 0) flag_st(f, e);
 }
 
-// A workgroup's waits within one step.  The first wait of a step also waits
-// for the previous step's ARGMAX and reads `done` (the chain emitted eos).
+// Step handoffs of the persistent decode kernel past the last layer.
+//  - Workgroup 0 (attention item 0's) forms the last layer's residual and the
+//    final norm once and publishes the normed row's Q6 records as tagged
+//    pairs (tag st.tag + L) at P.rec; every lm_head workgroup loads those 2 KB
+//    instead of gathering the last layer's 110 KB of down partials itself.
+//  - Every lm_head tile stores its first maximum (value, row) as two tagged
+//    pairs at P.amt (tag st.tag + TAGL - 2), without waiting for its stores.
+//    The pairs alternate between two buffers by step parity: step s + 2's
+//    tiles depend on every tile of step s + 1, and each of those was written
+//    by a workgroup after it read step s's maxima, so no reader of a step's
+//    maxima can find them overwritten.
+//  - At its first wait of the next step, every workgroup takes the first
+//    maximum over the tiles' pairs itself (the same total order, so the same
+//    token everywhere): the token for the embedding, and whether the chain
+//    emitted eos.  Workgroup 0 also records the step for the host (res,
+//    tok, pos0, the history, done, bad_tok; infer.js argmax and the chain
+//    rules of phase_argmax).  Its next attention output waits for all of its
+//    stores (attn_core), and every later reader of the history (the gpt2
+//    lm_head lists) depends on that output, so those stores need no wait of
+//    their own.  The last step's maximum is taken by workgroup 0 at the end
+//    of the launch.
+constexpr int TAG_LM = TAGL - 2;  // st.tag + TAG_LM: the lm_head tiles' maxima
+
+
+// Waves 0-7 (AMW): the first maximum over the ntiles tiles' tagged pairs of
+// tag `want`; tile k is taken by wave (k / 64) % AMW, one 16-byte load per
+// lane and round, polled (bounded) until both of its pairs carry the tag (one
+// round up to 512 tiles).  Each wave leaves its (value, row) in slots
+// [5 + 2 wv], [6 + 2 wv]; the caller combines them after a barrier.
+constexpr int AMW = 8;
+__device__ __forceinline__ uint2 *flow_amt(const DecParams &P, int e) {
+  return P.amt + (size_t)(e & 1) * 2 * P.lm_tiles;
+}
+__device__ __forceinline__ void flow_tiles_argmax(const DecParams &P, const uint2 *amt, int ntiles, int want,
+                                                  int *slots) {
+  const int lane = lane_id(), wv = wave_id();
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int b = 64 * wv; b < ntiles; b += AMW * 64) {
+    const uint32_t off = 16u * (uint32_t)min(b + lane, ntiles - 1);
+    uint4 u = coh_ld16(amt, off);
+    for (unsigned spins = 1; !__all(pair_ok(make_uint2(u.x, u.y), want) && pair_ok(make_uint2(u.z, u.w), want)) &&
+                             !poll_give_up(P, spins);
+         ++spins) {
+      poll_fence();
+      u = coh_ld16(amt, off);
+    }
+    const float v = __uint_as_float(u.x);
+    const int i = (int)u.z;
+    if (b + lane < ntiles && amax_better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  wave_argmax(bv, bi);
+  if (lane == 0) {
+    slots[5 + 2 * wv] = __float_as_int(bv);
+    slots[6 + 2 * wv] = bi;
+  }
+}
+
+// Thread 0: the first maximum's row from the AMW waves' slots.
+__device__ __forceinline__ int flow_tiles_combine(const int *slots) {
+  float v = __int_as_float(slots[5]);
+  int i = slots[6];
+  for (int k = 1; k < AMW; ++k)
+    if (amax_better(__int_as_float(slots[5 + 2 * k]), slots[6 + 2 * k], v, i)) {
+      v = __int_as_float(slots[5 + 2 * k]);
+      i = slots[6 + 2 * k];
+    }
+  return i;
+}
+
+// Wave 0 of workgroup 0, lane 0: the host's record of a finished step whose
+// first maximum is row i at position pos (phase_argmax's rules).
+__device__ __forceinline__ void flow_record_step(const DecParams &P, int *slots, int i, int pos) {
+  st_st(P, ST_OFF(res), i);
+  if (slots[4]) {
+    int tok = i;
+    if (tok < 0 || tok >= P.V) {  // no finite maximum (non-finite logits)
+      st_st(P, ST_OFF(bad_tok), 1);
+      tok = 0;
+    }
+    const int n_hist = slots[2];
+    coh_sti(P.hist, 4u * n_hist, tok);
+    slots[2] = n_hist + 1;
+    st_st(P, ST_OFF(n_hist), n_hist + 1);
+    st_st(P, ST_OFF(tok), tok);
+    st_st(P, ST_OFF(pos0), pos + 1);
+    if (tok == slots[3]) st_st(P, ST_OFF(done), 1);
+  }
+}
+
+// A workgroup's waits within one step.  resolve(), at the top of every step
+// after the first, takes the previous step's token from the lm_head tiles'
+// maxima (there no item holds registers, so the poll costs none of theirs).
 struct FlowCtl {
   const DecParams &P;
-  const int *am_flag;
-  int e;
-  bool pending;  // the step's ARGMAX wait is still due
+  int *slots;
+  int w, ntiles;
+  int e, pos;     // the step's epoch and position
+  bool pending;   // the previous step's token is still due
   bool done;
+  __device__ void resolve() {
+    if (pending) {
+      if (wave_id() < AMW)
+        flow_tiles_argmax(P, flow_amt(P, e - 1), ntiles, (int)((uint32_t)(e - 1) * (uint32_t)TAGL) + TAG_LM, slots);
+      __syncthreads();
+      if (tid() == 0) {
+        const int i = flow_tiles_combine(slots);
+        const int tok = i < 0 || i >= P.V ? 0 : i;
+        if (w == 0) flow_record_step(P, slots, i, pos - 1);
+        slots[0] = tok;
+        slots[1] = slots[4] && tok == slots[3];
+      }
+      __syncthreads();
+      done = slots[1] != 0;
+      __syncthreads();  // slot 1 is written again only at the next step's resolve
+      pending = false;
+    }
+  }
   template <int SLEEP = 0>
   __device__ bool wait(const int *f0, int n0, const int *f1 = nullptr, int n1 = 0, const int *f2 = nullptr,
                        int n2 = 0) {
-    if (pending) {
-      flow_wait<SLEEP>(P, am_flag, 1, nullptr, 0, nullptr, 0, e - 1);
-      pending = false;
-      done = st_ld(P, ST_OFF(done)) != 0;
-    }
     if (done) return true;
     if (n0 + n1 + n2) flow_wait<SLEEP>(P, f0, n0, f1, n1, f2, n2, e);
     return false;
@@ -1691,12 +1818,15 @@ struct FlowCtl {
 };
 
 // The persistent kernel's lm_head share of one workgroup (tiles wg, wg + G,
-// ...), after the final norm it forms itself.  Returns true when this
-// workgroup computed at least one tile.
+// ...).  Workgroup 0 (pub) forms the final norm and publishes its records;
+// the others load them.  Returns true when this workgroup computed at least
+// one tile.
 template <class W>
-__device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, const Step &st, float *smem, W &&wait) {
-  if (wg >= L.ntiles) return false;
-  const int D = P.D, ng = D >> 5;
+__device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, const Step &st, float *smem, bool pub,
+                        W &&wait) {
+  if (wg >= L.ntiles && !pub) return false;
+  const int D = P.D, ng = D >> 5, nrec = ng * Q6R;
+  const int ftag = st.tag + P.L;  // the final norm's records
   TileRegs<FTC> Ra, Rb;
   int tile = wg;
   lm_load<FTC, FLT>(P, L, tile, Ra);
@@ -1707,23 +1837,46 @@ __device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, co
   s.out = s.part + FTC * FLT;
   s.lists = reinterpret_cast<int *>(s.out + L.rpt);
   float *blk = reinterpret_cast<float *>(s.lists + 34 + P.max_seq);
-  const float *rbias = P.arch == 1 ? P.last_mproj_b : nullptr;
-  GainsReg GR;
-  gains_load(P, P.norm_f, rbias, GR);
-  gains_store(P, rbias, GR, gl);
+  if (pub) {
+    const float *rbias = P.arch == 1 ? P.last_mproj_b : nullptr;
+    GainsReg GR;
+    gains_load(P, P.norm_f, rbias, GR);
+    gains_store(P, rbias, GR, gl);
+  }
   if (wait()) return false;
   const bool penal = P.arch == 1 && st_ld(P, ST_OFF(chain)) != 0;
   if (penal && tid() == 0) gpt2_lists(P, s.lists);
-  final_row<2>(P, 0, blk, gl, s.qx, false, st.tag + P.L - 1);
+  if (pub) {
+    final_row<2>(P, 0, blk, gl, s.qx, false, st.tag + P.L - 1);
+    __syncthreads();
+    for (int i = tid(); i < nrec; i += FLT) coh_st8(P.rec, (uint32_t)i * 8u, tag_pair(s.qx[i], ftag));
+  } else {
+    // the records, two tagged pairs per 16-byte load (nrec is even)
+    const int i = min((int)tid(), (nrec >> 1) - 1);
+    uint4 u = coh_ld16(P.rec, 16u * (uint32_t)i);
+    if ((int)tid() < (nrec >> 1)) {
+      for (unsigned spins = 1; !(pair_ok(make_uint2(u.x, u.y), ftag) && pair_ok(make_uint2(u.z, u.w), ftag)) &&
+                               !poll_give_up(P, spins);
+           ++spins) {
+        poll_fence();
+        u = coh_ld16(P.rec, 16u * (uint32_t)i);
+      }
+      s.qx[2 * i] = u.x;
+      s.qx[2 * i + 1] = u.z;
+    }
+  }
   __syncthreads();
-  const int nban = penal ? s.lists[0] : 0, nrec = penal ? s.lists[1] : 0;
+  if (tile >= L.ntiles) return false;
+  const int nban = penal ? s.lists[0] : 0, nrc = penal ? s.lists[1] : 0;
+  const int amtag = st.tag + TAG_LM;
+  uint2 *const amt = flow_amt(P, (int)((uint32_t)st.tag / TAGL));
   while (tile < L.ntiles) {
     lm_load<FTC, FLT>(P, L, tile + nwg, Rb);
-    lm_tile<FTC, FLT>(P, L, Ra, tile, 0, 1, s, penal, nban, nrec);
+    lm_tile<FTC, FLT>(P, L, Ra, tile, 0, 1, s, penal, nban, nrc, amt, amtag);
     tile += nwg;
     if (tile >= L.ntiles) break;
     lm_load<FTC, FLT>(P, L, tile + nwg, Ra);
-    lm_tile<FTC, FLT>(P, L, Rb, tile, 0, 1, s, penal, nban, nrec);
+    lm_tile<FTC, FLT>(P, L, Rb, tile, 0, 1, s, penal, nban, nrc, amt, amtag);
     tile += nwg;
   }
   return true;
@@ -1738,15 +1891,28 @@ __global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   const int w = blockIdx.x, G = gridDim.x;
   const int stride = P.NH + F.nm;
-  int *const lm_cnt = F.flags + P.L * stride;
-  int *const am_flag = lm_cnt + 1;
   const int nlm = min(G, F.lm_tiles);  // workgroups with lm_head tiles
   const LmGeom lg{F.lm_rpt, F.lm_tiles};
   const int pos_start = st_ld(P, ST_OFF(pos0));
-  int *const red = reinterpret_cast<int *>(smem);
+  int *const slots = flow_slots(smem, F.kvp);
   if (wave_id() == 1 || wave_id() == 2) *kv_slot(smem, F.kvp) = kv_pad(P);  // no deferred K/V row yet
+  if (tid() == 0) {
+    slots[0] = min(max(st_ld(P, ST_OFF(tok)), 0), P.V - 1);  // the first step's input token
+    slots[1] = 0;
+    slots[2] = st_ld(P, ST_OFF(n_hist));
+    slots[3] = st_ld(P, ST_OFF(eos));
+    slots[4] = st_ld(P, ST_OFF(chain));
+  }
+  __syncthreads();
+  if (w >= F.ni && w >= nlm && w != 0) return;  // no item and no lm_head tile in any step
+  bool stopped = false;
   for (int step = 0; step < F.steps; ++step) {
-    FlowCtl C{P, am_flag, F.ep0 + step, step > 0, false};
+    FlowCtl C{P, slots, w, F.lm_tiles, F.ep0 + step, pos_start + step, step > 0, false};
+    C.resolve();
+    if (C.done) {
+      stopped = true;
+      break;
+    }
     const int e = C.e;
     const Step st{pos_start + step, false, (int)((uint32_t)e * (uint32_t)TAGL)};
     for (int lv = 0; lv < P.L && !C.done; ++lv) {
@@ -1761,8 +1927,8 @@ __global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
         int j = jv;
         asm volatile("" : "+s"(j));
         // items poll their inputs' tags (the previous layer's residual and
-        // down partials, or this layer's attention partials); the waits
-        // below only take the step's ARGMAX and `done`
+        // down partials, or this layer's attention partials); the step's
+        // token and `done` were taken at its top (resolve)
         if (j < F.na) {
           phase_attn1<true, AQC>(P, Lw, li, j, st, smem, [&] { return C.wait(nullptr, 0); }, F.kvp);
         } else {
@@ -1774,7 +1940,7 @@ __global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
         }
       }
     }
-    if (!C.done && w < nlm) {
+    if (!C.done && (w < nlm || w == 0)) {
       // the lm_head waits through the whole layer stack: first slowly on
       // earlier layers, then closely on the last one
       if (P.L > 4) {
@@ -1782,27 +1948,19 @@ __global__ __launch_bounds__(FLT) void k_flow(DecParams P, FlowGeom F) {
         C.wait<16>(F.flags + (P.L - 2) * stride + P.NH, F.nm);
       }
       const int *dep = F.flags + (P.L - 1) * stride + P.NH;
-      const bool did = flow_lm(P, lg, w, G, st, smem, [&] { return C.wait(dep, F.nm); });
-      if (did && !C.done) {
-        // the last lm_head workgroup to finish takes the argmax
-        wait_stores();
-        __syncthreads();
-        if (tid() == 0) {
-          const int arrived = atomicAdd(lm_cnt, 1);
-          red[0] = arrived == nlm - 1;
-          if (red[0]) __hip_atomic_store(lm_cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (red[0]) {
-          __syncthreads();
-          phase_argmax<FLT>(P, F.lm_tiles, st, smem);
-          flow_publish(am_flag, e);
-        }
-      }
+      // workgroup 0 polls the last layer's data itself; the others wait for
+      // its flags, then for the published records
+      flow_lm(P, lg, w, G, st, smem, w == 0, [&] { return C.wait(dep, w == 0 ? 0 : F.nm); });
     }
-    if (C.done) break;
   }
   kv_flush(P, smem, F.kvp);
+  if (!stopped && w == 0) {
+    // the last step's token, for the host
+    const uint32_t e = (uint32_t)(F.ep0 + F.steps - 1);
+    if (wave_id() < AMW) flow_tiles_argmax(P, flow_amt(P, (int)e), F.lm_tiles, (int)(e * (uint32_t)TAGL) + TAG_LM, slots);
+    __syncthreads();
+    if (tid() == 0) flow_record_step(P, slots, flow_tiles_combine(slots), pos_start + F.steps - 1);
+  }
 }
 
 // ---------------------------------------------------------------- verify step
@@ -2352,8 +2510,7 @@ __global__ __launch_bounds__(FLT) void k_flowm(DecParams P, FlowGeom F) {
   const int nlm = min(G, F.lm_tiles);
   const LmGeom lg{F.lm_rpt, F.lm_tiles};
   int *const red = reinterpret_cast<int *>(smem);
-  FlowCtl C{P, am_flag, F.ep0, false, false};
-  const int e = C.e;
+  const int e = F.ep0;
   const Step st{st_ld(P, ST_OFF(pos0)), false, (int)((uint32_t)e * (uint32_t)TAGL)};
   const int nrh = P.NH + 2 * P.NKV;
   const int ngq = (m + F.tq - 1) / F.tq, nga = (m + F.ta - 1) / F.ta, ngm = (m + F.mt - 1) / F.mt;  // token groups
@@ -2393,8 +2550,8 @@ __global__ __launch_bounds__(FLT) void k_flowm(DecParams P, FlowGeom F) {
   }
   if (w < nlm) {
     if (P.L > 4) {
-      C.wait<127>(F.flags + (P.L - 4) * stride + P.NH, F.nm);
-      C.wait<16>(F.flags + (P.L - 2) * stride + P.NH, F.nm);
+      flow_wait<127>(P, F.flags + (P.L - 4) * stride + P.NH, F.nm, nullptr, 0, nullptr, 0, e);
+      flow_wait<16>(P, F.flags + (P.L - 2) * stride + P.NH, F.nm, nullptr, 0, nullptr, 0, e);
     }
     __syncthreads();
     if (flowm_lm(P, lg, w, G, st, m, F.fuse, smem)) {
@@ -2971,6 +3128,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   if (!rc) rc = dev_alloc(M, (void **)&M->d_logits, sizeof(float) * MAXT * (size_t)V);
   if (!rc) rc = dev_alloc(M, (void **)&P.amv, sizeof(float) * MAXT * P.lm_tiles);
   if (!rc) rc = dev_alloc(M, (void **)&P.ami, sizeof(int) * MAXT * P.lm_tiles);
+  if (!rc) rc = dev_alloc(M, (void **)&P.amt, sizeof(uint2) * 4 * P.lm_tiles);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_hist, sizeof(int) * (c.max_seq_len + 1));
   if (!rc) rc = dev_alloc(M, (void **)&M->d_st, sizeof(PassState));
   if (!rc) rc = dev_alloc(M, (void **)&M->d_gemv_x, sizeof(float) * std::max(FF, D) * 4);
@@ -2982,6 +3140,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       hipMemset(P.xa, 0, tagged_bytes[0]) != hipSuccess || hipMemset(P.xb, 0, tagged_bytes[1]) != hipSuccess ||
       hipMemset(P.opart, 0, tagged_bytes[2]) != hipSuccess || hipMemset(P.dpart, 0, tagged_bytes[3]) != hipSuccess ||
       hipMemset(P.cnt, 0, sizeof(unsigned) * MAXT * NH) != hipSuccess ||
+      hipMemset(P.amt, 0, sizeof(uint2) * 4 * P.lm_tiles) != hipSuccess ||
       hipMemset(P.rec, 0, sizeof(uint2) * 2 * MAXT * ngd * Q6R) != hipSuccess ||
       hipMemset(P.qkvr, 0, sizeof(uint2) * L * MAXT * (NH + 2 * NKV) * HD) != hipSuccess ||
       hipMemset(P.kv, 0, kv_elems * (c.kv_fp16 ? 2 : 4)) != hipSuccess)
@@ -3065,7 +3224,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
     F.lm_rpt = std::min(V, std::max(1, (FTC * FLT) / ngd));
     F.lm_tiles = (V + F.lm_rpt - 1) / F.lm_rpt;
     F.kvp = (int)al4(flow_lds_bytes(P, F) / sizeof(float));
-    M->flow_lds = ((size_t)F.kvp + 2 * 128) * sizeof(float);  // + the deferred K/V-row slots
+    M->flow_lds = ((size_t)F.kvp + 2 * 128 + 24) * sizeof(float);  // + the deferred K/V-row slots and flow_slots
     int per_cu = 0;
     const bool lds_ok = M->flow_lds <= lds_cap &&
                         (M->flow_lds <= 64 * 1024 ||
