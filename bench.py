@@ -341,7 +341,11 @@ def graph_us(torch, enqueue, n_launch, replays=5):
     return round(us, 3)
 
 
-def bench_gemv(torch, abi, pgw, oracle=None):
+def bench_gemv(torch, abi, pgw, oracle=None, quick=False):
+    """Config 2's sweep.  quick: 20 warm launches, 40 cold ones over 40
+    copies, 10 stacked ones and no graph replays -- for counter runs, where
+    every launch is serialised and sampled (the per-launch counters do not
+    depend on the repetition count)."""
     shapes = [(960, 960), (320, 960), (2560, 960), (960, 2560), (49152, 960)]
     stream = torch.cuda.current_stream()
     sp = C.c_void_p(stream.cuda_stream)
@@ -353,6 +357,8 @@ def bench_gemv(torch, abi, pgw, oracle=None):
             sbytes = m * (n // 32) * 4
             algo = wbytes + sbytes + 4 * n + 4 * m
             copies = max(4, math.ceil((1 << 30) / (wbytes + sbytes)))
+            if quick:
+                copies = min(copies, 40)
             W = torch.randint(0, 256, (copies, wbytes), dtype=torch.uint8, device="cuda")
             S = torch.empty((copies, sbytes // 4), dtype=torch.float32, device="cuda").uniform_(1e-3, 1e-2)
             x = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).cuda()
@@ -370,6 +376,8 @@ def bench_gemv(torch, abi, pgw, oracle=None):
             res = {"fmt": fmt, "shape": [m, n], "bytes": algo}
             for mode in ("warm", "cold"):
                 reps = 200 if mode == "warm" else max(200, copies)  # cold: every copy once, >= 1 GiB
+                if quick:
+                    reps = 20 if mode == "warm" else copies
                 for i in range(10):
                     launch(0 if mode == "warm" else i % copies)
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -383,8 +391,9 @@ def bench_gemv(torch, abi, pgw, oracle=None):
                 res[f"{mode}_gbs"] = round(algo / us / 1e3, 1)
             # the cold launches again, replayed from a captured graph: kernel
             # time without the host's per-call cost (ctypes, launch)
-            res["cold_graph_us"] = graph_us(torch, lambda s: [launch(i % copies, s) for i in range(reps)], reps)
-            res["cold_graph_gbs"] = round(algo / res["cold_graph_us"] / 1e3, 1)
+            if not quick:
+                res["cold_graph_us"] = graph_us(torch, lambda s: [launch(i % copies, s) for i in range(reps)], reps)
+                res["cold_graph_gbs"] = round(algo / res["cold_graph_us"] / 1e3, 1)
             if fmt == "q4":
                 # layer-stacked: 32 distinct matrices per launch
                 cnt = 32
@@ -398,7 +407,7 @@ def bench_gemv(torch, abi, pgw, oracle=None):
                     ys = torch.empty((cnt, m), dtype=torch.float32, device="cuda")
                     ty = torch.tensor([ys[j].data_ptr() for j in range(cnt)], dtype=torch.int64, device="cuda")
                     tabs.append((tp, ts, tx, ty, ys))
-                reps = 100
+                reps = 10 if quick else 100
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 for i in range(3):
                     tp, ts, tx, ty, _ = tabs[i % len(tabs)]
@@ -420,8 +429,9 @@ def bench_gemv(torch, abi, pgw, oracle=None):
                         tp, ts, tx, ty, _ = tabs[i % len(tabs)]
                         abi.check("batched", abi.lib().mllm_gemv_q4_batched(cnt, m, n, tp.data_ptr(), ts.data_ptr(),
                                                                             tx.data_ptr(), ty.data_ptr(), s))
-                res["stacked32_graph_us"] = graph_us(torch, stacked, reps)
-                res["stacked32_graph_gbs"] = round(cnt * algo / res["stacked32_graph_us"] / 1e3, 1)
+                if not quick:
+                    res["stacked32_graph_us"] = graph_us(torch, stacked, reps)
+                    res["stacked32_graph_gbs"] = round(cnt * algo / res["stacked32_graph_us"] / 1e3, 1)
                 del tabs
             res["cold_frac_hbm"] = round(res["cold_gbs"] / HBM_PEAK_GBS, 4)
             if fmt == "q4" and oracle is not None:
@@ -595,6 +605,8 @@ def main():
     ap.add_argument("--prefill-only", action="store_true", help="config 5's prompt, batched, three times")
     ap.add_argument("--sweep-only", action="store_true",
                     help="only the Q4 / Q8 GEMV sweep (config 2), no decode and no cooperative launch")
+    ap.add_argument("--sweep-quick", action="store_true",
+                    help="the sweep with few launches per shape and no graph replays (counter runs)")
     ap.add_argument("--verify-only", action="store_true",
                     help="only config 3's verify passes at M = 1, 5, 9 (and the batched path at M = 5, 9)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -621,8 +633,8 @@ def main():
     if args.copy_calibration:
         copy_calibration(torch)
         return
-    if args.sweep_only:
-        print(json.dumps({"gemv_sweep": bench_gemv(torch, abi, pgw)}))
+    if args.sweep_only or args.sweep_quick:
+        print(json.dumps({"gemv_sweep": bench_gemv(torch, abi, pgw, quick=args.sweep_quick)}))
         return
     if args.verify_only:
         print(json.dumps(bench_verify(mllm, pgw, args)))

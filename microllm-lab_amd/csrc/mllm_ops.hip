@@ -51,11 +51,13 @@ extern "C" int mllm_kernel_version(void) { return 1; }
 // record and the loads of a pass are contiguous across the workgroup; the
 // row sums go through LDS in a fixed order that depends only on ng.
 constexpr int GX_BATCH = 4;          // float4s of x per thread loaded ahead of the weights
-// The weights are loaded with the non-temporal policy: every byte of a matrix
-// is read once per launch, so its lines need not displace what the caches
-// hold (x, the scales, the other launches' data).  Measured on the lm_head
-// shape: 8.06 -> 7.78 us cold, 75% -> 83% of HBM peak when 32 matrices share
-// a launch.
+// The Q4 weights are loaded with the non-temporal policy: every byte of a
+// matrix is read once per launch, so its lines need not displace what the
+// caches hold (x, the scales, the other launches' data).  Measured on the
+// lm_head shape: 8.06 -> 7.78 us cold, 75% -> 83% of HBM peak when 32
+// matrices share a launch.  The Q8 weights keep the default policy: with
+// twice the bytes per group, the same change made the Q8 lm_head slower
+// (10.9 -> 12.0 us cold).
 constexpr int CP_NT = 2;             // cache-policy operand: non-temporal
 
 // x through buffer loads, like the weights: vector-memory loads of one kind
@@ -383,8 +385,8 @@ __device__ __forceinline__ void q8_gemv_tile(const int8_t *__restrict__ q, const
   for (int p = 0; p < P; ++p) {
     const int row = min(row0 + p * G.rpp + rr, last);
     const uint32_t c = (uint32_t)(row * ng + g);
-    wa[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(c * 32), 0, CP_NT));
-    wb[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(c * 32 + 16), 0, CP_NT));
+    wa[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(c * 32), 0, 0));
+    wb[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(c * 32 + 16), 0, 0));
     s[p] = PERROW ? 1.f : __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(c * 4), 0, 0));
     __builtin_amdgcn_sched_barrier(0);  // chunk p's loads before chunk p + 1's
   }
