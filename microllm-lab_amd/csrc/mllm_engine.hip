@@ -844,39 +844,44 @@ __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, i
   const int kp = tid() >> 2, ku = tid() & 3;
   const int lane = lane_id(), wv = wave_id();
   __syncthreads();
-  float part = 0.f;
-  if (kp < cnt) {
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    const float *qq = A.qs + 16 * ku;
-    const bool nk = kp == knew;
+  // A wave whose 16 keys all lie past the split's end skips the arithmetic:
+  // its maximum -inf, sum +0 and P.V +0 are what the arithmetic gives it (no
+  // score, every weight 0), and it leaves the SIMDs to the waves with keys.
+  float mw = -INFINITY, lw = 0.f, acc = 0.f;
+  if (16 * wv < cnt) {
+    float part = 0.f;
+    if (kp < cnt) {
+      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+      const float *qq = A.qs + 16 * ku;
+      const bool nk = kp == knew;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float4 kk = nk ? reinterpret_cast<const float4 *>(kvn)[4 * ku + j] : kr[j];
-      a0 = __builtin_fmaf(qq[4 * j + 0], kk.x, a0);
-      a1 = __builtin_fmaf(qq[4 * j + 1], kk.y, a1);
-      a2 = __builtin_fmaf(qq[4 * j + 2], kk.z, a2);
-      a3 = __builtin_fmaf(qq[4 * j + 3], kk.w, a3);
+      for (int j = 0; j < 4; ++j) {
+        const float4 kk = nk ? reinterpret_cast<const float4 *>(kvn)[4 * ku + j] : kr[j];
+        a0 = __builtin_fmaf(qq[4 * j + 0], kk.x, a0);
+        a1 = __builtin_fmaf(qq[4 * j + 1], kk.y, a1);
+        a2 = __builtin_fmaf(qq[4 * j + 2], kk.z, a2);
+        a3 = __builtin_fmaf(qq[4 * j + 3], kk.w, a3);
+      }
+      part = (a0 + a1) + (a2 + a3);
     }
-    part = (a0 + a1) + (a2 + a3);
-  }
-  // the four quarters: (q0 + q1) + (q2 + q3) in every lane of the quad
-  part = part + dpp_f<0xB1>(part);
-  part = part + dpp_f<0x4E>(part);
-  const float score = kp < cnt ? part * P.attn_scale : -INFINITY;
-  // the wave's 16 keys: maximum, weights, their sum and P.V (lane = dimension)
-  const float mw = wave_max(score);  // -inf in a wave with no key
-  const float e = kp < cnt ? expf(score - mw) : 0.f;
-  const float lw = wave_sum(ku == 0 ? e : 0.f);
-  // branch-free: the new key's value is read from LDS once, and selected
-  const float vnew = kvn[HD + lane];
-  float acc = 0.f;
+    // the four quarters: (q0 + q1) + (q2 + q3) in every lane of the quad
+    part = part + dpp_f<0xB1>(part);
+    part = part + dpp_f<0x4E>(part);
+    const float score = kp < cnt ? part * P.attn_scale : -INFINITY;
+    // the wave's 16 keys: maximum, weights, their sum and P.V (lane = dimension)
+    mw = wave_max(score);
+    const float e = kp < cnt ? expf(score - mw) : 0.f;
+    lw = wave_sum(ku == 0 ? e : 0.f);
+    // branch-free: the new key's value is read from LDS once, and selected
+    const float vnew = kvn[HD + lane];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int key = 16 * wv + k;
-    const float ek = readlane_f(e, 4 * k);
-    float vv = key == knew ? vnew : vr[k];
-    vv = key < cnt ? vv : 0.f;
-    acc = __builtin_fmaf(ek, vv, acc);
+    for (int k = 0; k < 16; ++k) {
+      const int key = 16 * wv + k;
+      const float ek = readlane_f(e, 4 * k);
+      float vv = key == knew ? vnew : vr[k];
+      vv = key < cnt ? vv : 0.f;
+      acc = __builtin_fmaf(ek, vv, acc);
+    }
   }
   A.wacc[wv * HD + lane] = acc;
   if (lane == 0) {
