@@ -2060,7 +2060,7 @@ __device__ __forceinline__ void resid_norm(const DecParams &P, int li, int t, in
     const uint2 *brow = (side ? P.xa : P.xb) + (size_t)t * D;
     const uint2 *prow = side ? P.opart + (size_t)t * P.NH * D : P.dpart + (size_t)t * P.nchunk * D;
     const float4 base = col_base_load<true>(P, brow, nq, want);
-    resid_blocks<true>(P, prow, np, want, blk);
+    resid_blocks<1, true>(P, prow, np, want, blk);
     __syncthreads();
     x = col_finish(blk, nq, np, base, gl, D, rbias != nullptr);
   }
