@@ -115,13 +115,6 @@ def measured_traffic(kernel):
     return None if rec is None else rec.get("hbm_bytes_per_launch")
 
 
-def flow_kernel_name(cfg):
-    """Template instance of the persistent kernel the engine picks for cfg
-    (chunk registers of the fused attention item: ceil(3 * 64 * D/32 / 1024),
-    at least 4)."""
-    return f"k_flow<{max(4, -(-3 * 64 * (cfg.d_model // 32) // 1024))}>"
-
-
 def copy_calibration(torch):
     """A plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE."""
     n = 256 << 20
@@ -142,6 +135,7 @@ def bench_decode(mllm, pgw, torch, args):
     prompt = [int(v) for v in np.random.default_rng(1).integers(0, cfg.vocab_size, 32)]
     g = mllm.PetitGPT(bundle, exec_mode=args.exec_mode)
     mode = g.execMode  # the mode the engine really uses (a refused cooperative launch falls back to 1)
+    kname = g.decodeKernel  # the kernel the engine really runs the decode step with
     # warmup: W chained steps after a prefill
     g.resetCache()
     g.forwardPrompt(prompt)
@@ -176,7 +170,6 @@ def bench_decode(mllm, pgw, torch, args):
     if mode >= 3:
         # one k_flow launch ran the whole timed chain: step i attends over
         # len(prompt) + 1 + i cached positions
-        kname = flow_kernel_name(cfg)
         chain_bytes = sum(token_bytes(cfg, len(prompt) + 1 + i) for i in range(args.steps))
         achieved = chain_bytes / (gpu_ms * 1e-3) / 1e9
         rec = traffic_record(kname)

@@ -212,6 +212,11 @@ int mllm_set_exec_mode(mllm_model *model, int mode);
  * 1); -1 for a null model. */
 int mllm_get_exec_mode(const mllm_model *model);
 
+/* No reference counterpart: the name of the kernel that runs the next decode
+ * step ("k_flow3", "k_flow<4>" ... in exec modes 3 and 4, "phase kernels" in
+ * modes 1 and 2), for reports; "" for a null model. */
+const char *mllm_decode_kernel_name(const mllm_model *model);
+
 /* No reference counterpart: the most tokens a verify pass (mllm_forward_verify)
  * runs as one step of the persistent kernel in exec modes 3 and 4; longer
  * passes, and every pass in modes 1 and 2, run the phase kernels (the same

@@ -2037,8 +2037,7 @@ __device__ __forceinline__ uint2 *rec_row(const DecParams &P, int side, int t) {
 // barriers); the records are complete after the caller's next barrier.
 __host__ __device__ inline size_t norm_scratch(size_t D, size_t nbd) { return al4(3 * D) + nbd * D + 32; }
 __device__ __forceinline__ void resid_norm(const DecParams &P, int li, int t, int side, const Step &st, float *scratch,
-                                           uint32_t *qx,
-                           bool write_x) {
+                                           uint32_t *qx, bool write_x, int tok_in = -1) {
   const int D = P.D, nq = D >> 2;
   const bool gpt2 = P.arch == 1, fin = li == P.L;
   const LayerW &Lw = P.layers[min(li, P.L - 1)];
@@ -2053,7 +2052,8 @@ __device__ __forceinline__ void resid_norm(const DecParams &P, int li, int t, in
   gains_store(P, rbias, GR, gl);
   float4 x;
   if (side == 0 && li == 0) {
-    const int tok = min(max(st_ld(P, ST_OFF(tok) + 4u * t), 0), P.V - 1);
+    // tok_in: the chained kernel's token (taken at the step's top)
+    const int tok = tok_in >= 0 ? tok_in : min(max(st_ld(P, ST_OFF(tok) + 4u * t), 0), P.V - 1);
     x = embed_col(P, tok, min(st.pos0 + t, P.max_seq - 1));
     __syncthreads();
   } else {
@@ -2086,7 +2086,7 @@ __device__ void flowm_norm(const DecParams &P, int li, int t, int side, const St
 // also to the cache.  nt <= VQT.
 constexpr int VQT = 8;  // tokens per QKV item at most (its LDS)
 __device__ void flowm_qkv(const DecParams &P, const LayerW &Lw, int li, int rh, int t0, int nt, const Step &st,
-                          bool fused, float *smem) {
+                          bool fused, float *smem, int tok_in = -1) {
   const int D = P.D, ng = D >> 5, nch = HD * ng;
   const int nrow = (P.NH + 2 * P.NKV) * HD;
   const bool gpt2 = P.arch == 1;
@@ -2110,7 +2110,7 @@ __device__ void flowm_qkv(const DecParams &P, const LayerW &Lw, int li, int rh, 
   if (fused) {
     // each token's residual and norm here (the row head 0 item writes xa)
     float *scratch = rt + al4(nt * 2 * HD);
-    for (int tt = 0; tt < nt; ++tt) resid_norm(P, li, t0 + tt, 0, st, scratch, qx + tt * ng * Q6R, rh == 0);
+    for (int tt = 0; tt < nt; ++tt) resid_norm(P, li, t0 + tt, 0, st, scratch, qx + tt * ng * Q6R, rh == 0, tok_in);
   } else {
     rec_get(P, rec_row(P, 0, t0), nt * ng * Q6R, st.tag + li, qx);
   }
@@ -2577,8 +2577,94 @@ __global__ __launch_bounds__(FLT) void k_flowm(DecParams P, FlowGeom F) {
   }
 }
 
+// The chained decode step in three stages per layer (the verify step's fused
+// items at one row): QKV items (row head: 64 rows of attn.qkv, each forming
+// the token's residual and norm; row head 0 writes the residual row),
+// attention items (split, head) that read the q/k/v rows from P.qkvr, and
+// the MLP items; then k_flow's lm_head share and step handoffs.  Every row
+// head's rows are formed once, where k_flow's attention items each form
+// their query head's and their K/V head's rows; that costs a handoff per
+// layer and pays where the rows are many (d_model 960) or the splits are (a
+// head's split items each form its rows).  Each QKV item first waits for
+// its workgroup's earlier stores: the K/V cache row of the previous layer
+// (or step) is then complete before the workgroup's next tagged output, on
+// which every later reader of that row depends.  The arithmetic is the
+// verify step's, so the rows are bit for bit k_flow's.
+__global__ __launch_bounds__(FLT) void k_flow3(DecParams P, FlowGeom F) {
+  extern __shared__ float4 smem4[];
+  float *smem = reinterpret_cast<float *>(smem4);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // as in k_flow: no stale cache lines of the KV cache
+  const int w = blockIdx.x, G = gridDim.x;
+  const int stride = P.NH + F.nm;
+  const int nlm = min(G, F.lm_tiles);
+  const LmGeom lg{F.lm_rpt, F.lm_tiles};
+  const int nrh = P.NH + 2 * P.NKV;
+  const int ia = nrh, im = ia + F.na, ni = im + F.nm;  // items per layer: QKV | attention | MLP
+  const int pos_start = st_ld(P, ST_OFF(pos0));
+  int *const slots = flow_slots(smem, F.kvp);
+  if (tid() == 0) {
+    slots[0] = min(max(st_ld(P, ST_OFF(tok)), 0), P.V - 1);
+    slots[1] = 0;
+    slots[2] = st_ld(P, ST_OFF(n_hist));
+    slots[3] = st_ld(P, ST_OFF(eos));
+    slots[4] = st_ld(P, ST_OFF(chain));
+  }
+  __syncthreads();
+  if (w >= ni && w >= nlm && w != 0) return;  // no item and no lm_head tile in any step
+  bool stopped = false;
+  for (int step = 0; step < F.steps; ++step) {
+    FlowCtl C{P, slots, w, F.lm_tiles, F.ep0 + step, pos_start + step, step > 0, false};
+    C.resolve();
+    if (C.done) {
+      stopped = true;
+      break;
+    }
+    const int e = C.e;
+    const Step st{pos_start + step, false, (int)((uint32_t)e * (uint32_t)TAGL)};
+    const int tok = slots[0];
+    for (int lv = 0; lv < P.L; ++lv) {
+      int li = lv;
+      asm volatile("" : "+s"(li));
+      const LayerW &Lw = P.layers[li];
+      int *const fl = F.flags + li * stride;
+      for (int jv = w; jv < ni; jv += G) {
+        int j = jv;
+        asm volatile("" : "+s"(j));
+        __syncthreads();  // the previous item's LDS is free
+        if (j < ia) {
+          wait_stores();
+          flowm_qkv(P, Lw, li, j, 0, 1, st, true, smem, tok);
+        } else if (j < im) {
+          flowm_attn(P, Lw, li, j - ia, 0, 1, st, 1, smem);
+        } else {
+          const int it = j - im;
+          flowm_mlp(P, Lw, li, it, st, 0, 1, true, smem);
+          if (tid() == 0) flag_st(fl + P.NH + it, e);  // the lm_head's coarse waits
+        }
+      }
+    }
+    if (w < nlm || w == 0) {
+      __syncthreads();  // the last item's LDS is free
+      if (P.L > 4) {
+        C.wait<127>(F.flags + (P.L - 4) * stride + P.NH, F.nm);
+        C.wait<16>(F.flags + (P.L - 2) * stride + P.NH, F.nm);
+      }
+      const int *dep = F.flags + (P.L - 1) * stride + P.NH;
+      flow_lm(P, lg, w, G, st, smem, w == 0, [&] { return C.wait(dep, w == 0 ? 0 : F.nm); });
+    }
+    __syncthreads();  // the slots are read before the next step's resolve writes them
+  }
+  if (!stopped && w == 0) {
+    const uint32_t e = (uint32_t)(F.ep0 + F.steps - 1);
+    if (wave_id() < AMW) flow_tiles_argmax(P, flow_amt(P, (int)e), F.lm_tiles, (int)(e * (uint32_t)TAGL) + TAG_LM, slots);
+    __syncthreads();
+    if (tid() == 0) flow_record_step(P, slots, flow_tiles_combine(slots), pos_start + F.steps - 1);
+  }
+}
+
 using FlowKernel = void (*)(DecParams, FlowGeom);
 static const FlowKernel kFlowKernels[3] = {k_flow<4>, k_flow<5>, k_flow<6>};
+
 
 
 }  // namespace mllm
@@ -2618,6 +2704,8 @@ struct mllm_model {
   FlowGeom flow{};
   int flow_grid = 0;      // 0: not available on this device
   int flowm_max = 0;      // most tokens of a verify step in the persistent kernel (0: verify uses the phase kernels)
+  bool flow3_ok = false;  // k_flow3 is resident on the persistent grid
+  int flow3_policy = 1;   // the decode step's kernel: 0 k_flow, 1 k_flow3, 2 by shape (MLLM_FLOW3)
   int verify_fuse = 9;    // verify steps of at most this many tokens run fused (MLLM_VERIFY_FUSE); faster at every M <= 9 measured
   size_t flowm_lds = 0;
   bool flow_default = false;  // mode 3 was chosen by default, not by mllm_set_exec_mode
@@ -2781,24 +2869,37 @@ int launch_phase(mllm_model *M, int ph, int li, int m, hipEvent_t e0 = nullptr, 
 // enqueues the phase kernels instead (same results, bit for bit).
 constexpr int kFlowFellBack = -1;
 int launch_flowm(mllm_model *M, int m, int pos0);
+// The decode step's kernel: k_flow3 (three stages per layer) whenever it is
+// resident on the persistent grid, k_flow otherwise (or with MLLM_FLOW3=0).
+// Measured chains, us per token, k_flow vs k_flow3: 135M after a 32-token
+// prompt 413.2 vs 413.5, after 512 tokens 522.0 vs 486.6; 360M after 32
+// tokens 733.3 vs 594.0, after 1536 tokens 1005.7 vs 809.3; GPT-2 124M after
+// 16 tokens 258.1 vs 245.7.  With MLLM_FLOW3=2 the choice goes by shape:
+// k_flow3 for d_model >= 960 or past the first attention split.
+bool use_flow3(const mllm_model *M, int pos) {
+  if (!M->flow3_ok || M->flow3_policy == 0) return false;
+  return M->flow3_policy == 1 || M->P.D >= 960 || pos >= ACH;
+}
+
 int launch_flow(mllm_model *M, int steps) {
   FlowGeom F = M->flow;
   F.ep0 = M->flow_epoch + 1;
   F.steps = steps;
   F.m = 1;
   void *args[] = {&M->P, &F};
+  const FlowKernel kern = use_flow3(M, M->h_st->pos0) ? k_flow3 : kFlowKernels[M->aq_idx];
   if (M->exec_mode == 4) {
     // the same kernel and grid through an ordinary launch (profilers that do
     // not follow cooperative launches): every workgroup is resident only if
     // the device runs nothing else meanwhile; a wait that times out is
     // reported as an error, as in mode 3
-    hipLaunchKernelGGL(kFlowKernels[M->aq_idx], dim3(M->flow_grid), dim3(FLT), M->flow_lds, M->stream, M->P, F);
+    hipLaunchKernelGGL(kern, dim3(M->flow_grid), dim3(FLT), M->flow_lds, M->stream, M->P, F);
     MLLM_HIP(hipGetLastError());
     M->flow_epoch += steps;
     return 0;
   }
-  const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(kFlowKernels[M->aq_idx]),
-                                                  dim3(M->flow_grid), dim3(FLT), args, M->flow_lds, M->stream);
+  const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(kern), dim3(M->flow_grid), dim3(FLT),
+                                                  args, M->flow_lds, M->stream);
   if (e == hipSuccess) {
     M->flow_epoch += steps;
     return 0;
@@ -3228,7 +3329,8 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
     F.ni = F.na + F.nm;
     F.lm_rpt = std::min(V, std::max(1, (FTC * FLT) / ngd));
     F.lm_tiles = (V + F.lm_rpt - 1) / F.lm_rpt;
-    F.kvp = (int)al4(flow_lds_bytes(P, F) / sizeof(float));
+    // one LDS layout for k_flow and k_flow3 (the verify step's items at one row)
+    F.kvp = (int)al4(std::max(flow_lds_bytes(P, F), flowm_lds_bytes(P, F, 1)) / sizeof(float));
     M->flow_lds = ((size_t)F.kvp + 2 * 128 + 24) * sizeof(float);  // + the deferred K/V-row slots and flow_slots
     int per_cu = 0;
     const bool lds_ok = M->flow_lds <= lds_cap &&
@@ -3249,6 +3351,15 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       M->flow_grid = G;
       M->exec_mode = 3;
       M->flow_default = true;
+      // the three-stage chained kernel, when it is resident on the same grid
+      const void *k3 = reinterpret_cast<const void *>(k_flow3);
+      int pc3 = 0;
+      M->flow3_ok = (M->flow_lds <= 64 * 1024 ||
+                     hipFuncSetAttribute(k3, hipFuncAttributeMaxDynamicSharedMemorySize, (int)M->flow_lds) ==
+                         hipSuccess) &&
+                    hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc3, k3, FLT, M->flow_lds) == hipSuccess &&
+                    pc3 >= per_cu;
+      if (const char *v = getenv("MLLM_FLOW3")) M->flow3_policy = atoi(v);
       // the verify kernel: the most tokens whose LDS still lets the same grid
       // be resident (one workgroup per CU)
       if (const char *v = getenv("MLLM_VERIFY_FUSE")) M->verify_fuse = atoi(v);
@@ -3328,6 +3439,13 @@ extern "C" int mllm_set_exec_mode(mllm_model *M, int mode) {
 }
 
 extern "C" int mllm_get_exec_mode(const mllm_model *M) { return M ? M->exec_mode : -1; }
+
+extern "C" const char *mllm_decode_kernel_name(const mllm_model *M) {
+  static const char *const names[3] = {"k_flow<4>", "k_flow<5>", "k_flow<6>"};
+  if (!M) return "";
+  if (M->exec_mode < 3) return "phase kernels";
+  return use_flow3(M, M->cache_len) ? "k_flow3" : names[M->aq_idx];
+}
 
 extern "C" int mllm_flow_verify_tokens(const mllm_model *M) { return M && M->exec_mode >= 3 ? M->flowm_max : 0; }
 

@@ -47,6 +47,7 @@ SIGNATURES = {
     "mllm_model_gemv": ([P, C.c_char_p, P, P], I),
     "mllm_set_exec_mode": ([P, I], I),
     "mllm_get_exec_mode": ([P], I),
+    "mllm_decode_kernel_name": ([P], C.c_char_p),
     "mllm_flow_verify_tokens": ([P], I),
     "mllm_set_prefill": ([P, I, I], I),
     "mllm_model_device_bytes": ([P], C.c_uint64),

@@ -116,6 +116,11 @@ class PetitGPT:
         return int(abi.lib().mllm_get_exec_mode(self._h))
 
     @property
+    def decodeKernel(self) -> str:
+        """The kernel that runs the next decode step (mllm_decode_kernel_name)."""
+        return abi.lib().mllm_decode_kernel_name(self._h).decode()
+
+    @property
     def flowVerifyTokens(self) -> int:
         """Most tokens a verify pass runs in the persistent kernel (0: phase kernels)."""
         return int(abi.lib().mllm_flow_verify_tokens(self._h))
