@@ -2246,28 +2246,32 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
   // most the sign of a zero sum, and the Q6 staging of the output drops it)
   for (int t = ta; t < u1; ++t) {
     const int cnt = min(ACH, pos0 + t + 1 - s0);
-    float pt = 0.f;
-    if (kp < cnt) {
-      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-      const float *qq = qrows + t * HD + 16 * ku;
+    // a wave whose keys all lie past the count skips the arithmetic (as in
+    // attn_core: -inf, +0 and +0 are what it would give)
+    float mw = -INFINITY, lw = 0.f, acc = 0.f;
+    if (16 * wv < cnt) {
+      float pt = 0.f;
+      if (kp < cnt) {
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        const float *qq = qrows + t * HD + 16 * ku;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        a0 = __builtin_fmaf(qq[4 * j + 0], kk[j].x, a0);
-        a1 = __builtin_fmaf(qq[4 * j + 1], kk[j].y, a1);
-        a2 = __builtin_fmaf(qq[4 * j + 2], kk[j].z, a2);
-        a3 = __builtin_fmaf(qq[4 * j + 3], kk[j].w, a3);
+        for (int j = 0; j < 4; ++j) {
+          a0 = __builtin_fmaf(qq[4 * j + 0], kk[j].x, a0);
+          a1 = __builtin_fmaf(qq[4 * j + 1], kk[j].y, a1);
+          a2 = __builtin_fmaf(qq[4 * j + 2], kk[j].z, a2);
+          a3 = __builtin_fmaf(qq[4 * j + 3], kk[j].w, a3);
+        }
+        pt = (a0 + a1) + (a2 + a3);
       }
-      pt = (a0 + a1) + (a2 + a3);
-    }
-    pt = pt + dpp_f<0xB1>(pt);
-    pt = pt + dpp_f<0x4E>(pt);
-    const float score = kp < cnt ? pt * P.attn_scale : -INFINITY;
-    const float mw = wave_max(score);
-    const float e = kp < cnt ? expf(score - mw) : 0.f;
-    const float lw = wave_sum(ku == 0 ? e : 0.f);
-    float acc = 0.f;
+      pt = pt + dpp_f<0xB1>(pt);
+      pt = pt + dpp_f<0x4E>(pt);
+      const float score = kp < cnt ? pt * P.attn_scale : -INFINITY;
+      mw = wave_max(score);
+      const float e = kp < cnt ? expf(score - mw) : 0.f;
+      lw = wave_sum(ku == 0 ? e : 0.f);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) acc = __builtin_fmaf(readlane_f(e, 4 * k), vs[k], acc);
+      for (int k = 0; k < 16; ++k) acc = __builtin_fmaf(readlane_f(e, 4 * k), vs[k], acc);
+    }
     wacc[(t * AW + wv) * HD + lane] = acc;
     if (lane == 0) {
       wm[t * AW + wv] = mw;
