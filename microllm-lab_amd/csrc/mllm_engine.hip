@@ -389,8 +389,13 @@ __device__ __forceinline__ float waves_sum(float v, int nw, float *red) {
     if (lane_id() == 0) red[wv] = w;
   }
   __syncthreads();
-  float t = red[0];
-  for (int k = 1; k < nw; ++k) t += red[k];
+  // the four slots read at once (red holds at least four floats; slots past
+  // nw are not added), then added in wave order
+  const float r0 = red[0], r1 = red[1], r2 = red[2], r3 = red[3];
+  float t = r0;
+  if (nw > 1) t += r1;
+  if (nw > 2) t += r2;
+  if (nw > 3) t += r3;
   return t;
 }
 
@@ -410,17 +415,17 @@ __device__ __forceinline__ void col_norm(const DecParams &P, float4 x, const flo
   const int qc = min(q, nq - 1);
   float4 y;
   if (P.arch == 1) {
+    const float4 g = g4[qc], b = g4[(D >> 2) + qc];  // read before the reductions' barriers
     const float mean = waves_sum((x.x + x.y) + (x.z + x.w), nw, red) * inv_d;
     const float4 d = in ? make_float4(x.x - mean, x.y - mean, x.z - mean, x.w - mean) : make_float4(0.f, 0.f, 0.f, 0.f);
     const float r =
         __builtin_amdgcn_rsqf(waves_sum((d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w), nw, red + 16) * inv_d + 1e-5f);
-    const float4 g = g4[qc], b = g4[(D >> 2) + qc];
     y = make_float4(__builtin_fmaf(d.x * r, g.x, b.x), __builtin_fmaf(d.y * r, g.y, b.y),
                     __builtin_fmaf(d.z * r, g.z, b.z), __builtin_fmaf(d.w * r, g.w, b.w));
   } else {
+    const float4 g = g4[qc];  // read before the reduction's barrier
     const float r = __builtin_amdgcn_rsqf(waves_sum((x.x * x.x + x.y * x.y) + (x.z * x.z + x.w * x.w), nw, red) * inv_d +
                                           P.eps);
-    const float4 g = g4[qc];
     y = make_float4(x.x * r * g.x, x.y * r * g.y, x.z * r * g.z, x.w * r * g.w);
   }
   if (!in) y = make_float4(0.f, 0.f, 0.f, 0.f);
