@@ -46,10 +46,10 @@ extern "C" int mllm_kernel_version(void) { return 1; }
 // group, mllm_device.h): one v_dot8 per 8 weights and digit plane, exact in
 // int32; a group adds (float)dot * sx * w_scale to its row.
 //
-// Work split: thread t < rpp * ng keeps group g = t % ng of rows
-// rpp * p + t / ng of its tile for p < P, so each thread reads one group
-// record and the loads of a pass are contiguous across the workgroup; the
-// row sums go through LDS in a fixed order that depends only on ng.
+// Work split (q4_gemv_tile): each row of a pass sits on one segment of L
+// lanes, lane l taking groups l, l + L, ... (K of them), so a row's sum
+// stays in registers (the lane's groups in order, then a DPP / swizzle tree
+// over the segment), in an order that depends only on ng.
 constexpr int GX_BATCH = 4;          // float4s of x per thread loaded ahead of the weights
 // The Q4 weights are loaded with the non-temporal policy: every byte of a
 // matrix is read once per launch, so its lines need not displace what the
@@ -107,19 +107,23 @@ struct RowMax {
   bool nan0 = false;
 };
 
-// One tile (P passes of rpp rows) of y = W x for m tokens.
-template <int WGT, int P, bool AMX = false>
+// One tile (P passes of rpp rows) of y = W x for m tokens.  Each row's
+// groups sit in one segment of L = G.lpr lanes (a power of two <= 64, L >=
+// ng / K): lane l of a segment takes groups l, l + L, ... (K of them), so a
+// row's sum is formed in registers, lane partials first (in group order),
+// then the DPP / swizzle tree over the segment, with no LDS pass and no
+// barrier after the dots.  The order depends only on ng (L and K follow
+// from it), so a row carries the same bits whatever the workgroup size, the
+// passes per tile or the launch (single, batched, argmax).
+template <int WGT, int P, int K, bool AMX = false>
 __device__ __forceinline__ void q4_gemv_tile(const uint8_t *__restrict__ packed, const float *__restrict__ scale,
                                              const float *__restrict__ x, float *__restrict__ y, const GemvGeom &G,
                                              int tile, uint32_t *lds, RowMax *rm = nullptr) {
-  const int ng = G.cols >> 5, nq = G.cols >> 2, nx = G.m * nq;
-  const int ngp = 4 * ((ng + 3) >> 2), RT = G.rpp * P;
-  uint32_t *rec = lds;                                          // [m][ng][Q6R]
-  float *part = reinterpret_cast<float *>(lds + G.m * ng * Q6R);  // [m][RT][ngp]
+  const int ng = G.cols >> 5, nq = G.cols >> 2, nx = G.m * nq, L = G.lpr;
+  const int RT = G.rpp * P;
+  uint32_t *rec = lds;  // [m][ng][Q6R]
   const int t = threadIdx.x;
-  const int rr0 = t / ng;
-  const bool act = rr0 < G.rpp;
-  const int rr = act ? rr0 : 0, g = act ? t - rr0 * ng : 0;
+  const int rr = t / L, l = t - rr * L;
   const int row0 = tile * RT;
   // x ahead of the weights: loads retire in order, so the staging below
   // waits for x alone while the weights are in flight
@@ -134,16 +138,19 @@ __device__ __forceinline__ void q4_gemv_tile(const uint8_t *__restrict__ packed,
                                                                       0x7fffffff, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(scale), (short)0,
                                                                       0x7fffffff, 0x00020000);
-  uint4 w[P];
-  float s[P];
+  uint4 w[P * K];
+  float s[P * K];
   const int last = G.rows - 1;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int row = min(row0 + p * G.rpp + rr, last);
-    const uint32_t c = (uint32_t)(row * ng + g);
-    w[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(c * 16), 0, CP_NT));
-    s[p] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(c * 4), 0, 0));
-    __builtin_amdgcn_sched_barrier(0);  // chunk p's loads (weights, scale) before chunk p + 1's
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const uint32_t c = (uint32_t)(row * ng + min(l + j * L, ng - 1));  // lanes past the row: a valid chunk, unused
+      w[p * K + j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(c * 16), 0, CP_NT));
+      s[p * K + j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(c * 4), 0, 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // pass p's loads (weights, scales) before pass p + 1's
   }
   x_pin(xv);
 #pragma unroll
@@ -154,67 +161,57 @@ __device__ __forceinline__ void q4_gemv_tile(const uint8_t *__restrict__ packed,
     q6_stage_col(x_ld4(rx, q < nx ? q : 0), q < nx, q, rec);
   }
   __syncthreads();
-  if (act && G.m == 1) {
-    // one token: chunk by chunk, in the loads' order, so each dot waits only
-    // for its own chunk and the dots run while later chunks stream in (inside
-    // a token loop the compiler would prepare every chunk before the first)
-    const Q6Rec xr = q6_load(rec + g * Q6R);
-    float *pp = part + rr * ngp + g;
+  const int nr = min(RT, G.rows - row0);
+  for (int tok = 0; tok < G.m; ++tok) {
+    // the lane's groups in order (group l + jL of every pass, one record in
+    // registers at a time), then each pass's segment tree
+    float acc[P];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const bool ok = l + j * L < ng;
+      const Q6Rec xr = q6_load(rec + (tok * ng + min(l + j * L, ng - 1)) * Q6R);
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const float d = q4_dot6(w[p * K + j], xr, s[p * K + j]);
+        acc[p] = j == 0 ? (ok ? d : 0.f) : (ok ? acc[p] + d : acc[p]);
+        if (K == 1) __builtin_amdgcn_sched_barrier(0);  // chunk by chunk: each dot waits only for its own loads
+      }
+    }
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-      pp[p * G.rpp * ngp] = q4_dot6(w[p], xr, s[p]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  } else if (act) {
-    for (int tok = 0; tok < G.m; ++tok) {
-      const Q6Rec xr = q6_load(rec + (tok * ng + g) * Q6R);
-      float *pp = part + (tok * RT + rr) * ngp + g;
-#pragma unroll
-      for (int p = 0; p < P; ++p) pp[p * G.rpp * ngp] = q4_dot6(w[p], xr, s[p]);
-    }
-  }
-  __syncthreads();
-  // row sums: lpr lanes per row, lane l adds float4s 4l, 4l + 4 lpr, ...
-  const int nr = min(RT, G.rows - row0);
-  for (int i = t; i < G.m * RT * G.lpr; i += WGT) {
-    const int r = i / G.lpr, l = i - r * G.lpr;
-    const int tok = r / RT, rl = r - tok * RT;
-    float a = 0.f;
-    for (int gi = 4 * l; gi < ng; gi += 4 * G.lpr) {
-      const float4 v = *reinterpret_cast<const float4 *>(part + r * ngp + gi);
-      a += ((v.x + (gi + 1 < ng ? v.y : 0.f)) + ((gi + 2 < ng ? v.z : 0.f) + (gi + 3 < ng ? v.w : 0.f)));
-    }
-    a = seg_sum(a, G.lpr);
-    if (l == 0 && rl < nr) {
-      y[tok * G.ystride + row0 + rl] = a;
-      if (AMX) {
-        const int row = row0 + rl;
-        if (amax_better(a, row, rm->v, rm->i)) {  // false for a NaN row
-          rm->v = a;
-          rm->i = row;
+      const float a = seg_sum(acc[p], L);
+      const int rl = p * G.rpp + rr;
+      if (l == 0 && rl < nr) {
+        y[tok * G.ystride + row0 + rl] = a;
+        if (AMX) {
+          const int row = row0 + rl;
+          if (amax_better(a, row, rm->v, rm->i)) {  // false for a NaN row
+            rm->v = a;
+            rm->i = row;
+          }
+          if (row == 0) rm->nan0 = a != a;
         }
-        if (row == 0) rm->nan0 = a != a;
       }
     }
   }
 }
 
-template <int WGT, int P>
+template <int WGT, int P, int K>
 __global__ __launch_bounds__(WGT) void k_gemv_q4(const uint8_t *__restrict__ packed, const float *__restrict__ scale,
                                                  const float *__restrict__ x, float *__restrict__ y, GemvGeom G) {
   extern __shared__ float4 smem4[];
-  q4_gemv_tile<WGT, P>(packed, scale, x, y, G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4));
+  q4_gemv_tile<WGT, P, K>(packed, scale, x, y, G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4));
 }
 
 // One launch over same-shape matrices: blockIdx.y selects the matrix.
-template <int WGT, int P>
+template <int WGT, int P, int K>
 __global__ __launch_bounds__(WGT) void k_gemv_q4_batched(const uint8_t *const *__restrict__ packed,
                                                          const float *const *__restrict__ scale,
                                                          const float *const *__restrict__ xv,
                                                          float *const *__restrict__ yv, GemvGeom G) {
   extern __shared__ float4 smem4[];
   const int b = blockIdx.y;
-  q4_gemv_tile<WGT, P>(packed[b], scale[b], xv[b], yv[b], G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4));
+  q4_gemv_tile<WGT, P, K>(packed[b], scale[b], xv[b], yv[b], G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4));
 }
 
 // y = W x (one token) and the first index of its maximum, in one launch
@@ -230,7 +227,7 @@ __global__ __launch_bounds__(WGT) void k_gemv_q4_batched(const uint8_t *const *_
 constexpr size_t kAmxHead = 64;
 __host__ __device__ constexpr size_t amx_scratch_bytes(int ntiles) { return kAmxHead + 8 * (size_t)ntiles; }
 
-template <int WGT, int P>
+template <int WGT, int P, int K>
 __global__ __launch_bounds__(WGT) void k_gemv_q4_argmax(const uint8_t *__restrict__ packed,
                                                         const float *__restrict__ scale, const float *__restrict__ x,
                                                         float *__restrict__ y, GemvGeom G, unsigned char *scratch,
@@ -243,7 +240,7 @@ __global__ __launch_bounds__(WGT) void k_gemv_q4_argmax(const uint8_t *__restric
   float *tv = reinterpret_cast<float *>(scratch + kAmxHead);
   int *ti = reinterpret_cast<int *>(scratch + kAmxHead + 4 * (size_t)gridDim.x);
   RowMax rm;
-  q4_gemv_tile<WGT, P, true>(packed, scale, x, y, G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4), &rm);
+  q4_gemv_tile<WGT, P, K, true>(packed, scale, x, y, G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4), &rm);
   const int t = threadIdx.x;
   float v = rm.v;
   int i = rm.i;
@@ -352,8 +349,10 @@ __device__ __forceinline__ float q8_dot3(const uint4 wa, const uint4 wb, const Q
   return ((float)dot * r.sx) * ws;
 }
 
-// One tile of y = W x (one token) for Q8 weights: q4_gemv_tile's layout and
-// row-sum order with 32-byte chunks.
+// One tile of y = W x (one token) for Q8 weights, 32-byte chunks: thread t
+// takes group t % ng of row t / ng of each pass, and the rows are summed from
+// LDS partials (lane l of a row's lpr lanes adds float4s 4l, 4l + 4 lpr, ...,
+// then a segment tree).
 template <int WGT, int P, bool PERROW>
 __device__ __forceinline__ void q8_gemv_tile(const int8_t *__restrict__ q, const float *__restrict__ scale,
                                              const float *__restrict__ x, float *__restrict__ y, const GemvGeom &G,
@@ -404,12 +403,12 @@ __device__ __forceinline__ void q8_gemv_tile(const int8_t *__restrict__ q, const
     float *pp = part + rr * ngp + g;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-      pp[p * G.rpp * ngp] = q8_dot3(wa[p], wb[p], xr, s[p]);  // chunk by chunk, as q4_gemv_tile
+      pp[p * G.rpp * ngp] = q8_dot3(wa[p], wb[p], xr, s[p]);  // chunk by chunk: each dot waits only for its own loads
       __builtin_amdgcn_sched_barrier(0);
     }
   }
   __syncthreads();
-  // row sums: q4_gemv_tile's order
+  // row sums
   const int nr = min(RT, G.rows - row0);
   for (int i = t; i < RT * G.lpr; i += WGT) {
     const int r = i / G.lpr, l = i - r * G.lpr;
@@ -522,14 +521,14 @@ struct Q4Plan {
 #endif
 long q4_target() { return (long)MLLM_Q4_WG_PER_CU * (device_wg_cap() / 8); }
 
-// Geometry of the Q4 GEMV for a shape and matrix count: workgroup size, rows
-// per pass (one group per thread), lanes per row sum.  256-thread workgroups
-// up to 256 groups per row; 512 above that, and also for long rows (>= 64
-// groups) where even one-pass tiles of 256 threads leave the launch below its
-// workgroup target: every workgroup stages all of x, and twice the rows
-// share that staging (960 x 2560 cold: 4.24 instead of 4.72 us of kernel time; at
-// 960 columns the 256-thread tiles stay faster).  The per-row arithmetic and
-// its summation order do not depend on the workgroup size.
+// Geometry of the Q8 GEMV (q8_gemv_tile) for a shape and matrix count:
+// workgroup size, rows per pass (one group per thread, a row's groups on
+// neighbouring threads), lanes per row sum of the LDS partials.  256-thread
+// workgroups up to 256 groups per row; 512 above that, and also for long rows
+// (>= 64 groups) where even one-pass tiles of 256 threads leave the launch
+// below its workgroup target: every workgroup stages all of x, and twice the
+// rows share that staging.  The per-row arithmetic and its summation order do
+// not depend on the workgroup size.
 Q4Plan q4_plan(int cols, int rows, int count) {
   const int ng = cols / 32;
   Q4Plan p;
@@ -570,23 +569,81 @@ int check_q4_shape(int m, int n, int group) {
   return 0;
 }
 
-template <int WGT, int P>
+template <int WGT, int P, int K>
 int q4_launch_one(dim3 grid, size_t lds, hipStream_t st, const uint8_t *packed, const float *scale, const float *x,
                   float *y, const GemvGeom &G) {
-  if (int rc = launch_dyn(k_gemv_q4<WGT, P>, grid, lds, st, "k_gemv_q4")) return rc;
-  hipLaunchKernelGGL((k_gemv_q4<WGT, P>), grid, dim3(WGT), lds, st, packed, scale, x, y, G);
+  if (int rc = launch_dyn(k_gemv_q4<WGT, P, K>, grid, lds, st, "k_gemv_q4")) return rc;
+  hipLaunchKernelGGL((k_gemv_q4<WGT, P, K>), grid, dim3(WGT), lds, st, packed, scale, x, y, G);
   MLLM_HIP(hipGetLastError());
   return 0;
 }
 
-template <int WGT, int P>
+template <int WGT, int P, int K>
 int q4_launch_batched(dim3 grid, size_t lds, hipStream_t st, const uint8_t *const *packed, const float *const *scale,
                       const float *const *x, float *const *y, const GemvGeom &G) {
-  if (int rc = launch_dyn(k_gemv_q4_batched<WGT, P>, grid, lds, st, "k_gemv_q4_batched")) return rc;
-  hipLaunchKernelGGL((k_gemv_q4_batched<WGT, P>), grid, dim3(WGT), lds, st, packed, scale, x, y, G);
+  if (int rc = launch_dyn(k_gemv_q4_batched<WGT, P, K>, grid, lds, st, "k_gemv_q4_batched")) return rc;
+  hipLaunchKernelGGL((k_gemv_q4_batched<WGT, P, K>), grid, dim3(WGT), lds, st, packed, scale, x, y, G);
   MLLM_HIP(hipGetLastError());
   return 0;
 }
+
+// Geometry of the Q4 GEMV (q4_gemv_tile): a row's ng groups on one segment
+// of L lanes (a power of two), K <= 8 groups per lane, rpp = wgt / L rows per
+// pass.  (L, K) wastes the fewest lane slots L K - ng; among equals, segments
+// of at most 16 lanes (reduced by DPP alone) and then the longer segment.
+// 256-thread workgroups, 512 for rows of 64 groups or more when the launch
+// still has a workgroup per CU: every workgroup stages all of x, and twice
+// the rows then share that staging (stacked 960 x 2560: 12.4 -> 11.5 us).  L
+// and K follow from ng alone, so a row's summation order does not depend on
+// the tile plan or the launch.
+struct Q4SegPlan {
+  int wgt, L, K, rpp;
+};
+Q4SegPlan q4_seg_plan(int cols, int rows, int count) {
+  const int ng = cols / 32;
+  Q4SegPlan p;
+  p.L = 64;
+  p.K = (ng + 63) / 64;  // ng <= 512: K <= 8
+  for (const int L : {32, 1, 2, 4, 8, 16}) {  // later entries win ties
+    const int K = (ng + L - 1) / L;
+    if (K <= 8 && L * K - ng <= p.L * p.K - ng) {
+      p.L = L;
+      p.K = K;
+    }
+  }
+  const long tiles512 = (long)((rows + 512 / p.L - 1) / (512 / p.L)) * count;
+  p.wgt = ng >= 64 && tiles512 >= device_wg_cap() / 8 ? 512 : 256;
+  p.rpp = p.wgt / p.L;
+  return p;
+}
+// Passes per tile: the largest P in {8, 4, 2, 1} with at most 8 chunks per
+// thread that still gives the launch its workgroup target: 4 per CU for one
+// matrix, 8 per CU for a batched launch (measured: stacked 960 x 2560 13.4 ->
+// 11.5 us with the higher target, while one lm_head launch is faster with
+// fewer, longer tiles: 7.6 against 8.6 us).
+int q4_seg_pick_p(const Q4SegPlan &pl, int rows, int count) {
+  const long target = (count > 1 ? 2L : 1L) * q4_target();
+  int P = 8;
+  while (P > 1 && (P * pl.K > 8 || (long)((rows + pl.rpp * P - 1) / (pl.rpp * P)) * count < target)) P >>= 1;
+  return P;
+}
+size_t q4_seg_lds(int ng, int m) { return sizeof(uint32_t) * (size_t)m * ng * Q6R; }
+
+// Run F<WGT, P, K>(args...) for the runtime (wgt, P, K) of a Q4 plan (P * K <= 8).
+#define MLLM_Q4K_PK(F, W, P, K, ...)                                                                       \
+  ((K) == 1   ? ((P) == 8   ? F<W, 8, 1>(__VA_ARGS__)                                                       \
+                 : (P) == 4 ? F<W, 4, 1>(__VA_ARGS__)                                                       \
+                 : (P) == 2 ? F<W, 2, 1>(__VA_ARGS__)                                                       \
+                            : F<W, 1, 1>(__VA_ARGS__))                                                      \
+   : (K) == 2 ? ((P) == 4 ? F<W, 4, 2>(__VA_ARGS__) : (P) == 2 ? F<W, 2, 2>(__VA_ARGS__) : F<W, 1, 2>(__VA_ARGS__)) \
+   : (K) == 3 ? ((P) == 2 ? F<W, 2, 3>(__VA_ARGS__) : F<W, 1, 3>(__VA_ARGS__))                              \
+   : (K) == 4 ? ((P) == 2 ? F<W, 2, 4>(__VA_ARGS__) : F<W, 1, 4>(__VA_ARGS__))                              \
+   : (K) == 5 ? F<W, 1, 5>(__VA_ARGS__)                                                                     \
+   : (K) == 6 ? F<W, 1, 6>(__VA_ARGS__)                                                                     \
+   : (K) == 7 ? F<W, 1, 7>(__VA_ARGS__)                                                                     \
+              : F<W, 1, 8>(__VA_ARGS__))
+#define MLLM_Q4K_DISPATCH(F, wgt, P, K, ...) \
+  ((wgt) == 256 ? MLLM_Q4K_PK(F, 256, P, K, __VA_ARGS__) : MLLM_Q4K_PK(F, 512, P, K, __VA_ARGS__))
 
 // Run F<WGT, P>(args...) for the runtime (wgt, P) of a plan.
 #define MLLM_Q4_DISPATCH(F, wgt, P, ...)                                     \
@@ -599,11 +656,11 @@ int q4_launch_batched(dim3 grid, size_t lds, hipStream_t st, const uint8_t *cons
                    : (P) == 2 ? F<512, 2>(__VA_ARGS__)                       \
                               : F<512, 1>(__VA_ARGS__)))
 
-template <int WGT, int P>
+template <int WGT, int P, int K>
 int q4_launch_argmax(dim3 grid, size_t lds, hipStream_t st, const uint8_t *packed, const float *scale, const float *x,
                      float *y, const GemvGeom &G, unsigned char *scratch, int32_t *out) {
-  if (int rc = launch_dyn(k_gemv_q4_argmax<WGT, P>, grid, lds, st, "k_gemv_q4_argmax")) return rc;
-  hipLaunchKernelGGL((k_gemv_q4_argmax<WGT, P>), grid, dim3(WGT), lds, st, packed, scale, x, y, G, scratch, out);
+  if (int rc = launch_dyn(k_gemv_q4_argmax<WGT, P, K>, grid, lds, st, "k_gemv_q4_argmax")) return rc;
+  hipLaunchKernelGGL((k_gemv_q4_argmax<WGT, P, K>), grid, dim3(WGT), lds, st, packed, scale, x, y, G, scratch, out);
   MLLM_HIP(hipGetLastError());
   return 0;
 }
@@ -611,22 +668,22 @@ int q4_launch_argmax(dim3 grid, size_t lds, hipStream_t st, const uint8_t *packe
 // The GEMV + argmax plan: the tiles of mllm_gemv_q4 for one token, so y is
 // bit-identical to mllm_gemv_q4's.
 struct AmxPlan {
-  Q4Plan pl;
+  Q4SegPlan pl;
   int P, ntiles;
 };
 AmxPlan amx_plan(int m, int n) {
   AmxPlan a;
-  a.pl = q4_plan(n, m, 1);
-  a.P = q4_pick_p(m, a.pl.rpp, 1);
+  a.pl = q4_seg_plan(n, m, 1);
+  a.P = q4_seg_pick_p(a.pl, m, 1);
   a.ntiles = (m + a.pl.rpp * a.P - 1) / (a.pl.rpp * a.P);
   return a;
 }
 
 int gemv_q4_argmax_run(const AmxPlan &a, int m, int n, const uint8_t *packed, const float *scale, const float *x,
                        float *y, int32_t *out, unsigned char *scratch, hipStream_t st) {
-  const GemvGeom G{m, n, 1, a.pl.rpp, a.pl.lpr, m};
-  return MLLM_Q4_DISPATCH(q4_launch_argmax, a.pl.wgt, a.P, dim3(a.ntiles), q4_lds_bytes(a.pl, n / 32, 1, a.P), st,
-                          packed, scale, x, y, G, scratch, out);
+  const GemvGeom G{m, n, 1, a.pl.rpp, a.pl.L, m};
+  return MLLM_Q4K_DISPATCH(q4_launch_argmax, a.pl.wgt, a.P, a.pl.K, dim3(a.ntiles), q4_seg_lds(n / 32, 1), st, packed,
+                           scale, x, y, G, scratch, out);
 }
 
 int check_argmax_args(int m, int n, int group, const uint8_t *packed, const float *scale, const float *x, float *y,
@@ -672,15 +729,15 @@ int q4_gemm(int t, int m, int n, const uint8_t *packed, const float *scale, cons
             hipStream_t st) {
   MLLM_CHECK((size_t)m * n / 2 < (1ull << 31), "matrix of %zu bytes exceeds 2 GiB", (size_t)m * n / 2);
   const int ng = n / 32;
-  const Q4Plan pl = q4_plan(n, m, 1);
-  const int P = q4_pick_p(m, pl.rpp, 1);
+  const Q4SegPlan pl = q4_seg_plan(n, m, 1);
+  const int P = q4_seg_pick_p(pl, m, 1);
   const int ntiles = (m + pl.rpp * P - 1) / (pl.rpp * P);
   for (int t0 = 0; t0 < t;) {
     int mt = t - t0 < kMaxTok ? t - t0 : kMaxTok;
-    while (mt > 1 && q4_lds_bytes(pl, ng, mt, P) > kQ4LdsMax) --mt;
-    const GemvGeom G{m, n, mt, pl.rpp, pl.lpr, m};
-    if (int rc = MLLM_Q4_DISPATCH(q4_launch_one, pl.wgt, P, dim3(ntiles), q4_lds_bytes(pl, ng, mt, P), st, packed,
-                                  scale, x + (size_t)t0 * n, y + (size_t)t0 * m, G))
+    while (mt > 1 && q4_seg_lds(ng, mt) > kQ4LdsMax) --mt;
+    const GemvGeom G{m, n, mt, pl.rpp, pl.L, m};
+    if (int rc = MLLM_Q4K_DISPATCH(q4_launch_one, pl.wgt, P, pl.K, dim3(ntiles), q4_seg_lds(ng, mt), st, packed, scale,
+                                   x + (size_t)t0 * n, y + (size_t)t0 * m, G))
       return rc;
     t0 += mt;
   }
@@ -713,12 +770,12 @@ extern "C" int mllm_gemv_q4_batched(int count, int m, int n, const uint8_t *cons
   MLLM_CHECK(packed && scale && x && y, "null pointer");
   MLLM_CHECK((size_t)m * n / 2 < (1ull << 31), "matrix of %zu bytes exceeds 2 GiB", (size_t)m * n / 2);
   const int ng = n / 32;
-  const Q4Plan pl = q4_plan(n, m, count);
-  const int P = q4_pick_p(m, pl.rpp, count);
+  const Q4SegPlan pl = q4_seg_plan(n, m, count);
+  const int P = q4_seg_pick_p(pl, m, count);
   const int ntiles = (m + pl.rpp * P - 1) / (pl.rpp * P);
-  const GemvGeom G{m, n, 1, pl.rpp, pl.lpr, m};
-  return MLLM_Q4_DISPATCH(q4_launch_batched, pl.wgt, P, dim3(ntiles, count), q4_lds_bytes(pl, ng, 1, P),
-                          as_stream(stream), packed, scale, x, y, G);
+  const GemvGeom G{m, n, 1, pl.rpp, pl.L, m};
+  return MLLM_Q4K_DISPATCH(q4_launch_batched, pl.wgt, P, pl.K, dim3(ntiles, count), q4_seg_lds(ng, 1), as_stream(stream),
+                           packed, scale, x, y, G);
 }
 
 extern "C" int mllm_gemv_q4_argmax(int m, int n, const uint8_t *packed, const float *scale, int group,

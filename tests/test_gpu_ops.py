@@ -91,9 +91,9 @@ def test_gemv_q4_batched_matches_single():
 @gpu
 @pytest.mark.parametrize("n", [2048, 2560, 4096, 8192])
 def test_gemv_q4_rows_do_not_depend_on_the_workgroup_width(n):
-    """960 x n alone (64 to 256 groups per row) launches 512-thread one-pass
-    tiles; 32 of them stacked launch 256-thread multi-pass tiles.  Every row
-    must carry the same bits."""
+    """960 x n alone (64 to 256 groups per row) and 32 of them stacked launch
+    different tile plans (workgroup width, passes per tile).  Every row must
+    carry the same bits: its summation order depends only on the row length."""
     rng = np.random.default_rng(8)
     count, m = 32, 960
     packed, sc = pgw.quant_q4((rng.standard_normal((m, n)) * 0.02).astype(np.float32))
