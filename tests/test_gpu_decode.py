@@ -326,3 +326,35 @@ def test_verify_across_splits_bit_identical_to_decode(kv_fp16, fuse, monkeypatch
         assert np.array_equal(row.view(np.uint32), lg[i].view(np.uint32)), i
         assert am[i] == g.last_argmax
     g.destroy()
+
+
+@gpu
+@pytest.mark.parametrize("case", ["135m", "long"])
+def test_two_and_three_stage_kernels_bit_identical(monkeypatch, case):
+    """The decode step's two persistent kernels, k_flow (MLLM_FLOW3=0:
+    attention items with QKV fused, MLP items) and k_flow3 (the default: QKV
+    row-head items, attention items, MLP items), give the same chained token
+    sequence and the same last logits, bit for bit: at the config 1 shape,
+    and past two attention splits (600-token context)."""
+    if case == "135m":
+        cfg = pgw.CONFIGS["smollm2-135m"]
+        bundle = pgw.parse_pgw(pgw.make_model(cfg, seed=0))
+        plen, steps = 32, 48
+    else:
+        bundle = build("llama", seed=13, max_seq_len=1024)
+        plen, steps = 600, 24
+    rng = np.random.default_rng(4)
+    prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, plen)]
+    outs = []
+    for policy in ("0", "1"):
+        monkeypatch.setenv("MLLM_FLOW3", policy)
+        g = mllm.PetitGPT(bundle, exec_mode=3)
+        print(f"{case} MLLM_FLOW3={policy}: {g.decodeKernel}", flush=True)
+        assert g.decodeKernel == "k_flow3" if policy == "1" else g.decodeKernel.startswith("k_flow<")
+        first = int(np.argmax(g.forwardPrompt(prompt)))
+        ids = g.decodeChain(first, steps)
+        last = g.forwardDecode(ids[-1]).copy()
+        outs.append((ids, last))
+        g.destroy()
+    assert outs[0][0] == outs[1][0]
+    assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))
