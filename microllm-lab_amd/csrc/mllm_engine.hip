@@ -69,6 +69,7 @@ constexpr int HD = 64;     // head dimension of every supported config
 constexpr int ACH = 256;   // positions per attention split (one per thread)
 constexpr int MAXT = 16;   // tokens per pass (upper bound; LDS sets the real one)
 constexpr int APS = 68;    // floats per attention partial: m, l, pad, pad, acc[64]
+constexpr int APT = 66;    // tagged pairs per attention partial of the persistent kernels: m, l, acc[64]
 constexpr int TC = 2;      // chunk registers per thread of an LM tile (TC * WG chunks)
 // Threads per workgroup of each phase.  The QKV, MLP and FINAL phases are
 // chains of dependent steps (loads, reductions, small GEMVs) inside few
@@ -148,6 +149,7 @@ struct DecParams {
   float *amv;     // [MAXT][lm_tiles]
   int *ami;
   uint2 *amt;     // [2][lm_tiles][2] persistent decode: each lm_head tile's first maximum (value, row) as tagged pairs, by step parity
+  uint2 *attpt;   // [MAXT][NH][nsplit_max][APT] persistent kernels: attention split partials (m, l, acc) as tagged pairs
   int lm_rpt, lm_tiles, lm_grid;
   PassState *st;
   int *hist;      // [max_seq + 1]
@@ -2206,6 +2208,7 @@ __device__ __forceinline__ void qkv_rows_get(const DecParams &P, int li, int wan
 // takes tokens ta + w, ta + w + 16, ...) and the W_o slice of each token
 // this item completes.  Cached keys (< pos0) come from the cache; the pass's
 // own K/V rows come from the QKV items (rounded as the cache holds them).
+template <bool MS = true>
 __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int item, int u0, int u1, const Step &st,
                            int m, float *smem) {
   const int sp = item / P.NH, h = item - sp * P.NH;
@@ -2221,7 +2224,6 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
   float *qrows = kvn + m * 2 * HD;    // m x 64 queries
   float *wacc = qrows + m * HD, *wm = wacc + m * AW * HD, *wl = wm + m * AW;  // per token: AW x 64 P.V, AW maxima, sums
   uint32_t *attq = reinterpret_cast<uint32_t *>(wl + m * AW);  // m x 2 Q6 records: the head outputs
-  int *flag = reinterpret_cast<int *>(attq + m * 2 * Q6R);     // m: this item writes token t's output
   TileRegs<SC> Ro;
   slice_load<SC, AT>(Lw.proj, 2 * h, D, Ro);
   float4 kr[4];
@@ -2283,79 +2285,101 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
       wl[t * AW + wv] = lw;
     }
   }
+  // the workgroup's earlier stores (a K/V cache row of an earlier item) are
+  // complete before any output of this item becomes visible
+  wait_stores();
   __syncthreads();
+  if constexpr (!MS) {
+    // every token of the pass in one split (the launch's positions < ACH):
+    // the split's statistics, its output, the W_o slice
+    for (int t = ta + wv; t < u1; t += NWV) {
+      float mx, l, own;
+      split_merge(wm + t * AW, wl + t * AW, wacc + t * AW * HD, mx, l, own);
+      q6_stage_lanes(own / l, attq + t * 2 * Q6R);
+    }
+    __syncthreads();
+    for (int t = ta; t < u1; ++t)
+      slice_gemv<SC, AT>(Ro, D, attq + t * 2 * Q6R, P.opart + (size_t)(t * P.NH + h) * D, st.tag + li);
+    return;
+  }
   // each token's split statistics from its wave partials, in wave order; a
-  // solo split stages its output, the others publish their partials
+  // solo split stages its output; of a multi-split token, the last split
+  // (the fewest keys) merges and the others publish their partials as tagged
+  // pairs (m, l, acc[64]): no completion wait and no counter on the chain
   for (int t = ta + wv; t < u1; t += NWV) {
     const int ns = (pos0 + t) / ACH + 1;
     float mx, l, own;
     split_merge(wm + t * AW, wl + t * AW, wacc + t * AW * HD, mx, l, own);
     if (ns == 1) {
       q6_stage_lanes(own / l, attq + t * 2 * Q6R);
-    } else {
-      float *dst = P.attp + ((size_t)(t * P.NH + h) * P.nsplit_max + sp) * APS;
-      coh_stf(dst, 4u * (4 + lane), own);
-      if (lane == 0) {
-        coh_stf(dst, 0, mx);
-        coh_stf(dst, 4, l);
-      }
-      // kept for the merge, should this split finish last
+    } else if (sp == ns - 1) {
+      // kept for the merge
       wacc[t * AW * HD + lane] = own;
       if (lane == 0) {
         wm[t * AW] = mx;
         wl[t * AW] = l;
       }
-    }
-  }
-  wait_stores();
-  __syncthreads();
-  if ((int)tid() < m) {
-    const int t = tid();
-    int mine = 0;
-    if (t >= ta && t < u1) {
-      const int ns = (pos0 + t) / ACH + 1;
-      if (ns == 1) {
-        mine = 1;
-      } else {
-        // count this split; the last of (t, h) merges
-        unsigned *c = P.cnt + t * P.NH + h;
-        const unsigned arrived = atomicAdd(c, 1u);
-        mine = arrived == (unsigned)(ns - 1);
-        if (mine) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      uint2 *dst = P.attpt + ((size_t)(t * P.NH + h) * P.nsplit_max + sp) * APT;
+      tag_st(dst, 2u + lane, own, st.tag + li);
+      if (lane == 0) {
+        tag_st(dst, 0, mx, st.tag + li);
+        tag_st(dst, 1, l, st.tag + li);
       }
     }
-    flag[t] = mine;
   }
   __syncthreads();
-  for (int t = ta + wv; t < u1; t += NWV) {
-    const int ns = (pos0 + t) / ACH + 1;
-    if (ns == 1 || !flag[t]) continue;
-    // the splits of (t, h) in split order, this one's from LDS
-    const float *parts = P.attp + (size_t)(t * P.NH + h) * P.nsplit_max * APS;
-    const float mx = wm[t * AW], l = wl[t * AW], own = wacc[t * AW * HD + lane];
-    const int d = lane;
-    float M = sp == 0 ? mx : coh_ldf(parts, 0);
-    for (int j = 1; j < ns; ++j) M = fmaxf(M, j == sp ? mx : coh_ldf(parts, 4u * (j * APS)));
-    const float m0 = sp == 0 ? mx : coh_ldf(parts, 0), l0 = sp == 0 ? l : coh_ldf(parts, 4),
-                a0 = sp == 0 ? own : coh_ldf(parts, 4u * (4 + d));
-    const float w0 = expf(m0 - M);
-    float ls = __builtin_fmaf(l0, w0, 0.f), as = __builtin_fmaf(a0, w0, 0.f);
-    for (int j = 1; j < ns; ++j) {
-      const float mj = j == sp ? mx : coh_ldf(parts, 4u * (j * APS));
-      const float lj = j == sp ? l : coh_ldf(parts, 4u * (j * APS + 1));
-      const float aj = j == sp ? own : coh_ldf(parts, 4u * (j * APS + 4 + d));
-      const float w = expf(mj - M);
-      ls = __builtin_fmaf(lj, w, ls);
-      as = __builtin_fmaf(aj, w, as);
+  // the merging tokens' other splits into LDS (wave partial slots 1 .. AW-1
+  // of the token, free after the merge above), polled until every tag is
+  // there, then the merges; nothing of this when the item merges no token
+  int nt = 0;  // tokens of [ta, u1) this item merges: t with ns(t) - 1 == sp > 0
+  for (int t = ta; t < u1; ++t) nt += (pos0 + t) / ACH == sp && sp > 0;
+  {
+    const int per = sp * APT;  // splits 0 .. sp-1
+    for (int b = 0; b < nt * per; b += 1024) {
+      const int i = min(b + (int)tid(), nt * per - 1);
+      int k = i / per, t = ta;
+      for (;; ++t)  // the k-th merging token
+        if ((pos0 + t) / ACH == sp && k-- == 0) break;
+      const int r = i - (i / per) * per, j = r / APT, e = r - j * APT;
+      const uint2 *src = P.attpt + ((size_t)(t * P.NH + h) * P.nsplit_max + j) * APT;
+      uint2 v = tag_ld(src, (uint32_t)e);
+      for (unsigned spins = 1; !pair_ok(v, st.tag + li) && !poll_give_up(P, spins); ++spins) {
+        poll_fence();
+        v = tag_ld(src, (uint32_t)e);
+      }
+      if (b + (int)tid() < nt * per) wacc[t * AW * HD + HD + r] = __uint_as_float(v.x);
     }
-    q6_stage_lanes(as / ls, attq + t * 2 * Q6R);
+    if (nt > 0) __syncthreads();  // uniform in the workgroup
+    for (int t = ta + wv; t < u1; t += NWV) {
+      const int ns = (pos0 + t) / ACH + 1;
+      if (ns == 1 || sp != ns - 1) continue;
+      // the splits of (t, h) in split order, this one's (the last) from its own slot
+      const float *parts = wacc + t * AW * HD + HD;  // split j: m, l, acc[64] at j * APT
+      const float mx = wm[t * AW], l = wl[t * AW], own = wacc[t * AW * HD + lane];
+      const int d = lane;
+      float M = parts[0];
+      for (int j = 1; j < ns; ++j) M = fmaxf(M, j == sp ? mx : parts[j * APT]);
+      const float m0 = parts[0], l0 = parts[1], a0 = parts[2 + d];
+      const float w0 = expf(m0 - M);
+      float ls = __builtin_fmaf(l0, w0, 0.f), as = __builtin_fmaf(a0, w0, 0.f);
+      for (int j = 1; j < ns; ++j) {
+        const float mj = j == sp ? mx : parts[j * APT];
+        const float lj = j == sp ? l : parts[j * APT + 1];
+        const float aj = j == sp ? own : parts[j * APT + 2 + d];
+        const float w = expf(mj - M);
+        ls = __builtin_fmaf(lj, w, ls);
+        as = __builtin_fmaf(aj, w, as);
+      }
+      q6_stage_lanes(as / ls, attq + t * 2 * Q6R);
+    }
+    if (nt > 0) __syncthreads();
   }
-  // the item's K/V cache rows are complete before any head output it writes
-  // becomes visible
-  wait_stores();
-  __syncthreads();
-  for (int t = ta; t < u1; ++t)
-    if (flag[t]) slice_gemv<SC, AT>(Ro, D, attq + t * 2 * Q6R, P.opart + (size_t)(t * P.NH + h) * D, st.tag + li);
+  for (int t = ta; t < u1; ++t) {
+    const int ns = (pos0 + t) / ACH + 1;
+    if (ns == 1 || sp == ns - 1)
+      slice_gemv<SC, AT>(Ro, D, attq + t * 2 * Q6R, P.opart + (size_t)(t * P.NH + h) * D, st.tag + li);
+  }
 }
 
 // MLP item of the verify step: hidden units [item*UNITS, (item+1)*UNITS) of
@@ -2599,6 +2623,7 @@ __global__ __launch_bounds__(FLT) void k_flowm(DecParams P, FlowGeom F) {
 // (or step) is then complete before the workgroup's next tagged output, on
 // which every later reader of that row depends.  The arithmetic is the
 // verify step's, so the rows are bit for bit k_flow's.
+template <bool MS>
 __global__ __launch_bounds__(FLT) void k_flow3(DecParams P, FlowGeom F) {
   extern __shared__ float4 smem4[];
   float *smem = reinterpret_cast<float *>(smem4);
@@ -2644,7 +2669,7 @@ __global__ __launch_bounds__(FLT) void k_flow3(DecParams P, FlowGeom F) {
           wait_stores();
           flowm_qkv(P, Lw, li, j, 0, 1, st, true, smem, tok);
         } else if (j < im) {
-          flowm_attn(P, Lw, li, j - ia, 0, 1, st, 1, smem);
+          flowm_attn<MS>(P, Lw, li, j - ia, 0, 1, st, 1, smem);
         } else {
           const int it = j - im;
           flowm_mlp(P, Lw, li, it, st, 0, 1, true, smem);
@@ -2896,7 +2921,11 @@ int launch_flow(mllm_model *M, int steps) {
   F.steps = steps;
   F.m = 1;
   void *args[] = {&M->P, &F};
-  const FlowKernel kern = use_flow3(M, M->h_st->pos0) ? k_flow3 : kFlowKernels[M->aq_idx];
+  // k_flow3<false> while every position of the chain lies in the first
+  // attention split (no split merges), k_flow3<true> past it
+  const FlowKernel kern = !use_flow3(M, M->h_st->pos0)               ? kFlowKernels[M->aq_idx]
+                          : M->h_st->pos0 + steps - 1 < ACH ? k_flow3<false>
+                                                                      : k_flow3<true>;
   if (M->exec_mode == 4) {
     // the same kernel and grid through an ordinary launch (profilers that do
     // not follow cooperative launches): every workgroup is resident only if
@@ -3239,6 +3268,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   // nothing is pending
   if (!rc) rc = dev_alloc(M, &P.kv, kv_elems * (c.kv_fp16 ? 2 : 4) + 256);
   if (!rc) rc = dev_alloc(M, (void **)&P.attp, sizeof(float) * MAXT * NH * P.nsplit_max * APS);
+  if (!rc) rc = dev_alloc(M, (void **)&P.attpt, sizeof(uint2) * MAXT * NH * P.nsplit_max * APT);
   if (!rc) rc = dev_alloc(M, (void **)&P.cnt, sizeof(unsigned) * MAXT * NH);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_logits, sizeof(float) * MAXT * (size_t)V);
   if (!rc) rc = dev_alloc(M, (void **)&P.amv, sizeof(float) * MAXT * P.lm_tiles);
@@ -3256,6 +3286,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       hipMemset(P.opart, 0, tagged_bytes[2]) != hipSuccess || hipMemset(P.dpart, 0, tagged_bytes[3]) != hipSuccess ||
       hipMemset(P.cnt, 0, sizeof(unsigned) * MAXT * NH) != hipSuccess ||
       hipMemset(P.amt, 0, sizeof(uint2) * 4 * P.lm_tiles) != hipSuccess ||
+      hipMemset(P.attpt, 0, sizeof(uint2) * MAXT * NH * P.nsplit_max * APT) != hipSuccess ||
       hipMemset(P.rec, 0, sizeof(uint2) * 2 * MAXT * ngd * Q6R) != hipSuccess ||
       hipMemset(P.qkvr, 0, sizeof(uint2) * L * MAXT * (NH + 2 * NKV) * HD) != hipSuccess ||
       hipMemset(P.kv, 0, kv_elems * (c.kv_fp16 ? 2 : 4)) != hipSuccess)
@@ -3361,19 +3392,28 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       M->exec_mode = 3;
       M->flow_default = true;
       // the three-stage chained kernel, when it is resident on the same grid
-      const void *k3 = reinterpret_cast<const void *>(k_flow3);
-      int pc3 = 0;
-      M->flow3_ok = (M->flow_lds <= 64 * 1024 ||
+      const void *k3 = reinterpret_cast<const void *>(k_flow3<true>);
+      const void *k3s = reinterpret_cast<const void *>(k_flow3<false>);
+      int pc3 = 0, pc3s = 0;
+      // (the merging split of an attention item gathers the other splits'
+      // partials into its wave-partial slots: at most AW - 1 splits)
+      M->flow3_ok = P.nsplit_max < AW &&
+                    (M->flow_lds <= 64 * 1024 ||
                      hipFuncSetAttribute(k3, hipFuncAttributeMaxDynamicSharedMemorySize, (int)M->flow_lds) ==
                          hipSuccess) &&
                     hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc3, k3, FLT, M->flow_lds) == hipSuccess &&
-                    pc3 >= per_cu;
+                    pc3 >= per_cu &&
+                    (M->flow_lds <= 64 * 1024 ||
+                     hipFuncSetAttribute(k3s, hipFuncAttributeMaxDynamicSharedMemorySize, (int)M->flow_lds) ==
+                         hipSuccess) &&
+                    hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc3s, k3s, FLT, M->flow_lds) == hipSuccess &&
+                    pc3s >= per_cu;
       if (const char *v = getenv("MLLM_FLOW3")) M->flow3_policy = atoi(v);
       // the verify kernel: the most tokens whose LDS still lets the same grid
       // be resident (one workgroup per CU)
       if (const char *v = getenv("MLLM_VERIFY_FUSE")) M->verify_fuse = atoi(v);
       const void *km = reinterpret_cast<const void *>(k_flowm);
-      for (int mm = std::min(MAXT, M->max_pass); mm >= 2; --mm) {
+      for (int mm = std::min(MAXT, M->max_pass); P.nsplit_max < AW && mm >= 2; --mm) {
         const size_t b = flowm_lds_bytes(P, F, mm);
         int pc = 0;
         if (b <= lds_cap &&
