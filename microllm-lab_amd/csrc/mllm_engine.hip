@@ -2092,9 +2092,12 @@ __device__ void flowm_norm(const DecParams &P, int li, int t, int side, const St
 // pairs (K and V rows rounded as the cache stores them), the K and V rows
 // also to the cache.  nt <= VQT.
 constexpr int VQT = 8;  // tokens per QKV item at most (its LDS)
+// hf >= 0 takes half of the row head: dimensions 16 hf .. 16 hf + 15 and
+// their RoPE partners 32 + 16 hf .. (32 rows; the per-row arithmetic is the
+// full item's, so the rows carry the same bits).
 __device__ void flowm_qkv(const DecParams &P, const LayerW &Lw, int li, int rh, int t0, int nt, const Step &st,
-                          bool fused, float *smem, int tok_in = -1) {
-  const int D = P.D, ng = D >> 5, nch = HD * ng;
+                          bool fused, float *smem, int tok_in = -1, int hf = -1) {
+  const int D = P.D, ng = D >> 5, rpi = hf < 0 ? HD : HD / 2, nch = rpi * ng;  // rows per item and token
   const int nrow = (P.NH + 2 * P.NKV) * HD;
   const bool gpt2 = P.arch == 1;
   const bool is_q = rh < P.NH, is_k = !is_q && rh < P.NH + P.NKV;
@@ -2103,7 +2106,10 @@ __device__ void flowm_qkv(const DecParams &P, const LayerW &Lw, int li, int rh, 
   float *rs = part + nt * nch;                        // nt x 64 row sums
   float *rt = rs + nt * HD;                           // nt x (cos, sin) (gpt2: the bias)
   TileRegs<QC> R;
-  tile_load<QC, QT>(Lw.qkv, rh * HD, HD, 0, ng, nch, R);
+  if (hf < 0)
+    tile_load<QC, QT>(Lw.qkv, rh * HD, HD, 0, ng, nch, R);
+  else
+    tile_load<QC, QT>(Lw.qkv, rh * HD + 16 * hf, 16, rh * HD + 32 + 16 * hf, ng, nch, R);
   if ((int)tid() < nt * HD) {
     const int tt = tid() / HD, d = tid() - tt * HD;
     if (gpt2) {
@@ -2117,19 +2123,22 @@ __device__ void flowm_qkv(const DecParams &P, const LayerW &Lw, int li, int rh, 
   if (fused) {
     // each token's residual and norm here (the row head 0 item writes xa)
     float *scratch = rt + al4(nt * 2 * HD);
-    for (int tt = 0; tt < nt; ++tt) resid_norm(P, li, t0 + tt, 0, st, scratch, qx + tt * ng * Q6R, rh == 0, tok_in);
+    for (int tt = 0; tt < nt; ++tt)
+      resid_norm(P, li, t0 + tt, 0, st, scratch, qx + tt * ng * Q6R, rh == 0 && hf <= 0, tok_in);
   } else {
     rec_get(P, rec_row(P, 0, t0), nt * ng * Q6R, st.tag + li, qx);
   }
   __syncthreads();
   tile_partials<QC>(R, ng, nch, nt, qx, part);
   __syncthreads();
-  // the nt x 64 row sums, four lanes each (the decode attention item's order)
-  for (int base = 0; base < nt * HD; base += 256) {
+  // the nt x rpi row sums, four lanes each (the decode attention item's
+  // order), at their head dimension
+  for (int base = 0; base < nt * rpi; base += 256) {
     const int r = base + (int)(tid() >> 2);
-    const int rr = min(r, nt * HD - 1), tr = rr / HD;
-    const float a = row_sum4(part + tr * nch + (rr - tr * HD) * ng, ng, tid() & 3);
-    if ((tid() & 3) == 0 && r < nt * HD) rs[r] = a;
+    const int rr = min(r, nt * rpi - 1), tr = rr / rpi, lr = rr - tr * rpi;
+    const float a = row_sum4(part + tr * nch + lr * ng, ng, tid() & 3);
+    const int dim = hf < 0 ? lr : (lr < 16 ? 16 * hf + lr : 16 + 16 * hf + lr);
+    if ((tid() & 3) == 0 && r < nt * rpi) rs[tr * HD + dim] = a;
   }
   __syncthreads();
   // token t0 + tt on wave tt, lane d = head dimension d
@@ -2142,6 +2151,7 @@ __device__ void flowm_qkv(const DecParams &P, const LayerW &Lw, int li, int rh, 
       const float mate = __shfl_xor(v, 32);  // rotate-half partner d +- 32
       v = __builtin_fmaf(v, rt[tt * 2 * HD + d], (d < 32 ? -mate : mate) * rt[tt * 2 * HD + HD + d]);
     }
+    if (hf >= 0 && ((d >> 4) & 1) != hf) continue;  // a dimension of the other half
     float r = v;
     if (!is_q) {
       const int kvh = is_k ? rh - P.NH : rh - P.NH - P.NKV;
@@ -2611,8 +2621,12 @@ __global__ __launch_bounds__(FLT) void k_flowm(DecParams P, FlowGeom F) {
 }
 
 // The chained decode step in three stages per layer (the verify step's fused
-// items at one row): QKV items (row head: 64 rows of attn.qkv, each forming
-// the token's residual and norm; row head 0 writes the residual row),
+// items at one row): QKV items (half a row head: 32 rows of attn.qkv, the
+// dimensions 16 hf .. 16 hf + 15 and their RoPE partners, each item forming
+// the token's residual and norm; row head 0's first half writes the residual
+// row; measured against whole row heads: 135M after a 512-token prompt 455 ->
+// 450 us per token, 360M after 1536 tokens 674 -> 664, unchanged at short
+// context),
 // attention items (split, head) that read the q/k/v rows from P.qkvr, and
 // the MLP items; then k_flow's lm_head share and step handoffs.  Every row
 // head's rows are formed once, where k_flow's attention items each form
@@ -2633,7 +2647,7 @@ __global__ __launch_bounds__(FLT) void k_flow3(DecParams P, FlowGeom F) {
   const int nlm = min(G, F.lm_tiles);
   const LmGeom lg{F.lm_rpt, F.lm_tiles};
   const int nrh = P.NH + 2 * P.NKV;
-  const int ia = nrh, im = ia + F.na, ni = im + F.nm;  // items per layer: QKV | attention | MLP
+  const int ia = 2 * nrh, im = ia + F.na, ni = im + F.nm;  // items per layer: QKV halves | attention | MLP
   const int pos_start = st_ld(P, ST_OFF(pos0));
   int *const slots = flow_slots(smem, F.kvp);
   if (tid() == 0) {
@@ -2667,7 +2681,7 @@ __global__ __launch_bounds__(FLT) void k_flow3(DecParams P, FlowGeom F) {
         __syncthreads();  // the previous item's LDS is free
         if (j < ia) {
           wait_stores();
-          flowm_qkv(P, Lw, li, j, 0, 1, st, true, smem, tok);
+          flowm_qkv(P, Lw, li, j >> 1, 0, 1, st, true, smem, tok, j & 1);
         } else if (j < im) {
           flowm_attn<MS>(P, Lw, li, j - ia, 0, 1, st, 1, smem);
         } else {
