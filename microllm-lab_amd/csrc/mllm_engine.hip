@@ -2315,7 +2315,9 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
   // each token's split statistics from its wave partials, in wave order; a
   // solo split stages its output; of a multi-split token, the last split
   // (the fewest keys) merges and the others publish their partials as tagged
-  // pairs (m, l, acc[64]): no completion wait and no counter on the chain
+  // pairs (m, l, acc[64]): no completion wait and no counter on the chain.
+  // A lower split of the head has a lower item index, so a merging item
+  // never waits for an item that its own workgroup has yet to run.
   for (int t = ta + wv; t < u1; t += NWV) {
     const int ns = (pos0 + t) / ACH + 1;
     float mx, l, own;
