@@ -617,12 +617,13 @@ Q4SegPlan q4_seg_plan(int cols, int rows, int count) {
   return p;
 }
 // Passes per tile: the largest P in {8, 4, 2, 1} with at most 8 chunks per
-// thread that still gives the launch its workgroup target: 4 per CU for one
-// matrix, 8 per CU for a batched launch (measured: stacked 960 x 2560 13.4 ->
-// 11.5 us with the higher target, while one lm_head launch is faster with
-// fewer, longer tiles: 7.6 against 8.6 us).
+// thread that still gives the launch its workgroup target: 2 per CU for one
+// matrix, 8 per CU for a batched launch (measured, graph-replayed: stacked
+// 960 x 2560 13.4 -> 11.5 us with 8 per CU instead of 4; one cold lm_head
+// launch 7.8 -> 7.5 us with 2 per CU instead of 4: fewer, longer tiles, so
+// fewer workgroups stage x).
 int q4_seg_pick_p(const Q4SegPlan &pl, int rows, int count) {
-  const long target = (count > 1 ? 2L : 1L) * q4_target();
+  const long target = count > 1 ? 2L * q4_target() : q4_target() / 2;
   int P = 8;
   while (P > 1 && (P * pl.K > 8 || (long)((rows + pl.rpp * P - 1) / (pl.rpp * P)) * count < target)) P >>= 1;
   return P;
