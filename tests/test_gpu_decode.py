@@ -358,3 +358,26 @@ def test_two_and_three_stage_kernels_bit_identical(monkeypatch, case):
         g.destroy()
     assert outs[0][0] == outs[1][0]
     assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))
+
+
+@gpu
+def test_chain_across_first_split_boundary_equals_graph():
+    """A chain that starts inside the first 256-position attention split and
+    ends past it (the persistent kernel's instance with split merges) gives
+    the graph replay's tokens and last logits bit for bit, as does a chain
+    that stays inside the split (the instance without them)."""
+    bundle = build("llama", seed=21, max_seq_len=1024)
+    rng = np.random.default_rng(9)
+    prompt = [int(v) for v in rng.integers(0, bundle.cfg.vocab_size, 240)]
+    for steps in (12, 30):  # positions 240-251, then 240-269
+        outs = []
+        for mode in (1, 3):
+            print(f"chain from 240, {steps} steps, mode={mode}", flush=True)
+            g = mllm.PetitGPT(bundle, exec_mode=mode)
+            first = int(np.argmax(g.forwardPrompt(prompt)))
+            ids = g.decodeChain(first, steps)
+            last = g.forwardDecode(ids[-1]).copy()
+            outs.append((ids, last))
+            g.destroy()
+        assert outs[0][0] == outs[1][0]
+        assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))
