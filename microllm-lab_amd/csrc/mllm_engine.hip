@@ -2758,8 +2758,10 @@ struct mllm_model {
   int verify_fuse = 9;    // verify steps of at most this many tokens run fused (MLLM_VERIFY_FUSE); faster at every M <= 9 measured
   size_t flowm_lds = 0;
   bool flow_default = false;  // mode 3 was chosen by default, not by mllm_set_exec_mode
+  bool refuse_coop = false;   // test hook (MLLM_REFUSE_COOPERATIVE): cooperative launches act as refused
+  std::vector<std::pair<void *, size_t>> tagged;  // every tagged buffer and flag array (cleared when the epochs restart)
   size_t flow_lds = 0;
-  int flow_epoch = 0;     // epochs used so far (flags hold epochs, never cleared)
+  int flow_epoch = 0;     // epochs used so far (flags hold epochs; cleared only when the epochs restart)
   int aq_idx = 0;         // instance of the decode attention item / persistent kernel (tile size 4, 5, 6)
   hipEvent_t ev0 = nullptr, ev1 = nullptr;  // around the kernels of the last call
   std::vector<hipEvent_t> prof_ev;          // mllm_profile_decode
@@ -2918,6 +2920,27 @@ int launch_phase(mllm_model *M, int ph, int li, int m, hipEvent_t e0 = nullptr, 
 // enqueues the phase kernels instead (same results, bit for bit).
 constexpr int kFlowFellBack = -1;
 int launch_flowm(mllm_model *M, int m, int pos0);
+
+// A cooperative launch of a persistent kernel (decode chain or verify step).
+// With refuse_coop set (MLLM_REFUSE_COOPERATIVE=1 at create, a test hook)
+// the runtime's refusal is simulated without launching anything.  A refusal
+// while mode 3 is only the default switches the model to mode 1 for good and
+// returns kFlowFellBack: the caller enqueues the phase kernels instead (same
+// results, bit for bit).  An explicit mllm_set_exec_mode(3) reports it.
+int launch_coop(mllm_model *M, const void *kern, void **args, size_t lds, const char *what) {
+  const hipError_t e = M->refuse_coop ? hipErrorCooperativeLaunchTooLarge
+                                      : hipLaunchCooperativeKernel(kern, dim3(M->flow_grid), dim3(FLT), args, lds,
+                                                                   M->stream);
+  if (e == hipSuccess) return 0;
+  if (M->flow_default && (e == hipErrorIllegalState || e == hipErrorNotSupported ||
+                          e == hipErrorCooperativeLaunchTooLarge)) {
+    (void)hipGetLastError();
+    M->exec_mode = 1;
+    M->flow_grid = 0;
+    return kFlowFellBack;
+  }
+  return hip_fail(e, what, __FILE__, __LINE__);
+}
 // The decode step's kernel: k_flow3 (three stages per layer) whenever it is
 // resident on the persistent grid, k_flow otherwise (or with MLLM_FLOW3=0).
 // Measured chains, us per token, k_flow vs k_flow3: 135M after a 32-token
@@ -2925,12 +2948,28 @@ int launch_flowm(mllm_model *M, int m, int pos0);
 // tokens 733.3 vs 594.0, after 1536 tokens 1005.7 vs 809.3; GPT-2 124M after
 // 16 tokens 258.1 vs 245.7.  With MLLM_FLOW3=2 the choice goes by shape:
 // k_flow3 for d_model >= 960 or past the first attention split.
+// Tags are epoch * TAGL + layer in 32 bits, so epochs must stay below
+// 2^32 / TAGL.  Before a launch would pass that, the stream is drained, every
+// tagged buffer and flag is cleared (tag 0: below every tag a launch waits
+// for, since launches start at epoch 1) and the epochs start again from 0.
+// This runs on the host between launches, never inside a graph.
+constexpr int64_t kEpochEnd = int64_t(1) << 25;  // 2^32 / TAGL
+int flow_epoch_room(mllm_model *M, int steps) {
+  if ((int64_t)M->flow_epoch + steps < kEpochEnd) return 0;
+  MLLM_HIP(hipStreamSynchronize(M->stream));
+  for (const auto &b : M->tagged) MLLM_HIP(hipMemset(b.first, 0, b.second));
+  MLLM_HIP(hipDeviceSynchronize());
+  M->flow_epoch = 0;
+  return 0;
+}
+
 bool use_flow3(const mllm_model *M, int pos) {
   if (!M->flow3_ok || M->flow3_policy == 0) return false;
   return M->flow3_policy == 1 || M->P.D >= 960 || pos >= ACH;
 }
 
 int launch_flow(mllm_model *M, int steps) {
+  if (int rc = flow_epoch_room(M, steps)) return rc;
   FlowGeom F = M->flow;
   F.ep0 = M->flow_epoch + 1;
   F.steps = steps;
@@ -2951,20 +2990,10 @@ int launch_flow(mllm_model *M, int steps) {
     M->flow_epoch += steps;
     return 0;
   }
-  const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(kern), dim3(M->flow_grid), dim3(FLT),
-                                                  args, M->flow_lds, M->stream);
-  if (e == hipSuccess) {
-    M->flow_epoch += steps;
-    return 0;
-  }
-  if (M->flow_default && (e == hipErrorIllegalState || e == hipErrorNotSupported ||
-                          e == hipErrorCooperativeLaunchTooLarge)) {
-    (void)hipGetLastError();
-    M->exec_mode = 1;
-    M->flow_grid = 0;
-    return kFlowFellBack;
-  }
-  return hip_fail(e, "hipLaunchCooperativeKernel(k_flow)", __FILE__, __LINE__);
+  const int rc = launch_coop(M, reinterpret_cast<const void *>(kern), args, M->flow_lds,
+                             "hipLaunchCooperativeKernel(k_flow)");
+  if (rc == 0) M->flow_epoch += steps;
+  return rc;
 }
 
 // One verify step of m tokens at positions pos0 .. pos0+m-1 in the
@@ -2973,6 +3002,7 @@ int launch_flow(mllm_model *M, int steps) {
 // items, and the stages' token groups are as small as the grid allows (every
 // item of a layer on its own workgroup).
 int launch_flowm(mllm_model *M, int m, int pos0) {
+  if (int rc = flow_epoch_room(M, 1)) return rc;
   FlowGeom F = M->flow;
   F.ep0 = M->flow_epoch + 1;
   F.steps = 1;
@@ -2990,13 +3020,16 @@ int launch_flowm(mllm_model *M, int m, int pos0) {
     const int ni = 2 * m + nrh * groups(F.tq) + F.na * groups(F.ta) + F.nm * groups(F.mt);
     if (F.fuse || ni <= M->flow_grid) break;
   }
-  const void *k = reinterpret_cast<const void *>(k_flowm);
   if (M->exec_mode == 4) {
     hipLaunchKernelGGL(k_flowm, dim3(M->flow_grid), dim3(FLT), M->flowm_lds, M->stream, M->P, F);
     MLLM_HIP(hipGetLastError());
   } else {
     void *args[] = {&M->P, &F};
-    MLLM_HIP(hipLaunchCooperativeKernel(k, dim3(M->flow_grid), dim3(FLT), args, M->flowm_lds, M->stream));
+    // a refusal falls back like the decode step's: in spec decode the first
+    // persistent launch is usually a verify step
+    const int rc = launch_coop(M, reinterpret_cast<const void *>(k_flowm), args, M->flowm_lds,
+                               "hipLaunchCooperativeKernel(k_flowm)");
+    if (rc) return rc;
   }
   M->flow_epoch += 1;
   return 0;
@@ -3309,6 +3342,14 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   P.logits = M->d_logits;
   P.hist = M->d_hist;
   P.st = M->d_st;
+  M->tagged = {{P.xa, tagged_bytes[0]},
+               {P.xb, tagged_bytes[1]},
+               {P.opart, tagged_bytes[2]},
+               {P.dpart, tagged_bytes[3]},
+               {P.amt, sizeof(uint2) * 4 * P.lm_tiles},
+               {P.attpt, sizeof(uint2) * MAXT * NH * P.nsplit_max * APT},
+               {P.rec, sizeof(uint2) * 2 * MAXT * ngd * Q6R},
+               {P.qkvr, sizeof(uint2) * L * MAXT * (NH + 2 * NKV) * HD}};
 
   // batched prompt processing: the weights as PGW1 matrices, work buffers
   // for up to 2048 tokens per chunk
@@ -3403,6 +3444,9 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       const size_t nflags = (size_t)L * (NH + F.nm) + 2 + G;
       if (int rc = dev_alloc(M, (void **)&F.flags, sizeof(int) * nflags)) return fail(rc);
       if (hipMemset(F.flags, 0, sizeof(int) * nflags) != hipSuccess) return fail(set_error(MLLM_ERR_HIP, "memset"));
+      M->tagged.emplace_back(F.flags, sizeof(int) * nflags);
+      // test hook: start the epochs near their end (MLLM_FLOW_EPOCH0)
+      if (const char *v = getenv("MLLM_FLOW_EPOCH0")) M->flow_epoch = (int)std::min<int64_t>(atoll(v), kEpochEnd - 1);
       M->flow_grid = G;
       M->exec_mode = 3;
       M->flow_default = true;
@@ -3424,6 +3468,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
                     hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc3s, k3s, FLT, M->flow_lds) == hipSuccess &&
                     pc3s >= per_cu;
       if (const char *v = getenv("MLLM_FLOW3")) M->flow3_policy = atoi(v);
+      if (const char *v = getenv("MLLM_REFUSE_COOPERATIVE")) M->refuse_coop = atoi(v) != 0;
       // the verify kernel: the most tokens whose LDS still lets the same grid
       // be resident (one workgroup per CU)
       if (const char *v = getenv("MLLM_VERIFY_FUSE")) M->verify_fuse = atoi(v);

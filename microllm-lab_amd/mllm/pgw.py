@@ -265,6 +265,56 @@ def make_llama(cfg: Config, seed: int = 0, std: float = 0.02, norm_gain: float =
     return w.finish(cfg)
 
 
+def make_cycle_llama(cfg: Config, cycle, seed: int = 0, std: float = 0.02, layer_std: float = 0.002,
+                     gain: float = 20.0) -> bytes:
+    """A llama model whose greedy decode follows a token cycle: after token
+    cycle[i] it emits cycle[(i + 1) % len(cycle)].  Synthetic N(0, std)
+    weights cannot show prompt-lookup speculation at work -- their greedy
+    output repeats one token or never repeats a 3-gram, so every draft is one
+    token long or empty -- and no trained checkpoint is available offline.
+
+    Layer 0's MLP carries the cycle.  Hidden unit i < len(cycle) has gate and
+    up rows 0.5 * e_i (e_i the unit direction of cycle[i]'s embedding row),
+    so it fires only for that token (silu(12) * 12 against ~0.1), and its
+    down column adds gain * e_{i+1} / 144 to the residual, which then points
+    at the next token's embedding.  The other units of the first 32 (one Q4
+    group of the down rows) are zero, so the cycle's columns quantise on
+    their own scale.  Every other weight is N(0, layer_std): the remaining
+    layers do real work without turning the residual away from the next
+    token.  The lm_head / embedding is N(0, std) as in make_llama."""
+    cycle = [int(t) for t in cycle]
+    c = len(cycle)
+    assert 1 < c <= 32 <= cfg.d_ff and len(set(cycle)) == c
+    rng = np.random.default_rng(seed)
+    hd = cfg.d_model // cfg.n_heads
+    kv = cfg.n_kv_heads * hd
+    w = PgwWriter()
+    emb = _normal(rng, (cfg.vocab_size, cfg.d_model), std)
+    w.add_q4("lm_head", emb)
+    unit = emb[cycle] / np.linalg.norm(emb[cycle], axis=1, keepdims=True)
+    ones = np.ones(cfg.d_model, np.float32)
+    for i in range(cfg.n_layers):
+        w.add_f32(f"blocks.{i}.norm1", ones)
+        w.add_q4(f"blocks.{i}.attn.qkv", _normal(rng, (cfg.d_model + 2 * kv, cfg.d_model), layer_std))
+        w.add_q4(f"blocks.{i}.attn.proj", _normal(rng, (cfg.d_model, cfg.d_model), layer_std))
+        w.add_f32(f"blocks.{i}.norm2", ones)
+        w1 = _normal(rng, (cfg.d_ff, cfg.d_model), layer_std)
+        w3 = _normal(rng, (cfg.d_ff, cfg.d_model), layer_std)
+        w2 = _normal(rng, (cfg.d_model, cfg.d_ff), layer_std)
+        if i == 0:
+            w1[:32] = 0.0
+            w3[:32] = 0.0
+            w2[:, :32] = 0.0
+            w1[:c] = 0.5 * unit
+            w3[:c] = 0.5 * unit
+            w2[:, :c] = (gain / 144.0) * np.roll(unit, -1, axis=0).T
+        w.add_q4(f"blocks.{i}.mlp.w1", w1.astype(np.float32))
+        w.add_q4(f"blocks.{i}.mlp.w3", w3.astype(np.float32))
+        w.add_q4(f"blocks.{i}.mlp.w2", w2.astype(np.float32))
+    w.add_f32("norm_f", ones)
+    return w.finish(cfg)
+
+
 def make_gpt2(cfg: Config, seed: int = 0, std: float = 0.02, scale_factors: Optional[np.ndarray] = None,
               bias_std: float = 0.0) -> bytes:
     """GPT-2 PGW1 in convert_gpt2_to_pgw.py:135-164 order; header qGroup = 1 as the

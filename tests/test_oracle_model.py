@@ -178,3 +178,28 @@ def test_generate_truncation_and_eos(oracle_lib):
     # first emitted token as eos stops immediately
     out2, stop2 = m.generate(ids, max_new_tokens=4, eos_id=out[0])
     assert out2 == [out[0]] and stop2 == "eos"
+
+
+def test_cycle_model_follows_its_cycle(oracle_lib):
+    """pgw.make_cycle_llama (the speculation benchmark's model): from any
+    token of the cycle, the oracle's greedy decode walks the cycle, with a
+    wide top-2 margin; the prompt-lookup drafts along it are full length."""
+    from mllm.engine import lookup_draft
+
+    cfg = pgw.small_config("llama", max_seq_len=128)
+    rng = np.random.default_rng(3)
+    cycle = [int(v) for v in rng.choice(cfg.vocab_size, 9, replace=False)]
+    ref = oracle_lib.OracleModel(pgw.parse_pgw(pgw.make_cycle_llama(cfg, cycle, seed=1)))
+    prompt = [int(v) for v in rng.integers(0, cfg.vocab_size, 10)] + cycle + cycle[:4]
+    lg = ref.forward_prompt(prompt)
+    seq, worst = list(prompt), np.inf
+    for i in range(20):
+        top2 = np.partition(lg, -2)[-2:]
+        worst = min(worst, float(top2[1] - top2[0]))
+        tok = int(np.argmax(lg))
+        assert tok == cycle[(4 + i) % 9], i
+        assert lookup_draft(seq, 4, 3) == [cycle[(4 + i + j) % 9] for j in range(4)]
+        seq.append(tok)
+        lg = ref.forward_decode(tok)
+    ref.close()
+    assert worst > 1.0, worst
