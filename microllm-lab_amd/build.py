@@ -3,6 +3,7 @@
     python microllm-lab_amd/build.py            # everything
     python microllm-lab_amd/build.py lib        # libmllm.so only
     python microllm-lab_amd/build.py convert    # the PGW1 converter (host C++)
+    python microllm-lab_amd/build.py probe      # libmllm_probe.so: the stage probe build (stage_probe.py)
 
 hipcc cross-compiles for gfx950 without a GPU.  All HIP code is built with
 packed-FP32 instructions disabled (-Xclang -target-feature -Xclang
@@ -76,15 +77,21 @@ def _resource_usage(lines):
     return out
 
 
-def build_lib(verbose: bool = False) -> str:
-    os.makedirs(BUILD, exist_ok=True)
+PROBE_LIB = os.path.join(PKG, "libmllm_probe.so")
+
+
+def build_lib(verbose: bool = False, defines=(), out: str = LIB) -> str:
+    """libmllm.so, or with defines another build of the same sources (its
+    objects under _build/<name>/, no resource record)."""
+    objdir = BUILD if out == LIB else os.path.join(BUILD, os.path.basename(out).replace(".so", ""))
+    os.makedirs(objdir, exist_ok=True)
     objs = []
+    dflags = [f"-D{d}" for d in defines]
 
     def compile_one(src):
-        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-        lines = _run([HIPCC, *HIP_FLAGS, *EXTRA_FLAGS.get(src, []), "-Rpass-analysis=kernel-resource-usage", "-c",
-                      os.path.join(CSRC, src),
-                      "-o", obj])
+        obj = os.path.join(objdir, src.replace(".hip", ".o"))
+        lines = _run([HIPCC, *HIP_FLAGS, *dflags, *EXTRA_FLAGS.get(src, []), "-Rpass-analysis=kernel-resource-usage",
+                      "-c", os.path.join(CSRC, src), "-o", obj])
         return obj, _resource_usage(lines)
 
     with ThreadPoolExecutor(max_workers=len(HIP_SOURCES)) as ex:
@@ -93,18 +100,19 @@ def build_lib(verbose: bool = False) -> str:
     usage = {}
     for _, u in results:
         usage.update(u)
-    with open(RESOURCE_JSON, "w") as f:
-        json.dump(usage, f, indent=1, sort_keys=True)
+    if out == LIB:
+        with open(RESOURCE_JSON, "w") as f:
+            json.dump(usage, f, indent=1, sort_keys=True)
     spilled = {k: v for k, v in usage.items() if v.get("ScratchSize", 0) > 0}
     if spilled:
         raise RuntimeError("kernels use scratch memory: " + ", ".join(f"{k} ({v['ScratchSize']} B/lane)"
                                                                       for k, v in sorted(spilled.items())))
-    tmp = LIB + ".tmp"
+    tmp = out + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {out}")
+    return out
 
 
 def build_napi(verbose: bool = False) -> str:
@@ -153,5 +161,7 @@ if __name__ == "__main__":
         build_napi(True)
     elif what == "convert":
         build_convert(True)
+    elif what == "probe":
+        build_lib(True, defines=["MLLM_STAGE_PROBE"], out=PROBE_LIB)
     else:
         build_all(True)

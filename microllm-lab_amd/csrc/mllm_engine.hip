@@ -163,6 +163,56 @@ struct Step {
 };
 constexpr int TAGL = 128;  // tags per step (layers < TAGL)
 
+// ---------------------------------------------------------------- stage probe
+// A library built with -DMLLM_STAGE_PROBE (microllm-lab_amd/stage_probe.py)
+// records when each item of the chained decode kernel k_flow3 reaches fixed
+// points: thread 0 reads the 100 MHz real-time counter into LDS, and an
+// item's stamps go out to the device array g_probe (vector stores) when its
+// workgroup takes its next item or ends.  mllm_probe_read copies the array
+// out, mllm_probe_clear zeroes it.  Layout [pos & 15][slot][item][PK] of u64:
+// slot = layer for the layer items (item = index within the layer), PROBE_LM
+// for the lm_head share and PROBE_TOP for the step-top token resolve (item =
+// workgroup).  Stamps in use, by item kind:
+//   all     0 item start, 7 item end
+//   QKV     1 inputs gathered, 2 norm records done, 3 chunk dots, 4 row sums
+//   ATT     1 q/k/v rows in, 2 scores + P.V done, 3 split merges done
+//   MLP     1 inputs gathered, 2 norm records done, 3 gate/up dots, 4 activation records
+//   LM      1 last layer's flags seen, 2 final-norm records in, 3 tiles done
+// The default build compiles none of this.
+#ifdef MLLM_STAGE_PROBE
+constexpr int PNI = 256, PSLOTS = 34, PK = 8, PROBE_TOP = 32, PROBE_LM = 33;
+__device__ unsigned long long g_probe[16 * PSLOTS * PNI * PK];
+__shared__ int g_pctx;
+__shared__ unsigned long long g_pl[PK];
+__device__ __forceinline__ void probe_flush() {
+  if (threadIdx.x == 0 && g_pctx >= 0)
+    for (int k = 0; k < PK; ++k)
+      coh_st8(g_probe, (uint32_t)(g_pctx + k) * 8u, make_uint2((uint32_t)g_pl[k], (uint32_t)(g_pl[k] >> 32)));
+}
+__device__ __forceinline__ void probe_init() {
+  if (threadIdx.x == 0) g_pctx = -1;
+}
+__device__ __forceinline__ void probe_set(int pos, int slot, int item) {
+  probe_flush();
+  if (threadIdx.x == 0) {
+    g_pctx = ((((pos & 15) * PSLOTS + min(slot, PSLOTS - 1)) * PNI + min(item, PNI - 1)) * PK);
+    for (int k = 0; k < PK; ++k) g_pl[k] = 0;
+  }
+}
+__device__ __forceinline__ void probe_stamp(int k) {
+  if (threadIdx.x == 0) g_pl[k] = __builtin_amdgcn_s_memrealtime();
+}
+#define PROBE_INIT() probe_init()
+#define PROBE_SET(pos, slot, item) probe_set(pos, slot, item)
+#define PROBE(k) probe_stamp(k)
+#define PROBE_END() probe_flush()
+#else
+#define PROBE_INIT() ((void)0)
+#define PROBE_SET(pos, slot, item) ((void)0)
+#define PROBE(k) ((void)0)
+#define PROBE_END() ((void)0)
+#endif
+
 // The pass state is read and written with coherent access: inside the
 // persistent kernel ARGMAX updates it for workgroups on other XCDs.
 #define ST_OFF(field) ((uint32_t)offsetof(PassState, field))
@@ -1804,6 +1854,8 @@ struct FlowCtl {
   bool done;
   __device__ void resolve() {
     if (pending) {
+      PROBE_SET(pos, PROBE_TOP, w);
+      PROBE(0);
       if (wave_id() < AMW)
         flow_tiles_argmax(P, flow_amt(P, e - 1), ntiles, (int)((uint32_t)(e - 1) * (uint32_t)TAGL) + TAG_LM, slots);
       __syncthreads();
@@ -1817,6 +1869,7 @@ struct FlowCtl {
       __syncthreads();
       done = slots[1] != 0;
       __syncthreads();  // slot 1 is written again only at the next step's resolve
+      PROBE(1);
       pending = false;
     }
   }
@@ -1855,7 +1908,10 @@ __device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, co
     gains_load(P, P.norm_f, rbias, GR);
     gains_store(P, rbias, GR, gl);
   }
+  PROBE_SET(st.pos0, PROBE_LM, wg);
+  PROBE(0);
   if (wait()) return false;
+  PROBE(1);
   const bool penal = P.arch == 1 && st_ld(P, ST_OFF(chain)) != 0;
   if (penal && tid() == 0) gpt2_lists(P, s.lists);
   if (pub) {
@@ -1878,6 +1934,7 @@ __device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, co
     }
   }
   __syncthreads();
+  PROBE(2);
   if (tile >= L.ntiles) return false;
   const int nban = penal ? s.lists[0] : 0, nrc = penal ? s.lists[1] : 0;
   const int amtag = st.tag + TAG_LM;
@@ -1891,6 +1948,7 @@ __device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, co
     lm_tile<FTC, FLT>(P, L, Rb, tile, 0, 1, s, penal, nban, nrc, amt, amtag);
     tile += nwg;
   }
+  PROBE(3);
   return true;
 }
 
@@ -2069,6 +2127,7 @@ __device__ __forceinline__ void resid_norm(const DecParams &P, int li, int t, in
     const float4 base = col_base_load<true>(P, brow, nq, want);
     resid_blocks<1, true>(P, prow, np, want, blk);
     __syncthreads();
+    PROBE(1);
     x = col_finish(blk, nq, np, base, gl, D, rbias != nullptr);
   }
   uint2 *xo = write_x && !fin ? (side ? P.xb : P.xa) + (size_t)t * D : nullptr;
@@ -2129,8 +2188,10 @@ __device__ void flowm_qkv(const DecParams &P, const LayerW &Lw, int li, int rh, 
     rec_get(P, rec_row(P, 0, t0), nt * ng * Q6R, st.tag + li, qx);
   }
   __syncthreads();
+  PROBE(2);
   tile_partials<QC>(R, ng, nch, nt, qx, part);
   __syncthreads();
+  PROBE(3);
   // the nt x rpi row sums, four lanes each (the decode attention item's
   // order), at their head dimension
   for (int base = 0; base < nt * rpi; base += 256) {
@@ -2141,6 +2202,7 @@ __device__ void flowm_qkv(const DecParams &P, const LayerW &Lw, int li, int rh, 
     if ((tid() & 3) == 0 && r < nt * rpi) rs[tr * HD + dim] = a;
   }
   __syncthreads();
+  PROBE(4);
   // token t0 + tt on wave tt, lane d = head dimension d
   for (int tt = wave_id(); tt < nt; tt += NWV) {
     const int d = lane_id(), t = t0 + tt, pos = st.pos0 + t;
@@ -2234,14 +2296,24 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
   float *qrows = kvn + m * 2 * HD;    // m x 64 queries
   float *wacc = qrows + m * HD, *wm = wacc + m * AW * HD, *wl = wm + m * AW;  // per token: AW x 64 P.V, AW maxima, sums
   uint32_t *attq = reinterpret_cast<uint32_t *>(wl + m * AW);  // m x 2 Q6 records: the head outputs
+  // the W_o slice, loaded only by an item that completes some token's head
+  // output (its only split, or the merging last split); at 2048 context the
+  // other seven split items of a head would fetch 38 KB each and drop it
+  bool need_o = !MS;
+  if constexpr (MS)
+    for (int t = ta; t < u1; ++t) {
+      const int ns = (pos0 + t) / ACH + 1;
+      need_o |= ns == 1 || sp == ns - 1;
+    }
   TileRegs<SC> Ro;
-  slice_load<SC, AT>(Lw.proj, 2 * h, D, Ro);
+  if (need_o) slice_load<SC, AT>(Lw.proj, 2 * h, D, Ro);
   float4 kr[4];
   float vr[16];
   attn_k_load(P, li, kvh, s0, ncached, kr);  // cached positions: written by earlier steps
   attn_v_load(P, li, kvh, s0, ncached, vr);
   qkv_rows_get(P, li, st.tag + li, u0, u1, h, kvh, qrows, kvn);
   __syncthreads();
+  PROBE(1);
   // this thread's K quarter and V values of the split, cached or the pass's
   // own (row key - knew, clamped: keys past the range's last row are past
   // every count of the range)
@@ -2299,6 +2371,7 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
   // complete before any output of this item becomes visible
   wait_stores();
   __syncthreads();
+  PROBE(2);
   if constexpr (!MS) {
     // every token of the pass in one split (the launch's positions < ACH):
     // the split's statistics, its output, the W_o slice
@@ -2308,6 +2381,7 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
       q6_stage_lanes(own / l, attq + t * 2 * Q6R);
     }
     __syncthreads();
+    PROBE(3);
     for (int t = ta; t < u1; ++t)
       slice_gemv<SC, AT>(Ro, D, attq + t * 2 * Q6R, P.opart + (size_t)(t * P.NH + h) * D, st.tag + li);
     return;
@@ -2387,6 +2461,7 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
     }
     if (nt > 0) __syncthreads();
   }
+  PROBE(3);
   for (int t = ta; t < u1; ++t) {
     const int ns = (pos0 + t) / ACH + 1;
     if (ns == 1 || sp == ns - 1)
@@ -2417,6 +2492,7 @@ __device__ void flowm_mlp(const DecParams &P, const LayerW &Lw, int li, int item
     rec_get(P, rec_row(P, 1, ta), m * ng * Q6R, want, qx);
   }
   __syncthreads();
+  PROBE(2);
   const int wv = wave_id(), lane = lane_id(), g = tid() % ng;
   for (int t0 = 0; t0 < m; t0 += VMB) {
     const int nt = min(VMB, m - t0);
@@ -2443,6 +2519,7 @@ __device__ void flowm_mlp(const DecParams &P, const LayerW &Lw, int li, int item
       }
     }
     __syncthreads();
+    PROBE(3);
     for (int tt = 0; tt < nt; ++tt) {
       // row r (gate rows, then up rows): lane s adds partials s, s + 8, ...
       // in order, then a fixed 8-lane tree
@@ -2473,6 +2550,7 @@ __device__ void flowm_mlp(const DecParams &P, const LayerW &Lw, int li, int item
     }
   }
   __syncthreads();
+  PROBE(4);
   for (int t = 0; t < m; ++t)
     slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * Q6R, P.dpart + ((size_t)(ta + t) * P.nchunk + item) * D, want);
 }
@@ -2661,6 +2739,7 @@ __global__ __launch_bounds__(FLT) void k_flow3(DecParams P, FlowGeom F) {
   }
   __syncthreads();
   if (w >= ni && w >= nlm && w != 0) return;  // no item and no lm_head tile in any step
+  PROBE_INIT();
   bool stopped = false;
   for (int step = 0; step < F.steps; ++step) {
     FlowCtl C{P, slots, w, F.lm_tiles, F.ep0 + step, pos_start + step, step > 0, false};
@@ -2681,6 +2760,8 @@ __global__ __launch_bounds__(FLT) void k_flow3(DecParams P, FlowGeom F) {
         int j = jv;
         asm volatile("" : "+s"(j));
         __syncthreads();  // the previous item's LDS is free
+        PROBE_SET(st.pos0, li, j);
+        PROBE(0);
         if (j < ia) {
           wait_stores();
           flowm_qkv(P, Lw, li, j >> 1, 0, 1, st, true, smem, tok, j & 1);
@@ -2691,6 +2772,7 @@ __global__ __launch_bounds__(FLT) void k_flow3(DecParams P, FlowGeom F) {
           flowm_mlp(P, Lw, li, it, st, 0, 1, true, smem);
           if (tid() == 0) flag_st(fl + P.NH + it, e);  // the lm_head's coarse waits
         }
+        PROBE(7);
       }
     }
     if (w < nlm || w == 0) {
@@ -2709,6 +2791,7 @@ __global__ __launch_bounds__(FLT) void k_flow3(DecParams P, FlowGeom F) {
     __syncthreads();
     if (tid() == 0) flow_record_step(P, slots, flow_tiles_combine(slots), pos_start + F.steps - 1);
   }
+  PROBE_END();
 }
 
 using FlowKernel = void (*)(DecParams, FlowGeom);
@@ -3723,6 +3806,23 @@ extern "C" int mllm_last_timing(const mllm_model *M, float *gpu_ms, int *n_token
   if (n_tokens) *n_tokens = M->last_tokens;
   return 0;
 }
+
+#ifdef MLLM_STAGE_PROBE
+// The stage probe's stamps (a library built with MLLM_STAGE_PROBE only; not
+// part of include/mllm.h): 16 x 34 x 256 x 8 u64 values.
+extern "C" int mllm_probe_read(void *out) {
+  MLLM_CHECK(out, "null argument");
+  MLLM_HIP(hipDeviceSynchronize());
+  MLLM_HIP(hipMemcpyFromSymbol(out, HIP_SYMBOL(g_probe), sizeof(g_probe)));
+  return 0;
+}
+extern "C" int mllm_probe_clear(void) {
+  MLLM_HIP(hipDeviceSynchronize());
+  static unsigned long long zero[16 * PSLOTS * PNI * PK];
+  MLLM_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_probe), zero, sizeof(g_probe)));
+  return 0;
+}
+#endif
 
 extern "C" int mllm_model_gemv(mllm_model *M, const char *name, const float *x, float *y) {
   MLLM_CHECK(M && name && x && y, "null argument");
