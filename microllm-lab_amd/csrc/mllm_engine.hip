@@ -175,8 +175,10 @@ constexpr int TAGL = 128;  // tags per step (layers < TAGL)
 // workgroup).  Stamps in use, by item kind:
 //   all     0 item start, 7 item end
 //   QKV     1 inputs gathered, 2 norm records done, 3 chunk dots, 4 row sums
-//   ATT     1 q/k/v rows in, 2 scores + P.V done, 3 split merges done
+//   ATT     1 q/k/v rows in, 4 K/V assembled, 5 score/P.V loop done, 2 after
+//           the store wait and barrier, 3 split merges done
 //   MLP     1 inputs gathered, 2 norm records done, 3 gate/up dots, 4 activation records
+//   QKV, MLP (thread 0's wave, in the norm) 5 norm scale known, 6 records staged
 //   LM      1 last layer's flags seen, 2 final-norm records in, 3 tiles done
 // The default build compiles none of this.
 #ifdef MLLM_STAGE_PROBE
@@ -481,8 +483,10 @@ __device__ __forceinline__ void col_norm(const DecParams &P, float4 x, const flo
     y = make_float4(x.x * r * g.x, x.y * r * g.y, x.z * r * g.z, x.w * r * g.w);
   }
   if (!in) y = make_float4(0.f, 0.f, 0.f, 0.f);
+  PROBE(5);
   if (o.y && in) coh_st4(o.y, 16u * q, y);
   if (qx_t && wave_id() < nw) q6_stage_col(y, in, q, qx_t);
+  PROBE(6);
 }
 
 // The base column of this thread from a tagged row (branch-free); with POLL,
@@ -2128,7 +2132,9 @@ __device__ __forceinline__ void resid_norm(const DecParams &P, int li, int t, in
     resid_blocks<1, true>(P, prow, np, want, blk);
     __syncthreads();
     PROBE(1);
-    x = col_finish(blk, nq, np, base, gl, D, rbias != nullptr);
+    // the waves past the row's columns skip the block reads (col_norm leaves
+    // their x out)
+    x = wave_id() < ((nq + 63) >> 6) ? col_finish(blk, nq, np, base, gl, D, rbias != nullptr) : base;
   }
   uint2 *xo = write_x && !fin ? (side ? P.xb : P.xa) + (size_t)t * D : nullptr;
   col_norm(P, x, gl, red, qx, ColOut{xo, st.tag + li});
@@ -2320,7 +2326,9 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
   const int kp = tid() >> 2, ku = tid() & 3;
   float4 kk[4];
   float vs[16];
-  {
+  if (16 * wv + 15 >= knew) {
+    // a wave holding one of the pass's own keys (wave-uniform): LDS rows
+    // where the key is new, the cache's otherwise
     const float4 *kn = reinterpret_cast<const float4 *>(kvn + 2 * HD * min(max(kp - knew, 0), u1 - 1));
 #pragma unroll
     for (int j = 0; j < 4; ++j) kk[j] = kp >= knew ? kn[4 * ku + j] : kr[j];
@@ -2329,7 +2337,15 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
       const int key = 16 * wv + k;
       vs[k] = key >= knew ? kvn[2 * HD * min(max(key - knew, 0), u1 - 1) + HD + lane] : vr[k];
     }
+  } else {
+    // every key of the wave is cached: no LDS read (at decode all waves but
+    // the newest key's; the reads of the others cost the LDS 0.5 us a layer)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kk[j] = kr[j];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) vs[k] = vr[k];
   }
+  PROBE(4);
   // every token's scores, wave statistics and P.V (attn_core's arithmetic;
   // keys past the count have weight 0 and finite values, which changes at
   // most the sign of a zero sum, and the Q6 staging of the output drops it)
@@ -2367,6 +2383,7 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
       wl[t * AW + wv] = lw;
     }
   }
+  PROBE(5);
   // the workgroup's earlier stores (a K/V cache row of an earlier item) are
   // complete before any output of this item becomes visible
   wait_stores();

@@ -73,7 +73,9 @@ def analyse(b, geo):
             t0 = Mp[:, 7].max()
             add("QKV: inputs gathered after the previous MLP stage (first item)", Q[:, 1].min() - t0)
             add("QKV: inputs gathered after the previous MLP stage (last item)", Q[:, 1].max() - t0)
-            add("QKV: residual + norm + 24-bit records", np.median(Q[:, 2] - Q[:, 1]))
+            add("QKV: residual + norm scale (wave 0)", np.median(Q[:, 5] - Q[:, 1]))
+            add("QKV: records staged (wave 0)", np.median(Q[:, 6] - Q[:, 5]))
+            add("QKV: barrier after the records", np.median(Q[:, 2] - Q[:, 6]))
             add("QKV: chunk dots", np.median(Q[:, 3] - Q[:, 2]))
             add("QKV: row sums", np.median(Q[:, 4] - Q[:, 3]))
             add("QKV: RoPE + q/k/v and cache stores", np.median(Q[:, 7] - Q[:, 4]))
@@ -81,14 +83,18 @@ def analyse(b, geo):
             tq = Q[:, 7].max()
             add("ATT: q/k/v rows in after the QKV stage (first item)", A[:, 1].min() - tq)
             add("ATT: q/k/v rows in after the QKV stage (last item)", A[:, 1].max() - tq)
-            add("ATT: scores, softmax statistics, P.V", np.median(A[:, 2] - A[:, 1]))
+            add("ATT: K/V of the split assembled", np.median(A[:, 4] - A[:, 1]))
+            add("ATT: scores, softmax statistics, P.V (wave 0)", np.median(A[:, 5] - A[:, 4]))
+            add("ATT: store wait + barrier", np.median(A[:, 2] - A[:, 5]))
             add("ATT: split merges + head-output records", np.median(A[:, 3] - A[:, 2]))
             add("ATT: W_o slice", np.median(A[:, 7] - A[:, 3]))
             add("ATT stage (QKV stage done -> last attention item done)", A[:, 7].max() - tq)
             ta = A[:, 7].max()
             add("MLP: inputs gathered after the attention stage (first item)", M[:, 1].min() - ta)
             add("MLP: inputs gathered after the attention stage (last item)", M[:, 1].max() - ta)
-            add("MLP: residual + norm + 24-bit records", np.median(M[:, 2] - M[:, 1]))
+            add("MLP: residual + norm scale (wave 0)", np.median(M[:, 5] - M[:, 1]))
+            add("MLP: records staged (wave 0)", np.median(M[:, 6] - M[:, 5]))
+            add("MLP: barrier after the records", np.median(M[:, 2] - M[:, 6]))
             add("MLP: gate/up chunk dots", np.median(M[:, 3] - M[:, 2]))
             add("MLP: row sums + activation records", np.median(M[:, 4] - M[:, 3]))
             add("MLP: down slice", np.median(M[:, 7] - M[:, 4]))
