@@ -521,8 +521,29 @@ def bench_configs(mllm, pgw, args, oracle=None):
     # overlaps them); the verify pass itself at M = k + 1 rows, forced drafts:
     spec3["verify_pass_us"] = {f"m{m}": verify_pass_us(g, prompt, m) for m in (1, 5, 9)}
     spec3["note"] = ("greedy output of the synthetic model repeats one token: every draft is 1 token long; "
-                     "verify_pass_us times M-row passes with forced drafts")
+                     "verify_pass_us times M-row passes with forced drafts; full_drafts shows k at work")
     g.destroy()
+    # beside the BASELINE workload: the same shape with a 12-token greedy cycle
+    # (pgw.make_cycle_llama), the prompt holding the cycle once, so that
+    # prompt-lookup drafts are full length and accepted: what k changes
+    rng = np.random.default_rng(7)
+    cycle = [int(v) for v in rng.choice(cfg.vocab_size, 12, replace=False)]
+    gc = mllm.PetitGPT(pgw.parse_pgw(pgw.make_cycle_llama(cfg, cycle, seed=0)), exec_mode=args.exec_mode)
+    cprompt = spans_prompt(np.random.default_rng(3), cfg.vocab_size, 512 - 14) + cycle + cycle[:2]
+    cbase = gc.generate(cprompt, maxNewTokens=256, mode="chain")
+    cbase = gc.generate(cprompt, maxNewTokens=256, mode="chain")
+    full = {"model": "smollm2-135m shape, greedy output a 12-token cycle (pgw.make_cycle_llama)", "prompt": 512,
+            "new": 256, "chain_tok_s": round(255 / ((cbase["totalMs"] - cbase["ttftMs"]) / 1e3), 1)}
+    for k in (4, 8):
+        r = gc.generate(cprompt, maxNewTokens=256, mode="spec", specK=k)
+        r = gc.generate(cprompt, maxNewTokens=256, mode="spec", specK=k)
+        full[f"k{k}"] = {"tok_s": round(255 / ((r["totalMs"] - r["ttftMs"]) / 1e3), 1),
+                         "specHits": r["specHits"], "specTries": r["specTries"],
+                         "accepted_per_pass": round(r["specHits"] / max(1, r["specTries"]), 2),
+                         "same_as_greedy": r["generatedIds"] == cbase["generatedIds"]}
+        log(f"[bench] spec full drafts k={k}: {full[f'k{k}']}")
+    spec3["full_drafts"] = full
+    gc.destroy()
     if oracle is not None:
         # the reference's CPU path has no speculation (it is in the GPU engine
         # only, webgpu.js:1239-1270): greedy decode at the prompt's context

@@ -19,7 +19,7 @@
  *   (bytes 33-126, 161-172, 174-255 as themselves, the rest to U+0100 on);
  * - adjacent symbols merge, the lowest merge rank first (leftmost on ties),
  *   until no pair has a rank; each symbol is looked up in the vocabulary
- *   (missing: the unk token's id, else 1);
+ *   (missing: vocab[String(unk_token)], else 1);
  * - decode maps ids to symbols, symbols to bytes and decodes UTF-8 with
  *   U+FFFD for invalid sequences (ids outside the vocabulary are dropped).
  * encodeMessages (tokenizer.js:199-272) lays out a conversation for the
@@ -58,7 +58,10 @@ export class Tokenizer {
   constructor(spec) {
     const model = spec.model;
     this.vocab = new Map(Object.entries(model.vocab));
-    this.unkId = model.unk_token != null && this.vocab.has(model.unk_token) ? this.vocab.get(model.unk_token) : 1;
+    // tokenizer.js:60, vocab[spec.model.unk_token] ?? 1: the property name is
+    // String(unk_token), so a null unk_token finds the entry "null"
+    const unkKey = String(model.unk_token);
+    this.unkId = this.vocab.has(unkKey) && this.vocab.get(unkKey) != null ? this.vocab.get(unkKey) : 1;
     this.ranks = new Map();
     (model.merges || []).forEach((m, i) => {
       const [a, b] = Array.isArray(m) ? m : [m.slice(0, m.indexOf(" ")), m.slice(m.indexOf(" ") + 1)];

@@ -12,7 +12,7 @@ The algorithm (tokenizer.js:1-183):
   alphabet (bytes 33-126, 161-172, 174-255 as themselves, the rest to 256+);
 - merge adjacent symbols, the lowest merge rank first (leftmost on ties),
   until no pair has a rank; look each symbol up in the vocabulary (unknown ->
-  unk id, else 1);
+  the unk id: vocab[String(unk_token)], else 1);
 - special tokens (added_tokens with "special") are matched first, longest
   first, and the text between them is encoded as above; text longer than
   32768 characters keeps its last 32768;
@@ -72,11 +72,30 @@ def _js_text(text: str, limit: int = MAX_CHARS) -> str:
 SPECIAL = {"PAD": 0, "UNK": 1, "BOS": 2, "EOS": 3, "SYSTEM": 4, "USER": 5, "ASSISTANT": 6}
 
 
+def js_key(obj: dict, name: str) -> str:
+    """The property name JavaScript forms from obj[name] when it is used as a
+    key (String(value)): "undefined" when absent, "null", "true" / "false",
+    integral numbers without a fraction, strings as they are."""
+    if name not in obj:
+        return "undefined"
+    v = obj[name]
+    if v is None:
+        return "null"
+    if isinstance(v, bool):
+        return "true" if v else "false"
+    if isinstance(v, float) and v.is_integer():
+        return str(int(v))
+    return str(v)
+
+
 class Tokenizer:
     def __init__(self, spec: dict):
         model = spec["model"]
         self.vocab: Dict[str, int] = model["vocab"]
-        self.unk_id = self.vocab.get(model.get("unk_token"), 1) if model.get("unk_token") is not None else 1
+        # tokenizer.js:60 looks the unk token up as a property name,
+        # vocab[String(unk_token)] ?? 1: a null unk_token finds the entry
+        # "null" (18220 in the SmolLM2 vocabularies, 8423 in GPT-2's)
+        self.unk_id = self.vocab.get(js_key(model, "unk_token"), 1)
         self.ranks: Dict[tuple, int] = {}
         for i, m in enumerate(model.get("merges") or []):
             if isinstance(m, (list, tuple)):

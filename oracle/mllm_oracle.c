@@ -26,8 +26,12 @@
  *   orc_forward_*       HF transformers LlamaForCausalLM / GPT2LMHeadModel (float64)
  *                       built from the same dequantised weights; prefill/decode
  *                       consistency invariant
- *   orc_quant_q8*       parity unpinned against the reference (it has no Q8
- *                       quantiser); checked only for its stated rule.
+ *   orc_quant_q8*       the reference ships no Q8 quantiser (its Q8 format,
+ *                       weights.js:96-104, is per-row), so the rule is this
+ *                       build's: pinned by closed form and brute force (scale
+ *                       exactly f32(amax/127), the largest element to +-127,
+ *                       every element to the nearest of the 255 levels, ties
+ *                       to even).
  */
 #define _POSIX_C_SOURCE 200809L
 #include "mllm_oracle.h"

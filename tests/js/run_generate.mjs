@@ -7,8 +7,8 @@
  *         logits are returned for comparison)
  */
 import fs from "fs";
-import { parsePgw } from "./weights.mjs";
-import { HipPetitGPT } from "./engine.mjs";
+import { parsePgw } from "../../microllm-lab_amd/js/weights.mjs";
+import { HipPetitGPT } from "../../microllm-lab_amd/js/engine.mjs";
 
 async function main() {
   const [, , pgwPath, specPath] = process.argv;

@@ -4,8 +4,8 @@
  *   node selftest.mjs <model.pgw> <cases.json>   -> prints one JSON line
  */
 import fs from "fs";
-import { parsePgw, tensorTable } from "./weights.mjs";
-import { argmax, argmaxGpt2, lookupDraft } from "./sampling.mjs";
+import { parsePgw, tensorTable } from "../../microllm-lab_amd/js/weights.mjs";
+import { argmax, argmaxGpt2, lookupDraft } from "../../microllm-lab_amd/js/sampling.mjs";
 
 const [, , pgwPath, casesPath] = process.argv;
 const buf = fs.readFileSync(pgwPath);

@@ -13,7 +13,7 @@ import mllm
 from mllm import pgw
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-JS = os.path.join(ROOT, "microllm-lab_amd", "js")
+JS = os.path.join(ROOT, "tests", "js")  # the Node test drivers (they import microllm-lab_amd/js)
 NODE = shutil.which("node")
 pytestmark = pytest.mark.skipif(NODE is None, reason="node not installed")
 

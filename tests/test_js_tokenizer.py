@@ -18,7 +18,7 @@ import pytest
 from mllm import tokenizer as T
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-CLI = os.path.join(ROOT, "microllm-lab_amd", "js", "tokenize_cli.mjs")
+CLI = os.path.join(ROOT, "tests", "js", "tokenize_cli.mjs")
 NODE = shutil.which("node")
 pytestmark = pytest.mark.skipif(NODE is None, reason="node not installed")
 REF_MODELS = "/root/reference/models"
@@ -79,6 +79,7 @@ def test_js_tokenizer_equals_python_on_the_reference_models(tmp_path, name):
     cases = {"tokenizer": path, "encode": texts + cut, "decode": ids + [[10 ** 9], ids[3][:1]],
              "decodeSkip": ids[6:8]}
     out = run_js(tmp_path, cases)
+    assert out["unkId"] == tok.unk_id
     assert out["encode"][:len(texts)] == ids
     assert out["encode"][len(texts):] == [tok.encode(t) for t in cut]
     assert out["decode"] == [tok.decode(i) for i in cases["decode"]]

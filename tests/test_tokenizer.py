@@ -13,6 +13,7 @@ Pins:
 - the merge loop: the lowest rank first, leftmost on ties, on hand-made specs;
 - the templates: their token layout on hand-made tokenizers.
 """
+import json
 import os
 import random
 
@@ -190,3 +191,35 @@ def test_templates_with_the_reference_cards():
     ids2 = T.encode_messages(tok2, conv[1:], card2)
     assert ids2[0] == tok2.special["<|im_start|>"] == 1 and ids2.count(tok2.special["<|im_end|>"]) == 1
     assert tok2.decode(ids2) == "<|im_start|>user\nWhat is 2 + 2?<|im_end|>\n<|im_start|>assistant\n"
+
+
+@pytest.mark.parametrize("name,want", [("smollm2-135m-instruct", 18220), ("smollm2-360m-instruct", 18220),
+                                       ("l20-edu-135m", 18220), ("gpt2", 8423), ("petitgpt", 1), ("minimind2", 1)])
+def test_unk_id_follows_the_reference_lookup(name, want):
+    """tokenizer.js:60 takes vocab[spec.model.unk_token] ?? 1, a property
+    lookup by String(unk_token): the shipped SmolLM2 and GPT-2 files have
+    unk_token null, so the entry "null" is the unk id; petitgpt's "[UNK]"
+    and minimind2's null miss and give 1.  A symbol missing from the
+    vocabulary then encodes as that id."""
+    path = os.path.join(REF_MODELS, name, "tokenizer.json")
+    if not os.path.exists(path):
+        pytest.skip("the reference's tokenizer files are not present")
+    spec = json.load(open(path, encoding="utf-8"))
+    tok = T.load_tokenizer(spec)
+    assert tok.unk_id == want
+    assert T.js_key(spec["model"], "unk_token") == ("null" if spec["model"].get("unk_token") is None
+                                                     else spec["model"]["unk_token"])
+
+
+def test_js_key_rules():
+    assert T.js_key({}, "u") == "undefined"
+    assert T.js_key({"u": None}, "u") == "null"
+    assert T.js_key({"u": True}, "u") == "true"
+    assert T.js_key({"u": 3.0}, "u") == "3"
+    assert T.js_key({"u": "<unk>"}, "u") == "<unk>"
+    vocab = {T.BYTE_TO_CHAR[b]: b + 10 for b in range(256)}
+    vocab["null"] = 5
+    tok = T.load_tokenizer({"model": {"vocab": vocab, "merges": [], "unk_token": None}})
+    assert tok.unk_id == 5
+    tok = T.load_tokenizer({"model": {"vocab": vocab, "merges": []}})
+    assert tok.unk_id == 1  # vocab["undefined"] is absent
