@@ -223,6 +223,20 @@ const char *mllm_decode_kernel_name(const mllm_model *model);
  * results, bit for bit).  0 when the persistent kernel is not in use. */
 int mllm_flow_verify_tokens(const mllm_model *model);
 
+/* GpuPetitGPT's debug knobs debugMaxLayers / debugNoAttn / debugNoMlp /
+ * debugMlpTo (webgpu-metal.js:1263-1279; set from the page's query string,
+ * app.js:1317-1325): only the first max_layers layers run (< 0: all),
+ * no_attn != 0 drops every attention block, no_mlp != 0 every MLP block,
+ * mlp_to >= 0 keeps the MLP blocks of layers < mlp_to only (< 0: all).  A
+ * dropped block adds nothing to the residual, in every execution mode and in
+ * verify passes, so the logits are the truncated network's, as the
+ * reference's skipped dispatches give them (its q/k/v rows are still written
+ * to the KV cache, where the reference leaves them unwritten; no kept block
+ * reads them).  While a knob is set, prompts run through the decode passes
+ * instead of the batched path.  mllm_set_debug(m, -1, 0, 0, -1) restores the
+ * full network. */
+int mllm_set_debug(mllm_model *model, int max_layers, int no_attn, int no_mlp, int mlp_to);
+
 /* Prompts of at least min_tokens tokens (default 2; 0 = never) are
  * processed in batches (no counterpart in the reference, whose GPU path runs
  * a prompt token by token, webgpu.js:1178-1187): tokens 0 .. n-2 go through

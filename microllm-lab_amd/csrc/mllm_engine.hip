@@ -109,6 +109,8 @@ struct LayerW {
   const float *n1, *n2;         // RMS gains; gpt2: LayerNorm gamma || beta
   const float *qkv_b, *proj_b, *fc_b, *mproj_b;
   const float *prev_mproj_b;    // gpt2: the previous layer's mlp.proj bias
+  int dbg;                      // debug knobs (mllm_set_debug): bit 0 the attention block adds nothing to the
+                                // residual, bit 1 the MLP block adds nothing (its projection writes zero partials)
 };
 
 // Device-resident description of the current pass; every phase reads it.
@@ -582,8 +584,10 @@ __device__ __forceinline__ void slice_load(const Q4Mat &W, int g0, int rows, Til
 // row r = part(group g0) + part(group g0 + 1), the row_sum order of two
 // groups, stored as a tagged pair by the even lane of the row.  Every lane
 // takes part in the shuffle.
+// With zero (a block the debug knobs switch off) the partial is stored as 0.
 template <int C, int NT>
-__device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const uint32_t *v, uint2 *out, int tag) {
+__device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const uint32_t *v, uint2 *out, int tag,
+                                           bool zero = false) {
   const int L = lane_id(), wv = wave_id();
 #pragma unroll
   for (int k = 0; k < C; ++k) {
@@ -592,7 +596,7 @@ __device__ __forceinline__ void slice_gemv(const TileRegs<C> &R, int rows, const
     float p = 0.f;
     if (r < rows) p = q4_dot6(R.w[k], v + (L & 1) * Q6R, R.s[k]);
     const float sum = p + lane_xor1(p);  // rows past the end are 0
-    if ((L & 1) == 0 && r < rows) tag_st(out, (uint32_t)r, sum, tag);
+    if ((L & 1) == 0 && r < rows) tag_st(out, (uint32_t)r, zero ? 0.f : sum, tag);
   }
 }
 
@@ -1007,7 +1011,7 @@ __device__ bool attn_core(const DecParams &P, const LayerW &Lw, int t, int sp, i
   // output becomes visible, so whoever sees the output also sees them
   wait_stores();
   __syncthreads();
-  slice_gemv<C, AT>(Ro, D, A.attq, P.opart + (size_t)(t * P.NH + h) * D, tag);
+  slice_gemv<C, AT>(Ro, D, A.attq, P.opart + (size_t)(t * P.NH + h) * D, tag, Lw.dbg & 1);
   return true;
 }
 
@@ -1285,7 +1289,7 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
       resid_blocks<FLOW ? 2 : 0, FLOW>(P, P.opart + (size_t)t * P.NH * D, P.NH, want, bt);
     }
     __syncthreads();
-    col_norm(P, col_finish(bt, nq, P.NH, base, gl, D, gpt2), gl, red, qx + t * ng * Q6R,
+    col_norm(P, col_finish(bt, nq, P.NH, base, gl, D, rbias != nullptr), gl, red, qx + t * ng * Q6R,
              ColOut{item == 0 ? P.xb + (size_t)t * D : nullptr, want});
   }
   if (!FLOW) slice_load<MC, MT>(Lw.w2, 2 * item, D, M.Rd);  // needed last: behind everything the prologue reads
@@ -1348,7 +1352,7 @@ __device__ void phase_mlp(const DecParams &P, const LayerW &Lw, int m, int li, i
   }
   __syncthreads();
   for (int t = 0; t < m; ++t)
-    slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * Q6R, P.dpart + ((size_t)t * P.nchunk + item) * D, want);
+    slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * Q6R, P.dpart + ((size_t)t * P.nchunk + item) * D, want, Lw.dbg & 2);
 }
 
 // The last layer's residual and the final norm of token t: Q6 records (LDS)
@@ -1362,7 +1366,7 @@ __device__ __forceinline__ void final_row(const DecParams &P, int t, float *blk,
   const float4 base = col_base_load<(POLL != 0)>(P, P.xb + (size_t)t * D, nq, want);
   resid_blocks<POLL, POLL == 2>(P, P.dpart + (size_t)t * P.nchunk * D, P.nchunk, want, blk);
   __syncthreads();
-  const float4 x = col_finish(blk, nq, P.nchunk, base, gl, D, P.arch == 1);
+  const float4 x = col_finish(blk, nq, P.nchunk, base, gl, D, P.arch == 1 && P.last_mproj_b != nullptr);
   col_norm(P, x, gl, blk + ((P.nchunk + PB - 1) / PB) * D, qx, ColOut{nullptr, 0, to_global ? P.xn + (size_t)t * D : nullptr});
 }
 
@@ -2400,7 +2404,7 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
     __syncthreads();
     PROBE(3);
     for (int t = ta; t < u1; ++t)
-      slice_gemv<SC, AT>(Ro, D, attq + t * 2 * Q6R, P.opart + (size_t)(t * P.NH + h) * D, st.tag + li);
+      slice_gemv<SC, AT>(Ro, D, attq + t * 2 * Q6R, P.opart + (size_t)(t * P.NH + h) * D, st.tag + li, Lw.dbg & 1);
     return;
   }
   // each token's split statistics from its wave partials, in wave order; a
@@ -2482,7 +2486,7 @@ __device__ void flowm_attn(const DecParams &P, const LayerW &Lw, int li, int ite
   for (int t = ta; t < u1; ++t) {
     const int ns = (pos0 + t) / ACH + 1;
     if (ns == 1 || sp == ns - 1)
-      slice_gemv<SC, AT>(Ro, D, attq + t * 2 * Q6R, P.opart + (size_t)(t * P.NH + h) * D, st.tag + li);
+      slice_gemv<SC, AT>(Ro, D, attq + t * 2 * Q6R, P.opart + (size_t)(t * P.NH + h) * D, st.tag + li, Lw.dbg & 1);
   }
 }
 
@@ -2569,7 +2573,8 @@ __device__ void flowm_mlp(const DecParams &P, const LayerW &Lw, int li, int item
   __syncthreads();
   PROBE(4);
   for (int t = 0; t < m; ++t)
-    slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * Q6R, P.dpart + ((size_t)(ta + t) * P.nchunk + item) * D, want);
+    slice_gemv<MC, MT>(M.Rd, D, hq + t * 2 * Q6R, P.dpart + ((size_t)(ta + t) * P.nchunk + item) * D, want,
+                       Lw.dbg & 2);
 }
 
 // lm_head share of the verify step (tiles wg, wg + nwg, ...): every token's
@@ -2829,6 +2834,9 @@ struct mllm_model {
   uint64_t payload_bytes = 0;
   LayerW *d_layers = nullptr;
   std::vector<LayerW> layers;
+  std::vector<LayerW> layers_base;  // as created (the debug knobs edit layers)
+  int dbg_max_layers = -1, dbg_no_attn = 0, dbg_no_mlp = 0, dbg_mlp_to = -1;
+  bool dbg_on = false;              // some knob set: prompts take the pass path
   struct Named {
     std::string name;
     int storage, rows, cols;
@@ -3375,6 +3383,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   if (hipMemcpy(M->d_layers, M->layers.data(), sizeof(LayerW) * L, hipMemcpyHostToDevice) != hipSuccess)
     return fail(set_error(MLLM_ERR_HIP, "layer table upload"));
   P.layers = M->d_layers;
+  M->layers_base = M->layers;
 
   // tiles: QKV 16 rows x ng <= QC * QT chunks (d_model <= 1024); the MLP
   // tiles and slices fit MC * MT chunks (UNITS x ng and 2 x d_model), an
@@ -3656,6 +3665,49 @@ extern "C" const char *mllm_decode_kernel_name(const mllm_model *M) {
   return use_flow3(M, M->cache_len) ? "k_flow3" : names[M->aq_idx];
 }
 
+// The GPU engine's layer-truncation knobs (webgpu-metal.js:1263-1279, set
+// from the page's query string at app.js:1317-1325): only the first
+// max_layers layers run (< 0: all), no_attn drops every attention block,
+// no_mlp every MLP block, mlp_to < 0 keeps the MLP blocks of all layers,
+// else those of layers < mlp_to.  A dropped block adds nothing to the
+// residual: its output projection writes zero partials and (GPT-2) its bias
+// is left out, in every execution mode; so the logits are those of the
+// truncated network, as the reference's skipped dispatches give them.  Its
+// q/k/v rows still go to the KV cache (the reference leaves the dropped
+// layer's cache rows unwritten; no kept block reads them).  While a knob is
+// set, prompts run through the decode passes, not the batched path.
+extern "C" int mllm_set_debug(mllm_model *M, int max_layers, int no_attn, int no_mlp, int mlp_to) {
+  MLLM_CHECK(M, "null model");
+  const int L = M->cfg.n_layers;
+  MLLM_HIP(hipStreamSynchronize(M->stream));
+  bool on = false;
+  for (int li = 0; li < L; ++li) {
+    LayerW w = M->layers_base[li];
+    int d = 0;
+    if (max_layers >= 0 && li >= max_layers) d = 3;
+    if (no_attn) d |= 1;
+    if (no_mlp || (mlp_to >= 0 && li >= mlp_to)) d |= 2;
+    w.dbg = d;
+    if (d & 1) w.proj_b = nullptr;  // GPT-2: the attention block's bias goes with it
+    on |= d != 0;
+    M->layers[li] = w;
+  }
+  // GPT-2: the MLP block's bias enters the next layer's residual (or the final one)
+  for (int li = 1; li < L; ++li) M->layers[li].prev_mproj_b = (M->layers[li - 1].dbg & 2) ? nullptr : M->layers_base[li].prev_mproj_b;
+  M->P.last_mproj_b = (M->layers[L - 1].dbg & 2) ? nullptr : M->layers_base[L - 1].mproj_b;
+  MLLM_HIP(hipMemcpy(M->d_layers, M->layers.data(), sizeof(LayerW) * L, hipMemcpyHostToDevice));
+  if (M->chain_graph) {  // its kernel nodes hold the layers by value
+    (void)hipGraphExecDestroy(M->chain_graph);
+    M->chain_graph = nullptr;
+  }
+  M->dbg_max_layers = max_layers;
+  M->dbg_no_attn = no_attn != 0;
+  M->dbg_no_mlp = no_mlp != 0;
+  M->dbg_mlp_to = mlp_to;
+  M->dbg_on = on;
+  return 0;
+}
+
 extern "C" int mllm_flow_verify_tokens(const mllm_model *M) { return M && M->exec_mode >= 3 ? M->flowm_max : 0; }
 
 extern "C" int mllm_set_prefill(mllm_model *M, int min_tokens, int chunk_tokens) {
@@ -3683,7 +3735,7 @@ extern "C" int mllm_forward_prompt(mllm_model *M, const int32_t *ids, int n, flo
   MLLM_CHECK(M && ids, "null argument");
   MLLM_CHECK(n > 0 && n <= M->cfg.max_seq_len, "prompt length %d out of range", n);
   if (int rc = check_ids(M, ids, n)) return rc;
-  if (M->pf_min > 0 && n >= M->pf_min) {
+  if (M->pf_min > 0 && n >= M->pf_min && !M->dbg_on) {
     // the prompt in chunks; the last one also forms the logits
     MLLM_HIP(hipEventRecord(M->ev_pf, M->stream));
     for (int p0 = 0; p0 < n; p0 += M->pf.tc) {

@@ -128,6 +128,50 @@ export class HipPetitGPT {
     native.setExecMode(this._h, mode);
   }
 
+  // GpuPetitGPT's debug knobs (webgpu-metal.js:1263-1279, set by app.js:1317-1325
+  // from the page's query string): null / false restore the full network.
+  _applyDebug() {
+    const d = this._dbg;
+    native.setDebug(this._h, d.maxLayers == null ? -1 : d.maxLayers, d.noAttn ? 1 : 0, d.noMlp ? 1 : 0,
+                    d.mlpTo == null ? -1 : d.mlpTo);
+  }
+
+  get debugMaxLayers() {
+    return this._dbg ? this._dbg.maxLayers : null;
+  }
+
+  set debugMaxLayers(v) {
+    this._dbg = Object.assign({}, this._dbg || {}, { maxLayers: v });
+    this._applyDebug();
+  }
+
+  get debugNoAttn() {
+    return this._dbg ? !!this._dbg.noAttn : false;
+  }
+
+  set debugNoAttn(v) {
+    this._dbg = Object.assign({}, this._dbg || {}, { noAttn: !!v });
+    this._applyDebug();
+  }
+
+  get debugNoMlp() {
+    return this._dbg ? !!this._dbg.noMlp : false;
+  }
+
+  set debugNoMlp(v) {
+    this._dbg = Object.assign({}, this._dbg || {}, { noMlp: !!v });
+    this._applyDebug();
+  }
+
+  get debugMlpTo() {
+    return this._dbg ? this._dbg.mlpTo : null;
+  }
+
+  set debugMlpTo(v) {
+    this._dbg = Object.assign({}, this._dbg || {}, { mlpTo: v });
+    this._applyDebug();
+  }
+
   timing() {
     return native.lastTiming(this._h);
   }

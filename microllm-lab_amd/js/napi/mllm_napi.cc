@@ -337,6 +337,16 @@ napi_value SetPrefill(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+napi_value SetDebug(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  if (!get_args(env, info, 5, argv)) return nullptr;
+  Handle *h = get_handle(env, argv[0]);
+  if (!h) return nullptr;
+  MLLM_OK_OR_THROW("mllm_set_debug", mllm_set_debug(h->model, get_i32(env, argv[1]), get_i32(env, argv[2]),
+                                                    get_i32(env, argv[3]), get_i32(env, argv[4])));
+  return nullptr;
+}
+
 napi_value LastTiming(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!get_args(env, info, 1, argv)) return nullptr;
@@ -384,6 +394,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"forwardDecode", ForwardDecode}, {"forwardVerify", ForwardVerify}, {"decodeChain", DecodeChain},
       {"gemv", Gemv},               {"setExecMode", SetExecMode},   {"setPrefill", SetPrefill},   {"lastTiming", LastTiming},
       {"deviceBytes", DeviceBytes}, {"maxPassTokens", MaxPass},     {"version", Version},
+      {"setDebug", SetDebug},
   };
   for (const auto &f : fns) {
     napi_value v;

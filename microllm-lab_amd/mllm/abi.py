@@ -50,6 +50,7 @@ SIGNATURES = {
     "mllm_decode_kernel_name": ([P], C.c_char_p),
     "mllm_flow_verify_tokens": ([P], I),
     "mllm_set_prefill": ([P, I, I], I),
+    "mllm_set_debug": ([P, I, I, I, I], I),
     "mllm_model_device_bytes": ([P], C.c_uint64),
     "mllm_last_timing": ([P, P, P], I),
     "mllm_profile_decode": ([P, C.c_int32, I, P], I),

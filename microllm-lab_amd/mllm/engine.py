@@ -125,6 +125,25 @@ class PetitGPT:
         """Most tokens a verify pass runs in the persistent kernel (0: phase kernels)."""
         return int(abi.lib().mllm_flow_verify_tokens(self._h))
 
+    # ---------------------------------------------------------------- debug knobs
+    # GpuPetitGPT.debugMaxLayers / debugNoAttn / debugNoMlp / debugMlpTo
+    # (webgpu-metal.js:1263-1279): None / False restore the full network.
+    def _set_debug(self, **kw):
+        d = dict(getattr(self, "_dbg", {"max_layers": None, "no_attn": False, "no_mlp": False, "mlp_to": None}))
+        d.update(kw)
+        abi.call("mllm_set_debug", self._h, -1 if d["max_layers"] is None else int(d["max_layers"]),
+                 int(bool(d["no_attn"])), int(bool(d["no_mlp"])), -1 if d["mlp_to"] is None else int(d["mlp_to"]))
+        self._dbg = d
+
+    debugMaxLayers = property(lambda self: getattr(self, "_dbg", {}).get("max_layers"),
+                              lambda self, v: self._set_debug(max_layers=v))
+    debugNoAttn = property(lambda self: getattr(self, "_dbg", {}).get("no_attn", False),
+                           lambda self, v: self._set_debug(no_attn=v))
+    debugNoMlp = property(lambda self: getattr(self, "_dbg", {}).get("no_mlp", False),
+                          lambda self, v: self._set_debug(no_mlp=v))
+    debugMlpTo = property(lambda self: getattr(self, "_dbg", {}).get("mlp_to"),
+                          lambda self, v: self._set_debug(mlp_to=v))
+
     def set_prefill(self, min_tokens: int, chunk_tokens: int = 0):
         """Prompts of at least min_tokens tokens take the batched path (0: never),
         in chunks of at most chunk_tokens (0: the largest)."""

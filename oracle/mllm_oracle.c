@@ -496,6 +496,7 @@ struct orc_model {
   olayer *layers;
   float **kcache, **vcache;
   int cache_len;
+  int *dbg; /* per layer: bit 0 no attention block, bit 1 no MLP block (orc_set_debug) */
   oscratch s;
 };
 
@@ -716,6 +717,7 @@ void orc_model_destroy(orc_model *m) {
   free(m->kcache);
   free(m->vcache);
   free(m->layers);
+  free(m->dbg);
   free(m->rope_cos);
   free(m->rope_sin);
   free_scratch(&m->s);
@@ -723,6 +725,22 @@ void orc_model_destroy(orc_model *m) {
 }
 
 /* infer.js:348-358 */
+/* The GPU engine's debug knobs (webgpu-metal.js:1263-1279; app.js:1317-1325):
+ * layers >= max_layers run nothing (max_layers < 0: all run), no_attn skips
+ * every attention block, no_mlp every MLP block, mlp_to >= 0 the MLP blocks
+ * of layers >= mlp_to.  A skipped block leaves the residual as it is (and,
+ * as in the reference, writes nothing to its KV cache). */
+void orc_set_debug(orc_model *m, int max_layers, int no_attn, int no_mlp, int mlp_to) {
+  if (!m->dbg) m->dbg = calloc((size_t)m->cfg.n_layers, sizeof(int));
+  for (int li = 0; li < m->cfg.n_layers; li++) {
+    int d = 0;
+    if (max_layers >= 0 && li >= max_layers) d = 3;
+    if (no_attn) d |= 1;
+    if (no_mlp || (mlp_to >= 0 && li >= mlp_to)) d |= 2;
+    m->dbg[li] = d;
+  }
+}
+
 void orc_reset_cache(orc_model *m) {
   for (int i = 0; i < m->cfg.n_layers; i++) {
     memset(m->kcache[i], 0, sizeof(float) * (size_t)m->cfg.n_kv_heads * m->cfg.max_seq_len * m->head_dim);
@@ -881,12 +899,18 @@ static void forward_body(orc_model *m, const int32_t *ids, int t, int past) {
   const int D = c->d_model;
   embed(m, ids, t, s->x, past);
   for (int li = 0; li < c->n_layers; li++) {
-    norm(m, s->x, m->layers[li].norm1, s->xn, t);
-    const float *att = attention(m, li, s->xn, t, past);
-    for (int i = 0; i < t * D; i++) s->x[i] = (float)((double)s->x[i] + (double)att[i]);
-    norm(m, s->x, m->layers[li].norm2, s->xn, t);
-    const float *ff = ffn(m, li, s->xn, t);
-    for (int i = 0; i < t * D; i++) s->x[i] = (float)((double)s->x[i] + (double)ff[i]);
+    /* webgpu-metal.js:1263-1279: a dropped block's dispatches are skipped */
+    const int dbg = m->dbg ? m->dbg[li] : 0;
+    if (!(dbg & 1)) {
+      norm(m, s->x, m->layers[li].norm1, s->xn, t);
+      const float *att = attention(m, li, s->xn, t, past);
+      for (int i = 0; i < t * D; i++) s->x[i] = (float)((double)s->x[i] + (double)att[i]);
+    }
+    if (!(dbg & 2)) {
+      norm(m, s->x, m->layers[li].norm2, s->xn, t);
+      const float *ff = ffn(m, li, s->xn, t);
+      for (int i = 0; i < t * D; i++) s->x[i] = (float)((double)s->x[i] + (double)ff[i]);
+    }
   }
   m->cache_len = past + t;
   norm(m, s->x, m->norm_f, s->xn, t);

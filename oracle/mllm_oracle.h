@@ -101,6 +101,8 @@ typedef struct orc_model orc_model;
 orc_model *orc_model_create(const orc_config *cfg, const uint8_t *payload, const orc_tensor *tensors, int n_tensors);
 void orc_model_destroy(orc_model *m);
 void orc_reset_cache(orc_model *m);
+/* webgpu-metal.js:1263-1279: the GPU engine's layer-truncation knobs */
+void orc_set_debug(orc_model *m, int max_layers, int no_attn, int no_mlp, int mlp_to);
 int orc_cache_len(const orc_model *m);
 void orc_set_cache_len(orc_model *m, int len);
 /* infer.js:553-577 -- returns a pointer to the model's logits scratch [V]. */

@@ -79,6 +79,7 @@ def lib():
             "orc_reset_cache": [P],
             "orc_cache_len": [P],
             "orc_set_cache_len": [P, i],
+            "orc_set_debug": [P, i, i, i, i],
             "orc_forward_prompt": [P, P, i],
             "orc_forward_decode": [P, C.c_int32],
             "orc_forward_multi": [P, P, i, P],
@@ -98,7 +99,8 @@ def lib():
                      "orc_gemv_f32_js", "orc_gemv_q4_wasm", "orc_gemv_q8_wasm", "orc_gemv_f32_wasm",
                      "orc_rms_norm_wasm", "orc_silu_mul_wasm", "orc_rms_norm_js", "orc_layer_norm_js",
                      "orc_silu_mul_js", "orc_gelu_new_js", "orc_build_rope", "orc_apply_rope_js", "orc_softmax_js",
-                     "orc_model_destroy", "orc_reset_cache", "orc_set_cache_len", "orc_forward_multi"):
+                     "orc_model_destroy", "orc_reset_cache", "orc_set_cache_len", "orc_forward_multi",
+                     "orc_set_debug"):
             getattr(L, name).restype = None
         _lib = L
     return _lib
@@ -320,6 +322,11 @@ class OracleModel:
 
     def reset_cache(self):
         lib().orc_reset_cache(self.h)
+
+    def set_debug(self, max_layers=None, no_attn=False, no_mlp=False, mlp_to=None):
+        """The GPU engine's debug knobs (webgpu-metal.js:1263-1279)."""
+        lib().orc_set_debug(self.h, -1 if max_layers is None else int(max_layers), int(bool(no_attn)),
+                            int(bool(no_mlp)), -1 if mlp_to is None else int(mlp_to))
 
     def forward_prompt(self, ids) -> np.ndarray:
         a = np.ascontiguousarray(np.asarray(ids, np.int32))

@@ -3,8 +3,10 @@
  * load -> new engine -> generate with streaming onToken).
  *   node run_generate.mjs <model.pgw> <spec.json>   -> prints one JSON line
  * spec: { prompt: [...], maxNewTokens, eosId, mode, specK, kvFp16, execMode, prefillMin,
- *         decodeLogits: [ids...] }  (decodeLogits: teacher-forced tokens whose
- *         logits are returned for comparison)
+ *         decodeLogits: [ids...], debug: {maxLayers, noAttn, noMlp, mlpTo} }
+ *         (decodeLogits: teacher-forced tokens whose logits are returned for
+ *         comparison; debug: GpuPetitGPT's debug knobs, set as properties the
+ *         way app.js:1317-1325 sets them)
  */
 import fs from "fs";
 import { parsePgw } from "../../microllm-lab_amd/js/weights.mjs";
@@ -15,6 +17,12 @@ async function main() {
   const spec = JSON.parse(fs.readFileSync(specPath, "utf8"));
   const bundle = parsePgw(fs.readFileSync(pgwPath));
   const model = new HipPetitGPT(bundle, { kvFp16: !!spec.kvFp16, execMode: spec.execMode, prefillMin: spec.prefillMin });
+  if (spec.debug) {
+    if (spec.debug.maxLayers !== undefined) model.debugMaxLayers = spec.debug.maxLayers;
+    if (spec.debug.noAttn !== undefined) model.debugNoAttn = spec.debug.noAttn;
+    if (spec.debug.noMlp !== undefined) model.debugNoMlp = spec.debug.noMlp;
+    if (spec.debug.mlpTo !== undefined) model.debugMlpTo = spec.debug.mlpTo;
+  }
   const streamed = [];
   const res = await model.generate(spec.prompt, {
     maxNewTokens: spec.maxNewTokens,

@@ -50,21 +50,29 @@ def test_js_parse_pgw_and_sampling(tmp_path, oracle_lib):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("arch,mode,prefill_min", [("llama", "greedy", None), ("llama", "chain", None),
-                                                   ("llama", "spec", None), ("gpt2", "chain", None),
-                                                   ("llama", "greedy", 0)])
-def test_js_engine_matches_python_engine(tmp_path, arch, mode, prefill_min):
+@pytest.mark.parametrize("arch,mode,prefill_min,debug", [("llama", "greedy", None, None), ("llama", "chain", None, None),
+                                                         ("llama", "spec", None, None), ("gpt2", "chain", None, None),
+                                                         ("llama", "greedy", 0, None),
+                                                         ("llama", "chain", None, {"maxLayers": 1, "noAttn": True}),
+                                                         ("gpt2", "greedy", None, {"mlpTo": 1})])
+def test_js_engine_matches_python_engine(tmp_path, arch, mode, prefill_min, debug):
     bundle_bytes = pgw.make_model(pgw.small_config(arch), seed=5)
     (tmp_path / "m.pgw").write_bytes(bundle_bytes)
     prompt = [3, 9, 27, 81, 3, 9, 27, 81, 3, 9]
     spec = {"prompt": prompt, "maxNewTokens": 16, "mode": mode, "specK": 4, "decodeLogits": [5, 6]}
     if prefill_min is not None:
         spec["prefillMin"] = prefill_min  # the prompt through the 16-token passes
+    if debug is not None:
+        spec["debug"] = debug  # the debug knobs as properties, on the Node side and here
     (tmp_path / "spec.json").write_text(json.dumps(spec))
     out = run_node("run_generate.mjs", str(tmp_path / "m.pgw"), str(tmp_path / "spec.json"))
     g = mllm.PetitGPT(pgw.parse_pgw(bundle_bytes))
     if prefill_min is not None:
         g.set_prefill(prefill_min)
+    if debug is not None:
+        g.debugMaxLayers = debug.get("maxLayers")
+        g.debugNoAttn = debug.get("noAttn", False)
+        g.debugMlpTo = debug.get("mlpTo")
     want = g.generate(prompt, maxNewTokens=16, mode="greedy")
     rows = [g.forwardPrompt(prompt).copy()] + [g.forwardDecode(t).copy() for t in (5, 6)]
     g.destroy()

@@ -203,3 +203,45 @@ def test_cycle_model_follows_its_cycle(oracle_lib):
         lg = ref.forward_decode(tok)
     ref.close()
     assert worst > 1.0, worst
+
+
+def test_oracle_debug_knobs(oracle_lib):
+    """The GPU engine's layer-truncation knobs restated in the oracle
+    (webgpu-metal.js:1263-1279).  With no layer run, the logits are the
+    closed form lm_head . (rmsnorm(embedding) * norm_f) (infer.js:134-143,
+    360-420, 597-600) for every token; dropping both blocks everywhere is no
+    layer at all; max_layers = L and mlp_to = L are the full network; and the
+    knobs restore it."""
+    cfg = pgw.small_config("llama", max_seq_len=64)
+    bundle = pgw.parse_pgw(pgw.make_llama(cfg, seed=31))
+    ref = oracle_lib.OracleModel(bundle)
+    t = bundle.tensors
+    def arr(name, dtype, key="offset", nb="nbytes"):
+        return np.frombuffer(bundle.buffer, dtype, t[name][nb] // np.dtype(dtype).itemsize,
+                             bundle.payload_off + t[name][key])
+    lm = oracle_lib.dequant_q4(arr("lm_head", np.uint8).reshape(cfg.vocab_size, -1),
+                               arr("lm_head", np.float32, "scaleOffset", "scaleNbytes").reshape(cfg.vocab_size, -1))
+    gf = arr("norm_f", np.float32).astype(np.float64)
+    ids = [5, 17, 3, 99]
+    full = ref.forward_prompt(ids)
+    ref.set_debug(max_layers=0)
+    for i, tok in enumerate(ids):
+        ref.reset_cache()
+        got = ref.forward_prompt(ids[:i + 1])
+        e = lm[tok].astype(np.float64)
+        xn = (e / np.sqrt(np.mean(e * e) + 1e-6) * gf).astype(np.float32).astype(np.float64)
+        want = lm.astype(np.float64) @ xn
+        assert np.abs(got - want).max() < 1e-4 * np.abs(want).max()
+    ref.reset_cache()
+    none = ref.forward_prompt(ids)
+    ref.set_debug(no_attn=True, no_mlp=True)
+    ref.reset_cache()
+    assert np.array_equal(ref.forward_prompt(ids), none)
+    for kw in ({"max_layers": cfg.n_layers}, {"mlp_to": cfg.n_layers}, {}):
+        ref.set_debug(**kw)
+        ref.reset_cache()
+        assert np.array_equal(ref.forward_prompt(ids), full)
+    ref.set_debug(no_mlp=True)
+    ref.reset_cache()
+    assert not np.array_equal(ref.forward_prompt(ids), full)
+    ref.close()
