@@ -33,6 +33,10 @@ One JSON line on stdout carries, besides the driver's fields:
 
     python bench.py --prefill-only   config 5's prompt through the batched
                                      path three times (for profilers)
+    python bench.py --decode-360m    config 5's decode alone: the prompt, then
+                                     the 511-step chain as one dispatch (for
+                                     profilers; --exec-mode 4 keeps it an
+                                     ordinary launch)
 """
 from __future__ import annotations
 
@@ -587,12 +591,21 @@ def bench_configs(mllm, pgw, args, oracle=None):
     t0 = time.perf_counter()
     ids = g.decodeChain(first, 511)
     dt = time.perf_counter() - t0
-    mean_seq = 1536 + 256
+    chain_ms, n = g.last_timing()
+    # step i of the chain attends over 1537 + i cached positions
+    chain_bytes = sum(token_bytes(cfg, 1537 + i, 2) for i in range(n))
+    rec = traffic_record("k_flow3_360m_fp16kv")
+    achieved = chain_bytes / (chain_ms * 1e-3) / 1e9
     res["smollm2_360m_fp16kv"] = {"prefill_ms": round(ttft * 1e3, 2), "prefill_gpu_ms": round(prefill_gpu_ms, 2),
                                   "prefill_tok_s": round(1536 / ttft, 1),
                                   "prefill_pass_path_ms": round(pass_s * 1e3, 1),
                                   "decode_tok_s": round(len(ids) / dt, 1),
-                                  "decode_step_gbs": round(token_bytes(cfg, mean_seq, 2) / (dt / len(ids)) / 1e9, 1)}
+                                  "decode_roofline": {
+                                      "bound": "hbm", "kernel": f"{g.decodeKernel} (one launch = the 511-step chain)",
+                                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                      "frac": round(achieved / HBM_PEAK_GBS, 5),
+                                      "traffic": None if rec is None else int(rec["hbm_bytes_per_step"] * n),
+                                      "bytes_per_launch": int(chain_bytes), "us_per_launch": round(chain_ms * 1e3, 1)}}
     if oracle is not None:
         # the oracle keeps an f32 cache (the reference's); 1536 prompt tokens
         # would take minutes, so the cache length is set to 1792 directly
@@ -623,6 +636,9 @@ def main():
                     help="the sweep with few launches per shape and no graph replays (counter runs)")
     ap.add_argument("--verify-only", action="store_true",
                     help="only config 3's verify passes at M = 1, 5, 9 (and the batched path at M = 5, 9)")
+    ap.add_argument("--decode-360m", action="store_true",
+                    help="only config 5's decode: the 1536-token prompt (batched), then one chained decode of 511 "
+                         "steps to 2048 context (one persistent-kernel dispatch; the traffic record behind it)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (counter calibration for the traffic figure)")
     args = ap.parse_args()
@@ -664,6 +680,22 @@ def main():
             log(f"[bench] prefill 1536 tokens: {runs[-1]} ms (GPU)")
         g.destroy()
         print(json.dumps({"prefill_gpu_ms": runs, "tokens": 1536, "workload": "smollm2-360m fp16 KV (config 5)"}))
+        return
+    if args.decode_360m:
+        cfg = pgw.CONFIGS["smollm2-360m"]
+        g = mllm.PetitGPT(pgw.parse_pgw(pgw.make_llama(cfg, seed=0)), kv_fp16=True, exec_mode=args.exec_mode)
+        prompt = [int(v) for v in np.random.default_rng(5).integers(0, cfg.vocab_size, 1536)]
+        g.forwardPrompt(prompt)
+        kname = g.decodeKernel
+        ids = g.decodeChain(g.last_argmax, 511)
+        ms, n = g.last_timing()
+        chain_bytes = sum(token_bytes(cfg, 1537 + i, 2) for i in range(n))
+        g.destroy()
+        print(json.dumps({"workload": "smollm2-360m q4, fp16 KV: 511 chained decode steps after a 1536-token prompt "
+                                      "(config 5)", "kernel": kname, "exec_mode": args.exec_mode, "steps": n,
+                          "gpu_ms": round(ms, 3), "us_per_step": round(ms * 1e3 / n, 2),
+                          "tok_s": round(n / (ms * 1e-3), 1), "algorithmic_bytes_per_step": int(chain_bytes / n),
+                          "first_ids": ids[:6]}))
         return
     dec = bench_decode(mllm, pgw, torch, args)
     log(f"[bench] decode {dec['value']:.1f} tok/s, phases {dec['phase_us']}")
