@@ -239,13 +239,15 @@ int mllm_set_debug(mllm_model *model, int max_layers, int no_attn, int no_mlp, i
 
 /* Prompts of at least min_tokens tokens (default 2; 0 = never) are
  * processed in batches (no counterpart in the reference, whose GPU path runs
- * a prompt token by token, webgpu.js:1178-1187): tokens 0 .. n-2 go through
- * every layer as Q4 GEMMs on the int8 matrix cores and one causal attention
- * kernel per layer, in chunks of up to 2048 tokens, and write the KV cache;
- * the last token runs as a decode step and yields the logits.  Shorter
+ * a prompt token by token, webgpu.js:1178-1187): the tokens go through every
+ * layer as Q4 GEMMs on the int8 matrix cores and one causal attention kernel
+ * per layer, in chunks of up to 2048 tokens, and write the KV cache; the last
+ * chunk runs its last layer's attention and MLP on its final 32-token tile
+ * and forms the last token's logits (final norm, lm_head, argmax).  Shorter
  * prompts run in passes of mllm_max_pass_tokens() tokens through the decode
- * phases.  The two agree to the logits tolerance, not bit for bit (the
- * batched path quantises activations per token instead of per group).
+ * phases.  Both take 24-bit activations per token and 32-element group; they
+ * agree to 2e-5 of the logits' scale, not bit for bit (different summation
+ * orders: the matrix cores' accumulation against the decode GEMVs').
  * chunk_tokens (1 .. 2048 or max_seq_len if smaller; 0 = the largest) bounds
  * the tokens per chunk; later chunks read the earlier ones' keys from the
  * cache.  Models with more than 4 query heads per KV head, or d_model / d_ff

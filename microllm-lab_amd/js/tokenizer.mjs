@@ -159,46 +159,73 @@ export function encodeChat(tok, messages, defaultSystem = null) {
   return encodeMessages(tok, messages, { template: "petitgpt", defaultSystem });
 }
 
-/** encodeMessages (tokenizer.js:199-272): a conversation as prompt ids for the card's template. */
-export function encodeMessages(tok, messages, card = {}) {
-  card = card || {};
-  const msgs = messages.map((m) => ({
+// The first of its arguments that is neither undefined nor null (the
+// reference's `??` chains; Node 12 has no `??`).
+const pick = (...vals) => vals.find((v) => v !== undefined && v !== null);
+
+// A conversation's turns as every layout reads them: the role trimmed and
+// lower-cased, the content a string cut to its last MAX_CHARS units.
+function turnsOf(messages) {
+  return messages.map((m) => ({
     role: String(m.role).trim().toLowerCase(),
     content: jsText(m.content == null ? "" : String(m.content)),
   }));
-  const tpl = card.template || "petitgpt";
-  const specials = card.specials || {};
-  const first = (...vals) => vals.find((v) => v !== undefined && v !== null);
-  if (tpl === "completion") return tok.encode(msgs.length ? msgs[msgs.length - 1].content : "");
-  if (tpl === "chatml") {
-    if (card.defaultSystem && (!msgs.length || msgs[0].role !== "system"))
-      msgs.unshift({ role: "system", content: card.defaultSystem });
-    const imStart = first(tok.special.get("<|im_start|>"), specials["<|im_start|>"], card.bosId, 1);
-    const imEnd = first(tok.special.get("<|im_end|>"), specials["<|im_end|>"], card.eosId, 2);
+}
+
+// The card's default system turn in front, unless the conversation opens with one.
+function withSystem(turns, text) {
+  return text && !(turns.length && turns[0].role === "system") ? [{ role: "system", content: text }].concat(turns) : turns;
+}
+
+// One id layout per template name (tokenizer.js:208-271).  The ids and the
+// error messages are the interface: a prompt must come out as the same ids,
+// and a bad conversation must fail with the same message.
+const LAYOUTS = {
+  // the last turn's text alone
+  completion(tok, turns) {
+    return tok.encode(turns.length ? turns[turns.length - 1].content : "");
+  },
+  // <|im_start|>role\n content <|im_end|>\n per turn, then the assistant's header;
+  // the markers from the tokenizer's specials, then the card's, then its bos / eos
+  chatml(tok, turns, card, specials) {
+    const open = pick(tok.special.get("<|im_start|>"), specials["<|im_start|>"], card.bosId, 1);
+    const close = pick(tok.special.get("<|im_end|>"), specials["<|im_end|>"], card.eosId, 2);
     const nl = tok.encode("\n");
-    const ids = [];
-    for (const m of msgs) ids.push(imStart, ...tok.encode(m.role), ...nl, ...tok.encode(m.content), imEnd, ...nl);
-    ids.push(imStart, ...tok.encode("assistant"), ...nl);
-    return ids;
-  }
-  if (card.defaultSystem && (!msgs.length || msgs[0].role !== "system"))
-    msgs.unshift({ role: "system", content: card.defaultSystem });
-  const bos = first(card.bosId, SPECIAL.BOS);
-  const eos = first(card.eosId, SPECIAL.EOS);
-  const roleId = {
-    system: first(specials["<|system|>"], SPECIAL.SYSTEM),
-    user: first(specials["<|user|>"], SPECIAL.USER),
-    assistant: first(specials["<|assistant|>"], SPECIAL.ASSISTANT),
-  };
-  const ids = [bos];
-  for (const m of msgs) {
-    if (roleId[m.role] === undefined) throw new Error(`invalid role ${m.role}`);
-    const content = tok.encode(m.content);
-    if (!content.length) throw new Error("empty message encoding");
-    ids.push(roleId[m.role], ...content);
-    if (m.role === "assistant") ids.push(eos);
-  }
-  if (!msgs.length || msgs[msgs.length - 1].role !== "user") throw new Error("prompt must end with a user turn");
-  ids.push(roleId.assistant);
-  return ids;
+    const header = (role) => [open].concat(tok.encode(role), nl);
+    const out = [];
+    for (const turn of withSystem(turns, card.defaultSystem)) out.push(...header(turn.role), ...tok.encode(turn.content), close, ...nl);
+    return out.concat(header("assistant"));
+  },
+  // bos, then per turn its role marker and text (an assistant turn closed by
+  // eos); the conversation must end with the user, and the assistant's marker
+  // follows.  Turns are checked in order, as they are laid out.
+  petitgpt(tok, turns, card, specials) {
+    const marker = {
+      system: pick(specials["<|system|>"], SPECIAL.SYSTEM),
+      user: pick(specials["<|user|>"], SPECIAL.USER),
+      assistant: pick(specials["<|assistant|>"], SPECIAL.ASSISTANT),
+    };
+    const all = withSystem(turns, card.defaultSystem || null);
+    const out = [pick(card.bosId, SPECIAL.BOS)];
+    for (const turn of all) {
+      const id = marker[turn.role];
+      if (id === undefined || id === null) throw new Error(`invalid role ${turn.role}`);
+      const text = tok.encode(turn.content);
+      if (text.length === 0) throw new Error("empty message encoding");
+      out.push(id, ...text);
+      if (turn.role === "assistant") out.push(pick(card.eosId, SPECIAL.EOS));
+    }
+    if (!all.length || all[all.length - 1].role !== "user") throw new Error("prompt must end with a user turn");
+    out.push(marker.assistant);
+    return out;
+  },
+};
+
+/** encodeMessages (tokenizer.js:199-272): a conversation as prompt ids for the card's template. */
+export function encodeMessages(tok, messages, card = {}) {
+  card = card || {};
+  const layout = card.template || "petitgpt";
+  // any other template name takes the petitgpt layout, as in the reference
+  const build = layout === "completion" || layout === "chatml" ? LAYOUTS[layout] : LAYOUTS.petitgpt;
+  return build(tok, turnsOf(messages), card, card.specials || {});
 }

@@ -230,10 +230,14 @@ def encode_messages(tok: Tokenizer, messages, card: Optional[dict] = None) -> Li
         msgs.insert(0, {"role": "system", "content": default_system})
     bos = card.get("bosId") if card.get("bosId") is not None else SPECIAL["BOS"]
     eos = card.get("eosId") if card.get("eosId") is not None else SPECIAL["EOS"]
+    def marker(name, default):  # `??`: a null entry falls back too
+        v = specials.get(name)
+        return default if v is None else v
+
     role_id = {
-        "system": specials.get("<|system|>", SPECIAL["SYSTEM"]),
-        "user": specials.get("<|user|>", SPECIAL["USER"]),
-        "assistant": specials.get("<|assistant|>", SPECIAL["ASSISTANT"]),
+        "system": marker("<|system|>", SPECIAL["SYSTEM"]),
+        "user": marker("<|user|>", SPECIAL["USER"]),
+        "assistant": marker("<|assistant|>", SPECIAL["ASSISTANT"]),
     }
     ids = [bos]
     for m in msgs:

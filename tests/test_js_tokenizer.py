@@ -110,6 +110,15 @@ def test_js_tokenizer_merges_specials_and_templates(tmp_path):
         ([{"role": "user", "content": ""}], {"template": "petitgpt"}),
         ([{"role": "system", "content": "s"}, {"role": "user", "content": "u"}],
          {"template": "petitgpt", "bosId": 7, "eosId": 8, "specials": {"<|user|>": 11, "<|assistant|>": 12}}),
+        # a null special falls back to the fixed id; an unknown template name
+        # takes the petitgpt layout; empty conversations in every layout
+        ([{"role": "user", "content": "u"}], {"template": "petitgpt", "specials": {"<|user|>": None}}),
+        ([{"role": "user", "content": "u"}], {"template": "llama3", "defaultSystem": "s"}),
+        ([], {"template": "completion"}),
+        ([], {"template": "chatml"}),
+        ([], {"template": "chatml", "defaultSystem": "s"}),
+        ([], {"template": "petitgpt"}),
+        ([{"role": "assistant", "content": "b"}, {"role": "tool", "content": ""}], {"template": "petitgpt"}),
     ]
     out = run_js(tmp_path, {"tokenizer": spec, "encode": texts,
                             "messages": [{"messages": m, "card": c} for m, c in convs]})
