@@ -470,7 +470,7 @@ def verify_pass_us(g, prompt, m, reps=20):
 
 
 def batched_pass_us(g, prompt, m, reps=20):
-    """GPU time of the batched prompt path (int8 matrix-core GEMMs) over the
+    """GPU time of the batched prompt path (matrix-core GEMMs) over the
     same m rows, as a prompt at position 0 (its lm_head forms the last row
     only): the matrix-core alternative to a verify pass of m rows.  Prompts
     of two tokens or more take that path by default."""

@@ -240,14 +240,15 @@ int mllm_set_debug(mllm_model *model, int max_layers, int no_attn, int no_mlp, i
 /* Prompts of at least min_tokens tokens (default 2; 0 = never) are
  * processed in batches (no counterpart in the reference, whose GPU path runs
  * a prompt token by token, webgpu.js:1178-1187): the tokens go through every
- * layer as Q4 GEMMs on the int8 matrix cores and one causal attention kernel
- * per layer, in chunks of up to 2048 tokens, and write the KV cache; the last
+ * layer as Q4 GEMMs and one causal attention kernel on the f16 matrix
+ * cores, in chunks of up to 2048 tokens, and write the KV cache; the last
  * chunk runs its last layer's attention and MLP on its final 32-token tile
  * and forms the last token's logits (final norm, lm_head, argmax).  Shorter
  * prompts run in passes of mllm_max_pass_tokens() tokens through the decode
- * phases.  Both take 24-bit activations per token and 32-element group; they
- * agree to 2e-5 of the logits' scale, not bit for bit (different summation
- * orders: the matrix cores' accumulation against the decode GEMVs').
+ * phases.  The GEMMs take each activation exactly (three f16 pieces of the
+ * row scaled by a power of two), the decode GEMVs as 24-bit integers per
+ * 32-element group; the two agree to 2e-5 of the logits' scale, not bit for
+ * bit (different roundings and summation orders).
  * chunk_tokens (1 .. 2048 or max_seq_len if smaller; 0 = the largest) bounds
  * the tokens per chunk; later chunks read the earlier ones' keys from the
  * cache.  Models with more than 4 query heads per KV head, or d_model / d_ff

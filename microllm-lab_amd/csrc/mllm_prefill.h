@@ -1,8 +1,7 @@
 // mllm_prefill.h -- batched prompt processing (infer.js:553-577 forwardPrompt):
-// every layer of a chunk of prompt tokens as a few wide kernels (Q4 GEMMs on
-// int8 matrix cores, one causal attention kernel), writing the KV cache.
-// The engine runs the prompt's last token through its decode step, which
-// produces the logits from that cache.
+// every layer of a chunk of prompt tokens as a few wide kernels (Q4 GEMMs and
+// one causal attention kernel on the f16 matrix cores), writing the KV cache;
+// the last chunk also forms the last token's logits.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -43,7 +42,7 @@ struct PfArgs {
   float *q;      // [tc][D] roped queries
   float *att;    // [tc][D] attention output
   float *h;      // [tc][FF] MLP activation
-  uint8_t *px;   // [tc / 32][max(D, FF) / 32]: 3 x [64 lanes][16] int8 activation planes, [32] f32 group scales
+  uint8_t *px;   // per 32-token tile: [K / 32][3 pieces x 2 K halves][64 lanes][16 B] f16, then [32] int exponents
 };
 
 // The tiled copy of a Q4 matrix that the prefill GEMMs read (rows and cols

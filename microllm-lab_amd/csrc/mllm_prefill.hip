@@ -2,33 +2,35 @@
 // (infer.js:553-577): a chunk of T prompt tokens goes through every layer as
 // a handful of wide kernels instead of 16-token passes of the decode phases.
 //
-// Q4 GEMMs on int8 matrix cores.  Activations are quantised per token and
-// 32-element group (the Q4 group) to 24-bit integers, xi = rint(x * Q3MAX /
-// amax) (amax = max |x| of the group; sx = amax / Q3MAX), which moves x by at
-// most 6.0e-8 amax: one float32 rounding of the group's largest element.  xi
-// is split into three signed bytes, xi = 65536 h + 256 m + l (l and m the
-// low bytes sign-extended, |xi| <= Q3MAX keeps h within [-128, 127]).  With
-// the weights as signed nibbles q - 8 the group's dot product is exact:
-//   sum_k (q_k - 8) xi_k = 65536 sum (q-8) h + 256 sum (q-8) m + sum (q-8) l,
-// three v_mfma_i32_32x32x32_i8 per 32-row x 32-token x 32-column group (K =
-// 32 = one Q4 group), combined in 32-bit wrapping arithmetic (the exact sum
-// is below 2^31 in magnitude: 32 * 8 * Q3MAX).  The group's float
-// contribution is added as
-//   acc = fma((float)dot, w_scale * sx, acc)
-// in group order.  The VALU epilogue (five operations per output and group)
-// and the matrix cores bound these GEMMs together.
+// Q4 GEMMs on the f16 matrix cores with exact operands.  Each token's row
+// is scaled by a power of two, 2^-e with e = ilogb(max |x|) - 14 (so the
+// row's largest element lands in [2^14, 2^15), far from the f16 limits), and
+// every scaled element x' is split into three f16 pieces,
+//   p1 = f16(x'),  p2 = f16(x' - p1),  p3 = f16(x' - p1 - p2),
+// whose sum is x' exactly (24 significant bits in three 11-bit pieces; only
+// elements below 2^-16 of the row's max can lose bits, at 2^-39 of it).  The
+// weights q - 8 of a Q4 group are small integers, exact in f16: the packed
+// nibbles become f16 pairs 1024 + q with one v_perm_b32 against 0x64 bytes,
+// then one packed f16 add of -1032.  A group (K = 32) is six
+// v_mfma_f32_32x32x16_f16 per 32-row x 32-token sub-tile (three pieces x two
+// K halves) chained in one f32 accumulator z, so the group's dot with the
+// exact activations costs no integer combine; the epilogue is
+//   acc = fma(z, w_scale, acc)
+// in group order, one VALU operation per output and group, and the token's
+// 2^e is applied once after the last group.  The matrix cores and the
+// weight conversion then bound these GEMMs about equally.
 //
-// Operand layouts (v_mfma_i32_32x32x32_i8, checked on gfx950): A (the
-// activations) lane l holds row l % 32 (a token), 16 bytes of k; B (the
-// weights) lane l holds column l % 32 (a weight row), the same 16 k; D lane l
-// value v is (row 8(v/4) + 4(l/32) + v%4, column l % 32).  Only the pairing of
-// A's and B's k matters, so lane half hh = l / 32 takes the group's elements
-// 16hh .. 16hh+15 in the order its weight bytes unpack: the low nibbles of
-// packed bytes 8hh .. 8hh+3 (elements 0, 2, 4, 6), of bytes 8hh+4 .. 8hh+7
-// (elements 8 .. 14), then the high nibbles of each (elements 1 .. 7 and
-// 9 .. 15, odd).  The activation planes are stored in that order, PX_TILE
-// bytes per (32-token tile, group): the h plane (half 0 then half 1, 16 bytes
-// per token each), the m plane, the l plane, then the 32 tokens' scales.
+// Operand layouts (v_mfma_f32_32x32x16_f16, checked on gfx950): A (the
+// activations) lane l holds row l % 32 (a token) and 8 halves of k; B (the
+// weights) lane l holds column l % 32 (a weight row) and the same 8 k; D
+// lane l value v is (row 8(v/4) + 4(l/32) + v%4, column l % 32).  Only the
+// pairing of A's and B's k matters: lane half hh = l / 32 holds the group's
+// elements 16hh .. 16hh+15 (its 8 packed bytes), the first K half of the
+// group takes elements 0 2 4 6 1 3 5 7 of those (the nibble order the
+// conversion gives), the second 8 10 12 14 9 11 13 15.  The activation
+// pieces are stored in that order, PXG bytes per (32-token tile, group):
+// piece p, K half m at ((2p + m) * 64 + lane) * 16; after a tile's groups,
+// its 32 tokens' exponents e.
 //
 // Attention: causal, one (32-query tile, KV head) per workgroup, 32-key
 // blocks staged in LDS, S = Q K^T and O = P V on the f16 matrix cores with
@@ -52,14 +54,18 @@
 namespace mllm {
 namespace {
 
-constexpr float Q3MAX = 8355000.0f;  // |xi| bound of the 24-bit activations (three signed bytes need < 8355712)
-constexpr int PX_PLANE = 1024;  // bytes per plane of a (32-token tile, group)
-constexpr int PX_SC = 3 * PX_PLANE;  // offset of the 32 tokens' scales
-constexpr int PX_TILE = PX_SC + 128;  // bytes per (32-token tile, group)
-constexpr int PF_HD = 64;       // head dimension
+constexpr int PXG = 6 * 1024;  // bytes per (32-token tile, group): 3 pieces x 2 K halves x 64 lanes x 16
+constexpr int PX_TOK = 128;    // after a tile's groups: its 32 tokens' exponents (int)
+constexpr int PF_HD = 64;      // head dimension
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
+// bytes per 32-token tile of activations with K columns
+__host__ __device__ constexpr size_t px_tile_bytes(int K) { return (size_t)(K >> 5) * PXG + PX_TOK; }
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 enum { EPI_QKV = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_GELU = 3 };
 enum { NORM_RMS = 0, NORM_LN = 1, NORM_NONE = 2 };
@@ -95,8 +101,8 @@ __global__ __launch_bounds__(WG) void k_pf_embed(PfArgs A, int n, int pos0) {
 
 // ---------------------------------------------------------------- norm + quantise
 // One token row of K floats per wave (tokens t0 .. t1-1): optional RMSNorm /
-// LayerNorm (the decode engine's formulas), then the 24-bit planes and the
-// group scales.  Wave reductions only; the row is re-read from cache per pass.
+// LayerNorm (the decode engine's formulas), then the row's exponent and the
+// three f16 pieces of every scaled element.  Wave reductions only.
 template <int NORM>
 __device__ __forceinline__ float4 pf_norm_col(const float4 *xr, const float4 *g4, int nq, int q, float r, float mean) {
   const float4 v = xr[q];
@@ -145,11 +151,20 @@ __device__ __forceinline__ void pf_norm_stats(const float4 *xr, int K, float eps
 
 // Lane u of the wave owns (group u / 2, half u % 2) of the row -- 16
 // consecutive elements, PPL such units per lane (K <= 1024 PPL) -- held in
-// registers from one load; the two halves of a group are neighbouring lanes
-// (their amax is joined with one DPP step).  The unit's h, m and l operands
-// go out as three 16-byte stores.
-__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-  return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) | ((uint32_t)d << 24);
+// registers from one load.  The unit's pieces go out as six 16-byte stores
+// (three pieces x two K halves).
+__device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
+  const v2h v = {a, b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// The three f16 pieces of x (x = p[0] + p[1] + p[2] exactly for the scaled
+// rows, see the file comment); each conversion rounds to nearest.
+__device__ __forceinline__ void pf_split3(float x, _Float16 (&p)[3]) {
+  p[0] = (_Float16)x;
+  const float r1 = x - (float)p[0];
+  p[1] = (_Float16)r1;
+  p[2] = (_Float16)(r1 - (float)p[1]);
 }
 
 template <int NORM, int PPL>
@@ -221,47 +236,41 @@ __global__ __launch_bounds__(WG) void k_pf_quant(const float *src, int K, const 
         }
     }
   }
-  // token t is row j = t % 32 of token tile t / 32
-  uint8_t *tile = px + (size_t)(t >> 5) * ng * PX_TILE;
+  // the row's exponent: its largest element scaled into [2^14, 2^15)
+  float am = 0.f;
 #pragma unroll
-  for (int i = 0; i < PPL; ++i) {
-    const int u = lane + 64 * i;
-    float am = 0.f;
+  for (int i = 0; i < PPL; ++i)
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const float4 v = y[i][c];  // zero past the row
       am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
-    am = fmaxf(am, dpp_f<0xB1>(am));  // the other half of the group (lane ^ 1)
-    if (u >= nu) continue;            // whole waves took part in the DPP step
-    const float inv = am > 0.f ? Q3MAX * __builtin_amdgcn_rcpf(am) : 0.f;
-    int hq[16], mq[16], lq[16];
+  am = wave_max(am);
+  const int e = am > 0.f && am <= 3.4e38f ? __builtin_amdgcn_frexp_expf(am) - 1 - 14 : 0;
+  // token t is row j = t % 32 of token tile t / 32
+  uint8_t *tile = px + (size_t)(t >> 5) * px_tile_bytes(K);
+  if (lane == 0) reinterpret_cast<int *>(tile + (size_t)ng * PXG)[t & 31] = e;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float e[4] = {y[i][c].x, y[i][c].y, y[i][c].z, y[i][c].w};
+  for (int i = 0; i < PPL; ++i) {
+    const int u = lane + 64 * i;
+    if (u >= nu) continue;
+    // element order per K half: 0 2 4 6 1 3 5 7 (then + 8)
+    const float4 *yc = y[i];
+    _Float16 pc[16][3];
+    const float ev[16] = {yc[0].x, yc[0].z, yc[1].x, yc[1].z, yc[0].y, yc[0].w, yc[1].y, yc[1].w,
+                          yc[2].x, yc[2].z, yc[3].x, yc[3].z, yc[2].y, yc[2].w, yc[3].y, yc[3].w};
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int x = (int)__builtin_rintf(e[k] * inv);
-        // balanced bytes: l, then m, sign-extended low bytes; h the rest
-        const int l = (int)(signed char)(x & 255);
-        const int x1 = (x - l) >> 8;
-        const int m = (int)(signed char)(x1 & 255);
-        lq[4 * c + k] = l;
-        mq[4 * c + k] = m;
-        hq[4 * c + k] = (x1 - m) >> 8;
+    for (int k = 0; k < 16; ++k) pf_split3(__builtin_amdgcn_ldexpf(ev[k], -e), pc[k]);
+    uint8_t *rec = tile + (size_t)(u >> 1) * PXG + 16 * (32 * (u & 1) + (t & 31));  // lane 32 hh + j
+#pragma unroll
+    for (int pi = 0; pi < 3; ++pi)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const _Float16(*q)[3] = pc + 8 * m;
+        *reinterpret_cast<uint4 *>(rec + (size_t)(2 * pi + m) * 1024) =
+            make_uint4(pack_h2(q[0][pi], q[1][pi]), pack_h2(q[2][pi], q[3][pi]), pack_h2(q[4][pi], q[5][pi]),
+                       pack_h2(q[6][pi], q[7][pi]));
       }
-    }
-    // operand order: elements 0 2 4 6 | 8 10 12 14 | 1 3 5 7 | 9 11 13 15
-    auto plane = [](const int (&v)[16]) {
-      return make_uint4(pack4(v[0], v[2], v[4], v[6]), pack4(v[8], v[10], v[12], v[14]),
-                        pack4(v[1], v[3], v[5], v[7]), pack4(v[9], v[11], v[13], v[15]));
-    };
-    uint8_t *grp = tile + (size_t)(u >> 1) * PX_TILE;
-    uint8_t *rec = grp + 512 * (u & 1) + 16 * (t & 31);  // lane 32 hh + j of each plane
-    *reinterpret_cast<uint4 *>(rec) = plane(hq);
-    *reinterpret_cast<uint4 *>(rec + PX_PLANE) = plane(mq);
-    *reinterpret_cast<uint4 *>(rec + 2 * PX_PLANE) = plane(lq);
-    if ((u & 1) == 0) reinterpret_cast<float *>(grp + PX_SC)[t & 31] = am * (1.0f / Q3MAX);
   }
 }
 
@@ -326,50 +335,57 @@ struct PfGemm {
   int ldo;
 };
 
-__device__ __forceinline__ v4i pf_unpack(uint2 w) {
-  // nibble q -> signed byte q - 8: (q + 0x78) ^ 0x80, no carry between bytes
-  const uint32_t e0 = w.x & 0x0F0F0F0Fu, e1 = w.y & 0x0F0F0F0Fu;
-  const uint32_t o0 = (w.x >> 4) & 0x0F0F0F0Fu, o1 = (w.y >> 4) & 0x0F0F0F0Fu;
-  v4i r;
-  r.x = (int)((e0 + 0x78787878u) ^ 0x80808080u);
-  r.y = (int)((e1 + 0x78787878u) ^ 0x80808080u);
-  r.z = (int)((o0 + 0x78787878u) ^ 0x80808080u);
-  r.w = (int)((o1 + 0x78787878u) ^ 0x80808080u);
-  return r;
+// Eight packed nibbles q (one dword of a lane's weight operand, elements
+// 0 .. 7 in nibble order) as the f16 values q - 8 in the order 0 2 4 6 1 3 5 7:
+// each byte pair becomes the f16 pair 1024 + q by one v_perm_b32 against
+// 0x64 high bytes, then one packed add of -1032 (exact: integers below 2048).
+__device__ __forceinline__ v8h pf_w8(uint32_t w) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu, k64 = 0x64646464u;
+  const v2h off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  const v2h a = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(lo, k64, 0x00050004u)) + off;  // elements 0 2
+  const v2h b = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(lo, k64, 0x00070006u)) + off;  // 4 6
+  const v2h c = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(hi, k64, 0x00050004u)) + off;  // 1 3
+  const v2h d = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(hi, k64, 0x00070006u)) + off;  // 5 7
+  return __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3), __builtin_shufflevector(c, d, 0, 1, 2, 3),
+                                 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-constexpr int GPF = 4;  // groups of loads in flight per wave
+#ifndef MLLM_PF_GPF
+#define MLLM_PF_GPF 3
+#endif
+constexpr int GPF = MLLM_PF_GPF;  // groups of loads in flight per wave
+
+struct Pieces {
+  v8h p0a, p0b, p1a, p1b, p2a, p2b;  // piece 0 .. 2, K half a / b
+};
 
 struct GemmLd {
   uint2 w0, w1;
   float c0, c1;
-  v4i ah, am, al;
+  Pieces x;
 };
 
 constexpr int PF_NGMAX = 128;  // groups per row (d_model, d_ff <= 4096)
 
-// One sub-tile's group: the three plane products combined into the exact
-// integer dot (32-bit wrapping arithmetic), then acc += dot * (w_scale * sx)
-// for the lane's 16 tokens.
-__device__ __forceinline__ void pf_group_acc(const v4i &ah, const v4i &am, const v4i &al, const v4i &b, float c,
-                                             const float4 (&sx)[4], float (&acc)[16]) {
-  const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  const v16i H = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, b, zero, 0, 0, 0);
-  const v16i M = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, b, zero, 0, 0, 0);
-  const v16i L = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, b, zero, 0, 0, 0);
+// One sub-tile's group: the exact dot of the group's weights with the three
+// pieces, chained in one f32 accumulator, then acc += dot * w_scale for the
+// lane's 16 tokens.
+__device__ __forceinline__ void pf_group_acc(const Pieces &x, uint2 w, float c, float (&acc)[16]) {
+  const v8h b0 = pf_w8(w.x), b1 = pf_w8(w.y);
+  v16f z = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  z = __builtin_amdgcn_mfma_f32_32x32x16_f16(x.p0a, b0, z, 0, 0, 0);
+  z = __builtin_amdgcn_mfma_f32_32x32x16_f16(x.p0b, b1, z, 0, 0, 0);
+  z = __builtin_amdgcn_mfma_f32_32x32x16_f16(x.p1a, b0, z, 0, 0, 0);
+  z = __builtin_amdgcn_mfma_f32_32x32x16_f16(x.p1b, b1, z, 0, 0, 0);
+  z = __builtin_amdgcn_mfma_f32_32x32x16_f16(x.p2a, b0, z, 0, 0, 0);
+  z = __builtin_amdgcn_mfma_f32_32x32x16_f16(x.p2b, b1, z, 0, 0, 0);
 #pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const uint32_t d = ((uint32_t)H[v] << 16) + ((uint32_t)M[v] << 8) + (uint32_t)L[v];
-    const float4 s4 = sx[v >> 2];
-    const float sv = (v & 3) == 0 ? s4.x : (v & 3) == 1 ? s4.y : (v & 3) == 2 ? s4.z : s4.w;
-    acc[v] = __builtin_fmaf((float)(int)d, c * sv, acc[v]);
-  }
+  for (int v = 0; v < 16; ++v) acc[v] = __builtin_fmaf(z[v], c, acc[v]);
 }
 
 template <int EPI, int KS>
 __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
   __shared__ float red[KS > 1 ? WG * 32 : 1];
-  __shared__ float4 sxs[PF_NGMAX * 8];  // the token tile's group scales: [group][32 tokens]
   const int wv = tid() >> 6, lane = tid() & 63, j = lane & 31, hh = lane >> 5;
   const int ks = wv % KS;
   const int R = (blockIdx.x * (WG / 64 / KS) + wv / KS) * G.rstep;
@@ -377,25 +393,25 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
   const int T0 = (G.tt0 + blockIdx.y) * 32;
   const int ng = G.ng, gb = ng * ks / KS, ge = ng * (ks + 1) / KS;  // this wave's groups
   // tiled operands (every row tile and token tile whole): per group, the
-  // wave's weights are 512 contiguous bytes, its scales 128, its
-  // activations 2 x 1024
+  // wave's weights are 512 contiguous bytes, its scales 128, the tile's
+  // activation pieces 6 x 1024
   const size_t ta = (size_t)(R >> 5) * ng, tb = (size_t)((R + G.off1) >> 5) * ng;
   const uint8_t *wa = G.q0 + ta * 512 + 8 * lane, *wb = G.q1 + tb * 512 + 8 * lane;
   const float *sa = G.s0 + ta * 32 + j, *sb = G.s1 + tb * 32 + j;
-  const uint8_t *xt = A.px + (size_t)(G.tt0 + blockIdx.y) * ng * PX_TILE, *xa = xt + 16 * lane;
-  // every wave of the workgroup takes the same token tile: its scales to LDS
-  for (int i = tid(); i < ng * 8; i += WG)
-    sxs[i] = *reinterpret_cast<const float4 *>(xt + (size_t)(i >> 3) * PX_TILE + PX_SC + 16 * (i & 7));
-  __syncthreads();
+  const uint8_t *xt = A.px + (size_t)(G.tt0 + blockIdx.y) * px_tile_bytes(32 * ng), *xa = xt + 16 * lane;
   auto load = [&](int g) {
     GemmLd L;
     L.w0 = *reinterpret_cast<const uint2 *>(wa + 512 * g);
     L.w1 = *reinterpret_cast<const uint2 *>(wb + 512 * g);
     L.c0 = sa[32 * g];
     L.c1 = sb[32 * g];
-    L.ah = *reinterpret_cast<const v4i *>(xa + PX_TILE * g);
-    L.am = *reinterpret_cast<const v4i *>(xa + PX_TILE * g + PX_PLANE);
-    L.al = *reinterpret_cast<const v4i *>(xa + PX_TILE * g + 2 * PX_PLANE);
+    const v4u *xg = reinterpret_cast<const v4u *>(xa + (size_t)PXG * g);
+    L.x.p0a = __builtin_bit_cast(v8h, xg[0]);
+    L.x.p0b = __builtin_bit_cast(v8h, xg[64]);
+    L.x.p1a = __builtin_bit_cast(v8h, xg[128]);
+    L.x.p1b = __builtin_bit_cast(v8h, xg[192]);
+    L.x.p2a = __builtin_bit_cast(v8h, xg[256]);
+    L.x.p2b = __builtin_bit_cast(v8h, xg[320]);
     return L;
   };
   float acc0[16], acc1[16];
@@ -404,24 +420,19 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
   // the loads of group g + GPF go out before group g is computed
   GemmLd ring[GPF];
   if (active) {
-  // (groups past ge are loaded and not used: the tiled matrices and the
-  // planes carry GPF groups of padding)
+    // (groups past ge are loaded and not used: the tiled matrices and the
+    // activation tiles carry GPF groups of padding)
 #pragma unroll
-  for (int i = 0; i < GPF; ++i) ring[i] = load(gb + i);
-  for (int g0 = gb; g0 < ge; g0 += GPF)
+    for (int i = 0; i < GPF; ++i) ring[i] = load(gb + i);
+    for (int g0 = gb; g0 < ge; g0 += GPF)
 #pragma unroll
-    for (int i = 0; i < GPF; ++i) {
-    if (g0 + i >= ge) break;
-    const GemmLd cur = ring[i];
-    ring[i] = load(g0 + i + GPF);
-    // value v of this lane is token 8(v/4) + 4hh + v%4 of the tile
-    float4 sx[4];
-    const float4 *sg = sxs + (g0 + i) * 8 + hh;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) sx[k] = sg[2 * k];
-    pf_group_acc(cur.ah, cur.am, cur.al, pf_unpack(cur.w0), cur.c0, sx, acc0);
-    pf_group_acc(cur.ah, cur.am, cur.al, pf_unpack(cur.w1), cur.c1, sx, acc1);
-  }
+      for (int i = 0; i < GPF; ++i) {
+        if (g0 + i >= ge) break;
+        const GemmLd cur = ring[i];
+        ring[i] = load(g0 + i + GPF);
+        pf_group_acc(cur.x, cur.w0, cur.c0, acc0);
+        pf_group_acc(cur.x, cur.w1, cur.c1, acc1);
+      }
   }
   if (KS > 1) {
     float *mine = red + (size_t)tid() * 32;
@@ -445,14 +456,27 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
     }
   }
   if (!active) return;
-  // epilogue: value v is token T0 + 8(v/4) + 4hh + v%4, rows r0 / r1
+  // epilogue: value v is token T0 + 8(v/4) + 4hh + v%4, rows r0 / r1; the
+  // token's exponent undoes its row scaling (exact)
   const int r0 = R + j, r1 = R + G.off1 + j;
   const bool in0 = r0 < G.rows, in1 = r1 < G.rows;
+  int ex[16];
+  {
+    const int4 *et = reinterpret_cast<const int4 *>(xt + (size_t)ng * PXG) + hh;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int4 e4 = et[2 * k];
+      ex[4 * k] = e4.x;
+      ex[4 * k + 1] = e4.y;
+      ex[4 * k + 2] = e4.z;
+      ex[4 * k + 3] = e4.w;
+    }
+  }
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
     const int t = T0 + 8 * (v >> 2) + 4 * hh + (v & 3);
     if (t >= G.n) continue;
-    float y0 = acc0[v], y1 = acc1[v];
+    float y0 = __builtin_amdgcn_ldexpf(acc0[v], ex[v]), y1 = __builtin_amdgcn_ldexpf(acc1[v], ex[v]);
     if (EPI == EPI_QKV) {
       // rows R .. R+63 are one head: query head, K head or V head
       const int head = R >> 6, pos = G.pos0 + t;
@@ -522,10 +546,6 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
 // (the query scaled by attn_scale * log2 e) for v_exp_f32.
 constexpr int QTL = 32;   // queries per wave
 constexpr int KROW = 72;  // halves per staged key row (64 + pad)
-
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-typedef float v16f __attribute__((ext_vector_type(16)));
 
 // Eight consecutive cache values as loaded (f16: one 16-byte load, f32: two),
 // widened to f32 when staged.
@@ -843,8 +863,9 @@ bool pf_supported(const PfArgs &A) {
 size_t pf_buffer_bytes(const PfArgs &A, int tc) {
   const size_t kmax = (size_t)(A.D > A.FF ? A.D : A.FF);
   auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  // + GPF groups of padding after the last tile (read ahead, never used)
   return al(sizeof(int32_t) * tc) + 3 * al(sizeof(float) * tc * A.D) + al(sizeof(float) * tc * A.FF) +
-         al((size_t)(((tc + 31) / 32) * (kmax / 32) + GPF) * PX_TILE);
+         al((size_t)((tc + 31) / 32) * px_tile_bytes((int)kmax) + (size_t)GPF * PXG);
 }
 
 void pf_carve(PfArgs &A, void *base, int tc) {
