@@ -391,45 +391,45 @@ def bench_gemv(torch, abi, pgw, oracle=None, quick=False):
             if not quick:
                 res["cold_graph_us"] = graph_us(torch, lambda s: [launch(i % copies, s) for i in range(reps)], reps)
                 res["cold_graph_gbs"] = round(algo / res["cold_graph_us"] / 1e3, 1)
-            if fmt == "q4":
-                # layer-stacked: 32 distinct matrices per launch
-                cnt = 32
-                groups = max(1, copies // cnt)
-                tabs = []
-                for gi in range(min(groups, 64)):
-                    idx = [(gi * cnt + j) % copies for j in range(cnt)]
-                    tp = torch.tensor([W[i].data_ptr() for i in idx], dtype=torch.int64, device="cuda")
-                    ts = torch.tensor([S[i].data_ptr() for i in idx], dtype=torch.int64, device="cuda")
-                    tx = torch.tensor([x.data_ptr()] * cnt, dtype=torch.int64, device="cuda")
-                    ys = torch.empty((cnt, m), dtype=torch.float32, device="cuda")
-                    ty = torch.tensor([ys[j].data_ptr() for j in range(cnt)], dtype=torch.int64, device="cuda")
-                    tabs.append((tp, ts, tx, ty, ys))
-                reps = 10 if quick else 100
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                for i in range(3):
-                    tp, ts, tx, ty, _ = tabs[i % len(tabs)]
-                    abi.check("batched", abi.lib().mllm_gemv_q4_batched(cnt, m, n, tp.data_ptr(), ts.data_ptr(),
-                                                                        tx.data_ptr(), ty.data_ptr(), sp))
-                e0.record(stream)
+            batched = abi.lib().mllm_gemv_q4_batched if fmt == "q4" else abi.lib().mllm_gemv_q8_g32_batched
+            # layer-stacked: 32 distinct matrices per launch
+            cnt = 32
+            groups = max(1, copies // cnt)
+            tabs = []
+            for gi in range(min(groups, 64)):
+                idx = [(gi * cnt + j) % copies for j in range(cnt)]
+                tp = torch.tensor([W[i].data_ptr() for i in idx], dtype=torch.int64, device="cuda")
+                ts = torch.tensor([S[i].data_ptr() for i in idx], dtype=torch.int64, device="cuda")
+                tx = torch.tensor([x.data_ptr()] * cnt, dtype=torch.int64, device="cuda")
+                ys = torch.empty((cnt, m), dtype=torch.float32, device="cuda")
+                ty = torch.tensor([ys[j].data_ptr() for j in range(cnt)], dtype=torch.int64, device="cuda")
+                tabs.append((tp, ts, tx, ty, ys))
+            reps = 10 if quick else 100
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            for i in range(3):
+                tp, ts, tx, ty, _ = tabs[i % len(tabs)]
+                abi.check("batched", batched(cnt, m, n, tp.data_ptr(), ts.data_ptr(), tx.data_ptr(),
+                                             ty.data_ptr(), sp))
+            e0.record(stream)
+            for i in range(reps):
+                tp, ts, tx, ty, _ = tabs[i % len(tabs)]
+                abi.check("batched", batched(cnt, m, n, tp.data_ptr(), ts.data_ptr(), tx.data_ptr(),
+                                             ty.data_ptr(), sp))
+            e1.record(stream)
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            res["stacked32_us"] = round(us, 3)
+            res["stacked32_gbs"] = round(cnt * algo / us / 1e3, 1)
+
+            def stacked(s):
                 for i in range(reps):
                     tp, ts, tx, ty, _ = tabs[i % len(tabs)]
-                    abi.check("batched", abi.lib().mllm_gemv_q4_batched(cnt, m, n, tp.data_ptr(), ts.data_ptr(),
-                                                                        tx.data_ptr(), ty.data_ptr(), sp))
-                e1.record(stream)
-                e1.synchronize()
-                us = e0.elapsed_time(e1) * 1e3 / reps
-                res["stacked32_us"] = round(us, 3)
-                res["stacked32_gbs"] = round(cnt * algo / us / 1e3, 1)
-
-                def stacked(s):
-                    for i in range(reps):
-                        tp, ts, tx, ty, _ = tabs[i % len(tabs)]
-                        abi.check("batched", abi.lib().mllm_gemv_q4_batched(cnt, m, n, tp.data_ptr(), ts.data_ptr(),
-                                                                            tx.data_ptr(), ty.data_ptr(), s))
-                if not quick:
-                    res["stacked32_graph_us"] = graph_us(torch, stacked, reps)
-                    res["stacked32_graph_gbs"] = round(cnt * algo / res["stacked32_graph_us"] / 1e3, 1)
-                del tabs
+                    abi.check("batched", batched(cnt, m, n, tp.data_ptr(), ts.data_ptr(), tx.data_ptr(),
+                                                 ty.data_ptr(), s))
+            if not quick:
+                res["stacked32_graph_us"] = graph_us(torch, stacked, reps)
+                res["stacked32_graph_gbs"] = round(cnt * algo / res["stacked32_graph_us"] / 1e3, 1)
+            del tabs
             res["cold_frac_hbm"] = round(res["cold_gbs"] / HBM_PEAK_GBS, 4)
             if fmt == "q4" and oracle is not None:
                 res["cpu_kernels_rs"] = cpu_gemv_q4(oracle, pgw, m, n)

@@ -103,6 +103,14 @@ int mllm_gemm_q4(int t, int m, int n, const uint8_t *packed, const float *scale,
 int mllm_gemv_q4_batched(int count, int m, int n, const uint8_t *const *packed, const float *const *scale,
                          const float *const *x, float *const *y, void *stream);
 
+/* No reference counterpart (BASELINE config 2 times the Q8 group-32 variant
+ * of each layer shape stacked): one launch over `count` mllm_gemv_q8_g32
+ * calls of the same shape, arrays of device pointers in device memory
+ * (every q and x pointer 16-byte aligned); each matrix's rows are
+ * bit-identical to a single mllm_gemv_q8_g32 call's. */
+int mllm_gemv_q8_g32_batched(int count, int m, int n, const int8_t *const *q, const float *const *scale,
+                             const float *const *x, float *const *y, void *stream);
+
 /* kernels.rs:99-120 rms_norm(n, x, w, out, tokens) with eps as a parameter
  * (the reference hard-codes 1e-6: infer.js:8, kernels.rs:106). */
 int mllm_rms_norm(int n, const float *x, const float *w, float *out, int tokens, float eps, void *stream);

@@ -429,6 +429,17 @@ __global__ __launch_bounds__(WGT) void k_gemv_q8i(const int8_t *__restrict__ q, 
   q8_gemv_tile<WGT, P, PERROW>(q, scale, x, y, G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4));
 }
 
+// One launch over same-shape Q8 matrices: blockIdx.y selects the matrix.
+template <int WGT, int P, bool PERROW>
+__global__ __launch_bounds__(WGT) void k_gemv_q8i_batched(const int8_t *const *__restrict__ q,
+                                                          const float *const *__restrict__ scale,
+                                                          const float *const *__restrict__ xv,
+                                                          float *const *__restrict__ yv, GemvGeom G) {
+  extern __shared__ float4 smem4[];
+  const int b = blockIdx.y;
+  q8_gemv_tile<WGT, P, PERROW>(q[b], scale[b], xv[b], yv[b], G, blockIdx.x, reinterpret_cast<uint32_t *>(smem4));
+}
+
 // ---------------------------------------------------------------- f32 GEMV
 // One wavefront per row, lanes over float4s, fixed-pattern wave reduction.
 __global__ __launch_bounds__(WG) void k_gemv_f32(const float *__restrict__ w, const float *__restrict__ x,
@@ -851,6 +862,15 @@ int q8_launch(dim3 grid, size_t lds, hipStream_t st, const int8_t *q, const floa
   return 0;
 }
 
+template <int WGT, int P>
+int q8_launch_batched(dim3 grid, size_t lds, hipStream_t st, const int8_t *const *q, const float *const *scale,
+                      const float *const *x, float *const *y, const GemvGeom &G) {
+  if (int rc = launch_dyn(k_gemv_q8i_batched<WGT, P, false>, grid, lds, st, "k_gemv_q8i_batched")) return rc;
+  hipLaunchKernelGGL((k_gemv_q8i_batched<WGT, P, false>), grid, dim3(WGT), lds, st, q, scale, x, y, G);
+  MLLM_HIP(hipGetLastError());
+  return 0;
+}
+
 // The Q8 GEMVs on integer dots, with the Q4 path's tile plan (the chunk of a
 // (row, group) is 32 bytes instead of 16).
 static int q8_common(int m, int n, const int8_t *q, const float *scale, const float *x, float *y, int per_row,
@@ -877,6 +897,24 @@ extern "C" int mllm_gemv_q8(int m, int n, const int8_t *q, const float *scale, c
 extern "C" int mllm_gemv_q8_g32(int m, int n, const int8_t *q, const float *scale, const float *x, float *y,
                                 void *stream) {
   return q8_common(m, n, q, scale, x, y, 0, as_stream(stream));
+}
+
+extern "C" int mllm_gemv_q8_g32_batched(int count, int m, int n, const int8_t *const *q, const float *const *scale,
+                                        const float *const *x, float *const *y, void *stream) {
+  MLLM_CHECK(m > 0 && n > 0 && n % 32 == 0, "invalid shape m=%d n=%d (n %% 32 == 0 required)", m, n);
+  if (n > kMaxCols) return set_error(MLLM_ERR_UNSUPPORTED, "n=%d exceeds %d", n, kMaxCols);
+  MLLM_CHECK(count > 0 && count <= 65535, "count=%d", count);
+  MLLM_CHECK(q && scale && x && y, "null pointer");
+  MLLM_CHECK((size_t)m * n < (1ull << 31), "matrix of %zu bytes exceeds 2 GiB", (size_t)m * n);
+  // the tile plan chosen for the whole batch; a row's sum depends only on
+  // its group count (lpr), so each matrix's rows come out as mllm_gemv_q8_g32's
+  const int ng = n / 32;
+  const Q4Plan pl = q4_plan(n, m, count);
+  const int P = q4_pick_p(m, pl.rpp, count);
+  const int ntiles = (m + pl.rpp * P - 1) / (pl.rpp * P);
+  const GemvGeom G{m, n, 1, pl.rpp, pl.lpr, m};
+  return MLLM_Q4_DISPATCH(q8_launch_batched, pl.wgt, P, dim3(ntiles, count), q4_lds_bytes(pl, ng, 1, P),
+                          as_stream(stream), q, scale, x, y, G);
 }
 
 extern "C" int mllm_gemv_f32(int m, int n, const float *w, const float *x, float *y, void *stream) {

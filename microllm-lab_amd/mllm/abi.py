@@ -29,6 +29,7 @@ SIGNATURES = {
     "mllm_gemv_q8_g32": ([I, I, P, P, P, P, P], I),
     "mllm_gemm_q4": ([I, I, I, P, P, I, P, P, P], I),
     "mllm_gemv_q4_batched": ([I, I, I, P, P, P, P, P], I),
+    "mllm_gemv_q8_g32_batched": ([I, I, I, P, P, P, P, P], I),
     "mllm_gemv_q4_argmax": ([I, I, P, P, I, P, P, P, P], I),
     "mllm_gemv_q4_argmax_noalloc": ([I, I, P, P, I, P, P, P, P], I),
     "mllm_rms_norm": ([I, P, P, P, I, C.c_float, P], I),

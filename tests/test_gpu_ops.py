@@ -96,6 +96,28 @@ def test_gemv_q4_batched_matches_single():
 
 
 @gpu
+@pytest.mark.parametrize("m,n", [(320, 960), (960, 2560)])
+def test_gemv_q8_g32_batched_matches_single(m, n):
+    """A stacked launch of Q8 group-32 GEMVs (config 2's Q8 variant): every
+    matrix's rows carry the bits of a single mllm_gemv_q8_g32 call."""
+    rng = np.random.default_rng(9)
+    count = 6
+    mats = [pgw.quant_q8g32((rng.standard_normal((m, n)) * 0.02).astype(np.float32)) for _ in range(count)]
+    xs = [dev(rng.standard_normal(n).astype(np.float32)) for _ in range(count)]
+    dqs = [dev(q) for q, _ in mats]
+    dss = [dev(s) for _, s in mats]
+    ys = [torch.empty(m, dtype=torch.float32, device="cuda") for _ in range(count)]
+    table = lambda ts: dev(np.array([t.data_ptr() for t in ts], np.uint64))  # noqa: E731
+    tq, ts_, tx, ty = table(dqs), table(dss), table(xs), table(ys)
+    abi.call("mllm_gemv_q8_g32_batched", count, m, n, ptr(tq), ptr(ts_), ptr(tx), ptr(ty), None)
+    torch.cuda.synchronize()
+    for i in range(count):
+        d1 = torch.empty(m, dtype=torch.float32, device="cuda")
+        abi.call("mllm_gemv_q8_g32", m, n, ptr(dqs[i]), ptr(dss[i]), ptr(xs[i]), ptr(d1), None)
+        assert np.array_equal(host(d1).view(np.uint32), host(ys[i]).view(np.uint32)), i
+
+
+@gpu
 @pytest.mark.parametrize("n", [2048, 2560, 4096, 8192])
 def test_gemv_q4_rows_do_not_depend_on_the_workgroup_width(n):
     """960 x n alone (64 to 256 groups per row) and 32 of them stacked launch
