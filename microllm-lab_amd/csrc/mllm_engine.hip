@@ -151,6 +151,7 @@ struct DecParams {
   float *amv;     // [MAXT][lm_tiles]
   int *ami;
   uint2 *amt;     // [2][lm_tiles][2] persistent decode: each lm_head tile's first maximum (value, row) as tagged pairs, by step parity
+  uint2 *amtv;    // [MAXT][lm_tiles][2] persistent verify: each token's tile maxima as tagged pairs
   uint2 *attpt;   // [MAXT][NH][nsplit_max][APT] persistent kernels: attention split partials (m, l, acc) as tagged pairs
   int lm_rpt, lm_tiles, lm_grid;
   PassState *st;
@@ -1414,8 +1415,8 @@ struct LmGeom {
 // One lm_head tile whose weights are in R: logits rows [r0, r0+nr) of the m
 // tokens from tb, then the tile's first maximum per token (gpt2 chain: with
 // the argmaxGpt2 adjustments).
-// With amt (one token), the tile's first maximum goes out as two tagged pairs
-// (value, row) at amt[2 tile] instead of to amv / ami.
+// With amt, token t's tile maximum goes out as two tagged pairs (value, row)
+// at amt[2 ((tb + t) ntiles + tile)] instead of to amv / ami.
 template <int TCN, int NT>
 __device__ __forceinline__ void lm_tile(const DecParams &P, const LmGeom &L, const TileRegs<TCN> &R, int tile, int tb,
                                         int m, const LmLds &s, bool penal, int nban, int nrec, uint2 *amt = nullptr,
@@ -1442,7 +1443,7 @@ __device__ __forceinline__ void lm_tile(const DecParams &P, const LmGeom &L, con
     if (lane_id() == 0) {
       if (amt) {
         const uint2 pv = tag_pair(__float_as_uint(bv), amtag), pi = tag_pair((uint32_t)bi, amtag);
-        coh_st16(amt, 16u * tile, make_uint4(pv.x, pv.y, pi.x, pi.y));
+        coh_st16(amt, 16u * (uint32_t)((tb + t) * L.ntiles + tile), make_uint4(pv.x, pv.y, pi.x, pi.y));
       } else {
         coh_stf(P.amv, 4u * ((tb + t) * P.lm_tiles + tile), bv);
         coh_sti(P.ami, 4u * ((tb + t) * P.lm_tiles + tile), bi);
@@ -2582,7 +2583,7 @@ __device__ void flowm_mlp(const DecParams &P, const LayerW &Lw, int li, int item
 // per pass over a tile (no penalties: a verify pass is greedy).  Returns
 // true when this workgroup computed at least one tile.
 __device__ bool flowm_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, const Step &st, int m, bool fused,
-                         float *smem) {
+                         float *smem, int amtag) {
   if (wg >= L.ntiles) return false;
   const int ng = P.D >> 5;
   TileRegs<FTC> R;
@@ -2605,7 +2606,7 @@ __device__ bool flowm_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, c
     for (int t0 = 0; t0 < m; t0 += VLB) {
       LmLds u = s;
       u.qx = s.qx + t0 * ng * Q6R;
-      lm_tile<FTC, FLT>(P, L, R, tile, t0, min(VLB, m - t0), u, false, 0, 0);
+      lm_tile<FTC, FLT>(P, L, R, tile, t0, min(VLB, m - t0), u, false, 0, 0, P.amtv, amtag);
     }
     tile += nwg;
     if (tile >= L.ntiles) break;
@@ -2614,28 +2615,29 @@ __device__ bool flowm_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, c
   return true;
 }
 
-// Every row's first maximum over the tile maxima, one wave per row (the
-// relation is a total order on (value, index), so the order of the
-// comparisons does not change the result).
-__device__ void flowm_argmax(const DecParams &P, int ntiles, int m) {
+// Every row's first maximum over the tiles' tagged maxima (tag `want`), one
+// wave per row, each lane's 16-byte loads polled (bounded) until both pairs
+// carry the tag; the relation is a total order on (value, index), so the
+// order of the comparisons does not change the result.
+__device__ void flowm_argmax(const DecParams &P, int ntiles, int m, int want) {
   for (int t = wave_id(); t < m; t += NWV) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int base = 0; base < ntiles; base += 8 * 64) {
-      float vv[8];
-      int iv[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {  // all loads of the batch before any compare
-        const int k = min(base + lane_id() + j * 64, ntiles - 1);
-        vv[j] = coh_ldf(P.amv, 4u * (t * P.lm_tiles + k));
-        iv[j] = coh_ldi(P.ami, 4u * (t * P.lm_tiles + k));
+    for (int base = 0; base < ntiles; base += 64) {
+      const uint32_t off = 16u * (uint32_t)(t * ntiles + min(base + lane_id(), ntiles - 1));
+      uint4 u = coh_ld16(P.amtv, off);
+      for (unsigned spins = 1; !__all(pair_ok(make_uint2(u.x, u.y), want) && pair_ok(make_uint2(u.z, u.w), want)) &&
+                               !poll_give_up(P, spins);
+           ++spins) {
+        poll_fence();
+        u = coh_ld16(P.amtv, off);
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (amax_better(vv[j], iv[j], bv, bi)) {
-          bv = vv[j];
-          bi = iv[j];
-        }
+      const float v = __uint_as_float(u.x);
+      const int i = (int)u.z;
+      if (base + lane_id() < ntiles && amax_better(v, i, bv, bi)) {
+        bv = v;
+        bi = i;
+      }
     }
     wave_argmax(bv, bi);
     if (lane_id() == 0) st_st(P, ST_OFF(res) + 4u * t, bi);
@@ -2655,8 +2657,6 @@ __global__ __launch_bounds__(FLT) void k_flowm(DecParams P, FlowGeom F) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // as in k_flow: no stale cache lines of the KV cache
   const int w = blockIdx.x, G = gridDim.x, m = F.m;
   const int stride = P.NH + F.nm;
-  int *const lm_cnt = F.flags + P.L * stride;
-  int *const am_flag = lm_cnt + 1;
   const int nlm = min(G, F.lm_tiles);
   const LmGeom lg{F.lm_rpt, F.lm_tiles};
   int *const red = reinterpret_cast<int *>(smem);
@@ -2704,21 +2704,10 @@ __global__ __launch_bounds__(FLT) void k_flowm(DecParams P, FlowGeom F) {
       flow_wait<16>(P, F.flags + (P.L - 2) * stride + P.NH, F.nm, nullptr, 0, nullptr, 0, e);
     }
     __syncthreads();
-    if (flowm_lm(P, lg, w, G, st, m, F.fuse, smem)) {
-      // the last lm_head workgroup to finish takes every row's argmax
-      wait_stores();
-      __syncthreads();
-      if (tid() == 0) {
-        const int arrived = atomicAdd(lm_cnt, 1);
-        red[0] = arrived == nlm - 1;
-        if (red[0]) __hip_atomic_store(lm_cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      __syncthreads();
-      if (red[0]) {
-        flowm_argmax(P, F.lm_tiles, m);
-        flow_publish(am_flag, e);
-      }
-    }
+    // each tile stores its tokens' maxima as tagged pairs, without waiting;
+    // workgroup 0 then takes every row's argmax over them
+    flowm_lm(P, lg, w, G, st, m, F.fuse, smem, st.tag + TAG_LM);
+    if (w == 0) flowm_argmax(P, F.lm_tiles, m, st.tag + TAG_LM);
   }
 }
 
@@ -3431,6 +3420,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
   if (!rc) rc = dev_alloc(M, (void **)&P.amv, sizeof(float) * MAXT * P.lm_tiles);
   if (!rc) rc = dev_alloc(M, (void **)&P.ami, sizeof(int) * MAXT * P.lm_tiles);
   if (!rc) rc = dev_alloc(M, (void **)&P.amt, sizeof(uint2) * 4 * P.lm_tiles);
+  if (!rc) rc = dev_alloc(M, (void **)&P.amtv, sizeof(uint2) * 2 * MAXT * P.lm_tiles);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_hist, sizeof(int) * (c.max_seq_len + 1));
   if (!rc) rc = dev_alloc(M, (void **)&M->d_st, sizeof(PassState));
   if (!rc) rc = dev_alloc(M, (void **)&M->d_gemv_x, sizeof(float) * std::max(FF, D) * 4);
@@ -3443,6 +3433,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       hipMemset(P.opart, 0, tagged_bytes[2]) != hipSuccess || hipMemset(P.dpart, 0, tagged_bytes[3]) != hipSuccess ||
       hipMemset(P.cnt, 0, sizeof(unsigned) * MAXT * NH) != hipSuccess ||
       hipMemset(P.amt, 0, sizeof(uint2) * 4 * P.lm_tiles) != hipSuccess ||
+      hipMemset(P.amtv, 0, sizeof(uint2) * 2 * MAXT * P.lm_tiles) != hipSuccess ||
       hipMemset(P.attpt, 0, sizeof(uint2) * MAXT * NH * P.nsplit_max * APT) != hipSuccess ||
       hipMemset(P.rec, 0, sizeof(uint2) * 2 * MAXT * ngd * Q6R) != hipSuccess ||
       hipMemset(P.qkvr, 0, sizeof(uint2) * L * MAXT * (NH + 2 * NKV) * HD) != hipSuccess ||
@@ -3456,6 +3447,7 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
                {P.opart, tagged_bytes[2]},
                {P.dpart, tagged_bytes[3]},
                {P.amt, sizeof(uint2) * 4 * P.lm_tiles},
+               {P.amtv, sizeof(uint2) * 2 * MAXT * P.lm_tiles},
                {P.attpt, sizeof(uint2) * MAXT * NH * P.nsplit_max * APT},
                {P.rec, sizeof(uint2) * 2 * MAXT * ngd * Q6R},
                {P.qkvr, sizeof(uint2) * L * MAXT * (NH + 2 * NKV) * HD}};
