@@ -151,8 +151,13 @@ __device__ __forceinline__ void pf_norm_stats(const float4 *xr, int K, float eps
 
 // Lane u of the wave owns (group u / 2, half u % 2) of the row -- 16
 // consecutive elements, PPL such units per lane (K <= 1024 PPL) -- held in
-// registers from one load.  The unit's pieces go out as six 16-byte stores
-// (three pieces x two K halves).
+// registers from one load.  A workgroup is QT waves: QT consecutive tokens
+// of one 32-token tile.  The units' pieces (three pieces x two K halves of
+// 16 bytes each) go to LDS first, unit u of token jj at u * qstr(QT) +
+// ((2p + m) QT + jj) * 16 (padded so the 64 lanes' writes spread over the
+// banks); then the workgroup copies them out so that the QT tokens' records
+// of each (unit, piece, half) -- QT * 16 contiguous bytes of the GEMM operand
+// layout, one whole 128-byte line at QT = 8 -- go out together.
 __device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
   const v2h v = {a, b};
   return __builtin_bit_cast(uint32_t, v);
@@ -167,11 +172,17 @@ __device__ __forceinline__ void pf_split3(float x, _Float16 (&p)[3]) {
   p[2] = (_Float16)(r1 - (float)p[1]);
 }
 
-template <int NORM, int PPL>
-__global__ __launch_bounds__(WG) void k_pf_quant(const float *src, int K, const float *g, float eps, uint8_t *px,
-                                                 int t0, int t1) {
-  const int t = t0 + (int)blockIdx.x * (WG / 64) + (tid() >> 6);
-  if (t >= t1) return;  // no barriers below
+// QT tokens (waves) per quantise workgroup: 8, or 4 where 8 tokens' records
+// of a long row would not fit the LDS; qstr: LDS bytes per unit (its 6 x QT
+// records, padded)
+__host__ __device__ constexpr int qstr(int qt) { return 6 * qt * 16 + 16; }
+
+// Token t's row (one wave, t < t1): the norm, the exponent (to the tile's
+// exponent slot jt) and the unit records into the workgroup's LDS (token
+// slot jj).
+template <int NORM, int PPL, int QT>
+__device__ __forceinline__ void pf_quant_row(const float *src, int K, const float *g, float eps, int t, int jj,
+                                             int jt, uint8_t *tb, uint8_t *qs) {
   const int lane = tid() & 63, nu = K >> 4, ng = K >> 5;
   const float4 *xr = reinterpret_cast<const float4 *>(src + (size_t)t * K);
   const float4 *g4 = reinterpret_cast<const float4 *>(g);
@@ -247,9 +258,7 @@ __global__ __launch_bounds__(WG) void k_pf_quant(const float *src, int K, const 
     }
   am = wave_max(am);
   const int e = am > 0.f && am <= 3.4e38f ? __builtin_amdgcn_frexp_expf(am) - 1 - 14 : 0;
-  // token t is row j = t % 32 of token tile t / 32
-  uint8_t *tile = px + (size_t)(t >> 5) * px_tile_bytes(K);
-  if (lane == 0) reinterpret_cast<int *>(tile + (size_t)ng * PXG)[t & 31] = e;
+  if (lane == 0) reinterpret_cast<int *>(tb + (size_t)ng * PXG)[jt] = e;
 #pragma unroll
   for (int i = 0; i < PPL; ++i) {
     const int u = lane + 64 * i;
@@ -261,16 +270,38 @@ __global__ __launch_bounds__(WG) void k_pf_quant(const float *src, int K, const 
                           yc[2].x, yc[2].z, yc[3].x, yc[3].z, yc[2].y, yc[2].w, yc[3].y, yc[3].w};
 #pragma unroll
     for (int k = 0; k < 16; ++k) pf_split3(__builtin_amdgcn_ldexpf(ev[k], -e), pc[k]);
-    uint8_t *rec = tile + (size_t)(u >> 1) * PXG + 16 * (32 * (u & 1) + (t & 31));  // lane 32 hh + j
+    uint8_t *rec = qs + (size_t)u * qstr(QT) + 16 * jj;
 #pragma unroll
     for (int pi = 0; pi < 3; ++pi)
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const _Float16(*q)[3] = pc + 8 * m;
-        *reinterpret_cast<uint4 *>(rec + (size_t)(2 * pi + m) * 1024) =
-            make_uint4(pack_h2(q[0][pi], q[1][pi]), pack_h2(q[2][pi], q[3][pi]), pack_h2(q[4][pi], q[5][pi]),
-                       pack_h2(q[6][pi], q[7][pi]));
+        *reinterpret_cast<v4u *>(rec + (size_t)(2 * pi + m) * QT * 16) =
+            v4u{pack_h2(q[0][pi], q[1][pi]), pack_h2(q[2][pi], q[3][pi]), pack_h2(q[4][pi], q[5][pi]),
+                pack_h2(q[6][pi], q[7][pi])};
       }
+  }
+}
+
+template <int NORM, int PPL, int QT>
+__global__ __launch_bounds__(QT * 64) void k_pf_quant(const float *src, int K, const float *g, float eps,
+                                                      uint8_t *px, int t0, int t1) {
+  extern __shared__ float4 qsm4[];
+  uint8_t *qs = reinterpret_cast<uint8_t *>(qsm4);
+  const int jj = tid() >> 6, j0 = QT * ((int)blockIdx.x % (32 / QT));
+  const int tile = t0 / 32 + (int)blockIdx.x / (32 / QT), t = tile * 32 + j0 + jj;
+  const int nu = K >> 4;
+  uint8_t *tb = px + (size_t)tile * px_tile_bytes(K);
+  if (t < t1) pf_quant_row<NORM, PPL, QT>(src, K, g, eps, t, jj, j0 + jj, tb, qs);  // wave-uniform
+  __syncthreads();
+  // the records out: unit u = (group u / 2, half hh = u % 2), piece p, K half
+  // m, token jj at tile + (u / 2) PXG + (2p + m) 1024 + 16 (32 hh + j0 + jj)
+  // (tokens past t1 carry whatever the LDS held: the GEMMs never use them)
+  const int nrec = nu * 6 * QT;
+  for (int f = tid(); f < nrec; f += QT * 64) {
+    const int r = f % QT, pm = (f / QT) % 6, u = f / (6 * QT);
+    const v4u v = *reinterpret_cast<const v4u *>(qs + (size_t)u * qstr(QT) + (pm * QT + r) * 16);
+    *reinterpret_cast<v4u *>(tb + (size_t)(u >> 1) * PXG + pm * 1024 + 16 * (32 * (u & 1) + j0 + r)) = v;
   }
 }
 
@@ -794,16 +825,34 @@ __global__ __launch_bounds__(WG) void k_pf_tile(PfMat W, uint8_t *q, float *s) {
 }
 
 // ---------------------------------------------------------------- host
+// One quantise instance: past 64 KB of LDS a kernel needs the opt-in, made
+// once per instance.
+template <int NORM, int PPL, int QT>
+void quant_launch(dim3 grid, size_t lds, hipStream_t s, const PfArgs &A, const float *src, int K, const float *g,
+                  int t0, int t1) {
+  static bool opted = false;
+  if (lds > 64 * 1024 && !opted)
+    opted = hipFuncSetAttribute(reinterpret_cast<const void *>(k_pf_quant<NORM, PPL, QT>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+  hipLaunchKernelGGL((k_pf_quant<NORM, PPL, QT>), grid, dim3(QT * 64), lds, s, src, K, g, A.eps, A.px, t0, t1);
+}
+
 template <int NORM>
 void launch_quant(const PfArgs &A, const float *src, int K, const float *g, int t0, int t1, hipStream_t s) {
-  const int per = WG / 64;
-  const dim3 grid((t1 - t0 + per - 1) / per);
+  // QT tokens per workgroup (t0 is a multiple of 32); the LDS holds the QT
+  // tokens' records of every unit: (K / 16) * qstr(QT) bytes, 125 KB at
+  // K = 2560 with QT = 8, at most 100 KB at K = 4096 with QT = 4
+  const int qt = (K >> 4) * qstr(8) <= 160 * 1024 ? 8 : 4;
+  const dim3 grid(((t1 - t0 + 31) / 32) * (32 / qt));
+  const size_t lds = (size_t)(K >> 4) * qstr(qt);
   if (K <= 1024)
-    hipLaunchKernelGGL((k_pf_quant<NORM, 1>), grid, dim3(WG), 0, s, src, K, g, A.eps, A.px, t0, t1);
+    quant_launch<NORM, 1, 8>(grid, lds, s, A, src, K, g, t0, t1);
   else if (K <= 2048)
-    hipLaunchKernelGGL((k_pf_quant<NORM, 2>), grid, dim3(WG), 0, s, src, K, g, A.eps, A.px, t0, t1);
+    quant_launch<NORM, 2, 8>(grid, lds, s, A, src, K, g, t0, t1);
+  else if (qt == 8)
+    quant_launch<NORM, 4, 8>(grid, lds, s, A, src, K, g, t0, t1);
   else
-    hipLaunchKernelGGL((k_pf_quant<NORM, 4>), grid, dim3(WG), 0, s, src, K, g, A.eps, A.px, t0, t1);
+    quant_launch<NORM, 4, 4>(grid, lds, s, A, src, K, g, t0, t1);
 }
 
 // Group slices per row range: the fewest (1, 2 or 4) that give at least
