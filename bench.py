@@ -101,6 +101,51 @@ def token_bytes(cfg, seq, kv_bytes=4):
     return weights + norms + kv
 
 
+def kind_bytes(rows, cols, kind):
+    """Bytes of one matrix in its storage (data + scales)."""
+    return {"q4": q4_bytes(rows, cols), "q8": rows * cols + 4 * rows, "q8g32": rows * cols + rows * (cols // 32) * 4,
+            "f16": 2 * rows * cols, "bf16": 2 * rows * cols, "f32": 4 * rows * cols}[kind]
+
+
+def kind_token_bytes(cfg, seq, kind, kv_bytes=4):
+    """token_bytes for a model whose matrices are stored as `kind`."""
+    D, FF = cfg.d_model, cfg.d_ff
+    hd = D // cfg.n_heads
+    kvd = cfg.n_kv_heads * hd
+    mats = (kind_bytes(D + 2 * kvd, D, kind) + kind_bytes(D, D, kind) +
+            (1 if cfg.arch == "gpt2" else 2) * kind_bytes(FF, D, kind) + kind_bytes(D, FF, kind))
+    weights = cfg.n_layers * mats + kind_bytes(cfg.vocab_size, D, kind)
+    norms = (2 * cfg.n_layers + 1) * D * 4
+    kv = 2 * cfg.n_kv_heads * hd * kv_bytes * cfg.n_layers * seq
+    return weights + norms + kv
+
+
+def bench_kinds(mllm, pgw, steps=127):
+    """Config 1's workload (135M shape, 32-token prompt, greedy chain) with
+    the matrices stored per-row Q8, f16, bf16 and f32 -- the kinds the
+    reference times on its GPU engine (WRITEUP.md:31-35) -- through the
+    kind-generic step."""
+    cfg = pgw.CONFIGS["smollm2-135m"]
+    prompt = [int(v) for v in np.random.default_rng(1).integers(0, cfg.vocab_size, 32)]
+    res = {}
+    for kind in ("q8", "f16", "bf16", "f32"):
+        g = mllm.PetitGPT(pgw.parse_pgw(pgw.make_llama(cfg, seed=0, kind=kind)))
+        for _ in range(2):
+            g.resetCache()
+            g.forwardPrompt(prompt)
+            g.decodeChain(g.last_argmax, steps)
+        ms, n = g.last_timing()
+        algo = sum(kind_token_bytes(cfg, 33 + i, kind) for i in range(n)) / n
+        us = ms * 1e3 / n
+        res[kind] = {"kernel": g.decodeKernel, "us_per_token": round(us, 2), "tok_s": round(n / (ms * 1e-3), 1),
+                     "algorithmic_bytes_per_token": int(algo), "gbs": round(algo / us / 1e3, 1)}
+        log(f"[bench] kinds {kind}: {res[kind]}")
+        g.destroy()
+    res["workload"] = (f"smollm2-135m shape, matrices stored as each kind (N(0,0.02), seed 0), 32-token prompt, "
+                       f"{steps} chained greedy decode steps (config 1's workload)")
+    return res
+
+
 def traffic_record(kernel):
     """The rocprofv3 FETCH_SIZE / WRITE_SIZE record of `kernel` in
     profiles/decode_traffic.json (counters scaled by what they read on a plain
@@ -639,6 +684,8 @@ def main():
     ap.add_argument("--decode-360m", action="store_true",
                     help="only config 5's decode: the 1536-token prompt (batched), then one chained decode of 511 "
                          "steps to 2048 context (one persistent-kernel dispatch; the traffic record behind it)")
+    ap.add_argument("--kinds-only", action="store_true",
+                    help="only config 1's workload with Q8 / f16 / bf16 / f32 matrices (the kind-generic step)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (counter calibration for the traffic figure)")
     args = ap.parse_args()
@@ -668,6 +715,9 @@ def main():
         return
     if args.verify_only:
         print(json.dumps(bench_verify(mllm, pgw, args)))
+        return
+    if args.kinds_only:
+        print(json.dumps({"kinds_135m": bench_kinds(mllm, pgw)}))
         return
     if args.prefill_only:
         cfg = pgw.CONFIGS["smollm2-360m"]
@@ -746,6 +796,7 @@ def main():
                                  "us_per_launch": lm["cold_us"]}
     if not args.no_configs:
         line["configs"] = bench_configs(mllm, pgw, args, oracle)
+        line["configs"]["kinds_135m"] = bench_kinds(mllm, pgw)
     print(json.dumps(line), flush=True)
 
 

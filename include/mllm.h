@@ -157,8 +157,15 @@ typedef struct mllm_model mllm_model;
 /* new PetitGPT(bundle) (infer.js:290-311) + the device upload of
  * GpuPetitGPT.init (webgpu.js:892-1106): copies the payload to HBM once and
  * allocates the KV cache and scratch.  payload is host memory.  Tensor names
- * follow the converters (lm_head, blocks.{i}.attn.qkv, ...).  Q4 matrices only
- * (plus f32 norms/biases/positions). */
+ * follow the converters (lm_head, blocks.{i}.attn.qkv, ...).  Matrices may be
+ * stored in any kind infer.js:313-346 binds (f32, f16, bf16, per-row Q8, Q4
+ * of a group size that is a multiple of 8) or as Q8 group-32, each 16-byte
+ * aligned; norms, biases and positions are f32.  A model whose layer matrices
+ * and lm_head are all Q4 group-32, at the fused step's shapes, runs the
+ * fused decode step (mllm_decode_kernel_name: "k_flow3", "phase kernels",
+ * ...); any other runs the kind-generic step ("generic kernels": a few
+ * kernels per layer and token, exec modes 1 and 2 only, prompts token by
+ * token). */
 int mllm_model_create(const mllm_config *cfg, const void *payload, uint64_t payload_nbytes,
                       const mllm_tensor *tensors, int n_tensors, mllm_model **out);
 /* GpuPetitGPT.destroy (webgpu.js:1284-1297); NULL is accepted. */

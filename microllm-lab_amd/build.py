@@ -37,7 +37,7 @@ CONVERT_LIB = os.path.join(PKG, "convert", "libpgwconvert.so")
 CONVERT_BIN = os.path.join(PKG, "convert", "pgw_convert")
 NAPI_OUT = os.path.join(PKG, "js", "mllm_napi.node")
 
-HIP_SOURCES = ["mllm_ops.hip", "mllm_engine.hip", "mllm_prefill.hip"]
+HIP_SOURCES = ["mllm_ops.hip", "mllm_engine.hip", "mllm_prefill.hip", "mllm_generic.hip"]
 # per-source flags: the prefill kernels consume their matrix-core results in
 # VALU epilogues, so the results go to VGPRs (no AGPR-to-VGPR copies)
 EXTRA_FLAGS = {"mllm_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}

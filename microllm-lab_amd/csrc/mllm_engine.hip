@@ -57,6 +57,7 @@
 
 #include "mllm_device.h"
 #include "mllm_host.h"
+#include "mllm_generic.h"
 #include "mllm_prefill.h"
 
 namespace mllm {
@@ -2828,7 +2829,7 @@ struct mllm_model {
   bool dbg_on = false;              // some knob set: prompts take the pass path
   struct Named {
     std::string name;
-    int storage, rows, cols;
+    int storage, rows, cols, group;
     const void *data;
     const float *scale;
   };
@@ -2872,6 +2873,12 @@ struct mllm_model {
   int pf_tc_max = 0;  // tokens the work buffers hold
   hipEvent_t ev_pf = nullptr;
   std::vector<void *> allocs;
+  // models the fused step does not take (a matrix other than Q4 group-32, or
+  // a shape outside its limits) run the kind-generic step (mllm_generic.hip)
+  bool generic = false;
+  GArgs g{};
+  std::vector<GLayer> g_layers, g_layers_base;
+  int *d_ids = nullptr;  // a call's token ids (+ a slot for a chain's first token)
 };
 
 namespace {
@@ -2946,9 +2953,9 @@ const mllm_model::Named *find(const mllm_model *M, const std::string &n) {
 int get_q4(mllm_model *M, const std::string &n, int rows, int cols, Q4Mat *out) {
   const auto *t = find(M, n);
   if (!t) return set_error(MLLM_ERR_INVALID, "missing tensor %s", n.c_str());
-  if (t->storage != MLLM_Q4)
-    return set_error(MLLM_ERR_UNSUPPORTED, "tensor %s: storage %d unsupported by the decode engine (q4 only)",
-                     n.c_str(), t->storage);
+  if (t->storage != MLLM_Q4 || t->group != 32)
+    return set_error(MLLM_ERR_UNSUPPORTED, "tensor %s: storage %d group %d unsupported by the fused step (q4 group 32 only)",
+                     n.c_str(), t->storage, t->group);
   if (t->rows != rows || t->cols != cols)
     return set_error(MLLM_ERR_INVALID, "tensor %s has shape [%d,%d], expected [%d,%d]", n.c_str(), t->rows, t->cols,
                      rows, cols);
@@ -3246,6 +3253,138 @@ std::vector<float> build_rope_table(const mllm_config &c, int hd, bool sin_table
   return tab;
 }
 
+// Every layer matrix and the lm_head stored Q4 group-32 (the fused step's
+// weights); missing tensors are reported by the path that reads them.
+bool all_q4_g32(const mllm_model *M) {
+  static const char *const llama[] = {"attn.qkv", "attn.proj", "mlp.w1", "mlp.w3", "mlp.w2"};
+  static const char *const gpt2[] = {"attn.qkv", "attn.proj", "mlp.fc", "mlp.proj"};
+  auto q4 = [&](const std::string &n) {
+    const auto *t = find(M, n);
+    return !t || (t->storage == MLLM_Q4 && t->group == 32);
+  };
+  if (!q4("lm_head")) return false;
+  for (int i = 0; i < M->cfg.n_layers; ++i) {
+    const std::string b = "blocks." + std::to_string(i) + ".";
+    if (M->cfg.arch == 1) {
+      for (const char *m : gpt2)
+        if (!q4(b + m)) return false;
+    } else {
+      for (const char *m : llama)
+        if (!q4(b + m)) return false;
+    }
+  }
+  return true;
+}
+
+// A matrix for the kind-generic step: any storage it reads, rows x cols,
+// 16-byte aligned data (chunks of 8 columns are read as one vector).
+int get_gmat(mllm_model *M, const std::string &n, int rows, int cols, GMat *out) {
+  const auto *t = find(M, n);
+  if (!t) return set_error(MLLM_ERR_INVALID, "missing tensor %s", n.c_str());
+  if (!g_kind_supported(t->storage, t->group))
+    return set_error(MLLM_ERR_UNSUPPORTED, "tensor %s: storage %d (group %d) unsupported", n.c_str(), t->storage,
+                     t->group);
+  if (t->rows != rows || t->cols != cols)
+    return set_error(MLLM_ERR_INVALID, "tensor %s has shape [%d,%d], expected [%d,%d]", n.c_str(), t->rows, t->cols,
+                     rows, cols);
+  if (cols % 8 || ((t->storage == MLLM_Q4 || t->storage == MLLM_Q8G32) && cols % t->group))
+    return set_error(MLLM_ERR_UNSUPPORTED, "tensor %s: %d columns do not divide into its groups", n.c_str(), cols);
+  if (((uintptr_t)t->data & 15) != 0) return set_error(MLLM_ERR_INVALID, "tensor %s is not 16-byte aligned", n.c_str());
+  *out = GMat{t->data, t->scale, t->storage, rows, cols, t->storage == MLLM_Q8G32 ? 32 : t->group};
+  return 0;
+}
+
+// The kind-generic model: its matrices as stored, the f32 vectors, the
+// RoPE tables, the KV cache and one token's work rows.
+int generic_create(mllm_model *M) {
+  const mllm_config &c = M->cfg;
+  const int D = c.d_model, FF = c.d_ff, NH = c.n_heads, NKV = c.n_kv_heads, V = c.vocab_size, L = c.n_layers;
+  const int kvd = NKV * HD;
+  // the staged input row (k_g_gemv), the attention weights (k_g_attn) and
+  // the history lists (k_g_argmax) live in LDS
+  if (std::max(D, FF) > 15000)
+    return set_error(MLLM_ERR_UNSUPPORTED, "rows of %d columns exceed the staged row", std::max(D, FF));
+  if ((size_t)(HD + c.max_seq_len + 4 + 256 + 4) * sizeof(float) > 64 * 1024)
+    return set_error(MLLM_ERR_UNSUPPORTED, "max_seq_len %d exceeds the attention workgroup's LDS", c.max_seq_len);
+  GArgs &A = M->g;
+  A.arch = c.arch;
+  A.L = L;
+  A.D = D;
+  A.NH = NH;
+  A.NKV = NKV;
+  A.FF = FF;
+  A.V = V;
+  A.max_seq = c.max_seq_len;
+  A.kv_fp16 = c.kv_fp16 ? 1 : 0;
+  A.eps = c.norm_eps > 0 ? c.norm_eps : 1e-6f;
+  A.attn_scale = (float)(1.0 / sqrt((double)HD));
+  M->g_layers.assign(L, GLayer{});
+  for (int i = 0; i < L; ++i) {
+    GLayer &w = M->g_layers[i];
+    const std::string b = "blocks." + std::to_string(i) + ".";
+    int rc = get_gmat(M, b + "attn.qkv", D + 2 * kvd, D, &w.qkv);
+    if (!rc) rc = get_gmat(M, b + "attn.proj", D, D, &w.proj);
+    if (c.arch == 1) {
+      if (!rc) rc = get_gmat(M, b + "mlp.fc", FF, D, &w.w1);
+      if (!rc) rc = get_gmat(M, b + "mlp.proj", D, FF, &w.w2);
+      if (!rc) rc = get_f32(M, b + "ln1", 2 * D, &w.n1);
+      if (!rc) rc = get_f32(M, b + "ln2", 2 * D, &w.n2);
+      if (!rc) rc = get_f32(M, b + "attn.qkv_bias", D + 2 * kvd, &w.qkv_b);
+      if (!rc) rc = get_f32(M, b + "attn.proj_bias", D, &w.proj_b);
+      if (!rc) rc = get_f32(M, b + "mlp.fc_bias", FF, &w.fc_b);
+      if (!rc) rc = get_f32(M, b + "mlp.proj_bias", D, &w.mproj_b);
+    } else {
+      if (!rc) rc = get_gmat(M, b + "mlp.w1", FF, D, &w.w1);
+      if (!rc) rc = get_gmat(M, b + "mlp.w3", FF, D, &w.w3);
+      if (!rc) rc = get_gmat(M, b + "mlp.w2", D, FF, &w.w2);
+      if (!rc) rc = get_f32(M, b + "norm1", D, &w.n1);
+      if (!rc) rc = get_f32(M, b + "norm2", D, &w.n2);
+    }
+    if (rc) return rc;
+  }
+  M->g_layers_base = M->g_layers;
+  A.layers = M->g_layers.data();
+  if (int rc = get_gmat(M, "lm_head", V, D, &A.lm)) return rc;
+  if (c.arch == 1) {
+    int rc = get_f32(M, "ln_f", 2 * D, &A.norm_f);
+    if (!rc) rc = get_f32(M, "wpe", (size_t)c.max_seq_len * D, &A.wpe);
+    if (!rc) rc = get_f32(M, "scale_factors", D, &A.sf, false);
+    if (rc) return rc;
+  } else {
+    if (int rc = get_f32(M, "norm_f", D, &A.norm_f)) return rc;
+    int rd = 0;
+    std::vector<float> cs = build_rope_table(c, HD, false, &rd), sn = build_rope_table(c, HD, true, &rd);
+    if (int rc = dev_alloc(M, (void **)&M->d_rope_cos, cs.size() * 4)) return rc;
+    if (int rc = dev_alloc(M, (void **)&M->d_rope_sin, sn.size() * 4)) return rc;
+    MLLM_HIP(hipMemcpy(M->d_rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    MLLM_HIP(hipMemcpy(M->d_rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    A.rope_cos = M->d_rope_cos;
+    A.rope_sin = M->d_rope_sin;
+    A.rope_dim = rd;
+  }
+  const size_t kv_bytes = (size_t)L * 2 * NKV * c.max_seq_len * HD * (c.kv_fp16 ? 2 : 4);
+  int rc = dev_alloc(M, &A.kv, kv_bytes);
+  if (!rc) rc = dev_alloc(M, (void **)&A.x, sizeof(float) * D);
+  if (!rc) rc = dev_alloc(M, (void **)&A.qkv, sizeof(float) * (D + 2 * kvd));
+  if (!rc) rc = dev_alloc(M, (void **)&A.att, sizeof(float) * D);
+  if (!rc) rc = dev_alloc(M, (void **)&A.h, sizeof(float) * FF);
+  if (!rc) rc = dev_alloc(M, (void **)&M->d_logits, sizeof(float) * MAXT * (size_t)V);
+  if (!rc) rc = dev_alloc(M, (void **)&A.res, sizeof(int) * MAXT);
+  if (!rc) rc = dev_alloc(M, (void **)&A.state, sizeof(int) * 2);
+  if (!rc) rc = dev_alloc(M, (void **)&M->d_ids, sizeof(int) * ((size_t)c.max_seq_len + 1));
+  if (!rc) rc = dev_alloc(M, (void **)&M->d_hist, sizeof(int) * ((size_t)c.max_seq_len + 1));
+  if (!rc) rc = dev_alloc(M, (void **)&M->d_gemv_x, sizeof(float) * std::max(FF, D) * 4);
+  if (!rc) rc = dev_alloc(M, (void **)&M->d_gemv_y, sizeof(float) * std::max((size_t)V, (size_t)std::max(FF, D + 2 * kvd)));
+  if (rc) return rc;
+  MLLM_HIP(hipMemset(A.kv, 0, kv_bytes));
+  MLLM_HIP(hipMemset(A.state, 0, sizeof(int) * 2));
+  A.logits = M->d_logits;
+  M->generic = true;
+  M->max_pass = MAXT;
+  M->exec_mode = 1;
+  return 0;
+}
+
 }  // namespace
 
 extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, uint64_t payload_nbytes,
@@ -3258,21 +3397,16 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
                  c.vocab_size > 0 && c.max_seq_len > 0,
              "invalid config");
   MLLM_CHECK(c.d_model % c.n_heads == 0 && c.n_heads % c.n_kv_heads == 0, "heads do not divide");
-  if (c.n_layers >= TAGL) return set_error(MLLM_ERR_UNSUPPORTED, "%d layers (at most %d)", c.n_layers, TAGL - 1);
   // coherent loads and stores address the KV cache with 32-bit byte offsets
   MLLM_CHECK((uint64_t)c.n_layers * 2 * c.n_kv_heads * c.max_seq_len * HD * (c.kv_fp16 ? 2 : 4) < (1ull << 31),
              "KV cache of %d layers x %d positions exceeds 2 GiB", c.n_layers, c.max_seq_len);
   if (c.d_model / c.n_heads != HD)
     return set_error(MLLM_ERR_UNSUPPORTED, "head_dim %d unsupported (64 only)", c.d_model / c.n_heads);
-  if (c.d_model % 32 || c.d_model > 1024)
-    return set_error(MLLM_ERR_UNSUPPORTED, "d_model %d unsupported (a multiple of 32, <= 1024)", c.d_model);
-  if (c.d_ff % UNITS || c.d_ff > UNITS * PB * NBMAX)
-    return set_error(MLLM_ERR_UNSUPPORTED, "d_ff %d unsupported (a multiple of %d, <= %d)", c.d_ff, UNITS,
-                     UNITS * PB * NBMAX);
-  if (c.n_heads > PB * NBMAX) return set_error(MLLM_ERR_UNSUPPORTED, "n_heads %d > %d", c.n_heads, PB * NBMAX);
   if (c.arch == 1 && c.n_kv_heads != c.n_heads) return set_error(MLLM_ERR_INVALID, "gpt2 needs n_kv_heads == n_heads");
-  if (c.arch == 0 && (int)floor(HD * c.rope_pct) != HD)
-    return set_error(MLLM_ERR_UNSUPPORTED, "partial rotary (ropePct %g) unsupported", c.rope_pct);
+  // the fused step's shape limits; other shapes take the kind-generic step
+  const bool fused_shape = c.n_layers < TAGL && c.d_model % 32 == 0 && c.d_model <= 1024 && c.d_ff % UNITS == 0 &&
+                           c.d_ff <= UNITS * PB * NBMAX && c.n_heads <= PB * NBMAX &&
+                           (c.arch == 1 || (int)floor(HD * c.rope_pct) == HD);
 
   mllm_model *M = new mllm_model();
   M->cfg = c;
@@ -3301,10 +3435,16 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
     if (t.offset + t.nbytes > payload_nbytes || t.scale_offset + t.scale_nbytes > payload_nbytes)
       return fail(set_error(MLLM_ERR_INVALID, "tensor %s exceeds the payload", t.name));
     const bool scaled = t.storage == MLLM_Q4 || t.storage == MLLM_Q8 || t.storage == MLLM_Q8G32;
-    M->tensors.push_back({t.name, t.storage, t.rows, t.cols, M->d_payload + t.offset,
+    M->tensors.push_back({t.name, t.storage, t.rows, t.cols, t.group > 0 ? t.group : 32, M->d_payload + t.offset,
                           scaled ? reinterpret_cast<const float *>(M->d_payload + t.scale_offset) : nullptr});
   }
 
+  if (!fused_shape || !all_q4_g32(M)) {
+    if (int rc = generic_create(M)) return fail(rc);
+    *out = M;
+    clear_error();
+    return 0;
+  }
   const int D = c.d_model, FF = c.d_ff, NH = c.n_heads, NKV = c.n_kv_heads, V = c.vocab_size, L = c.n_layers;
   const int kvd = NKV * HD;
   M->layers.resize(L);
@@ -3653,6 +3793,7 @@ extern "C" int mllm_get_exec_mode(const mllm_model *M) { return M ? M->exec_mode
 extern "C" const char *mllm_decode_kernel_name(const mllm_model *M) {
   static const char *const names[3] = {"k_flow<4>", "k_flow<5>", "k_flow<6>"};
   if (!M) return "";
+  if (M->generic) return "generic kernels";
   if (M->exec_mode < 3) return "phase kernels";
   return use_flow3(M, M->cache_len) ? "k_flow3" : names[M->aq_idx];
 }
@@ -3673,6 +3814,24 @@ extern "C" int mllm_set_debug(mllm_model *M, int max_layers, int no_attn, int no
   const int L = M->cfg.n_layers;
   MLLM_HIP(hipStreamSynchronize(M->stream));
   bool on = false;
+  if (M->generic) {
+    // a dropped block's kernels are not launched (its bias goes with it)
+    for (int li = 0; li < L; ++li) {
+      int d = 0;
+      if (max_layers >= 0 && li >= max_layers) d = 3;
+      if (no_attn) d |= 1;
+      if (no_mlp || (mlp_to >= 0 && li >= mlp_to)) d |= 2;
+      M->g_layers[li] = M->g_layers_base[li];
+      M->g_layers[li].dbg = d;
+      on |= d != 0;
+    }
+    M->dbg_max_layers = max_layers;
+    M->dbg_no_attn = no_attn != 0;
+    M->dbg_no_mlp = no_mlp != 0;
+    M->dbg_mlp_to = mlp_to;
+    M->dbg_on = on;
+    return 0;
+  }
   for (int li = 0; li < L; ++li) {
     LayerW w = M->layers_base[li];
     int d = 0;
@@ -3723,10 +3882,33 @@ static int fetch_outputs(mllm_model *M, int row, int nrows, float *logits, int32
   return 0;
 }
 
+// The kind-generic step over ids[0..n) at positions pos0..: logits and
+// argmax of every row (rows: verify) or of the last token only.
+static int g_run(mllm_model *M, const int32_t *ids, int n, int pos0, bool rows, float *logits, int32_t *argmax) {
+  MLLM_HIP(hipMemcpyAsync(M->d_ids, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, M->stream));
+  MLLM_HIP(hipEventRecord(M->ev0, M->stream));
+  for (int t = 0; t < n; ++t)
+    if (int rc = g_step(M->g, M->d_ids + t, pos0 + t, rows ? t : (t == n - 1 ? 0 : -1), nullptr, M->stream)) return rc;
+  MLLM_HIP(hipEventRecord(M->ev1, M->stream));
+  MLLM_HIP(hipStreamSynchronize(M->stream));
+  MLLM_HIP(hipEventElapsedTime(&M->last_ms, M->ev0, M->ev1));
+  M->last_tokens = n;
+  const int nr = rows ? n : 1;
+  if (logits)
+    MLLM_HIP(hipMemcpy(logits, M->d_logits, sizeof(float) * (size_t)nr * M->cfg.vocab_size, hipMemcpyDeviceToHost));
+  if (argmax) MLLM_HIP(hipMemcpy(argmax, M->g.res, sizeof(int32_t) * nr, hipMemcpyDeviceToHost));
+  return 0;
+}
+
 extern "C" int mllm_forward_prompt(mllm_model *M, const int32_t *ids, int n, float *logits, int32_t *argmax) {
   MLLM_CHECK(M && ids, "null argument");
   MLLM_CHECK(n > 0 && n <= M->cfg.max_seq_len, "prompt length %d out of range", n);
   if (int rc = check_ids(M, ids, n)) return rc;
+  if (M->generic) {
+    if (int rc = g_run(M, ids, n, 0, false, logits, argmax)) return rc;
+    M->cache_len = n;
+    return 0;
+  }
   if (M->pf_min > 0 && n >= M->pf_min && !M->dbg_on) {
     // the prompt in chunks; the last one also forms the logits
     MLLM_HIP(hipEventRecord(M->ev_pf, M->stream));
@@ -3756,6 +3938,11 @@ extern "C" int mllm_forward_decode(mllm_model *M, int32_t id, float *logits, int
   MLLM_CHECK(M, "null model");
   MLLM_CHECK(M->cache_len < M->cfg.max_seq_len, "KV cache full (%d)", M->cache_len);
   if (int rc = check_ids(M, &id, 1)) return rc;
+  if (M->generic) {
+    if (int rc = g_run(M, &id, 1, M->cache_len, false, logits, argmax)) return rc;
+    M->cache_len += 1;
+    return 0;
+  }
   if (int rc = run_pass(M, &id, 1, M->cache_len, 1)) return rc;
   M->cache_len += 1;
   return fetch_outputs(M, 0, 1, logits, argmax);
@@ -3766,6 +3953,11 @@ extern "C" int mllm_forward_verify(mllm_model *M, const int32_t *ids, int n, int
   MLLM_CHECK(n > 0 && n <= M->max_pass, "verify length %d out of range [1, %d]", n, M->max_pass);
   MLLM_CHECK(M->cache_len + n <= M->cfg.max_seq_len, "verify pass exceeds the context");
   if (int rc = check_ids(M, ids, n)) return rc;
+  if (M->generic) {
+    if (int rc = g_run(M, ids, n, M->cache_len, true, logits, argmax)) return rc;
+    M->cache_len += n;
+    return 0;
+  }
   if (int rc = run_pass(M, ids, n, M->cache_len, 2)) return rc;
   M->cache_len += n;
   return fetch_outputs(M, 0, n, logits, argmax);
@@ -3780,6 +3972,29 @@ extern "C" int mllm_decode_chain(mllm_model *M, int32_t first, int n_steps, int3
   MLLM_CHECK(n_hist == 0 || hist, "null history");
   if (int rc = check_ids(M, &first, 1)) return rc;
   if (n_hist) MLLM_HIP(hipMemcpyAsync(M->d_hist, hist, sizeof(int32_t) * n_hist, hipMemcpyHostToDevice, M->stream));
+  if (M->generic) {
+    // each step's argmax lands at d_hist[n_hist + i] and is step i + 1's
+    // input; a step after an EOS returns at once
+    MLLM_HIP(hipMemcpyAsync(M->d_ids, &first, sizeof(int32_t), hipMemcpyHostToDevice, M->stream));
+    MLLM_HIP(hipMemsetAsync(M->g.state, 0, sizeof(int) * 2, M->stream));
+    MLLM_HIP(hipEventRecord(M->ev0, M->stream));
+    for (int i = 0; i < n_steps; ++i) {
+      const GChain ch{M->d_hist, n_hist, i, eos_id, M->cfg.arch == 1 ? 1 : 0};
+      const int *tok = i == 0 ? M->d_ids : M->d_hist + n_hist + i - 1;
+      if (int rc = g_step(M->g, tok, M->cache_len + i, 0, &ch, M->stream)) return rc;
+    }
+    MLLM_HIP(hipEventRecord(M->ev1, M->stream));
+    MLLM_HIP(hipStreamSynchronize(M->stream));
+    MLLM_HIP(hipEventElapsedTime(&M->last_ms, M->ev0, M->ev1));
+    int st[2] = {0, 0};
+    MLLM_HIP(hipMemcpy(st, M->g.state, sizeof st, hipMemcpyDeviceToHost));
+    MLLM_CHECK(st[1] >= 1 && st[1] <= n_steps, "chain emitted %d ids of %d steps", st[1], n_steps);
+    MLLM_HIP(hipMemcpy(out_ids, M->d_hist + n_hist, sizeof(int32_t) * st[1], hipMemcpyDeviceToHost));
+    *n_out = st[1];
+    M->last_tokens = st[1];
+    M->cache_len += st[1];
+    return 0;
+  }
   PassState &s = *M->h_st;
   memset(&s, 0, sizeof s);
   s.pos0 = M->cache_len;
@@ -3817,6 +4032,7 @@ extern "C" int mllm_decode_chain(mllm_model *M, int32_t first, int n_steps, int3
 
 extern "C" int mllm_profile_decode(mllm_model *M, int32_t first, int n_steps, float *phase_us) {
   MLLM_CHECK(M && phase_us, "null argument");
+  if (M->generic) return set_error(MLLM_ERR_UNSUPPORTED, "phase profile: the fused step's phases only");
   MLLM_CHECK(n_steps > 0, "n_steps %d", n_steps);
   MLLM_CHECK(M->cache_len + n_steps <= M->cfg.max_seq_len, "profile run exceeds the context");
   if (int rc = check_ids(M, &first, 1)) return rc;
@@ -3899,7 +4115,14 @@ extern "C" int mllm_model_gemv(mllm_model *M, const char *name, const float *x, 
   int rc;
   switch (t->storage) {
   case MLLM_Q4:
-    rc = mllm_gemv_q4(t->rows, t->cols, (const uint8_t *)t->data, t->scale, 32, M->d_gemv_x, M->d_gemv_y, M->stream);
+    rc = t->group == 32 ? mllm_gemv_q4(t->rows, t->cols, (const uint8_t *)t->data, t->scale, 32, M->d_gemv_x,
+                                       M->d_gemv_y, M->stream)
+                        : g_gemv(GMat{t->data, t->scale, t->storage, t->rows, t->cols, t->group}, M->d_gemv_x,
+                                 M->d_gemv_y, M->stream);
+    break;
+  case MLLM_F16:
+  case MLLM_BF16:
+    rc = g_gemv(GMat{t->data, nullptr, t->storage, t->rows, t->cols, 0}, M->d_gemv_x, M->d_gemv_y, M->stream);
     break;
   case MLLM_Q8:
     rc = mllm_gemv_q8(t->rows, t->cols, (const int8_t *)t->data, t->scale, M->d_gemv_x, M->d_gemv_y, M->stream);

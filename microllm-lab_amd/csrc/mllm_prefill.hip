@@ -65,6 +65,7 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 enum { EPI_QKV = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_GELU = 3 };
@@ -466,23 +467,30 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
       }
   }
   if (KS > 1) {
-    float *mine = red + (size_t)tid() * 32;
+    // partials value-major in 16-byte quads, red4[q * WG + thread]: the 64
+    // lanes of a wave touch 1 KiB of consecutive LDS per access, so no two
+    // lanes of a pass share a bank
+    v4f *red4 = reinterpret_cast<v4f *>(red);
     if (ks > 0) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        mine[v] = acc0[v];
-        mine[16 + v] = acc1[v];
+      for (int q = 0; q < 4; ++q) {
+        red4[q * WG + tid()] = v4f{acc0[4 * q], acc0[4 * q + 1], acc0[4 * q + 2], acc0[4 * q + 3]};
+        red4[(4 + q) * WG + tid()] = v4f{acc1[4 * q], acc1[4 * q + 1], acc1[4 * q + 2], acc1[4 * q + 3]};
       }
     }
     __syncthreads();
     if (ks > 0) return;
 #pragma unroll
     for (int k = 1; k < KS; ++k) {
-      const float *o = mine + (size_t)k * 64 * 32;  // the same lane of slice k's wave
+      const int o = tid() + 64 * k;  // the same lane of slice k's wave
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        acc0[v] = acc0[v] + o[v];
-        acc1[v] = acc1[v] + o[16 + v];
+      for (int q = 0; q < 4; ++q) {
+        const v4f a = red4[q * WG + o], b = red4[(4 + q) * WG + o];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc0[4 * q + e] = acc0[4 * q + e] + a[e];
+          acc1[4 * q + e] = acc1[4 * q + e] + b[e];
+        }
       }
     }
   }

@@ -76,6 +76,14 @@ def quant_q8row(mat: np.ndarray):
     return np.ascontiguousarray(q), np.ascontiguousarray(sc)
 
 
+def f32_to_bf16_bits(mat: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns of f32 values, rounded to nearest even (NaN kept quiet)."""
+    u = np.ascontiguousarray(mat, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(np.asarray(mat, np.float32))
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
 def dequant_q4(packed: np.ndarray, scales: np.ndarray, group: int = GROUP) -> np.ndarray:
     """weights.js:106-123 (vectorised)."""
     rows = packed.shape[0]
@@ -208,7 +216,51 @@ class PgwWriter:
             "nbytes": int(data.nbytes),
         })
 
-    def finish(self, cfg: Config, header_group: Optional[int] = None) -> bytes:
+    def add_matrix(self, name: str, arr: np.ndarray, storage: str = "q4", kind: Optional[str] = None,
+                   group: int = GROUP):
+        """A matrix in any storage weights.js reads (f32, f16, bf16, per-row
+        q8, q4 of any group) or q8g32.  q4 at group 32 is add_q4 (the
+        converters' layout, byte for byte); the other storages have no writer
+        in the reference, so their blobs (scales first, then data) each start
+        on a 16-byte boundary, which the GPU engine reads them with."""
+        if storage == "q4" and group == GROUP and kind in (None, "q4"):
+            self.add_q4(name, arr)
+            return
+        arr = np.ascontiguousarray(arr, dtype=np.float32)
+        rows, cols = arr.shape
+        scales = None
+        if storage == "q4":
+            data, scales = quant_q4(arr, group)
+        elif storage == "q8":
+            data, scales = quant_q8row(arr)
+        elif storage == "q8g32":
+            data, scales = quant_q8g32(arr)
+        elif storage == "f16":
+            data = arr.astype(np.float16).view(np.uint16)
+        elif storage == "bf16":
+            data = f32_to_bf16_bits(arr)
+        elif storage == "f32":
+            data = arr
+        else:
+            raise ValueError(storage)
+        e = {"name": name, "shape": [int(rows), int(cols)], "kind": kind or storage, "storage": storage}
+        if storage in ("q4", "q8g32"):
+            e["group"] = int(group if storage == "q4" else 32)
+        if scales is not None:
+            self._pad16()
+            e["scaleOffset"] = self.blobs.tell()
+            e["scaleNbytes"] = int(scales.size * 4)
+            self.blobs.write(np.ascontiguousarray(scales, np.float32).tobytes())
+        self._pad16()
+        e["offset"] = self.blobs.tell()
+        e["nbytes"] = int(data.nbytes)
+        self.blobs.write(np.ascontiguousarray(data).tobytes())
+        self.entries.append(e)
+
+    def _pad16(self):
+        self.blobs.write(b"\x00" * (-self.blobs.tell() % 16))
+
+    def finish(self, cfg: Config, header_group: Optional[int] = None, kind: str = "q4") -> bytes:
         payload = self.blobs.getvalue()
         table = json.dumps(self.entries, separators=(",", ":")).encode("utf-8")
         table_off = 256
@@ -216,7 +268,7 @@ class PgwWriter:
         payload_off = table_off + len(table) + pad
         header = bytearray(256)
         header[0:4] = b"PGW1"
-        header[4] = 4
+        header[4] = {v: k for k, v in DTYPE_CODE.items()}.get(kind, 4)
         header[5] = 1 if cfg.arch == "gpt2" else 0
         qg = GROUP if header_group is None else header_group
         struct.pack_into("<8I", header, 8, cfg.vocab_size, cfg.n_layers, cfg.d_model, cfg.n_heads,
@@ -244,25 +296,39 @@ def _normal(rng: np.random.Generator, shape, std: float = 0.02) -> np.ndarray:
     return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
 
 
-def make_llama(cfg: Config, seed: int = 0, std: float = 0.02, norm_gain: float = 1.0) -> bytes:
-    """Llama-style PGW1 in convert_hf_to_pgw.py:104-122 order; weights N(0, std),
-    quantised by quant_q4; norm gains constant."""
+def _storages(kind: str, storages: Optional[Dict[str, str]]):
+    """The matrix storage of each tensor name: `kind` (q4, q8, q8g32, f16,
+    bf16, f32) unless `storages` names another (a mixed model)."""
+    return lambda name: (storages or {}).get(name, kind)
+
+
+def make_llama(cfg: Config, seed: int = 0, std: float = 0.02, norm_gain: float = 1.0, kind: str = "q4",
+               storages: Optional[Dict[str, str]] = None, group: int = GROUP) -> bytes:
+    """Llama-style PGW1 in convert_hf_to_pgw.py:104-122 order; weights N(0, std)
+    stored as `kind` (q4: quant_q4, the converter's format); norm gains
+    constant.  `storages` overrides the storage of named matrices; `group` is
+    the Q4 group size."""
     rng = np.random.default_rng(seed)
     hd = cfg.d_model // cfg.n_heads
     kv = cfg.n_kv_heads * hd
     w = PgwWriter()
-    w.add_q4("lm_head", _normal(rng, (cfg.vocab_size, cfg.d_model), std))
+    st = _storages(kind, storages)
+
+    def mat(name, shape):
+        w.add_matrix(name, _normal(rng, shape, std), st(name), kind=kind, group=group)
+
+    mat("lm_head", (cfg.vocab_size, cfg.d_model))
     ones = np.full(cfg.d_model, norm_gain, np.float32)
     for i in range(cfg.n_layers):
         w.add_f32(f"blocks.{i}.norm1", ones)
-        w.add_q4(f"blocks.{i}.attn.qkv", _normal(rng, (cfg.d_model + 2 * kv, cfg.d_model), std))
-        w.add_q4(f"blocks.{i}.attn.proj", _normal(rng, (cfg.d_model, cfg.d_model), std))
+        mat(f"blocks.{i}.attn.qkv", (cfg.d_model + 2 * kv, cfg.d_model))
+        mat(f"blocks.{i}.attn.proj", (cfg.d_model, cfg.d_model))
         w.add_f32(f"blocks.{i}.norm2", ones)
-        w.add_q4(f"blocks.{i}.mlp.w1", _normal(rng, (cfg.d_ff, cfg.d_model), std))
-        w.add_q4(f"blocks.{i}.mlp.w3", _normal(rng, (cfg.d_ff, cfg.d_model), std))
-        w.add_q4(f"blocks.{i}.mlp.w2", _normal(rng, (cfg.d_model, cfg.d_ff), std))
+        mat(f"blocks.{i}.mlp.w1", (cfg.d_ff, cfg.d_model))
+        mat(f"blocks.{i}.mlp.w3", (cfg.d_ff, cfg.d_model))
+        mat(f"blocks.{i}.mlp.w2", (cfg.d_model, cfg.d_ff))
     w.add_f32("norm_f", ones)
-    return w.finish(cfg)
+    return w.finish(cfg, kind=kind if kind in DTYPE_CODE.values() else "q8")
 
 
 def make_cycle_llama(cfg: Config, cycle, seed: int = 0, std: float = 0.02, layer_std: float = 0.002,
@@ -316,16 +382,23 @@ def make_cycle_llama(cfg: Config, cycle, seed: int = 0, std: float = 0.02, layer
 
 
 def make_gpt2(cfg: Config, seed: int = 0, std: float = 0.02, scale_factors: Optional[np.ndarray] = None,
-              bias_std: float = 0.0) -> bytes:
+              bias_std: float = 0.0, kind: str = "q4", storages: Optional[Dict[str, str]] = None,
+              group: int = GROUP) -> bytes:
     """GPT-2 PGW1 in convert_gpt2_to_pgw.py:135-164 order; header qGroup = 1 as the
     converter writes it (convert_gpt2_to_pgw.py:175).  LN gamma 1, beta 0,
-    biases N(0, bias_std) (0 by default), scale_factors 1 unless given."""
+    biases N(0, bias_std) (0 by default), scale_factors 1 unless given;
+    matrices stored as `kind` (storages / group as in make_llama)."""
     rng = np.random.default_rng(seed)
     d, ff = cfg.d_model, cfg.d_ff
     w = PgwWriter()
+    st = _storages(kind, storages)
+
+    def mat(name, shape):
+        w.add_matrix(name, _normal(rng, shape, std), st(name), kind=kind, group=group)
+
     sf = np.ones(d, np.float32) if scale_factors is None else np.asarray(scale_factors, np.float32)
     w.add_f32("scale_factors", sf)
-    w.add_q4("lm_head", _normal(rng, (cfg.vocab_size, d), std))
+    mat("lm_head", (cfg.vocab_size, d))
     w.add_f32("wpe", _normal(rng, (cfg.max_seq_len, d), std))
     w.add_f32("ln_f", np.concatenate([np.ones(d, np.float32) / sf, np.zeros(d, np.float32) / sf]))
     ln = np.concatenate([np.ones(d, np.float32), np.zeros(d, np.float32)])
@@ -335,16 +408,16 @@ def make_gpt2(cfg: Config, seed: int = 0, std: float = 0.02, scale_factors: Opti
 
     for i in range(cfg.n_layers):
         w.add_f32(f"blocks.{i}.ln1", ln)
-        w.add_q4(f"blocks.{i}.attn.qkv", _normal(rng, (3 * d, d), std))
+        mat(f"blocks.{i}.attn.qkv", (3 * d, d))
         w.add_f32(f"blocks.{i}.attn.qkv_bias", bias(3 * d))
-        w.add_q4(f"blocks.{i}.attn.proj", _normal(rng, (d, d), std))
+        mat(f"blocks.{i}.attn.proj", (d, d))
         w.add_f32(f"blocks.{i}.attn.proj_bias", bias(d))
         w.add_f32(f"blocks.{i}.ln2", ln)
-        w.add_q4(f"blocks.{i}.mlp.fc", _normal(rng, (ff, d), std))
+        mat(f"blocks.{i}.mlp.fc", (ff, d))
         w.add_f32(f"blocks.{i}.mlp.fc_bias", bias(ff))
-        w.add_q4(f"blocks.{i}.mlp.proj", _normal(rng, (d, ff), std))
+        mat(f"blocks.{i}.mlp.proj", (d, ff))
         w.add_f32(f"blocks.{i}.mlp.proj_bias", bias(d))
-    return w.finish(cfg, header_group=1)
+    return w.finish(cfg, header_group=1, kind=kind if kind in DTYPE_CODE.values() else "q8")
 
 
 def make_model(cfg: Config, seed: int = 0, **kw) -> bytes:

@@ -381,34 +381,3 @@ def test_chain_across_first_split_boundary_equals_graph():
             g.destroy()
         assert outs[0][0] == outs[1][0]
         assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))
-
-
-@gpu
-def test_decode_engine_rejects_non_q4_matrices():
-    """The decode engine takes Q4 layer matrices only (every benchmark
-    configuration is Q4; infer.js:313-346 also binds f32 / f16 / bf16 / q8).
-    A model whose MLP gate matrix is stored per-row Q8 is refused at creation
-    with MLLM_ERR_UNSUPPORTED and a message naming the tensor, instead of
-    being decoded through some other path."""
-    import dataclasses
-
-    from mllm import abi
-
-    bundle = build("llama", seed=5)
-    name = "blocks.0.mlp.w1"
-    rows, cols = bundle.tensors[name]["shape"]
-    q, sc = pgw.quant_q8row(np.random.default_rng(0).standard_normal((rows, cols)).astype(np.float32))
-    payload = bytearray(bundle.buffer[bundle.payload_off:])
-    payload += b"\x00" * (-len(payload) % 16)
-    off = len(payload)
-    payload += q.tobytes()
-    soff = len(payload)
-    payload += sc.tobytes()
-    tensors = dict(bundle.tensors)
-    tensors[name] = {**tensors[name], "storage": "q8", "offset": off, "nbytes": q.nbytes, "scaleOffset": soff,
-                     "scaleNbytes": sc.nbytes}
-    bad = dataclasses.replace(bundle, tensors=tensors, buffer=bytes(payload), payload_off=0)
-    print("decode engine: q8 layer matrix refused", flush=True)
-    with pytest.raises(abi.MllmError, match=f"{name}.*q4 only") as e:
-        mllm.PetitGPT(bad)
-    assert "UNSUPPORTED" in str(e.value)

@@ -16,7 +16,21 @@ transformers = pytest.importorskip("transformers")
 
 
 def _deq(bundle, name):
-    return pgw.dequant_q4(bundle.array(name), bundle.scales(name)).astype(np.float64)
+    """A matrix in float64 from its storage (weights.js:69-123 restated in
+    numpy, independently of the oracle's C dequantisers)."""
+    t = bundle.tensors[name]
+    st, a = t["storage"], bundle.array(name)
+    if st == "q4":
+        return pgw.dequant_q4(a, bundle.scales(name), int(t.get("group", 32))).astype(np.float64)
+    if st == "q8":
+        return a.astype(np.float64) * bundle.scales(name).astype(np.float64).reshape(-1, 1)
+    if st == "q8g32":
+        return a.astype(np.float64) * np.repeat(bundle.scales(name).astype(np.float64), 32, axis=1)
+    if st == "f16":
+        return a.view(np.float16).astype(np.float64)
+    if st == "bf16":
+        return (a.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    return a.astype(np.float64)
 
 
 def hf_llama(bundle):
@@ -105,6 +119,37 @@ def test_llama_forward_vs_hf(oracle_lib, norm_gain):
     got2 = ref.forward_decode(123)
     want2 = hf_logits(hf_llama(bundle), ids + [123])[-1]
     assert np.abs(got2 - want2).max() < 2e-4 * max(1.0, np.abs(want2).max())
+
+
+KINDS = [("q8", 32), ("q8g32", 32), ("f16", 32), ("bf16", 32), ("f32", 32), ("q4", 64)]
+
+
+@pytest.mark.parametrize("kind,group", KINDS)
+def test_llama_kinds_vs_hf(oracle_lib, kind, group):
+    """The oracle on every matrix storage infer.js:313-346 binds (and Q8
+    group-32, Q4 at group 64): its GEMVs and embedding rows against HF in
+    float64 on the same dequantised weights."""
+    cfg = pgw.small_config("llama", n_layers=2, n_heads=4, n_kv_heads=2, d_model=256, d_ff=512)
+    bundle = pgw.parse_pgw(pgw.make_llama(cfg, seed=3, std=0.05, kind=kind, group=group))
+    assert bundle.tensors["blocks.0.mlp.w1"]["storage"] == kind and bundle.tensors["lm_head"]["storage"] == kind
+    ref = oracle_lib.OracleModel(bundle)
+    ids = [5, 77, 300, 12, 9, 500, 41]
+    want = hf_logits(hf_llama(bundle), ids + [123])
+    got = ref.forward_prompt(ids)
+    assert np.abs(got - want[-2]).max() < 2e-4 * max(1.0, np.abs(want[-2]).max())
+    got2 = ref.forward_decode(123)
+    assert np.abs(got2 - want[-1]).max() < 2e-4 * max(1.0, np.abs(want[-1]).max())
+
+
+@pytest.mark.parametrize("kind,group", KINDS)
+def test_gpt2_kinds_vs_hf(oracle_lib, kind, group):
+    cfg = pgw.small_config("gpt2", n_layers=2, n_heads=4, n_kv_heads=4, d_model=256, d_ff=1024, max_seq_len=32)
+    bundle = pgw.parse_pgw(pgw.make_gpt2(cfg, seed=4, std=0.05, bias_std=0.05, kind=kind, group=group))
+    ref = oracle_lib.OracleModel(bundle)
+    ids = [3, 141, 59, 26, 5]
+    want = hf_logits(hf_gpt2(bundle), ids)
+    got = ref.forward_prompt(ids)
+    assert np.abs(got - want[-1]).max() < 2e-4 * max(1.0, np.abs(want[-1]).max())
 
 
 def test_gpt2_forward_vs_hf(oracle_lib):

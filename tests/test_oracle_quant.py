@@ -177,3 +177,53 @@ def test_quant_q8_ties_to_even(oracle_lib):
     q, s = oracle_lib.quant_q8g32(x)
     assert s[0, 0] == 1.0
     assert list(q[0, :6]) == [127, 0, 2, -2, 4, 0]
+
+
+def test_bf16_bits_round_to_nearest_even():
+    """pgw.f32_to_bf16_bits against torch's float32 -> bfloat16 conversion
+    (round to nearest even), including exact halfway cases and infinities."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(4096).astype(np.float32) * np.float32(3.0)
+    # exact halfway patterns: low 16 bits 0x8000 with even and odd bf16 lsb
+    u = np.array([0x3F808000, 0x3F818000, 0xBF808000, 0xBF818000, 0x7F7F8000], np.uint32)
+    x = np.concatenate([x, u.view(np.float32), np.array([np.inf, -np.inf, 0.0, -0.0], np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(pgw.f32_to_bf16_bits(x), want)
+
+
+@pytest.mark.parametrize("storage", ["q4", "q8", "q8g32", "f16", "bf16", "f32"])
+def test_add_matrix_round_trip(storage):
+    """A matrix written by PgwWriter.add_matrix reads back (Bundle.array /
+    scales, weights.js:42-67) as its quantiser's output, each blob 16-byte
+    aligned; q4 at group 32 is add_q4's layout byte for byte."""
+    rng = np.random.default_rng(11)
+    m = rng.standard_normal((48, 128)).astype(np.float32)
+    w = pgw.PgwWriter()
+    w.add_f32("pad", np.ones(3, np.float32))  # misaligns the blob on purpose
+    w.add_matrix("m", m, storage, group=64 if storage == "q4" else 32)
+    cfg = pgw.small_config("llama")
+    b = pgw.parse_pgw(w.finish(cfg, kind=storage if storage != "q8g32" else "q8"))
+    t = b.tensors["m"]
+    assert t["storage"] == storage and t["offset"] % 16 == 0
+    a = b.array("m")
+    if storage == "q4":
+        p, s = pgw.quant_q4(m, 64)
+        assert t["group"] == 64 and np.array_equal(a, p) and np.array_equal(b.scales("m"), s)
+    elif storage == "q8":
+        q, s = pgw.quant_q8row(m)
+        assert np.array_equal(a, q) and np.array_equal(b.scales("m").ravel(), s)
+    elif storage == "q8g32":
+        q, s = pgw.quant_q8g32(m)
+        assert np.array_equal(a, q) and np.array_equal(b.scales("m"), s)
+    elif storage == "f16":
+        assert np.array_equal(a.view(np.float16), m.astype(np.float16))
+    elif storage == "bf16":
+        assert np.array_equal(a, pgw.f32_to_bf16_bits(m))
+    else:
+        assert np.array_equal(a, m)
+    # group-32 q4 through add_matrix is add_q4 byte for byte
+    w1, w2 = pgw.PgwWriter(), pgw.PgwWriter()
+    w1.add_matrix("m", m, "q4")
+    w2.add_q4("m", m)
+    assert w1.finish(cfg) == w2.finish(cfg)
