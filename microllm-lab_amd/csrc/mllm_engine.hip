@@ -2878,7 +2878,9 @@ struct mllm_model {
   bool generic = false;
   GArgs g{};
   std::vector<GLayer> g_layers, g_layers_base;
-  int *d_ids = nullptr;  // a call's token ids (+ a slot for a chain's first token)
+  int *d_ids = nullptr;              // a call's token ids
+  GCursor *h_gcur = nullptr;         // pinned: the cursor a call starts from
+  hipGraphExec_t g_graph[2] = {};    // one step without / with the lm_head (exec mode 1)
 };
 
 namespace {
@@ -3370,15 +3372,18 @@ int generic_create(mllm_model *M) {
   if (!rc) rc = dev_alloc(M, (void **)&A.h, sizeof(float) * FF);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_logits, sizeof(float) * MAXT * (size_t)V);
   if (!rc) rc = dev_alloc(M, (void **)&A.res, sizeof(int) * MAXT);
-  if (!rc) rc = dev_alloc(M, (void **)&A.state, sizeof(int) * 2);
+  if (!rc) rc = dev_alloc(M, (void **)&A.cur, sizeof(GCursor));
   if (!rc) rc = dev_alloc(M, (void **)&M->d_ids, sizeof(int) * ((size_t)c.max_seq_len + 1));
   if (!rc) rc = dev_alloc(M, (void **)&M->d_hist, sizeof(int) * ((size_t)c.max_seq_len + 1));
   if (!rc) rc = dev_alloc(M, (void **)&M->d_gemv_x, sizeof(float) * std::max(FF, D) * 4);
   if (!rc) rc = dev_alloc(M, (void **)&M->d_gemv_y, sizeof(float) * std::max((size_t)V, (size_t)std::max(FF, D + 2 * kvd)));
   if (rc) return rc;
   MLLM_HIP(hipMemset(A.kv, 0, kv_bytes));
-  MLLM_HIP(hipMemset(A.state, 0, sizeof(int) * 2));
+  MLLM_HIP(hipMemset(A.cur, 0, sizeof(GCursor)));
+  MLLM_HIP(hipHostMalloc((void **)&M->h_gcur, sizeof(GCursor), hipHostMallocDefault));
   A.logits = M->d_logits;
+  A.ids = M->d_ids;
+  A.hist = M->d_hist;
   M->generic = true;
   M->max_pass = MAXT;
   M->exec_mode = 1;
@@ -3748,6 +3753,9 @@ extern "C" int mllm_model_destroy(mllm_model *M) {
   if (!M) return 0;
   if (M->stream) hipStreamSynchronize(M->stream);
   if (M->chain_graph) hipGraphExecDestroy(M->chain_graph);
+  for (hipGraphExec_t &ge : M->g_graph)
+    if (ge) hipGraphExecDestroy(ge);
+  if (M->h_gcur) hipHostFree(M->h_gcur);
   for (void *p : M->allocs) hipFree(p);
   if (M->h_st) hipHostFree(M->h_st);
   for (hipEvent_t e : M->prof_ev) (void)hipEventDestroy(e);
@@ -3825,6 +3833,11 @@ extern "C" int mllm_set_debug(mllm_model *M, int max_layers, int no_attn, int no
       M->g_layers[li].dbg = d;
       on |= d != 0;
     }
+    for (hipGraphExec_t &ge : M->g_graph)  // their launch sequence changed
+      if (ge) {
+        (void)hipGraphExecDestroy(ge);
+        ge = nullptr;
+      }
     M->dbg_max_layers = max_layers;
     M->dbg_no_attn = no_attn != 0;
     M->dbg_no_mlp = no_mlp != 0;
@@ -3882,13 +3895,55 @@ static int fetch_outputs(mllm_model *M, int row, int nrows, float *logits, int32
   return 0;
 }
 
-// The kind-generic step over ids[0..n) at positions pos0..: logits and
-// argmax of every row (rows: verify) or of the last token only.
+// The kind-generic step: a call writes the cursor it starts from, then
+// enqueues one step per token -- replayed from a captured graph (exec mode
+// 1) or launched directly (mode 2).
+static int g_begin(mllm_model *M, const int32_t *ids, int n, int pos0, int chain, int rows, int first, int n_hist,
+                   int eos) {
+  GCursor &c = *M->h_gcur;
+  memset(&c, 0, sizeof c);
+  c.pos_next = pos0;
+  c.chain = chain;
+  c.rows = rows;
+  c.tok = first;
+  c.n_hist = n_hist;
+  c.eos = eos;
+  c.gpt2_rule = M->cfg.arch == 1;
+  MLLM_HIP(hipMemcpyAsync(M->g.cur, &c, sizeof c, hipMemcpyHostToDevice, M->stream));
+  if (ids) MLLM_HIP(hipMemcpyAsync(M->d_ids, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, M->stream));
+  return 0;
+}
+
+static int g_enqueue(mllm_model *M, bool lm) {
+  if (M->exec_mode == 2) return g_step(M->g, lm, M->stream);
+  hipGraphExec_t &ge = M->g_graph[lm ? 1 : 0];
+  if (!ge) {
+    MLLM_HIP(hipStreamBeginCapture(M->stream, hipStreamCaptureModeThreadLocal));
+    const int rc = g_step(M->g, lm, M->stream);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(M->stream, &g);
+    if (rc || e != hipSuccess) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc ? rc : hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
+    }
+    const hipError_t ei = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ei != hipSuccess) {
+      ge = nullptr;
+      return hip_fail(ei, "hipGraphInstantiate", __FILE__, __LINE__);
+    }
+  }
+  MLLM_HIP(hipGraphLaunch(ge, M->stream));
+  return 0;
+}
+
+// ids[0..n) at positions pos0..: logits and argmax of every row (rows:
+// verify) or of the last token only.
 static int g_run(mllm_model *M, const int32_t *ids, int n, int pos0, bool rows, float *logits, int32_t *argmax) {
-  MLLM_HIP(hipMemcpyAsync(M->d_ids, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, M->stream));
+  if (int rc = g_begin(M, ids, n, pos0, 0, rows ? 1 : 0, 0, 0, -1)) return rc;
   MLLM_HIP(hipEventRecord(M->ev0, M->stream));
   for (int t = 0; t < n; ++t)
-    if (int rc = g_step(M->g, M->d_ids + t, pos0 + t, rows ? t : (t == n - 1 ? 0 : -1), nullptr, M->stream)) return rc;
+    if (int rc = g_enqueue(M, rows || t == n - 1)) return rc;
   MLLM_HIP(hipEventRecord(M->ev1, M->stream));
   MLLM_HIP(hipStreamSynchronize(M->stream));
   MLLM_HIP(hipEventElapsedTime(&M->last_ms, M->ev0, M->ev1));
@@ -3974,25 +4029,21 @@ extern "C" int mllm_decode_chain(mllm_model *M, int32_t first, int n_steps, int3
   if (n_hist) MLLM_HIP(hipMemcpyAsync(M->d_hist, hist, sizeof(int32_t) * n_hist, hipMemcpyHostToDevice, M->stream));
   if (M->generic) {
     // each step's argmax lands at d_hist[n_hist + i] and is step i + 1's
-    // input; a step after an EOS returns at once
-    MLLM_HIP(hipMemcpyAsync(M->d_ids, &first, sizeof(int32_t), hipMemcpyHostToDevice, M->stream));
-    MLLM_HIP(hipMemsetAsync(M->g.state, 0, sizeof(int) * 2, M->stream));
+    // input; the steps after an EOS return at once
+    if (int rc = g_begin(M, nullptr, 0, M->cache_len, 1, 0, first, n_hist, eos_id)) return rc;
     MLLM_HIP(hipEventRecord(M->ev0, M->stream));
-    for (int i = 0; i < n_steps; ++i) {
-      const GChain ch{M->d_hist, n_hist, i, eos_id, M->cfg.arch == 1 ? 1 : 0};
-      const int *tok = i == 0 ? M->d_ids : M->d_hist + n_hist + i - 1;
-      if (int rc = g_step(M->g, tok, M->cache_len + i, 0, &ch, M->stream)) return rc;
-    }
+    for (int i = 0; i < n_steps; ++i)
+      if (int rc = g_enqueue(M, true)) return rc;
     MLLM_HIP(hipEventRecord(M->ev1, M->stream));
     MLLM_HIP(hipStreamSynchronize(M->stream));
     MLLM_HIP(hipEventElapsedTime(&M->last_ms, M->ev0, M->ev1));
-    int st[2] = {0, 0};
-    MLLM_HIP(hipMemcpy(st, M->g.state, sizeof st, hipMemcpyDeviceToHost));
-    MLLM_CHECK(st[1] >= 1 && st[1] <= n_steps, "chain emitted %d ids of %d steps", st[1], n_steps);
-    MLLM_HIP(hipMemcpy(out_ids, M->d_hist + n_hist, sizeof(int32_t) * st[1], hipMemcpyDeviceToHost));
-    *n_out = st[1];
-    M->last_tokens = st[1];
-    M->cache_len += st[1];
+    GCursor c;
+    MLLM_HIP(hipMemcpy(&c, M->g.cur, sizeof c, hipMemcpyDeviceToHost));
+    MLLM_CHECK(c.emitted >= 1 && c.emitted <= n_steps, "chain emitted %d ids of %d steps", c.emitted, n_steps);
+    MLLM_HIP(hipMemcpy(out_ids, M->d_hist + n_hist, sizeof(int32_t) * c.emitted, hipMemcpyDeviceToHost));
+    *n_out = c.emitted;
+    M->last_tokens = c.emitted;
+    M->cache_len += c.emitted;
     return 0;
   }
   PassState &s = *M->h_st;

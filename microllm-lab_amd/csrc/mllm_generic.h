@@ -29,6 +29,21 @@ struct GLayer {
   int dbg;  // debug knobs: bit 0 drops the attention block, bit 1 the MLP block
 };
 
+// Where a call stands, in device memory.  The host writes it before a call
+// (pos_next = the first position, i_next = 0, the call's kind); each step's
+// first kernel takes position and token index from it and advances them, so
+// every step of a call launches the same kernels with the same arguments
+// (and can be replayed from a graph).
+struct GCursor {
+  int pos_next, i_next;  // the next step's position and token index
+  int pos, i;            // this step's
+  int tok;               // chained calls: the next input token (the host sets the first)
+  int chain;             // 1: chained decode (the input token is the previous argmax)
+  int rows;              // 1: logits row i per step (verify); 0: row 0
+  int n_hist, eos, gpt2_rule;  // chained calls: history length, EOS id, argmaxGpt2 (gpt2)
+  int done, emitted;     // chained calls: an EOS was emitted; ids emitted so far
+};
+
 struct GArgs {
   int arch, L, D, NH, NKV, FF, V, max_seq, kv_fp16;
   int rope_dim;          // rotated components per head (llama; infer.js:185-206)
@@ -40,21 +55,17 @@ struct GArgs {
   float *x, *qkv, *att, *h;  // one token's rows: [D], [D + 2 NKV 64], [D], [FF]
   float *logits;             // [rows][V]
   int *res;                  // argmax per logits row
-  int *state;                // chained steps: [0] stop flag (EOS emitted), [1] ids emitted
+  GCursor *cur;
+  const int *ids;            // a call's token ids (cursor index i)
+  int *hist;                 // chained calls: the history, then the ids emitted
 };
 
-// A chained step's argmax: appended at hist[n_hist + step]; gpt2_rule
-// applies argmaxGpt2 (infer.js:252-287) over hist[0 .. n_hist + step).
-struct GChain {
-  int *hist;
-  int n_hist, step, eos, gpt2_rule;
-};
-
-// One token (its id read on the device at tok) at position pos through
-// every layer; with row >= 0, the final norm, the lm_head into logits row
-// `row` and its argmax into res[row] (and, with chain, the chain's
-// bookkeeping).  With chain, every kernel returns at once once state[0] is set.
-int g_step(const GArgs &A, const int *tok, int pos, int row, const GChain *chain, hipStream_t s);
+// Enqueue one token's step: embedding of the cursor's token at its
+// position, every layer, and with lm the final norm, the lm_head (logits
+// row: the cursor's i with rows set, else 0) and the argmax (res[row]; in
+// chained calls the chain's bookkeeping).  In chained calls every kernel
+// returns at once once an EOS has been emitted.
+int g_step(const GArgs &A, bool lm, hipStream_t s);
 
 // y[rows] = W . x[cols] (model.gemv for any storage).
 int g_gemv(const GMat &W, const float *x, float *y, hipStream_t s);

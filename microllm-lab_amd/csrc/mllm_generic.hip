@@ -13,14 +13,18 @@
 //                storage kind dotted with the staged row, the wave's sum,
 //                and an epilogue: store (+ bias), residual add (+ bias),
 //                SwiGLU over the w1 / w3 rows, or bias + GELU-tanh
-//   k_g_rope_kv  rotate-half RoPE of q and k (infer.js:208-225), k / v to
-//                the KV cache (the engine's layout)
-//   k_g_attn     one workgroup per query head: scores over the cache, the
-//                softmax of infer.js:227-238, P.V (infer.js:466-495)
+//   k_g_attn     one workgroup per query head: rotate-half RoPE of its q
+//                and of its KV group's new k (infer.js:208-225) in LDS, the
+//                group's first head writes k / v to the KV cache (the
+//                engine's layout); scores over the cache, the softmax of
+//                infer.js:227-238, P.V (infer.js:466-495)
 //   k_g_argmax   first maximum (infer.js:240-250), or argmaxGpt2
 //                (infer.js:252-287) in gpt2 chains
 // These matrices are read once per token, as by the Q4 engine, at the
-// bytes their storage takes (f32 4, f16 / bf16 2, Q8 1 per weight).
+// bytes their storage takes (f32 4, f16 / bf16 2, Q8 1 per weight).  A
+// step's position and token come from a device cursor (GCursor) that the
+// step's first kernel advances, so the host replays one captured graph per
+// token.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -40,9 +44,9 @@ constexpr int GAT = 1024;  // threads of the argmax workgroup
 enum { G_STORE = 0, G_RESID = 1, G_SWIGLU = 2, G_GELU = 3 };
 enum { GN_NONE = 0, GN_RMS = 1, GN_LN = 2 };
 
-// Chained steps stop once the flag is set (an EOS was emitted).
-__device__ __forceinline__ bool stopped(const int *state) {
-  return state && *reinterpret_cast<const volatile int *>(state) != 0;
+// Chained calls stop once an EOS was emitted.
+__device__ __forceinline__ bool stopped(const GCursor *c) {
+  return c && *reinterpret_cast<const volatile int *>(&c->done) != 0;
 }
 
 __device__ __forceinline__ float f16_bits(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)h)); }
@@ -115,15 +119,17 @@ struct GemvArgs {
   const float *bias;   // per output row, or null
   float *y;            // output row [W.rows]; G_RESID adds to it
   int rpw;             // rows per wave
-  const int *state;
+  const GCursor *cur;
+  int lm;              // 1: y is the logits, row cur->i when cur->rows (verify)
 };
 
 // Dynamic LDS: W.cols + 4 floats.
 template <int EPI, int NORM>
 __global__ __launch_bounds__(GT) void k_g_gemv(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) float xs[];
-  if (stopped(a.state)) return;
+  if (stopped(a.cur)) return;
   const int K = a.W.cols;
+  float *y = a.y + (a.lm && a.cur->rows ? (size_t)a.cur->i * a.W.rows : 0);
   float *red = xs + K;
   if (NORM == GN_NONE) {
     for (int i = tid(); i < K; i += GT) xs[i] = a.x[i];
@@ -167,14 +173,14 @@ __global__ __launch_bounds__(GT) void k_g_gemv(GemvArgs a) {
     if (a.W.kind == MLLM_Q8) acc *= a.W.s[r];
     if (EPI == G_SWIGLU && a.W3.kind == MLLM_Q8) acc3 *= a.W3.s[r];
     if (EPI == G_STORE) {
-      a.y[r] = a.bias ? acc + a.bias[r] : acc;
+      y[r] = a.bias ? acc + a.bias[r] : acc;
     } else if (EPI == G_RESID) {
-      a.y[r] = a.y[r] + (a.bias ? acc + a.bias[r] : acc);
+      y[r] = y[r] + (a.bias ? acc + a.bias[r] : acc);
     } else if (EPI == G_SWIGLU) {
-      a.y[r] = (acc / (1.0f + expf(-acc))) * acc3;  // infer.js:175-181
+      y[r] = (acc / (1.0f + expf(-acc))) * acc3;  // infer.js:175-181
     } else {
       const float v = a.bias ? acc + a.bias[r] : acc;  // infer.js:166-172
-      a.y[r] = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+      y[r] = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
     }
   }
 }
@@ -183,10 +189,21 @@ __device__ __forceinline__ size_t g_kv_index(const GArgs &A, int li, int which, 
   return ((((size_t)li * 2 + which) * A.NKV + h) * A.max_seq + pos) * GHD;
 }
 
-// The token's embedding row (tok read on the device).
-__global__ __launch_bounds__(GT) void k_g_embed(GArgs A, const int *tok, int pos) {
-  if (stopped(A.state)) return;
-  const int D = A.D, id = *tok;
+// The step's start: position and token index from the cursor (advanced for
+// the next step), the input token (chained calls: the previous argmax),
+// its embedding row.
+__global__ __launch_bounds__(GT) void k_g_embed(GArgs A) {
+  GCursor *cur = A.cur;
+  if (stopped(cur)) return;
+  const int D = A.D, pos = cur->pos_next, ti = cur->i_next;
+  const int id = cur->chain ? cur->tok : A.ids[ti];
+  __syncthreads();  // every thread has read the cursor
+  if (tid() == 0) {
+    cur->pos = pos;
+    cur->i = ti;
+    cur->pos_next = pos + 1;
+    cur->i_next = ti + 1;
+  }
   const GMat &W = A.lm;
   const bool quant = W.kind == MLLM_Q8 || W.kind == MLLM_Q8G32 || W.kind == MLLM_Q4;
   for (int c = tid(); c < (D >> 3); c += GT) {
@@ -202,42 +219,6 @@ __global__ __launch_bounds__(GT) void k_g_embed(GArgs A, const int *tok, int pos
         v = v + A.wpe[(size_t)min(pos, A.max_seq - 1) * D + i];
       }
       A.x[i] = v;
-    }
-  }
-}
-
-// RoPE of the q heads (in place) and the k heads, then k and v to the cache.
-__global__ __launch_bounds__(GT) void k_g_rope_kv(GArgs A, int li, int pos) {
-  if (stopped(A.state)) return;
-  const int D = A.D, kvd = A.NKV * GHD, rope_dim = A.rope_dim, half = rope_dim >> 1;
-  float *q = A.qkv;
-  const float *k = q + D, *v = q + D + kvd;
-  const float *cs = A.rope_cos + (size_t)pos * rope_dim, *sn = A.rope_sin + (size_t)pos * rope_dim;
-  auto rot = [&](const float *hd, int d) {
-    // out[i] = x[i] cos[i] + rot[i] sin[i], rot = (-x[half..rd), x[0..half))
-    if (d >= rope_dim) return hd[d];
-    return d < half ? hd[d] * cs[d] + (-hd[d + half]) * sn[d] : hd[d] * cs[d] + hd[d - half] * sn[d];
-  };
-  if (A.arch == 0) {
-    // a thread owns both members of each rotated pair, so it may write them in place
-    for (int i = tid(); i < A.NH * half; i += GT) {
-      float *hd = q + (i / half) * GHD;
-      const int d = i % half;
-      const float lo = rot(hd, d), hi = rot(hd, d + half);
-      hd[d] = lo;
-      hd[d + half] = hi;
-    }
-  }
-  for (int i = tid(); i < kvd; i += GT) {
-    const int h = i / GHD, d = i % GHD;
-    const float kr = A.arch == 0 ? rot(k + h * GHD, d) : k[i];
-    const size_t ko = g_kv_index(A, li, 0, h, pos) + d, vo = g_kv_index(A, li, 1, h, pos) + d;
-    if (A.kv_fp16) {
-      reinterpret_cast<__half *>(A.kv)[ko] = __float2half_rn(kr);
-      reinterpret_cast<__half *>(A.kv)[vo] = __float2half_rn(v[i]);
-    } else {
-      reinterpret_cast<float *>(A.kv)[ko] = kr;
-      reinterpret_cast<float *>(A.kv)[vo] = v[i];
     }
   }
 }
@@ -265,19 +246,58 @@ __device__ __forceinline__ void kv_row(const GArgs &A, size_t off, float (&r)[GH
   }
 }
 
-// Dynamic LDS: 64 (q) + max_seq (weights) + 256 (P.V partials) + 4 floats.
-__global__ __launch_bounds__(GT) void k_g_attn(GArgs A, int li, int pos) {
+// One head's rotated component d (rotate-half on the first rope_dim
+// components: out[d] = x[d] cos[d] + rot[d] sin[d], rot = (-x[half .. rd),
+// x[0 .. half))).
+__device__ __forceinline__ float rope_at(const GArgs &A, const float *hd, int d, int pos) {
+  const int rd = A.rope_dim, half = rd >> 1;
+  if (A.arch != 0 || d >= rd) return hd[d];
+  const float c = A.rope_cos[(size_t)pos * rd + d], sn = A.rope_sin[(size_t)pos * rd + d];
+  return d < half ? hd[d] * c + (-hd[d + half]) * sn : hd[d] * c + hd[d - half] * sn;
+}
+
+// Dynamic LDS: 3 x 64 (q, the new k and v) + max_seq (weights) + 256 (P.V
+// partials) + 4 floats.  The new position's k and v are used from LDS (as
+// the cache holds them: f16-rounded for an f16 cache), so the heads of a
+// group do not wait for the one that writes them to the cache.
+__global__ __launch_bounds__(GT) void k_g_attn(GArgs A, int li) {
   extern __shared__ __attribute__((aligned(16))) float sa[];
-  if (stopped(A.state)) return;
-  const int h = blockIdx.x, kvh = h / (A.NH / A.NKV), n = pos + 1;
-  float *qs = sa, *p = sa + GHD, *part = p + ((A.max_seq + 3) & ~3), *red = part + GT;
-  if (tid() < GHD) qs[tid()] = A.qkv[h * GHD + tid()];
-  __syncthreads();
+  if (stopped(A.cur)) return;
+  const int pos = A.cur->pos, rep = A.NH / A.NKV;
+  const int h = blockIdx.x, kvh = h / rep, n = pos + 1;
+  float *qs = sa, *kn = sa + GHD, *vn = kn + GHD, *p = vn + GHD;
+  float *part = p + ((A.max_seq + 3) & ~3), *red = part + GT;
   const size_t kb = g_kv_index(A, li, 0, kvh, 0), vb = g_kv_index(A, li, 1, kvh, 0);
+  if (tid() < GHD) {
+    const int d = tid();
+    const float *k = A.qkv + A.D + kvh * GHD, *v = A.qkv + A.D + A.NKV * GHD + kvh * GHD;
+    qs[d] = rope_at(A, A.qkv + h * GHD, d, pos);
+    float kr = rope_at(A, k, d, pos), vr = v[d];
+    if (A.kv_fp16) {
+      const __half kh = __float2half_rn(kr), vh = __float2half_rn(vr);
+      kr = __half2float(kh);
+      vr = __half2float(vh);
+      if (h % rep == 0) {
+        reinterpret_cast<__half *>(A.kv)[kb + (size_t)pos * GHD + d] = kh;
+        reinterpret_cast<__half *>(A.kv)[vb + (size_t)pos * GHD + d] = vh;
+      }
+    } else if (h % rep == 0) {
+      reinterpret_cast<float *>(A.kv)[kb + (size_t)pos * GHD + d] = kr;
+      reinterpret_cast<float *>(A.kv)[vb + (size_t)pos * GHD + d] = vr;
+    }
+    kn[d] = kr;
+    vn[d] = vr;
+  }
+  __syncthreads();
   float mx = -INFINITY;
   for (int j = tid(); j < n; j += GT) {
     float kr[GHD];
-    kv_row(A, kb + (size_t)j * GHD, kr);
+    if (j == pos) {
+#pragma unroll
+      for (int e = 0; e < GHD; ++e) kr[e] = kn[e];
+    } else {
+      kv_row(A, kb + (size_t)j * GHD, kr);
+    }
     float d = 0.f;
 #pragma unroll
     for (int e = 0; e < GHD; ++e) d = __builtin_fmaf(qs[e], kr[e], d);
@@ -298,8 +318,9 @@ __global__ __launch_bounds__(GT) void k_g_attn(GArgs A, int li, int pos) {
   float o = 0.f;
   for (int j = sl; j < n; j += GT / GHD) {
     const size_t off = vb + (size_t)j * GHD + d;
-    const float vv = A.kv_fp16 ? __half2float(reinterpret_cast<const __half *>(A.kv)[off])
-                               : reinterpret_cast<const float *>(A.kv)[off];
+    const float vv = j == pos ? vn[d]
+                              : (A.kv_fp16 ? __half2float(reinterpret_cast<const __half *>(A.kv)[off])
+                                           : reinterpret_cast<const float *>(A.kv)[off]);
     o = __builtin_fmaf(p[j] * inv, vv, o);
   }
   part[tid()] = o;
@@ -307,30 +328,33 @@ __global__ __launch_bounds__(GT) void k_g_attn(GArgs A, int li, int pos) {
   if (tid() < GHD) A.att[h * GHD + tid()] = (part[tid()] + part[GHD + tid()]) + (part[2 * GHD + tid()] + part[3 * GHD + tid()]);
 }
 
-// First maximum of logits row `row` (infer.js:240-250: NaN never wins, and
-// a NaN in slot 0 keeps index 0); in a gpt2 chain argmaxGpt2 over the
-// history (infer.js:252-287: trigram-banned ids -1e9, ids among the last
-// 32 scaled by 1/1.15 or 1.15, then the first strict maximum from -inf).
-// Dynamic LDS: 2 + 32 + max_seq ints.
-__global__ __launch_bounds__(GAT) void k_g_argmax(GArgs A, int row, GChain ch, int chained) {
+// First maximum of the step's logits row (infer.js:240-250: NaN never
+// wins, and a NaN in slot 0 keeps index 0); in a gpt2 chain argmaxGpt2
+// over the history (infer.js:252-287: trigram-banned ids -1e9, ids among
+// the last 32 scaled by 1/1.15 or 1.15, then the first strict maximum from
+// -inf).  Dynamic LDS: 2 + 32 + max_seq ints.
+__global__ __launch_bounds__(GAT) void k_g_argmax(GArgs A) {
   extern __shared__ int lists[];
-  if (chained && stopped(A.state)) return;
+  GCursor *cur = A.cur;
+  if (stopped(cur)) return;
+  const int row = cur->rows ? cur->i : 0, chained = cur->chain;
   const float *lg = A.logits + (size_t)row * A.V;
-  const bool rule = chained && ch.gpt2_rule;
+  const bool rule = chained && cur->gpt2_rule;
   int *nb = lists, *nr = lists + 1, *rec = lists + 2, *ban = lists + 34;
-  const int nh = chained ? ch.n_hist + ch.step : 0;
+  const int nh = chained ? cur->n_hist + cur->emitted : 0;
+  const int *hist = A.hist;
   if (rule) {
     if (tid() == 0) {
       *nb = 0;
       int k = 0;
-      for (int h = max(0, nh - 32); h < nh; ++h) rec[k++] = ch.hist[h];
+      for (int h = max(0, nh - 32); h < nh; ++h) rec[k++] = hist[h];
       *nr = k;
     }
     __syncthreads();
     if (nh >= 2) {
-      const int t1 = ch.hist[nh - 2], t2 = ch.hist[nh - 1];
+      const int t1 = hist[nh - 2], t2 = hist[nh - 1];
       for (int h = tid(); h < nh - 2; h += GAT)
-        if (ch.hist[h] == t1 && ch.hist[h + 1] == t2) ban[atomicAdd(nb, 1)] = ch.hist[h + 2];
+        if (hist[h] == t1 && hist[h + 1] == t2) ban[atomicAdd(nb, 1)] = hist[h + 2];
     }
     __syncthreads();
   }
@@ -376,9 +400,10 @@ __global__ __launch_bounds__(GAT) void k_g_argmax(GArgs A, int row, GChain ch, i
   if (!rule && isnan(lg[0])) best = 0;   // infer.js:241-243 starts from logits[0]
   A.res[row] = best;
   if (chained) {
-    ch.hist[nh] = best;
-    A.state[1] = ch.step + 1;
-    if (best == ch.eos) A.state[0] = 1;
+    A.hist[nh] = best;
+    cur->tok = best;
+    cur->emitted = cur->emitted + 1;
+    if (best == cur->eos) cur->done = 1;
   }
 }
 
@@ -397,7 +422,7 @@ int launch_gemv(const GemvArgs &a, hipStream_t s) {
 }
 
 GemvArgs gemv_args(const GMat &W, const float *x, const float *gains, float eps, const float *bias, float *y,
-                   const int *state) {
+                   const GCursor *cur) {
   GemvArgs a{};
   a.W = W;
   a.x = x;
@@ -405,7 +430,7 @@ GemvArgs gemv_args(const GMat &W, const float *x, const float *gains, float eps,
   a.eps = eps;
   a.bias = bias;
   a.y = y;
-  a.state = state;
+  a.cur = cur;
   return a;
 }
 
@@ -432,46 +457,41 @@ int g_gemv(const GMat &W, const float *x, float *y, hipStream_t s) {
   return 0;
 }
 
-int g_step(const GArgs &A, const int *tok, int pos, int row, const GChain *chain, hipStream_t s) {
+int g_step(const GArgs &A, bool lm, hipStream_t s) {
   const bool gpt2 = A.arch == 1;
-  const int *st = chain ? A.state : nullptr;
-  GArgs K = A;
-  K.state = const_cast<int *>(st);
-  hipLaunchKernelGGL(k_g_embed, dim3(1), dim3(GT), 0, s, K, tok, pos);
-  const size_t att_lds = sizeof(float) * (GHD + ((A.max_seq + 3) & ~3) + GT + 4);
+  const GCursor *cur = A.cur;
+  hipLaunchKernelGGL(k_g_embed, dim3(1), dim3(GT), 0, s, A);
+  const size_t att_lds = sizeof(float) * (3 * GHD + ((A.max_seq + 3) & ~3) + GT + 4);
   for (int li = 0; li < A.L; ++li) {
     const GLayer &w = A.layers[li];
     if (!(w.dbg & 1)) {
-      GemvArgs q = gemv_args(w.qkv, A.x, w.n1, A.eps, w.qkv_b, A.qkv, st);
+      GemvArgs q = gemv_args(w.qkv, A.x, w.n1, A.eps, w.qkv_b, A.qkv, cur);
       if (gpt2)
         launch_gemv<G_STORE, GN_LN>(q, s);
       else
         launch_gemv<G_STORE, GN_RMS>(q, s);
-      hipLaunchKernelGGL(k_g_rope_kv, dim3(1), dim3(GT), 0, s, K, li, pos);
-      hipLaunchKernelGGL(k_g_attn, dim3(A.NH), dim3(GT), att_lds, s, K, li, pos);
-      launch_gemv<G_RESID, GN_NONE>(gemv_args(w.proj, A.att, nullptr, 0.f, w.proj_b, A.x, st), s);
+      hipLaunchKernelGGL(k_g_attn, dim3(A.NH), dim3(GT), att_lds, s, A, li);
+      launch_gemv<G_RESID, GN_NONE>(gemv_args(w.proj, A.att, nullptr, 0.f, w.proj_b, A.x, cur), s);
     }
     if (!(w.dbg & 2)) {
       if (gpt2) {
-        launch_gemv<G_GELU, GN_LN>(gemv_args(w.w1, A.x, w.n2, A.eps, w.fc_b, A.h, st), s);
+        launch_gemv<G_GELU, GN_LN>(gemv_args(w.w1, A.x, w.n2, A.eps, w.fc_b, A.h, cur), s);
       } else {
-        GemvArgs u = gemv_args(w.w1, A.x, w.n2, A.eps, nullptr, A.h, st);
+        GemvArgs u = gemv_args(w.w1, A.x, w.n2, A.eps, nullptr, A.h, cur);
         u.W3 = w.w3;
         launch_gemv<G_SWIGLU, GN_RMS>(u, s);
       }
-      launch_gemv<G_RESID, GN_NONE>(gemv_args(w.w2, A.h, nullptr, 0.f, w.mproj_b, A.x, st), s);
+      launch_gemv<G_RESID, GN_NONE>(gemv_args(w.w2, A.h, nullptr, 0.f, w.mproj_b, A.x, cur), s);
     }
   }
-  if (row >= 0) {
-    GemvArgs f = gemv_args(A.lm, A.x, A.norm_f, A.eps, nullptr, A.logits + (size_t)row * A.V, st);
+  if (lm) {
+    GemvArgs f = gemv_args(A.lm, A.x, A.norm_f, A.eps, nullptr, A.logits, cur);
+    f.lm = 1;
     if (gpt2)
       launch_gemv<G_STORE, GN_LN>(f, s);
     else
       launch_gemv<G_STORE, GN_RMS>(f, s);
-    GChain c{};
-    if (chain) c = *chain;
-    hipLaunchKernelGGL(k_g_argmax, dim3(1), dim3(GAT), sizeof(int) * (34 + (size_t)A.max_seq), s, K, row, c,
-                       chain ? 1 : 0);
+    hipLaunchKernelGGL(k_g_argmax, dim3(1), dim3(GAT), sizeof(int) * (34 + (size_t)A.max_seq), s, A);
   }
   MLLM_HIP(hipGetLastError());
   return 0;
