@@ -1698,6 +1698,7 @@ struct FlowGeom {
   int na, nm, ni;         // items per layer: attention (split, head) items, MLP chunks; ni = na + nm
   int lm_rpt, lm_tiles;   // lm_head tiles of the 1024-thread role (one per workgroup w < lm_tiles, then w + G ...)
   int kvp;                // k_flow: LDS float offset of the deferred K/V-row slots (kv_flush)
+  int xcd;                // k_flow3: the attention items of a (split, KV head) group share an XCD
 };
 
 constexpr int FLT = 1024;               // threads per workgroup of the persistent kernel
@@ -2712,6 +2713,22 @@ __global__ __launch_bounds__(FLT) void k_flowm(DecParams P, FlowGeom F) {
   }
 }
 
+// The attention item that stage slot a (workgroup ia + a, or ia + a - G
+// ...) runs in k_flow3.  Workgroups go to the eight XCDs round-robin, each
+// with its own L2; with F.xcd the rep items of a (split, KV head) group --
+// the query heads that read the same K/V split -- sit on workgroups of one
+// XCD, so the group's split is read from HBM once and from that L2 by the
+// others.  Slot a is the k-th of its XCD's slots; XCD x runs groups
+// x, x + 8, ... (g = split * NKV + kvh), rep items each.  (F.xcd is set
+// when the stage's items and groups divide evenly over the eight XCDs.)
+__device__ __forceinline__ int flow3_attn_item(const DecParams &P, const FlowGeom &F, int a, int ia) {
+  if (!F.xcd) return a;
+  const int x = (ia + a) & 7, first = (x - ia) & 7, k = (a - first) >> 3;
+  const int rep = P.NH / P.NKV, kg = k / rep, r = k - kg * rep;
+  const int g = x + 8 * kg, sp = g / P.NKV, kvh = g - sp * P.NKV;
+  return sp * P.NH + kvh * rep + r;
+}
+
 // The chained decode step in three stages per layer (the verify step's fused
 // items at one row): QKV items (half a row head: 32 rows of attn.qkv, the
 // dimensions 16 hf .. 16 hf + 15 and their RoPE partners, each item forming
@@ -2778,7 +2795,7 @@ __global__ __launch_bounds__(FLT) void k_flow3(DecParams P, FlowGeom F) {
           wait_stores();
           flowm_qkv(P, Lw, li, j >> 1, 0, 1, st, true, smem, tok, j & 1);
         } else if (j < im) {
-          flowm_attn<MS>(P, Lw, li, j - ia, 0, 1, st, 1, smem);
+          flowm_attn<MS>(P, Lw, li, flow3_attn_item(P, F, j - ia, ia), 0, 1, st, 1, smem);
         } else {
           const int it = j - im;
           flowm_mlp(P, Lw, li, it, st, 0, 1, true, smem);
@@ -3696,6 +3713,10 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       M->flow_grid = G;
       M->exec_mode = 3;
       M->flow_default = true;
+      // the attention items of a (split, KV head) group on one XCD when the
+      // stage's items and groups divide over the eight (MLLM_ATTN_XCD=0: off)
+      const char *ax = getenv("MLLM_ATTN_XCD");
+      F.xcd = (!ax || atoi(ax) != 0) && G % 8 == 0 && F.na % 8 == 0 && (F.na / (NH / NKV)) % 8 == 0;
       // the three-stage chained kernel, when it is resident on the same grid
       const void *k3 = reinterpret_cast<const void *>(k_flow3<true>);
       const void *k3s = reinterpret_cast<const void *>(k_flow3<false>);

@@ -50,13 +50,14 @@ def test_js_parse_pgw_and_sampling(tmp_path, oracle_lib):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("arch,mode,prefill_min,debug", [("llama", "greedy", None, None), ("llama", "chain", None, None),
-                                                         ("llama", "spec", None, None), ("gpt2", "chain", None, None),
-                                                         ("llama", "greedy", 0, None),
-                                                         ("llama", "chain", None, {"maxLayers": 1, "noAttn": True}),
-                                                         ("gpt2", "greedy", None, {"mlpTo": 1})])
-def test_js_engine_matches_python_engine(tmp_path, arch, mode, prefill_min, debug):
-    bundle_bytes = pgw.make_model(pgw.small_config(arch), seed=5)
+@pytest.mark.parametrize("arch,mode,prefill_min,debug,kind", [
+    ("llama", "greedy", None, None, "q4"), ("llama", "chain", None, None, "q4"), ("llama", "spec", None, None, "q4"),
+    ("gpt2", "chain", None, None, "q4"), ("llama", "greedy", 0, None, "q4"),
+    ("llama", "chain", None, {"maxLayers": 1, "noAttn": True}, "q4"), ("gpt2", "greedy", None, {"mlpTo": 1}, "q4"),
+    # the kind-generic step through the N-API addon
+    ("llama", "spec", None, None, "q8"), ("gpt2", "chain", None, None, "bf16")])
+def test_js_engine_matches_python_engine(tmp_path, arch, mode, prefill_min, debug, kind):
+    bundle_bytes = pgw.make_model(pgw.small_config(arch), seed=5, kind=kind)
     (tmp_path / "m.pgw").write_bytes(bundle_bytes)
     prompt = [3, 9, 27, 81, 3, 9, 27, 81, 3, 9]
     spec = {"prompt": prompt, "maxNewTokens": 16, "mode": mode, "specK": 4, "decodeLogits": [5, 6]}
