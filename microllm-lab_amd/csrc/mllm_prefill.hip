@@ -619,22 +619,28 @@ __device__ __forceinline__ void widen8(const Raw8 &r, float (&v)[8]) {
     }
   }
 }
-constexpr int SCH = 4;   // staged 8-value chunks per thread and super-block (64 keys x 8 chunks, >= 128 threads)
-constexpr int KSB = 64;  // keys per super-block: two 32-key blocks, one per wave set
-constexpr int VROW2 = 68;  // halves per staged value column (64 keys + pad)
+constexpr int SCH = 4;   // staged 8-value chunks per thread and super-block (32 NSET keys x 8 chunks, >= 64 NSET threads)
 
-// The tile's key blocks alternate between two sets of waves (block 2i to set
-// 0, 2i + 1 to set 1; a wave per query head in each set), so two waves share
-// each SIMD; set 1's running (max, sum, output) is merged into set 0's at the
-// end through LDS.
-template <bool SPLIT_KV>
-__global__ __launch_bounds__(512) void k_pf_attn(PfArgs A, int li, int n, int pos0, int tt0) {
-  constexpr int KB_BYTES = KSB * KROW * 2, VB_BYTES = PF_HD * VROW2 * 2;
+// The tile's key blocks are dealt round-robin to NSET sets of waves (block
+// NSET i + s to set s; a wave per query head in each set), each set keeping
+// its own running (max, sum, output); at the end sets 1 .. NSET-1 hand theirs
+// to set 0 through LDS, which merges them in set order.  A super-block is the
+// NSET blocks the sets take at once.  NSET = 2 puts 2 rep waves on the 4
+// SIMDs (two SIMDs run two of a KV head's three query-head waves and the
+// others one); NSET = 4 with rep 3 puts three waves on every SIMD and takes
+// twice the keys per staging round.  (NSET = 4 needs rep <= 3 and the f16
+// cache: 4 rep waves of an f32 cache's registers would not fit.)
+template <bool SPLIT_KV, int NSET>
+__global__ __launch_bounds__(NSET == 4 ? 768 : 512) void k_pf_attn(PfArgs A, int li, int n, int pos0, int tt0) {
+  constexpr int KSB = 32 * NSET;    // keys per super-block
+  constexpr int VROW = KSB + 4;     // halves per staged value column (KSB keys + pad)
+  constexpr int MAXREP = NSET == 4 ? 3 : 4;
+  constexpr int KB_BYTES = KSB * KROW * 2, VB_BYTES = PF_HD * VROW * 2;
   constexpr int STAGE = (SPLIT_KV ? 2 : 1) * (KB_BYTES + VB_BYTES);
-  constexpr int MERGE = 4 * 64 * 34 * 4;  // up to 4 heads x 64 lanes x (32 outputs, max, sum)
+  constexpr int MERGE = (NSET - 1) * MAXREP * 64 * 34 * 4;  // sets 1.. x heads x 64 lanes x (32 outputs, max, sum)
   __shared__ __attribute__((aligned(16))) uint8_t smem[STAGE > MERGE ? STAGE : MERGE];
   _Float16 *Kh = reinterpret_cast<_Float16 *>(smem), *Vh = Kh + KSB * KROW;
-  _Float16 *Kl = Vh + PF_HD * VROW2, *Vl = Kl + KSB * KROW;  // SPLIT_KV only
+  _Float16 *Kl = Vh + PF_HD * VROW, *Vl = Kl + KSB * KROW;  // SPLIT_KV only
   const int rep = A.NH / A.NKV;
   const int T0 = (tt0 + gridDim.x - 1 - blockIdx.x) * QTL, kvh = blockIdx.y;  // the longest tiles first
   const int lane = tid() & 63, j = lane & 31, hh = lane >> 5;
@@ -692,16 +698,16 @@ __global__ __launch_bounds__(512) void k_pf_attn(PfArgs A, int li, int n, int po
         for (int i = 0; i < 8; ++i) {
           const _Float16 kh = (_Float16)kv[i], vh = (_Float16)vv[i];
           Kh[kk * KROW + d0 + i] = kh;
-          Vh[(d0 + i) * VROW2 + kk] = vh;
+          Vh[(d0 + i) * VROW + kk] = vh;
           Kl[kk * KROW + d0 + i] = (_Float16)(kv[i] - (float)kh);
-          Vl[(d0 + i) * VROW2 + kk] = (_Float16)(vv[i] - (float)vh);
+          Vl[(d0 + i) * VROW + kk] = (_Float16)(vv[i] - (float)vh);
         }
       } else {  // an f16 cache is staged as is
         *reinterpret_cast<uint4 *>(Kh + kk * KROW + d0) = rk[ci].a;
         const uint32_t w[4] = {rv[ci].a.x, rv[ci].a.y, rv[ci].a.z, rv[ci].a.w};
         unsigned short *vt = reinterpret_cast<unsigned short *>(Vh);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vt[(d0 + i) * VROW2 + kk] = (unsigned short)(w[i >> 1] >> (16 * (i & 1)));
+        for (int i = 0; i < 8; ++i) vt[(d0 + i) * VROW + kk] = (unsigned short)(w[i >> 1] >> (16 * (i & 1)));
       }
     }
     if (sb + 1 < nsb) fetch((sb + 1) * KSB);
@@ -759,10 +765,10 @@ __global__ __launch_bounds__(512) void k_pf_attn(PfArgs A, int li, int n, int po
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int kc = kr + 16 * u + 4 * hh;
-      const v4h a0 = *reinterpret_cast<const v4h *>(Vh + j * VROW2 + kc);
-      const v4h a1 = *reinterpret_cast<const v4h *>(Vh + j * VROW2 + kc + 8);
-      const v4h b0 = *reinterpret_cast<const v4h *>(Vh + (32 + j) * VROW2 + kc);
-      const v4h b1 = *reinterpret_cast<const v4h *>(Vh + (32 + j) * VROW2 + kc + 8);
+      const v4h a0 = *reinterpret_cast<const v4h *>(Vh + j * VROW + kc);
+      const v4h a1 = *reinterpret_cast<const v4h *>(Vh + j * VROW + kc + 8);
+      const v4h b0 = *reinterpret_cast<const v4h *>(Vh + (32 + j) * VROW + kc);
+      const v4h b1 = *reinterpret_cast<const v4h *>(Vh + (32 + j) * VROW + kc + 8);
       const v8h va = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
       const v8h vb = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
       o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph[u], o0, 0, 0, 0);
@@ -770,10 +776,10 @@ __global__ __launch_bounds__(512) void k_pf_attn(PfArgs A, int li, int n, int po
       o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb, ph[u], o1, 0, 0, 0);
       o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb, pl[u], o1, 0, 0, 0);
       if (SPLIT_KV) {
-        const v4h c0 = *reinterpret_cast<const v4h *>(Vl + j * VROW2 + kc);
-        const v4h c1 = *reinterpret_cast<const v4h *>(Vl + j * VROW2 + kc + 8);
-        const v4h d0 = *reinterpret_cast<const v4h *>(Vl + (32 + j) * VROW2 + kc);
-        const v4h d1 = *reinterpret_cast<const v4h *>(Vl + (32 + j) * VROW2 + kc + 8);
+        const v4h c0 = *reinterpret_cast<const v4h *>(Vl + j * VROW + kc);
+        const v4h c1 = *reinterpret_cast<const v4h *>(Vl + j * VROW + kc + 8);
+        const v4h d0 = *reinterpret_cast<const v4h *>(Vl + (32 + j) * VROW + kc);
+        const v4h d1 = *reinterpret_cast<const v4h *>(Vl + (32 + j) * VROW + kc + 8);
         o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_shufflevector(c0, c1, 0, 1, 2, 3, 4, 5, 6, 7), ph[u], o0,
                                                     0, 0, 0);
         o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_shufflevector(d0, d1, 0, 1, 2, 3, 4, 5, 6, 7), ph[u], o1,
@@ -781,10 +787,13 @@ __global__ __launch_bounds__(512) void k_pf_attn(PfArgs A, int li, int n, int po
       }
     }
   }
-  // merge: set 1 hands (outputs, max, sum) to set 0 through LDS
-  float *mrg = reinterpret_cast<float *>(smem) + (size_t)(hsel * 64 + lane) * 34;
+  // merge: sets 1 .. NSET-1 hand (outputs, max, sum) to set 0 through LDS
+  // (slot (s - 1, head, lane)); set 0 adds them in set order
+  float *const mrg0 = reinterpret_cast<float *>(smem) + (size_t)(hsel * 64 + lane) * 34;
+  constexpr size_t MSET = (size_t)MAXREP * 64 * 34;  // floats per set's slots
   __syncthreads();  // the staging area is free
-  if (set == 1) {
+  if (set > 0) {
+    float *mrg = mrg0 + (set - 1) * MSET;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       mrg[v] = o0[v];
@@ -795,18 +804,31 @@ __global__ __launch_bounds__(512) void k_pf_attn(PfArgs A, int li, int n, int po
   }
   __syncthreads();
   if (set == 0 && T0 + j < n) {
-    const float m1 = mrg[32], l1 = mrg[33];
-    const float M = fmaxf(m_run, m1);  // finite: set 0 holds key 0
-    const float a0 = __builtin_amdgcn_exp2f(m_run - M), a1 = __builtin_amdgcn_exp2f(m1 - M);
-    const float l = l_run * a0 + l1 * a1;
+    float M = m_run;  // finite: set 0 holds key 0
+#pragma unroll
+    for (int s = 1; s < NSET; ++s) M = fmaxf(M, mrg0[(s - 1) * MSET + 32]);
+    float a[NSET];
+    a[0] = __builtin_amdgcn_exp2f(m_run - M);
+    float l = l_run * a[0];
+#pragma unroll
+    for (int s = 1; s < NSET; ++s) {
+      a[s] = __builtin_amdgcn_exp2f(mrg0[(s - 1) * MSET + 32] - M);
+      l = l + mrg0[(s - 1) * MSET + 33] * a[s];
+    }
     float *out = A.att + (size_t)(T0 + j) * A.D + hq * PF_HD + 4 * hh;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       float r[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        r[e] = (o0[4 * g + e] * a0 + mrg[4 * g + e] * a1) / l;
-        r[4 + e] = (o1[4 * g + e] * a0 + mrg[16 + 4 * g + e] * a1) / l;
+        float r0 = o0[4 * g + e] * a[0], r1 = o1[4 * g + e] * a[0];
+#pragma unroll
+        for (int s = 1; s < NSET; ++s) {
+          r0 = r0 + mrg0[(s - 1) * MSET + 4 * g + e] * a[s];
+          r1 = r1 + mrg0[(s - 1) * MSET + 16 + 4 * g + e] * a[s];
+        }
+        r[e] = r0 / l;
+        r[4 + e] = r1 / l;
       }
       *reinterpret_cast<float4 *>(out + 8 * g) = make_float4(r[0], r[1], r[2], r[3]);
       *reinterpret_cast<float4 *>(out + 32 + 8 * g) = make_float4(r[4], r[5], r[6], r[7]);
@@ -968,10 +990,12 @@ int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, bool last, h
     const bool final_layer = li == A.L - 1;
     if (final_layer && !last) break;
     const int tt0 = final_layer ? nqt - 1 : 0, t0 = tt0 * QTL;
-    if (A.kv_fp16)
-      hipLaunchKernelGGL(k_pf_attn<false>, dim3(nqt - tt0, A.NKV), dim3(128 * rep), 0, s, A, li, n, pos0, tt0);
+    if (A.kv_fp16 && rep <= 3)
+      hipLaunchKernelGGL((k_pf_attn<false, 4>), dim3(nqt - tt0, A.NKV), dim3(256 * rep), 0, s, A, li, n, pos0, tt0);
+    else if (A.kv_fp16)
+      hipLaunchKernelGGL((k_pf_attn<false, 2>), dim3(nqt - tt0, A.NKV), dim3(128 * rep), 0, s, A, li, n, pos0, tt0);
     else
-      hipLaunchKernelGGL(k_pf_attn<true>, dim3(nqt - tt0, A.NKV), dim3(128 * rep), 0, s, A, li, n, pos0, tt0);
+      hipLaunchKernelGGL((k_pf_attn<true, 2>), dim3(nqt - tt0, A.NKV), dim3(128 * rep), 0, s, A, li, n, pos0, tt0);
     launch_quant<NORM_NONE>(A, A.att, A.D, nullptr, t0, n, s);
     PfGemm O = gemm_same(W.proj, n, gpt2 ? W.proj_b : nullptr, A.x, A.D);
     O.tt0 = tt0;
