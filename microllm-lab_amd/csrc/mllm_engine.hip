@@ -183,7 +183,9 @@ constexpr int TAGL = 128;  // tags per step (layers < TAGL)
 //           the store wait and barrier, 3 split merges done
 //   MLP     1 inputs gathered, 2 norm records done, 3 gate/up dots, 4 activation records
 //   QKV, MLP (thread 0's wave, in the norm) 5 norm scale known, 6 records staged
-//   LM      1 last layer's flags seen, 2 final-norm records in, 3 tiles done
+//   LM      1 last layer's flags seen, 2 final-norm records in, 3 tiles done;
+//           workgroup 0 (the final norm) also 4 partials gathered, 7 residual
+//           summed, 5 norm scale known, 6 records staged
 // The default build compiles none of this.
 #ifdef MLLM_STAGE_PROBE
 constexpr int PNI = 256, PSLOTS = 34, PK = 8, PROBE_TOP = 32, PROBE_LM = 33;
@@ -1368,7 +1370,9 @@ __device__ __forceinline__ void final_row(const DecParams &P, int t, float *blk,
   const float4 base = col_base_load<(POLL != 0)>(P, P.xb + (size_t)t * D, nq, want);
   resid_blocks<POLL, POLL == 2>(P, P.dpart + (size_t)t * P.nchunk * D, P.nchunk, want, blk);
   __syncthreads();
+  PROBE(4);
   const float4 x = col_finish(blk, nq, P.nchunk, base, gl, D, P.arch == 1 && P.last_mproj_b != nullptr);
+  PROBE(7);
   col_norm(P, x, gl, blk + ((P.nchunk + PB - 1) / PB) * D, qx, ColOut{nullptr, 0, to_global ? P.xn + (size_t)t * D : nullptr});
 }
 
