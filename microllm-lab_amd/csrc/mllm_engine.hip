@@ -1912,11 +1912,12 @@ __device__ bool flow_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, co
   lm_load<FTC, FLT>(P, L, tile, Ra);
   LmLds s;
   float *gl = smem;
+  // every region 16-byte aligned (the block sums are read as float4s)
   s.qx = reinterpret_cast<uint32_t *>(gl + al4(3 * D));
-  s.part = gl + al4(3 * D) + ng * Q6R;
+  s.part = gl + al4(3 * D) + al4(ng * Q6R);
   s.out = s.part + FTC * FLT;
-  s.lists = reinterpret_cast<int *>(s.out + L.rpt);
-  float *blk = reinterpret_cast<float *>(s.lists + 34 + P.max_seq);
+  s.lists = reinterpret_cast<int *>(s.out + al4(L.rpt));
+  float *blk = reinterpret_cast<float *>(s.lists + al4(34 + P.max_seq));
   if (pub) {
     const float *rbias = P.arch == 1 ? P.last_mproj_b : nullptr;
     GainsReg GR;
@@ -2514,7 +2515,7 @@ __device__ void flowm_mlp(const DecParams &P, const LayerW &Lw, int li, int item
   const int want = st.tag + li;
   if (fused) {
     // each token's residual and norm here (the unit block 0 item writes xb)
-    float *scratch = reinterpret_cast<float *>(hq + m * 2 * Q6R);
+    float *scratch = reinterpret_cast<float *>(hq + al4(m * 2 * Q6R));  // 16-byte aligned: float4 gains and blocks
     for (int tt = 0; tt < m; ++tt) resid_norm(P, li, ta + tt, 1, st, scratch, qx + tt * ng * Q6R, item == 0);
   } else {
     rec_get(P, rec_row(P, 1, ta), m * ng * Q6R, want, qx);
@@ -2602,7 +2603,7 @@ __device__ bool flowm_lm(const DecParams &P, const LmGeom &L, int wg, int nwg, c
   s.lists = nullptr;
   if (fused) {
     // each token's final norm here
-    float *scratch = s.out + VLB * L.rpt;
+    float *scratch = s.out + al4(VLB * L.rpt);  // 16-byte aligned
     for (int t = 0; t < m; ++t) resid_norm(P, P.L, t, 0, st, scratch, s.qx + t * ng * Q6R, false);
   } else {
     rec_get(P, rec_row(P, 0, 0), m * ng * Q6R, st.tag + P.L, s.qx);
@@ -2941,8 +2942,8 @@ size_t flow_lds_bytes(const DecParams &P, const FlowGeom &F) {
   size_t f = 2 * (FLT / 64);
   for (int ph = PH_QKV; ph <= PH_FINAL; ++ph) f = std::max(f, lds_floats(P, ph, 1));
   const size_t nbd = (P.nchunk + PB - 1) / PB;
-  f = std::max(f, al4(3 * (size_t)P.D) + ngd * Q6R + (size_t)FTC * FLT + (size_t)F.lm_rpt + 34 + P.max_seq +
-                      nbd * P.D + 32);
+  f = std::max(f, al4(3 * (size_t)P.D) + al4(ngd * Q6R) + (size_t)FTC * FLT + al4((size_t)F.lm_rpt) +
+                      al4(34 + (size_t)P.max_seq) + nbd * P.D + 32);
   return f * sizeof(float);
 }
 
@@ -2956,8 +2957,8 @@ size_t flowm_lds_bytes(const DecParams &P, const FlowGeom &F, int m) {
   f = std::max(f, al4(ngd * Q6R) + ns);                                                 // norm items
   f = std::max(f, al4(mq * ngd * Q6R) + mq * (HD * ngd + HD) + al4(mq * 2 * HD) + ns);  // QKV items
   f = std::max(f, mm * (3 * HD + AW * HD + 2 * AW + 2 * Q6R) + al4(mm));               // attention items
-  f = std::max(f, rec + VMB * (2 * UNITS * ngd + 2 * UNITS) + mm * 2 * Q6R + ns);       // MLP items
-  f = std::max(f, rec + (size_t)VLB * FTC * FLT + (size_t)VLB * F.lm_rpt + ns);         // lm_head share
+  f = std::max(f, rec + VMB * (2 * UNITS * ngd + 2 * UNITS) + al4(mm * 2 * Q6R) + ns);  // MLP items
+  f = std::max(f, rec + (size_t)VLB * FTC * FLT + al4((size_t)VLB * F.lm_rpt) + ns);    // lm_head share
   return f * sizeof(float);
 }
 
