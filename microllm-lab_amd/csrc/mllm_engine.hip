@@ -3718,6 +3718,19 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       M->flow_grid = G;
       M->exec_mode = 3;
       M->flow_default = true;
+      // the lm_head tiles dealt evenly over the grid: k tiles per workgroup
+      // (the fewest that cover the vocabulary at FTC chunk registers per
+      // thread), each of ceil(V / (k G)) rows, so that no workgroup takes a
+      // second tile while others are idle; kept only when the tile count
+      // still fits the tile-maxima buffers (amt, amtv: P.lm_tiles tiles)
+      {
+        const int k = (F.lm_tiles + G - 1) / G;
+        const int rpt = std::min(F.lm_rpt, (V + k * G - 1) / (k * G)), nt = (V + rpt - 1) / rpt;
+        if (nt <= P.lm_tiles) {
+          F.lm_rpt = rpt;
+          F.lm_tiles = nt;
+        }
+      }
       // the attention items of a (split, KV head) group on one XCD when the
       // stage's items and groups divide over the eight (MLLM_ATTN_XCD=0: off)
       const char *ax = getenv("MLLM_ATTN_XCD");
