@@ -3665,6 +3665,9 @@ extern "C" int mllm_model_create(const mllm_config *cfg, const void *payload, ui
       void *buf = nullptr;
       if (int rc = dev_alloc(M, &buf, pf_buffer_bytes(A, tc))) return fail(rc);
       pf_carve(A, buf, tc);
+      // the lm_head argmax's counter starts at zero (each launch leaves it so)
+      if (hipMemset(A.amx, 0, gemv_q4_argmax_scratch(A.emb.rows, A.emb.cols)) != hipSuccess)
+        return fail(set_error(MLLM_ERR_HIP, "memset"));
       // the layer matrices as tiled copies (about the payload's size again)
       size_t tiled = 0;
       for (PfLayer &f : M->pf_layer)

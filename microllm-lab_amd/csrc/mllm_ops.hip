@@ -802,6 +802,17 @@ extern "C" int mllm_gemv_q4_argmax(int m, int n, const uint8_t *packed, const fl
   return gemv_q4_argmax_run(a, m, n, packed, scale, x, y, argmax, scratch, as_stream(stream));
 }
 
+namespace mllm {
+size_t gemv_q4_argmax_scratch(int m, int n) { return amx_scratch_bytes(amx_plan(m, n).ntiles); }
+
+int gemv_q4_argmax_into(int m, int n, const uint8_t *packed, const float *scale, const float *x, float *y,
+                        int32_t *argmax, unsigned char *scratch, hipStream_t st) {
+  if (int rc = check_argmax_args(m, n, 32, packed, scale, x, y, argmax)) return rc;
+  MLLM_CHECK(scratch != nullptr, "null argmax scratch");
+  return gemv_q4_argmax_run(amx_plan(m, n), m, n, packed, scale, x, y, argmax, scratch, st);
+}
+}  // namespace mllm
+
 // ---------------------------------------------------------------- no-allocation variant
 // mllm_gemv_q4_argmax_noalloc keeps the argmax scratch in a file-scope device
 // array of fixed size instead of memory the library allocates: every call on

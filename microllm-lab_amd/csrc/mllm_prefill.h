@@ -35,6 +35,7 @@ struct PfArgs {
   void *kv;               // [L][2][NKV][max_seq][64], f32 or f16
   float *logits;          // [V] the last token's logits
   int *res;               // its argmax
+  unsigned char *amx;     // the lm_head argmax launch's scratch (gemv_q4_argmax_scratch bytes, first word zero)
   // work buffers for up to tc tokens
   int tc;
   int32_t *ids;  // [tc]

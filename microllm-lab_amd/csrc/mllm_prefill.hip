@@ -316,34 +316,6 @@ __global__ __launch_bounds__(64) void k_pf_final(const float *x, int K, int t, c
     reinterpret_cast<float4 *>(xn)[q] = pf_norm_col<NORM>(xr, reinterpret_cast<const float4 *>(g), K >> 2, q, r, mean);
 }
 
-// Greedy argmax (infer.js:240-250): the first index of the maximum.
-__global__ __launch_bounds__(1024) void k_pf_argmax(const float *v, int n, int *res) {
-  __shared__ float bv[1024];
-  __shared__ int bi[1024];
-  float best = -INFINITY;
-  int idx = 0x7fffffff;
-  for (int i = tid(); i < n; i += 1024)
-    if (v[i] > best) {  // ascending per thread: ties keep the first
-      best = v[i];
-      idx = i;
-    }
-  bv[tid()] = best;
-  bi[tid()] = idx;
-  __syncthreads();
-  for (int w = 512; w > 0; w >>= 1) {
-    if (tid() < w) {
-      const float o = bv[tid() + w];
-      const int oi = bi[tid() + w];
-      if (o > bv[tid()] || (o == bv[tid()] && oi < bi[tid()])) {
-        bv[tid()] = o;
-        bi[tid()] = oi;
-      }
-    }
-    __syncthreads();
-  }
-  if (tid() == 0) *res = bi[0] == 0x7fffffff ? 0 : bi[0];
-}
-
 // ---------------------------------------------------------------- Q4 GEMM
 // A wave computes two 32-row sub-tiles (sub-tile 1 is either the next 32
 // rows of the same matrix -- a 64-row head of attn.qkv, 64 rows of the
@@ -944,6 +916,7 @@ size_t pf_buffer_bytes(const PfArgs &A, int tc) {
   auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
   // + GPF groups of padding after the last tile (read ahead, never used)
   return al(sizeof(int32_t) * tc) + 3 * al(sizeof(float) * tc * A.D) + al(sizeof(float) * tc * A.FF) +
+         al(gemv_q4_argmax_scratch(A.emb.rows, A.emb.cols)) +
          al((size_t)((tc + 31) / 32) * px_tile_bytes((int)kmax) + (size_t)GPF * PXG);
 }
 
@@ -962,6 +935,8 @@ void pf_carve(PfArgs &A, void *base, int tc) {
   p += al(sizeof(float) * tc * A.D);
   A.h = reinterpret_cast<float *>(p);
   p += al(sizeof(float) * tc * A.FF);
+  A.amx = p;
+  p += al(gemv_q4_argmax_scratch(A.emb.rows, A.emb.cols));
   A.px = p;
 }
 
@@ -1030,15 +1005,16 @@ int pf_layers(const PfArgs &A, const int32_t *ids, int n, int pos0, bool last, h
     launch_gemm<EPI_RESID>(A, Dn, s);
   }
   if (last) {
-    // the final norm of the last token, the lm_head (the standalone Q4 GEMV)
-    // and the greedy argmax
+    // the final norm of the last token, then the lm_head and the greedy
+    // argmax in one launch (the standalone Q4 GEMV's rows, infer.js:240-250's
+    // first maximum)
     float *xn = A.att;  // free once the layers are done
     if (gpt2)
       hipLaunchKernelGGL(k_pf_final<NORM_LN>, dim3(1), dim3(64), 0, s, A.x, A.D, n - 1, A.norm_f, A.eps, xn);
     else
       hipLaunchKernelGGL(k_pf_final<NORM_RMS>, dim3(1), dim3(64), 0, s, A.x, A.D, n - 1, A.norm_f, A.eps, xn);
-    if (int rc = mllm_gemv_q4(A.emb.rows, A.emb.cols, A.emb.q, A.emb.s, 32, xn, A.logits, s)) return rc;
-    hipLaunchKernelGGL(k_pf_argmax, dim3(1), dim3(1024), 0, s, A.logits, A.emb.rows, A.res);
+    if (int rc = gemv_q4_argmax_into(A.emb.rows, A.emb.cols, A.emb.q, A.emb.s, xn, A.logits, A.res, A.amx, s))
+      return rc;
   }
   MLLM_HIP(hipGetLastError());
   return 0;
