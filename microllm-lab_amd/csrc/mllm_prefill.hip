@@ -859,11 +859,19 @@ void launch_quant(const PfArgs &A, const float *src, int K, const float *g, int 
 
 // Group slices per row range: the fewest (1, 2 or 4) that give at least
 // 2048 waves (two per SIMD on 256 CUs), keeping >= 8 groups per slice.
+#ifndef MLLM_PF_WAVES
+#define MLLM_PF_WAVES 1024
+#endif
+#ifndef MLLM_PF_MINSLICE
+#define MLLM_PF_MINSLICE 8
+#endif
+// Group slices per row range (KS): doubled while the launch has fewer than
+// MLLM_PF_WAVES row waves and every slice keeps MLLM_PF_MINSLICE groups.
 template <int EPI>
 void launch_gemm(const PfArgs &A, const PfGemm &G, hipStream_t s) {
   const int tt = (G.n + 31) / 32 - G.tt0, rw = (G.rows + G.rstep - 1) / G.rstep;
   int ks = 1;
-  while (ks < 4 && rw * tt * ks < 2048 && G.ng / (2 * ks) >= 8) ks *= 2;
+  while (ks < 4 && rw * tt * ks < MLLM_PF_WAVES && G.ng / (2 * ks) >= MLLM_PF_MINSLICE) ks *= 2;
   const int per_wg = (WG / 64 / ks) * G.rstep;
   const dim3 grid((G.rows + per_wg - 1) / per_wg, tt);
   if (ks == 1) hipLaunchKernelGGL((k_pf_gemm<EPI, 1>), grid, dim3(WG), 0, s, A, G);
