@@ -320,7 +320,7 @@ __global__ __launch_bounds__(64) void k_pf_final(const float *x, int K, int t, c
 // A wave computes two 32-row sub-tiles (sub-tile 1 is either the next 32
 // rows of the same matrix -- a 64-row head of attn.qkv, 64 rows of the
 // others -- or the same rows of a second matrix: mlp.w3 beside mlp.w1) for
-// 32 tokens.  Workgroup: 4 waves, one token tile; with KS > 1, KS waves
+// 32 tokens.  Workgroup: GWG / 64 waves, one token tile; with KS > 1, KS waves
 // share a row range and take consecutive slices of the groups, and their
 // sums are added in slice order through LDS (deterministic) before the
 // epilogue -- more waves for the GEMMs with few row ranges.
@@ -358,6 +358,10 @@ __device__ __forceinline__ v8h pf_w8(uint32_t w) {
 #define MLLM_PF_GPF 3
 #endif
 constexpr int GPF = MLLM_PF_GPF;  // groups of loads in flight per wave
+#ifndef MLLM_PF_GWG
+#define MLLM_PF_GWG 512
+#endif
+constexpr int GWG = MLLM_PF_GWG;  // threads per GEMM workgroup (waves sharing one token tile)
 
 struct Pieces {
   v8h p0a, p0b, p1a, p1b, p2a, p2b;  // piece 0 .. 2, K half a / b
@@ -388,11 +392,11 @@ __device__ __forceinline__ void pf_group_acc(const Pieces &x, uint2 w, float c, 
 }
 
 template <int EPI, int KS>
-__global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
-  __shared__ float red[KS > 1 ? WG * 32 : 1];
+__global__ __launch_bounds__(GWG) void k_pf_gemm(PfArgs A, PfGemm G) {
+  __shared__ float red[KS > 1 ? GWG * 32 : 1];
   const int wv = tid() >> 6, lane = tid() & 63, j = lane & 31, hh = lane >> 5;
   const int ks = wv % KS;
-  const int R = (blockIdx.x * (WG / 64 / KS) + wv / KS) * G.rstep;
+  const int R = (blockIdx.x * (GWG / 64 / KS) + wv / KS) * G.rstep;
   const bool active = R < G.rows;
   const int T0 = (G.tt0 + blockIdx.y) * 32;
   const int ng = G.ng, gb = ng * ks / KS, ge = ng * (ks + 1) / KS;  // this wave's groups
@@ -439,15 +443,15 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
       }
   }
   if (KS > 1) {
-    // partials value-major in 16-byte quads, red4[q * WG + thread]: the 64
+    // partials value-major in 16-byte quads, red4[q * GWG + thread]: the 64
     // lanes of a wave touch 1 KiB of consecutive LDS per access, so no two
     // lanes of a pass share a bank
     v4f *red4 = reinterpret_cast<v4f *>(red);
     if (ks > 0) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        red4[q * WG + tid()] = v4f{acc0[4 * q], acc0[4 * q + 1], acc0[4 * q + 2], acc0[4 * q + 3]};
-        red4[(4 + q) * WG + tid()] = v4f{acc1[4 * q], acc1[4 * q + 1], acc1[4 * q + 2], acc1[4 * q + 3]};
+        red4[q * GWG + tid()] = v4f{acc0[4 * q], acc0[4 * q + 1], acc0[4 * q + 2], acc0[4 * q + 3]};
+        red4[(4 + q) * GWG + tid()] = v4f{acc1[4 * q], acc1[4 * q + 1], acc1[4 * q + 2], acc1[4 * q + 3]};
       }
     }
     __syncthreads();
@@ -457,7 +461,7 @@ __global__ __launch_bounds__(WG) void k_pf_gemm(PfArgs A, PfGemm G) {
       const int o = tid() + 64 * k;  // the same lane of slice k's wave
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const v4f a = red4[q * WG + o], b = red4[(4 + q) * WG + o];
+        const v4f a = red4[q * GWG + o], b = red4[(4 + q) * GWG + o];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           acc0[4 * q + e] = acc0[4 * q + e] + a[e];
@@ -872,11 +876,11 @@ void launch_gemm(const PfArgs &A, const PfGemm &G, hipStream_t s) {
   const int tt = (G.n + 31) / 32 - G.tt0, rw = (G.rows + G.rstep - 1) / G.rstep;
   int ks = 1;
   while (ks < 4 && rw * tt * ks < MLLM_PF_WAVES && G.ng / (2 * ks) >= MLLM_PF_MINSLICE) ks *= 2;
-  const int per_wg = (WG / 64 / ks) * G.rstep;
+  const int per_wg = (GWG / 64 / ks) * G.rstep;
   const dim3 grid((G.rows + per_wg - 1) / per_wg, tt);
-  if (ks == 1) hipLaunchKernelGGL((k_pf_gemm<EPI, 1>), grid, dim3(WG), 0, s, A, G);
-  if (ks == 2) hipLaunchKernelGGL((k_pf_gemm<EPI, 2>), grid, dim3(WG), 0, s, A, G);
-  if (ks == 4) hipLaunchKernelGGL((k_pf_gemm<EPI, 4>), grid, dim3(WG), 0, s, A, G);
+  if (ks == 1) hipLaunchKernelGGL((k_pf_gemm<EPI, 1>), grid, dim3(GWG), 0, s, A, G);
+  if (ks == 2) hipLaunchKernelGGL((k_pf_gemm<EPI, 2>), grid, dim3(GWG), 0, s, A, G);
+  if (ks == 4) hipLaunchKernelGGL((k_pf_gemm<EPI, 4>), grid, dim3(GWG), 0, s, A, G);
 }
 
 PfGemm gemm_same(const PfMat &W, int n, const float *bias, float *out, int ldo) {
