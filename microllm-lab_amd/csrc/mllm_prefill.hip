@@ -54,6 +54,18 @@
 namespace mllm {
 namespace {
 
+// Workgroups of one token tile on one XCD (workgroup b runs on XCD b % 8):
+// the GEMMs (MLLM_PF_XCD), the quantise kernels (MLLM_PF_XCDQ) and the
+// attention (MLLM_PF_XCDA) put relative tile r on XCD r % 8.
+#ifndef MLLM_PF_XCD
+#define MLLM_PF_XCD 1
+#endif
+#ifndef MLLM_PF_XCDQ
+#define MLLM_PF_XCDQ 1
+#endif
+#ifndef MLLM_PF_XCDA
+#define MLLM_PF_XCDA 1
+#endif
 constexpr int PXG = 6 * 1024;  // bytes per (32-token tile, group): 3 pieces x 2 K halves x 64 lanes x 16
 constexpr int PX_TOK = 128;    // after a tile's groups: its 32 tokens' exponents (int)
 constexpr int PF_HD = 64;      // head dimension
@@ -289,8 +301,16 @@ __global__ __launch_bounds__(QT * 64) void k_pf_quant(const float *src, int K, c
                                                       uint8_t *px, int t0, int t1) {
   extern __shared__ float4 qsm4[];
   uint8_t *qs = reinterpret_cast<uint8_t *>(qsm4);
-  const int jj = tid() >> 6, j0 = QT * ((int)blockIdx.x % (32 / QT));
-  const int tile = t0 / 32 + (int)blockIdx.x / (32 / QT), t = tile * 32 + j0 + jj;
+  // workgroup -> (tile rt, token slot); with MLLM_PF_XCDQ a tile's workgroups
+  // run on the XCD that the GEMMs give it (relative tile rt on XCD rt % 8)
+  int bq = blockIdx.x, rt = bq / (32 / QT), qs8 = bq % (32 / QT);
+  if (MLLM_PF_XCDQ && gridDim.x % (8 * (32 / QT)) == 0) {
+    const int k = bq >> 3;
+    rt = (bq & 7) + 8 * (k / (32 / QT));
+    qs8 = k % (32 / QT);
+  }
+  const int jj = tid() >> 6, j0 = QT * qs8;
+  const int tile = t0 / 32 + rt, t = tile * 32 + j0 + jj;
   const int nu = K >> 4;
   uint8_t *tb = px + (size_t)tile * px_tile_bytes(K);
   if (t < t1) pf_quant_row<NORM, PPL, QT>(src, K, g, eps, t, jj, j0 + jj, tb, qs);  // wave-uniform
@@ -359,7 +379,7 @@ __device__ __forceinline__ v8h pf_w8(uint32_t w) {
 #endif
 constexpr int GPF = MLLM_PF_GPF;  // groups of loads in flight per wave
 #ifndef MLLM_PF_GWG
-#define MLLM_PF_GWG 512
+#define MLLM_PF_GWG 256
 #endif
 constexpr int GWG = MLLM_PF_GWG;  // threads per GEMM workgroup (waves sharing one token tile)
 
@@ -396,9 +416,20 @@ __global__ __launch_bounds__(GWG) void k_pf_gemm(PfArgs A, PfGemm G) {
   __shared__ float red[KS > 1 ? GWG * 32 : 1];
   const int wv = tid() >> 6, lane = tid() & 63, j = lane & 31, hh = lane >> 5;
   const int ks = wv % KS;
-  const int R = (blockIdx.x * (GWG / 64 / KS) + wv / KS) * G.rstep;
+  // workgroup -> (row range bx, token tile by); with MLLM_PF_XCD the
+  // workgroups of one token tile sit on one XCD (workgroup b runs on XCD b % 8,
+  // each with its own L2), so the tile's activation pieces are fetched into one
+  // L2 and read there by every row range (a bijection when the tiles divide
+  // over the eight XCDs)
+  int bx = blockIdx.x, by = blockIdx.y;
+  if (MLLM_PF_XCD && gridDim.y % 8 == 0) {
+    const int b = bx + (int)gridDim.x * by, k = b >> 3;
+    by = (b & 7) + 8 * (k / (int)gridDim.x);
+    bx = k % (int)gridDim.x;
+  }
+  const int R = (bx * (GWG / 64 / KS) + wv / KS) * G.rstep;
   const bool active = R < G.rows;
-  const int T0 = (G.tt0 + blockIdx.y) * 32;
+  const int T0 = (G.tt0 + by) * 32;
   const int ng = G.ng, gb = ng * ks / KS, ge = ng * (ks + 1) / KS;  // this wave's groups
   // tiled operands (every row tile and token tile whole): per group, the
   // wave's weights are 512 contiguous bytes, its scales 128, the tile's
@@ -406,7 +437,7 @@ __global__ __launch_bounds__(GWG) void k_pf_gemm(PfArgs A, PfGemm G) {
   const size_t ta = (size_t)(R >> 5) * ng, tb = (size_t)((R + G.off1) >> 5) * ng;
   const uint8_t *wa = G.q0 + ta * 512 + 8 * lane, *wb = G.q1 + tb * 512 + 8 * lane;
   const float *sa = G.s0 + ta * 32 + j, *sb = G.s1 + tb * 32 + j;
-  const uint8_t *xt = A.px + (size_t)(G.tt0 + blockIdx.y) * px_tile_bytes(32 * ng), *xa = xt + 16 * lane;
+  const uint8_t *xt = A.px + (size_t)(G.tt0 + by) * px_tile_bytes(32 * ng), *xa = xt + 16 * lane;
   auto load = [&](int g) {
     GemmLd L;
     L.w0 = *reinterpret_cast<const uint2 *>(wa + 512 * g);
@@ -618,7 +649,15 @@ __global__ __launch_bounds__(NSET == 4 ? 768 : 512) void k_pf_attn(PfArgs A, int
   _Float16 *Kh = reinterpret_cast<_Float16 *>(smem), *Vh = Kh + KSB * KROW;
   _Float16 *Kl = Vh + PF_HD * VROW, *Vl = Kl + KSB * KROW;  // SPLIT_KV only
   const int rep = A.NH / A.NKV;
-  const int T0 = (tt0 + gridDim.x - 1 - blockIdx.x) * QTL, kvh = blockIdx.y;  // the longest tiles first
+  // the longest tiles first; with MLLM_PF_XCDA relative tile r runs on XCD
+  // r % 8, where the GEMMs put it
+  int rtile = gridDim.x - 1 - blockIdx.x, kvh = blockIdx.y;
+  if (MLLM_PF_XCDA && gridDim.x % 8 == 0) {
+    const int b = blockIdx.x + gridDim.x * blockIdx.y, k = b >> 3;
+    rtile = (b & 7) + 8 * ((int)gridDim.x / 8 - 1 - k / (int)gridDim.y);
+    kvh = k % (int)gridDim.y;
+  }
+  const int T0 = (tt0 + rtile) * QTL;
   const int lane = tid() & 63, j = lane & 31, hh = lane >> 5;
   const int wv = tid() >> 6, set = wv / rep, hsel = wv - set * rep;
   const int hq = kvh * rep + hsel;
