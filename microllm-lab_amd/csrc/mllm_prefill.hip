@@ -900,16 +900,15 @@ void launch_quant(const PfArgs &A, const float *src, int K, const float *g, int 
     quant_launch<NORM, 4, 4>(grid, lds, s, A, src, K, g, t0, t1);
 }
 
-// Group slices per row range: the fewest (1, 2 or 4) that give at least
-// 2048 waves (two per SIMD on 256 CUs), keeping >= 8 groups per slice.
 #ifndef MLLM_PF_WAVES
 #define MLLM_PF_WAVES 1024
 #endif
 #ifndef MLLM_PF_MINSLICE
 #define MLLM_PF_MINSLICE 8
 #endif
-// Group slices per row range (KS): doubled while the launch has fewer than
-// MLLM_PF_WAVES row waves and every slice keeps MLLM_PF_MINSLICE groups.
+// Group slices per row range (KS, 1, 2 or 4): doubled while the launch has
+// fewer than MLLM_PF_WAVES row waves and every slice keeps MLLM_PF_MINSLICE
+// groups (1024 and 8 measured best: 2048 or 4096 waves gave longer prompts).
 template <int EPI>
 void launch_gemm(const PfArgs &A, const PfGemm &G, hipStream_t s) {
   const int tt = (G.n + 31) / 32 - G.tt0, rw = (G.rows + G.rstep - 1) / G.rstep;
