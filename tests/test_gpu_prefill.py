@@ -226,6 +226,31 @@ def test_batched_prompt_precision_vs_oracle(oracle_lib, arch):
 
 
 @gpu
+@pytest.mark.parametrize("arch", ["llama", "gpt2"])
+@pytest.mark.parametrize("n", [256, 288, 512])
+def test_batched_prompt_tile_placement_vs_oracle(oracle_lib, arch, n):
+    """Prompts of 8 and 16 token tiles, whose prompt kernels place each tile's
+    workgroups on one XCD (the tile count divides by eight), and of 9 tiles,
+    which keep the plain workgroup order: the last-token logits within
+    PREFILL_TOL of the oracle relative to their scale, and the greedy argmax
+    equal wherever the oracle's top-2 margin exceeds MARGIN."""
+    bundle = build(arch, seed=28, max_seq_len=640)
+    print(f"prefill tile placement {arch} n={n}", flush=True)
+    g = mllm.PetitGPT(bundle)
+    g.set_prefill(2)
+    ref = oracle_lib.OracleModel(bundle)
+    prompt = [int(v) for v in np.random.default_rng(n).integers(0, bundle.cfg.vocab_size, n)]
+    lg = g.forwardPrompt(prompt).copy()
+    lr = ref.forward_prompt(prompt)
+    g.destroy()
+    ref.close()
+    rel = float(np.abs(lg - lr).max()) / float(np.abs(lr).max())
+    print(f"  relative {rel:.2e}", flush=True)
+    assert rel <= PREFILL_TOL, rel
+    assert int(np.argmax(lg)) == int(np.argmax(lr)) or margin(lr) <= MARGIN
+
+
+@gpu
 def test_batched_prompt_precision_full_size_360m(oracle_lib):
     """The 360M shape at full depth (f32 KV cache, as the oracle's), a 64-token
     prompt through the batched path: its last-token logits within PREFILL_TOL
