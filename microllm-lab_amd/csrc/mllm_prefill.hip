@@ -303,13 +303,13 @@ __global__ __launch_bounds__(QT * 64) void k_pf_quant(const float *src, int K, c
   uint8_t *qs = reinterpret_cast<uint8_t *>(qsm4);
   // workgroup -> (tile rt, token slot); with MLLM_PF_XCDQ a tile's workgroups
   // run on the XCD that the GEMMs give it (relative tile rt on XCD rt % 8)
-  int bq = blockIdx.x, rt = bq / (32 / QT), qs8 = bq % (32 / QT);
+  int bq = blockIdx.x, rt = bq / (32 / QT), jslot = bq % (32 / QT);
   if (MLLM_PF_XCDQ && gridDim.x % (8 * (32 / QT)) == 0) {
     const int k = bq >> 3;
     rt = (bq & 7) + 8 * (k / (32 / QT));
-    qs8 = k % (32 / QT);
+    jslot = k % (32 / QT);
   }
-  const int jj = tid() >> 6, j0 = QT * qs8;
+  const int jj = tid() >> 6, j0 = QT * jslot;
   const int tile = t0 / 32 + rt, t = tile * 32 + j0 + jj;
   const int nu = K >> 4;
   uint8_t *tb = px + (size_t)tile * px_tile_bytes(K);
